@@ -1,0 +1,146 @@
+// rl_dev_common.h - gfx950 device helpers shared by the kernels: bf16/fp16
+// conversion, DPP row reductions, LDS-direct (global_load_lds) staging.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 rl_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 rl_f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t rl_u32x4 __attribute__((ext_vector_type(4)));
+typedef float rl_f32x4 __attribute__((ext_vector_type(4)));
+
+#define RL_LDS __attribute__((address_space(3)))
+#define RL_CONST __attribute__((address_space(4)))
+
+// Load through the constant address space: memory the kernel never writes,
+// read at a wave-uniform address, becomes a scalar (s_load) access.
+template <typename T>
+__device__ __forceinline__ T rl_sload(const T *p)
+{
+    return *(const RL_CONST T *)p;
+}
+
+// ---- scalar conversions ---------------------------------------------------
+
+__device__ __forceinline__ float rl_bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float rl_bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+
+__device__ __forceinline__ float rl_f16_lo(uint32_t w)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+__device__ __forceinline__ float rl_f16_hi(uint32_t w)
+{
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// float -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint16_t rl_f32_to_bf16(float f)
+{
+    const uint32_t u = __float_as_uint(f);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+__device__ __forceinline__ uint16_t rl_f32_to_f16(float f)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Element pair of a packed dword -> two fp32 values.
+template <int DT>
+__device__ __forceinline__ void rl_unpack2(uint32_t w, float &lo, float &hi)
+{
+    if constexpr (DT == 0) {
+        lo = rl_bf16_lo(w);
+        hi = rl_bf16_hi(w);
+    } else {
+        lo = rl_f16_lo(w);
+        hi = rl_f16_hi(w);
+    }
+}
+
+// acc + a.x*b.x + a.y*b.y with 2-byte operands and an fp32 accumulator.
+template <int DT>
+__device__ __forceinline__ float rl_dot2(uint32_t a, uint32_t b, float acc)
+{
+    if constexpr (DT == 0)
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(rl_bf16x2, a),
+                                               __builtin_bit_cast(rl_bf16x2, b), acc, false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(rl_f16x2, a), __builtin_bit_cast(rl_f16x2, b),
+                                      acc, false);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t rl_from_f32(float f)
+{
+    if constexpr (DT == 0)
+        return rl_f32_to_bf16(f);
+    else
+        return rl_f32_to_f16(f);
+}
+
+// ---- DPP reductions inside a row of 16 lanes ------------------------------
+// quad_perm(1,0,3,2) = 0xB1, quad_perm(2,3,0,1) = 0x4E, row_half_mirror =
+// 0x141, row_mirror = 0x140. After the four steps every lane of the row holds
+// the reduction over its 16 lanes.
+
+template <int CTRL>
+__device__ __forceinline__ float rl_dpp(float x)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float rl_row_max(float x)
+{
+    x = fmaxf(x, rl_dpp<0xB1>(x));
+    x = fmaxf(x, rl_dpp<0x4E>(x));
+    x = fmaxf(x, rl_dpp<0x141>(x));
+    x = fmaxf(x, rl_dpp<0x140>(x));
+    return x;
+}
+
+__device__ __forceinline__ float rl_row_sum(float x)
+{
+    x += rl_dpp<0xB1>(x);
+    x += rl_dpp<0x4E>(x);
+    x += rl_dpp<0x141>(x);
+    x += rl_dpp<0x140>(x);
+    return x;
+}
+
+// ---- LDS-direct staging ---------------------------------------------------
+// global_load_lds_dwordx4: each lane fetches 16 bytes from its own global
+// address; they land at lds_base + lane * 16 (lds_base wave-uniform).
+__device__ __forceinline__ void rl_g2lds_16(const void *gsrc, RL_LDS void *lds_base)
+{
+    __builtin_amdgcn_global_load_lds(gsrc, lds_base, 16, 0, 0);
+}
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding (loads retire in issue order), e.g. the LDS-direct copies of
+// one staged unit while the next unit's copies stay in flight. The memory
+// clobber keeps the compiler from hoisting LDS reads above the wait.
+template <int N>
+__device__ __forceinline__ void rl_wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Waits for all of this wave's LDS reads to return (before an LDS-direct
+// copy may overwrite what they read).
+__device__ __forceinline__ void rl_wait_lgkmcnt0()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Orders this wave's LDS writes before its later LDS reads (the LDS unit
+// serves one wave in issue order; this keeps the compiler from reordering).
+__device__ __forceinline__ void rl_wave_lds_fence()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}

@@ -1,0 +1,15 @@
+// rl_hip_internal.h - helpers shared by the HIP translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+void rl_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+int rl_check_hip(hipError_t e, const char *what);
+int rl_require_open(const char *what);
+hipStream_t rl_stream(void);
+
+// Reports a launch error (or a fault of an earlier asynchronous call).
+static inline int rl_check_launch(const char *what)
+{
+    return rl_check_hip(hipGetLastError(), what);
+}

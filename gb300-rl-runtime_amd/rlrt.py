@@ -1,0 +1,355 @@
+"""ctypes binding of librlrt_amd.so (the C ABI declared in include/*.h).
+
+The product is the C library: the reference's host C API (rings, submit,
+worker model, descriptor windows, arena, prefix table, reward) plus the thin
+HIP layer (rl_hip_*) in front of the gfx950 kernels. This module only mirrors
+those entry points for tests and benchmarks, with numpy arrays as host
+buffers. Every call checks the C return code and raises RlrtError with
+rl_hip_last_error() on failure; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "librlrt_amd.so")
+
+
+class RlrtError(RuntimeError):
+    pass
+
+
+# ---------------------------------------------------------------- ABI types
+class KvLayoutDesc(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("token_count", "head_dim", "scalar_bytes", "vec_bytes",
+                                          "k_stride_bytes", "v_stride_bytes", "block_bytes", "alignment")]
+
+    @classmethod
+    def paged(cls, token_count: int, head_dim: int, scalar_bytes: int = 2) -> "KvLayoutDesc":
+        row = head_dim * scalar_bytes
+        return cls(token_count, head_dim, scalar_bytes, 16, row, row, 2 * token_count * row, 128)
+
+
+class HwDesc(C.Structure):
+    _pack_ = 1
+    _fields_ = [("opcode", C.c_uint16), ("flags", C.c_uint16), ("rollout_id", C.c_uint32),
+                ("kv_arena_id", C.c_uint32), ("prefix_id", C.c_uint32), ("kv_offset", C.c_uint64),
+                ("delta_offset", C.c_uint64), ("seq_len", C.c_uint32), ("max_tokens", C.c_uint32),
+                ("reward_model_id", C.c_uint32), ("reserved0", C.c_uint32), ("user_data", C.c_uint64),
+                ("checksum_or_cookie", C.c_uint64)]
+
+
+class InferHwCtx(C.Structure):
+    _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("doorbell", C.c_void_p),
+                ("gpu_group_id", C.c_uint32), ("kv_arena_id", C.c_uint32)]
+
+
+class HwWorkerSim(C.Structure):
+    _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("stop", C.c_void_p),
+                ("decoded_tokens", C.c_uint64), ("completions", C.c_uint64)]
+
+
+class Descriptor(C.Structure):
+    _pack_ = 1
+    _fields_ = [("seq_id", C.c_uint64), ("kv_block_offset", C.c_uint32), ("num_kv_blocks", C.c_uint16),
+                ("attention_flags", C.c_uint8), ("pad", C.c_uint8), ("output_token_offset", C.c_uint32),
+                ("reward_cookie", C.c_uint64), ("batch_size", C.c_uint16), ("batch_index", C.c_uint16)]
+
+
+class DecodeDispatchBatch(C.Structure):
+    _fields_ = [("count", C.c_uint32), ("descs", Descriptor * 32)]
+
+
+class DecodeBatchContract(C.Structure):
+    _fields_ = [("batch_size", C.c_uint16), ("batch_index", C.c_uint16)]
+
+
+class Completion(C.Structure):
+    _pack_ = 1
+    _fields_ = [("seq_id", C.c_uint64), ("token_id", C.c_uint32), ("kv_block_offset", C.c_uint32),
+                ("reward_cookie", C.c_uint64), ("cycles_taken", C.c_uint64)]
+
+
+class RolloutRequest(C.Structure):
+    _pack_ = 1
+    _fields_ = [("request_id", C.c_uint64), ("max_tokens", C.c_uint32), ("kv_blocks", C.c_uint32),
+                ("temperature", C.c_float), ("top_k", C.c_uint16), ("top_p", C.c_float),
+                ("rng_seed", C.c_uint64)]
+
+
+class RolloutDone(C.Structure):
+    _pack_ = 1
+    _fields_ = [("request_id", C.c_uint64), ("rollout_id", C.c_uint32), ("tokens_generated", C.c_uint32),
+                ("reward", C.c_float), ("status", C.c_uint32)]
+
+
+class KVPrefix(C.Structure):
+    _pack_ = 1
+    _fields_ = [("prefix_id", C.c_uint32), ("refcnt", C.c_uint32), ("kv_block_offset", C.c_int64),
+                ("token_len", C.c_uint32), ("kv_block_count", C.c_uint32), ("flags", C.c_uint32)]
+
+
+class KVBranch(C.Structure):
+    _pack_ = 1
+    _fields_ = [("branch_id", C.c_uint32), ("rollout_id", C.c_uint32), ("prefix_id", C.c_uint32),
+                ("delta_kv_offset", C.c_int64), ("delta_len", C.c_uint32), ("delta_block_count", C.c_uint32),
+                ("state", C.c_uint32), ("flags", C.c_uint32)]
+
+
+class KVArenaHead(C.Structure):
+    """First 24 bytes of KVArena; the 131,072-byte bitmap follows."""
+    _fields_ = [("base", C.c_void_p), ("capacity", C.c_size_t), ("block_size", C.c_size_t)]
+
+
+class DecodeMicrokernelConfig(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("head_dim", "tokens_per_block", "tile_tokens", "prefetch_stages",
+                                          "shared_bytes")]
+
+
+class DecodeStepResult(C.Structure):
+    _fields_ = [("path_kind", C.c_uint32), ("token_id", C.c_uint32), ("bytes_touched", C.c_uint32),
+                ("tile_count", C.c_uint32), ("cycle_estimate", C.c_uint64)]
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("device", C.c_int32), ("cu_count", C.c_uint32), ("wave_size", C.c_uint32),
+                ("lds_bytes_per_block", C.c_uint32), ("clock_khz", C.c_uint32), ("mem_clock_khz", C.c_uint32),
+                ("mem_bus_width_bits", C.c_uint32), ("l2_bytes", C.c_uint32), ("hbm_bytes", C.c_uint64),
+                ("arch", C.c_char * 64)]
+
+
+class AttnArgs(C.Structure):
+    _fields_ = [("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64), ("layout", KvLayoutDesc),
+                ("block_table", C.c_void_p), ("table_stride", C.c_uint32), ("batch", C.c_uint32),
+                ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32), ("dtype", C.c_uint32),
+                ("ctx_lens", C.c_void_p), ("max_ctx", C.c_uint32), ("chunk_tokens", C.c_uint32),
+                ("scale", C.c_float), ("q", C.c_void_p), ("out", C.c_void_p), ("out_f32", C.c_void_p),
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
+class SampleArgs(C.Structure):
+    _fields_ = [("logits", C.c_void_p), ("rows", C.c_uint32), ("vocab", C.c_uint32), ("row_stride", C.c_uint32),
+                ("greedy", C.c_uint32), ("temperature", C.c_void_p), ("top_k", C.c_void_p),
+                ("top_p", C.c_void_p), ("seed", C.c_void_p), ("temperature_all", C.c_float),
+                ("top_k_all", C.c_uint32), ("top_p_all", C.c_float), ("seed_all", C.c_uint64),
+                ("step", C.c_uint64), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
+class AppendArgs(C.Structure):
+    _fields_ = [("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64), ("layout", KvLayoutDesc),
+                ("block_table", C.c_void_p), ("table_stride", C.c_uint32), ("batch", C.c_uint32),
+                ("kv_heads", C.c_uint32), ("positions", C.c_void_p), ("cow_src", C.c_void_p),
+                ("k_new", C.c_void_p), ("v_new", C.c_void_p)]
+
+
+DTYPE_BF16 = 0
+DTYPE_FP16 = 1
+
+
+# ---------------------------------------------------------------- library
+def load(path: str = LIB_PATH) -> C.CDLL:
+    if not os.path.exists(path):
+        raise RlrtError(f"{path} is not built: run __graft_entry__.build()")
+    lib = C.CDLL(path)
+    vp, sz, u32, u64, i64, i32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_uint64, C.c_int64, C.c_int
+    sigs = {
+        "rl_hip_open": (i32, [i32]), "rl_hip_close": (i32, []), "rl_hip_is_open": (i32, []),
+        "rl_hip_device_info": (i32, [C.POINTER(DeviceInfo)]), "rl_hip_last_error": (C.c_char_p, []),
+        "rl_hip_host_alloc_coherent": (vp, [sz]), "rl_hip_host_free": (i32, [vp]),
+        "rl_hip_is_coherent_host": (i32, [vp]), "rl_hip_dev_alloc": (vp, [sz]),
+        "rl_hip_is_device_ptr": (i32, [vp]), "rl_hip_dev_free": (i32, [vp]),
+        "rl_hip_memcpy_h2d": (i32, [vp, vp, sz]), "rl_hip_memcpy_d2h": (i32, [vp, vp, sz]),
+        "rl_hip_memcpy_d2d": (i32, [vp, vp, sz]), "rl_hip_memset_d": (i32, [vp, i32, sz]),
+        "rl_hip_sync": (i32, []), "rl_hip_timer_begin": (i32, []),
+        "rl_hip_timer_end": (i32, [C.POINTER(C.c_float)]),
+        "rl_hip_attn_decode_workspace": (sz, [C.POINTER(AttnArgs)]),
+        "rl_hip_attn_decode": (i32, [C.POINTER(AttnArgs)]),
+        "rl_hip_sample_workspace": (sz, [C.POINTER(SampleArgs)]),
+        "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
+        "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
+        # reference host API
+        "hw_ring_create": (vp, []), "hw_ring_reset": (None, [vp]), "hw_ring_destroy": (None, [vp]),
+        "hw_ring_load_acquire": (u32, [vp]), "hw_ring_store_release": (None, [vp, u32]),
+        "infer_submit_decode": (i32, [C.POINTER(InferHwCtx), u32, u64, u64, u32, u32, u32]),
+        "hw_worker_sim_run": (None, [C.POINTER(HwWorkerSim)]),
+        "hw_worker_apply_decode_rule": (u32, [C.POINTER(HwDesc)]),
+        "ring_create": (vp, []), "ring_destroy": (None, [vp]),
+        "comp_ring_create": (vp, []), "comp_ring_destroy": (None, [vp]),
+        "req_ring_create": (vp, []), "req_ring_destroy": (None, [vp]),
+        "done_ring_create": (vp, []), "done_ring_destroy": (None, [vp]),
+        "decode_batch_reset": (None, [C.POINTER(DecodeDispatchBatch)]),
+        "decode_batch_push": (i32, [C.POINTER(DecodeDispatchBatch), C.POINTER(Descriptor)]),
+        "decode_batch_submit": (i32, [vp, C.POINTER(DecodeDispatchBatch)]),
+        "decode_batch_contract": (DecodeBatchContract, [C.POINTER(Descriptor)]),
+        "arena_init": (None, [vp, sz, sz]), "arena_acquire": (i64, [vp]), "arena_release": (None, [vp, i64]),
+        "arena_destroy": (None, [vp]), "arena_is_device": (i32, [vp]),
+        "kv_prefix_table_init": (None, [vp]),
+        "kv_prefix_register": (i32, [vp, i64, u32, u32, C.POINTER(u32)]),
+        "kv_prefix_acquire": (i32, [vp, u32]), "kv_prefix_release": (i32, [vp, u32]),
+        "kv_prefix_get": (C.POINTER(KVPrefix), [vp, u32]),
+        "kv_branch_alloc": (i32, [vp, u32, u32, i64, u32, u32, C.POINTER(u32)]),
+        "kv_branch_free": (i32, [vp, u32]), "kv_branch_get": (C.POINTER(KVBranch), [vp, u32]),
+        "kv_branch_total_offset": (i64, [vp, u32]),
+        "reward_score_mock": (C.c_float, [vp, u32]),
+        "reward_match_count": (u32, [vp, vp, u32]),
+        "reward_group_advantage": (i32, [vp, u32, u32, vp]),
+        "attention_decode_config_fixed128": (DecodeMicrokernelConfig, []),
+        "attention_decode_result_fixed128": (DecodeStepResult, [u32]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_LIB: C.CDLL | None = None
+
+
+def lib() -> C.CDLL:
+    global _LIB
+    if _LIB is None:
+        _LIB = load()
+    return _LIB
+
+
+def _err() -> str:
+    return lib().rl_hip_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RlrtError(f"{what} failed: {_err()}")
+
+
+def ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+# ---------------------------------------------------------------- device
+class DeviceBuffer:
+    """Device allocation owned by Python; freed on close()/GC."""
+
+    def __init__(self, nbytes: int, zero: bool = False):
+        self.nbytes = int(nbytes)
+        p = lib().rl_hip_dev_alloc(max(self.nbytes, 1))
+        if not p:
+            raise RlrtError(f"rl_hip_dev_alloc({nbytes}) failed: {_err()}")
+        self.ptr = p
+        if zero:
+            check(lib().rl_hip_memset_d(p, 0, max(self.nbytes, 1)), "rl_hip_memset_d")
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib().rl_hip_memcpy_h2d(self.ptr + offset, ptr(a), a.nbytes), "rl_hip_memcpy_h2d")
+
+    def download(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().rl_hip_memcpy_d2h(ptr(out), self.ptr + offset, out.nbytes), "rl_hip_memcpy_d2h")
+        return out
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().rl_hip_dev_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def open_device(device: int = 0) -> DeviceInfo:
+    check(lib().rl_hip_open(device), "rl_hip_open")
+    info = DeviceInfo()
+    check(lib().rl_hip_device_info(C.byref(info)), "rl_hip_device_info")
+    return info
+
+
+def sync() -> None:
+    check(lib().rl_hip_sync(), "rl_hip_sync")
+
+
+class Timer:
+    """HIP events on the library stream."""
+
+    def begin(self) -> None:
+        check(lib().rl_hip_timer_begin(), "rl_hip_timer_begin")
+
+    def end(self) -> float:
+        ms = C.c_float()
+        check(lib().rl_hip_timer_end(C.byref(ms)), "rl_hip_timer_end")
+        return float(ms.value)
+
+
+# ---------------------------------------------------------------- kernels
+def attn_args(arena: DeviceBuffer, layout: KvLayoutDesc, table: DeviceBuffer, table_stride: int, batch: int,
+              q_heads: int, kv_heads: int, dtype: int, ctx: DeviceBuffer, max_ctx: int, q: DeviceBuffer,
+              out: DeviceBuffer, out_f32: DeviceBuffer | None = None, chunk_tokens: int = 0,
+              scale: float = 0.0) -> AttnArgs:
+    a = AttnArgs()
+    a.arena_base, a.arena_bytes, a.layout = arena.ptr, arena.nbytes, layout
+    a.block_table, a.table_stride = table.ptr, table_stride
+    a.batch, a.q_heads, a.kv_heads, a.dtype = batch, q_heads, kv_heads, dtype
+    a.ctx_lens, a.max_ctx, a.chunk_tokens, a.scale = ctx.ptr, max_ctx, chunk_tokens, scale
+    a.q, a.out, a.out_f32 = q.ptr, out.ptr, (out_f32.ptr if out_f32 is not None else None)
+    return a
+
+
+def attn_workspace(args: AttnArgs) -> DeviceBuffer:
+    n = lib().rl_hip_attn_decode_workspace(C.byref(args))
+    if n == 0:
+        raise RlrtError(f"rl_hip_attn_decode_workspace: {_err()}")
+    ws = DeviceBuffer(n, zero=True)  # split counters must start at zero
+    args.workspace, args.workspace_bytes = ws.ptr, n
+    return ws
+
+
+def attn_decode(args: AttnArgs) -> None:
+    check(lib().rl_hip_attn_decode(C.byref(args)), "rl_hip_attn_decode")
+
+
+def sample_args(logits: DeviceBuffer, rows: int, vocab: int, row_stride: int, tokens: DeviceBuffer,
+                logprobs: DeviceBuffer, greedy: bool = False, temperature: float = 1.0, top_k: int = 0,
+                top_p: float = 1.0, seed: int = 0, step: int = 0,
+                seeds: DeviceBuffer | None = None) -> SampleArgs:
+    """Scalar parameters for every row; `seeds` (device u64[rows]) overrides `seed`."""
+    s = SampleArgs()
+    s.logits, s.rows, s.vocab, s.row_stride, s.greedy = logits.ptr, rows, vocab, row_stride, int(greedy)
+    s.temperature = s.top_k = s.top_p = None
+    s.seed = seeds.ptr if seeds is not None else None
+    s.temperature_all, s.top_k_all, s.top_p_all, s.seed_all, s.step = temperature, top_k, top_p, seed, step
+    s.token_out, s.logprob_out = tokens.ptr, logprobs.ptr
+    return s
+
+
+def sample_workspace(args: SampleArgs) -> DeviceBuffer:
+    n = lib().rl_hip_sample_workspace(C.byref(args))
+    if n == 0:
+        raise RlrtError(f"rl_hip_sample_workspace: {_err()}")
+    ws = DeviceBuffer(n)
+    args.workspace, args.workspace_bytes = ws.ptr, n
+    return ws
+
+
+def sample(args: SampleArgs) -> None:
+    check(lib().rl_hip_sample(C.byref(args)), "rl_hip_sample")
+
+
+def kv_append(args: AppendArgs) -> None:
+    check(lib().rl_hip_kv_append(C.byref(args)), "rl_hip_kv_append")

@@ -1,0 +1,164 @@
+/*
+ * rl_hip.h - thin C ABI between the host C runtime and the gfx950 kernels.
+ *
+ * The reference launches its kernels from CUDA translation units that
+ * declare __global__ prototypes (src/main.c:39-41, test/test_bench.cu:35-37,
+ * bench/bench_gpu_scheduler.cu:9-10) and allocates with cudaMalloc /
+ * cudaHostAlloc inline. Here every device interaction of the C host code goes
+ * through these extern "C" entry points instead: plain pointers and sizes,
+ * no C++ or framework types. Conventions follow the reference: 0 on success,
+ * -1 on failure (rl_hip_last_error() then holds a message); pointers to
+ * device memory are marked "device".
+ *
+ * Threading: one host thread drives the library at a time. All work is
+ * queued on one non-blocking HIP stream owned by the library (never the
+ * legacy default stream, so a running persistent worker cannot deadlock a
+ * synchronisation behind it).
+ */
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+#include "hw_ring.h"
+#include "kv_layout.h"
+
+RL_EXTERN_C_BEGIN
+
+/* ---- session -------------------------------------------------------------
+ * Replaces the reference's inline cudaSetDevice / cudaGetDeviceProperties
+ * (test/test_bench.cu:333-337, src/main.c:56-60). */
+typedef struct {
+    int32_t device;
+    uint32_t cu_count;            /* hipDeviceAttributeMultiprocessorCount */
+    uint32_t wave_size;
+    uint32_t lds_bytes_per_block; /* max dynamic+static LDS per workgroup */
+    uint32_t clock_khz;
+    uint32_t mem_clock_khz;
+    uint32_t mem_bus_width_bits;
+    uint32_t l2_bytes;
+    uint64_t hbm_bytes;
+    char arch[64];                /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} rl_hip_device_info_t;
+
+int rl_hip_open(int device);
+int rl_hip_close(void);
+int rl_hip_is_open(void);
+int rl_hip_device_info(rl_hip_device_info_t *out);
+const char *rl_hip_last_error(void);
+
+/* ---- memory --------------------------------------------------------------
+ * Coherent host memory replaces cudaHostAlloc(Mapped)
+ * (bench/bench_gpu_scheduler.cu:43-44) and the mmap'd rings of
+ * src/ring.c:10-27; device memory replaces cudaMalloc (src/main.c:84-93). */
+void *rl_hip_host_alloc_coherent(size_t bytes);  /* zero-filled, 4 KiB aligned */
+int rl_hip_host_free(void *p);                   /* -1 if p is not such memory */
+int rl_hip_is_coherent_host(const void *p);      /* 1 if p lies in such memory */
+void *rl_hip_dev_alloc(size_t bytes);
+int rl_hip_is_device_ptr(const void *p);         /* 1 if p is device memory */
+int rl_hip_dev_free(void *p);
+int rl_hip_memcpy_h2d(void *dst_device, const void *src, size_t bytes);
+int rl_hip_memcpy_d2h(void *dst, const void *src_device, size_t bytes);
+int rl_hip_memcpy_d2d(void *dst_device, const void *src_device, size_t bytes);
+int rl_hip_memset_d(void *dst_device, int value, size_t bytes);
+int rl_hip_sync(void);
+
+/* ---- timing on the library stream (HIP events) --------------------------- */
+int rl_hip_timer_begin(void);
+int rl_hip_timer_end(float *elapsed_ms);
+
+#define RL_DTYPE_BF16 0u
+#define RL_DTYPE_FP16 1u
+
+/* ---- paged GQA decode attention -------------------------------------------
+ * Replaces attention_decode_step_fixed128 (cu/attention_decode.cu:60-204)
+ * and its per-descriptor driver process_descriptor (cu/worker.cu:26-64).
+ * One query token per (rollout, q head); q head h reads KV head
+ * h / (q_heads / kv_heads). Rollout b's logical block j of KV head g is
+ * physical block block_table[(b * kv_heads + g) * table_stride + j] of the
+ * arena; tokens [0, ctx_lens[b]) are attended. out = softmax(scale q K^T) V
+ * with fp32 accumulation, stored in the input dtype (and optionally fp32).
+ * ctx_lens[b] == 0 yields zeros. A rollout whose ctx_lens exceeds max_ctx or
+ * whose block table names a block past arena_bytes gets NaN outputs (the
+ * offending block is not read). Long contexts are split into chunks of
+ * `chunk_tokens` processed by different workgroups and merged with an fp32
+ * log-sum-exp combine inside the same launch. */
+typedef struct {
+    const void *arena_base;      /* device: KVArena.base */
+    uint64_t arena_bytes;        /* KVArena.capacity: blocks past it are never read */
+    KvLayoutDesc layout;         /* must pass kv_layout_check_paged */
+    const uint32_t *block_table; /* device */
+    uint32_t table_stride;       /* entries per (rollout, kv head) row */
+    uint32_t batch;
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t dtype;              /* RL_DTYPE_* of q, K, V and out */
+    const uint32_t *ctx_lens;    /* device [batch] */
+    uint32_t max_ctx;            /* upper bound of ctx_lens; sizes the grid */
+    uint32_t chunk_tokens;       /* multiple of 16; 0 selects a default */
+    float scale;                 /* 0 selects 1/sqrt(head_dim) */
+    const void *q;               /* device [batch][q_heads][head_dim] */
+    void *out;                   /* device [batch][q_heads][head_dim] */
+    float *out_f32;              /* device, optional */
+    void *workspace;             /* device, >= rl_hip_attn_decode_workspace() */
+    size_t workspace_bytes;
+} rl_attn_decode_args_t;
+
+size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *args);
+int rl_hip_attn_decode(const rl_attn_decode_args_t *args);
+
+/* ---- sampling -------------------------------------------------------------
+ * Replaces sample_token (cu/sample.cu:41-123) with the specification in
+ * sample.h: greedy, or temperature / top-k (k <= 256) / top-p with a
+ * Philox4x32-10 draw and an integer CDF, plus the token's logprob.
+ * Per-row parameter arrays may be NULL, in which case the *_all scalar is
+ * used for every row. Rows with top_k == 0 or top_k >= vocab and top_p < 1
+ * need a whole-vocabulary nucleus, which this entry point rejects (-1). */
+typedef struct {
+    const float *logits;         /* device [rows][row_stride] fp32 */
+    uint32_t rows;
+    uint32_t vocab;
+    uint32_t row_stride;         /* elements; multiple of 4 */
+    uint32_t greedy;             /* 1: argmax path, parameters ignored */
+    const float *temperature;    /* device [rows] or NULL */
+    const uint32_t *top_k;       /* device [rows] or NULL */
+    const float *top_p;          /* device [rows] or NULL */
+    const uint64_t *seed;        /* device [rows] or NULL */
+    float temperature_all;
+    uint32_t top_k_all;
+    float top_p_all;
+    uint64_t seed_all;
+    uint64_t step;               /* Philox counter of this sampling event */
+    uint32_t *token_out;         /* device [rows] */
+    float *logprob_out;          /* device [rows] */
+    void *workspace;             /* device, >= rl_hip_sample_workspace() */
+    size_t workspace_bytes;
+} rl_sample_args_t;
+
+size_t rl_hip_sample_workspace(const rl_sample_args_t *args);
+int rl_hip_sample(const rl_sample_args_t *args);
+
+/* ---- KV append with copy-on-write ----------------------------------------
+ * Writes one new token per (rollout, kv head): K row and V row into slot
+ * positions[b] % token_count of physical block
+ * block_table[(b * kv_heads + g) * table_stride + positions[b] / token_count].
+ * When cow_src is non-NULL and cow_src[b * kv_heads + g] >= 0, the slots
+ * [0, positions[b] % token_count) of that (shared) source block are first
+ * copied into the destination block: the copy-on-write of a partially
+ * filled prefix block. */
+typedef struct {
+    void *arena_base;            /* device */
+    uint64_t arena_bytes;        /* blocks past it are never written */
+    KvLayoutDesc layout;
+    const uint32_t *block_table; /* device */
+    uint32_t table_stride;
+    uint32_t batch;
+    uint32_t kv_heads;
+    const uint32_t *positions;   /* device [batch]; >= table_stride * token_count: skipped */
+    const int32_t *cow_src;      /* device [batch][kv_heads] or NULL */
+    const void *k_new;           /* device [batch][kv_heads][head_dim] */
+    const void *v_new;           /* device [batch][kv_heads][head_dim] */
+} rl_kv_append_args_t;
+
+int rl_hip_kv_append(const rl_kv_append_args_t *args);
+
+RL_EXTERN_C_END

@@ -1,0 +1,79 @@
+/* Prints sizeof/offsetof of the runtime's ABI structs (include/) as JSON, in
+ * the same key format as oracle/ref_layout.c does for the reference headers. */
+#include <stddef.h>
+#include <stdio.h>
+
+#include "arena.h"
+#include "attention_decode.h"
+#include "completion.h"
+#include "decode_batch.h"
+#include "descriptor.h"
+#include "hw_desc.h"
+#include "hw_ring.h"
+#include "hw_worker_sim.h"
+#include "infer_submit.h"
+#include "kv_layout.h"
+#include "kv_prefix.h"
+#include "request.h"
+#include "reward.h"
+#include "ring.h"
+#include "sample.h"
+
+static int first = 1;
+#define S(T) emit(#T, "sizeof", sizeof(T))
+#define O(T, f) emit(#T, #f, offsetof(T, f))
+
+static void
+emit(const char *t, const char *f, size_t v)
+{
+    printf("%s\n  \"%s.%s\": %zu", first ? "{" : ",", t, f, v);
+    first = 0;
+}
+
+int
+main(void)
+{
+    S(hw_desc_t); O(hw_desc_t, opcode); O(hw_desc_t, flags); O(hw_desc_t, rollout_id);
+    O(hw_desc_t, kv_arena_id); O(hw_desc_t, prefix_id); O(hw_desc_t, kv_offset); O(hw_desc_t, delta_offset);
+    O(hw_desc_t, seq_len); O(hw_desc_t, max_tokens); O(hw_desc_t, reward_model_id); O(hw_desc_t, reserved0);
+    O(hw_desc_t, user_data); O(hw_desc_t, checksum_or_cookie);
+    S(hw_ring_t); O(hw_ring_t, head); O(hw_ring_t, tail); O(hw_ring_t, desc);
+    S(infer_hw_ctx_t); O(infer_hw_ctx_t, cmdq); O(infer_hw_ctx_t, doneq); O(infer_hw_ctx_t, doorbell);
+    O(infer_hw_ctx_t, gpu_group_id); O(infer_hw_ctx_t, kv_arena_id);
+    S(hw_worker_sim_t); O(hw_worker_sim_t, stop); O(hw_worker_sim_t, decoded_tokens); O(hw_worker_sim_t, completions);
+    S(Descriptor); O(Descriptor, seq_id); O(Descriptor, kv_block_offset); O(Descriptor, num_kv_blocks);
+    O(Descriptor, attention_flags); O(Descriptor, pad); O(Descriptor, output_token_offset);
+    O(Descriptor, reward_cookie); O(Descriptor, batch_size); O(Descriptor, batch_index);
+    S(CommandRing); O(CommandRing, cons); O(CommandRing, prod); O(CommandRing, slots);
+    S(Completion); O(Completion, seq_id); O(Completion, token_id); O(Completion, kv_block_offset);
+    O(Completion, reward_cookie); O(Completion, cycles_taken);
+    S(CompletionRing); O(CompletionRing, cons); O(CompletionRing, prod); O(CompletionRing, overflow);
+    O(CompletionRing, slots);
+    S(DecodeDispatchBatch); O(DecodeDispatchBatch, descs); S(DecodeBatchContract);
+    S(RolloutRequest); O(RolloutRequest, request_id); O(RolloutRequest, max_tokens); O(RolloutRequest, kv_blocks);
+    O(RolloutRequest, temperature); O(RolloutRequest, top_k); O(RolloutRequest, top_p); O(RolloutRequest, rng_seed);
+    S(RolloutDone); O(RolloutDone, request_id); O(RolloutDone, rollout_id); O(RolloutDone, tokens_generated);
+    O(RolloutDone, reward); O(RolloutDone, status);
+    S(RequestRing); O(RequestRing, prod); O(RequestRing, slots);
+    S(DoneRing); O(DoneRing, prod); O(DoneRing, overflow); O(DoneRing, slots);
+    S(GpuRolloutSlot); O(GpuRolloutSlot, rng_state); O(GpuRolloutSlot, temperature); O(GpuRolloutSlot, top_k);
+    O(GpuRolloutSlot, top_p);
+    S(GpuRolloutState); O(GpuRolloutState, bitmap);
+    S(KVArena); O(KVArena, base); O(KVArena, capacity); O(KVArena, block_size); O(KVArena, bitmap);
+    S(KvLayoutDesc); O(KvLayoutDesc, block_bytes); O(KvLayoutDesc, alignment);
+    S(RewardDesc); O(RewardDesc, reward); O(RewardDesc, flags);
+    /* not compilable from the reference headers: pinned by Appendix-A arithmetic */
+    S(KVPrefix); O(KVPrefix, refcnt); O(KVPrefix, kv_block_offset); O(KVPrefix, token_len);
+    O(KVPrefix, kv_block_count); O(KVPrefix, flags);
+    S(KVBranch); O(KVBranch, prefix_id); O(KVBranch, delta_kv_offset); O(KVBranch, delta_len);
+    O(KVBranch, delta_block_count); O(KVBranch, state); O(KVBranch, flags);
+    S(KVPrefixTable); O(KVPrefixTable, prefix_bitmap); O(KVPrefixTable, branches);
+    O(KVPrefixTable, branch_bitmap); O(KVPrefixTable, next_branch_id);
+    S(SampleState); O(SampleState, temperature); O(SampleState, top_k); O(SampleState, top_p);
+    O(SampleState, vocab_size);
+    S(DecodeStepArgs); O(DecodeStepArgs, seq_len); O(DecodeStepArgs, output_token_offset);
+    S(DecodeStepResult); O(DecodeStepResult, cycle_estimate);
+    S(DecodeMicrokernelConfig);
+    printf("\n}\n");
+    return 0;
+}

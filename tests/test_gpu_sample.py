@@ -1,0 +1,83 @@
+"""On-device sampling vs the oracle: token ids bit-exact, logprobs within 1e-4."""
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(rl, logits, vocab=None, greedy=False, temperature=1.0, top_k=0, top_p=1.0, seeds=None, step=0):
+    rows, stride = logits.shape
+    vocab = stride if vocab is None else vocab
+    lg = rl.DeviceBuffer.from_array(np.ascontiguousarray(logits, dtype=np.float32))
+    tok = rl.DeviceBuffer(rows * 4)
+    lp = rl.DeviceBuffer(rows * 4)
+    sd = rl.DeviceBuffer.from_array(np.asarray(seeds, dtype=np.uint64)) if seeds is not None else None
+    args = rl.sample_args(lg, rows, vocab, stride, tok, lp, greedy=greedy, temperature=temperature, top_k=top_k,
+                          top_p=top_p, step=step, seeds=sd)
+    ws = rl.sample_workspace(args)
+    rl.sample(args)
+    rl.sync()
+    out = tok.download(np.uint32, rows), lp.download(np.float32, rows)
+    for b in (lg, tok, lp, ws) + ((sd,) if sd is not None else ()):
+        b.close()
+    return out
+
+
+def _check(rl, orc, olib, logits, vocab=None, **kw):
+    rows, stride = logits.shape
+    print(f"[sample] rows={rows} vocab={vocab or stride} {kw.get('greedy')} T={kw.get('temperature')} "
+          f"k={kw.get('top_k')} p={kw.get('top_p')} step={kw.get('step', 0)}", flush=True)
+    gt, gl = _run(rl, logits, vocab=vocab, **kw)
+    seeds = kw.get("seeds")
+    ot, ol = orc.sample_rows(olib, logits, kw.get("greedy", False), kw.get("temperature", 1.0), kw.get("top_k", 0),
+                             kw.get("top_p", 1.0), seeds if seeds is not None else 0, kw.get("step", 0), vocab=vocab)
+    bad = np.nonzero(gt != ot)[0]
+    assert bad.size == 0, (bad[:10], gt[bad[:10]], ot[bad[:10]])
+    assert np.abs(gl.astype(np.float64) - ol).max() < 1e-4
+    return gt
+
+
+def test_greedy_config3_shape_with_spike_ties(rl, gpu, orc, olib):
+    """256 rows x 128,256 fp32 ~N(0,1) with 5 spike tokens per row SET to 8.0
+    (5-way ties: the lowest index must win)."""
+    x = synth.make_logits(3, 256, 128256, spikes=5)
+    tok = _check(rl, orc, olib, x, greedy=True)
+    for r in range(0, 256, 37):
+        assert tok[r] == np.flatnonzero(x[r] == np.float32(8.0)).min()
+
+
+def test_topk_topp_config3(rl, gpu, orc, olib):
+    """Temperature 0.8, top-k 50, top-p 0.9, Philox per-row seed, several steps."""
+    x = synth.make_logits(3, 256, 128256, spikes=5)
+    seeds = np.random.default_rng(33).integers(0, 2**63, 256, dtype=np.uint64)
+    prev = None
+    for step in (0, 1, 12345):
+        tok = _check(rl, orc, olib, x, temperature=0.8, top_k=50, top_p=0.9, seeds=seeds, step=step)
+        if prev is not None:
+            assert (tok != prev).any()
+        prev = tok
+
+
+@pytest.mark.parametrize("vocab,stride", [(32000, 32000), (50257, 50260), (1000, 1000), (16384, 16384),
+                                          (16385, 16388)])
+@pytest.mark.parametrize("k,p,T", [(1, 1.0, 1.0), (50, 0.9, 0.8), (256, 0.95, 1.3), (300, 0.5, 1.0),
+                                   (7, 0.05, 0.6)])
+def test_vocab_and_parameter_grid(rl, gpu, orc, olib, vocab, stride, k, p, T):
+    rng = np.random.default_rng(vocab + k)
+    x = np.full((24, stride), -1e30, dtype=np.float32)
+    x[:, :vocab] = rng.standard_normal((24, vocab), dtype=np.float32) * 2
+    x[3, :vocab] = np.round(x[3, :vocab])                    # heavy ties, also at the cutoff
+    x[5, :vocab] = 0.0                                       # all equal
+    x[7, :vocab] = -np.inf
+    x[7, vocab // 2] = 1.0                                   # one finite logit
+    _check(rl, orc, olib, x, vocab=vocab, temperature=T, top_k=k, top_p=p,
+           seeds=np.arange(24, dtype=np.uint64) * 7919 + 1, step=3)
+    _check(rl, orc, olib, x, vocab=vocab, greedy=True)
+
+
+def test_whole_vocab_nucleus_is_rejected(rl, gpu):
+    x = np.zeros((2, 1000), dtype=np.float32)
+    with pytest.raises(rl.RlrtError):
+        _run(rl, x, temperature=1.0, top_k=0, top_p=0.9)
