@@ -198,9 +198,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append"])
+    ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--chunk", type=int, default=0, help="attention split-KV chunk in tokens (0: library default)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the decode hot path on one GPU only; multi-GPU runs are not part of it "
@@ -209,7 +210,24 @@ def main():
 
     info = rlrt.open_device(0)
     log(f"[bench] device {info.arch.decode()} cu={info.cu_count} clock={info.clock_khz / 1e3:.0f} MHz")
+    if args.only == "copy":
+        # calibration for the PMC byte counters: device copies of a known size
+        n = 256 << 20
+        a, b = rlrt.DeviceBuffer(n), rlrt.DeviceBuffer(n)
+        rlrt.check(rlrt.lib().rl_hip_memset_d(a.ptr, 1, n), "memset")
+        rlrt.sync()
+        timer = rlrt.Timer()
+        timer.begin()
+        for _ in range(args.steps):
+            rlrt.check(rlrt.lib().rl_hip_memcpy_d2d(b.ptr, a.ptr, n), "d2d")
+        ms = timer.end()
+        print(json.dumps({"only": "copy", "bytes_per_copy": n, "avg_launch_us": ms / args.steps * 1e3,
+                          "gbps_read_plus_write": 2 * n / (ms / args.steps * 1e-3) / 1e9}), flush=True)
+        return
     step = Step()
+    step.attn.chunk_tokens = args.chunk
+    if args.chunk:
+        step.attn_ws = rlrt.attn_workspace(step.attn)
 
     for i in range(args.warmup):
         step.run(i, args.only)

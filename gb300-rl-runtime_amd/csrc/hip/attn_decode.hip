@@ -21,9 +21,12 @@
 //         row_mirror); p and the rescale factor go through LDS.
 //  PV     lane owns one dword (2 dims) of V for every head of the group, so
 //         each V element is converted to fp32 once; p is a broadcast LDS read.
-//  merge  waves of a workgroup merge through LDS; chunks of one rollout merge
-//         with an fp32 log-sum-exp combine done by the last workgroup to
-//         finish (device-scope counter, self-resetting).
+//  merge  waves of a workgroup merge through LDS; the chunks of a long
+//         context write fp32 partials (max, sum, unnormalised output) that a
+//         second small kernel combines with an fp32 log-sum-exp merge. (A
+//         last-workgroup merge inside the same launch needs agent-scope
+//         release/acquire fences, which on gfx950 write back and invalidate
+//         the whole L2 of the XCD for every workgroup: measured 12x slower.)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -54,7 +57,6 @@ struct AttnParams {
     uint32_t max_chunks;
     float *ws_o;           // [rollout][kv_head][chunk][G][D]
     float *ws_ml;          // [rollout][kv_head][chunk][G][2]
-    uint32_t *ws_cnt;      // [rollout][kv_head]
 };
 
 template <int D, int G, int DT, int TPB, int W>
@@ -239,7 +241,6 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
     __shared__ __attribute__((aligned(1024))) uint8_t lds_stage0[C::STAGE0_BYTES];
     __shared__ __attribute__((aligned(1024))) uint8_t lds_stage1[W * C::STAGE];
     __shared__ float lds_p[W * C::PBUF];
-    __shared__ uint32_t s_last;
     __shared__ uint32_t s_bad;
 
     const int lane = threadIdx.x & 63;
@@ -415,32 +416,35 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
             }
         }
     }
-    if (!split)
-        return;
+}
 
-    // ---- cross-chunk log-sum-exp merge by the last workgroup -------------------
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = (atomicAdd(&p.ws_cnt[row_id], 1u) == nchunks - 1) ? 1u : 0u;
-    __syncthreads();
-    if (!s_last)
-        return;
-    __threadfence();
-
+// Combines the chunk partials of every split (rollout, kv head):
+// M = max_c m_c, L = sum_c l_c 2^(m_c - M), O = sum_c o_c 2^(m_c - M), out = O / L.
+template <int D, int G, int DT>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
+{
+    const uint32_t g = blockIdx.x;
+    const uint32_t b = blockIdx.y;
+    const uint32_t ctx_in = rl_sload(p.ctx + b);
+    const uint32_t ctx = ctx_in > p.max_ctx ? p.max_ctx : ctx_in;
+    const uint32_t ntiles = (ctx + kTileTokens - 1) / kTileTokens;
+    const uint32_t nchunks = (ntiles + p.chunk_tiles - 1) / p.chunk_tiles;
+    if (nchunks <= 1)
+        return;  // written directly by the decode kernel
+    const uint32_t row_id = b * p.kv_heads + g;
     const float *row_o = p.ws_o + (size_t)row_id * p.max_chunks * G * D;
     const float *row_ml = p.ws_ml + (size_t)row_id * p.max_chunks * G * 2;
-    for (int e = threadIdx.x; e < G * D; e += W * 64) {
+    for (int e = threadIdx.x; e < G * D; e += 256) {
         const int h = e / D;
         float M = -INFINITY;
         for (uint32_t c = 0; c < nchunks; c++)
-            M = fmaxf(M, __builtin_nontemporal_load(&row_ml[(c * G + h) * 2]));
+            M = fmaxf(M, row_ml[(c * G + h) * 2]);
         float L = 0.f, O = 0.f;
         for (uint32_t c = 0; c < nchunks; c++) {
-            const float mc = __builtin_nontemporal_load(&row_ml[(c * G + h) * 2]);
+            const float mc = row_ml[(c * G + h) * 2];
             const float f = (mc == -INFINITY) ? 0.f : exp2f(mc - M);
-            L = fmaf(__builtin_nontemporal_load(&row_ml[(c * G + h) * 2 + 1]), f, L);
-            O = fmaf(__builtin_nontemporal_load(&row_o[c * G * D + e]), f, O);
+            L = fmaf(row_ml[(c * G + h) * 2 + 1], f, L);
+            O = fmaf(row_o[c * G * D + e], f, O);
         }
         const float v = (L > 0.f || L != L) ? O / L : 0.f;
         const size_t o = ((size_t)b * p.q_heads + g * G) * D + e;
@@ -448,8 +452,6 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
         if (p.out_f32)
             p.out_f32[o] = v;
     }
-    if (threadIdx.x == 0)
-        p.ws_cnt[row_id] = 0u;
 }
 
 }  // namespace
@@ -471,7 +473,7 @@ constexpr int waves_for()
 constexpr uint32_t kDefaultChunkTokens = 512;
 
 struct WsLayout {
-    size_t cnt_off, ml_off, o_off, total;
+    size_t ml_off, o_off, total;
 };
 
 WsLayout ws_layout(const rl_attn_decode_args_t *a, uint32_t chunk_tiles)
@@ -482,8 +484,7 @@ WsLayout ws_layout(const rl_attn_decode_args_t *a, uint32_t chunk_tiles)
     const uint32_t max_chunks = max_tiles == 0 ? 1 : (max_tiles + chunk_tiles - 1) / chunk_tiles;
     const size_t rows = (size_t)a->batch * a->kv_heads;
     WsLayout w;
-    w.cnt_off = 0;
-    w.ml_off = ((rows * 4 + 255) / 256) * 256;
+    w.ml_off = 0;
     w.o_off = w.ml_off + ((rows * max_chunks * G * 2 * 4 + 255) / 256) * 256;
     w.total = w.o_off + rows * max_chunks * G * D * 4;
     return w;
@@ -501,7 +502,13 @@ int launch(const AttnParams &p, dim3 grid)
     constexpr int W = waves_for<D, G>();
     auto kern = attn_decode_kernel<D, G, DT, TPB, W>;
     hipLaunchKernelGGL(kern, grid, dim3(W * 64), 0, rl_stream(), p);
-    return rl_check_launch("attn_decode_kernel launch");
+    if (rl_check_launch("attn_decode_kernel launch"))
+        return -1;
+    if (grid.x > 1) {
+        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(grid.y, grid.z), dim3(256), 0, rl_stream(), p);
+        return rl_check_launch("attn_merge_kernel launch");
+    }
+    return 0;
 }
 
 template <int D, int G, int DT>
@@ -615,7 +622,6 @@ extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
     p.chunk_tiles = chunk_tiles;
     p.max_chunks = max_chunks;
     uint8_t *ws = (uint8_t *)a->workspace;
-    p.ws_cnt = (uint32_t *)(ws + w.cnt_off);
     p.ws_ml = (float *)(ws + w.ml_off);
     p.ws_o = (float *)(ws + w.o_off);
 

@@ -36,7 +36,6 @@ constexpr int kSplitLen = kThreads * kPerThread;  // 16,384 elements
 constexpr int kCandCap = 1024;                    // candidates per split
 constexpr int kMergeCap = 8192;                   // candidates per row in the merge
 constexpr int kKeptCap = 1024;                    // kept (top-k with ties) per row
-constexpr uint32_t kOverflowToken = 0xFFFFFFFFu;
 
 struct SplitStat {
     float max_x;     // slice max of x
@@ -311,14 +310,172 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
     return v;
 }
 
-__device__ __forceinline__ void write_failure(const SampleParams &p, uint32_t row)
-{
-    p.token_out[row] = kOverflowToken;
-    p.logprob_out[row] = __builtin_nanf("");
-}
 
 // One wave per row: every barrier below is a single-wave s_barrier.
 constexpr int kMergeThreads = 64;
+
+// ---- exact full-row path -----------------------------------------------------
+// Used for rows without top-k (whole-vocabulary nucleus) and for rows whose
+// top-k candidates overflow the slice buffers (massive ties). Streams the row
+// from global memory (L2-resident after the first pass) several times:
+// radix select of the top-k cutoff on the float keys; the kept weight W_K; the
+// nucleus boundary as an exact 64-bit composite key (float key, ~index) found
+// by MSB-first radix search on weight histograms; W_P; the ascending-index
+// integer CDF walk.
+__device__ __forceinline__ uint64_t composite_key(uint32_t key, uint32_t idx)
+{
+    return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+
+__device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff, float topp,
+                                     float m, uint32_t *s_hist, unsigned long long *s_whist)
+{
+    const int lane = threadIdx.x;
+    const float *l = p.logits + (size_t)row * p.row_stride;
+    const uint32_t V = p.vocab;
+
+    // (1) cutoff key: k_eff-th largest finite x (multiplicity counted); 0 keeps all.
+    uint32_t cutoff = 0;
+    if (k_eff) {
+        uint32_t prefix = 0, mask = 0, need = k_eff;
+        for (int pass = 3; pass >= 0; pass--) {
+            const int shift = pass * 8;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                s_hist[lane * 4 + b] = 0;
+            __syncthreads();
+            for (uint32_t i = lane; i < V; i += kMergeThreads) {
+                const float x = l[i] * inv_t;
+                const uint32_t key = rl_float_key(x);
+                if (x != -INFINITY && (key & mask) == prefix)
+                    atomicAdd(&s_hist[(key >> shift) & 0xFFu], 1u);
+            }
+            __syncthreads();
+            if (lane == 0) {
+                uint32_t acc = 0;
+                int d = 255;
+                for (; d > 0; d--) {
+                    if (acc + s_hist[d] >= need)
+                        break;
+                    acc += s_hist[d];
+                }
+                s_hist[256] = (uint32_t)d;
+                s_hist[257] = need - acc;
+            }
+            __syncthreads();
+            prefix |= s_hist[256] << shift;
+            mask |= 0xFFu << shift;
+            need = s_hist[257];
+            __syncthreads();
+        }
+        cutoff = prefix;
+    }
+
+    // (2) W_K
+    uint64_t wk_own = 0;
+    for (uint32_t i = lane; i < V; i += kMergeThreads) {
+        const float x = l[i] * inv_t;
+        if (x != -INFINITY && rl_float_key(x) >= cutoff)
+            wk_own += rl_sample_weight(x - m);
+    }
+    const uint64_t wk = __shfl(wave_inclusive_scan_u64(wk_own), 63);
+
+    // (3) nucleus boundary tau: the largest composite key whose suffix weight reaches thr.
+    uint64_t tau = 0;
+    if (topp > 0.f && topp < 1.f) {
+        const uint64_t thr = rl_topp_threshold(topp, wk);
+        uint64_t prefix = 0, mask = 0, above = 0;
+        for (int pass = 7; pass >= 0; pass--) {
+            const int shift = pass * 8;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                s_whist[lane * 4 + b] = 0;
+            __syncthreads();
+            for (uint32_t i = lane; i < V; i += kMergeThreads) {
+                const float x = l[i] * inv_t;
+                const uint32_t key = rl_float_key(x);
+                if (x == -INFINITY || key < cutoff)
+                    continue;
+                const uint64_t ck = composite_key(key, i);
+                if ((ck & mask) == prefix)
+                    atomicAdd(&s_whist[(ck >> shift) & 0xFFu], (unsigned long long)rl_sample_weight(x - m));
+            }
+            __syncthreads();
+            if (lane == 0) {
+                // Highest digit whose cumulative weight from the top reaches thr
+                // (thr >= 1 whenever K is non-empty: the row maximum weighs 2^24).
+                uint64_t acc = above;
+                int d = 255;
+                for (; d > 0; d--) {
+                    if (acc + s_whist[d] >= thr)
+                        break;
+                    acc += s_whist[d];
+                }
+                s_whist[256] = (unsigned long long)d;
+                s_whist[257] = acc;
+            }
+            __syncthreads();
+            prefix |= (uint64_t)s_whist[256] << shift;
+            mask |= 0xFFull << shift;
+            above = s_whist[257];
+            __syncthreads();
+        }
+        tau = prefix;
+    }
+
+    // (4) W_P and the lowest index of P
+    uint64_t wp_own = 0;
+    uint32_t lowest = 0xFFFFFFFFu;
+    for (uint32_t i = lane; i < V; i += kMergeThreads) {
+        const float x = l[i] * inv_t;
+        const uint32_t key = rl_float_key(x);
+        if (x != -INFINITY && key >= cutoff && composite_key(key, i) >= tau) {
+            wp_own += rl_sample_weight(x - m);
+            lowest = min(lowest, i);
+        }
+    }
+    const uint64_t wp = __shfl(wave_inclusive_scan_u64(wp_own), 63);
+    lowest = wave_min_u32(lowest);
+
+    // (5) ascending-index walk: chunks of 64 lanes x 8 contiguous elements
+    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+    uint64_t carry = 0;
+    uint32_t tok = 0xFFFFFFFFu;
+    for (uint32_t base = 0; base < V && tok == 0xFFFFFFFFu; base += kMergeThreads * 8) {
+        uint64_t w8[8], own = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const uint32_t i = base + lane * 8 + e;
+            w8[e] = 0;
+            if (i < V) {
+                const float x = l[i] * inv_t;
+                const uint32_t key = rl_float_key(x);
+                if (x != -INFINITY && key >= cutoff && composite_key(key, i) >= tau)
+                    w8[e] = rl_sample_weight(x - m);
+            }
+            own += w8[e];
+        }
+        const uint64_t incl = wave_inclusive_scan_u64(own);
+        const uint64_t total = __shfl(incl, 63);
+        if (carry + total > u) {
+            uint64_t c = carry + incl - own;
+            uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                c += w8[e];
+                if (cand == 0xFFFFFFFFu && c > u)
+                    cand = base + lane * 8 + e;
+            }
+            tok = wave_min_u32(cand);
+        }
+        carry += total;
+    }
+    if (tok == 0xFFFFFFFFu)
+        tok = lowest;        // zero total weight: lowest index of P
+    if (tok >= V)
+        tok = 0;             // every logit -inf
+    return tok;
+}
 
 __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParams p)
 {
@@ -326,7 +483,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const int lane = threadIdx.x;
 
     __shared__ uint2 s_cand[kMergeCap];
-    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_hist[258];
+    __shared__ unsigned long long s_whist[258];
     __shared__ uint64_t s_sort[kKeptCap];
     __shared__ uint32_t s_w[kKeptCap];
     __shared__ uint32_t s_nk;
@@ -363,19 +521,16 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const float inv_t = 1.0f / row_temperature(p, row);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
     const float topp = row_topp(p, row);
-    if (k_eff == 0) {  // whole-vocabulary nucleus: rejected on the host
-        if (lane == 0)
-            write_failure(p, row);
-        return;
-    }
-
     // ---- gather the slices' candidates --------------------------------------
     const bool split_over = __ballot(ncand > (uint32_t)kCandCap) != 0;
     const uint64_t cum = wave_inclusive_scan_u64(ncand);
     const uint32_t n = (uint32_t)__shfl(cum, 63);
-    if (split_over || n > (uint32_t)kMergeCap) {
-        if (lane == 0)
-            write_failure(p, row);
+    if (k_eff == 0 || split_over || n > (uint32_t)kMergeCap) {
+        const uint32_t tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist);
+        if (lane == 0) {
+            p.token_out[row] = tok;
+            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+        }
         return;
     }
     for (uint32_t s = 0; s < p.splits; s++) {
@@ -455,8 +610,11 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     __syncthreads();
     const uint32_t nk = s_nk;
     if (nk > (uint32_t)kKeptCap) {
-        if (lane == 0)
-            write_failure(p, row);
+        const uint32_t tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist);
+        if (lane == 0) {
+            p.token_out[row] = tok;
+            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+        }
         return;
     }
     uint32_t np2 = 1;
@@ -574,14 +732,6 @@ int validate(const rl_sample_args_t *a)
     if (splits_for(a->vocab) > 64) {
         rl_set_error("rl_hip_sample: vocab %u exceeds %d elements", a->vocab, 64 * kSplitLen);
         return -1;
-    }
-    if (!a->greedy) {
-        // Whole-vocabulary nucleus (no top-k) is not served by this entry point.
-        const uint32_t k = a->top_k_all;
-        if (!a->top_k && (k == 0 || k >= a->vocab) && a->temperature_all > 0.f) {
-            rl_set_error("rl_hip_sample: top_k must be in [1, vocab) for sampling (got %u)", k);
-            return -1;
-        }
     }
     return 0;
 }

@@ -81,7 +81,7 @@ int rl_hip_timer_end(float *elapsed_ms);
  * whose block table names a block past arena_bytes gets NaN outputs (the
  * offending block is not read). Long contexts are split into chunks of
  * `chunk_tokens` processed by different workgroups and merged with an fp32
- * log-sum-exp combine inside the same launch. */
+ * log-sum-exp combine (a second, small kernel on the same stream). */
 typedef struct {
     const void *arena_base;      /* device: KVArena.base */
     uint64_t arena_bytes;        /* KVArena.capacity: blocks past it are never read */

@@ -1,9 +1,11 @@
 """Paged GQA decode attention on the GPU vs the fp64 oracle.
 
-Tolerance (stated by the task for floating point): attention outputs within
-2e-3 relative (bf16 in, fp32 accumulate), measured row-normalised
-(max_d |delta| / max_d |ref| per rollout and head); the fp32 output within
-1e-4; the bf16/fp16 output bit-equal to the RNE rounding of the fp32 output.
+Tolerance: attention outputs within 2e-3 relative (bf16 in, fp32
+accumulate), measured row-normalised (max_d |delta| / max_d |ref| per rollout
+and head) on the fp32-accumulated result, which is held to 1e-4. The stored
+bf16/fp16 output must be bit-equal to the round-to-nearest-even of that fp32
+value; its own rounding (up to 2^-8 relative for bf16) is the format's, not
+the kernel's.
 """
 import numpy as np
 import pytest
@@ -97,7 +99,7 @@ def test_guards_poison_instead_of_faulting(rl, gpu, orc, olib):
     that rollout only (the bad block is never read)."""
     w = synth.make_decode(10, 3, 8, 2, 128, 100, 100, dtype="bf16")
     w.ctx[1] = 130                                  # > max_ctx passed below
-    w.table[2, 1, 3] = 10_000_000                   # far outside the arena
+    w.table[2, 1, 3] = 10_000_000                   # far outside the arena (kv head 1 = q heads 4..7)
     out16, out32 = gh.run_attn(rl, w, max_ctx=100)
-    assert np.isnan(out32[1]).all() and np.isnan(out32[2, 2:4]).all()
-    assert np.isfinite(out32[0]).all() and np.isfinite(out32[2, :2]).all()
+    assert np.isnan(out32[1]).all() and np.isnan(out32[2, 4:8]).all()
+    assert np.isfinite(out32[0]).all() and np.isfinite(out32[2, :4]).all()

@@ -35,7 +35,7 @@ def _check(rl, orc, olib, logits, vocab=None, **kw):
                              kw.get("top_p", 1.0), seeds if seeds is not None else 0, kw.get("step", 0), vocab=vocab)
     bad = np.nonzero(gt != ot)[0]
     assert bad.size == 0, (bad[:10], gt[bad[:10]], ot[bad[:10]])
-    assert np.abs(gl.astype(np.float64) - ol).max() < 1e-4
+    np.testing.assert_allclose(gl.astype(np.float64), ol, rtol=0, atol=1e-4, equal_nan=True)
     return gt
 
 
@@ -77,7 +77,24 @@ def test_vocab_and_parameter_grid(rl, gpu, orc, olib, vocab, stride, k, p, T):
     _check(rl, orc, olib, x, vocab=vocab, greedy=True)
 
 
-def test_whole_vocab_nucleus_is_rejected(rl, gpu):
-    x = np.zeros((2, 1000), dtype=np.float32)
-    with pytest.raises(rl.RlrtError):
-        _run(rl, x, temperature=1.0, top_k=0, top_p=0.9)
+def test_whole_vocab_nucleus_rollout_shape(rl, gpu, orc, olib):
+    """Top-p 0.9 with no top-k over 32,000 logits (the rollout-loop sampler):
+    the exact full-row path, 512 rows."""
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((512, 32000), dtype=np.float32) * np.float32(0.3)
+    seeds = rng.integers(0, 2**63, 512, dtype=np.uint64)
+    _check(rl, orc, olib, x, temperature=1.0, top_k=0, top_p=0.9, seeds=seeds, step=5)
+
+
+@pytest.mark.parametrize("k", [0, 3])
+def test_exact_path_edge_rows(rl, gpu, orc, olib, k):
+    """Rows forcing the exact path: every logit equal, heavy ties, all -inf."""
+    x = np.zeros((6, 20000), dtype=np.float32)
+    x[1] = np.round(np.random.default_rng(1).standard_normal(20000) * 2)
+    x[2, :] = -np.inf
+    x[3, :] = -np.inf
+    x[3, 12345] = 0.5
+    x[4, ::2] = 1.0
+    x[5] = np.random.default_rng(2).standard_normal(20000)
+    for p in (1.0, 0.9, 0.3):
+        _check(rl, orc, olib, x, temperature=0.7, top_k=k, top_p=p, seeds=np.arange(6, dtype=np.uint64) + 9, step=2)
