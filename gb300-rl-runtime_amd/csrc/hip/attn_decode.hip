@@ -92,10 +92,25 @@ struct WaveState {
 };
 
 // Issues the HBM -> LDS copies of one unit (NT tiles, K and V planes).
+// The chunk's block-table entries, loaded once into VGPRs (entry j of the
+// chunk in lane j % 64 of word j / 64) so that no table load latency sits
+// between consuming a unit and issuing the next unit's copies.
+struct ChunkTable {
+    uint32_t w0, w1;
+    uint32_t first;  // first logical block of the chunk
+
+    __device__ __forceinline__ uint32_t block(uint32_t logical) const
+    {
+        const uint32_t j = logical - first;  // wave-uniform, < 128
+        const uint32_t v = j < 64 ? w0 : w1;
+        return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)(j & 63));
+    }
+};
+
 // Returns false if the block table names a block outside the arena (that
 // block is not read).
 template <int D, int G, int DT, int TPB, int W>
-__device__ __forceinline__ bool stage_unit(const AttnParams &p, const uint32_t *table_row, uint32_t tile0,
+__device__ __forceinline__ bool stage_unit(const AttnParams &p, const ChunkTable &tbl, uint32_t tile0,
                                            uint32_t tile_end, uint32_t lane_off, RL_LDS uint8_t *dst)
 {
     using C = Cfg<D, G, DT, TPB, W>;
@@ -104,7 +119,7 @@ __device__ __forceinline__ bool stage_unit(const AttnParams &p, const uint32_t *
     for (int n = 0; n < C::NT; n++) {
         const uint32_t tile = tile0 + n;
         if (tile < tile_end) {
-            const uint32_t blk = rl_sload(table_row + tile / C::SUB);
+            const uint32_t blk = tbl.block(tile / C::SUB);
             if (blk >= p.arena_blocks) {
                 ok = false;
                 continue;
@@ -276,8 +291,15 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
     const uint32_t tile_begin = chunk * p.chunk_tiles;
     const uint32_t tile_end = min(tile_begin + p.chunk_tiles, ntiles);
     const uint32_t units = (tile_end - tile_begin + C::NT - 1) / C::NT;
-    const uint32_t *table_row = p.table + (size_t)row_id * p.table_stride;
     const uint32_t lane_off = (uint32_t)lane * 16u;
+    ChunkTable tbl;
+    {
+        const uint32_t *table_row = p.table + (size_t)row_id * p.table_stride;
+        tbl.first = tile_begin / C::SUB;
+        const uint32_t last = (tile_end + C::SUB - 1) / C::SUB;  // one past the chunk's last block
+        tbl.w0 = (tbl.first + lane < last) ? table_row[tbl.first + lane] : 0u;
+        tbl.w1 = (tbl.first + 64 + lane < last) ? table_row[tbl.first + 64 + lane] : 0u;
+    }
 
     RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_stage0 + wave * C::STAGE;
     RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_stage1 + wave * C::STAGE;
@@ -315,9 +337,9 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
     constexpr int UNIT_OPS = C::NT == 1 ? 2 * (C::PLANE / 1024) : 0;
 
     if ((uint32_t)wave < units)
-        bad |= !stage_unit<D, G, DT, TPB, W>(p, table_row, tile_begin + wave * C::NT, tile_end, lane_off, st0);
+        bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + wave * C::NT, tile_end, lane_off, st0);
     if ((uint32_t)wave + W < units)
-        bad |= !stage_unit<D, G, DT, TPB, W>(p, table_row, tile_begin + (wave + W) * C::NT, tile_end, lane_off, st1);
+        bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (wave + W) * C::NT, tile_end, lane_off, st1);
 
     for (uint32_t u = wave; u < units; u += 2 * W) {
         // stage 0 holds unit u; stage 1 may hold unit u + W (in flight)
@@ -328,7 +350,7 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
         consume_any<D, G, DT, TPB, W>(p, ws, st0, pbuf, (tile_begin + u * C::NT) * kTileTokens, ctx, lane);
         if (u + 2 * W < units) {
             rl_wait_lgkmcnt0();
-            bad |= !stage_unit<D, G, DT, TPB, W>(p, table_row, tile_begin + (u + 2 * W) * C::NT, tile_end, lane_off,
+            bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (u + 2 * W) * C::NT, tile_end, lane_off,
                                                  st0);
         }
         if (u + W >= units)
@@ -342,7 +364,7 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
                                        lane);
         if (u + 3 * W < units) {
             rl_wait_lgkmcnt0();
-            bad |= !stage_unit<D, G, DT, TPB, W>(p, table_row, tile_begin + (u + 3 * W) * C::NT, tile_end, lane_off,
+            bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (u + 3 * W) * C::NT, tile_end, lane_off,
                                                  st1);
         }
     }
@@ -420,9 +442,15 @@ __global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
 
 // Combines the chunk partials of every split (rollout, kv head):
 // M = max_c m_c, L = sum_c l_c 2^(m_c - M), O = sum_c o_c 2^(m_c - M), out = O / L.
+// The per-chunk scale factors go through LDS so every partial-output load
+// is independent of the others and they can all be in flight together.
+constexpr int kMergeMaxChunks = 128;
+
 template <int D, int G, int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
 {
+    __shared__ float s_f[kMergeMaxChunks * G];
+    __shared__ float s_l[G];
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
     const uint32_t ctx_in = rl_sload(p.ctx + b);
@@ -434,18 +462,28 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
     const uint32_t row_id = b * p.kv_heads + g;
     const float *row_o = p.ws_o + (size_t)row_id * p.max_chunks * G * D;
     const float *row_ml = p.ws_ml + (size_t)row_id * p.max_chunks * G * 2;
-    for (int e = threadIdx.x; e < G * D; e += 256) {
-        const int h = e / D;
+    if (threadIdx.x < G) {
+        const int h = threadIdx.x;
         float M = -INFINITY;
         for (uint32_t c = 0; c < nchunks; c++)
             M = fmaxf(M, row_ml[(c * G + h) * 2]);
-        float L = 0.f, O = 0.f;
+        float L = 0.f;
         for (uint32_t c = 0; c < nchunks; c++) {
             const float mc = row_ml[(c * G + h) * 2];
             const float f = (mc == -INFINITY) ? 0.f : exp2f(mc - M);
+            s_f[c * G + h] = f;
             L = fmaf(row_ml[(c * G + h) * 2 + 1], f, L);
-            O = fmaf(row_o[c * G * D + e], f, O);
         }
+        s_l[h] = L;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * D; e += 256) {
+        const int h = e / D;
+        float O = 0.f;
+#pragma unroll 8
+        for (uint32_t c = 0; c < nchunks; c++)
+            O = fmaf(row_o[c * G * D + e], s_f[c * G + h], O);
+        const float L = s_l[h];
         const float v = (L > 0.f || L != L) ? O / L : 0.f;
         const size_t o = ((size_t)b * p.q_heads + g * G) * D + e;
         p.out[o] = rl_from_f32<DT>(v);
@@ -559,8 +597,8 @@ int validate(const rl_attn_decode_args_t *a)
         return -1;
     }
     const uint32_t tok = a->chunk_tokens ? a->chunk_tokens : kDefaultChunkTokens;
-    if (tok % 64 != 0 || tok == 0) {
-        rl_set_error("rl_hip_attn_decode: chunk_tokens %u must be a positive multiple of 64", tok);
+    if (tok % 64 != 0 || tok == 0 || tok > 2048) {
+        rl_set_error("rl_hip_attn_decode: chunk_tokens %u must be a multiple of 64 in [64, 2048]", tok);
         return -1;
     }
     if (!a->arena_base || !a->block_table || !a->ctx_lens || !a->q || !a->out) {
@@ -572,6 +610,11 @@ int validate(const rl_attn_decode_args_t *a)
         return -1;
     }
     const uint32_t max_tiles = (a->max_ctx + kTileTokens - 1) / kTileTokens;
+    if ((max_tiles + tok / kTileTokens - 1) / (tok / kTileTokens) > (uint32_t)kMergeMaxChunks) {
+        rl_set_error("rl_hip_attn_decode: max_ctx %u needs more than %d chunks of %u tokens", a->max_ctx,
+                     kMergeMaxChunks, tok);
+        return -1;
+    }
     const uint32_t table_need = (max_tiles + a->layout.token_count / kTileTokens - 1) /
                                 (a->layout.token_count / kTileTokens);
     if (a->table_stride < table_need) {

@@ -36,6 +36,7 @@ constexpr int kSplitLen = kThreads * kPerThread;  // 16,384 elements
 constexpr int kCandCap = 1024;                    // candidates per split
 constexpr int kMergeCap = 8192;                   // candidates per row in the merge
 constexpr int kKeptCap = 1024;                    // kept (top-k with ties) per row
+constexpr int kRegCand = 16;                      // merge fast path: candidates per lane
 
 struct SplitStat {
     float max_x;     // slice max of x
@@ -146,6 +147,7 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     __shared__ float s_red[4];
     __shared__ uint32_t s_red_i[4];
     __shared__ uint32_t s_key[4];
+    __shared__ uint32_t s_wtot[4];
     __shared__ uint32_t s_ncand;
 
     const float *lrow = p.logits + (size_t)row * p.row_stride;
@@ -254,26 +256,41 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
 
     if (k_eff != 0) {
         const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
+        // count, block-wide exclusive scan, then write: no per-element ballots
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++)
+            cnt += (rl_float_key(x[i]) >= clb && x[i] != -INFINITY) ? 1u : 0u;
+        uint32_t incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off);
+            if (lane >= off)
+                incl += o;
+        }
+        if (lane == 63)
+            s_wtot[wave] = incl;
+        __syncthreads();
+        uint32_t base = incl - cnt;
+        for (int w = 0; w < wave; w++)
+            base += s_wtot[w];
+        if (tid == 0)
+            s_ncand = s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3];
         uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandCap;
+        if (cnt) {
 #pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++)
+            for (int k = 0; k < kPerThread / 4; k++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t key = rl_float_key(x[k * 4 + e]);
-                const bool take = key >= clb && x[k * 4 + e] != -INFINITY;
-                const uint64_t mask = __ballot(take);
-                if (mask) {
-                    uint32_t base = 0;
-                    if (lane == 0)
-                        base = atomicAdd(&s_ncand, (uint32_t)__popcll(mask));
-                    base = __shfl(base, 0);
-                    if (take) {
-                        const uint32_t pos = base + (uint32_t)__popcll(mask & ((1ull << lane) - 1ull));
-                        if (pos < kCandCap)
-                            cand[pos] = make_uint2(key, c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                for (int e = 0; e < 4; e++) {
+                    const float v = x[k * 4 + e];
+                    const uint32_t key = rl_float_key(v);
+                    if (key >= clb && v != -INFINITY) {
+                        if (base < (uint32_t)kCandCap)
+                            cand[base] = make_uint2(key, c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                        base++;
                     }
                 }
-            }
+        }
     }
     __syncthreads();
     if (lane == 0)
@@ -299,6 +316,14 @@ __device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v)
         if (lane >= off)
             v += o;
     }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
+{
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1)
+        v += __shfl_xor(v, off);
     return v;
 }
 
@@ -541,6 +566,101 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             s_cand[off + i] = src[i];
     }
     __syncthreads();
+
+    // ---- fast path: candidates in registers, kept set of at most 64 ---------
+    if (n <= (uint32_t)(kMergeThreads * kRegCand)) {
+        uint32_t key[kRegCand], idx[kRegCand];
+#pragma unroll
+        for (int j = 0; j < kRegCand; j++) {
+            const uint32_t f = (uint32_t)(j * kMergeThreads + lane);
+            const uint2 c = f < n ? s_cand[f] : make_uint2(0u, 0u);  // key 0: below every real key
+            key[j] = c.x;
+            idx[j] = c.y;
+        }
+        // exact k_eff-th largest key: MSB-first, counting keys >= candidate
+        uint32_t cutoff = 0;
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t cand = cutoff | (1u << bit);
+            uint32_t cnt = 0;
+#pragma unroll
+            for (int j = 0; j < kRegCand; j++)
+                cnt += key[j] >= cand ? 1u : 0u;
+            if (wave_sum_u32(cnt) >= k_eff)
+                cutoff = cand;
+        }
+        // (padding slots hold key 0, below every finite key, and are never kept;
+        // cutoff itself stays 0 only when the row has fewer than k finite logits)
+        uint32_t kept = 0;
+#pragma unroll
+        for (int j = 0; j < kRegCand; j++)
+            kept += (key[j] >= cutoff && key[j] != 0u) ? 1u : 0u;
+        const uint32_t nk = wave_sum_u32(kept);
+        if (nk <= 64u) {
+            // compact the kept set to one element per lane
+            uint32_t pos = 0;
+            {
+                uint32_t incl = kept;
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1) {
+                    const uint32_t o = __shfl_up(incl, off);
+                    if (lane >= off)
+                        incl += o;
+                }
+                pos = incl - kept;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < kRegCand; j++)
+                if (key[j] >= cutoff && key[j] != 0u)
+                    s_sort[pos++] = ((uint64_t)key[j] << 32) | (uint64_t)(0xFFFFFFFFu - idx[j]);
+            __syncthreads();
+            uint64_t mine = (uint32_t)lane < nk ? s_sort[lane] : 0ull;
+            // bitonic sort of 64 lanes, descending by (key, ~index)
+#pragma unroll
+            for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+                for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                    const uint64_t other = __shfl_xor(mine, stride);
+                    const bool lower = (lane & stride) == 0;
+                    const bool desc = (lane & size) == 0;
+                    const uint64_t hi = mine > other ? mine : other;
+                    const uint64_t lo = mine > other ? other : mine;
+                    mine = (lower == desc) ? hi : lo;
+                }
+            }
+            const bool valid = (uint32_t)lane < nk;
+            const uint32_t my_idx = 0xFFFFFFFFu - (uint32_t)mine;
+            const uint64_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(mine >> 32)) - m) : 0ull;
+            const uint64_t cw = wave_inclusive_scan_u64(w);
+            const uint64_t wk = __shfl(cw, 63);
+            uint32_t np = nk;
+            if (topp > 0.f && topp < 1.f) {
+                const uint64_t thr = rl_topp_threshold(topp, wk);
+                const uint64_t hit = __ballot(valid && cw >= thr);
+                np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
+            }
+            const uint64_t wp = np ? __shfl(cw, np - 1) : 0ull;
+            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+            const bool in_p = (uint32_t)lane < np;
+            uint64_t s_le = 0;
+            for (uint32_t j = 0; j < np; j++) {
+                const uint32_t idx_j = (uint32_t)__shfl((int)my_idx, (int)j);
+                const uint64_t w_j = __shfl(w, (int)j);
+                if (idx_j <= my_idx)
+                    s_le += w_j;
+            }
+            uint32_t tok = wave_min_u32(in_p && s_le > u ? my_idx : 0xFFFFFFFFu);
+            if (tok == 0xFFFFFFFFu)
+                tok = wave_min_u32(in_p ? my_idx : 0xFFFFFFFFu);
+            if (tok >= p.vocab)
+                tok = 0;
+            if (lane == 0) {
+                p.token_out[row] = tok;
+                p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+            }
+            return;
+        }
+    }
 
     // ---- exact k_eff-th largest key: 4 passes of 8-bit radix select ----------
     uint32_t prefix = 0, prefix_mask = 0, need = k_eff;

@@ -15,7 +15,9 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "librlrt_amd.so")
+# RLRT_LIB points the binding at another build of the same library (used to
+# compare builds); by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("RLRT_LIB", os.path.join(_HERE, "lib", "librlrt_amd.so"))
 
 
 class RlrtError(RuntimeError):

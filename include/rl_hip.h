@@ -94,7 +94,7 @@ typedef struct {
     uint32_t dtype;              /* RL_DTYPE_* of q, K, V and out */
     const uint32_t *ctx_lens;    /* device [batch] */
     uint32_t max_ctx;            /* upper bound of ctx_lens; sizes the grid */
-    uint32_t chunk_tokens;       /* multiple of 16; 0 selects a default */
+    uint32_t chunk_tokens;       /* multiple of 64 in [64, 2048]; 0 selects a default */
     float scale;                 /* 0 selects 1/sqrt(head_dim) */
     const void *q;               /* device [batch][q_heads][head_dim] */
     void *out;                   /* device [batch][q_heads][head_dim] */

@@ -147,7 +147,7 @@ orc_sample_row(const float *l, uint32_t vocab, int greedy, float temperature, ui
             if (c >= thr)
                 break;
         }
-        if (np == 0)
+        if (np == 0 && nk > 0) /* at least one element of a non-empty kept set */
             np = 1;
     }
     uint64_t wp = 0;

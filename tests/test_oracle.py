@@ -305,3 +305,13 @@ def test_kv_append_oracle(olib):
     assert np.array_equal(blk[:, :5], s[:, :5])            # copied slots
     assert np.all(blk[0, 5] == 0xAA) and np.all(blk[1, 5] == 0xBB)
     assert np.all(blk[:, 6:] == 0)
+
+
+def test_sampling_all_masked_row(olib):
+    """Every logit -inf: the kept set is empty and the token is 0 (specified),
+    whatever the nucleus; the logprob is NaN."""
+    x = np.full(300, -np.inf, dtype=np.float32)
+    lp = C.c_double()
+    for k, p in ((0, 1.0), (0, 0.9), (3, 0.3), (50, 1.0)):
+        assert olib.orc_sample_row(x.ctypes.data, 300, 0, 0.7, k, p, 9, 2, 2, C.byref(lp)) == 0
+        assert math.isnan(lp.value)
