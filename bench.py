@@ -201,7 +201,8 @@ def main():
     ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append", "copy"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--chunk", type=int, default=0, help="attention split-KV chunk in tokens (0: library default)")
+    ap.add_argument("--grid-waves", type=int, default=0,
+                    help="attention: persistent waves sharing the KV stream (0: library default, a full device)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs the decode hot path on one GPU only; multi-GPU runs are not part of it "
@@ -225,8 +226,8 @@ def main():
                           "gbps_read_plus_write": 2 * n / (ms / args.steps * 1e-3) / 1e9}), flush=True)
         return
     step = Step()
-    step.attn.chunk_tokens = args.chunk
-    if args.chunk:
+    step.attn.grid_waves = args.grid_waves
+    if args.grid_waves:
         step.attn_ws = rlrt.attn_workspace(step.attn)
 
     for i in range(args.warmup):

@@ -3,30 +3,37 @@
 //
 // Replaces the reference microkernel attention_decode_step_fixed128
 // (cu/attention_decode.cu:60-204: one warp, one head, <= 32 tokens, lane-0
-// serial softmax) with a split-KV kernel for batched GQA decode:
+// serial softmax) with a persistent, balanced split-KV kernel:
 //
-//  grid   (chunk, kv_head, rollout); one workgroup of W wave64s per chunk of
-//         `chunk_tiles` 16-token tiles of one (rollout, kv head).
-//  stage  every tile's K and V planes are copied HBM -> LDS with
+//  work   the KV of row (rollout b, kv head g) is ceil(ctx_b / 16) tiles of
+//         16 tokens. All tiles of all rows, rows in (b, g) order, form one
+//         sequence of U tiles; wave w of the NW = min(resident waves, U) waves
+//         takes tiles [floor(w U / NW), floor((w + 1) U / NW)), so every wave
+//         streams the same number of bytes whatever the context lengths, and
+//         there is no tail of short workgroups. A wave that covers a whole row
+//         writes the output; otherwise it writes an fp32 partial (max, sum,
+//         unnormalised O) that attn_merge_kernel combines with a log-sum-exp
+//         merge.
+//  stage  each tile's K and V planes are copied HBM -> LDS with
 //         global_load_lds_dwordx4 (16 B per lane, 1 KiB per instruction,
-//         fully coalesced), double-buffered per wave so the next tile's
-//         loads are in flight while the current one is consumed.
-//  QK     lane (row r, lane t) of a 16-lane DPP row owns token t and q head
-//         r (GQA group <= 4; two heads per lane for groups of 8): a full
-//         head_dim dot product with v_dot2_f32_bf16 against q held in VGPRs.
-//         K rows are read from LDS with an XOR swizzle (chunk j ^ t) so the
-//         16 lanes of a row hit 16 different bank groups.
-//  softmax online, in the exp2 domain (scale folded with log2 e); row max
-//         and row sum with four DPP steps (quad_perm x2, row_half_mirror,
-//         row_mirror); p and the rescale factor go through LDS.
-//  PV     lane owns one dword (2 dims) of V for every head of the group, so
-//         each V element is converted to fp32 once; p is a broadcast LDS read.
-//  merge  waves of a workgroup merge through LDS; the chunks of a long
-//         context write fp32 partials (max, sum, unnormalised output) that a
-//         second small kernel combines with an fp32 log-sum-exp merge. (A
-//         last-workgroup merge inside the same launch needs agent-scope
-//         release/acquire fences, which on gfx950 write back and invalidate
-//         the whole L2 of the XCD for every workgroup: measured 12x slower.)
+//         coalesced), double-buffered per wave and continuing across row
+//         boundaries. Lanes fetch the 16-byte chunks of a row in XOR-permuted
+//         order (chunk c of row t lands at position c ^ t), which makes both
+//         MFMA operand reads below free of LDS bank conflicts. The query of a
+//         new row rides in the same copy stream into one of two q slots.
+//  QK     v_mfma_f32_16x16x32_{bf16,f16}: A = the tile's 16 K rows, B = q^T
+//         with the G heads of the group padded to 16 columns, so each K byte
+//         is read from LDS once. The result S^T[token][head] has lane l
+//         holding head l % 16 and tokens 4 (l / 16) .. + 3 - exactly the A
+//         operand layout of the PV product.
+//  softmax online, in the exp2 domain: per-head max over a lane's 4 tokens and
+//         two cross-lane steps; per-lane partial sums reduced once per row;
+//         the output is rescaled only when some head's max grows.
+//  PV     v_mfma_f32_16x16x16_{bf16,f16}: A = P, B = V read with
+//         ds_read_b64_tr_b16 (a 4x4 transpose inside each 16-lane group turns
+//         row-major V into the k-major operand). P is split into a 16-bit
+//         high part and the 16-bit remainder, two MFMAs per block, so the
+//         products keep ~16 mantissa bits: fp32-grade accuracy.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,458 +44,614 @@
 
 namespace {
 
-constexpr int kTileTokens = 16;
+constexpr int kTile = 16;  // tokens per tile (the MFMA M/K block)
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 struct AttnParams {
     const uint8_t *arena;
     uint64_t block_bytes;
     uint64_t arena_blocks;  // blocks at or past this index are never read
-    uint32_t max_ctx;
     const uint32_t *table;
     uint32_t table_stride;
     const uint32_t *ctx;
+    uint32_t max_ctx;
+    uint32_t batch;
+    uint32_t q_heads;
+    uint32_t kv_heads;
     const uint16_t *q;
     uint16_t *out;
     float *out_f32;
-    float scale_log2;      // softmax scale * log2(e)
-    uint32_t q_heads;
-    uint32_t kv_heads;
-    uint32_t chunk_tiles;  // tiles per workgroup (multiple of 4)
-    uint32_t max_chunks;
-    float *ws_o;           // [rollout][kv_head][chunk][G][D]
-    float *ws_ml;          // [rollout][kv_head][chunk][G][2]
+    float scale_log2;  // softmax scale * log2(e)
+    uint32_t nwaves;   // waves sharing the tile sequence
+    float *part;       // [nwaves + rows][G * D + 2 * G] partials of split rows
+    uint32_t *cum;     // [batch + 1] tiles of all rows before rollout b
 };
 
-template <int D, int G, int DT, int TPB, int W>
+template <int D, int G, int DT, int TPB>
 struct Cfg {
-    static constexpr int RB = 2 * D;                 // bytes per K/V row
-    static constexpr int NC = D / 8;                 // 16-byte chunks per row
-    static constexpr int PLANE = kTileTokens * RB;   // bytes of one tile's K (or V)
-    static constexpr int GH = G < 4 ? G : 4;         // heads per DPP row set
-    static constexpr int HPL = G / GH;               // heads per lane in QK
-    static constexpr int NT = 4 / GH;                // tiles per iteration ("unit")
-    static constexpr int UNIT_TOK = NT * kTileTokens;
-    static constexpr int STAGE = NT * 2 * PLANE;     // LDS bytes of one unit
-    static constexpr int DW = D / 2;                 // dwords per row
-    static constexpr int TG = 64 / DW;               // PV token groups
-    static constexpr int SUB = TPB / kTileTokens;    // tiles per arena block
-    static constexpr int PBUF = UNIT_TOK * G + G;    // p[token][head] + alpha[head]
-    static constexpr int MERGE_FLOATS = W * (TG * G * D + 2 * G);
+    static constexpr int W = 4;                   // waves per workgroup
+    static constexpr int RB = 2 * D;              // bytes per K or V row
+    static constexpr int NC = D / 8;              // 16-byte chunks per row
+    static constexpr int PLANE = kTile * RB;      // one tile of K (or V)
+    static constexpr int POPS = PLANE / 1024;     // copies per plane
+    static constexpr int UNIT_OPS = 2 * POPS;     // copies per staged tile
+    static constexpr int STAGE = 2 * PLANE;
+    static constexpr int QBYTES = G * D * 2;
+    static constexpr int QOPS = (QBYTES + 1023) / 1024;
+    static constexpr int QSLOT = QOPS * 1024;
+    static constexpr int WAVE_LDS = 2 * STAGE + 2 * QSLOT;
+    static constexpr int KS = D / 32;             // QK MFMA k-steps
+    static constexpr int NB = D / 16;             // PV MFMA column blocks
+    static constexpr int SUB = TPB / kTile;       // tiles per arena block
+    static constexpr int PART = G * D + 2 * G;    // floats per partial
+    static constexpr int LDS_CU = 160 * 1024;
+    static constexpr int WG_PER_CU_LDS = LDS_CU / (W * WAVE_LDS);
+    static constexpr int WG_PER_CU = WG_PER_CU_LDS > 4 ? 4 : WG_PER_CU_LDS;
     static_assert(D == 64 || D == 128, "head_dim");
     static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group");
-    static_assert(PLANE % 1024 == 0, "plane must be whole 1 KiB DMA rows");
-    // Stage 0 doubles as the merge area once the unit loop is done.
-    static constexpr int STAGE0_BYTES = MERGE_FLOATS * 4 > W * STAGE ? MERGE_FLOATS * 4 : W * STAGE;
+    static_assert(PLANE % 1024 == 0, "plane must be whole 1 KiB copies");
+    static_assert(WG_PER_CU >= 1, "LDS budget");
+    static_assert(2 * QSLOT >= 16 * 4, "q slots double as prologue scratch");
 };
 
-// Per-wave decode state: q in VGPRs, running max/sum, PV accumulators.
-template <int D, int G, int DT, int TPB, int W>
-struct WaveState {
-    using C = Cfg<D, G, DT, TPB, W>;
-    uint32_t qreg[C::HPL][C::NC][4];  // register j holds q chunk j ^ tsw
-    float m_run[C::HPL];
-    float l_run[C::HPL];
-    float acc[G][2];
-};
+// ---- 16-bit element helpers -----------------------------------------------
 
-// Issues the HBM -> LDS copies of one unit (NT tiles, K and V planes).
-// The chunk's block-table entries, loaded once into VGPRs (entry j of the
-// chunk in lane j % 64 of word j / 64) so that no table load latency sits
-// between consuming a unit and issuing the next unit's copies.
-struct ChunkTable {
-    uint32_t w0, w1;
-    uint32_t first;  // first logical block of the chunk
-
-    __device__ __forceinline__ uint32_t block(uint32_t logical) const
-    {
-        const uint32_t j = logical - first;  // wave-uniform, < 128
-        const uint32_t v = j < 64 ? w0 : w1;
-        return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)(j & 63));
-    }
-};
-
-// Returns false if the block table names a block outside the arena (that
-// block is not read).
-template <int D, int G, int DT, int TPB, int W>
-__device__ __forceinline__ bool stage_unit(const AttnParams &p, const ChunkTable &tbl, uint32_t tile0,
-                                           uint32_t tile_end, uint32_t lane_off, RL_LDS uint8_t *dst)
+template <int DT>
+__device__ __forceinline__ uint16_t to16(float f)
 {
-    using C = Cfg<D, G, DT, TPB, W>;
-    bool ok = true;
-#pragma unroll
-    for (int n = 0; n < C::NT; n++) {
-        const uint32_t tile = tile0 + n;
-        if (tile < tile_end) {
-            const uint32_t blk = tbl.block(tile / C::SUB);
-            if (blk >= p.arena_blocks) {
-                ok = false;
-                continue;
-            }
-            const uint8_t *kp = p.arena + (uint64_t)blk * p.block_bytes + (tile % C::SUB) * C::PLANE;
-            const uint8_t *vp = kp + TPB * C::RB;
-#pragma unroll
-            for (int i = 0; i < C::PLANE / 1024; i++) {
-                rl_g2lds_16(kp + lane_off + i * 1024, dst + n * 2 * C::PLANE + i * 1024);
-                rl_g2lds_16(vp + lane_off + i * 1024, dst + n * 2 * C::PLANE + C::PLANE + i * 1024);
-            }
-        }
-    }
-    return ok;
-}
-
-// Consumes one staged unit: QK, online softmax update, PV. FULL units lie
-// entirely below ctx and skip the masking of tokens past the end.
-template <int D, int G, int DT, int TPB, int W, bool FULL>
-__device__ __forceinline__ void consume_unit(const AttnParams &p, WaveState<D, G, DT, TPB, W> &ws,
-                                             RL_LDS const uint8_t *st, RL_LDS float *pbuf, uint32_t unit_tok0,
-                                             uint32_t ctx, int lane)
-{
-    using C = Cfg<D, G, DT, TPB, W>;
-    const int r = lane >> 4;
-    const int t = lane & 15;
-    const int n_qk = r / C::GH;
-    const int hb = r % C::GH;
-    const int dw = lane % C::DW;
-    const int tg = lane / C::DW;
-    const int tsw = t & (C::NC - 1);
-
-    // ---- QK: lane (row r, t) computes the full dot product of token t ------
-    float s2[C::HPL];
-    {
-        RL_LDS const uint8_t *krow = st + n_qk * 2 * C::PLANE + t * C::RB;
-        float dot[C::HPL];
-#pragma unroll
-        for (int i = 0; i < C::HPL; i++)
-            dot[i] = 0.f;
-#pragma unroll
-        for (int j = 0; j < C::NC; j++) {
-            const rl_u32x4 kv = *(RL_LDS const rl_u32x4 *)(krow + ((j ^ tsw) << 4));
-#pragma unroll
-            for (int i = 0; i < C::HPL; i++) {
-                dot[i] = rl_dot2<DT>(kv.x, ws.qreg[i][j][0], dot[i]);
-                dot[i] = rl_dot2<DT>(kv.y, ws.qreg[i][j][1], dot[i]);
-                dot[i] = rl_dot2<DT>(kv.z, ws.qreg[i][j][2], dot[i]);
-                dot[i] = rl_dot2<DT>(kv.w, ws.qreg[i][j][3], dot[i]);
-            }
-        }
-        const bool valid = FULL || (unit_tok0 + n_qk * kTileTokens + t < ctx);
-#pragma unroll
-        for (int i = 0; i < C::HPL; i++)
-            s2[i] = valid ? dot[i] * p.scale_log2 : -INFINITY;
-    }
-
-    // ---- online softmax over the unit ---------------------------------------
-#pragma unroll
-    for (int i = 0; i < C::HPL; i++) {
-        float mx = rl_row_max(s2[i]);
-        if constexpr (C::NT > 1) {
-#pragma unroll
-            for (int off = 16 * C::GH; off < 64; off <<= 1)
-                mx = fmaxf(mx, __shfl_xor(mx, off));
-        }
-        const float m_new = fmaxf(ws.m_run[i], mx);
-        const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-        const float pv = exp2f(s2[i] - m_use);
-        float sum = rl_row_sum(pv);
-        if constexpr (C::NT > 1) {
-#pragma unroll
-            for (int off = 16 * C::GH; off < 64; off <<= 1)
-                sum += __shfl_xor(sum, off);
-        }
-        const float alpha = exp2f(ws.m_run[i] - m_use);
-        ws.l_run[i] = ws.l_run[i] * alpha + sum;
-        ws.m_run[i] = m_new;
-        const int head = hb + 4 * i;
-        pbuf[(n_qk * kTileTokens + t) * G + head] = pv;
-        if (t == 0 && n_qk == 0)
-            pbuf[C::UNIT_TOK * G + head] = alpha;
-    }
-    rl_wave_lds_fence();
-
-    // ---- PV: lane owns dword dw (2 dims) of V for all G heads ------------------
-    {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            const float alpha = pbuf[C::UNIT_TOK * G + h];
-            ws.acc[h][0] *= alpha;
-            ws.acc[h][1] *= alpha;
-        }
-#pragma unroll
-        for (int k = 0; k < C::UNIT_TOK / C::TG; k++) {
-            const int tok = k * C::TG + tg;
-            const int n = tok / kTileTokens;
-            const int tt = tok % kTileTokens;
-            uint32_t vw = *(RL_LDS const uint32_t *)(st + n * 2 * C::PLANE + C::PLANE + tt * C::RB + dw * 4);
-            if (!FULL && unit_tok0 + tok >= ctx)
-                vw = 0u;  // stale or uninitialised slot: contributes exactly 0
-            float v0, v1;
-            rl_unpack2<DT>(vw, v0, v1);
-#pragma unroll
-            for (int h = 0; h < G; h++) {
-                const float pw = pbuf[tok * G + h];
-                ws.acc[h][0] = fmaf(pw, v0, ws.acc[h][0]);
-                ws.acc[h][1] = fmaf(pw, v1, ws.acc[h][1]);
-            }
-        }
-    }
-    rl_wave_lds_fence();
-}
-
-template <int D, int G, int DT, int TPB, int W>
-__device__ __forceinline__ void consume_any(const AttnParams &p, WaveState<D, G, DT, TPB, W> &ws,
-                                            RL_LDS const uint8_t *st, RL_LDS float *pbuf, uint32_t unit_tok0,
-                                            uint32_t ctx, int lane)
-{
-    using C = Cfg<D, G, DT, TPB, W>;
-    if (unit_tok0 + C::UNIT_TOK <= ctx)
-        consume_unit<D, G, DT, TPB, W, true>(p, ws, st, pbuf, unit_tok0, ctx, lane);
+    if constexpr (DT == 0)
+        return __builtin_bit_cast(uint16_t, (__bf16)f);
     else
-        consume_unit<D, G, DT, TPB, W, false>(p, ws, st, pbuf, unit_tok0, ctx, lane);
+        return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-template <int D, int G, int DT, int TPB, int W>
-__global__ __launch_bounds__(W * 64) void attn_decode_kernel(AttnParams p)
+template <int DT>
+__device__ __forceinline__ float from16(uint16_t h)
 {
-    using C = Cfg<D, G, DT, TPB, W>;
-    // Two static stage buffers (not one indexed array) so the waitcnt pass can
-    // tell the DMA into stage 1 apart from reads of stage 0 and leave the next
-    // unit's loads in flight while the current unit is consumed.
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_stage0[C::STAGE0_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_stage1[W * C::STAGE];
-    __shared__ float lds_p[W * C::PBUF];
-    __shared__ uint32_t s_bad;
+    if constexpr (DT == 0)
+        return __uint_as_float((uint32_t)h << 16);
+    else
+        return (float)__builtin_bit_cast(_Float16, h);
+}
+
+template <int DT>
+__device__ __forceinline__ rl_f32x4 mfma_qk(s16x8 a, s16x8 b, rl_f32x4 c)
+{
+    if constexpr (DT == 0)
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                       c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                      0, 0, 0);
+}
+
+template <int DT>
+__device__ __forceinline__ rl_f32x4 mfma_pv(s16x4 a, s16x4 b, rl_f32x4 c)
+{
+    if constexpr (DT == 0)
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
+                                                     0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t tiles_of(const AttnParams &p, uint32_t ctx_in)
+{
+    const uint32_t c = ctx_in > p.max_ctx ? p.max_ctx : ctx_in;
+    return (c + kTile - 1) / kTile;
+}
+
+// What the copy stream put into one stage, read back when it is consumed.
+struct StageMeta {
+    uint32_t b, g, u, nu, ctx;  // row, tile index within the row, tiles of the row, clamped ctx
+    uint32_t qslot;
+    bool first;                 // first tile of its row in this wave (q arrives with it)
+    bool last;                  // last tile of its row in this wave
+    bool bad;                   // ctx beyond max_ctx or a block outside the arena
+};
+
+// Issue side of a wave: walks the wave's tile range and starts the copies.
+template <int D, int G, int DT, int TPB>
+struct Issuer {
+    using C = Cfg<D, G, DT, TPB>;
+    uint32_t b, g, u, nu, ctx;
+    bool ctx_bad;
+    bool first;
+    uint32_t left;     // tiles still to issue
+    uint32_t qcount;   // rows entered so far (q slot parity)
+    uint32_t win0, win1, wrow, wfirst;  // block-table window: entries wfirst .. wfirst + 127 of row wrow
+    uint32_t soff[C::POPS];             // per-lane source offset of each copy within a plane
+
+    __device__ __forceinline__ void init_offsets(int lane)
+    {
+#pragma unroll
+        for (int i = 0; i < C::POPS; i++) {
+            const uint32_t byte = (uint32_t)i * 1024u + (uint32_t)lane * 16u;
+            const uint32_t t = byte / C::RB;
+            const uint32_t pos = (byte % C::RB) / 16u;
+            soff[i] = t * C::RB + ((pos ^ (t & (C::NC - 1))) * 16u);
+        }
+    }
+
+    __device__ __forceinline__ void set_rollout(const AttnParams &p, uint32_t nb)
+    {
+        b = nb;
+        const uint32_t cin = rl_sload(p.ctx + nb);
+        ctx_bad = cin > p.max_ctx;
+        ctx = ctx_bad ? p.max_ctx : cin;
+        nu = (ctx + kTile - 1) / kTile;
+    }
+
+    __device__ __forceinline__ void issue(const AttnParams &p, RL_LDS uint8_t *st, RL_LDS uint8_t *qslots,
+                                          StageMeta &m, int lane)
+    {
+        const uint32_t row = b * p.kv_heads + g;
+        const uint32_t lb = u / C::SUB;
+        if (row != wrow || lb < wfirst || lb >= wfirst + 128u) {
+            // New row or past the window: reload 128 table entries. The wait
+            // drains the copies in flight, once per row change.
+            const uint32_t nblk = (ctx + TPB - 1) / TPB;
+            const uint32_t *trow = p.table + (size_t)row * p.table_stride;
+            win0 = (lb + (uint32_t)lane < nblk) ? trow[lb + lane] : 0u;
+            win1 = (lb + 64u + (uint32_t)lane < nblk) ? trow[lb + 64u + lane] : 0u;
+            rl_wait_vmcnt<0>();
+            wrow = row;
+            wfirst = lb;
+        }
+        const uint32_t j = lb - wfirst;
+        uint32_t blk = (uint32_t)__builtin_amdgcn_readlane((int)(j < 64u ? win0 : win1), (int)(j & 63u));
+        m.bad = ctx_bad;
+        if (blk >= p.arena_blocks) {
+            // Never read outside the arena; copy block 0 instead so the number
+            // of copies per tile stays fixed, and poison the row.
+            m.bad = true;
+            blk = 0;
+        }
+        m.b = b;
+        m.g = g;
+        m.u = u;
+        m.nu = nu;
+        m.ctx = ctx;
+        m.first = first;
+        if (first) {
+            m.qslot = qcount & 1u;
+            qcount++;
+            const uint8_t *qsrc = (const uint8_t *)(p.q + ((size_t)b * p.q_heads + (size_t)g * G) * D);
+#pragma unroll
+            for (int i = 0; i < C::QOPS; i++) {
+                uint32_t off = (uint32_t)i * 1024u + (uint32_t)lane * 16u;
+                off = off < (uint32_t)C::QBYTES ? off : (uint32_t)C::QBYTES - 16u;
+                rl_g2lds_16_off(qsrc, off, qslots + m.qslot * C::QSLOT + i * 1024);
+            }
+        }
+        const uint8_t *kp = p.arena + (uint64_t)blk * p.block_bytes + (u % C::SUB) * C::PLANE;
+        const uint8_t *vp = kp + TPB * C::RB;
+#pragma unroll
+        for (int i = 0; i < C::POPS; i++) {
+            rl_g2lds_16_off(kp, soff[i], st + i * 1024);
+            rl_g2lds_16_off(vp, soff[i], st + C::PLANE + i * 1024);
+        }
+        // advance
+        left--;
+        u++;
+        first = false;
+        m.last = (u == nu) || (left == 0);
+        if (u == nu && left != 0) {
+            u = 0;
+            first = true;
+            if (++g == p.kv_heads) {
+                g = 0;
+                // tiles remain, so a later rollout has some (bounded anyway)
+                uint32_t nb = b;
+                do {
+                    set_rollout(p, ++nb);
+                } while (nu == 0 && nb + 1 < p.batch);
+            }
+        }
+    }
+};
+
+// Consume side: running softmax state of the current row and its output.
+template <int D, int G, int DT, int TPB>
+struct RowState {
+    using C = Cfg<D, G, DT, TPB>;
+    s16x8 qf[C::KS];          // B operand of QK: q[head lane%16][32 s + 8 (lane/16) .. + 7]
+    rl_f32x4 acc[C::NB];      // O[head 4 (lane/16) + r][16 n + lane % 16]
+    float m_run;              // running max (log2 domain) of head lane % 16
+    float l_run;              // this lane's share of the running sum
+    bool from0;               // the row started at tile 0 in this wave
+    bool bad;
+};
+
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void row_begin(RowState<D, G, DT, TPB> &rs, RL_LDS const uint8_t *qslot,
+                                          const StageMeta &m, int lane)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    const int h = lane & 15;
+    const int hs = h < G ? h : G - 1;
+#pragma unroll
+    for (int s = 0; s < C::KS; s++) {
+        s16x8 v = *(RL_LDS const s16x8 *)(qslot + hs * C::RB + (32 * s + 8 * (lane >> 4)) * 2);
+        if (h >= G)
+            v = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
+        rs.qf[s] = v;
+    }
+#pragma unroll
+    for (int n = 0; n < C::NB; n++)
+        rs.acc[n] = rl_f32x4{0.f, 0.f, 0.f, 0.f};
+    rs.m_run = -INFINITY;
+    rs.l_run = 0.f;
+    rs.from0 = m.u == 0;
+    rs.bad = false;
+}
+
+// One staged tile: QK (MFMA), online softmax, PV (MFMA).
+template <int D, int G, int DT, int TPB, bool FULL>
+__device__ __forceinline__ void consume_tile(const AttnParams &p, RowState<D, G, DT, TPB> &rs,
+                                             RL_LDS const uint8_t *st, const StageMeta &m, int lane)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    const int h = lane & 15;   // head (QK output column / PV A row)
+    const int tg = lane >> 4;  // token group: tokens 4 tg .. 4 tg + 3
+
+    // ---- S^T = K q^T ---------------------------------------------------------
+    rl_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+    {
+        const int t = lane & 15;
+#pragma unroll
+        for (int s = 0; s < C::KS; s++) {
+            const int c = 4 * s + tg;
+            const s16x8 kf = *(RL_LDS const s16x8 *)(st + t * C::RB + ((c ^ (t & (C::NC - 1))) << 4));
+            sc = mfma_qk<DT>(kf, rs.qf[s], sc);
+        }
+    }
+
+    // ---- online softmax ------------------------------------------------------
+    const uint32_t tok0 = m.u * kTile + 4 * tg;
+    float sv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const bool ok = (h < G) && (FULL || tok0 + r < m.ctx);
+        sv[r] = ok ? sc[r] * p.scale_log2 : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(rs.m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const bool grow = (m_new > rs.m_run) && (rs.m_run != -INFINITY);
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float alpha = grow ? exp2f(rs.m_run - m_use) : 1.f;
+        rs.l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float a = __shfl(alpha, 4 * tg + r);
+#pragma unroll
+            for (int n = 0; n < C::NB; n++)
+                rs.acc[n][r] *= a;
+        }
+    }
+    rs.m_run = m_new;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+        pr[r] = exp2f(sv[r] - m_use);
+    rs.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+
+    // ---- P split into high and low 16-bit parts --------------------------------
+    s16x4 phi, plo;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint16_t hi = to16<DT>(pr[r]);
+        const uint16_t lo = to16<DT>(pr[r] - from16<DT>(hi));
+        phi[r] = (short)hi;
+        plo[r] = (short)lo;
+    }
+
+    // ---- O += P V --------------------------------------------------------------
+    uint32_t vm0 = 0xFFFFFFFFu, vm1 = 0xFFFFFFFFu;
+    if constexpr (!FULL) {
+        // element r of the transposed operand is token 4 tg + r
+        vm0 = (tok0 + 0 < m.ctx ? 0x0000FFFFu : 0u) | (tok0 + 1 < m.ctx ? 0xFFFF0000u : 0u);
+        vm1 = (tok0 + 2 < m.ctx ? 0x0000FFFFu : 0u) | (tok0 + 3 < m.ctx ? 0xFFFF0000u : 0u);
+    }
+    {
+        const int L = lane & 15;
+        const int t = 4 * tg + (L >> 2);
+        const int sw = t & (C::NC - 1);
+        RL_LDS const uint8_t *vrow = st + C::PLANE + t * C::RB + 8 * (L & 1);
+#pragma unroll
+        for (int n = 0; n < C::NB; n++) {
+            const int c = 2 * n + ((L & 3) >> 1);
+            s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (RL_LDS s16x4 *)(vrow + ((c ^ sw) << 4)));
+            if constexpr (!FULL) {
+                // stale slots past ctx may hold anything, NaN included: zero them
+                uint32_t w0 = __builtin_bit_cast(uint32_t, __builtin_shufflevector(vb, vb, 0, 1)) & vm0;
+                uint32_t w1 = __builtin_bit_cast(uint32_t, __builtin_shufflevector(vb, vb, 2, 3)) & vm1;
+                typedef short s16x2 __attribute__((ext_vector_type(2)));
+                const s16x2 a = __builtin_bit_cast(s16x2, w0);
+                const s16x2 b2 = __builtin_bit_cast(s16x2, w1);
+                vb = s16x4{a[0], a[1], b2[0], b2[1]};
+            }
+            rs.acc[n] = mfma_pv<DT>(phi, vb, rs.acc[n]);
+            rs.acc[n] = mfma_pv<DT>(plo, vb, rs.acc[n]);
+        }
+    }
+}
+
+// Row done in this wave: direct output, or an fp32 partial for the merge.
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void row_end(const AttnParams &p, RowState<D, G, DT, TPB> &rs, const StageMeta &m,
+                                        uint32_t wave_id, int lane)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    const int h = lane & 15;
+    const int tg = lane >> 4;
+    float lt = rs.l_run + __shfl_xor(rs.l_run, 16);
+    lt += __shfl_xor(lt, 32);
+    const bool poison = rs.bad || m.bad;
+    const uint32_t row = m.b * p.kv_heads + m.g;
+    if (rs.from0 && m.u + 1 == m.nu) {
+        const size_t obase = ((size_t)m.b * p.q_heads + (size_t)m.g * G) * D;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float L = __shfl(lt, 4 * tg + r);
+            const int hh = 4 * tg + r;
+            if (hh < G) {
+#pragma unroll
+                for (int n = 0; n < C::NB; n++) {
+                    float v = L > 0.f ? rs.acc[n][r] / L : 0.f;
+                    if (poison)
+                        v = __builtin_nanf("");
+                    const size_t o = obase + (size_t)hh * D + 16 * n + h;
+                    p.out[o] = rl_from_f32<DT>(v);
+                    if (p.out_f32)
+                        p.out_f32[o] = v;
+                }
+            }
+        }
+    } else {
+        float *part = p.part + (size_t)(wave_id + row) * C::PART;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int hh = 4 * tg + r;
+            if (hh < G) {
+#pragma unroll
+                for (int n = 0; n < C::NB; n++)
+                    part[hh * D + 16 * n + h] = rs.acc[n][r];
+            }
+        }
+        if (lane < G) {
+            part[G * D + 2 * lane + 0] = rs.m_run;
+            part[G * D + 2 * lane + 1] = poison ? __builtin_nanf("") : lt;
+        }
+    }
+}
+
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void consume(const AttnParams &p, RowState<D, G, DT, TPB> &rs, RL_LDS const uint8_t *st,
+                                        RL_LDS const uint8_t *qslots, const StageMeta &m, uint32_t wave_id, int lane)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    if (m.first)
+        row_begin<D, G, DT, TPB>(rs, qslots + m.qslot * C::QSLOT, m, lane);
+    rs.bad |= m.bad;
+    if (m.u * kTile + kTile <= m.ctx)
+        consume_tile<D, G, DT, TPB, true>(p, rs, st, m, lane);
+    else
+        consume_tile<D, G, DT, TPB, false>(p, rs, st, m, lane);
+    if (m.last)
+        row_end<D, G, DT, TPB>(p, rs, m, wave_id, lane);
+}
+
+template <int D, int G, int DT, int TPB>
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    constexpr int W = C::W;
+    static_assert(W * 64 == 256, "launch bounds");
+    // Separate arrays per stage so the compiler's wait insertion can tell a
+    // copy into one stage from reads of the other.
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_st0[W * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_st1[W * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * 2 * C::QSLOT];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t chunk = blockIdx.x;
-    const uint32_t g = blockIdx.y;
-    const uint32_t b = blockIdx.z;
 
-    const uint32_t ctx_in = rl_sload(p.ctx + b);
-    // A context past max_ctx cannot be covered by the grid: clamp it, and
-    // poison the output below.
-    bool bad = ctx_in > p.max_ctx;
-    const uint32_t ctx = bad ? p.max_ctx : ctx_in;
-    const uint32_t ntiles = (ctx + kTileTokens - 1) / kTileTokens;
-    const uint32_t nchunks = (ntiles + p.chunk_tiles - 1) / p.chunk_tiles;
-    const uint32_t row_id = b * p.kv_heads + g;
-
-    if (ctx == 0) {
-        if (chunk == 0) {
-            for (int e = threadIdx.x; e < G * D; e += W * 64) {
-                const size_t o = ((size_t)b * p.q_heads + g * G) * D + e;
-                const float v = bad ? __builtin_nanf("") : 0.f;
-                p.out[o] = rl_from_f32<DT>(v);
-                if (p.out_f32)
-                    p.out_f32[o] = v;
+    // ---- plan: tile prefix over rollouts, each wave's starting rollout -------
+    // (q slot memory doubles as scratch until the copies start)
+    RL_LDS uint32_t *wave_tot = (RL_LDS uint32_t *)lds_q;  // [W]
+    RL_LDS uint32_t *start = wave_tot + W;                  // [W][2] rollout, tiles before it
+    const uint32_t T = W * 64;
+    const uint32_t per = (p.batch + T - 1) / T;
+    const uint32_t b0 = min(threadIdx.x * per, p.batch);
+    const uint32_t b1 = min(b0 + per, p.batch);
+    uint32_t S = 0;
+    for (uint32_t bb = b0; bb < b1; bb++)
+        S += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+    uint32_t inc = S;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const uint32_t v = __shfl_up(inc, off);
+        if (lane >= off)
+            inc += v;
+    }
+    if (lane == 63)
+        wave_tot[wave] = inc;
+    __syncthreads();
+    uint32_t U = 0, before = 0;
+#pragma unroll
+    for (int v = 0; v < W; v++) {
+        const uint32_t t = wave_tot[v];
+        before += v < wave ? t : 0u;
+        U += t;
+    }
+    const uint32_t P0 = before + inc - S;  // tiles before this thread's rollouts
+    // Waves that share the tiles: never more than there are tiles, so every
+    // wave of a row's range holds part of it.
+    const uint32_t NW = min(p.nwaves, U);
+#pragma unroll
+    for (int v = 0; v < W; v++) {
+        const uint32_t w = blockIdx.x * W + v;
+        if (w < NW && S > 0) {
+            const uint32_t s = (uint32_t)(((uint64_t)w * U) / NW);
+            if (s >= P0 && s < P0 + S) {
+                uint32_t c = P0;
+                for (uint32_t bb = b0; bb < b1; bb++) {
+                    const uint32_t n = tiles_of(p, p.ctx[bb]) * p.kv_heads;
+                    if (s < c + n) {
+                        start[2 * v] = bb;
+                        start[2 * v + 1] = c;
+                        break;
+                    }
+                    c += n;
+                }
             }
         }
-        return;
     }
-    if (chunk >= nchunks)
-        return;
-
-    const uint32_t tile_begin = chunk * p.chunk_tiles;
-    const uint32_t tile_end = min(tile_begin + p.chunk_tiles, ntiles);
-    const uint32_t units = (tile_end - tile_begin + C::NT - 1) / C::NT;
-    const uint32_t lane_off = (uint32_t)lane * 16u;
-    ChunkTable tbl;
-    {
-        const uint32_t *table_row = p.table + (size_t)row_id * p.table_stride;
-        tbl.first = tile_begin / C::SUB;
-        const uint32_t last = (tile_end + C::SUB - 1) / C::SUB;  // one past the chunk's last block
-        tbl.w0 = (tbl.first + lane < last) ? table_row[tbl.first + lane] : 0u;
-        tbl.w1 = (tbl.first + 64 + lane < last) ? table_row[tbl.first + 64 + lane] : 0u;
-    }
-
-    RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_stage0 + wave * C::STAGE;
-    RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_stage1 + wave * C::STAGE;
-    RL_LDS float *pbuf = (RL_LDS float *)lds_p + wave * C::PBUF;
-
-    WaveState<D, G, DT, TPB, W> ws;
-    {
-        const int r = lane >> 4;
-        const int hb = r % C::GH;
-        const int tsw = (lane & 15) & (C::NC - 1);
-#pragma unroll
-        for (int i = 0; i < C::HPL; i++) {
-            const uint16_t *qrow = p.q + ((size_t)b * p.q_heads + g * G + hb + 4 * i) * D;
-#pragma unroll
-            for (int j = 0; j < C::NC; j++) {
-                const rl_u32x4 v = *(const rl_u32x4 *)(qrow + (j ^ tsw) * 8);
-                ws.qreg[i][j][0] = v.x;
-                ws.qreg[i][j][1] = v.y;
-                ws.qreg[i][j][2] = v.z;
-                ws.qreg[i][j][3] = v.w;
-            }
-            ws.m_run[i] = -INFINITY;
-            ws.l_run[i] = 0.f;
+    if (blockIdx.x == 0) {
+        uint32_t c = P0;
+        for (uint32_t bb = b0; bb < b1; bb++) {
+            p.cum[bb] = c;
+            c += tiles_of(p, p.ctx[bb]) * p.kv_heads;
         }
-#pragma unroll
-        for (int h = 0; h < G; h++)
-            ws.acc[h][0] = ws.acc[h][1] = 0.f;
+        if (threadIdx.x == T - 1)
+            p.cum[p.batch] = U;
     }
+    __syncthreads();
+    const uint32_t wave_id = blockIdx.x * W + wave;
+    const bool active = wave_id < NW;
+    const uint32_t s_begin = active ? (uint32_t)(((uint64_t)wave_id * U) / NW) : 0u;
+    const uint32_t s_end = active ? (uint32_t)(((uint64_t)(wave_id + 1) * U) / NW) : 0u;
+    uint32_t rb = 0, rcum = 0;
+    if (active) {
+        rb = __builtin_amdgcn_readfirstlane(start[2 * wave]);
+        rcum = __builtin_amdgcn_readfirstlane(start[2 * wave + 1]);
+    }
+    __syncthreads();  // scratch reads done before any copy lands in the q slots
+    if (!active)
+        return;
 
-    // Copies per staged unit. Vector-memory operations retire in issue order,
-    // so "at most UNIT_OPS outstanding" means every copy older than the most
-    // recently staged unit (and the q loads above) has landed in LDS. Units
-    // of several tiles can be partial at the end of a chunk, so those waves
-    // drain fully instead.
-    constexpr int UNIT_OPS = C::NT == 1 ? 2 * (C::PLANE / 1024) : 0;
+    RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_st0 + wave * C::STAGE;
+    RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_st1 + wave * C::STAGE;
+    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * 2 * C::QSLOT;
 
-    if ((uint32_t)wave < units)
-        bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + wave * C::NT, tile_end, lane_off, st0);
-    if ((uint32_t)wave + W < units)
-        bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (wave + W) * C::NT, tile_end, lane_off, st1);
+    Issuer<D, G, DT, TPB> is;
+    is.init_offsets(lane);
+    is.set_rollout(p, rb);
+    {
+        const uint32_t rem = s_begin - rcum;
+        is.g = rem / is.nu;
+        is.u = rem % is.nu;
+    }
+    is.left = s_end - s_begin;
+    is.first = true;
+    is.qcount = 0;
+    is.wrow = 0xFFFFFFFFu;
+    is.wfirst = 0;
+    is.win0 = is.win1 = 0;
 
-    for (uint32_t u = wave; u < units; u += 2 * W) {
-        // stage 0 holds unit u; stage 1 may hold unit u + W (in flight)
-        if (u + W < units)
-            rl_wait_vmcnt<UNIT_OPS>();
+    RowState<D, G, DT, TPB> rs;
+    StageMeta mc, mn;  // tile to consume next, tile in flight behind it
+    RL_LDS uint8_t *stc = st0;
+    RL_LDS uint8_t *stn = st1;
+    bool has_next = false;
+    is.issue(p, stc, qs, mc, lane);
+    if (is.left) {
+        is.issue(p, stn, qs, mn, lane);
+        has_next = true;
+    }
+    for (;;) {
+        // Copies complete in issue order: once at most one tile's worth is
+        // outstanding, everything older - this tile and its q - has landed.
+        // (A tile that brings a q slot issues one more copy: the wait is then
+        // slightly stronger than needed, never weaker.)
+        if (has_next)
+            rl_wait_vmcnt<C::UNIT_OPS>();
         else
             rl_wait_vmcnt<0>();
-        consume_any<D, G, DT, TPB, W>(p, ws, st0, pbuf, (tile_begin + u * C::NT) * kTileTokens, ctx, lane);
-        if (u + 2 * W < units) {
-            rl_wait_lgkmcnt0();
-            bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (u + 2 * W) * C::NT, tile_end, lane_off,
-                                                 st0);
-        }
-        if (u + W >= units)
+        consume<D, G, DT, TPB>(p, rs, stc, qs, mc, wave_id, lane);
+        if (!has_next)
             break;
-        // stage 1 holds unit u + W; stage 0 may hold unit u + 2W (in flight)
-        if (u + 2 * W < units)
-            rl_wait_vmcnt<UNIT_OPS>();
-        else
-            rl_wait_vmcnt<0>();
-        consume_any<D, G, DT, TPB, W>(p, ws, st1, pbuf, (tile_begin + (u + W) * C::NT) * kTileTokens, ctx,
-                                       lane);
-        if (u + 3 * W < units) {
+        // the stage just consumed takes the tile after next
+        StageMeta mi;
+        bool has_after = false;
+        if (is.left) {
             rl_wait_lgkmcnt0();
-            bad |= !stage_unit<D, G, DT, TPB, W>(p, tbl, tile_begin + (u + 3 * W) * C::NT, tile_end, lane_off,
-                                                 st1);
+            is.issue(p, stc, qs, mi, lane);
+            has_after = true;
         }
-    }
-
-    // ---- merge the waves of the workgroup (merge area aliases stage 0) -------
-    if (threadIdx.x == 0)
-        s_bad = 0;
-    __syncthreads();
-    if (bad && lane == 0)
-        s_bad = 1;
-    RL_LDS float *mo = (RL_LDS float *)lds_stage0;      // [W][TG][G][D]
-    RL_LDS float *mml = mo + W * C::TG * G * D;         // [W][G][2]
-    {
-        const int r = lane >> 4;
-        const int t = lane & 15;
-        const int dw = lane % C::DW;
-        const int tg = lane / C::DW;
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            mo[((wave * C::TG + tg) * G + h) * D + dw * 2 + 0] = ws.acc[h][0];
-            mo[((wave * C::TG + tg) * G + h) * D + dw * 2 + 1] = ws.acc[h][1];
-        }
-        if (t == 0 && r / C::GH == 0) {
-#pragma unroll
-            for (int i = 0; i < C::HPL; i++) {
-                mml[(wave * G + r % C::GH + 4 * i) * 2 + 0] = ws.m_run[i];
-                mml[(wave * G + r % C::GH + 4 * i) * 2 + 1] = ws.l_run[i];
-            }
-        }
-    }
-    __syncthreads();
-
-    const bool poison = s_bad != 0;
-    const bool split = nchunks > 1;
-    float *ws_o = p.ws_o + ((size_t)row_id * p.max_chunks + chunk) * G * D;
-    float *ws_ml = p.ws_ml + ((size_t)row_id * p.max_chunks + chunk) * G * 2;
-
-    for (int e = threadIdx.x; e < G * D; e += W * 64) {
-        const int h = e / D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < W; w++)
-            M = fmaxf(M, mml[(w * G + h) * 2]);
-        float L = 0.f, O = 0.f;
-#pragma unroll
-        for (int w = 0; w < W; w++) {
-            const float mw = mml[(w * G + h) * 2];
-            const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-            L = fmaf(mml[(w * G + h) * 2 + 1], f, L);
-            float ow = 0.f;
-#pragma unroll
-            for (int q = 0; q < C::TG; q++)
-                ow += mo[((w * C::TG + q) * G + h) * D + (e % D)];
-            O = fmaf(ow, f, O);
-        }
-        if (poison) {
-            O = __builtin_nanf("");
-            L = __builtin_nanf("");
-        }
-        if (!split) {
-            const float v = L > 0.f ? O / L : (poison ? L : 0.f);
-            const size_t o = ((size_t)b * p.q_heads + g * G) * D + e;
-            p.out[o] = rl_from_f32<DT>(v);
-            if (p.out_f32)
-                p.out_f32[o] = v;
-        } else {
-            ws_o[e] = O;
-            if (e % D == 0) {
-                ws_ml[h * 2 + 0] = M;
-                ws_ml[h * 2 + 1] = L;
-            }
-        }
+        RL_LDS uint8_t *t = stc;
+        stc = stn;
+        stn = t;
+        mc = mn;
+        mn = mi;
+        has_next = has_after;
     }
 }
 
-// Combines the chunk partials of every split (rollout, kv head):
-// M = max_c m_c, L = sum_c l_c 2^(m_c - M), O = sum_c o_c 2^(m_c - M), out = O / L.
-// The per-chunk scale factors go through LDS so every partial-output load
-// is independent of the others and they can all be in flight together.
-constexpr int kMergeMaxChunks = 128;
-
+// Combines the partials of every row split across waves:
+// M = max_w m_w, L = sum_w l_w 2^(m_w - M), O = sum_w o_w 2^(m_w - M), out = O / L.
+// Also writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN).
 template <int D, int G, int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
 {
-    __shared__ float s_f[kMergeMaxChunks * G];
-    __shared__ float s_l[G];
+    constexpr int PART = G * D + 2 * G;
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
-    const uint32_t ctx_in = rl_sload(p.ctx + b);
-    const uint32_t ctx = ctx_in > p.max_ctx ? p.max_ctx : ctx_in;
-    const uint32_t ntiles = (ctx + kTileTokens - 1) / kTileTokens;
-    const uint32_t nchunks = (ntiles + p.chunk_tiles - 1) / p.chunk_tiles;
-    if (nchunks <= 1)
-        return;  // written directly by the decode kernel
-    const uint32_t row_id = b * p.kv_heads + g;
-    const float *row_o = p.ws_o + (size_t)row_id * p.max_chunks * G * D;
-    const float *row_ml = p.ws_ml + (size_t)row_id * p.max_chunks * G * 2;
-    if (threadIdx.x < G) {
-        const int h = threadIdx.x;
-        float M = -INFINITY;
-        for (uint32_t c = 0; c < nchunks; c++)
-            M = fmaxf(M, row_ml[(c * G + h) * 2]);
-        float L = 0.f;
-        for (uint32_t c = 0; c < nchunks; c++) {
-            const float mc = row_ml[(c * G + h) * 2];
-            const float f = (mc == -INFINITY) ? 0.f : exp2f(mc - M);
-            s_f[c * G + h] = f;
-            L = fmaf(row_ml[(c * G + h) * 2 + 1], f, L);
+    const uint32_t row = b * p.kv_heads + g;
+    const uint32_t cin = rl_sload(p.ctx + b);
+    const bool bad = cin > p.max_ctx;
+    const uint32_t nu = tiles_of(p, cin);
+    const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
+    if (nu == 0) {
+        for (int e = threadIdx.x; e < G * D; e += 256) {
+            const float v = bad ? __builtin_nanf("") : 0.f;
+            p.out[obase + e] = rl_from_f32<DT>(v);
+            if (p.out_f32)
+                p.out_f32[obase + e] = v;
         }
-        s_l[h] = L;
+        return;
     }
-    __syncthreads();
+    const uint32_t U = rl_sload(p.cum + p.batch);  // > 0: this row has tiles
+    const uint32_t NW = min(p.nwaves, U);
+    const uint32_t R0 = rl_sload(p.cum + b) + g * nu;
+    const uint32_t R1 = R0 + nu;
+    // wave holding tile R0 / tile R1 - 1: the largest w with floor(w U / NW) <= tile
+    const uint32_t wf = (uint32_t)((((uint64_t)R0 + 1) * NW - 1) / U);
+    const uint32_t wl = (uint32_t)(((uint64_t)R1 * NW - 1) / U);
+    if (wf == wl)
+        return;  // one wave covered the row and wrote it
+    const float *part = p.part + (size_t)(wf + row) * PART;
+    const uint32_t np = wl - wf + 1;
     for (int e = threadIdx.x; e < G * D; e += 256) {
         const int h = e / D;
-        float O = 0.f;
-#pragma unroll 8
-        for (uint32_t c = 0; c < nchunks; c++)
-            O = fmaf(row_o[c * G * D + e], s_f[c * G + h], O);
-        const float L = s_l[h];
-        const float v = (L > 0.f || L != L) ? O / L : 0.f;
-        const size_t o = ((size_t)b * p.q_heads + g * G) * D + e;
-        p.out[o] = rl_from_f32<DT>(v);
+        float M = -INFINITY;
+        for (uint32_t i = 0; i < np; i++)
+            M = fmaxf(M, part[(size_t)i * PART + G * D + 2 * h]);
+        float L = 0.f, O = 0.f;
+        for (uint32_t i = 0; i < np; i++) {
+            const float *pp = part + (size_t)i * PART;
+            const float mi = pp[G * D + 2 * h];
+            const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
+            L = fmaf(pp[G * D + 2 * h + 1], f, L);
+            O = fmaf(pp[e], f, O);
+        }
+        float v = (L > 0.f || L != L) ? O / L : 0.f;
+        if (bad)
+            v = __builtin_nanf("");
+        p.out[obase + e] = rl_from_f32<DT>(v);
         if (p.out_f32)
-            p.out_f32[o] = v;
+            p.out_f32[obase + e] = v;
     }
 }
 
@@ -498,77 +661,71 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
 
 namespace {
 
-// Waves per workgroup: up to 4, with both stage buffers within 64 KiB so two
-// workgroups share a CU's 160 KiB of LDS.
-template <int D, int G>
-constexpr int waves_for()
-{
-    constexpr int nt = 4 / (G < 4 ? G : 4);
-    constexpr int stage = nt * 2 * kTileTokens * 2 * D;
-    constexpr int w = 65536 / (2 * stage);
-    return w < 1 ? 1 : (w > 4 ? 4 : w);
-}
-constexpr uint32_t kDefaultChunkTokens = 512;
-
-struct WsLayout {
-    size_t ml_off, o_off, total;
-};
-
-WsLayout ws_layout(const rl_attn_decode_args_t *a, uint32_t chunk_tiles)
+uint32_t part_floats(const rl_attn_decode_args_t *a)
 {
     const uint32_t G = a->q_heads / a->kv_heads;
+    return G * a->layout.head_dim + 2 * G;
+}
+
+uint32_t waves_of(const rl_attn_decode_args_t *a)
+{
+    if (a->grid_waves)
+        return a->grid_waves;
+    const uint32_t G = a->q_heads / a->kv_heads;
     const uint32_t D = a->layout.head_dim;
-    const uint32_t max_tiles = (a->max_ctx + kTileTokens - 1) / kTileTokens;
-    const uint32_t max_chunks = max_tiles == 0 ? 1 : (max_tiles + chunk_tiles - 1) / chunk_tiles;
-    const size_t rows = (size_t)a->batch * a->kv_heads;
+    // LDS per wave: two stages of one tile's K and V, two q slots
+    const uint32_t wave_lds = 2 * (2 * 16 * 2 * D) + 2 * ((G * D * 2 + 1023) / 1024) * 1024;
+    uint32_t wg = (160u * 1024u) / (4 * wave_lds);
+    wg = wg > 4 ? 4 : wg;
+    return rl_cu_count() * wg * 4;
+}
+
+struct WsLayout {
+    size_t cum_off, part_off, total;
+};
+
+WsLayout ws_layout(const rl_attn_decode_args_t *a)
+{
     WsLayout w;
-    w.ml_off = 0;
-    w.o_off = w.ml_off + ((rows * max_chunks * G * 2 * 4 + 255) / 256) * 256;
-    w.total = w.o_off + rows * max_chunks * G * D * 4;
+    const size_t rows = (size_t)a->batch * a->kv_heads;
+    w.cum_off = 0;
+    w.part_off = (((size_t)a->batch + 1) * 4 + 255) / 256 * 256;
+    w.total = w.part_off + ((size_t)waves_of(a) + rows) * part_floats(a) * 4;
     return w;
 }
 
-uint32_t chunk_tiles_of(const rl_attn_decode_args_t *a)
-{
-    const uint32_t tok = a->chunk_tokens ? a->chunk_tokens : kDefaultChunkTokens;
-    return tok / kTileTokens;
-}
-
 template <int D, int G, int DT, int TPB>
-int launch(const AttnParams &p, dim3 grid)
+int launch(const AttnParams &p)
 {
-    constexpr int W = waves_for<D, G>();
-    auto kern = attn_decode_kernel<D, G, DT, TPB, W>;
-    hipLaunchKernelGGL(kern, grid, dim3(W * 64), 0, rl_stream(), p);
+    using C = Cfg<D, G, DT, TPB>;
+    const uint32_t wgs = (p.nwaves + C::W - 1) / C::W;
+    hipLaunchKernelGGL((attn_decode_kernel<D, G, DT, TPB>), dim3(wgs), dim3(C::W * 64), 0, rl_stream(), p);
     if (rl_check_launch("attn_decode_kernel launch"))
         return -1;
-    if (grid.x > 1) {
-        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(grid.y, grid.z), dim3(256), 0, rl_stream(), p);
-        return rl_check_launch("attn_merge_kernel launch");
-    }
-    return 0;
+    hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(), p);
+    return rl_check_launch("attn_merge_kernel launch");
 }
 
 template <int D, int G, int DT>
-int dispatch_tpb(const AttnParams &p, dim3 grid, uint32_t tpb)
+int dispatch_tpb(const AttnParams &p, uint32_t tpb)
 {
-    return tpb == 16 ? launch<D, G, DT, 16>(p, grid) : launch<D, G, DT, 32>(p, grid);
+    return tpb == 16 ? launch<D, G, DT, 16>(p) : launch<D, G, DT, 32>(p);
 }
 
 template <int D, int G>
-int dispatch_dt(const AttnParams &p, dim3 grid, uint32_t dt, uint32_t tpb)
+int dispatch_dt(const AttnParams &p, uint32_t dt, uint32_t tpb)
 {
-    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, grid, tpb) : dispatch_tpb<D, G, 1>(p, grid, tpb);
+    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, tpb) : dispatch_tpb<D, G, 1>(p, tpb);
 }
 
 template <int D>
-int dispatch_g(const AttnParams &p, dim3 grid, uint32_t G, uint32_t dt, uint32_t tpb)
+int dispatch_g(const AttnParams &p, uint32_t G, uint32_t dt, uint32_t tpb)
 {
     switch (G) {
-    case 1: return dispatch_dt<D, 1>(p, grid, dt, tpb);
-    case 2: return dispatch_dt<D, 2>(p, grid, dt, tpb);
-    case 4: return dispatch_dt<D, 4>(p, grid, dt, tpb);
-    default: return dispatch_dt<D, 8>(p, grid, dt, tpb);
+    case 1: return dispatch_dt<D, 1>(p, dt, tpb);
+    case 2: return dispatch_dt<D, 2>(p, dt, tpb);
+    case 4: return dispatch_dt<D, 4>(p, dt, tpb);
+    default: return dispatch_dt<D, 8>(p, dt, tpb);
     }
 }
 
@@ -596,27 +753,29 @@ int validate(const rl_attn_decode_args_t *a)
         rl_set_error("rl_hip_attn_decode: dtype %u", a->dtype);
         return -1;
     }
-    const uint32_t tok = a->chunk_tokens ? a->chunk_tokens : kDefaultChunkTokens;
-    if (tok % 64 != 0 || tok == 0 || tok > 2048) {
-        rl_set_error("rl_hip_attn_decode: chunk_tokens %u must be a multiple of 64 in [64, 2048]", tok);
-        return -1;
-    }
     if (!a->arena_base || !a->block_table || !a->ctx_lens || !a->q || !a->out) {
         rl_set_error("rl_hip_attn_decode: NULL device pointer");
+        return -1;
+    }
+    if (a->arena_bytes < a->layout.block_bytes) {
+        rl_set_error("rl_hip_attn_decode: arena of %llu bytes holds no block", (unsigned long long)a->arena_bytes);
         return -1;
     }
     if (a->batch == 0 || a->batch > 65535 || a->kv_heads > 65535) {
         rl_set_error("rl_hip_attn_decode: batch %u / kv_heads %u out of range", a->batch, a->kv_heads);
         return -1;
     }
-    const uint32_t max_tiles = (a->max_ctx + kTileTokens - 1) / kTileTokens;
-    if ((max_tiles + tok / kTileTokens - 1) / (tok / kTileTokens) > (uint32_t)kMergeMaxChunks) {
-        rl_set_error("rl_hip_attn_decode: max_ctx %u needs more than %d chunks of %u tokens", a->max_ctx,
-                     kMergeMaxChunks, tok);
+    const uint64_t max_tiles = (a->max_ctx + 15ull) / 16ull;
+    if ((uint64_t)a->batch * a->kv_heads * max_tiles >= (1ull << 32)) {
+        rl_set_error("rl_hip_attn_decode: batch %u x kv_heads %u x %llu tiles of max_ctx %u exceeds 2^32 tiles",
+                     a->batch, a->kv_heads, (unsigned long long)max_tiles, a->max_ctx);
         return -1;
     }
-    const uint32_t table_need = (max_tiles + a->layout.token_count / kTileTokens - 1) /
-                                (a->layout.token_count / kTileTokens);
+    if (a->grid_waves > (1u << 20)) {
+        rl_set_error("rl_hip_attn_decode: grid_waves %u above 2^20", a->grid_waves);
+        return -1;
+    }
+    const uint32_t table_need = (a->max_ctx + a->layout.token_count - 1) / a->layout.token_count;
     if (a->table_stride < table_need) {
         rl_set_error("rl_hip_attn_decode: table_stride %u < %u blocks needed for max_ctx %u", a->table_stride,
                      table_need, a->max_ctx);
@@ -629,48 +788,43 @@ int validate(const rl_attn_decode_args_t *a)
 
 extern "C" size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *a)
 {
-    if (validate(a))
+    if (rl_require_open("rl_hip_attn_decode_workspace") || validate(a))
         return 0;
-    return ws_layout(a, chunk_tiles_of(a)).total;
+    return ws_layout(a).total;
 }
 
 extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
 {
     if (rl_require_open("rl_hip_attn_decode") || validate(a))
         return -1;
-    const uint32_t chunk_tiles = chunk_tiles_of(a);
-    const WsLayout w = ws_layout(a, chunk_tiles);
+    const WsLayout w = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < w.total) {
         rl_set_error("rl_hip_attn_decode: workspace %zu bytes < %zu required", a->workspace_bytes, w.total);
         return -1;
     }
-    const uint32_t max_tiles = (a->max_ctx + kTileTokens - 1) / kTileTokens;
-    const uint32_t max_chunks = max_tiles == 0 ? 1 : (max_tiles + chunk_tiles - 1) / chunk_tiles;
-
     AttnParams p;
     p.arena = (const uint8_t *)a->arena_base;
     p.block_bytes = a->layout.block_bytes;
     p.arena_blocks = a->arena_bytes / a->layout.block_bytes;
-    p.max_ctx = a->max_ctx;
     p.table = a->block_table;
     p.table_stride = a->table_stride;
     p.ctx = a->ctx_lens;
+    p.max_ctx = a->max_ctx;
+    p.batch = a->batch;
+    p.q_heads = a->q_heads;
+    p.kv_heads = a->kv_heads;
     p.q = (const uint16_t *)a->q;
     p.out = (uint16_t *)a->out;
     p.out_f32 = a->out_f32;
     const float scale = a->scale != 0.f ? a->scale : 1.0f / sqrtf((float)a->layout.head_dim);
     p.scale_log2 = scale * 1.4426950408889634f;
-    p.q_heads = a->q_heads;
-    p.kv_heads = a->kv_heads;
-    p.chunk_tiles = chunk_tiles;
-    p.max_chunks = max_chunks;
+    p.nwaves = waves_of(a);
     uint8_t *ws = (uint8_t *)a->workspace;
-    p.ws_ml = (float *)(ws + w.ml_off);
-    p.ws_o = (float *)(ws + w.o_off);
+    p.cum = (uint32_t *)(ws + w.cum_off);
+    p.part = (float *)(ws + w.part_off);
 
-    const dim3 grid(max_chunks, a->kv_heads, a->batch);
     const uint32_t G = a->q_heads / a->kv_heads;
     if (a->layout.head_dim == 128)
-        return dispatch_g<128>(p, grid, G, a->dtype, a->layout.token_count);
-    return dispatch_g<64>(p, grid, G, a->dtype, a->layout.token_count);
+        return dispatch_g<128>(p, G, a->dtype, a->layout.token_count);
+    return dispatch_g<64>(p, G, a->dtype, a->layout.token_count);
 }

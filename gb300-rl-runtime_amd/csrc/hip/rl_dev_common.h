@@ -118,6 +118,30 @@ __device__ __forceinline__ void rl_g2lds_16(const void *gsrc, RL_LDS void *lds_b
     __builtin_amdgcn_global_load_lds(gsrc, lds_base, 16, 0, 0);
 }
 
+// The same copy with a wave-uniform global base and a per-lane 32-bit offset,
+// issued as inline assembly: the compiler's wait insertion does not see it,
+// so it adds no conservative vmcnt(0) before LDS reads it cannot prove
+// disjoint. The caller orders every use with rl_wait_vmcnt. (Writing M0 needs
+// one wait state before an LDS-direct load reads it. M0 is reserved to the
+// compiler, which does not keep values in it across inline assembly; the
+// kernels using this helper make no other use of M0.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void rl_g2lds_16_off(const void *gbase, uint32_t voff, RL_LDS void *lds_base)
+{
+    // base and LDS address are wave-uniform; readfirstlane puts them in SGPRs
+    const uint64_t a = (uint64_t)(uintptr_t)gbase;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    const uint64_t base = ((uint64_t)hi << 32) | lo;
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)lds_base);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
 // Waits until at most N vector-memory operations of this wave are
 // outstanding (loads retire in issue order), e.g. the LDS-direct copies of
 // one staged unit while the next unit's copies stay in flight. The memory

@@ -2,11 +2,14 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 void rl_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int rl_check_hip(hipError_t e, const char *what);
 int rl_require_open(const char *what);
 hipStream_t rl_stream(void);
+// Compute units of the open device (0 when no device is open).
+uint32_t rl_cu_count(void);
 
 // Reports a launch error (or a fault of an earlier asynchronous call).
 static inline int rl_check_launch(const char *what)

@@ -22,6 +22,7 @@ constexpr int kMaxCoherent = 4096;
 struct Session {
     int open = 0;
     int device = -1;
+    uint32_t cu_count = 0;
     hipStream_t stream = nullptr;
     hipEvent_t ev_begin = nullptr;
     hipEvent_t ev_end = nullptr;
@@ -52,6 +53,8 @@ int rl_check_hip(hipError_t e, const char *what)
 }
 
 hipStream_t rl_stream(void) { return g_session.stream; }
+
+uint32_t rl_cu_count(void) { return g_session.cu_count; }
 
 int rl_require_open(const char *what)
 {
@@ -85,6 +88,11 @@ int rl_hip_open(int device)
     if (rl_check_hip(hipEventCreate(&g_session.ev_begin), "hipEventCreate") ||
         rl_check_hip(hipEventCreate(&g_session.ev_end), "hipEventCreate"))
         return -1;
+    int cus = 0;
+    if (rl_check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
+                     "hipDeviceGetAttribute(MultiprocessorCount)"))
+        return -1;
+    g_session.cu_count = cus > 0 ? (uint32_t)cus : 1u;
     g_session.device = device;
     g_session.open = 1;
     return 0;

@@ -127,7 +127,7 @@ class AttnArgs(C.Structure):
     _fields_ = [("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64), ("layout", KvLayoutDesc),
                 ("block_table", C.c_void_p), ("table_stride", C.c_uint32), ("batch", C.c_uint32),
                 ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32), ("dtype", C.c_uint32),
-                ("ctx_lens", C.c_void_p), ("max_ctx", C.c_uint32), ("chunk_tokens", C.c_uint32),
+                ("ctx_lens", C.c_void_p), ("max_ctx", C.c_uint32), ("grid_waves", C.c_uint32),
                 ("scale", C.c_float), ("q", C.c_void_p), ("out", C.c_void_p), ("out_f32", C.c_void_p),
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
@@ -302,13 +302,13 @@ class Timer:
 # ---------------------------------------------------------------- kernels
 def attn_args(arena: DeviceBuffer, layout: KvLayoutDesc, table: DeviceBuffer, table_stride: int, batch: int,
               q_heads: int, kv_heads: int, dtype: int, ctx: DeviceBuffer, max_ctx: int, q: DeviceBuffer,
-              out: DeviceBuffer, out_f32: DeviceBuffer | None = None, chunk_tokens: int = 0,
+              out: DeviceBuffer, out_f32: DeviceBuffer | None = None, grid_waves: int = 0,
               scale: float = 0.0) -> AttnArgs:
     a = AttnArgs()
     a.arena_base, a.arena_bytes, a.layout = arena.ptr, arena.nbytes, layout
     a.block_table, a.table_stride = table.ptr, table_stride
     a.batch, a.q_heads, a.kv_heads, a.dtype = batch, q_heads, kv_heads, dtype
-    a.ctx_lens, a.max_ctx, a.chunk_tokens, a.scale = ctx.ptr, max_ctx, chunk_tokens, scale
+    a.ctx_lens, a.max_ctx, a.grid_waves, a.scale = ctx.ptr, max_ctx, grid_waves, scale
     a.q, a.out, a.out_f32 = q.ptr, out.ptr, (out_f32.ptr if out_f32 is not None else None)
     return a
 
@@ -317,7 +317,7 @@ def attn_workspace(args: AttnArgs) -> DeviceBuffer:
     n = lib().rl_hip_attn_decode_workspace(C.byref(args))
     if n == 0:
         raise RlrtError(f"rl_hip_attn_decode_workspace: {_err()}")
-    ws = DeviceBuffer(n, zero=True)  # split counters must start at zero
+    ws = DeviceBuffer(n)
     args.workspace, args.workspace_bytes = ws.ptr, n
     return ws
 

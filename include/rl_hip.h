@@ -79,9 +79,10 @@ int rl_hip_timer_end(float *elapsed_ms);
  * with fp32 accumulation, stored in the input dtype (and optionally fp32).
  * ctx_lens[b] == 0 yields zeros. A rollout whose ctx_lens exceeds max_ctx or
  * whose block table names a block past arena_bytes gets NaN outputs (the
- * offending block is not read). Long contexts are split into chunks of
- * `chunk_tokens` processed by different workgroups and merged with an fp32
- * log-sum-exp combine (a second, small kernel on the same stream). */
+ * offending block is not read). The KV of all rows is split evenly over
+ * `grid_waves` persistent waves (0: every wave the device holds at once);
+ * rows shared by several waves are combined with an fp32 log-sum-exp merge
+ * (a second, small kernel on the same stream). */
 typedef struct {
     const void *arena_base;      /* device: KVArena.base */
     uint64_t arena_bytes;        /* KVArena.capacity: blocks past it are never read */
@@ -94,7 +95,7 @@ typedef struct {
     uint32_t dtype;              /* RL_DTYPE_* of q, K, V and out */
     const uint32_t *ctx_lens;    /* device [batch] */
     uint32_t max_ctx;            /* upper bound of ctx_lens; sizes the grid */
-    uint32_t chunk_tokens;       /* multiple of 64 in [64, 2048]; 0 selects a default */
+    uint32_t grid_waves;         /* waves sharing the KV stream, <= 2^20; 0 selects a full device */
     float scale;                 /* 0 selects 1/sqrt(head_dim) */
     const void *q;               /* device [batch][q_heads][head_dim] */
     void *out;                   /* device [batch][q_heads][head_dim] */

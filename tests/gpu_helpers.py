@@ -4,7 +4,7 @@ import numpy as np
 import synth
 
 
-def run_attn(rl, w, chunk_tokens=0, max_ctx=None, repeats=1, arena_bytes=None):
+def run_attn(rl, w, grid_waves=0, max_ctx=None, repeats=1, arena_bytes=None):
     """Uploads a DecodeWorkload, runs rl_hip_attn_decode, returns (out16, out_f32)."""
     layout = rl.KvLayoutDesc.paged(w.token_count, w.head_dim)
     arena = rl.DeviceBuffer.from_array(w.arena)
@@ -17,7 +17,7 @@ def run_attn(rl, w, chunk_tokens=0, max_ctx=None, repeats=1, arena_bytes=None):
     mc = w.max_ctx if max_ctx is None else max_ctx
     args = rl.attn_args(arena, layout, table, w.table_stride, w.batch, w.q_heads, w.kv_heads,
                         rl.DTYPE_BF16 if w.dtype == "bf16" else rl.DTYPE_FP16, ctx, max(mc, 1), q, out, out32,
-                        chunk_tokens=chunk_tokens)
+                        grid_waves=grid_waves)
     if arena_bytes is not None:
         args.arena_bytes = arena_bytes
     ws = rl.attn_workspace(args)

@@ -50,11 +50,22 @@ def test_mha_fp16_d64_plumbing_shape(rl, gpu, orc, olib):
                                             (4, 1, 64, "fp16", 32), (8, 1, 128, "bf16", 16),
                                             (2, 2, 64, "bf16", 16)])
 def test_shapes_and_edges(rl, gpu, orc, olib, qh, kvh, d, dt, tpb):
-    # contexts straddling tile (16), unit, chunk (64/128) and block boundaries
+    # contexts straddling tile (16) and block (16/32) boundaries; the wave
+    # counts put row starts and ends at every position of a wave's range:
+    # one wave streaming every row, odd splits, more waves than tiles
     ctx = np.array([1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 513], dtype=np.uint32)
     w = synth.make_decode(7, len(ctx), qh, kvh, d, 0, 0, dtype=dt, token_count=tpb, ctx=ctx)
-    for chunk in (0, 64, 128):
-        _case(rl, orc, olib, w, chunk_tokens=chunk)
+    for waves in (0, 1, 7, 61, 5000):
+        _case(rl, orc, olib, w, grid_waves=waves)
+
+
+def test_long_rows_in_few_waves(rl, gpu, orc, olib):
+    """Rows of up to 512 tiles streamed by 1-3 waves: block-table windows of
+    128 entries are reloaded inside a row, rows continue across waves."""
+    ctx = np.array([8192, 3000, 17, 4100], dtype=np.uint32)
+    w = synth.make_decode(11, len(ctx), 16, 4, 128, 0, 0, dtype="bf16", ctx=ctx)
+    for waves in (1, 2, 3):
+        _case(rl, orc, olib, w, grid_waves=waves)
 
 
 def test_empty_context_gives_zeros(rl, gpu, orc, olib):
@@ -85,10 +96,10 @@ def test_fixed128_reference_vector(rl, gpu, orc, olib):
 
 
 def test_repeated_split_launches_are_identical(rl, gpu, orc, olib):
-    """The cross-chunk merge counters reset themselves: back-to-back launches
-    give bit-identical results."""
+    """Back-to-back launches (partials and prefix rewritten each time) give
+    bit-identical results."""
     w = synth.make_decode(9, 4, 32, 8, 128, 1500, 3000, dtype="bf16")
-    res = gh.run_attn(rl, w, chunk_tokens=256, repeats=3)
+    res = gh.run_attn(rl, w, grid_waves=37, repeats=3)
     for o16, o32 in res[1:]:
         assert np.array_equal(o16, res[0][0]) and np.array_equal(o32, res[0][1])
     gh.check_attn(res[0][0], res[0][1], orc.attn_f64(olib, w, 0), "bf16")
