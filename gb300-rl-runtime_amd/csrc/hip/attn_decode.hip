@@ -602,10 +602,18 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
 // Combines the partials of every row split across waves:
 // M = max_w m_w, L = sum_w l_w 2^(m_w - M), O = sum_w o_w 2^(m_w - M), out = O / L.
 // Also writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN).
+// The (max, sum) pairs of up to kMergeLds partials are loaded in parallel into
+// LDS, the per-head scale factors computed once, and every output element then
+// sums its partials with independent loads.
+constexpr int kMergeLds = 256;
+
 template <int D, int G, int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
 {
     constexpr int PART = G * D + 2 * G;
+    __shared__ float s_f[kMergeLds * G];  // m, then the scale 2^(m - M)
+    __shared__ float s_l[kMergeLds * G];
+    __shared__ float s_L[G];
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
     const uint32_t row = b * p.kv_heads + g;
@@ -633,6 +641,87 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
         return;  // one wave covered the row and wrote it
     const float *part = p.part + (size_t)(wf + row) * PART;
     const uint32_t np = wl - wf + 1;
+    constexpr int EPT = (G * D + 255) / 256;  // output elements per thread
+    constexpr int NPR = 8;                    // partials merged from registers
+    if (np <= (uint32_t)NPR) {
+        // few partials: every load is issued before the first use
+        float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
+#pragma unroll
+        for (int i = 0; i < NPR; i++)
+#pragma unroll
+            for (int k = 0; k < EPT; k++) {
+                const int e = threadIdx.x + 256 * k;
+                const bool ok = (uint32_t)i < np && e < G * D;
+                const float *pp = part + (size_t)(ok ? i : 0) * PART;
+                const int h = (e < G * D ? e : 0) / D;
+                o[i][k] = ok ? pp[e] : 0.f;
+                mm[i][k] = ok ? pp[G * D + 2 * h] : -INFINITY;
+                ll[i][k] = ok ? pp[G * D + 2 * h + 1] : 0.f;
+            }
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const int e = threadIdx.x + 256 * k;
+            if (e >= G * D)
+                break;
+            float M = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < NPR; i++)
+                M = fmaxf(M, mm[i][k]);
+            float L = 0.f, O = 0.f;
+#pragma unroll
+            for (int i = 0; i < NPR; i++) {
+                const float f = mm[i][k] == -INFINITY ? 0.f : exp2f(mm[i][k] - M);
+                L = fmaf(ll[i][k], f, L);
+                O = fmaf(o[i][k], f, O);
+            }
+            float v = (L > 0.f || L != L) ? O / L : 0.f;
+            if (bad)
+                v = __builtin_nanf("");
+            p.out[obase + e] = rl_from_f32<DT>(v);
+            if (p.out_f32)
+                p.out_f32[obase + e] = v;
+        }
+        return;
+    }
+    if (np <= (uint32_t)kMergeLds) {
+        for (uint32_t t = threadIdx.x; t < np * G; t += 256) {
+            const uint32_t i = t / G, h = t % G;
+            s_f[t] = part[(size_t)i * PART + G * D + 2 * h];
+            s_l[t] = part[(size_t)i * PART + G * D + 2 * h + 1];
+        }
+        __syncthreads();
+        if (threadIdx.x < G) {
+            const int h = threadIdx.x;
+            float M = -INFINITY;
+            for (uint32_t i = 0; i < np; i++)
+                M = fmaxf(M, s_f[i * G + h]);
+            float L = 0.f;
+            for (uint32_t i = 0; i < np; i++) {
+                const float mi = s_f[i * G + h];
+                const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
+                s_f[i * G + h] = f;
+                L = fmaf(s_l[i * G + h], f, L);
+            }
+            s_L[h] = L;
+        }
+        __syncthreads();
+        for (int e = threadIdx.x; e < G * D; e += 256) {
+            const int h = e / D;
+            float O = 0.f;
+#pragma unroll 8
+            for (uint32_t i = 0; i < np; i++)
+                O = fmaf(part[(size_t)i * PART + e], s_f[i * G + h], O);
+            const float L = s_L[h];
+            float v = (L > 0.f || L != L) ? O / L : 0.f;
+            if (bad)
+                v = __builtin_nanf("");
+            p.out[obase + e] = rl_from_f32<DT>(v);
+            if (p.out_f32)
+                p.out_f32[obase + e] = v;
+        }
+        return;
+    }
+    // very long rows: stream the partials per element
     for (int e = threadIdx.x; e < G * D; e += 256) {
         const int h = e / D;
         float M = -INFINITY;

@@ -110,6 +110,57 @@ __device__ __forceinline__ float rl_row_sum(float x)
     return x;
 }
 
+// ---- whole-wave scans and reductions on u32 (DPP, no LDS crossbar) ---------
+// row_shr:1/2/4/8 (0x111, 0x112, 0x114, 0x118; lanes without a source read 0)
+// give an inclusive scan inside each row of 16 lanes; row_bcast:15 (0x142) on
+// rows 1 and 3 and row_bcast:31 (0x143) on rows 2 and 3 carry the row totals.
+
+template <int CTRL, int ROW_MASK, bool BOUND_ZERO>
+__device__ __forceinline__ uint32_t rl_dpp_u32(uint32_t x)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, BOUND_ZERO);
+}
+
+__device__ __forceinline__ uint32_t rl_wave_incl_scan_u32(uint32_t x)
+{
+    x += rl_dpp_u32<0x111, 0xF, true>(x);
+    x += rl_dpp_u32<0x112, 0xF, true>(x);
+    x += rl_dpp_u32<0x114, 0xF, true>(x);
+    x += rl_dpp_u32<0x118, 0xF, true>(x);
+    x += rl_dpp_u32<0x142, 0xA, false>(x);
+    x += rl_dpp_u32<0x143, 0xC, false>(x);
+    return x;
+}
+
+__device__ __forceinline__ uint32_t rl_readlane(uint32_t x, int lane)
+{
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
+}
+
+// Wave-uniform min / max / sum of a u32 held by every lane.
+__device__ __forceinline__ uint32_t rl_wave_min_u32(uint32_t x)
+{
+    x = min(x, rl_dpp_u32<0xB1, 0xF, false>(x));
+    x = min(x, rl_dpp_u32<0x4E, 0xF, false>(x));
+    x = min(x, rl_dpp_u32<0x141, 0xF, false>(x));
+    x = min(x, rl_dpp_u32<0x140, 0xF, false>(x));
+    return min(min(rl_readlane(x, 0), rl_readlane(x, 16)), min(rl_readlane(x, 32), rl_readlane(x, 48)));
+}
+
+__device__ __forceinline__ uint32_t rl_wave_max_u32(uint32_t x)
+{
+    x = max(x, rl_dpp_u32<0xB1, 0xF, false>(x));
+    x = max(x, rl_dpp_u32<0x4E, 0xF, false>(x));
+    x = max(x, rl_dpp_u32<0x141, 0xF, false>(x));
+    x = max(x, rl_dpp_u32<0x140, 0xF, false>(x));
+    return max(max(rl_readlane(x, 0), rl_readlane(x, 16)), max(rl_readlane(x, 32), rl_readlane(x, 48)));
+}
+
+__device__ __forceinline__ uint32_t rl_wave_sum_u32(uint32_t x)
+{
+    return rl_readlane(rl_wave_incl_scan_u32(x), 63);
+}
+
 // ---- LDS-direct staging ---------------------------------------------------
 // global_load_lds_dwordx4: each lane fetches 16 bytes from its own global
 // address; they land at lds_base + lane * 16 (lds_base wave-uniform).

@@ -4,19 +4,21 @@
 // thread, O(V*k) insertion top-k, xoshiro256** draw, float CDF walk) with a
 // two-kernel, HBM-streaming design:
 //
-//  split  grid (split, row): each 256-thread workgroup streams a 16,384-
-//         element slice of one row (64 fp32 per thread, 16-byte loads) and
+//  split  grid (split, row): each 256-thread workgroup streams an 8,192-
+//         element slice of one row (32 fp32 per thread, 16-byte loads) and
 //         emits: the slice max of x = l * inv_t and sum exp(x - max) (for the
 //         log-sum-exp), the slice argmax (greedy), and for top-k the slice's
 //         candidates: every element >= a lower bound of the slice's k-th
 //         largest value. The bound is the minimum over the four waves of each
 //         wave's ceil(k/4)-th largest lane maximum (found with a 32-step ballot
 //         radix select), so at least k distinct elements lie above it.
-//  merge  grid (row): one workgroup merges the slices: global max and
-//         log-sum-exp, exact k-th largest among the candidates (4-pass 8-bit
-//         radix select in LDS), sort of the kept set by (x desc, index asc),
+//  merge  grid (row): one 256-thread workgroup merges the slices: global max
+//         and log-sum-exp, exact k-th largest among the candidates (4-pass
+//         8-bit radix select on LDS histograms, each wave finding the digit
+//         with DPP scans), rank sort of the kept set by (x desc, index asc),
 //         24-bit integer weights rl_sample_weight(x - max), nucleus prefix,
-//         Philox4x32-10 draw and the ascending-index integer CDF walk.
+//         Philox4x32-10 draw and the ascending-index integer CDF walk - in one
+//         wave when at most 64 elements are kept.
 // Integer weights make every sum exact, so the token is bit-identical to the
 // host restatement whatever the reduction order.
 #include <hip/hip_runtime.h>
@@ -31,12 +33,11 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerThread = 64;
-constexpr int kSplitLen = kThreads * kPerThread;  // 16,384 elements
+constexpr int kPerThread = 32;
+constexpr int kSplitLen = kThreads * kPerThread;  // 8,192 elements
 constexpr int kCandCap = 1024;                    // candidates per split
 constexpr int kMergeCap = 8192;                   // candidates per row in the merge
 constexpr int kKeptCap = 1024;                    // kept (top-k with ties) per row
-constexpr int kRegCand = 16;                      // merge fast path: candidates per lane
 
 struct SplitStat {
     float max_x;     // slice max of x
@@ -44,7 +45,8 @@ struct SplitStat {
     float arg_val;   // greedy: slice max of raw logits
     uint32_t arg_idx;
     uint32_t n_cand;  // candidates written (> kCandCap: overflow)
-    uint32_t pad[3];
+    uint32_t cand_lo; // every candidate key is >= this
+    uint32_t pad[2];
 };
 
 struct SampleParams {
@@ -91,20 +93,22 @@ __device__ __forceinline__ uint32_t effective_k(uint32_t k, uint32_t vocab)
     return k < RL_SAMPLE_TOPK_MAX ? k : RL_SAMPLE_TOPK_MAX;
 }
 
+__device__ __forceinline__ float readlane_f(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// wave-uniform max / sum: DPP inside each row of 16, then the four row results
 __device__ __forceinline__ float wave_max(float v)
 {
     v = rl_row_max(v);
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 __device__ __forceinline__ float wave_sum(float v)
 {
     v = rl_row_sum(v);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 // (value desc, index asc) argmax across the wave.
@@ -207,7 +211,7 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
             const float ml = m * 1.4426950408889634f;
 #pragma unroll
             for (int i = 0; i < kPerThread; i++)
-                z += exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
+                z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
         }
         z = wave_sum(z);
         __syncthreads();
@@ -233,6 +237,7 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
     const float wmax = wave_max(tmax);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
+    uint32_t cand_lo = 0;
     if (k_eff != 0) {
         const uint32_t kw = (k_eff + 3) / 4;
         const uint32_t ck = wave_kth_largest_key(rl_float_key(tmax), kw);
@@ -250,12 +255,13 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
         const float ml = m * 1.4426950408889634f;
 #pragma unroll
         for (int i = 0; i < kPerThread; i++)
-            z += exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
+            z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
     }
     z = wave_sum(z);
 
     if (k_eff != 0) {
         const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
+        cand_lo = clb;
         // count, block-wide exclusive scan, then write: no per-element ballots
         uint32_t cnt = 0;
 #pragma unroll
@@ -302,10 +308,14 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
         st->arg_val = m;
         st->arg_idx = 0;
         st->n_cand = s_ncand;
+        st->cand_lo = cand_lo;
     }
 }
 
-// ---- single-wave merge helpers ---------------------------------------------
+// ---- block-wide helpers of the merge (256 threads = 4 waves) ----------------
+
+constexpr int kMergeThreads = 256;
+constexpr int kMergeWaves = kMergeThreads / 64;
 
 __device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v)
 {
@@ -319,14 +329,6 @@ __device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v)
     return v;
 }
 
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
-{
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1)
-        v += __shfl_xor(v, off);
-    return v;
-}
-
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
 {
 #pragma unroll
@@ -335,9 +337,96 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1)
+        v = max(v, __shfl_xor(v, off));
+    return v;
+}
 
-// One wave per row: every barrier below is a single-wave s_barrier.
-constexpr int kMergeThreads = 64;
+struct BlockShared {
+    unsigned long long w64[kMergeWaves];
+    uint32_t w32[kMergeWaves];
+    unsigned long long sel64;
+    uint32_t n;
+};
+
+// Exclusive prefix over the block in thread order; `total` gets the block sum.
+__device__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t &total, BlockShared &bs)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t incl = wave_inclusive_scan_u64(v);
+    if (lane == 63)
+        bs.w64[wave] = incl;
+    __syncthreads();
+    uint64_t base = 0, t = 0;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; w++) {
+        const uint64_t x = bs.w64[w];
+        base += w < wave ? x : 0ull;
+        t += x;
+    }
+    __syncthreads();
+    total = t;
+    return base + incl - v;
+}
+
+__device__ uint64_t block_sum_u64(uint64_t v, BlockShared &bs)
+{
+    uint64_t total;
+    (void)block_excl_scan_u64(v, total, bs);
+    return total;
+}
+
+__device__ uint32_t block_min_u32(uint32_t v, BlockShared &bs)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_min_u32(v);
+    if (lane == 0)
+        bs.w32[wave] = v;
+    __syncthreads();
+    uint32_t r = bs.w32[0];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; w++)
+        r = min(r, bs.w32[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ uint32_t block_max_u32(uint32_t v, BlockShared &bs)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    v = wave_max_u32(v);
+    if (lane == 0)
+        bs.w32[wave] = v;
+    __syncthreads();
+    uint32_t r = bs.w32[0];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; w++)
+        r = max(r, bs.w32[w]);
+    __syncthreads();
+    return r;
+}
+
+// One digit of an MSB-first radix search over a 256-bin histogram (thread t
+// passes bin 255 - t): the highest digit d in [1, 255] for which
+// above + sum(bins >= d) reaches need, else 0. `acc` receives
+// above + sum(bins > d), the amount ranked strictly above the chosen digit.
+__device__ uint32_t block_pick_digit(uint64_t h, uint64_t above, uint64_t need, uint64_t &acc, BlockShared &bs)
+{
+    const uint32_t r = 255u - threadIdx.x;
+    uint64_t total;
+    const uint64_t S = block_excl_scan_u64(h, total, bs);  // bins > r
+    const bool cross = r >= 1u && above + S < need && above + S + h >= need;
+    const uint32_t d = block_max_u32(cross ? r : 0u, bs);
+    if (r == d)
+        bs.sel64 = above + S;
+    __syncthreads();
+    acc = bs.sel64;
+    __syncthreads();
+    return d;
+}
 
 // ---- exact full-row path -----------------------------------------------------
 // Used for rows without top-k (whole-vocabulary nucleus) and for rows whose
@@ -353,57 +442,45 @@ __device__ __forceinline__ uint64_t composite_key(uint32_t key, uint32_t idx)
 }
 
 __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff, float topp,
-                                     float m, uint32_t *s_hist, unsigned long long *s_whist)
+                                     float m, uint32_t *s_hist, unsigned long long *s_whist, BlockShared &bs)
 {
-    const int lane = threadIdx.x;
+    const uint32_t tid = threadIdx.x;
     const float *l = p.logits + (size_t)row * p.row_stride;
     const uint32_t V = p.vocab;
 
     // (1) cutoff key: k_eff-th largest finite x (multiplicity counted); 0 keeps all.
     uint32_t cutoff = 0;
     if (k_eff) {
-        uint32_t prefix = 0, mask = 0, need = k_eff;
+        uint32_t prefix = 0, mask = 0;
+        uint64_t need = k_eff;
         for (int pass = 3; pass >= 0; pass--) {
             const int shift = pass * 8;
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-                s_hist[lane * 4 + b] = 0;
+            s_hist[tid] = 0;
             __syncthreads();
-            for (uint32_t i = lane; i < V; i += kMergeThreads) {
+            for (uint32_t i = tid; i < V; i += kMergeThreads) {
                 const float x = l[i] * inv_t;
                 const uint32_t key = rl_float_key(x);
                 if (x != -INFINITY && (key & mask) == prefix)
                     atomicAdd(&s_hist[(key >> shift) & 0xFFu], 1u);
             }
             __syncthreads();
-            if (lane == 0) {
-                uint32_t acc = 0;
-                int d = 255;
-                for (; d > 0; d--) {
-                    if (acc + s_hist[d] >= need)
-                        break;
-                    acc += s_hist[d];
-                }
-                s_hist[256] = (uint32_t)d;
-                s_hist[257] = need - acc;
-            }
-            __syncthreads();
-            prefix |= s_hist[256] << shift;
+            uint64_t acc;
+            const uint32_t d = block_pick_digit(s_hist[255 - tid], 0, need, acc, bs);
+            prefix |= d << shift;
             mask |= 0xFFu << shift;
-            need = s_hist[257];
-            __syncthreads();
+            need -= acc;
         }
         cutoff = prefix;
     }
 
     // (2) W_K
     uint64_t wk_own = 0;
-    for (uint32_t i = lane; i < V; i += kMergeThreads) {
+    for (uint32_t i = tid; i < V; i += kMergeThreads) {
         const float x = l[i] * inv_t;
         if (x != -INFINITY && rl_float_key(x) >= cutoff)
             wk_own += rl_sample_weight(x - m);
     }
-    const uint64_t wk = __shfl(wave_inclusive_scan_u64(wk_own), 63);
+    const uint64_t wk = block_sum_u64(wk_own, bs);
 
     // (3) nucleus boundary tau: the largest composite key whose suffix weight reaches thr.
     uint64_t tau = 0;
@@ -412,11 +489,9 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
         uint64_t prefix = 0, mask = 0, above = 0;
         for (int pass = 7; pass >= 0; pass--) {
             const int shift = pass * 8;
-#pragma unroll
-            for (int b = 0; b < 4; b++)
-                s_whist[lane * 4 + b] = 0;
+            s_whist[tid] = 0;
             __syncthreads();
-            for (uint32_t i = lane; i < V; i += kMergeThreads) {
+            for (uint32_t i = tid; i < V; i += kMergeThreads) {
                 const float x = l[i] * inv_t;
                 const uint32_t key = rl_float_key(x);
                 if (x == -INFINITY || key < cutoff)
@@ -426,24 +501,12 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
                     atomicAdd(&s_whist[(ck >> shift) & 0xFFu], (unsigned long long)rl_sample_weight(x - m));
             }
             __syncthreads();
-            if (lane == 0) {
-                // Highest digit whose cumulative weight from the top reaches thr
-                // (thr >= 1 whenever K is non-empty: the row maximum weighs 2^24).
-                uint64_t acc = above;
-                int d = 255;
-                for (; d > 0; d--) {
-                    if (acc + s_whist[d] >= thr)
-                        break;
-                    acc += s_whist[d];
-                }
-                s_whist[256] = (unsigned long long)d;
-                s_whist[257] = acc;
-            }
-            __syncthreads();
-            prefix |= (uint64_t)s_whist[256] << shift;
+            // (thr >= 1 whenever K is non-empty: the row maximum weighs 2^24)
+            uint64_t acc;
+            const uint32_t d = block_pick_digit(s_whist[255 - tid], above, thr, acc, bs);
+            prefix |= (uint64_t)d << shift;
             mask |= 0xFFull << shift;
-            above = s_whist[257];
-            __syncthreads();
+            above = acc;
         }
         tau = prefix;
     }
@@ -451,7 +514,7 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
     // (4) W_P and the lowest index of P
     uint64_t wp_own = 0;
     uint32_t lowest = 0xFFFFFFFFu;
-    for (uint32_t i = lane; i < V; i += kMergeThreads) {
+    for (uint32_t i = tid; i < V; i += kMergeThreads) {
         const float x = l[i] * inv_t;
         const uint32_t key = rl_float_key(x);
         if (x != -INFINITY && key >= cutoff && composite_key(key, i) >= tau) {
@@ -459,10 +522,10 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
             lowest = min(lowest, i);
         }
     }
-    const uint64_t wp = __shfl(wave_inclusive_scan_u64(wp_own), 63);
-    lowest = wave_min_u32(lowest);
+    const uint64_t wp = block_sum_u64(wp_own, bs);
+    lowest = block_min_u32(lowest, bs);
 
-    // (5) ascending-index walk: chunks of 64 lanes x 8 contiguous elements
+    // (5) ascending-index walk: chunks of 256 threads x 8 contiguous elements
     const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
     uint64_t carry = 0;
     uint32_t tok = 0xFFFFFFFFu;
@@ -470,7 +533,7 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
         uint64_t w8[8], own = 0;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const uint32_t i = base + lane * 8 + e;
+            const uint32_t i = base + tid * 8 + e;
             w8[e] = 0;
             if (i < V) {
                 const float x = l[i] * inv_t;
@@ -480,18 +543,18 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
             }
             own += w8[e];
         }
-        const uint64_t incl = wave_inclusive_scan_u64(own);
-        const uint64_t total = __shfl(incl, 63);
+        uint64_t total;
+        const uint64_t excl = block_excl_scan_u64(own, total, bs);
         if (carry + total > u) {
-            uint64_t c = carry + incl - own;
+            uint64_t c = carry + excl;
             uint32_t cand = 0xFFFFFFFFu;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 c += w8[e];
                 if (cand == 0xFFFFFFFFu && c > u)
-                    cand = base + lane * 8 + e;
+                    cand = base + tid * 8 + e;
             }
-            tok = wave_min_u32(cand);
+            tok = block_min_u32(cand, bs);
         }
         carry += total;
     }
@@ -502,32 +565,39 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
     return tok;
 }
 
+// One workgroup of 256 threads per row.
 __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParams p)
 {
     const uint32_t row = blockIdx.x;
-    const int lane = threadIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63;
 
     __shared__ uint2 s_cand[kMergeCap];
-    __shared__ uint32_t s_hist[258];
-    __shared__ unsigned long long s_whist[258];
-    __shared__ uint64_t s_sort[kKeptCap];
-    __shared__ uint32_t s_w[kKeptCap];
-    __shared__ uint32_t s_nk;
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_h2[2][256];
+    __shared__ unsigned long long s_whist[256];
+    __shared__ uint64_t s_keep[kKeptCap];   // kept composite keys, unordered
+    __shared__ uint64_t s_sort[kKeptCap];   // ... sorted descending
+    __shared__ uint32_t s_w[kKeptCap];      // weights in sorted order
+    __shared__ uint32_t s_idx[kKeptCap];    // token index in sorted order
+    __shared__ BlockShared bs;
 
     const SplitStat *st = p.stats + (size_t)row * p.splits;
     const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
 
-    // Global max and log-sum-exp over the slices (splits <= 64: one per lane).
+    // Global max and log-sum-exp over the slices (splits <= 64: one per lane;
+    // every wave computes the same values).
     float mx = -INFINITY, zs = 0.f;
     uint32_t ncand = 0;
     float av = -INFINITY;
-    uint32_t ai = 0xFFFFFFFFu;
+    uint32_t ai = 0xFFFFFFFFu, clo = 0xFFFFFFFFu;
     if ((uint32_t)lane < p.splits) {
         mx = st[lane].max_x;
         zs = st[lane].sum_exp;
         ncand = st[lane].n_cand;
         av = st[lane].arg_val;
         ai = st[lane].arg_idx;
+        clo = st[lane].n_cand ? st[lane].cand_lo : 0xFFFFFFFFu;
     }
     const float m = wave_max(mx);
     const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
@@ -535,7 +605,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 
     if (greedy) {
         wave_argmax(av, ai);
-        if (lane == 0) {
+        if (tid == 0) {
             const uint32_t i = ai >= p.vocab ? 0u : ai;  // all -inf: lowest index
             p.token_out[row] = i;
             p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + i] - lse;
@@ -546,274 +616,234 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const float inv_t = 1.0f / row_temperature(p, row);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
     const float topp = row_topp(p, row);
-    // ---- gather the slices' candidates --------------------------------------
     const bool split_over = __ballot(ncand > (uint32_t)kCandCap) != 0;
     const uint64_t cum = wave_inclusive_scan_u64(ncand);
     const uint32_t n = (uint32_t)__shfl(cum, 63);
+    uint32_t tok;
     if (k_eff == 0 || split_over || n > (uint32_t)kMergeCap) {
-        const uint32_t tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist);
-        if (lane == 0) {
-            p.token_out[row] = tok;
-            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+        tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist, bs);
+    } else {
+        // ---- gather the slices' candidates ----------------------------------
+        // Flat slot f belongs to the split whose inclusive count first exceeds
+        // it; each thread issues all its loads before storing any.
+        constexpr int kGather = 8;
+        const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandCap;
+        for (uint32_t base = 0; base < n; base += kMergeThreads * kGather) {
+            uint32_t sp[kGather], excl[kGather];
+#pragma unroll
+            for (int r = 0; r < kGather; r++)
+                sp[r] = excl[r] = 0;
+            for (uint32_t t = 0; t < p.splits; t++) {
+                const uint32_t inc = rl_readlane((uint32_t)cum, (int)t);
+#pragma unroll
+                for (int r = 0; r < kGather; r++) {
+                    const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
+                    if (inc <= f) {
+                        sp[r] = t + 1;
+                        excl[r] = inc;
+                    }
+                }
+            }
+            uint2 v[kGather];
+#pragma unroll
+            for (int r = 0; r < kGather; r++) {
+                const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
+                v[r] = f < n ? rbase[(size_t)sp[r] * kCandCap + (f - excl[r])] : make_uint2(0u, 0u);
+            }
+#pragma unroll
+            for (int r = 0; r < kGather; r++) {
+                const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
+                if (f < n)
+                    s_cand[f] = v[r];
+            }
         }
-        return;
-    }
-    for (uint32_t s = 0; s < p.splits; s++) {
-        const uint32_t cnt = __shfl(ncand, s);
-        const uint32_t off = (uint32_t)__shfl(cum, s) - cnt;
-        const uint2 *src = p.cand + ((size_t)row * p.splits + s) * kCandCap;
-        for (uint32_t i = lane; i < cnt; i += kMergeThreads)
-            s_cand[off + i] = src[i];
-    }
-    __syncthreads();
+        if (tid == 0)
+            bs.n = 0;
+        s_h2[0][tid] = 0;
+        __syncthreads();
 
-    // ---- fast path: candidates in registers, kept set of at most 64 ---------
-    if (n <= (uint32_t)(kMergeThreads * kRegCand)) {
-        uint32_t key[kRegCand], idx[kRegCand];
-#pragma unroll
-        for (int j = 0; j < kRegCand; j++) {
-            const uint32_t f = (uint32_t)(j * kMergeThreads + lane);
-            const uint2 c = f < n ? s_cand[f] : make_uint2(0u, 0u);  // key 0: below every real key
-            key[j] = c.x;
-            idx[j] = c.y;
-        }
-        // exact k_eff-th largest key: MSB-first, counting keys >= candidate
+        // ---- exact k_eff-th largest key --------------------------------------
+        // Every candidate key lies in [key_lo, key_hi] (the slices' bounds and
+        // the row max), so the MSB-first radix select starts at the highest bit
+        // where those differ: 8-bit digits, and the first pass already spreads
+        // the candidates over many bins. The pass's histogram is filled while
+        // the other one is cleared; every wave then finds the digit itself:
+        // lane l holds bins 255-4l .. 252-4l, a DPP scan gives the count in
+        // higher bins, and the digit is the bin where that count reaches need.
+        // With fewer than k_eff candidates the row has fewer than k_eff finite
+        // logits, and every finite one is kept.
         uint32_t cutoff = 0;
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t cand = cutoff | (1u << bit);
-            uint32_t cnt = 0;
+        if (n >= k_eff) {
+            const uint32_t key_lo = rl_wave_min_u32(clo);
+            const uint32_t key_hi = rl_float_key(m);
+            const uint32_t diff = key_lo ^ key_hi;
+            if (diff == 0) {
+                cutoff = key_hi;
+            } else {
+                const int hb = 31 - __builtin_clz(diff);
+                uint32_t prefix = key_hi & ~((2u << hb) - 1u);
+                uint32_t need = k_eff;
+                int pass = 0;
+                for (int top = hb; top >= 0; top -= 8, pass++) {
+                    const int shift = top >= 7 ? top - 7 : 0;
+                    const uint32_t above = top >= 31 ? 0u : ~((2u << top) - 1u);
+                    uint32_t *H = s_h2[pass & 1];
+                    for (uint32_t i = tid; i < n; i += kMergeThreads) {
+                        const uint32_t key = s_cand[i].x;
+                        if ((key & above) == prefix)
+                            atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
+                    }
+                    __syncthreads();
+                    s_h2[(pass & 1) ^ 1][tid] = 0;
+                    uint32_t h[4], own = 0;
 #pragma unroll
-            for (int j = 0; j < kRegCand; j++)
-                cnt += key[j] >= cand ? 1u : 0u;
-            if (wave_sum_u32(cnt) >= k_eff)
-                cutoff = cand;
+                    for (int j = 0; j < 4; j++) {
+                        h[j] = H[255 - 4 * lane - j];
+                        own += h[j];
+                    }
+                    uint32_t acc = rl_wave_incl_scan_u32(own) - own;
+                    int found = -1;
+                    uint32_t rem = 0;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        if (found < 0 && acc < need && acc + h[j] >= need) {
+                            found = 255 - 4 * lane - j;
+                            rem = need - acc;
+                        }
+                        acc += h[j];
+                    }
+                    const uint64_t hit = __ballot(found >= 0);  // never empty: need <= matching keys
+                    const int src = hit ? (int)__ffsll((long long)hit) - 1 : 0;
+                    prefix |= (uint32_t)__builtin_amdgcn_readlane(found, src) << shift;
+                    need = rl_readlane(rem, src);
+                    __syncthreads();
+                }
+                cutoff = prefix;
+            }
         }
-        // (padding slots hold key 0, below every finite key, and are never kept;
-        // cutoff itself stays 0 only when the row has fewer than k finite logits)
-        uint32_t kept = 0;
-#pragma unroll
-        for (int j = 0; j < kRegCand; j++)
-            kept += (key[j] >= cutoff && key[j] != 0u) ? 1u : 0u;
-        const uint32_t nk = wave_sum_u32(kept);
-        if (nk <= 64u) {
-            // compact the kept set to one element per lane
-            uint32_t pos = 0;
-            {
-                uint32_t incl = kept;
-#pragma unroll
-                for (int off = 1; off < 64; off <<= 1) {
-                    const uint32_t o = __shfl_up(incl, off);
-                    if (lane >= off)
-                        incl += o;
+
+        // ---- kept set K = {key >= cutoff} ------------------------------------
+        for (uint32_t i = tid; i < n; i += kMergeThreads) {
+            const uint2 c = s_cand[i];
+            if (c.x >= cutoff) {
+                const uint32_t pos = atomicAdd(&bs.n, 1u);
+                if (pos < (uint32_t)kKeptCap)
+                    s_keep[pos] = composite_key(c.x, c.y);
+            }
+        }
+        __syncthreads();
+        const uint32_t nk = bs.n;
+        __syncthreads();
+        if (nk > (uint32_t)kKeptCap) {
+            tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist, bs);
+        } else if (nk <= 64u) {
+            // ---- one wave: lane i holds sorted element i; with at most 64
+            // weights of at most 2^24 every prefix fits in 32 bits ------------
+            tok = 0;
+            if (tid < 64) {
+                const bool valid = (uint32_t)lane < nk;
+                const uint64_t ck = valid ? s_keep[lane] : 0ull;  // real keys are > 0
+                // rank = kept keys above mine (broadcast LDS reads, independent)
+                uint32_t rank = 0;
+                for (uint32_t j = 0; j < nk; j++)
+                    rank += s_keep[j] > ck ? 1u : 0u;
+                if (valid)
+                    s_sort[rank] = ck;
+                rl_wave_lds_fence();
+                const uint64_t cs = valid ? s_sort[lane] : 0ull;
+                const uint32_t idx = 0xFFFFFFFFu - (uint32_t)cs;
+                const uint32_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(cs >> 32)) - m) : 0u;
+                s_idx[lane] = idx;
+                s_w[lane] = w;
+                const uint32_t c = rl_wave_incl_scan_u32(w);
+                const uint32_t wk = rl_readlane(c, 63);
+                uint32_t np = nk;
+                if (topp > 0.f && topp < 1.f) {
+                    const uint64_t thr = rl_topp_threshold(topp, wk);
+                    const uint64_t hit = __ballot(valid && (uint64_t)c >= thr);
+                    np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
                 }
-                pos = incl - kept;
+                const uint32_t wp = np ? rl_readlane(c, (int)np - 1) : 0u;
+                const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+                const bool in_p = (uint32_t)lane < np;
+                rl_wave_lds_fence();
+                uint32_t s_le = 0;
+                for (uint32_t j = 0; j < np; j++)
+                    s_le += s_idx[j] <= idx ? s_w[j] : 0u;
+                tok = rl_wave_min_u32(in_p && (uint64_t)s_le > u ? idx : 0xFFFFFFFFu);
+                if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
+                    tok = rl_wave_min_u32(in_p ? idx : 0xFFFFFFFFu);
+                if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
+                    tok = 0;
+            }
+        } else {
+            // ---- rank sort by (x desc, index asc): composite keys are distinct
+            for (uint32_t i = tid; i < nk; i += kMergeThreads) {
+                const uint64_t ck = s_keep[i];
+                uint32_t rank = 0;
+                for (uint32_t j = 0; j < nk; j++)
+                    rank += s_keep[j] > ck ? 1u : 0u;
+                s_sort[rank] = ck;
             }
             __syncthreads();
-#pragma unroll
-            for (int j = 0; j < kRegCand; j++)
-                if (key[j] >= cutoff && key[j] != 0u)
-                    s_sort[pos++] = ((uint64_t)key[j] << 32) | (uint64_t)(0xFFFFFFFFu - idx[j]);
-            __syncthreads();
-            uint64_t mine = (uint32_t)lane < nk ? s_sort[lane] : 0ull;
-            // bitonic sort of 64 lanes, descending by (key, ~index)
-#pragma unroll
-            for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-                for (int stride = size >> 1; stride > 0; stride >>= 1) {
-                    const uint64_t other = __shfl_xor(mine, stride);
-                    const bool lower = (lane & stride) == 0;
-                    const bool desc = (lane & size) == 0;
-                    const uint64_t hi = mine > other ? mine : other;
-                    const uint64_t lo = mine > other ? other : mine;
-                    mine = (lower == desc) ? hi : lo;
-                }
+            for (uint32_t i = tid; i < nk; i += kMergeThreads) {
+                const uint64_t ck = s_sort[i];
+                s_w[i] = rl_sample_weight(rl_key_float((uint32_t)(ck >> 32)) - m);
+                s_idx[i] = 0xFFFFFFFFu - (uint32_t)ck;
             }
-            const bool valid = (uint32_t)lane < nk;
-            const uint32_t my_idx = 0xFFFFFFFFu - (uint32_t)mine;
-            const uint64_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(mine >> 32)) - m) : 0ull;
-            const uint64_t cw = wave_inclusive_scan_u64(w);
-            const uint64_t wk = __shfl(cw, 63);
+            __syncthreads();
+
+            // ---- nucleus prefix over the sorted order -----------------------
+            // thread t owns the contiguous sorted positions [t*per, (t+1)*per)
+            const uint32_t per = (nk + kMergeThreads - 1) / kMergeThreads;
+            const uint32_t i0 = min(nk, tid * per), i1 = min(nk, (tid + 1) * per);
+            uint64_t own = 0;
+            for (uint32_t i = i0; i < i1; i++)
+                own += s_w[i];
+            uint64_t wk;
+            const uint64_t excl = block_excl_scan_u64(own, wk, bs);
             uint32_t np = nk;
             if (topp > 0.f && topp < 1.f) {
                 const uint64_t thr = rl_topp_threshold(topp, wk);
-                const uint64_t hit = __ballot(valid && cw >= thr);
-                np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
-            }
-            const uint64_t wp = np ? __shfl(cw, np - 1) : 0ull;
-            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
-            const bool in_p = (uint32_t)lane < np;
-            uint64_t s_le = 0;
-            for (uint32_t j = 0; j < np; j++) {
-                const uint32_t idx_j = (uint32_t)__shfl((int)my_idx, (int)j);
-                const uint64_t w_j = __shfl(w, (int)j);
-                if (idx_j <= my_idx)
-                    s_le += w_j;
-            }
-            uint32_t tok = wave_min_u32(in_p && s_le > u ? my_idx : 0xFFFFFFFFu);
-            if (tok == 0xFFFFFFFFu)
-                tok = wave_min_u32(in_p ? my_idx : 0xFFFFFFFFu);
-            if (tok >= p.vocab)
-                tok = 0;
-            if (lane == 0) {
-                p.token_out[row] = tok;
-                p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
-            }
-            return;
-        }
-    }
-
-    // ---- exact k_eff-th largest key: 4 passes of 8-bit radix select ----------
-    uint32_t prefix = 0, prefix_mask = 0, need = k_eff;
-    for (int pass = 3; pass >= 0; pass--) {
-        const int shift = pass * 8;
-#pragma unroll
-        for (int b = 0; b < 4; b++)
-            s_hist[lane * 4 + b] = 0;
-        __syncthreads();
-        for (uint32_t i = lane; i < n; i += kMergeThreads) {
-            const uint32_t key = s_cand[i].x;
-            if ((key & prefix_mask) == prefix)
-                atomicAdd(&s_hist[(key >> shift) & 0xFFu], 1u);
-        }
-        __syncthreads();
-        // Lane l owns digits 4l..4l+3; above = count of digits > 4l+3.
-        uint32_t h[4], own = 0;
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            h[b] = s_hist[lane * 4 + b];
-            own += h[b];
-        }
-        uint32_t above = 0;  // suffix sum over lanes > lane
-        {
-            uint32_t v = own;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint32_t o = __shfl_down(v, off);
-                if (lane + off < 64)
-                    v += o;
-            }
-            above = v - own;
-        }
-        int found = -1;
-        uint32_t rem = 0;
-        uint32_t acc = above;
-#pragma unroll
-        for (int b = 3; b >= 0; b--) {
-            if (found < 0 && acc < need && acc + h[b] >= need) {
-                found = lane * 4 + b;
-                rem = need - acc;
-            }
-            acc += h[b];
-        }
-        const uint64_t hit = __ballot(found >= 0);
-        const int src = hit ? (int)__ffsll((long long)hit) - 1 : 0;
-        const uint32_t digit = hit ? (uint32_t)__shfl(found, src) : 0u;
-        need = hit ? __shfl(rem, src) : need;
-        prefix |= digit << shift;
-        prefix_mask |= 0xFFu << shift;
-        __syncthreads();
-    }
-    const uint32_t cutoff = prefix;
-
-    // ---- kept set K = {key >= cutoff}, sorted by (x desc, index asc) ---------
-    if (lane == 0)
-        s_nk = 0;
-    __syncthreads();
-    for (uint32_t i = lane; i < n; i += kMergeThreads) {
-        const uint2 c = s_cand[i];
-        if (c.x >= cutoff) {
-            const uint32_t pos = atomicAdd(&s_nk, 1u);
-            if (pos < kKeptCap)
-                s_sort[pos] = ((uint64_t)c.x << 32) | (uint64_t)(0xFFFFFFFFu - c.y);
-        }
-    }
-    __syncthreads();
-    const uint32_t nk = s_nk;
-    if (nk > (uint32_t)kKeptCap) {
-        const uint32_t tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist);
-        if (lane == 0) {
-            p.token_out[row] = tok;
-            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
-        }
-        return;
-    }
-    uint32_t np2 = 1;
-    while (np2 < nk)
-        np2 <<= 1;
-    for (uint32_t i = nk + lane; i < np2; i += kMergeThreads)
-        s_sort[i] = 0;  // sorts last in descending order
-    __syncthreads();
-    for (uint32_t size = 2; size <= np2; size <<= 1) {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-            for (uint32_t i = lane; i < np2 / 2; i += kMergeThreads) {
-                const uint32_t lo = 2 * i - (i & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const bool desc = (lo & size) == 0;
-                const uint64_t a = s_sort[lo], b = s_sort[hi];
-                if ((a < b) == desc) {
-                    s_sort[lo] = b;
-                    s_sort[hi] = a;
+                // first sorted position whose inclusive prefix reaches thr
+                uint32_t first = 0xFFFFFFFFu;
+                uint64_t c = excl;
+                for (uint32_t i = i0; i < i1; i++) {
+                    c += s_w[i];
+                    if (c >= thr) {
+                        first = i;
+                        break;
+                    }
                 }
+                first = block_min_u32(first, bs);
+                np = (first == 0xFFFFFFFFu) ? nk : first + 1;
             }
-            __syncthreads();
-        }
-    }
+            uint64_t wp_own = 0;
+            for (uint32_t i = i0; i < min(i1, np); i++)
+                wp_own += s_w[i];
+            const uint64_t wp = block_sum_u64(wp_own, bs);
 
-    // ---- integer weights; nucleus prefix over the sorted order ----------------
-    for (uint32_t i = lane; i < nk; i += kMergeThreads)
-        s_w[i] = rl_sample_weight(rl_key_float((uint32_t)(s_sort[i] >> 32)) - m);
-    __syncthreads();
-    // Lane l owns the contiguous sorted positions [l*per, (l+1)*per).
-    const uint32_t per = (nk + kMergeThreads - 1) / kMergeThreads;
-    uint64_t own = 0;
-    for (uint32_t i = lane * per; i < min(nk, (lane + 1) * per); i++)
-        own += s_w[i];
-    const uint64_t incl = wave_inclusive_scan_u64(own);
-    const uint64_t wk = __shfl(incl, 63);
-    uint32_t np = nk;
-    if (topp > 0.f && topp < 1.f) {
-        const uint64_t thr = rl_topp_threshold(topp, wk);
-        // First position whose inclusive prefix reaches thr.
-        uint32_t first = 0xFFFFFFFFu;
-        uint64_t c = incl - own;
-        for (uint32_t i = lane * per; i < min(nk, (lane + 1) * per); i++) {
-            c += s_w[i];
-            if (c >= thr) {
-                first = i;
-                break;
+            // ---- draw; smallest index whose ascending-index prefix weight exceeds u
+            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+            uint32_t cand = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
+            for (uint32_t i = tid; i < np; i += kMergeThreads) {
+                const uint32_t idx_i = s_idx[i];
+                lowest = min(lowest, idx_i);
+                uint64_t s_le = 0;
+                for (uint32_t j = 0; j < np; j++)
+                    s_le += s_idx[j] <= idx_i ? (uint64_t)s_w[j] : 0ull;
+                if (s_le > u)
+                    cand = min(cand, idx_i);
             }
+            tok = block_min_u32(cand, bs);
+            lowest = block_min_u32(lowest, bs);
+            if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
+                tok = lowest;
+            if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
+                tok = 0;
         }
-        first = wave_min_u32(first);
-        np = (first == 0xFFFFFFFFu) ? nk : first + 1;
     }
-    uint64_t wp_own = 0;
-    for (uint32_t i = lane * per; i < min(np, (lane + 1) * per); i++)
-        wp_own += s_w[i];
-    const uint64_t wp = __shfl(wave_inclusive_scan_u64(wp_own), 63);
-
-    // ---- draw; smallest index whose ascending-index prefix weight exceeds u ---
-    const uint64_t r = rl_sample_draw64(row_seed(p, row), p.step, row);
-    const uint64_t u = rl_mulhi_u64(r, wp);
-    uint32_t tok = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
-    for (uint32_t i = lane; i < np; i += kMergeThreads) {
-        const uint32_t idx_i = 0xFFFFFFFFu - (uint32_t)s_sort[i];
-        lowest = min(lowest, idx_i);
-        uint64_t s_le = 0;
-        for (uint32_t j = 0; j < np; j++) {
-            const uint32_t idx_j = 0xFFFFFFFFu - (uint32_t)s_sort[j];
-            if (idx_j <= idx_i)
-                s_le += s_w[j];
-        }
-        if (s_le > u)
-            tok = min(tok, idx_i);
-    }
-    tok = wave_min_u32(tok);
-    lowest = wave_min_u32(lowest);
-    if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
-        tok = lowest;
-    if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
-        tok = 0;
-    if (lane == 0) {
+    if (tid == 0) {
         p.token_out[row] = tok;
         p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
     }

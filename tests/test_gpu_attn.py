@@ -68,6 +68,15 @@ def test_long_rows_in_few_waves(rl, gpu, orc, olib):
         _case(rl, orc, olib, w, grid_waves=waves)
 
 
+def test_row_split_over_hundreds_of_waves(rl, gpu, orc, olib):
+    """One 16,384-token row per kv head shared by 300 / 700 waves: partial
+    counts below and above the merge's 256-entry LDS stage."""
+    ctx = np.array([16384], dtype=np.uint32)
+    w = synth.make_decode(12, 1, 8, 2, 128, 0, 0, dtype="bf16", ctx=ctx)
+    for waves in (300, 700):
+        _case(rl, orc, olib, w, grid_waves=waves)
+
+
 def test_empty_context_gives_zeros(rl, gpu, orc, olib):
     ctx = np.array([0, 40, 0, 1], dtype=np.uint32)
     w = synth.make_decode(8, 4, 8, 2, 128, 0, 0, dtype="bf16", ctx=ctx)
