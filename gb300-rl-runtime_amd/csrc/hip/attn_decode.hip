@@ -37,6 +37,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attn_core.h"
 #include "kv_layout.h"
 #include "rl_dev_common.h"
 #include "rl_hip.h"
@@ -44,413 +45,6 @@
 
 namespace {
 
-constexpr int kTile = 16;  // tokens per tile (the MFMA M/K block)
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef short s16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-struct AttnParams {
-    const uint8_t *arena;
-    uint64_t block_bytes;
-    uint64_t arena_blocks;  // blocks at or past this index are never read
-    const uint32_t *table;
-    uint32_t table_stride;
-    const uint32_t *ctx;
-    uint32_t max_ctx;
-    uint32_t batch;
-    uint32_t q_heads;
-    uint32_t kv_heads;
-    const uint16_t *q;
-    uint16_t *out;
-    float *out_f32;
-    float scale_log2;  // softmax scale * log2(e)
-    uint32_t nwaves;   // waves sharing the tile sequence
-    float *part;       // [nwaves + rows][G * D + 2 * G] partials of split rows
-    uint32_t *cum;     // [batch + 1] tiles of all rows before rollout b
-};
-
-template <int D, int G, int DT, int TPB>
-struct Cfg {
-    static constexpr int W = 4;                   // waves per workgroup
-    static constexpr int RB = 2 * D;              // bytes per K or V row
-    static constexpr int NC = D / 8;              // 16-byte chunks per row
-    static constexpr int PLANE = kTile * RB;      // one tile of K (or V)
-    static constexpr int POPS = PLANE / 1024;     // copies per plane
-    static constexpr int UNIT_OPS = 2 * POPS;     // copies per staged tile
-    static constexpr int STAGE = 2 * PLANE;
-    static constexpr int QBYTES = G * D * 2;
-    static constexpr int QOPS = (QBYTES + 1023) / 1024;
-    static constexpr int QSLOT = QOPS * 1024;
-    static constexpr int WAVE_LDS = 2 * STAGE + 2 * QSLOT;
-    static constexpr int KS = D / 32;             // QK MFMA k-steps
-    static constexpr int NB = D / 16;             // PV MFMA column blocks
-    static constexpr int SUB = TPB / kTile;       // tiles per arena block
-    static constexpr int PART = G * D + 2 * G;    // floats per partial
-    static constexpr int LDS_CU = 160 * 1024;
-    static constexpr int WG_PER_CU_LDS = LDS_CU / (W * WAVE_LDS);
-    static constexpr int WG_PER_CU = WG_PER_CU_LDS > 4 ? 4 : WG_PER_CU_LDS;
-    static_assert(D == 64 || D == 128, "head_dim");
-    static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group");
-    static_assert(PLANE % 1024 == 0, "plane must be whole 1 KiB copies");
-    static_assert(WG_PER_CU >= 1, "LDS budget");
-    static_assert(2 * QSLOT >= 16 * 4, "q slots double as prologue scratch");
-};
-
-// ---- 16-bit element helpers -----------------------------------------------
-
-template <int DT>
-__device__ __forceinline__ uint16_t to16(float f)
-{
-    if constexpr (DT == 0)
-        return __builtin_bit_cast(uint16_t, (__bf16)f);
-    else
-        return __builtin_bit_cast(uint16_t, (_Float16)f);
-}
-
-template <int DT>
-__device__ __forceinline__ float from16(uint16_t h)
-{
-    if constexpr (DT == 0)
-        return __uint_as_float((uint32_t)h << 16);
-    else
-        return (float)__builtin_bit_cast(_Float16, h);
-}
-
-template <int DT>
-__device__ __forceinline__ rl_f32x4 mfma_qk(s16x8 a, s16x8 b, rl_f32x4 c)
-{
-    if constexpr (DT == 0)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
-                                                       c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                      0, 0, 0);
-}
-
-template <int DT>
-__device__ __forceinline__ rl_f32x4 mfma_pv(s16x4 a, s16x4 b, rl_f32x4 c)
-{
-    if constexpr (DT == 0)
-        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
-                                                     0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t tiles_of(const AttnParams &p, uint32_t ctx_in)
-{
-    const uint32_t c = ctx_in > p.max_ctx ? p.max_ctx : ctx_in;
-    return (c + kTile - 1) / kTile;
-}
-
-// What the copy stream put into one stage, read back when it is consumed.
-struct StageMeta {
-    uint32_t b, g, u, nu, ctx;  // row, tile index within the row, tiles of the row, clamped ctx
-    uint32_t qslot;
-    bool first;                 // first tile of its row in this wave (q arrives with it)
-    bool last;                  // last tile of its row in this wave
-    bool bad;                   // ctx beyond max_ctx or a block outside the arena
-};
-
-// Issue side of a wave: walks the wave's tile range and starts the copies.
-template <int D, int G, int DT, int TPB>
-struct Issuer {
-    using C = Cfg<D, G, DT, TPB>;
-    uint32_t b, g, u, nu, ctx;
-    bool ctx_bad;
-    bool first;
-    uint32_t left;     // tiles still to issue
-    uint32_t qcount;   // rows entered so far (q slot parity)
-    uint32_t win0, win1, wrow, wfirst;  // block-table window: entries wfirst .. wfirst + 127 of row wrow
-    uint32_t soff[C::POPS];             // per-lane source offset of each copy within a plane
-
-    __device__ __forceinline__ void init_offsets(int lane)
-    {
-#pragma unroll
-        for (int i = 0; i < C::POPS; i++) {
-            const uint32_t byte = (uint32_t)i * 1024u + (uint32_t)lane * 16u;
-            const uint32_t t = byte / C::RB;
-            const uint32_t pos = (byte % C::RB) / 16u;
-            soff[i] = t * C::RB + ((pos ^ (t & (C::NC - 1))) * 16u);
-        }
-    }
-
-    __device__ __forceinline__ void set_rollout(const AttnParams &p, uint32_t nb)
-    {
-        b = nb;
-        const uint32_t cin = rl_sload(p.ctx + nb);
-        ctx_bad = cin > p.max_ctx;
-        ctx = ctx_bad ? p.max_ctx : cin;
-        nu = (ctx + kTile - 1) / kTile;
-    }
-
-    __device__ __forceinline__ void issue(const AttnParams &p, RL_LDS uint8_t *st, RL_LDS uint8_t *qslots,
-                                          StageMeta &m, int lane)
-    {
-        const uint32_t row = b * p.kv_heads + g;
-        const uint32_t lb = u / C::SUB;
-        if (row != wrow || lb < wfirst || lb >= wfirst + 128u) {
-            // New row or past the window: reload 128 table entries. The wait
-            // drains the copies in flight, once per row change.
-            const uint32_t nblk = (ctx + TPB - 1) / TPB;
-            const uint32_t *trow = p.table + (size_t)row * p.table_stride;
-            win0 = (lb + (uint32_t)lane < nblk) ? trow[lb + lane] : 0u;
-            win1 = (lb + 64u + (uint32_t)lane < nblk) ? trow[lb + 64u + lane] : 0u;
-            rl_wait_vmcnt<0>();
-            wrow = row;
-            wfirst = lb;
-        }
-        const uint32_t j = lb - wfirst;
-        uint32_t blk = (uint32_t)__builtin_amdgcn_readlane((int)(j < 64u ? win0 : win1), (int)(j & 63u));
-        m.bad = ctx_bad;
-        if (blk >= p.arena_blocks) {
-            // Never read outside the arena; copy block 0 instead so the number
-            // of copies per tile stays fixed, and poison the row.
-            m.bad = true;
-            blk = 0;
-        }
-        m.b = b;
-        m.g = g;
-        m.u = u;
-        m.nu = nu;
-        m.ctx = ctx;
-        m.first = first;
-        if (first) {
-            m.qslot = qcount & 1u;
-            qcount++;
-            const uint8_t *qsrc = (const uint8_t *)(p.q + ((size_t)b * p.q_heads + (size_t)g * G) * D);
-#pragma unroll
-            for (int i = 0; i < C::QOPS; i++) {
-                uint32_t off = (uint32_t)i * 1024u + (uint32_t)lane * 16u;
-                off = off < (uint32_t)C::QBYTES ? off : (uint32_t)C::QBYTES - 16u;
-                rl_g2lds_16_off(qsrc, off, qslots + m.qslot * C::QSLOT + i * 1024);
-            }
-        }
-        const uint8_t *kp = p.arena + (uint64_t)blk * p.block_bytes + (u % C::SUB) * C::PLANE;
-        const uint8_t *vp = kp + TPB * C::RB;
-#pragma unroll
-        for (int i = 0; i < C::POPS; i++) {
-            rl_g2lds_16_off(kp, soff[i], st + i * 1024);
-            rl_g2lds_16_off(vp, soff[i], st + C::PLANE + i * 1024);
-        }
-        // advance
-        left--;
-        u++;
-        first = false;
-        m.last = (u == nu) || (left == 0);
-        if (u == nu && left != 0) {
-            u = 0;
-            first = true;
-            if (++g == p.kv_heads) {
-                g = 0;
-                // tiles remain, so a later rollout has some (bounded anyway)
-                uint32_t nb = b;
-                do {
-                    set_rollout(p, ++nb);
-                } while (nu == 0 && nb + 1 < p.batch);
-            }
-        }
-    }
-};
-
-// Consume side: running softmax state of the current row and its output.
-template <int D, int G, int DT, int TPB>
-struct RowState {
-    using C = Cfg<D, G, DT, TPB>;
-    s16x8 qf[C::KS];          // B operand of QK: q[head lane%16][32 s + 8 (lane/16) .. + 7]
-    rl_f32x4 acc[C::NB];      // O[head 4 (lane/16) + r][16 n + lane % 16]
-    float m_run;              // running max (log2 domain) of head lane % 16
-    float l_run;              // this lane's share of the running sum
-    bool from0;               // the row started at tile 0 in this wave
-    bool bad;
-};
-
-template <int D, int G, int DT, int TPB>
-__device__ __forceinline__ void row_begin(RowState<D, G, DT, TPB> &rs, RL_LDS const uint8_t *qslot,
-                                          const StageMeta &m, int lane)
-{
-    using C = Cfg<D, G, DT, TPB>;
-    const int h = lane & 15;
-    const int hs = h < G ? h : G - 1;
-#pragma unroll
-    for (int s = 0; s < C::KS; s++) {
-        s16x8 v = *(RL_LDS const s16x8 *)(qslot + hs * C::RB + (32 * s + 8 * (lane >> 4)) * 2);
-        if (h >= G)
-            v = s16x8{0, 0, 0, 0, 0, 0, 0, 0};
-        rs.qf[s] = v;
-    }
-#pragma unroll
-    for (int n = 0; n < C::NB; n++)
-        rs.acc[n] = rl_f32x4{0.f, 0.f, 0.f, 0.f};
-    rs.m_run = -INFINITY;
-    rs.l_run = 0.f;
-    rs.from0 = m.u == 0;
-    rs.bad = false;
-}
-
-// One staged tile: QK (MFMA), online softmax, PV (MFMA).
-template <int D, int G, int DT, int TPB, bool FULL>
-__device__ __forceinline__ void consume_tile(const AttnParams &p, RowState<D, G, DT, TPB> &rs,
-                                             RL_LDS const uint8_t *st, const StageMeta &m, int lane)
-{
-    using C = Cfg<D, G, DT, TPB>;
-    const int h = lane & 15;   // head (QK output column / PV A row)
-    const int tg = lane >> 4;  // token group: tokens 4 tg .. 4 tg + 3
-
-    // ---- S^T = K q^T ---------------------------------------------------------
-    rl_f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-    {
-        const int t = lane & 15;
-#pragma unroll
-        for (int s = 0; s < C::KS; s++) {
-            const int c = 4 * s + tg;
-            const s16x8 kf = *(RL_LDS const s16x8 *)(st + t * C::RB + ((c ^ (t & (C::NC - 1))) << 4));
-            sc = mfma_qk<DT>(kf, rs.qf[s], sc);
-        }
-    }
-
-    // ---- online softmax ------------------------------------------------------
-    const uint32_t tok0 = m.u * kTile + 4 * tg;
-    float sv[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const bool ok = (h < G) && (FULL || tok0 + r < m.ctx);
-        sv[r] = ok ? sc[r] * p.scale_log2 : -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(rs.m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const bool grow = (m_new > rs.m_run) && (rs.m_run != -INFINITY);
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float alpha = grow ? exp2f(rs.m_run - m_use) : 1.f;
-        rs.l_run *= alpha;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float a = __shfl(alpha, 4 * tg + r);
-#pragma unroll
-            for (int n = 0; n < C::NB; n++)
-                rs.acc[n][r] *= a;
-        }
-    }
-    rs.m_run = m_new;
-    float pr[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-        pr[r] = exp2f(sv[r] - m_use);
-    rs.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-
-    // ---- P split into high and low 16-bit parts --------------------------------
-    s16x4 phi, plo;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint16_t hi = to16<DT>(pr[r]);
-        const uint16_t lo = to16<DT>(pr[r] - from16<DT>(hi));
-        phi[r] = (short)hi;
-        plo[r] = (short)lo;
-    }
-
-    // ---- O += P V --------------------------------------------------------------
-    uint32_t vm0 = 0xFFFFFFFFu, vm1 = 0xFFFFFFFFu;
-    if constexpr (!FULL) {
-        // element r of the transposed operand is token 4 tg + r
-        vm0 = (tok0 + 0 < m.ctx ? 0x0000FFFFu : 0u) | (tok0 + 1 < m.ctx ? 0xFFFF0000u : 0u);
-        vm1 = (tok0 + 2 < m.ctx ? 0x0000FFFFu : 0u) | (tok0 + 3 < m.ctx ? 0xFFFF0000u : 0u);
-    }
-    {
-        const int L = lane & 15;
-        const int t = 4 * tg + (L >> 2);
-        const int sw = t & (C::NC - 1);
-        RL_LDS const uint8_t *vrow = st + C::PLANE + t * C::RB + 8 * (L & 1);
-#pragma unroll
-        for (int n = 0; n < C::NB; n++) {
-            const int c = 2 * n + ((L & 3) >> 1);
-            s16x4 vb = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (RL_LDS s16x4 *)(vrow + ((c ^ sw) << 4)));
-            if constexpr (!FULL) {
-                // stale slots past ctx may hold anything, NaN included: zero them
-                uint32_t w0 = __builtin_bit_cast(uint32_t, __builtin_shufflevector(vb, vb, 0, 1)) & vm0;
-                uint32_t w1 = __builtin_bit_cast(uint32_t, __builtin_shufflevector(vb, vb, 2, 3)) & vm1;
-                typedef short s16x2 __attribute__((ext_vector_type(2)));
-                const s16x2 a = __builtin_bit_cast(s16x2, w0);
-                const s16x2 b2 = __builtin_bit_cast(s16x2, w1);
-                vb = s16x4{a[0], a[1], b2[0], b2[1]};
-            }
-            rs.acc[n] = mfma_pv<DT>(phi, vb, rs.acc[n]);
-            rs.acc[n] = mfma_pv<DT>(plo, vb, rs.acc[n]);
-        }
-    }
-}
-
-// Row done in this wave: direct output, or an fp32 partial for the merge.
-template <int D, int G, int DT, int TPB>
-__device__ __forceinline__ void row_end(const AttnParams &p, RowState<D, G, DT, TPB> &rs, const StageMeta &m,
-                                        uint32_t wave_id, int lane)
-{
-    using C = Cfg<D, G, DT, TPB>;
-    const int h = lane & 15;
-    const int tg = lane >> 4;
-    float lt = rs.l_run + __shfl_xor(rs.l_run, 16);
-    lt += __shfl_xor(lt, 32);
-    const bool poison = rs.bad || m.bad;
-    const uint32_t row = m.b * p.kv_heads + m.g;
-    if (rs.from0 && m.u + 1 == m.nu) {
-        const size_t obase = ((size_t)m.b * p.q_heads + (size_t)m.g * G) * D;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float L = __shfl(lt, 4 * tg + r);
-            const int hh = 4 * tg + r;
-            if (hh < G) {
-#pragma unroll
-                for (int n = 0; n < C::NB; n++) {
-                    float v = L > 0.f ? rs.acc[n][r] / L : 0.f;
-                    if (poison)
-                        v = __builtin_nanf("");
-                    const size_t o = obase + (size_t)hh * D + 16 * n + h;
-                    p.out[o] = rl_from_f32<DT>(v);
-                    if (p.out_f32)
-                        p.out_f32[o] = v;
-                }
-            }
-        }
-    } else {
-        float *part = p.part + (size_t)(wave_id + row) * C::PART;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int hh = 4 * tg + r;
-            if (hh < G) {
-#pragma unroll
-                for (int n = 0; n < C::NB; n++)
-                    part[hh * D + 16 * n + h] = rs.acc[n][r];
-            }
-        }
-        if (lane < G) {
-            part[G * D + 2 * lane + 0] = rs.m_run;
-            part[G * D + 2 * lane + 1] = poison ? __builtin_nanf("") : lt;
-        }
-    }
-}
-
-template <int D, int G, int DT, int TPB>
-__device__ __forceinline__ void consume(const AttnParams &p, RowState<D, G, DT, TPB> &rs, RL_LDS const uint8_t *st,
-                                        RL_LDS const uint8_t *qslots, const StageMeta &m, uint32_t wave_id, int lane)
-{
-    using C = Cfg<D, G, DT, TPB>;
-    if (m.first)
-        row_begin<D, G, DT, TPB>(rs, qslots + m.qslot * C::QSLOT, m, lane);
-    rs.bad |= m.bad;
-    if (m.u * kTile + kTile <= m.ctx)
-        consume_tile<D, G, DT, TPB, true>(p, rs, st, m, lane);
-    else
-        consume_tile<D, G, DT, TPB, false>(p, rs, st, m, lane);
-    if (m.last)
-        row_end<D, G, DT, TPB>(p, rs, m, wave_id, lane);
-}
 
 template <int D, int G, int DT, int TPB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
@@ -544,204 +138,30 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
     RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_st0 + wave * C::STAGE;
     RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_st1 + wave * C::STAGE;
     RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * 2 * C::QSLOT;
-
-    Issuer<D, G, DT, TPB> is;
-    is.init_offsets(lane);
-    is.set_rollout(p, rb);
-    {
-        const uint32_t rem = s_begin - rcum;
-        is.g = rem / is.nu;
-        is.u = rem % is.nu;
-    }
-    is.left = s_end - s_begin;
-    is.first = true;
-    is.qcount = 0;
-    is.wrow = 0xFFFFFFFFu;
-    is.wfirst = 0;
-    is.win0 = is.win1 = 0;
-
-    RowState<D, G, DT, TPB> rs;
-    StageMeta mc, mn;  // tile to consume next, tile in flight behind it
-    RL_LDS uint8_t *stc = st0;
-    RL_LDS uint8_t *stn = st1;
-    bool has_next = false;
-    is.issue(p, stc, qs, mc, lane);
-    if (is.left) {
-        is.issue(p, stn, qs, mn, lane);
-        has_next = true;
-    }
-    for (;;) {
-        // Copies complete in issue order: once at most one tile's worth is
-        // outstanding, everything older - this tile and its q - has landed.
-        // (A tile that brings a q slot issues one more copy: the wait is then
-        // slightly stronger than needed, never weaker.)
-        if (has_next)
-            rl_wait_vmcnt<C::UNIT_OPS>();
-        else
-            rl_wait_vmcnt<0>();
-        consume<D, G, DT, TPB>(p, rs, stc, qs, mc, wave_id, lane);
-        if (!has_next)
-            break;
-        // the stage just consumed takes the tile after next
-        StageMeta mi;
-        bool has_after = false;
-        if (is.left) {
-            rl_wait_lgkmcnt0();
-            is.issue(p, stc, qs, mi, lane);
-            has_after = true;
-        }
-        RL_LDS uint8_t *t = stc;
-        stc = stn;
-        stn = t;
-        mc = mn;
-        mn = mi;
-        has_next = has_after;
-    }
+    attn_stream<D, G, DT, TPB>(p, CtxFromArray{p.ctx}, wave_id, s_begin, s_end, rb, rcum, st0, st1, qs, lane);
 }
 
-// Combines the partials of every row split across waves:
-// M = max_w m_w, L = sum_w l_w 2^(m_w - M), O = sum_w o_w 2^(m_w - M), out = O / L.
-// Also writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN).
-// The (max, sum) pairs of up to kMergeLds partials are loaded in parallel into
-// LDS, the per-head scale factors computed once, and every output element then
-// sums its partials with independent loads.
-constexpr int kMergeLds = 256;
-
+// Combines the partials of every row split across waves (merge_row) and
+// writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN).
 template <int D, int G, int DT>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
 {
-    constexpr int PART = G * D + 2 * G;
-    __shared__ float s_f[kMergeLds * G];  // m, then the scale 2^(m - M)
+    __shared__ float s_f[kMergeLds * G];
     __shared__ float s_l[kMergeLds * G];
     __shared__ float s_L[G];
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
-    const uint32_t row = b * p.kv_heads + g;
     const uint32_t cin = rl_sload(p.ctx + b);
     const bool bad = cin > p.max_ctx;
     const uint32_t nu = tiles_of(p, cin);
-    const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
     if (nu == 0) {
-        for (int e = threadIdx.x; e < G * D; e += 256) {
-            const float v = bad ? __builtin_nanf("") : 0.f;
-            p.out[obase + e] = rl_from_f32<DT>(v);
-            if (p.out_f32)
-                p.out_f32[obase + e] = v;
-        }
+        empty_row<D, G, DT>(p, b, g, bad, threadIdx.x, 256);
         return;
     }
     const uint32_t U = rl_sload(p.cum + p.batch);  // > 0: this row has tiles
     const uint32_t NW = min(p.nwaves, U);
     const uint32_t R0 = rl_sload(p.cum + b) + g * nu;
-    const uint32_t R1 = R0 + nu;
-    // wave holding tile R0 / tile R1 - 1: the largest w with floor(w U / NW) <= tile
-    const uint32_t wf = (uint32_t)((((uint64_t)R0 + 1) * NW - 1) / U);
-    const uint32_t wl = (uint32_t)(((uint64_t)R1 * NW - 1) / U);
-    if (wf == wl)
-        return;  // one wave covered the row and wrote it
-    const float *part = p.part + (size_t)(wf + row) * PART;
-    const uint32_t np = wl - wf + 1;
-    constexpr int EPT = (G * D + 255) / 256;  // output elements per thread
-    constexpr int NPR = 8;                    // partials merged from registers
-    if (np <= (uint32_t)NPR) {
-        // few partials: every load is issued before the first use
-        float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
-#pragma unroll
-        for (int i = 0; i < NPR; i++)
-#pragma unroll
-            for (int k = 0; k < EPT; k++) {
-                const int e = threadIdx.x + 256 * k;
-                const bool ok = (uint32_t)i < np && e < G * D;
-                const float *pp = part + (size_t)(ok ? i : 0) * PART;
-                const int h = (e < G * D ? e : 0) / D;
-                o[i][k] = ok ? pp[e] : 0.f;
-                mm[i][k] = ok ? pp[G * D + 2 * h] : -INFINITY;
-                ll[i][k] = ok ? pp[G * D + 2 * h + 1] : 0.f;
-            }
-#pragma unroll
-        for (int k = 0; k < EPT; k++) {
-            const int e = threadIdx.x + 256 * k;
-            if (e >= G * D)
-                break;
-            float M = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < NPR; i++)
-                M = fmaxf(M, mm[i][k]);
-            float L = 0.f, O = 0.f;
-#pragma unroll
-            for (int i = 0; i < NPR; i++) {
-                const float f = mm[i][k] == -INFINITY ? 0.f : exp2f(mm[i][k] - M);
-                L = fmaf(ll[i][k], f, L);
-                O = fmaf(o[i][k], f, O);
-            }
-            float v = (L > 0.f || L != L) ? O / L : 0.f;
-            if (bad)
-                v = __builtin_nanf("");
-            p.out[obase + e] = rl_from_f32<DT>(v);
-            if (p.out_f32)
-                p.out_f32[obase + e] = v;
-        }
-        return;
-    }
-    if (np <= (uint32_t)kMergeLds) {
-        for (uint32_t t = threadIdx.x; t < np * G; t += 256) {
-            const uint32_t i = t / G, h = t % G;
-            s_f[t] = part[(size_t)i * PART + G * D + 2 * h];
-            s_l[t] = part[(size_t)i * PART + G * D + 2 * h + 1];
-        }
-        __syncthreads();
-        if (threadIdx.x < G) {
-            const int h = threadIdx.x;
-            float M = -INFINITY;
-            for (uint32_t i = 0; i < np; i++)
-                M = fmaxf(M, s_f[i * G + h]);
-            float L = 0.f;
-            for (uint32_t i = 0; i < np; i++) {
-                const float mi = s_f[i * G + h];
-                const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
-                s_f[i * G + h] = f;
-                L = fmaf(s_l[i * G + h], f, L);
-            }
-            s_L[h] = L;
-        }
-        __syncthreads();
-        for (int e = threadIdx.x; e < G * D; e += 256) {
-            const int h = e / D;
-            float O = 0.f;
-#pragma unroll 8
-            for (uint32_t i = 0; i < np; i++)
-                O = fmaf(part[(size_t)i * PART + e], s_f[i * G + h], O);
-            const float L = s_L[h];
-            float v = (L > 0.f || L != L) ? O / L : 0.f;
-            if (bad)
-                v = __builtin_nanf("");
-            p.out[obase + e] = rl_from_f32<DT>(v);
-            if (p.out_f32)
-                p.out_f32[obase + e] = v;
-        }
-        return;
-    }
-    // very long rows: stream the partials per element
-    for (int e = threadIdx.x; e < G * D; e += 256) {
-        const int h = e / D;
-        float M = -INFINITY;
-        for (uint32_t i = 0; i < np; i++)
-            M = fmaxf(M, part[(size_t)i * PART + G * D + 2 * h]);
-        float L = 0.f, O = 0.f;
-        for (uint32_t i = 0; i < np; i++) {
-            const float *pp = part + (size_t)i * PART;
-            const float mi = pp[G * D + 2 * h];
-            const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
-            L = fmaf(pp[G * D + 2 * h + 1], f, L);
-            O = fmaf(pp[e], f, O);
-        }
-        float v = (L > 0.f || L != L) ? O / L : 0.f;
-        if (bad)
-            v = __builtin_nanf("");
-        p.out[obase + e] = rl_from_f32<DT>(v);
-        if (p.out_f32)
-            p.out_f32[obase + e] = v;
-    }
+    merge_row<D, G, DT>(p, b, g, R0, nu, U, NW, bad, threadIdx.x, 256, s_f, s_l, s_L);
 }
 
 }  // namespace

@@ -148,6 +148,17 @@ class AppendArgs(C.Structure):
                 ("k_new", C.c_void_p), ("v_new", C.c_void_p)]
 
 
+class HwWorkerArgs(C.Structure):
+    _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
+                ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
+                ("layout", KvLayoutDesc), ("block_table", C.c_void_p), ("table_stride", C.c_uint32),
+                ("rollouts", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
+                ("dtype", C.c_uint32), ("scale", C.c_float), ("max_steps", C.c_uint32), ("q", C.c_void_p),
+                ("k_new", C.c_void_p), ("v_new", C.c_void_p), ("logits", C.c_void_p), ("vocab", C.c_uint32),
+                ("attn_out", C.c_void_p), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
+                ("stats", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+
+
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 
@@ -173,6 +184,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample_workspace": (sz, [C.POINTER(SampleArgs)]),
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
+        "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
+        "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
         # reference host API
         "hw_ring_create": (vp, []), "hw_ring_reset": (None, [vp]), "hw_ring_destroy": (None, [vp]),
         "hw_ring_load_acquire": (u32, [vp]), "hw_ring_store_release": (None, [vp, u32]),
@@ -355,3 +368,48 @@ def sample(args: SampleArgs) -> None:
 
 def kv_append(args: AppendArgs) -> None:
     check(lib().rl_hip_kv_append(C.byref(args)), "rl_hip_kv_append")
+
+
+# ---------------------------------------------------------------- hw_desc rings
+HW_RING_SIZE = 1 << 16
+
+
+def hw_ring_push(ring: int, d: HwDesc) -> int:
+    """Producer side of hw_ring.h's push on a ring at address `ring`."""
+    L = lib()
+    tail = L.hw_ring_load_acquire(ring + 64)
+    head = L.hw_ring_load_acquire(ring)
+    if (tail - head) & 0xFFFFFFFF >= HW_RING_SIZE:
+        return -1
+    C.memmove(ring + 128 + (tail & (HW_RING_SIZE - 1)) * 64, C.byref(d), 64)
+    L.hw_ring_store_release(ring + 64, (tail + 1) & 0xFFFFFFFF)
+    return 0
+
+
+def hw_ring_pop(ring: int) -> HwDesc | None:
+    """Consumer side of hw_ring.h's pop; None when empty."""
+    L = lib()
+    head = L.hw_ring_load_acquire(ring)
+    if head == L.hw_ring_load_acquire(ring + 64):
+        return None
+    d = HwDesc.from_buffer_copy((C.c_char * 64).from_address(ring + 128 + (head & (HW_RING_SIZE - 1)) * 64))
+    L.hw_ring_store_release(ring, (head + 1) & 0xFFFFFFFF)
+    return d
+
+
+def hw_ring_indices(ring: int) -> tuple[int, int]:
+    L = lib()
+    return L.hw_ring_load_acquire(ring), L.hw_ring_load_acquire(ring + 64)
+
+
+def hw_worker_workspace(args: HwWorkerArgs) -> DeviceBuffer:
+    n = lib().rl_hip_hw_worker_workspace(C.byref(args))
+    if n == 0:
+        raise RlrtError(f"rl_hip_hw_worker_workspace: {_err()}")
+    ws = DeviceBuffer(n)
+    args.workspace, args.workspace_bytes = ws.ptr, n
+    return ws
+
+
+def hw_worker_launch(args: HwWorkerArgs) -> None:
+    check(lib().rl_hip_hw_worker_launch(C.byref(args)), "rl_hip_hw_worker_launch")

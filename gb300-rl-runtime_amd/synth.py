@@ -96,15 +96,18 @@ def _fill_normal(rng: np.random.Generator, n: int, std: float, dtype: str, out: 
 
 def make_decode(seed: int, batch: int, q_heads: int, kv_heads: int, head_dim: int, ctx_lo: int, ctx_hi: int,
                 dtype: str = "bf16", kv_std: float = 1.0, token_count: int = 16, max_ctx: int | None = None,
-                ctx: np.ndarray | None = None, spare_blocks: int = 0) -> DecodeWorkload:
-    """Ragged contexts uniform in [ctx_lo, ctx_hi] (or given), permuted blocks."""
+                ctx: np.ndarray | None = None, spare_blocks: int = 0,
+                reserve_tokens: int = 0) -> DecodeWorkload:
+    """Ragged contexts uniform in [ctx_lo, ctx_hi] (or given), permuted blocks;
+    every row owns blocks for max(ctx + 1, reserve_tokens) tokens."""
     rng = np.random.default_rng(seed)
     if ctx is None:
         ctx = rng.integers(ctx_lo, ctx_hi + 1, size=batch, dtype=np.int64)
     ctx = np.asarray(ctx, dtype=np.uint32)
     cap = int(max_ctx if max_ctx is not None else (ctx.max() if batch else 0))
+    cap = max(cap, reserve_tokens - 1)
     stride = max(1, -(-(cap + 1) // token_count))
-    nblk = -(-(ctx.astype(np.int64) + 1) // token_count)          # blocks per (b, g) incl. append slot
+    nblk = -(-np.maximum(ctx.astype(np.int64) + 1, reserve_tokens) // token_count)  # blocks per (b, g)
     total = int(nblk.sum()) * kv_heads + spare_blocks
     perm = rng.permutation(total).astype(np.uint32)
     table = np.zeros((batch, kv_heads, stride), dtype=np.uint32)

@@ -107,6 +107,59 @@ typedef struct {
 size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *args);
 int rl_hip_attn_decode(const rl_attn_decode_args_t *args);
 
+/* ---- persistent worker on the hw_desc rings ---------------------------------
+ * Replaces hw_worker_sim_run (src/hw_worker_sim.c:23-59, include/
+ * hw_worker_sim.h:6-14) and the device worker decode_worker
+ * (cu/worker.cu:66-131). One persistent workgroup per ring pair: the single
+ * consumer of cmdq[g] and producer of doneq[g] (rings from hw_ring_create()
+ * with a device open, i.e. fine-grained coherent host memory; the two pointer
+ * arrays themselves device-readable). Each DECODE descriptor gets the control
+ * rule of hw_worker_sim (seq_len++ up to max_tokens, DONE / NEEDS_REWARD) with
+ * one real decode step per token: attention of rollout `rollout_id` over its
+ * seq_len cached tokens (block_table rows rollout * kv_heads + h), the greedy
+ * token and logprob of the step's logits, and the append of the step's K/V
+ * token at position seq_len. Group g's k-th step reads q/k_new/v_new/logits
+ * row g * max_steps + k and writes attn_out / token_out / logprob_out there.
+ * STOP ends the worker without a completion; other opcodes are dropped.
+ * The launch returns at once; rl_hip_sync() waits until every worker exited:
+ * on STOP, when *stop becomes nonzero, or after max_idle_polls consecutive
+ * empty polls (a full completion ring likewise). stats[g] = {decoded tokens,
+ * completions, steps, status}; status 0 stopped, 1 idle limit, 2 inputs
+ * exhausted or rollout id >= rollouts, 3 completion ring full, 4 appended
+ * token outside the block table or arena. */
+typedef struct {
+    hw_ring_t *const *cmdq;      /* device-readable [groups] */
+    hw_ring_t *const *doneq;     /* device-readable [groups] */
+    uint32_t groups;             /* <= compute units */
+    const volatile uint32_t *stop; /* coherent host memory */
+    uint64_t max_idle_polls;     /* 0 selects 2^22 */
+    void *arena_base;            /* device: KVArena.base (appended tokens are written) */
+    uint64_t arena_bytes;
+    KvLayoutDesc layout;
+    const uint32_t *block_table; /* device [rollouts * kv_heads][table_stride] */
+    uint32_t table_stride;
+    uint32_t rollouts;
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t dtype;              /* RL_DTYPE_* of q, K, V */
+    float scale;                 /* 0 selects 1/sqrt(head_dim) */
+    uint32_t max_steps;          /* decode steps per group the inputs hold */
+    const void *q;               /* device [groups][max_steps][q_heads][head_dim] */
+    const void *k_new;           /* device [groups][max_steps][kv_heads][head_dim] */
+    const void *v_new;
+    const float *logits;         /* device [groups][max_steps][vocab] */
+    uint32_t vocab;
+    float *attn_out;             /* device [groups][max_steps][q_heads][head_dim] */
+    uint32_t *token_out;         /* device [groups][max_steps] */
+    float *logprob_out;          /* device [groups][max_steps] */
+    uint64_t *stats;             /* device or coherent [groups][4] */
+    void *workspace;             /* device, >= rl_hip_hw_worker_workspace() */
+    size_t workspace_bytes;
+} rl_hw_worker_args_t;
+
+size_t rl_hip_hw_worker_workspace(const rl_hw_worker_args_t *args);
+int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
+
 /* ---- sampling -------------------------------------------------------------
  * Replaces sample_token (cu/sample.cu:41-123) with the specification in
  * sample.h: greedy, or temperature / top-k (k <= 256) / top-p with a
