@@ -502,17 +502,18 @@ __device__ __forceinline__ void attn_stream(const AttnParams &p, const CtxFn &cf
 // Log-sum-exp merge of one split row (rollout b, kv head g) whose tiles are
 // [R0, R0 + nu) of a sequence of U tiles shared by NW waves, the partials of
 // waves wf..wl at p.part[(w + row)]: M = max_w m_w, L = sum_w l_w 2^(m_w - M),
-// O = sum_w o_w 2^(m_w - M), out = O / L. Threads tid, tid + nthr, ... of the
+// O = sum_w o_w 2^(m_w - M), out = O / L. Threads tid, tid + NTHR, ... of the
 // caller take the output elements; s_f / s_l hold kMergeLds * G floats and
 // s_L G floats of LDS. Returns without writing when one wave covered the row.
 constexpr int kMergeLds = 256;
 
-template <int D, int G, int DT>
+template <int D, int G, int DT, int NTHR>
 __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t R0, uint32_t nu,
-                                          uint32_t U, uint32_t NW, bool bad, uint32_t tid, uint32_t nthr,
-                                          float *s_f, float *s_l, float *s_L)
+                                          uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f, float *s_l,
+                                          float *s_L)
 {
     constexpr int PART = G * D + 2 * G;
+    constexpr uint32_t nthr = NTHR;
     const uint32_t row = b * p.kv_heads + g;
     const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
     const uint32_t R1 = R0 + nu;
@@ -532,30 +533,38 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
         if (p.out_f32)
             p.out_f32[obase + e] = v;
     };
-    constexpr int NPR = 8;  // partials merged from registers
+    constexpr int NPR = 8;                              // partials merged from registers
+    constexpr int EPT = (G * D + NTHR - 1) / NTHR;      // output elements per thread
     if (np <= (uint32_t)NPR) {
         // few partials: every load is issued before the first use
-        for (uint32_t e = tid; e < (uint32_t)(G * D); e += nthr) {
-            const int h = e / D;
-            float o[NPR], mm[NPR], ll[NPR];
+        float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
 #pragma unroll
-            for (int i = 0; i < NPR; i++) {
-                const bool ok = (uint32_t)i < np;
+        for (int i = 0; i < NPR; i++)
+#pragma unroll
+            for (int k = 0; k < EPT; k++) {
+                const uint32_t e = tid + nthr * k;
+                const bool ok = (uint32_t)i < np && e < (uint32_t)(G * D);
                 const float *pp = part + (size_t)(ok ? i : 0) * PART;
-                o[i] = ok ? pp[e] : 0.f;
-                mm[i] = ok ? pp[G * D + 2 * h] : -INFINITY;
-                ll[i] = ok ? pp[G * D + 2 * h + 1] : 0.f;
+                const int h = (ok ? e : 0) / D;
+                o[i][k] = ok ? pp[e] : 0.f;
+                mm[i][k] = ok ? pp[G * D + 2 * h] : -INFINITY;
+                ll[i][k] = ok ? pp[G * D + 2 * h + 1] : 0.f;
             }
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const uint32_t e = tid + nthr * k;
+            if (e >= (uint32_t)(G * D))
+                break;
             float M = -INFINITY;
 #pragma unroll
             for (int i = 0; i < NPR; i++)
-                M = fmaxf(M, mm[i]);
+                M = fmaxf(M, mm[i][k]);
             float L = 0.f, O = 0.f;
 #pragma unroll
             for (int i = 0; i < NPR; i++) {
-                const float f = mm[i] == -INFINITY ? 0.f : exp2f(mm[i] - M);
-                L = fmaf(ll[i], f, L);
-                O = fmaf(o[i], f, O);
+                const float f = mm[i][k] == -INFINITY ? 0.f : exp2f(mm[i][k] - M);
+                L = fmaf(ll[i][k], f, L);
+                O = fmaf(o[i][k], f, O);
             }
             store(e, O, L);
         }

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
     const uint32_t U = rl_sload(p.cum + p.batch);  // > 0: this row has tiles
     const uint32_t NW = min(p.nwaves, U);
     const uint32_t R0 = rl_sload(p.cum + b) + g * nu;
-    merge_row<D, G, DT>(p, b, g, R0, nu, U, NW, bad, threadIdx.x, 256, s_f, s_l, s_L);
+    merge_row<D, G, DT, 256>(p, b, g, R0, nu, U, NW, bad, threadIdx.x, s_f, s_l, s_L);
 }
 
 }  // namespace

@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                 }
                 __syncthreads();
                 for (uint32_t g = 0; g < kvh; g++)
-                    merge_row<D, G, DT>(a, 0, g, g * nu, nu, U, NW, false, tid, kWorkerThreads, s_f, s_l, s_L);
+                    merge_row<D, G, DT, kWorkerThreads>(a, 0, g, g * nu, nu, U, NW, false, tid, s_f, s_l, s_L);
             }
 
             // greedy token (lowest index among maxima) and its logprob
