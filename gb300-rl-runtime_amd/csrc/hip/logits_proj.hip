@@ -1,0 +1,186 @@
+// logits_proj.hip - the dense hidden-to-vocab logits projection on gfx950:
+// logits[M][N] (fp32) = X[M][K] (bf16) . W[N][K]^T (bf16), fp32 accumulate.
+//
+// No reference kernel exists; the nearest analog is the
+// fp16 GEMV query_prepare_kernel (cu/query_producer.cu:5-26). W is stored
+// like an lm_head weight, one row of K per vocabulary entry, so both
+// operands are K-contiguous.
+//
+//  tiles   128 x 128 output tile per 256-thread workgroup, K in steps of 64;
+//          the four waves each own 64 x 64 (4 x 4 MFMA blocks of 16 x 16).
+//          Workgroups are ordered M-fastest, so the M tiles sharing a W tile
+//          run together and W streams from HBM about once.
+//  staging the X and W tiles of a K step (16 KiB each) are copied HBM -> LDS
+//          with global_load_lds_dwordx4, double-buffered; 16-byte chunk c of
+//          row r lands at chunk position c ^ (r & 7) (lanes fetch permuted
+//          sources), so the MFMA operand reads are free of bank conflicts.
+//  MFMA    v_mfma_f32_16x16x32_bf16: lane l reads 16 B of row l % 16 at
+//          k-chunk 4 s + l / 16 for both operands; 32 MFMAs per wave and K step.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rl_dev_common.h"
+#include "rl_hip.h"
+#include "rl_hip_internal.h"
+
+namespace {
+
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int TILE_BYTES = BM * BK * 2;   // 16 KiB per operand tile
+constexpr int OPS = TILE_BYTES / 1024;    // 1 KiB copies per operand tile
+constexpr int OPS_PER_WAVE = OPS / 4;     // per operand, per wave
+
+struct ProjParams {
+    const uint16_t *x;  // [M][ldx]
+    const uint16_t *w;  // [N][ldw]
+    float *out;         // [M][ldo]
+    uint32_t M, N, K, ldx, ldw, ldo;
+    uint32_t m_tiles;
+};
+
+// Copies rows [row0, row0 + 128) x k [k0, k0 + 64) of a K-contiguous
+// operand into an LDS tile, this wave's share of the 16 copies. Rows past
+// `rows` re-read the last row (in bounds; their results are never stored).
+__device__ __forceinline__ void stage_tile(const uint16_t *src, uint32_t ld, uint32_t rows, uint32_t row0,
+                                           uint32_t k0, RL_LDS uint8_t *dst, int wave, int lane)
+{
+#pragma unroll
+    for (int j = 0; j < OPS_PER_WAVE; j++) {
+        const int op = wave * OPS_PER_WAVE + j;
+        const uint32_t r = (uint32_t)op * 8 + (uint32_t)lane / 8;
+        const uint32_t pos = (uint32_t)lane % 8;
+        const uint32_t c = pos ^ (r & 7);
+        const uint32_t grow = min(row0 + r, rows - 1);
+        const uint16_t *rowp = src + (size_t)grow * ld + k0;
+        // wave-uniform base: the tile's first row; per-lane offset to its chunk
+        const uint16_t *base = src + (size_t)min(row0, rows - 1) * ld + k0;
+        const uint32_t off = (uint32_t)((const uint8_t *)(rowp + c * 8) - (const uint8_t *)base);
+        rl_g2lds_16_off(base, off, dst + op * 1024);
+    }
+}
+
+__global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t sA0[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB0[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sA1[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sB1[TILE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t mt = blockIdx.x % p.m_tiles;
+    const uint32_t nt = blockIdx.x / p.m_tiles;
+    const uint32_t m0 = mt * BM, n0 = nt * BN;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    rl_f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            acc[i][j] = rl_f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const uint32_t ksteps = p.K / BK;
+    // fragment addressing inside a tile: row (l % 16) of block i, chunk 4 s + l / 16
+    const int fr = lane & 15;
+    const int fc = lane >> 4;
+
+    stage_tile(p.x, p.ldx, p.M, m0, 0, (RL_LDS uint8_t *)sA0, wave, lane);
+    stage_tile(p.w, p.ldw, p.N, n0, 0, (RL_LDS uint8_t *)sB0, wave, lane);
+    for (uint32_t kt = 0; kt < ksteps; kt++) {
+        RL_LDS uint8_t *a_cur = (kt & 1) ? (RL_LDS uint8_t *)sA1 : (RL_LDS uint8_t *)sA0;
+        RL_LDS uint8_t *b_cur = (kt & 1) ? (RL_LDS uint8_t *)sB1 : (RL_LDS uint8_t *)sB0;
+        if (kt + 1 < ksteps) {
+            RL_LDS uint8_t *a_nxt = (kt & 1) ? (RL_LDS uint8_t *)sA0 : (RL_LDS uint8_t *)sA1;
+            RL_LDS uint8_t *b_nxt = (kt & 1) ? (RL_LDS uint8_t *)sB0 : (RL_LDS uint8_t *)sB1;
+            stage_tile(p.x, p.ldx, p.M, m0, (kt + 1) * BK, a_nxt, wave, lane);
+            stage_tile(p.w, p.ldw, p.N, n0, (kt + 1) * BK, b_nxt, wave, lane);
+            rl_wait_vmcnt<2 * OPS_PER_WAVE>();  // this wave's copies of step kt landed
+        } else {
+            rl_wait_vmcnt<0>();
+        }
+        __syncthreads();  // ... and every other wave's
+#pragma unroll
+        for (int s = 0; s < BK / 32; s++) {
+            s16x8 af[4], bf[4];
+            const int c = 4 * s + fc;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int ra = wm * 64 + i * 16 + fr;
+                const int rb = wn * 64 + i * 16 + fr;
+                af[i] = *(RL_LDS const s16x8 *)(a_cur + ra * (BK * 2) + ((c ^ (ra & 7)) << 4));
+                bf[i] = *(RL_LDS const s16x8 *)(b_cur + rb * (BK * 2) + ((c ^ (rb & 7)) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
+                                                                        __builtin_bit_cast(bf16x8, bf[j]),
+                                                                        acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();  // the stage is rewritten two steps later
+    }
+
+    // C block (i, j): lane holds rows 4 (l / 16) + r, column l % 16
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t m = m0 + wm * 64 + i * 16 + 4 * fc + r;
+            if (m >= p.M)
+                continue;
+            float *orow = p.out + (size_t)m * p.ldo;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t n = n0 + wn * 64 + j * 16 + fr;
+                if (n < p.N)
+                    orow[n] = acc[i][j][r];
+            }
+        }
+}
+
+}  // namespace
+
+extern "C" int rl_hip_logits_proj(const rl_logits_proj_args_t *a)
+{
+    if (rl_require_open("rl_hip_logits_proj"))
+        return -1;
+    if (!a || !a->x || !a->w || !a->logits) {
+        rl_set_error("rl_hip_logits_proj: NULL argument");
+        return -1;
+    }
+    if (a->rows == 0 || a->vocab == 0 || a->hidden == 0 || a->hidden % BK != 0) {
+        rl_set_error("rl_hip_logits_proj: rows %u vocab %u hidden %u (hidden must be a positive multiple of %d)",
+                     a->rows, a->vocab, a->hidden, BK);
+        return -1;
+    }
+    if (a->x_stride < a->hidden || a->w_stride < a->hidden || a->logits_stride < a->vocab ||
+        a->x_stride % 8 != 0 || a->w_stride % 8 != 0) {
+        rl_set_error("rl_hip_logits_proj: strides x %u w %u logits %u invalid (x, w multiples of 8 elements)",
+                     a->x_stride, a->w_stride, a->logits_stride);
+        return -1;
+    }
+    ProjParams p;
+    p.x = (const uint16_t *)a->x;
+    p.w = (const uint16_t *)a->w;
+    p.out = a->logits;
+    p.M = a->rows;
+    p.N = a->vocab;
+    p.K = a->hidden;
+    p.ldx = a->x_stride;
+    p.ldw = a->w_stride;
+    p.ldo = a->logits_stride;
+    p.m_tiles = (a->rows + BM - 1) / BM;
+    const uint64_t n_tiles = (a->vocab + BN - 1) / BN;
+    const uint64_t grid = n_tiles * p.m_tiles;
+    if (grid > 0x7FFFFFFFull) {
+        rl_set_error("rl_hip_logits_proj: %llu workgroups", (unsigned long long)grid);
+        return -1;
+    }
+    hipLaunchKernelGGL(logits_proj_kernel, dim3((uint32_t)grid), dim3(256), 0, rl_stream(), p);
+    return rl_check_launch("logits_proj_kernel launch");
+}

@@ -148,6 +148,12 @@ class AppendArgs(C.Structure):
                 ("k_new", C.c_void_p), ("v_new", C.c_void_p)]
 
 
+class ProjArgs(C.Structure):
+    _fields_ = [("x", C.c_void_p), ("w", C.c_void_p), ("logits", C.c_void_p), ("rows", C.c_uint32),
+                ("vocab", C.c_uint32), ("hidden", C.c_uint32), ("x_stride", C.c_uint32),
+                ("w_stride", C.c_uint32), ("logits_stride", C.c_uint32)]
+
+
 class HwWorkerArgs(C.Structure):
     _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
                 ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
@@ -184,6 +190,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample_workspace": (sz, [C.POINTER(SampleArgs)]),
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
+        "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
         # reference host API
@@ -413,3 +420,9 @@ def hw_worker_workspace(args: HwWorkerArgs) -> DeviceBuffer:
 
 def hw_worker_launch(args: HwWorkerArgs) -> None:
     check(lib().rl_hip_hw_worker_launch(C.byref(args)), "rl_hip_hw_worker_launch")
+
+
+def logits_proj(x: DeviceBuffer, w: DeviceBuffer, logits: DeviceBuffer, rows: int, vocab: int, hidden: int) -> None:
+    a = ProjArgs(x=x.ptr, w=w.ptr, logits=logits.ptr, rows=rows, vocab=vocab, hidden=hidden, x_stride=hidden,
+                 w_stride=hidden, logits_stride=vocab)
+    check(lib().rl_hip_logits_proj(C.byref(a)), "rl_hip_logits_proj")

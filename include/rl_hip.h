@@ -107,6 +107,26 @@ typedef struct {
 size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *args);
 int rl_hip_attn_decode(const rl_attn_decode_args_t *args);
 
+/* ---- logits projection ------------------------------------------------------
+ * No reference function (the nearest analog is the fp16 GEMV
+ * query_prepare_kernel, cu/query_producer.cu:5-26). logits[r][v] =
+ * sum_k x[r][k] * w[v][k]: bf16 operands (w stored like an lm_head weight,
+ * one row of `hidden` per vocabulary entry), fp32 accumulate and output, on
+ * MFMA. `hidden` must be a multiple of 64; x and w strides multiples of 8. */
+typedef struct {
+    const void *x;               /* device [rows][x_stride] bf16 */
+    const void *w;               /* device [vocab][w_stride] bf16 */
+    float *logits;               /* device [rows][logits_stride] fp32 */
+    uint32_t rows;
+    uint32_t vocab;
+    uint32_t hidden;
+    uint32_t x_stride;           /* elements */
+    uint32_t w_stride;
+    uint32_t logits_stride;
+} rl_logits_proj_args_t;
+
+int rl_hip_logits_proj(const rl_logits_proj_args_t *args);
+
 /* ---- persistent worker on the hw_desc rings ---------------------------------
  * Replaces hw_worker_sim_run (src/hw_worker_sim.c:23-59, include/
  * hw_worker_sim.h:6-14) and the device worker decode_worker

@@ -1,0 +1,60 @@
+"""Logits projection on MFMA vs an fp64 GEMM of the same bf16 operands.
+
+logits = X[rows, hidden] . W[vocab, hidden]^T, X ~N(0,1), W ~N(0, 0.02^2)
+(the rollout-loop shape is 512 x 4096 -> 32,000). The products of bf16 values
+are exact in fp32, so the only error is fp32 summation: any summation order
+keeps |got - exact| <= (hidden - 1) * 2^-24 * sum_k |x_k w_k| (first order);
+the test allows twice that. A transposed operand, a wrong row or a dropped
+K step breaks the bound by orders of magnitude.
+"""
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(rl, rows, vocab, hidden, seed, check_rows=None, check_cols=None, repeats=1):
+    print(f"[proj] rows={rows} vocab={vocab} hidden={hidden}", flush=True)
+    rng = np.random.default_rng(seed)
+    x = synth.f32_to_bf16(rng.standard_normal((rows, hidden), dtype=np.float32))
+    w = synth.f32_to_bf16(rng.standard_normal((vocab, hidden), dtype=np.float32) * np.float32(0.02))
+    dx, dw = rl.DeviceBuffer.from_array(x), rl.DeviceBuffer.from_array(w)
+    out = rl.DeviceBuffer(rows * vocab * 4)
+    timer = rl.Timer()
+    rl.logits_proj(dx, dw, out, rows, vocab, hidden)
+    rl.sync()
+    timer.begin()
+    for _ in range(repeats):
+        rl.logits_proj(dx, dw, out, rows, vocab, hidden)
+    ms = timer.end() / repeats
+    got = out.download(np.float32, (rows, vocab))
+    xr = np.arange(rows) if check_rows is None else check_rows
+    vc = np.arange(vocab) if check_cols is None else check_cols
+    xf = synth.bf16_to_f32(x).astype(np.float64)
+    wf = synth.bf16_to_f32(w).astype(np.float64)
+    ref = xf[xr] @ wf[vc].T
+    mag = np.abs(xf[xr]) @ np.abs(wf[vc]).T
+    err = np.abs(got[np.ix_(xr, vc)] - ref)
+    bound = 2.0 * (hidden - 1) * 2.0**-24 * mag
+    assert np.all(err <= bound + 1e-30), float((err / np.maximum(bound, 1e-30)).max())
+    print(f"[proj] max err {err.max():.3e}, worst err/bound {(err / np.maximum(bound, 1e-30)).max():.3f}, "
+          f"{ms * 1e3:.1f} us, {2.0 * rows * vocab * hidden / (ms * 1e-3) / 1e12:.1f} TFLOP/s", flush=True)
+    for b in (dx, dw, out):
+        b.close()
+
+
+@pytest.mark.parametrize("rows,vocab,hidden", [(1, 129, 64), (130, 1000, 128), (64, 32000, 256),
+                                               (257, 300, 4096)])
+def test_projection_shapes(rl, gpu, rows, vocab, hidden):
+    _case(rl, rows, vocab, hidden, seed=rows + vocab + hidden)
+
+
+def test_projection_rollout_shape(rl, gpu):
+    """512 x 4096 -> 32,000: every column of 24 rows, every row of 64 columns."""
+    rng = np.random.default_rng(5)
+    rows = np.sort(rng.choice(512, 24, replace=False))
+    _case(rl, 512, 32000, 4096, seed=4, check_rows=rows, repeats=5)
+    cols = np.sort(rng.choice(32000, 64, replace=False))
+    _case(rl, 512, 32000, 4096, seed=4, check_cols=cols)
