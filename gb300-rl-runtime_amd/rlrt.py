@@ -154,6 +154,13 @@ class ProjArgs(C.Structure):
                 ("w_stride", C.c_uint32), ("logits_stride", C.c_uint32)]
 
 
+class RewardArgs(C.Structure):
+    _fields_ = [("tokens", C.c_void_p), ("n_tokens", C.c_void_p), ("targets", C.c_void_p),
+                ("rollouts", C.c_uint32), ("group_size", C.c_uint32), ("token_stride", C.c_uint32),
+                ("target_stride", C.c_uint32), ("target_len", C.c_uint32), ("descs", C.c_void_p),
+                ("reward", C.c_void_p), ("advantage", C.c_void_p)]
+
+
 class HwWorkerArgs(C.Structure):
     _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
                 ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
@@ -191,6 +198,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
+        "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
         "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
         # reference host API

@@ -21,6 +21,7 @@
 #include <stdint.h>
 #include "hw_ring.h"
 #include "kv_layout.h"
+#include "reward.h"
 
 RL_EXTERN_C_BEGIN
 
@@ -126,6 +127,30 @@ typedef struct {
 } rl_logits_proj_args_t;
 
 int rl_hip_logits_proj(const rl_logits_proj_args_t *args);
+
+/* ---- reward and group advantage ---------------------------------------------
+ * Replaces reward_score_kernel (cu/reward.cu:4-15) and adds the GRPO group
+ * advantage (no reference function). Rollout r belongs to group
+ * r / group_size; count_r = #{i < min(n_tokens[r], target_len, token_stride) :
+ * tokens[r][i] == targets[group][i]}; reward_r = (count_r & 0xFF) / 255.0f;
+ * advantage_r = (reward_r - mean) / std over the group, population std, 0 when
+ * std is 0 - bit-identical to reward_match_count / reward_group_advantage in
+ * reward.h. descs, when given, receives one RewardDesc per rollout. */
+typedef struct {
+    const uint32_t *tokens;      /* device [rollouts][token_stride] */
+    const uint32_t *n_tokens;    /* device [rollouts] */
+    const uint32_t *targets;     /* device [rollouts / group_size][target_stride] */
+    uint32_t rollouts;
+    uint32_t group_size;         /* 1..64, divides rollouts */
+    uint32_t token_stride;
+    uint32_t target_stride;
+    uint32_t target_len;
+    RewardDesc *descs;           /* device [rollouts], optional */
+    float *reward;               /* device [rollouts] */
+    float *advantage;            /* device [rollouts] */
+} rl_reward_args_t;
+
+int rl_hip_reward_advantage(const rl_reward_args_t *args);
 
 /* ---- persistent worker on the hw_desc rings ---------------------------------
  * Replaces hw_worker_sim_run (src/hw_worker_sim.c:23-59, include/
