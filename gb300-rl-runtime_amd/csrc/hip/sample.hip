@@ -62,6 +62,7 @@ struct SampleParams {
     float top_p_all;
     uint64_t seed_all;
     uint64_t step;
+    const uint64_t *steps;
     uint32_t *token_out;
     float *logprob_out;
     SplitStat *stats;       // [rows][splits]
@@ -79,6 +80,10 @@ __device__ __forceinline__ uint32_t row_topk(const SampleParams &p, uint32_t row
 __device__ __forceinline__ float row_topp(const SampleParams &p, uint32_t row)
 {
     return p.top_p ? p.top_p[row] : p.top_p_all;
+}
+__device__ __forceinline__ uint64_t row_step(const SampleParams &p, uint32_t row)
+{
+    return p.steps ? p.steps[row] : p.step;
 }
 __device__ __forceinline__ uint64_t row_seed(const SampleParams &p, uint32_t row)
 {
@@ -526,7 +531,7 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
     lowest = block_min_u32(lowest, bs);
 
     // (5) ascending-index walk: chunks of 256 threads x 8 contiguous elements
-    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
     uint64_t carry = 0;
     uint32_t tok = 0xFFFFFFFFu;
     for (uint32_t base = 0; base < V && tok == 0xFFFFFFFFu; base += kMergeThreads * 8) {
@@ -764,7 +769,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
                 }
                 const uint32_t wp = np ? rl_readlane(c, (int)np - 1) : 0u;
-                const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+                const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
                 const bool in_p = (uint32_t)lane < np;
                 rl_wave_lds_fence();
                 uint32_t s_le = 0;
@@ -824,7 +829,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             const uint64_t wp = block_sum_u64(wp_own, bs);
 
             // ---- draw; smallest index whose ascending-index prefix weight exceeds u
-            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), p.step, row), wp);
+            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
             uint32_t cand = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
             for (uint32_t i = tid; i < np; i += kMergeThreads) {
                 const uint32_t idx_i = s_idx[i];
@@ -920,6 +925,7 @@ extern "C" int rl_hip_sample(const rl_sample_args_t *a)
     p.top_p_all = a->top_p_all;
     p.seed_all = a->seed_all;
     p.step = a->step;
+    p.steps = a->steps;
     p.token_out = a->token_out;
     p.logprob_out = a->logprob_out;
     uint8_t *ws = (uint8_t *)a->workspace;

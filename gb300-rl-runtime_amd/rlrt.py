@@ -137,7 +137,7 @@ class SampleArgs(C.Structure):
                 ("greedy", C.c_uint32), ("temperature", C.c_void_p), ("top_k", C.c_void_p),
                 ("top_p", C.c_void_p), ("seed", C.c_void_p), ("temperature_all", C.c_float),
                 ("top_k_all", C.c_uint32), ("top_p_all", C.c_float), ("seed_all", C.c_uint64),
-                ("step", C.c_uint64), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
+                ("step", C.c_uint64), ("steps", C.c_void_p), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
                 ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
 
@@ -159,6 +159,18 @@ class RewardArgs(C.Structure):
                 ("rollouts", C.c_uint32), ("group_size", C.c_uint32), ("token_stride", C.c_uint32),
                 ("target_stride", C.c_uint32), ("target_len", C.c_uint32), ("descs", C.c_void_p),
                 ("reward", C.c_void_p), ("advantage", C.c_void_p)]
+
+
+class SchedArgs(C.Structure):
+    _fields_ = [("req_ring", C.c_void_p), ("done_ring", C.c_void_p), ("state", C.c_void_p),
+                ("requests", C.c_uint32), ("prompt_len", C.c_void_p), ("req_table", C.c_void_p),
+                ("kv_heads", C.c_uint32), ("table_stride", C.c_uint32), ("gen_tokens", C.c_void_p),
+                ("gen_stride", C.c_uint32), ("targets", C.c_void_p), ("group_size", C.c_uint32),
+                ("target_len", C.c_uint32), ("rewards", C.c_void_p), ("slot_table", C.c_void_p),
+                ("slot_ctx", C.c_void_p), ("slot_pos", C.c_void_p), ("slot_temp", C.c_void_p),
+                ("slot_topk", C.c_void_p), ("slot_topp", C.c_void_p), ("slot_seed", C.c_void_p),
+                ("slot_step", C.c_void_p), ("sampled", C.c_void_p), ("counters", C.c_void_p),
+                ("max_spin", C.c_uint64)]
 
 
 class HwWorkerArgs(C.Structure):
@@ -199,6 +211,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
+        "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
         "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
         # reference host API

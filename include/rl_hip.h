@@ -21,6 +21,7 @@
 #include <stdint.h>
 #include "hw_ring.h"
 #include "kv_layout.h"
+#include "request.h"
 #include "reward.h"
 
 RL_EXTERN_C_BEGIN
@@ -152,6 +153,57 @@ typedef struct {
 
 int rl_hip_reward_advantage(const rl_reward_args_t *args);
 
+/* ---- rollout scheduler ----------------------------------------------------------
+ * Restates rollout_worker (cu/gpu_scheduler.cu:26-83) as one kernel launched
+ * between batched decode steps (GPU_MAX_ROLLOUTS = 256 slots of the
+ * byte-compatible GpuRolloutState, request.h:67-82). Per launch: a slot that
+ * took part in the last step stores `sampled[slot]` as its next generated
+ * token (gen_tokens[request][t]) and counts it; slots with tokens_generated >=
+ * max_tokens get reward (count & 0xFF) / 255 with count = generated tokens
+ * equal to targets[request / group_size] at the same position, push
+ * RolloutDone {request_id, slot, tokens_generated, reward, 0} to done_ring in
+ * slot order and free the slot; requests are then consumed from req_ring
+ * while a slot is free (lowest free slot first; never consumed without one;
+ * request_id UINT64_MAX sets counters[2]); admitted slots copy their
+ * request's kv_heads block-table rows into slot_table. Finally every slot
+ * writes the next step's per-row arguments: slot_ctx / slot_pos = prompt_len
+ * + tokens_generated (0 / UINT32_MAX when idle), and the sampler's
+ * temperature (0 when idle), top_k, top_p, seed (the request's rng_seed) and
+ * step (the index of the token being generated). Rings live in coherent host
+ * memory (req_ring_create / done_ring_create after rl_hip_open).
+ * counters: [0] dones pushed, [1] requests admitted, [2] end marker seen,
+ * [3] status (0 ok, 2 request id >= requests, 3 done ring full for max_spin
+ * polls; sticky). */
+typedef struct {
+    RequestRing *req_ring;
+    DoneRing *done_ring;
+    GpuRolloutState *state;      /* device, zero-initialised before the first launch */
+    uint32_t requests;           /* request ids index the side tables below */
+    const uint32_t *prompt_len;  /* device [requests]: tokens already in the KV */
+    const uint32_t *req_table;   /* device [requests][kv_heads][table_stride] */
+    uint32_t kv_heads;
+    uint32_t table_stride;
+    uint32_t *gen_tokens;        /* device [requests][gen_stride] */
+    uint32_t gen_stride;
+    const uint32_t *targets;     /* device [requests / group_size][target_len] */
+    uint32_t group_size;
+    uint32_t target_len;
+    float *rewards;              /* device [requests] */
+    uint32_t *slot_table;        /* device [256][kv_heads][table_stride] */
+    uint32_t *slot_ctx;          /* device [256] */
+    uint32_t *slot_pos;          /* device [256] */
+    float *slot_temp;            /* device [256] */
+    uint32_t *slot_topk;         /* device [256] */
+    float *slot_topp;            /* device [256] */
+    uint64_t *slot_seed;         /* device [256] */
+    uint64_t *slot_step;         /* device [256] */
+    const uint32_t *sampled;     /* device [256] tokens of the last step, NULL before the first */
+    uint32_t *counters;          /* device [4], zero-initialised */
+    uint64_t max_spin;           /* 0 selects 2^22 */
+} rl_rollout_sched_args_t;
+
+int rl_hip_rollout_schedule(const rl_rollout_sched_args_t *args);
+
 /* ---- persistent worker on the hw_desc rings ---------------------------------
  * Replaces hw_worker_sim_run (src/hw_worker_sim.c:23-59, include/
  * hw_worker_sim.h:6-14) and the device worker decode_worker
@@ -227,6 +279,7 @@ typedef struct {
     float top_p_all;
     uint64_t seed_all;
     uint64_t step;               /* Philox counter of this sampling event */
+    const uint64_t *steps;       /* device [rows] per-row step counters, or NULL: `step` for every row */
     uint32_t *token_out;         /* device [rows] */
     float *logprob_out;          /* device [rows] */
     void *workspace;             /* device, >= rl_hip_sample_workspace() */
