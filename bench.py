@@ -14,7 +14,15 @@ roofline (attention, HBM-bound) is measured over its own launches with HIP
 events on the library stream. The CPU baseline is the oracle's OpenMP
 restatement of the same step, timed on this host.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append]
+Before the timed run, two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE)
+in child processes measure the attention call's HBM traffic, calibrated on a
+256 MiB device copy in the same pass (--no-traffic skips them).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append|copy]
+  python bench.py --workload sample256|longctx|proj|plumbing|rollout
+      the other synthetic workloads (sampling at 256 rows, long-context
+      split-KV decode, the vocabulary projection, the hw_desc ring plumbing
+      decode, the GRPO rollout loop), one JSON line each
 """
 import argparse
 import json
@@ -25,10 +33,20 @@ import time
 import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(ROOT, "gb300-rl-runtime_amd"))
+PKG = os.path.join(ROOT, "gb300-rl-runtime_amd")
+sys.path.insert(0, PKG)
 
-import rlrt  # noqa: E402
-import synth  # noqa: E402
+# The library is loaded only after the counter passes (child processes) ran:
+# nothing in this process touches the GPU before them.
+rlrt = synth = None
+
+
+def _load():
+    global rlrt, synth
+    import rlrt as _rlrt
+    import synth as _synth
+    rlrt, synth = _rlrt, _synth
+
 
 METRIC = "decode steps/s + tokens/s at B=64 ctx≤4K; achieved HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
@@ -37,6 +55,7 @@ CTX_LO, CTX_HI, MAX_CTX = 512, 4096, 4096
 VOCAB, SPIKES, TEMP, TOPK, TOPP = 128256, 5, 0.8, 50, 0.9
 LOGIT_COPIES = 4
 SEED_KV, SEED_LOGITS = 2, 3
+PMC_CALLS, PMC_COPY_BYTES = 3, 256 << 20
 
 
 def log(msg):
@@ -193,24 +212,321 @@ def _cpu_model():
     return "unknown"
 
 
+# ---------------------------------------------------------------- HBM traffic (rocprofv3 counters)
+def _pmc_pass(counter, tmp):
+    """One rocprofv3 --pmc pass over `bench.py --only pmc` (a child process);
+    returns {kernel name: counter summed over its dispatches}."""
+    import csv
+    import glob
+    import subprocess
+
+    out = os.path.join(tmp, counter)
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", out, "-o", "pmc", "--",
+           sys.executable, os.path.abspath(__file__), "--only", "pmc"]
+    subprocess.run(cmd, check=True, timeout=120, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+    files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise RuntimeError(f"no counter_collection.csv under {out}")
+    acc = {}
+    with open(files[0], newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            k = row["Kernel_Name"]
+            acc[k] = acc.get(k, 0.0) + float(row["Counter_Value"])
+    return acc
+
+
+def measure_traffic():
+    """HBM bytes per attention call from FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch), each scaled by what the counter reads for a device copy of
+    256 MiB (read 256 MiB, write 256 MiB) run in the same pass. The runtime
+    may split one copy into several blit dispatches, so both the calls and
+    the copies are counted by what the target ran (PMC_CALLS of each)."""
+    import shutil
+    import tempfile
+
+    if not shutil.which("rocprofv3"):
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="rlrt_pmc_")
+    try:
+        fetch = _pmc_pass("FETCH_SIZE", tmp)
+        write = _pmc_pass("WRITE_SIZE", tmp)
+    except Exception as e:  # the counters are reported as null, the bench goes on
+        return None, f"counter pass failed: {e}"
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+    def pick(d, key):
+        v = [x for k, x in d.items() if key in k]
+        return sum(v) if v else None
+
+    copy_kib = PMC_COPY_BYTES / 1024.0
+    cf, cw = pick(fetch, "copyBuffer"), pick(write, "copyBuffer")
+    af, aw = pick(fetch, "attn_decode_kernel"), pick(write, "attn_decode_kernel")
+    mf, mw = pick(fetch, "attn_merge_kernel") or 0.0, pick(write, "attn_merge_kernel") or 0.0
+    if not (cf and cw and af is not None and aw is not None):
+        return None, f"kernels missing from the counter output: {sorted(fetch)}"
+    cf, cw = cf / PMC_CALLS, cw / PMC_CALLS                     # per 256 MiB copy
+    af, aw = (af + mf) / PMC_CALLS, (aw + mw) / PMC_CALLS       # per attention call (both kernels)
+    kf, kw = copy_kib / cf, copy_kib / cw
+    total = (af * kf + aw * kw) * 1024.0
+    return {"bytes": total, "fetch_kib": af, "write_kib": aw, "fetch_scale": kf, "write_scale": kw,
+            "copy_fetch_kib": cf, "copy_write_kib": cw}, None
+
+
+def pmc_target():
+    """What the counter passes profile: 3 attention calls and 3 device copies
+    of 256 MiB (the calibration kernel)."""
+    rlrt.open_device(0)
+    step = Step()
+    for i in range(PMC_CALLS):
+        rlrt.attn_decode(step.attn)
+    n = PMC_COPY_BYTES
+    a, b = rlrt.DeviceBuffer(n), rlrt.DeviceBuffer(n)
+    rlrt.check(rlrt.lib().rl_hip_memset_d(a.ptr, 1, n), "memset")
+    for _ in range(PMC_CALLS):
+        rlrt.check(rlrt.lib().rl_hip_memcpy_d2d(b.ptr, a.ptr, n), "d2d")
+    rlrt.sync()
+
+
+# ---------------------------------------------------------------- the other workloads
+def _event_us(fn, k, warmup=3):
+    for i in range(warmup):
+        fn(i)
+    rlrt.sync()
+    timer = rlrt.Timer()
+    timer.begin()
+    for i in range(k):
+        fn(i)
+    ms = timer.end()
+    return ms / k * 1e3
+
+
+def wl_sample256(args):
+    """256 rows x 128,256 fp32 logits ~N(0,1), 5 spikes per row at +8.0;
+    T 0.8, top-k 50, top-p 0.9, Philox per-row seed; greedy on the same rows.
+    Three copies of the logits (394 MB) rotate past the 256 MB Infinity Cache."""
+    rows, copies = 256, 3
+    x = synth.make_logits(3, rows, VOCAB, spikes=SPIKES)
+    lg = [rlrt.DeviceBuffer.from_array(x) for _ in range(copies)]
+    seeds = rlrt.DeviceBuffer.from_array(np.random.default_rng(34).integers(0, 2**63, rows, dtype=np.uint64))
+    tok, lp = rlrt.DeviceBuffer(rows * 4), rlrt.DeviceBuffer(rows * 4)
+    res = {}
+    for name, greedy in (("topk_topp", False), ("greedy", True)):
+        ss = [rlrt.sample_args(b, rows, VOCAB, VOCAB, tok, lp, greedy=greedy, temperature=TEMP, top_k=TOPK,
+                               top_p=TOPP, seeds=seeds) for b in lg]
+        ws = rlrt.sample_workspace(ss[0])
+        for s in ss[1:]:
+            s.workspace, s.workspace_bytes = ws.ptr, ws.nbytes
+
+        def run(i, ss=ss):
+            s = ss[i % copies]
+            s.step = i
+            rlrt.sample(s)
+
+        us = _event_us(run, args.steps)
+        nbytes = rows * VOCAB * 4 + rows * 8
+        res[name] = {"us_per_call": us, "rows_per_s": rows / (us * 1e-6), "alg_bytes": nbytes,
+                     "alg_gbps": nbytes / (us * 1e-6) / 1e9, "frac": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS}
+        ws.close()
+    return {"workload": "sample_r256_v128256_t0.8_k50_p0.9 (+ greedy)", **res}
+
+
+def wl_longctx(args):
+    """B=8, ctx 32,768, 64 q / 8 kv heads, d128, bf16 K/V ~N(0,1), permuted
+    16-token blocks, split-KV over the whole device with the fp32 LSE merge;
+    then greedy over 8 x 128,256 fp32 logits ~N(0,1)."""
+    bb, qh = 8, 64
+    w = synth.make_decode(5, bb, qh, KVH, D, 32768, 32768, dtype="bf16")
+    layout = rlrt.KvLayoutDesc.paged(TPB, D)
+    bufs = [rlrt.DeviceBuffer.from_array(a) for a in (w.arena, w.table, w.ctx, w.q)]
+    out = rlrt.DeviceBuffer(bb * qh * D * 2)
+    a = rlrt.attn_args(bufs[0], layout, bufs[1], w.table_stride, bb, qh, KVH, rlrt.DTYPE_BF16, bufs[2], w.max_ctx,
+                       bufs[3], out)
+    ws = rlrt.attn_workspace(a)
+    x = synth.make_logits(6, bb, VOCAB)
+    lg = rlrt.DeviceBuffer.from_array(x)
+    tok, lp = rlrt.DeviceBuffer(bb * 4), rlrt.DeviceBuffer(bb * 4)
+    s = rlrt.sample_args(lg, bb, VOCAB, VOCAB, tok, lp, greedy=True)
+    sws = rlrt.sample_workspace(s)
+    attn_bytes = w.kv_bytes() + bb * qh * D * 2 * 2 + int((-(-w.ctx.astype(np.int64) // TPB)).sum()) * KVH * 4
+    us_attn = _event_us(lambda i: rlrt.attn_decode(a), args.steps)
+    us_step = _event_us(lambda i: (rlrt.attn_decode(a), rlrt.sample(s)), args.steps)
+    step_bytes = attn_bytes + bb * VOCAB * 4
+    return {"workload": "gqa_decode_b8_q64kv8_d128_ctx32768 + greedy_b8_v128256",
+            "attn_us": us_attn, "attn_alg_bytes": attn_bytes, "attn_gbps": attn_bytes / (us_attn * 1e-6) / 1e9,
+            "attn_frac": attn_bytes / (us_attn * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "step_us": us_step, "steps_per_s": 1e6 / us_step, "tokens_per_s": bb * 1e6 / us_step,
+            "step_gbps": step_bytes / (us_step * 1e-6) / 1e9}
+
+
+def wl_proj(args):
+    """logits[rows, 32,000] = X[rows, 4,096] . W^T, bf16 in, fp32 out, at the
+    rollout loop's 256 slots and at 512 rows; W bf16 ~N(0, 0.02^2)."""
+    vocab, hid = 32000, 4096
+    rng = np.random.default_rng(7)
+    w = rlrt.DeviceBuffer.from_array(synth.f32_to_bf16(rng.standard_normal((vocab, hid), np.float32) * 0.02))
+    res = {}
+    for rows in (256, 512):
+        x = rlrt.DeviceBuffer.from_array(synth.f32_to_bf16(rng.standard_normal((rows, hid), np.float32)))
+        out = rlrt.DeviceBuffer(rows * vocab * 4)
+        us = _event_us(lambda i: rlrt.logits_proj(x, w, out, rows, vocab, hid), args.steps)
+        flop = 2.0 * rows * vocab * hid
+        nbytes = vocab * hid * 2 + rows * hid * 2 + rows * vocab * 4
+        res[f"rows{rows}"] = {"us": us, "tflops": flop / (us * 1e-6) / 1e12,
+                              "mfma_frac_bf16_dense": flop / (us * 1e-6) / 2.5e15,
+                              "alg_bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
+                              "hbm_frac": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+                              "ideal_us": max(flop / 2.5e15, nbytes / 8e12) * 1e6}
+        x.close()
+        out.close()
+    return {"workload": "logits_proj_h4096_v32000", **res}
+
+
+def wl_plumbing(args):
+    """One rollout, MHA 8 heads x d64 fp16 K/V ~N(0, 0.5^2), 16-token blocks,
+    KV length 256 at the start. 100 descriptors through infer_submit_decode
+    into the hw_desc command ring; the persistent worker runs each (attention,
+    greedy over 32,000 fp32 logits ~N(0, 2^2), KV append) and publishes on the
+    completion ring. Measured twice: pipelined (all submitted back to back)
+    and lock-step (submit one, wait for its completion)."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    steps, ctx0, vocab = 100, 256, 32000
+    rng = np.random.default_rng(1001)
+    w = synth.make_decode(1000, 1, 8, 8, 64, ctx0, ctx0, dtype="fp16", kv_std=0.5, reserve_tokens=ctx0 + 2 * steps + 1)
+    q = synth.f32_to_f16(rng.standard_normal((2 * steps, 8, 64), dtype=np.float32))
+    kv = synth.f32_to_f16(rng.standard_normal((2 * steps, 8, 64), dtype=np.float32) * np.float32(0.5))
+    logits = rng.standard_normal((2 * steps, vocab), dtype=np.float32) * np.float32(2.0)
+    bufs = {n: rlrt.DeviceBuffer.from_array(a) for n, a in
+            (("arena", w.arena), ("table", w.table), ("q", q), ("kv", kv), ("logits", logits))}
+    outs = [rlrt.DeviceBuffer(n, zero=True) for n in (2 * steps * 8 * 64 * 4, 2 * steps * 4, 2 * steps * 4, 32)]
+
+    def coherent(n):
+        p = L.rl_hip_host_alloc_coherent(n)
+        if not p:
+            raise rlrt.RlrtError("coherent host allocation failed")
+        return p
+
+    cq, dq = L.hw_ring_create(), L.hw_ring_create()
+    rings, stop, doorbell = coherent(16), coherent(64), coherent(64)
+    C.cast(rings, C.POINTER(C.c_void_p))[0] = cq
+    C.cast(rings, C.POINTER(C.c_void_p))[1] = dq
+    a = rlrt.HwWorkerArgs(cmdq=rings, doneq=rings + 8, groups=1, stop=stop, max_idle_polls=1 << 24,
+                          arena_base=bufs["arena"].ptr, arena_bytes=bufs["arena"].nbytes,
+                          layout=rlrt.KvLayoutDesc.paged(16, 64), block_table=bufs["table"].ptr,
+                          table_stride=w.table_stride, rollouts=1, q_heads=8, kv_heads=8, dtype=rlrt.DTYPE_FP16,
+                          scale=0.0, max_steps=2 * steps, q=bufs["q"].ptr, k_new=bufs["kv"].ptr, v_new=bufs["kv"].ptr,
+                          logits=bufs["logits"].ptr, vocab=vocab, attn_out=outs[0].ptr, token_out=outs[1].ptr,
+                          logprob_out=outs[2].ptr, stats=outs[3].ptr)
+    ws = rlrt.hw_worker_workspace(a)
+    ctx = rlrt.InferHwCtx(cmdq=cq, doneq=dq, doorbell=doorbell, gpu_group_id=7, kv_arena_id=42)
+    rlrt.hw_worker_launch(a)
+    lat = []
+    try:
+        t0 = time.perf_counter()
+        for i in range(steps):
+            if L.infer_submit_decode(C.byref(ctx), 0, 0x1000 * i, 0x40 * i, 0, ctx0 + i, ctx0 + i + 1) != 0:
+                raise rlrt.RlrtError("submit failed")
+        got, deadline = 0, time.perf_counter() + 30
+        while got < steps and time.perf_counter() < deadline:
+            if rlrt.hw_ring_pop(dq) is not None:
+                got += 1
+        pipelined = time.perf_counter() - t0
+        if got != steps:
+            raise rlrt.RlrtError(f"pipelined: {got} of {steps} completions")
+        for i in range(steps, 2 * steps):
+            t1 = time.perf_counter()
+            if L.infer_submit_decode(C.byref(ctx), 0, 0x1000 * i, 0x40 * i, 0, ctx0 + i, ctx0 + i + 1) != 0:
+                raise rlrt.RlrtError("submit failed")
+            deadline = t1 + 5
+            while rlrt.hw_ring_pop(dq) is None:
+                if time.perf_counter() > deadline:
+                    raise rlrt.RlrtError("lock-step completion timed out")
+            lat.append(time.perf_counter() - t1)
+        rlrt.hw_ring_push(cq, rlrt.HwDesc(opcode=255))
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rlrt.sync()
+    st = outs[3].download(np.uint64, 4)
+    lat_us = np.array(lat) * 1e6
+    for b in list(bufs.values()) + outs + [ws]:
+        b.close()
+    L.hw_ring_destroy(cq)
+    L.hw_ring_destroy(dq)
+    for p in (rings, stop, doorbell):
+        L.rl_hip_host_free(p)
+    return {"workload": "plumbing_mha8_d64_fp16_ctx256_v32000_100steps",
+            "pipelined_steps_per_s": steps / pipelined, "pipelined_ms": pipelined * 1e3,
+            "lockstep_latency_us": {"p50": float(np.percentile(lat_us, 50)), "p90": float(np.percentile(lat_us, 90)),
+                                    "p99": float(np.percentile(lat_us, 99)), "mean": float(lat_us.mean())},
+            "lockstep_steps_per_s": 1e6 / float(lat_us.mean()), "worker_stats": st.tolist(),
+            "note": "host side polls the completion ring from Python (ctypes)"}
+
+
+def wl_rollout(args):
+    """512 GRPO requests (64 groups of 8, shared 512-token prefix, U[0,512]
+    private prompt tokens, 256 generated tokens each) through the request
+    ring, the device scheduler, batched decode (attention, projection, top-p
+    sampling, KV append) over 256 slots and the done ring."""
+    import grpo
+
+    cfg = grpo.build_workload(404)
+    loop = grpo.RolloutLoop(cfg)
+    loop.submit_requests()
+    res = loop.run()
+    dones = len(loop.dones)
+    loop.close()
+    gen_tokens = grpo.REQ * grpo.GEN
+    return {"workload": "grpo_512req_64x8_prefix512_gen256_q32kv8_d128_v32000", "steps": res["steps"],
+            "wall_s": res["wall_s"], "generated_tokens_per_s": gen_tokens / res["wall_s"], "dones": dones,
+            "steady_us_per_step": res["window_us_per_step"],
+            "steady_tokens_per_s": grpo.SLOTS / res["window_us_per_step"] * 1e6}
+
+
+WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
+             "rollout": wl_rollout}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append", "copy"])
+    ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append", "copy", "pmc"])
+    ap.add_argument("--workload", default="step", choices=["step"] + sorted(WORKLOADS),
+                    help="step: the headline decode step; the others print one JSON line of their own")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--grid-waves", type=int, default=0,
                     help="attention: persistent waves sharing the KV stream (0: library default, a full device)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs the decode hot path on one GPU only; multi-GPU runs are not part of it "
-              "(DESIGN.md describes how the path would shard).", file=sys.stderr)
+        print("bench.py: this build runs the decode hot path on one GPU only; multi-GPU runs are not part of it; "
+              "the path shards by rollout, with no exchange inside a decode step.", file=sys.stderr)
         sys.exit(2)
 
+    traffic, traffic_note = None, "not measured (--no-traffic)"
+    headline = args.workload == "step" and args.only == "step"
+    if headline and not args.no_traffic:
+        t0 = time.time()
+        traffic, traffic_note = measure_traffic()
+        log(f"[bench] counter passes in {time.time() - t0:.1f}s: {traffic if traffic else traffic_note}")
+
+    _load()
     info = rlrt.open_device(0)
     log(f"[bench] device {info.arch.decode()} cu={info.cu_count} clock={info.clock_khz / 1e3:.0f} MHz")
+    if args.only == "pmc":
+        pmc_target()
+        return
+    if args.workload != "step":
+        res = WORKLOADS[args.workload](args)
+        res["device"] = info.arch.decode()
+        print(json.dumps(res), flush=True)
+        return
     if args.only == "copy":
         # calibration for the PMC byte counters: device copies of a known size
         n = 256 << 20
@@ -286,9 +602,11 @@ def main():
         "step_hbm_gbps": step_gbps,
         "step_hbm_frac": step_gbps / PEAK_HBM_GBPS,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBPS, "traffic": None,
-                     "kernel": "attn_decode_kernel<128,4,bf16,16,4>", "alg_bytes_per_launch": attn_bytes,
-                     "avg_launch_us": kern["attn"]},
+                     "frac": achieved / PEAK_HBM_GBPS,
+                     "traffic": traffic["bytes"] if traffic else None,
+                     "traffic_detail": traffic if traffic else traffic_note,
+                     "kernel": "attn_decode_kernel<128,4,bf16,16> + attn_merge_kernel (one call)",
+                     "alg_bytes_per_launch": attn_bytes, "avg_launch_us": kern["attn"]},
         "kernels_us": kern,
         "stream_copy_gbps": copy_gbps,
         "device": {"arch": info.arch.decode(), "cu": info.cu_count, "clock_mhz": info.clock_khz / 1e3},

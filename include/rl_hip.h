@@ -263,7 +263,8 @@ int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
  * Philox4x32-10 draw and an integer CDF, plus the token's logprob.
  * Per-row parameter arrays may be NULL, in which case the *_all scalar is
  * used for every row. Rows with top_k == 0 or top_k >= vocab and top_p < 1
- * need a whole-vocabulary nucleus, which this entry point rejects (-1). */
+ * (a whole-vocabulary nucleus) take an exact full-row path, as do rows whose
+ * top-k candidates overflow the per-slice lists. vocab <= 64 * 8192. */
 typedef struct {
     const float *logits;         /* device [rows][row_stride] fp32 */
     uint32_t rows;

@@ -28,73 +28,13 @@ import time
 import numpy as np
 import pytest
 
+import grpo
 import synth
+from grpo import D, GEN, GROUPS, GS, HID, KVH, POOL, PREFIX, QH, REQ, SLOTS, TPB, VOCAB
 
 pytestmark = pytest.mark.gpu
 
-GROUPS, GS = 64, 8
-REQ = GROUPS * GS
-PREFIX, PRIV_MAX, GEN = 512, 512, 256
-QH, KVH, D, TPB = 32, 8, 128, 16
-HID, VOCAB = QH * D, 32000
-SLOTS = 256
-POOL = 8
 CHECK_STEPS = (0, 137, 306)
-
-
-def req_ring_push(rl, ring, req):
-    L = rl.lib()
-    head, tail = L.hw_ring_load_acquire(ring), L.hw_ring_load_acquire(ring + 64)
-    if (tail - head) & 0xFFFFFFFF >= 1024:
-        return -1
-    C.memmove(ring + 128 + (tail & 1023) * 34, C.byref(req), 34)
-    L.hw_ring_store_release(ring + 64, (tail + 1) & 0xFFFFFFFF)
-    return 0
-
-
-def done_ring_pop(rl, ring):
-    L = rl.lib()
-    head = L.hw_ring_load_acquire(ring)
-    if head == L.hw_ring_load_acquire(ring + 64):
-        return None
-    d = rl.RolloutDone.from_buffer_copy((C.c_char * 24).from_address(ring + 256 + (head & 1023) * 24))
-    L.hw_ring_store_release(ring, (head + 1) & 0xFFFFFFFF)
-    return d
-
-
-def _build(seed):
-    rng = np.random.default_rng(seed)
-    priv = rng.integers(0, PRIV_MAX + 1, REQ)
-    prompt = (PREFIX + priv).astype(np.uint32)
-    n_prefix = PREFIX // TPB
-    n_priv = -(-(priv + GEN + 1) // TPB)
-    stride = n_prefix + -(-(PRIV_MAX + GEN + 1) // TPB)   # covers the largest context
-    total = GROUPS * KVH * n_prefix + int(n_priv.sum()) * KVH
-    perm = rng.permutation(total).astype(np.uint32)
-    table = np.zeros((REQ, KVH, stride), np.uint32)
-    k = 0
-    prefix_blocks = np.zeros((GROUPS, KVH, n_prefix), np.uint32)
-    for g in range(GROUPS):
-        for h in range(KVH):
-            prefix_blocks[g, h] = perm[k:k + n_prefix]
-            k += n_prefix
-    for r in range(REQ):
-        for h in range(KVH):
-            table[r, h, :n_prefix] = prefix_blocks[r // GS, h]
-            m = int(n_priv[r])
-            table[r, h, n_prefix:n_prefix + m] = perm[k:k + m]
-            k += m
-    arena = np.empty(total * 2 * TPB * D, np.uint16)
-    synth._fill_normal(rng, arena.size, 1.0, "bf16", arena)
-    w = synth.f32_to_bf16(rng.standard_normal((VOCAB, HID), dtype=np.float32) * np.float32(0.02))
-    qpool = synth.f32_to_bf16(rng.standard_normal((POOL, SLOTS, QH, D), dtype=np.float32))
-    kpool = synth.f32_to_bf16(rng.standard_normal((POOL, SLOTS, KVH, D), dtype=np.float32))
-    vpool = synth.f32_to_bf16(rng.standard_normal((POOL, SLOTS, KVH, D), dtype=np.float32))
-    targets = rng.integers(0, VOCAB, (GROUPS, GEN), dtype=np.uint32)
-    seeds = rng.integers(0, 2**63, REQ, dtype=np.uint64)
-    return dict(prompt=prompt, table=table, stride=stride, arena=arena.view(np.uint8), w=w, qpool=qpool,
-                kpool=kpool, vpool=vpool, targets=targets, seeds=seeds, prefix_blocks=prefix_blocks,
-                priv=priv, n_blocks=n_prefix + n_priv)
 
 
 def _check_step(rl, orc, olib, cfg, dev, t):
@@ -139,12 +79,12 @@ def _check_step(rl, orc, olib, cfg, dev, t):
 def test_grpo_rollout_loop(rl, gpu, orc, olib):
     L = rl.lib()
     t0 = time.perf_counter()
-    cfg = _build(404)
+    cfg = grpo.build_workload(404)
     print(f"[rollout] inputs built in {time.perf_counter() - t0:.1f}s (arena {cfg['arena'].nbytes / 1e9:.2f} GB)",
           flush=True)
 
     # kv_prefix bookkeeping of the shared prompts (host, src/kv_prefix.c rules)
-    ptab = (C.c_uint8 * 606280)()
+    ptab = (C.c_uint8 * grpo.PREFIX_TABLE_BYTES)()
     L.kv_prefix_table_init(ptab)
     pid, bid = C.c_uint32(), C.c_uint32()
     branch_ids = []
@@ -159,110 +99,22 @@ def test_grpo_rollout_loop(rl, gpu, orc, olib):
             branch_ids.append(bid.value)
     assert all(L.kv_prefix_get(ptab, g).contents.refcnt == GS + 1 for g in range(GROUPS))
 
-    dev = {}
-    up = lambda k, a: dev.__setitem__(k, rl.DeviceBuffer.from_array(a))  # noqa: E731
-    up("arena", cfg["arena"])
-    up("w", cfg["w"])
-    up("qpool", cfg["qpool"])
-    up("kpool", cfg["kpool"])
-    up("vpool", cfg["vpool"])
-    up("prompt", cfg["prompt"])
-    up("rtab", cfg["table"])
-    up("targets", cfg["targets"])
-    stride = cfg["stride"]
-    zeros = lambda k, n: dev.__setitem__(k, rl.DeviceBuffer(n, zero=True))  # noqa: E731
-    zeros("state", 18464)
-    zeros("counters", 16)
-    zeros("gen", REQ * GEN * 4)
-    zeros("rewards", REQ * 4)
-    zeros("stab", SLOTS * KVH * stride * 4)
-    zeros("ctx", SLOTS * 4)
-    up("pos", np.full(SLOTS, 0xFFFFFFFF, np.uint32))
-    zeros("temp", SLOTS * 4)
-    zeros("topk", SLOTS * 4)
-    zeros("topp", SLOTS * 4)
-    zeros("seed", SLOTS * 8)
-    zeros("step", SLOTS * 8)
-    zeros("out", SLOTS * HID * 2)
-    zeros("out32", SLOTS * HID * 4)
-    zeros("logits", SLOTS * VOCAB * 4)
-    zeros("tok", SLOTS * 4)
-    zeros("lp", SLOTS * 4)
-
-    rr, dr = L.req_ring_create(), L.done_ring_create()
-    assert L.rl_hip_is_coherent_host(rr) and L.rl_hip_is_coherent_host(dr)
-    for r in range(REQ):
-        req = rl.RolloutRequest(request_id=r, max_tokens=GEN, kv_blocks=int(cfg["n_blocks"][r]),
-                                temperature=1.0, top_k=0, top_p=0.9, rng_seed=int(cfg["seeds"][r]))
-        assert req_ring_push(rl, rr, req) == 0
-    assert req_ring_push(rl, rr, rl.RolloutRequest(request_id=2**64 - 1)) == 0
-
-    sched = rl.SchedArgs(req_ring=rr, done_ring=dr, state=dev["state"].ptr, requests=REQ,
-                         prompt_len=dev["prompt"].ptr, req_table=dev["rtab"].ptr, kv_heads=KVH, table_stride=stride,
-                         gen_tokens=dev["gen"].ptr, gen_stride=GEN, targets=dev["targets"].ptr, group_size=GS,
-                         target_len=GEN, rewards=dev["rewards"].ptr, slot_table=dev["stab"].ptr,
-                         slot_ctx=dev["ctx"].ptr, slot_pos=dev["pos"].ptr, slot_temp=dev["temp"].ptr,
-                         slot_topk=dev["topk"].ptr, slot_topp=dev["topp"].ptr, slot_seed=dev["seed"].ptr,
-                         slot_step=dev["step"].ptr, sampled=None, counters=dev["counters"].ptr)
-    layout = rl.KvLayoutDesc.paged(TPB, D)
-    max_ctx = PREFIX + PRIV_MAX + GEN + 1
-    attn = rl.attn_args(dev["arena"], layout, dev["stab"], stride, SLOTS, QH, KVH, rl.DTYPE_BF16, dev["ctx"],
-                        max_ctx, dev["qpool"], dev["out"], dev["out32"])
-    attn_ws = rl.attn_workspace(attn)
-    samp = rl.sample_args(dev["logits"], SLOTS, VOCAB, VOCAB, dev["tok"], dev["lp"])
-    samp.temperature, samp.top_k, samp.top_p = dev["temp"].ptr, dev["topk"].ptr, dev["topp"].ptr
-    samp.seed, samp.steps = dev["seed"].ptr, dev["step"].ptr
-    samp_ws = rl.sample_workspace(samp)
-    app = rl.AppendArgs(arena_base=dev["arena"].ptr, arena_bytes=dev["arena"].nbytes, layout=layout,
-                        block_table=dev["stab"].ptr, table_stride=stride, batch=SLOTS, kv_heads=KVH,
-                        positions=dev["pos"].ptr, cow_src=None)
-    q_row = SLOTS * QH * D * 2
-    kv_row = SLOTS * KVH * D * 2
-
-    dones = []
-    t = 0
-    timed = None
+    loop = grpo.RolloutLoop(cfg)
+    dev = loop.dev
+    assert L.rl_hip_is_coherent_host(loop.rr) and L.rl_hip_is_coherent_host(loop.dr)
+    loop.submit_requests()
     print("[rollout] running the loop", flush=True)
-    while len(dones) < REQ:
-        assert t < 700, ("loop did not finish", len(dones), dev["counters"].download(np.uint32, 4))
-        sched.sampled = dev["tok"].ptr if t > 0 else None
-        rl.check(L.rl_hip_rollout_schedule(C.byref(sched)), "rl_hip_rollout_schedule")
-        attn.q = dev["qpool"].ptr + (t % POOL) * q_row
-        rl.attn_decode(attn)
-        rl.logits_proj(dev["out"], dev["w"], dev["logits"], SLOTS, VOCAB, HID)
-        rl.sample(samp)
-        app.k_new = dev["kpool"].ptr + (t % POOL) * kv_row
-        app.v_new = dev["vpool"].ptr + (t % POOL) * kv_row
-        rl.kv_append(app)
-        if t in CHECK_STEPS:
-            rl.sync()
-            _check_step(rl, orc, olib, cfg, dev, t)
-        if t in (20, 120):             # a window without checkpoints or done polling
-            rl.sync()
-            if t == 20:
-                timed = time.perf_counter()
-            else:
-                timed = (time.perf_counter() - timed) / 100
-        t += 1
-        if t % 32 == 0 and t not in range(20, 121):
-            rl.sync()
-            while (d := done_ring_pop(rl, dr)) is not None:
-                dones.append((d.request_id, d.rollout_id, d.tokens_generated, d.reward, d.status))
-            st = dev["counters"].download(np.uint32, 4)
-            assert st[3] == 0, st
-    # the commit of the last step and the final retirements happen in one more launch
-    rl.check(L.rl_hip_rollout_schedule(C.byref(sched)), "rl_hip_rollout_schedule")
-    rl.sync()
-    while (d := done_ring_pop(rl, dr)) is not None:
-        dones.append((d.request_id, d.rollout_id, d.tokens_generated, d.reward, d.status))
-    print(f"[rollout] {t} steps; steps 20-119 (256 active slots): {timed * 1e6:.0f} us/step, "
-          f"{SLOTS / timed:.0f} tokens/s", flush=True)
+    res = loop.run(check_steps=CHECK_STEPS, on_check=lambda t: _check_step(rl, orc, olib, cfg, dev, t))
+    dones = loop.dones
+    print(f"[rollout] {res['steps']} steps in {res['wall_s']:.2f} s; steps 20-119 (256 active slots): "
+          f"{res['window_us_per_step']:.0f} us/step, {SLOTS / res['window_us_per_step'] * 1e6:.0f} tokens/s",
+          flush=True)
 
     counters = dev["counters"].download(np.uint32, 4)
     assert counters.tolist() == [REQ, REQ, 1, 0], counters
     assert len(dones) == REQ and sorted(d[0] for d in dones) == list(range(REQ))
     assert all(d[2] == GEN and d[4] == 0 and d[1] < SLOTS for d in dones)
-    state = dev["state"].download(np.uint8, 18464)
+    state = dev["state"].download(np.uint8, grpo.STATE_BYTES)
     assert not state[18432:].any()                        # bitmap
     assert not state.reshape(-1)[:256 * 72].reshape(256, 72)[:, :4].any()  # active flags
 
@@ -290,13 +142,13 @@ def test_grpo_rollout_loop(rl, gpu, orc, olib):
     hits = sum(int((gen[r] == cfg["targets"][r // GS]).sum()) for r in range(REQ))
     print(f"[rollout] {REQ} dones, {hits} target hits, mean reward {rew_dev.mean():.4f}", flush=True)
 
+    rr, dr = loop.rr, loop.dr
     assert L.hw_ring_load_acquire(rr) == REQ + 1 and L.hw_ring_load_acquire(rr + 64) == REQ + 1
     assert L.hw_ring_load_acquire(dr) == REQ and L.hw_ring_load_acquire(dr + 64) == REQ
     for b in branch_ids:
         assert L.kv_branch_free(ptab, b) == 0
     assert all(L.kv_prefix_get(ptab, g).contents.refcnt == 1 for g in range(GROUPS))
 
-    for b in list(dev.values()) + [attn_ws, samp_ws, ntok, rew2, adv]:
+    for b in (ntok, rew2, adv):
         b.close()
-    L.req_ring_destroy(rr)
-    L.done_ring_destroy(dr)
+    loop.close()
