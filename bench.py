@@ -505,7 +505,7 @@ def main():
                     help="attention: persistent waves sharing the KV stream (0: library default, a full device)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py: this build runs the decode hot path on one GPU only; multi-GPU runs are not part of it; "
+        print("bench.py: the decode hot path runs on one GPU here; multi-GPU runs are not part of it; "
               "the path shards by rollout, with no exchange inside a decode step.", file=sys.stderr)
         sys.exit(2)
 

@@ -100,6 +100,69 @@ __device__ __forceinline__ float wave_sum_f(float v)
     return v;
 }
 
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kGreedyBatch = 8;  // 16-byte loads in flight per thread
+
+// Folds value v at index i into a running (best, bidx, z): best the max,
+// bidx the lowest index holding it, z the sum of exp(v - best) so far.
+__device__ __forceinline__ void greedy_fold(float v, uint32_t i, float &best, uint32_t &bidx, float &z)
+{
+    if (v > best) {
+        z = (best == -INFINITY ? 0.f : z * __builtin_amdgcn_exp2f((best - v) * kLog2e)) + 1.f;
+        best = v;
+        bidx = i;
+    } else {
+        if (v == best && i < bidx)
+            bidx = i;
+        if (v != -INFINITY)
+            z += __builtin_amdgcn_exp2f((v - best) * kLog2e);
+    }
+}
+
+// One thread's share of a greedy scan over lg[0, n): 16-byte loads of
+// consecutive quads (quad q at thread q % threads) when the row is 16-byte
+// aligned, kGreedyBatch of them issued before any is used (a quad past the
+// end re-reads the last whole quad and is masked, so no load is
+// conditional); scalar loads for the remainder or an unaligned row.
+__device__ void greedy_scan(const float *lg, uint32_t n, uint32_t tid, float &best, uint32_t &bidx, float &z)
+{
+    constexpr uint32_t T = kWorkerThreads;
+    uint32_t done = 0;
+    const uint32_t quads = n / 4;
+    if (((uintptr_t)lg & 15u) == 0 && quads > 0) {
+        const RL_GLOBAL rl_f32x4 *l4 = (const RL_GLOBAL rl_f32x4 *)lg;
+        for (uint32_t q0 = 0; q0 < quads; q0 += T * kGreedyBatch) {
+            rl_f32x4 v[kGreedyBatch];
+#pragma unroll
+            for (int j = 0; j < kGreedyBatch; j++)
+                v[j] = l4[min(q0 + j * T + tid, quads - 1)];
+#pragma unroll
+            for (int j = 0; j < kGreedyBatch; j++) {
+                const uint32_t q = q0 + j * T + tid;
+                if (q >= quads)
+                    v[j] = rl_f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                const uint32_t i = q * 4;
+                greedy_fold(v[j].x, i, best, bidx, z);
+                greedy_fold(v[j].y, i + 1, best, bidx, z);
+                greedy_fold(v[j].z, i + 2, best, bidx, z);
+                greedy_fold(v[j].w, i + 3, best, bidx, z);
+            }
+        }
+        done = quads * 4;
+    }
+    for (uint32_t i0 = done; i0 < n; i0 += T * kGreedyBatch) {
+        float v[kGreedyBatch];
+#pragma unroll
+        for (int j = 0; j < kGreedyBatch; j++)
+            v[j] = lg[min(i0 + j * T + tid, n - 1)];
+#pragma unroll
+        for (int j = 0; j < kGreedyBatch; j++) {
+            const uint32_t i = i0 + j * T + tid;
+            greedy_fold(i < n ? v[j] : -INFINITY, i, best, bidx, z);
+        }
+    }
+}
+
 template <int D, int G, int DT, int TPB>
 __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams wp)
 {
@@ -117,6 +180,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
     __shared__ uint32_t s_ctl;
     __shared__ float s_red[W];
     __shared__ uint32_t s_redi[W];
+    __shared__ float s_z[W];
 
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63;
@@ -223,50 +287,43 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                     merge_row<D, G, DT, kWorkerThreads>(a, 0, g, g * nu, nu, U, NW, false, tid, s_f, s_l, s_L);
             }
 
-            // greedy token (lowest index among maxima) and its logprob
+            // greedy token (lowest index among maxima) and its logprob: one
+            // pass over the logits with kGreedyBatch independent loads in
+            // flight per thread and an online log-sum-exp (per-thread running
+            // max, sum rescaled when the max grows)
             {
                 const float *lg = wp.logits + step_row * wp.vocab;
-                float best = -INFINITY;
+                float best = -INFINITY, z = 0.f;
                 uint32_t bidx = 0xFFFFFFFFu;
-                for (uint32_t i = tid; i < wp.vocab; i += kWorkerThreads) {
-                    const float v = lg[i];
-                    if (v > best || (v == best && i < bidx)) {
-                        best = v;
-                        bidx = i;
-                    }
-                }
-                wave_argmax(best, bidx);
+                greedy_scan(lg, wp.vocab, tid, best, bidx, z);
+                // combine (best, bidx, z) over the workgroup; z is relative to best
+                float m = best;
+                wave_argmax(m, bidx);
+                z = wave_sum_f(best == -INFINITY ? 0.f : z * exp2f((best - m) * kLog2e));
                 if (lane == 0) {
-                    s_red[wave] = best;
+                    s_red[wave] = m;
                     s_redi[wave] = bidx;
+                    s_z[wave] = z;
                 }
                 __syncthreads();
-                float m = s_red[0];
+                float gm = s_red[0];
                 uint32_t mi = s_redi[0];
 #pragma unroll
                 for (int w = 1; w < W; w++)
-                    if (s_red[w] > m || (s_red[w] == m && s_redi[w] < mi)) {
-                        m = s_red[w];
+                    if (s_red[w] > gm || (s_red[w] == gm && s_redi[w] < mi)) {
+                        gm = s_red[w];
                         mi = s_redi[w];
                     }
-                const uint32_t tok = mi >= wp.vocab ? 0u : mi;  // no finite maximum: token 0
-                float z = 0.f;
-                if (m != -INFINITY)
-                    for (uint32_t i = tid; i < wp.vocab; i += kWorkerThreads)
-                        z += expf(lg[i] - m);
-                z = wave_sum_f(z);
-                __syncthreads();
-                if (lane == 0)
-                    s_red[wave] = z;
-                __syncthreads();
                 if (tid == 0) {
                     float zs = 0.f;
 #pragma unroll
                     for (int w = 0; w < W; w++)
-                        zs += s_red[w];
+                        zs += s_red[w] == -INFINITY ? 0.f : s_z[w] * exp2f((s_red[w] - gm) * kLog2e);
+                    const uint32_t tok = mi >= wp.vocab ? 0u : mi;  // no finite maximum: token 0
                     wp.token_out[step_row] = tok;
-                    wp.logprob_out[step_row] = lg[tok] - (m + logf(zs));
+                    wp.logprob_out[step_row] = lg[tok] - (gm + logf(zs));
                 }
+                __syncthreads();  // s_red is reused by the next step
             }
 
             // append the step's K and V token at position pos

@@ -1,15 +1,15 @@
 // logits_proj.hip - the dense hidden-to-vocab logits projection on gfx950:
 // logits[M][N] (fp32) = X[M][K] (bf16) . W[N][K]^T (bf16), fp32 accumulate.
 //
-// No reference kernel exists (SURVEY row a20); the nearest analog is the
+// No reference kernel exists; the nearest analog is the
 // fp16 GEMV query_prepare_kernel (cu/query_producer.cu:5-26). W is stored
 // like an lm_head weight, one row of K per vocabulary entry, so both
 // operands are K-contiguous.
 //
 //  tiles   128 x 128 output tile per 256-thread workgroup, K in steps of 64;
 //          the four waves each own 64 x 64 (4 x 4 MFMA blocks of 16 x 16).
-//          Workgroups are ordered M-fastest, so the M tiles sharing a W tile
-//          run together and W streams from HBM about once.
+//          The M tiles sharing a W tile run together on one XCD, so W
+//          streams from HBM about once.
 //  staging the X and W tiles of a K step (16 KiB each) are copied HBM -> LDS
 //          with global_load_lds_dwordx4, double-buffered; 16-byte chunk c of
 //          row r lands at chunk position c ^ (r & 7) (lanes fetch permuted
@@ -38,8 +38,14 @@ struct ProjParams {
     const uint16_t *w;  // [N][ldw]
     float *out;         // [M][ldo]
     uint32_t M, N, K, ldx, ldw, ldo;
-    uint32_t m_tiles;
+    uint32_t m_tiles, n_tiles;
 };
+
+// Workgroups are dispatched to the 8 XCDs round-robin (workgroup b on XCD
+// b % 8), each XCD with its own L2. The M tiles of one N tile (which share
+// the 128-row W tile) are given consecutive workgroups of one XCD, so they
+// run side by side behind one L2 and W leaves HBM about once.
+constexpr uint32_t kXcds = 8;
 
 // Copies rows [row0, row0 + 128) x k [k0, k0 + 64) of a K-contiguous
 // operand into an LDS tile, this wave's share of the 16 copies. Rows past
@@ -71,8 +77,11 @@ __global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t mt = blockIdx.x % p.m_tiles;
-    const uint32_t nt = blockIdx.x / p.m_tiles;
+    const uint32_t xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+    const uint32_t mt = local % p.m_tiles;
+    const uint32_t nt = xcd + kXcds * (local / p.m_tiles);
+    if (nt >= p.n_tiles)
+        return;
     const uint32_t m0 = mt * BM, n0 = nt * BN;
     const int wm = wave & 1, wn = wave >> 1;
 
@@ -175,8 +184,8 @@ extern "C" int rl_hip_logits_proj(const rl_logits_proj_args_t *a)
     p.ldw = a->w_stride;
     p.ldo = a->logits_stride;
     p.m_tiles = (a->rows + BM - 1) / BM;
-    const uint64_t n_tiles = (a->vocab + BN - 1) / BN;
-    const uint64_t grid = n_tiles * p.m_tiles;
+    p.n_tiles = (a->vocab + BN - 1) / BN;
+    const uint64_t grid = (uint64_t)(p.n_tiles + kXcds - 1) / kXcds * kXcds * p.m_tiles;
     if (grid > 0x7FFFFFFFull) {
         rl_set_error("rl_hip_logits_proj: %llu workgroups", (unsigned long long)grid);
         return -1;

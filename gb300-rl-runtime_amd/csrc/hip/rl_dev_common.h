@@ -11,6 +11,7 @@ typedef uint32_t rl_u32x4 __attribute__((ext_vector_type(4)));
 typedef float rl_f32x4 __attribute__((ext_vector_type(4)));
 
 #define RL_LDS __attribute__((address_space(3)))
+#define RL_GLOBAL __attribute__((address_space(1)))
 #define RL_CONST __attribute__((address_space(4)))
 
 // Load through the constant address space: memory the kernel never writes,

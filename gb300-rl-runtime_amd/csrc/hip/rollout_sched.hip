@@ -10,13 +10,18 @@
 //  retire  slots with tokens_generated >= max_tokens get their reward - the
 //          reference rule (count & 0xFF) / 255 applied to the number of
 //          generated tokens equal to the group's target at the same position
-//          - and thread 0 pushes their RolloutDone records in slot order to
-//          the done ring (coherent host memory, system-scope release), then
-//          frees the slots;
-//  admit   thread 0 consumes requests while a slot is free, each into the
-//          lowest free slot (slot fields seeded as in the reference). Unlike
-//          the reference, a request is never consumed without a free slot,
-//          so none is dropped. request_id UINT64_MAX marks the end;
+//          - and write their RolloutDone records in parallel, slot s at
+//          done-ring position tail + (retiring slots below s), so the ring
+//          holds them in slot order; after a barrier thread 0 publishes the
+//          new tail with one system-scope release (coherent host memory) and
+//          the slots are freed;
+//  admit   the free slots (after retirement) are ranked in slot order;
+//          threads read up to that many requests from the ring in parallel,
+//          thread 0 stops at the end marker (request_id UINT64_MAX) or a bad
+//          id and publishes the new head, and the i-th request goes to the
+//          i-th free slot - the lowest free slot first, as in the reference,
+//          whose seeding of the slot fields is kept. Unlike the reference, a
+//          request is never consumed without a free slot, so none is dropped;
 //  prepare every slot writes the next step's arguments: attention context and
 //          append position (prompt tokens + generated tokens), sampler
 //          temperature / top-k / top-p / seed / step (temperature 0 for an
@@ -27,6 +32,7 @@
 #include <stdint.h>
 
 #include "request.h"
+#include "rl_dev_common.h"
 #include "rl_hip.h"
 #include "rl_hip_internal.h"
 
@@ -61,14 +67,36 @@ __device__ RolloutRequest read_request(const RolloutRequest *src)
     return u.r;
 }
 
+// Exclusive prefix of v over the workgroup in thread order; total in `total`.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t &total, uint32_t *s_w)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t incl = rl_wave_incl_scan_u32(v);
+    if (lane == 63)
+        s_w[wave] = incl;
+    __syncthreads();
+    uint32_t base = 0, t = 0;
+#pragma unroll
+    for (int w = 0; w < kSlots / 64; w++) {
+        base += w < wave ? s_w[w] : 0u;
+        t += s_w[w];
+    }
+    __syncthreads();
+    total = t;
+    return base + incl - v;
+}
+
 __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sched_args_t p)
 {
-    __shared__ uint32_t s_retire[kSlots];
-    __shared__ float s_reward[kSlots];
-    __shared__ uint32_t s_admit[kSlots];  // request index admitted into the slot this launch, or ~0
+    __shared__ uint32_t s_w[kSlots / 64];
+    __shared__ uint32_t s_ctl[4];
+    __shared__ uint32_t s_admit[kSlots];           // request index admitted into the slot this launch, or ~0
+    __shared__ RolloutRequest s_req[kSlots];       // requests read from the ring this launch, in ring order
     const uint32_t s = threadIdx.x;
+    const int lane = s & 63, wave = s >> 6;
     GpuRolloutSlot *slot = &p.state->slots[s];
     const uint32_t row_entries = p.kv_heads * p.table_stride;
+    const uint32_t status0 = p.counters[3];
 
     // ---- commit the last step's token ------------------------------------
     uint32_t active = slot->active;
@@ -80,10 +108,10 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
         slot->tokens_generated = t + 1;
     }
 
-    // ---- retire ----------------------------------------------------------------
-    bool retire = false;
-    if (active && slot->tokens_generated >= slot->max_tokens) {
-        retire = true;
+    // ---- retire: reward, then the dones in slot order -------------------------
+    const bool retire = status0 == kOk && active && slot->tokens_generated >= slot->max_tokens;
+    float reward = 0.f;
+    if (retire) {
         const uint32_t req = slot->request_id;
         uint32_t count = 0;
         if (req < p.requests) {
@@ -93,93 +121,116 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
             for (uint32_t i = 0; i < n; i++)
                 count += tok[i] == tgt[i] ? 1u : 0u;
         }
-        s_reward[s] = (float)(count & 0xFFu) / 255.0f;
+        reward = (float)(count & 0xFFu) / 255.0f;
     }
-    s_retire[s] = retire ? 1u : 0u;
-    s_admit[s] = 0xFFFFFFFFu;
-    __syncthreads();
-
+    uint32_t n_ret;
+    const uint32_t rank = block_excl_scan(retire ? 1u : 0u, n_ret, s_w);
+    DoneRing *dr = p.done_ring;
     if (s == 0) {
-        uint32_t status = p.counters[3];
-        // dones, in slot order
-        DoneRing *dr = p.done_ring;
-        uint32_t dtail = sys_load(&dr->prod.tail);
-        for (uint32_t i = 0; i < (uint32_t)kSlots && status == kOk; i++) {
-            if (!s_retire[i])
-                continue;
-            GpuRolloutSlot *rs = &p.state->slots[i];
-            uint64_t spin = 0;
-            while (dtail - sys_load(&dr->cons.head) >= (uint32_t)REQUEST_RING_SIZE) {
-                if (++spin > p.max_spin) {
-                    status = kDoneFull;
-                    break;
-                }
+        uint32_t status = status0;
+        const uint32_t dtail = n_ret ? sys_load(&dr->prod.tail) : 0u;
+        uint64_t spin = 0;
+        while (n_ret && status == kOk && dtail - sys_load(&dr->cons.head) > (uint32_t)REQUEST_RING_SIZE - n_ret) {
+            if (++spin > p.max_spin)
+                status = kDoneFull;
+            else
                 __builtin_amdgcn_s_sleep(8);
-            }
-            if (status != kOk)
-                break;
-            volatile uint32_t *dst = (volatile uint32_t *)&dr->slots[dtail & (REQUEST_RING_SIZE - 1)];
-            const uint32_t req = rs->request_id;
-            dst[0] = req;  // request_id (low 32 bits kept by the slot, as in the reference)
-            dst[1] = 0;
-            dst[2] = i;    // rollout_id = slot
-            dst[3] = rs->tokens_generated;
-            dst[4] = __float_as_uint(s_reward[i]);
-            dst[5] = 0;    // status
-            dtail++;
-            sys_store_release(&dr->prod.tail, dtail);
-            if (req < p.requests)
-                p.rewards[req] = s_reward[i];
-            rs->active = 0;
-            p.state->bitmap[i / 64] &= ~(1ull << (i % 64));
-            p.counters[0]++;
         }
-        // admissions
-        RequestRing *rr = p.req_ring;
-        uint32_t head = sys_load(&rr->cons.head);
-        while (status == kOk && p.counters[2] == 0) {
-            int free_slot = -1;
-            for (int w = 0; w < kSlots / 64 && free_slot < 0; w++) {
-                const uint64_t bits = ~p.state->bitmap[w];
-                if (bits)
-                    free_slot = w * 64 + __ffsll((long long)bits) - 1;
-            }
-            if (free_slot < 0)
-                break;
-            if (sys_load(&rr->prod.tail) == head)
-                break;
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-            const RolloutRequest req = read_request(&rr->slots[head & (REQUEST_RING_SIZE - 1)]);
-            head++;
-            sys_store_release(&rr->cons.head, head);
-            if (req.request_id == ~0ull) {
-                p.counters[2] = 1;
-                break;
-            }
-            const uint32_t rid = (uint32_t)(req.request_id & 0xFFFFFFFFu);
-            if (rid >= p.requests) {
-                status = kBadRequest;
-                break;
-            }
-            GpuRolloutSlot *rs = &p.state->slots[free_slot];
-            rs->active = 1;
-            rs->request_id = rid;
-            rs->tokens_generated = 0;
-            rs->max_tokens = req.max_tokens;
-            rs->kv_blocks = req.kv_blocks;
-            rs->rng_state[0] = req.rng_seed;
-            rs->rng_state[1] = req.rng_seed ^ 0x9e3779b97f4a7c15ull;
-            rs->rng_state[2] = (req.rng_seed << 17) ^ 0x3c6ef372fe94f82aull;
-            rs->rng_state[3] = ~req.rng_seed;
-            rs->temperature = req.temperature;
-            rs->top_k = req.top_k;
-            rs->top_p = req.top_p;
-            p.state->bitmap[free_slot / 64] |= 1ull << (free_slot % 64);
-            s_admit[free_slot] = rid;
-            p.counters[1]++;
-        }
-        p.counters[3] = status;
+        s_ctl[0] = dtail;
+        s_ctl[1] = status;
     }
+    __syncthreads();
+    const uint32_t dtail = s_ctl[0];
+    const bool pushed = retire && s_ctl[1] == kOk;
+    if (pushed) {
+        volatile uint32_t *dst = (volatile uint32_t *)&dr->slots[(dtail + rank) & (REQUEST_RING_SIZE - 1)];
+        const uint32_t req = slot->request_id;
+        dst[0] = req;  // request_id (the slot keeps its low 32 bits, as in the reference)
+        dst[1] = 0;
+        dst[2] = s;    // rollout_id = slot
+        dst[3] = slot->tokens_generated;
+        dst[4] = __float_as_uint(reward);
+        dst[5] = 0;    // status
+        if (req < p.requests)
+            p.rewards[req] = reward;
+        slot->active = 0;
+    }
+    const uint64_t freed = __ballot(pushed);  // wave w owns bitmap word w
+    if (lane == 0 && freed)
+        p.state->bitmap[wave] &= ~freed;
+    __syncthreads();  // every record is written before the tail moves
+    if (s == 0 && s_ctl[1] == kOk && n_ret) {
+        sys_store_release(&dr->prod.tail, dtail + n_ret);
+        p.counters[0] += n_ret;
+    }
+
+    // ---- admit: requests in ring order into the free slots in slot order ------
+    const bool is_free = s_ctl[1] == kOk && p.counters[2] == 0 &&
+                         ((p.state->bitmap[wave] >> lane) & 1ull) == 0;
+    uint32_t n_free;
+    const uint32_t frank = block_excl_scan(is_free ? 1u : 0u, n_free, s_w);
+    RequestRing *rr = p.req_ring;
+    if (s == 0) {
+        uint32_t head = 0, n_try = 0;
+        if (n_free) {
+            head = sys_load(&rr->cons.head);
+            n_try = min(n_free, sys_load(&rr->prod.tail) - head);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        }
+        s_ctl[2] = head;
+        s_ctl[3] = n_try;
+    }
+    __syncthreads();
+    const uint32_t head = s_ctl[2], n_try = s_ctl[3];
+    if (s < n_try)
+        s_req[s] = read_request(&rr->slots[(head + s) & (REQUEST_RING_SIZE - 1)]);
+    __syncthreads();
+    if (s == 0) {
+        uint32_t status = s_ctl[1], n_adm = 0, used = 0;
+        for (; used < n_try; used++) {
+            const RolloutRequest &q = s_req[used];
+            if (q.request_id == ~0ull) {
+                p.counters[2] = 1;
+                used++;
+                break;
+            }
+            if ((uint32_t)(q.request_id & 0xFFFFFFFFu) >= p.requests) {
+                status = kBadRequest;
+                used++;
+                break;
+            }
+            n_adm++;
+        }
+        if (used)
+            sys_store_release(&rr->cons.head, head + used);
+        p.counters[1] += n_adm;
+        p.counters[3] = status;
+        s_ctl[3] = n_adm;
+    }
+    __syncthreads();
+    const uint32_t n_adm = s_ctl[3];
+    const bool admit = is_free && frank < n_adm;
+    s_admit[s] = 0xFFFFFFFFu;
+    if (admit) {
+        const RolloutRequest &q = s_req[frank];
+        const uint32_t rid = (uint32_t)(q.request_id & 0xFFFFFFFFu);
+        slot->active = 1;
+        slot->request_id = rid;
+        slot->tokens_generated = 0;
+        slot->max_tokens = q.max_tokens;
+        slot->kv_blocks = q.kv_blocks;
+        slot->rng_state[0] = q.rng_seed;
+        slot->rng_state[1] = q.rng_seed ^ 0x9e3779b97f4a7c15ull;
+        slot->rng_state[2] = (q.rng_seed << 17) ^ 0x3c6ef372fe94f82aull;
+        slot->rng_state[3] = ~q.rng_seed;
+        slot->temperature = q.temperature;
+        slot->top_k = q.top_k;
+        slot->top_p = q.top_p;
+        s_admit[s] = rid;
+    }
+    const uint64_t taken = __ballot(admit);
+    if (lane == 0 && taken)
+        p.state->bitmap[wave] |= taken;
     __syncthreads();
 
     // ---- block-table rows of the slots admitted now ---------------------------

@@ -165,21 +165,24 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
 
     // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
+    // Every load is issued unconditionally (a quad past the end re-reads the
+    // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
+    // masked afterwards, so all eight are in flight together.
     float x[kPerThread];
+    const uint32_t last_quad = (p.vocab - 1) & ~3u;
+    rl_f32x4 raw[kPerThread / 4];
 #pragma unroll
     for (int k = 0; k < kPerThread / 4; k++) {
         const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
-        if (col + 3 < p.vocab) {
-            const rl_f32x4 v = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + col));
-            x[k * 4 + 0] = v.x;
-            x[k * 4 + 1] = v.y;
-            x[k * 4 + 2] = v.z;
-            x[k * 4 + 3] = v.w;
-        } else {
+        raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
+    }
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                x[k * 4 + e] = (col + e < p.vocab) ? lrow[col + e] : -INFINITY;
-        }
+    for (int k = 0; k < kPerThread / 4; k++) {
+        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
+        x[k * 4 + 0] = col + 0 < p.vocab ? raw[k].x : -INFINITY;
+        x[k * 4 + 1] = col + 1 < p.vocab ? raw[k].y : -INFINITY;
+        x[k * 4 + 2] = col + 2 < p.vocab ? raw[k].z : -INFINITY;
+        x[k * 4 + 3] = col + 3 < p.vocab ? raw[k].w : -INFINITY;
     }
 
     SplitStat *st = p.stats + (size_t)row * p.splits + split;
@@ -319,7 +322,7 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
 
 // ---- block-wide helpers of the merge (256 threads = 4 waves) ----------------
 
-constexpr int kMergeThreads = 256;
+constexpr int kMergeThreads = 512;  // 8 waves: two per SIMD hide each other's latency
 constexpr int kMergeWaves = kMergeThreads / 64;
 
 __device__ __forceinline__ uint64_t wave_inclusive_scan_u64(uint64_t v)
@@ -355,6 +358,8 @@ struct BlockShared {
     uint32_t w32[kMergeWaves];
     unsigned long long sel64;
     uint32_t n;
+    unsigned long long res64[2];  // results published by one thread (whole-row path)
+    uint32_t cnt[2];              // LDS list counters (whole-row path)
 };
 
 // Exclusive prefix over the block in thread order; `total` gets the block sum.
@@ -415,17 +420,18 @@ __device__ uint32_t block_max_u32(uint32_t v, BlockShared &bs)
 }
 
 // One digit of an MSB-first radix search over a 256-bin histogram (thread t
-// passes bin 255 - t): the highest digit d in [1, 255] for which
-// above + sum(bins >= d) reaches need, else 0. `acc` receives
+// < 256 passes bin 255 - t, the others 0): the highest digit d in [1, 255]
+// for which above + sum(bins >= d) reaches need, else 0. `acc` receives
 // above + sum(bins > d), the amount ranked strictly above the chosen digit.
 __device__ uint32_t block_pick_digit(uint64_t h, uint64_t above, uint64_t need, uint64_t &acc, BlockShared &bs)
 {
-    const uint32_t r = 255u - threadIdx.x;
+    const bool has_bin = threadIdx.x < 256u;
+    const uint32_t r = has_bin ? 255u - threadIdx.x : 0u;
     uint64_t total;
     const uint64_t S = block_excl_scan_u64(h, total, bs);  // bins > r
-    const bool cross = r >= 1u && above + S < need && above + S + h >= need;
+    const bool cross = has_bin && r >= 1u && above + S < need && above + S + h >= need;
     const uint32_t d = block_max_u32(cross ? r : 0u, bs);
-    if (r == d)
+    if (has_bin && r == d)
         bs.sel64 = above + S;
     __syncthreads();
     acc = bs.sel64;
@@ -436,65 +442,173 @@ __device__ uint32_t block_pick_digit(uint64_t h, uint64_t above, uint64_t need, 
 // ---- exact full-row path -----------------------------------------------------
 // Used for rows without top-k (whole-vocabulary nucleus) and for rows whose
 // top-k candidates overflow the slice buffers (massive ties). Streams the row
-// from global memory (L2-resident after the first pass) several times:
-// radix select of the top-k cutoff on the float keys; the kept weight W_K; the
-// nucleus boundary as an exact 64-bit composite key (float key, ~index) found
-// by MSB-first radix search on weight histograms; W_P; the ascending-index
-// integer CDF walk.
+// (L2-resident after the split kernel) twice. Wave w takes the rounds
+// r = w, w + 8, ... of 256 consecutive elements, lane l the 4 elements
+// [256 r + 4 l, 256 r + 4 l + 4), so every load instruction reads 1 KiB of
+// consecutive logits; each wave keeps kRoundBatch rounds' loads in flight and
+// the per-element code is branch-free (rl_sample_weight_nb).
+//   cutoff  top-k only: radix select of the k-th largest float key.
+//   pass A  integer weights w = rl_sample_weight(x - max) of the kept
+//           elements, summed (W_K) and, for a nucleus, summed per bin of
+//           d = max - x (4096 bins over [0, 17): a monotone map, so the bins
+//           hold contiguous runs of the (x desc, index asc) order; weights
+//           vanish below d = 16.7).
+//   bin     the first bin where the cumulative weight reaches
+//           thr = ceil(p W_K) holds the nucleus boundary.
+//   pass B  each round's weight in the bins wholly inside the nucleus, and
+//           the boundary bin's elements (composite key (float key, ~index),
+//           weight) gathered into LDS.
+//   tau     the boundary bin is split into 4096 sub-bins (again monotone);
+//           the elements of the sub-bin where thr is reached are compared
+//           pairwise: the boundary element is the one whose strictly-higher
+//           weight plus the weight above its sub-bin is below thr while
+//           adding its own reaches it. The boundary bin's members join
+//           their rounds' weights.
+//   walk    the round where the cumulative weight first exceeds the draw u,
+//           then the element inside it, with one wave scan.
+// More than kBinCap elements in the boundary bin or kSubCap in its sub-bin
+// (massive ties) take the radix fallback: an exact 64-bit radix search on
+// weight histograms.
+constexpr int kBins = 4096;
+constexpr float kBinSpan = 17.0f;               // d in [0, 17): w(d) = 0 beyond 16.7
+constexpr int kBinCap = 1024;
+constexpr int kSubCap = 240;
+constexpr int kMaxRounds = 64 * kSplitLen / 256;  // rounds of the largest vocabulary
+
+struct RowScratch {
+    unsigned long long hist[kBins];       // bin weights, then the boundary bin's sub-bin weights
+    unsigned long long rounds[kMaxRounds];
+    unsigned long long bkey[kBinCap];     // the boundary bin: composite keys and weights
+    uint32_t bw[kBinCap];
+    unsigned long long skey[kSubCap];     // the boundary sub-bin
+    uint32_t sw[kSubCap];
+};
+
 __device__ __forceinline__ uint64_t composite_key(uint32_t key, uint32_t idx)
 {
     return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - idx);
 }
 
-__device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff, float topp,
-                                     float m, uint32_t *s_hist, unsigned long long *s_whist, BlockShared &bs)
+__device__ __forceinline__ float dist_t(float m, float x)
+{
+    return (m - x) * ((float)kBins / kBinSpan);
+}
+
+__device__ __forceinline__ uint32_t dist_bin(float m, float x)
+{
+    const float b = dist_t(m, x);
+    return b < (float)(kBins - 1) ? (uint32_t)b : (uint32_t)(kBins - 1);
+}
+
+// Sub-bin (1/kBins of a bin) of an element of bin b: monotone in x like the
+// bin itself, since t - b and the scaling by a power of two are monotone.
+__device__ __forceinline__ uint32_t dist_sub(float m, float x, uint32_t b)
+{
+    const float f = (dist_t(m, x) - (float)b) * (float)kBins;
+    return f < (float)(kBins - 1) ? (uint32_t)f : (uint32_t)(kBins - 1);
+}
+
+// Appends (key, w) to an LDS list for every lane with `take`, one atomic per
+// wave; returns the list position of this lane's entry.
+__device__ __forceinline__ uint32_t wave_append(bool take, uint32_t *counter)
+{
+    const uint64_t bal = __ballot(take);
+    if (!bal)
+        return 0;
+    const int first = (int)__ffsll((long long)bal) - 1;
+    uint32_t base = 0;
+    if ((int)(threadIdx.x & 63) == first)
+        base = atomicAdd(counter, (uint32_t)__popcll(bal));
+    base = (uint32_t)__builtin_amdgcn_readlane((int)base, first);
+    return base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+}
+
+// 4 consecutive logits from index i (i % 4 == 0), -inf past the end. The
+// load itself is unconditional - past the end it re-reads the row's last
+// quad, inside the row since row_stride % 4 == 0 - so a batch of them can
+// be in flight together.
+__device__ __forceinline__ rl_f32x4 load_quad(const float *l, uint32_t i, uint32_t V)
+{
+    const rl_f32x4 r = *(const RL_GLOBAL rl_f32x4 *)(l + min(i, (V - 1) & ~3u));
+    rl_f32x4 v;
+    v.x = i < V ? r.x : -INFINITY;
+    v.y = i + 1 < V ? r.y : -INFINITY;
+    v.z = i + 2 < V ? r.z : -INFINITY;
+    v.w = i + 3 < V ? r.w : -INFINITY;
+    return v;
+}
+
+__device__ __forceinline__ float quad_at(const rl_f32x4 &v, int e)
+{
+    return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+}
+
+// Calls f(r, i0, quad) for this wave's rounds r (i0 = 256 r + 4 lane, the
+// lane's first index), with the loads of kRoundBatch rounds issued before
+// any of them is used: one row pass has that many loads in flight per wave.
+constexpr int kRoundBatch = 8;
+
+template <class F>
+__device__ __forceinline__ void for_rounds(const float *l, uint32_t V, uint32_t R, int wave, int lane, F &&f)
+{
+    for (uint32_t r0 = wave; r0 < R; r0 += kMergeWaves * kRoundBatch) {
+        rl_f32x4 v[kRoundBatch];
+#pragma unroll
+        for (int j = 0; j < kRoundBatch; j++)
+            v[j] = load_quad(l, (r0 + j * kMergeWaves) * 256 + lane * 4, V);
+#pragma unroll
+        for (int j = 0; j < kRoundBatch; j++) {
+            const uint32_t r = r0 + j * kMergeWaves;
+            if (r < R)
+                f(r, r * 256 + lane * 4, v[j]);
+        }
+    }
+}
+
+// k_eff-th largest finite x (multiplicity counted) as a float key; 0 keeps all.
+__device__ uint32_t row_topk_cutoff(const float *l, uint32_t V, float inv_t, uint32_t k_eff, uint32_t *s_hist,
+                                    BlockShared &bs)
 {
     const uint32_t tid = threadIdx.x;
-    const float *l = p.logits + (size_t)row * p.row_stride;
-    const uint32_t V = p.vocab;
-
-    // (1) cutoff key: k_eff-th largest finite x (multiplicity counted); 0 keeps all.
-    uint32_t cutoff = 0;
-    if (k_eff) {
-        uint32_t prefix = 0, mask = 0;
-        uint64_t need = k_eff;
-        for (int pass = 3; pass >= 0; pass--) {
-            const int shift = pass * 8;
+    uint32_t prefix = 0, mask = 0;
+    uint64_t need = k_eff;
+    for (int pass = 3; pass >= 0; pass--) {
+        const int shift = pass * 8;
+        if (tid < 256)
             s_hist[tid] = 0;
-            __syncthreads();
-            for (uint32_t i = tid; i < V; i += kMergeThreads) {
-                const float x = l[i] * inv_t;
-                const uint32_t key = rl_float_key(x);
-                if (x != -INFINITY && (key & mask) == prefix)
-                    atomicAdd(&s_hist[(key >> shift) & 0xFFu], 1u);
-            }
-            __syncthreads();
-            uint64_t acc;
-            const uint32_t d = block_pick_digit(s_hist[255 - tid], 0, need, acc, bs);
-            prefix |= d << shift;
-            mask |= 0xFFu << shift;
-            need -= acc;
+        __syncthreads();
+        for (uint32_t i = tid; i < V; i += kMergeThreads) {
+            const float x = l[i] * inv_t;
+            const uint32_t key = rl_float_key(x);
+            if (x != -INFINITY && (key & mask) == prefix)
+                atomicAdd(&s_hist[(key >> shift) & 0xFFu], 1u);
         }
-        cutoff = prefix;
+        __syncthreads();
+        uint64_t acc;
+        const uint32_t d = block_pick_digit(tid < 256 ? s_hist[255 - tid] : 0u, 0, need, acc, bs);
+        prefix |= d << shift;
+        mask |= 0xFFu << shift;
+        need -= acc;
     }
+    return prefix;
+}
 
-    // (2) W_K
-    uint64_t wk_own = 0;
-    for (uint32_t i = tid; i < V; i += kMergeThreads) {
-        const float x = l[i] * inv_t;
-        if (x != -INFINITY && rl_float_key(x) >= cutoff)
-            wk_own += rl_sample_weight(x - m);
-    }
-    const uint64_t wk = block_sum_u64(wk_own, bs);
-
-    // (3) nucleus boundary tau: the largest composite key whose suffix weight reaches thr.
+// The radix fallback: nucleus boundary tau as the largest composite key whose
+// suffix weight reaches thr (8 passes of 8-bit digits), then W_P and the
+// ascending-index walk in chunks of 256 threads x 8 elements.
+__device__ uint32_t radix_row_sample(const SampleParams &p, uint32_t row, const float *l, float inv_t, uint32_t cutoff,
+                                     float topp, float m, uint64_t wk, unsigned long long *s_whist, BlockShared &bs)
+{
+    const uint32_t tid = threadIdx.x;
+    const uint32_t V = p.vocab;
     uint64_t tau = 0;
     if (topp > 0.f && topp < 1.f) {
         const uint64_t thr = rl_topp_threshold(topp, wk);
         uint64_t prefix = 0, mask = 0, above = 0;
         for (int pass = 7; pass >= 0; pass--) {
             const int shift = pass * 8;
-            s_whist[tid] = 0;
+            if (tid < 256)
+                s_whist[tid] = 0;
             __syncthreads();
             for (uint32_t i = tid; i < V; i += kMergeThreads) {
                 const float x = l[i] * inv_t;
@@ -508,7 +622,7 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
             __syncthreads();
             // (thr >= 1 whenever K is non-empty: the row maximum weighs 2^24)
             uint64_t acc;
-            const uint32_t d = block_pick_digit(s_whist[255 - tid], above, thr, acc, bs);
+            const uint32_t d = block_pick_digit(tid < 256 ? s_whist[255 - tid] : 0ull, above, thr, acc, bs);
             prefix |= (uint64_t)d << shift;
             mask |= 0xFFull << shift;
             above = acc;
@@ -516,7 +630,6 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
         tau = prefix;
     }
 
-    // (4) W_P and the lowest index of P
     uint64_t wp_own = 0;
     uint32_t lowest = 0xFFFFFFFFu;
     for (uint32_t i = tid; i < V; i += kMergeThreads) {
@@ -530,7 +643,6 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
     const uint64_t wp = block_sum_u64(wp_own, bs);
     lowest = block_min_u32(lowest, bs);
 
-    // (5) ascending-index walk: chunks of 256 threads x 8 contiguous elements
     const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
     uint64_t carry = 0;
     uint32_t tok = 0xFFFFFFFFu;
@@ -570,6 +682,226 @@ __device__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float 
     return tok;
 }
 
+__device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff, float topp,
+                                     float m, RowScratch &rs, uint32_t *s_hist, unsigned long long *s_whist,
+                                     BlockShared &bs)
+{
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const float *l = p.logits + (size_t)row * p.row_stride;
+    const uint32_t V = p.vocab;
+    const uint32_t R = (V + 255) / 256;  // rounds
+    const bool trunc = topp > 0.f && topp < 1.f;
+
+    const uint32_t cutoff = k_eff ? row_topk_cutoff(l, V, inv_t, k_eff, s_hist, bs) : 0u;
+
+    // ---- pass A: W_K and the per-bin weights --------------------------------
+    if (trunc)
+        for (uint32_t b = tid; b < (uint32_t)kBins; b += kMergeThreads)
+            rs.hist[b] = 0;
+    __syncthreads();
+    uint64_t wk_own = 0;
+    for_rounds(l, V, R, wave, lane, [&](uint32_t, uint32_t, const rl_f32x4 &v) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x = quad_at(v, e) * inv_t;  // -inf weighs 0
+            const uint32_t wx = rl_sample_weight_nb(x - m);
+            const uint32_t w = rl_float_key(x) >= cutoff ? wx : 0u;
+            wk_own += w;
+            if (trunc && w)
+                atomicAdd(&rs.hist[dist_bin(m, x)], (unsigned long long)w);
+        }
+    });
+    const uint64_t wk = block_sum_u64(wk_own, bs);  // (synchronises: the histogram is complete)
+    if (wk == 0)
+        return 0;  // no finite logit at or above the cutoff: token 0
+
+    // ---- nucleus boundary bin --------------------------------------------------
+    uint32_t bstar = kBins;   // bins below bstar are wholly in P; kBins: no truncation
+    uint64_t thr = 0, above = 0;
+    constexpr int per = kBins / kMergeThreads;
+    if (trunc) {
+        thr = rl_topp_threshold(topp, wk);
+        uint64_t own = 0;
+#pragma unroll
+        for (int j = 0; j < per; j++)
+            own += rs.hist[tid * per + j];
+        uint64_t total;
+        const uint64_t excl = block_excl_scan_u64(own, total, bs);
+        if (excl < thr && excl + own >= thr) {  // exactly one thread
+            uint64_t c = excl;
+            uint32_t b = tid * per;
+            while (c + rs.hist[b] < thr) {
+                c += rs.hist[b];
+                b++;
+            }
+            bs.n = b;
+            bs.sel64 = c;
+        }
+        if (tid == 0) {
+            bs.cnt[0] = 0;
+            bs.cnt[1] = 0;
+        }
+        __syncthreads();
+        bstar = bs.n;
+        above = bs.sel64;
+        for (uint32_t b = tid; b < (uint32_t)kBins; b += kMergeThreads)
+            rs.hist[b] = 0;  // reused for the sub-bins
+    }
+
+    // ---- pass B: each round's weight in the bins wholly in P; the boundary
+    // bin's elements, gathered with their indices --------------------------------
+    for_rounds(l, V, R, wave, lane, [&](uint32_t r, uint32_t i0, const rl_f32x4 &v) {
+        uint32_t s = 0;  // at most 4 x 2^24
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x = quad_at(v, e) * inv_t;  // -inf weighs 0
+            const uint32_t key = rl_float_key(x);
+            const uint32_t b = trunc ? dist_bin(m, x) : 0u;
+            const uint32_t w = rl_sample_weight_nb(x - m);
+            const bool ok = key >= cutoff;
+            s += ok && b < bstar ? w : 0u;
+            const bool edge = ok && b == bstar && w != 0;
+            const uint32_t pos = wave_append(edge, &bs.cnt[0]);
+            if (edge && pos < (uint32_t)kBinCap) {
+                rs.bkey[pos] = composite_key(key, i0 + e);
+                rs.bw[pos] = w;
+            }
+        }
+        // the wave sum can reach 2^32: two DPP sums of 24-bit and 8-bit parts
+        const uint32_t hi = rl_wave_sum_u32(s >> 8), lo = rl_wave_sum_u32(s & 0xFFu);
+        if (lane == 0)
+            rs.rounds[r] = ((uint64_t)hi << 8) + lo;
+    });
+    __syncthreads();
+
+    uint64_t tau = 0, wp = wk;
+    if (trunc) {
+        const uint32_t nb = bs.cnt[0];
+        if (nb > (uint32_t)kBinCap)
+            return radix_row_sample(p, row, l, inv_t, cutoff, topp, m, wk, s_whist, bs);
+
+        // ---- the boundary bin's sub-bins: the one where thr is reached ----------
+        for (uint32_t e = tid; e < nb; e += kMergeThreads) {
+            const float x = rl_key_float((uint32_t)(rs.bkey[e] >> 32));
+            atomicAdd(&rs.hist[dist_sub(m, x, bstar)], (unsigned long long)rs.bw[e]);
+        }
+        __syncthreads();
+        uint64_t sub_above = 0;
+        uint32_t sb = 0;
+        {
+            uint64_t own2 = 0;
+#pragma unroll
+            for (int j = 0; j < per; j++)
+                own2 += rs.hist[tid * per + j];
+            uint64_t total2;
+            const uint64_t excl2 = block_excl_scan_u64(own2, total2, bs);
+            if (above + excl2 < thr && above + excl2 + own2 >= thr) {  // exactly one thread
+                uint64_t c = above + excl2;
+                uint32_t b = tid * per;
+                while (c + rs.hist[b] < thr) {
+                    c += rs.hist[b];
+                    b++;
+                }
+                bs.res64[0] = c;
+                bs.n = b;
+            }
+            __syncthreads();
+            sub_above = bs.res64[0];
+            sb = bs.n;
+        }
+        // ---- its elements, compared pairwise (exact ties of x share a sub-bin) ---
+        for (uint32_t e0 = 0; e0 < nb; e0 += kMergeThreads) {
+            const uint32_t e = e0 + tid;
+            bool take = false;
+            if (e < nb)
+                take = dist_sub(m, rl_key_float((uint32_t)(rs.bkey[e] >> 32)), bstar) == sb;
+            const uint32_t pos = wave_append(take, &bs.cnt[1]);
+            if (take && pos < (uint32_t)kSubCap) {
+                rs.skey[pos] = rs.bkey[e];
+                rs.sw[pos] = rs.bw[e];
+            }
+        }
+        __syncthreads();
+        const uint32_t ns = bs.cnt[1];
+        if (ns > (uint32_t)kSubCap)
+            return radix_row_sample(p, row, l, inv_t, cutoff, topp, m, wk, s_whist, bs);
+        if (tid < ns) {
+            const uint64_t ck = rs.skey[tid];
+            uint64_t s = 0;  // sub-bin weight strictly above this element
+            for (uint32_t j = 0; j < ns; j++)
+                s += rs.skey[j] > ck ? (uint64_t)rs.sw[j] : 0ull;
+            if (sub_above + s < thr && sub_above + s + rs.sw[tid] >= thr) {  // exactly one element
+                bs.res64[0] = ck;
+                bs.res64[1] = sub_above + s + rs.sw[tid];
+            }
+        }
+        __syncthreads();
+        tau = bs.res64[0];
+        wp = bs.res64[1];
+        // the boundary bin's members of P join their rounds
+        for (uint32_t e = tid; e < nb; e += kMergeThreads) {
+            const uint64_t ck = rs.bkey[e];
+            if (ck >= tau)
+                atomicAdd(&rs.rounds[(0xFFFFFFFFu - (uint32_t)ck) / 256u], (unsigned long long)rs.bw[e]);
+        }
+        __syncthreads();
+    }
+
+    // ---- the draw and the round where the cumulative weight first exceeds it -----
+    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
+    {
+        const uint32_t per = (R + kMergeThreads - 1) / kMergeThreads;
+        const uint32_t r0 = min(R, tid * per), r1 = min(R, r0 + per);
+        uint64_t own = 0;
+        for (uint32_t r = r0; r < r1; r++)
+            own += rs.rounds[r];
+        uint64_t total;
+        const uint64_t excl = block_excl_scan_u64(own, total, bs);
+        if (excl <= u && u < excl + own) {  // exactly one thread: u < W_P = total
+            uint64_t c = excl;
+            uint32_t r = r0;
+            while (c + rs.rounds[r] <= u) {
+                c += rs.rounds[r];
+                r++;
+            }
+            bs.n = r;
+            bs.sel64 = c;
+        }
+        __syncthreads();
+    }
+    const uint32_t rstar = bs.n;
+    const uint64_t before = bs.sel64;
+    uint32_t tok = 0;
+    if (wave == 0) {
+        const uint32_t i0 = rstar * 256 + lane * 4;
+        const rl_f32x4 v = load_quad(l, i0, V);
+        uint32_t w4[4], own = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float x = quad_at(v, e) * inv_t;
+            const uint32_t key = rl_float_key(x);
+            const uint32_t b = trunc ? dist_bin(m, x) : 0u;
+            const bool in = key >= cutoff && (b < bstar || (b == bstar && composite_key(key, i0 + e) >= tau));
+            const uint32_t w = rl_sample_weight_nb(x - m);  // -inf weighs 0
+            w4[e] = in ? w : 0u;
+            own += w4[e];
+        }
+        uint64_t c = before + wave_inclusive_scan_u64(own) - own;
+        uint32_t cand = 0xFFFFFFFFu;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            c += w4[e];
+            if (cand == 0xFFFFFFFFu && c > u)
+                cand = i0 + e;
+        }
+        tok = rl_wave_min_u32(cand);
+        if (tok >= V)
+            tok = 0;
+    }
+    return tok;
+}
+
 // One workgroup of 256 threads per row.
 __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParams p)
 {
@@ -586,6 +918,9 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     __shared__ uint32_t s_w[kKeptCap];      // weights in sorted order
     __shared__ uint32_t s_idx[kKeptCap];    // token index in sorted order
     __shared__ BlockShared bs;
+    // the whole-row path's scratch reuses the candidate buffer
+    static_assert(sizeof(RowScratch) <= sizeof(s_cand), "row scratch fits the candidate buffer");
+    RowScratch &rs = *reinterpret_cast<RowScratch *>(s_cand);
 
     const SplitStat *st = p.stats + (size_t)row * p.splits;
     const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
@@ -624,10 +959,11 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const bool split_over = __ballot(ncand > (uint32_t)kCandCap) != 0;
     const uint64_t cum = wave_inclusive_scan_u64(ncand);
     const uint32_t n = (uint32_t)__shfl(cum, 63);
-    uint32_t tok;
-    if (k_eff == 0 || split_over || n > (uint32_t)kMergeCap) {
-        tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist, bs);
-    } else {
+    uint32_t tok = 0;
+    // the exact whole-row path (one call site, so it is inlined and its
+    // pointers stay in their address spaces): no top-k, or too many candidates
+    bool exact = k_eff == 0 || split_over || n > (uint32_t)kMergeCap;
+    if (!exact) {
         // ---- gather the slices' candidates ----------------------------------
         // Flat slot f belongs to the split whose inclusive count first exceeds
         // it; each thread issues all its loads before storing any.
@@ -664,7 +1000,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         }
         if (tid == 0)
             bs.n = 0;
-        s_h2[0][tid] = 0;
+        if (tid < 256)
+            s_h2[0][tid] = 0;
         __syncthreads();
 
         // ---- exact k_eff-th largest key --------------------------------------
@@ -699,7 +1036,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                             atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
                     }
                     __syncthreads();
-                    s_h2[(pass & 1) ^ 1][tid] = 0;
+                    if (tid < 256)
+                        s_h2[(pass & 1) ^ 1][tid] = 0;
                     uint32_t h[4], own = 0;
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
@@ -740,7 +1078,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         const uint32_t nk = bs.n;
         __syncthreads();
         if (nk > (uint32_t)kKeptCap) {
-            tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, s_hist, s_whist, bs);
+            exact = true;
         } else if (nk <= 64u) {
             // ---- one wave: lane i holds sorted element i; with at most 64
             // weights of at most 2^24 every prefix fits in 32 bits ------------
@@ -848,6 +1186,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                 tok = 0;
         }
     }
+    if (exact)
+        tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
     if (tid == 0) {
         p.token_out[row] = tok;
         p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
@@ -878,6 +1218,10 @@ int validate(const rl_sample_args_t *a)
     }
     if (!a->logits || !a->token_out || !a->logprob_out) {
         rl_set_error("rl_hip_sample: NULL device pointer");
+        return -1;
+    }
+    if (((uintptr_t)a->logits & 15u) != 0) {
+        rl_set_error("rl_hip_sample: logits must be 16-byte aligned");
         return -1;
     }
     if (a->rows == 0 || a->rows > 65535 || a->vocab == 0 || a->row_stride < a->vocab || a->row_stride % 4 != 0) {

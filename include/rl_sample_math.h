@@ -132,6 +132,35 @@ rl_sample_weight(float d)
     return (uint32_t)(rl_expf_cw(d) * 16777216.0f);
 }
 
+/* rl_sample_weight without branches, for d <= 0 (and NaN): the same
+ * operations in the same order on max(d, -87), then 0 selected for
+ * !(d >= -87). Equal to rl_sample_weight(d) bit for bit on that domain; the
+ * sampler kernels use it in their per-element loops. */
+RL_HD uint32_t
+rl_sample_weight_nb(float d)
+{
+    RL_FP_CONTRACT_OFF
+    const float x = d >= -87.0f ? d : -87.0f;
+    const float n = floorf(x * RL_EXP_LOG2E + 0.5f);
+    float r = fmaf(-n, RL_EXP_LN2_HI, x);
+    r = fmaf(-n, RL_EXP_LN2_LO, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    union {
+        uint32_t u;
+        float f;
+    } scale;
+    scale.u = (uint32_t)((int)n + 127) << 23;
+    const uint32_t w = (uint32_t)(p * scale.f * 16777216.0f);
+    return d >= -87.0f ? w : 0u;
+}
+
 /* Order-preserving u32 key of a non-NaN float; -0 and +0 share a key. */
 RL_HD uint32_t
 rl_float_key(float x)

@@ -3,12 +3,12 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product library links, loads or
  * calls this code; only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg use it, and only as the checker (or the timed CPU
+ * cpu_baseline leg use it, and only to check results (or as the timed CPU
  * baseline), never as a fallback.
  *
  * Every function cites the reference file:line it restates. Integer parts
  * (rings, submit, worker rule, windows, arena, prefix refcounts, reward) are
- * written against raw byte images at the Appendix-A offsets, independently
+ * written against raw byte images at the reference structs' byte offsets, independently
  * of the product headers. Floating-point parts: paged GQA decode attention in
  * fp64 (truth) and fp32 online softmax (CPU baseline), sampling by sorting,
  * KV append with copy-on-write, group advantage.

@@ -2,7 +2,7 @@
 sources compiled into oracle/_ref/libgbref.so.
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+cpu_baseline leg of bench.py, to check results or as the timed CPU baseline.
 """
 from __future__ import annotations
 

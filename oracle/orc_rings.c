@@ -1,6 +1,6 @@
 /*
  * orc_rings.c - oracle: rings, submit, worker rule, descriptor windows, on raw
- * byte images at the Appendix-A offsets (test infrastructure only).
+ * byte images at the reference structs' byte offsets (test infrastructure only).
  */
 #include <string.h>
 

@@ -62,7 +62,7 @@ main(void)
     S(KVArena); O(KVArena, base); O(KVArena, capacity); O(KVArena, block_size); O(KVArena, bitmap);
     S(KvLayoutDesc); O(KvLayoutDesc, block_bytes); O(KvLayoutDesc, alignment);
     S(RewardDesc); O(RewardDesc, reward); O(RewardDesc, flags);
-    /* not compilable from the reference headers: pinned by Appendix-A arithmetic */
+    /* not compilable from the reference headers: pinned by packed-layout arithmetic */
     S(KVPrefix); O(KVPrefix, refcnt); O(KVPrefix, kv_block_offset); O(KVPrefix, token_len);
     O(KVPrefix, kv_block_count); O(KVPrefix, flags);
     S(KVBranch); O(KVBranch, prefix_id); O(KVBranch, delta_kv_offset); O(KVBranch, delta_len);

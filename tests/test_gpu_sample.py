@@ -86,6 +86,22 @@ def test_whole_vocab_nucleus_rollout_shape(rl, gpu, orc, olib):
     _check(rl, orc, olib, x, temperature=1.0, top_k=0, top_p=0.9, seeds=seeds, step=5)
 
 
+@pytest.mark.parametrize("vocab,std,p,T", [(128256, 1.0, 0.9, 1.0), (50257, 2.0, 0.99, 0.7), (1000, 3.0, 0.5, 1.0),
+                                           (32000, 6.0, 0.95, 1.0), (4099, 0.05, 0.3, 2.0)])
+def test_whole_vocab_nucleus_spreads(rl, gpu, orc, olib, vocab, std, p, T):
+    """Whole-vocabulary nucleus over several spreads: the boundary lands in
+    dense bins (small std), in the sparse tail (large std, p near 1) and near
+    the zero-weight limit; rows with spike ties and a few -inf entries."""
+    rng = np.random.default_rng(vocab)
+    stride = -(-vocab // 4) * 4
+    x = np.full((40, stride), 5.0, dtype=np.float32)          # the padding is never read
+    x[:, :vocab] = rng.standard_normal((40, vocab), dtype=np.float32) * np.float32(std)
+    x[1, rng.choice(vocab, 7, replace=False)] = np.float32(3.0 * std)
+    x[2, rng.choice(vocab, vocab // 3, replace=False)] = -np.inf
+    seeds = rng.integers(0, 2**63, 40, dtype=np.uint64)
+    _check(rl, orc, olib, x, vocab=vocab, temperature=T, top_k=0, top_p=p, seeds=seeds, step=11)
+
+
 @pytest.mark.parametrize("k", [0, 3])
 def test_exact_path_edge_rows(rl, gpu, orc, olib, k):
     """Rows forcing the exact path: every logit equal, heavy ties, all -inf."""

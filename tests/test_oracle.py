@@ -23,7 +23,8 @@ def sm():
     for name, res, args in [("probe_philox", None, [C.c_void_p] * 3), ("probe_draw64", u64, [u64, u64, u32]),
                             ("probe_mulhi", u64, [u64, u64]), ("probe_expf_cw", f, [f]), ("probe_weight", u32, [f]),
                             ("probe_key", u32, [f]), ("probe_key_float", f, [u32]), ("probe_topp", u64, [f, u64]),
-                            ("probe_expf_many", None, [C.c_void_p, C.c_void_p, u32])]:
+                            ("probe_expf_many", None, [C.c_void_p, C.c_void_p, u32]),
+                            ("probe_weight_pair_many", None, [C.c_void_p, C.c_void_p, C.c_void_p, u32])]:
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = res, args
     return lib
@@ -100,6 +101,25 @@ def test_weights(sm):
     assert np.all(np.diff(w) >= 0)                  # monotone
     exact = np.floor(np.exp(d[::100].astype(np.float64)) * 2**24)
     assert np.max(np.abs(w - exact)) <= 8           # a few units of 2^-24
+
+
+def test_branch_free_weight_equals_weight(sm):
+    """rl_sample_weight_nb (the kernels' per-element form) equals
+    rl_sample_weight bit for bit on non-positive floats: a stride-997 sweep of
+    all 2^31 bit patterns with the sign bit set (through -inf and the NaNs), a
+    stride-211 sweep of [-18, -0] (the 2^-24 cut-off of the weights sits at
+    -16.6), and every float in [-87.5, -86.5] around the -87 clamp."""
+    neg0, m18 = 0x80000000, int(np.float32(-18.0).view(np.uint32))
+    lo87, hi87 = int(np.float32(-86.5).view(np.uint32)), int(np.float32(-87.5).view(np.uint32))
+    pats = np.arange(neg0, 0x100000000, 997, dtype=np.uint64).astype(np.uint32)
+    dense = np.concatenate([np.arange(neg0, m18 + 1, 211, dtype=np.uint64),
+                            np.arange(lo87, hi87 + 1, dtype=np.uint64)]).astype(np.uint32)
+    for u in (pats, dense):
+        d = np.concatenate([u.view(np.float32), np.float32([0.0, -0.0, -np.inf, np.nan])])
+        a = np.zeros(d.size, np.uint32)
+        b = np.zeros(d.size, np.uint32)
+        sm.probe_weight_pair_many(d.ctypes.data, a.ctypes.data, b.ctypes.data, d.size)
+        assert np.array_equal(a, b), d[np.nonzero(a != b)[0][:5]]
 
 
 def test_float_key_orders_like_floats(sm):
