@@ -8,7 +8,8 @@ One step = the batched decode work of 64 rollouts with inputs resident in HBM:
   2. sampling of 64 rows x 128,256 fp32 logits ~N(0,1) with 5 spike tokens per
      row at +8.0: temperature 0.8, top-k 50, top-p 0.9, Philox per-row seed,
      step counter = step index;
-  3. KV append of one token per rollout and KV head.
+  3. KV append of one token per rollout and KV head (rl_hip_decode_step runs
+     it inside the attention's merge kernel, after every context was read).
 value = tokens/s = 64 x steps/s (whole job, one GPU). The dominant kernel's
 roofline (attention, HBM-bound) is measured over its own launches with HIP
 events on the library stream. The CPU baseline is the oracle's OpenMP
@@ -118,14 +119,17 @@ class Step:
         return B * KVH * D * 2 * 2 * 2  # read new K/V rows, write them into the arena
 
     def run(self, i, only="step"):
-        if only in ("step", "attn"):
+        if only == "step":
+            # attention, then the KV append inside the attention's merge kernel
+            rlrt.decode_step(self.attn, self.app)
+        elif only == "attn":
             rlrt.attn_decode(self.attn)
+        elif only == "append":
+            rlrt.kv_append(self.app)
         if only in ("step", "sample"):
             s = self.samp[i % LOGIT_COPIES]
             s.step = i
             rlrt.sample(s)
-        if only in ("step", "append"):
-            rlrt.kv_append(self.app)
 
 
 def time_loop(step, k, only):

@@ -136,7 +136,9 @@ struct CtxFixed {
 };
 
 // Issue side of a wave: walks the wave's tile range and starts the copies.
-template <int D, int G, int DT, int TPB, class CtxFn>
+// NS stages (tiles in the pipeline) need NS q slots: every row whose first
+// tile is staged but not yet consumed holds one.
+template <int D, int G, int DT, int TPB, int NS, class CtxFn>
 struct Issuer {
     using C = Cfg<D, G, DT, TPB>;
     CtxFn cf;
@@ -200,7 +202,7 @@ struct Issuer {
         m.ctx = ctx;
         m.first = first;
         if (first) {
-            m.qslot = qcount & 1u;
+            m.qslot = qcount % (uint32_t)NS;
             qcount++;
             const uint8_t *qsrc = (const uint8_t *)(p.q + ((size_t)b * p.q_heads + (size_t)g * G) * D);
 #pragma unroll
@@ -434,17 +436,38 @@ __device__ __forceinline__ void consume(const AttnParams &p, RowState<D, G, DT, 
 }
 
 
+// Waits until at most n staged tiles' copies of this wave are outstanding
+// (copies complete in issue order; n * UNIT stays below the 6-bit vmcnt).
+template <int UNIT, int NMAX>
+__device__ __forceinline__ void wait_tiles(uint32_t n)
+{
+    static_assert(NMAX * UNIT < 64, "vmcnt range");
+    if constexpr (NMAX >= 7) { if (n >= 7) { rl_wait_vmcnt<7 * UNIT>(); return; } }
+    if constexpr (NMAX >= 6) { if (n == 6) { rl_wait_vmcnt<6 * UNIT>(); return; } }
+    if constexpr (NMAX >= 5) { if (n == 5) { rl_wait_vmcnt<5 * UNIT>(); return; } }
+    if constexpr (NMAX >= 4) { if (n == 4) { rl_wait_vmcnt<4 * UNIT>(); return; } }
+    if constexpr (NMAX >= 3) { if (n == 3) { rl_wait_vmcnt<3 * UNIT>(); return; } }
+    if constexpr (NMAX >= 2) { if (n == 2) { rl_wait_vmcnt<2 * UNIT>(); return; } }
+    if (n >= 1)
+        rl_wait_vmcnt<UNIT>();
+    else
+        rl_wait_vmcnt<0>();
+}
+
 // The main loop of one wave: stream tiles [s_begin, s_end) of the row
 // sequence, starting in rollout start_b whose first tile is start_cum.
-// Copies of the next tile are in flight while the current one is consumed;
-// rows finished in this wave are written directly or as partials.
-template <int D, int G, int DT, int TPB, class CtxFn>
+// NS stages form a ring (stage k at st + k * st_stride; q slots at qs): while
+// one tile is consumed the next NS - 1 are in flight, and the consumed stage
+// takes the tile NS ahead. Rows finished in this wave are written directly or
+// as partials.
+template <int D, int G, int DT, int TPB, int NS, class CtxFn>
 __device__ __forceinline__ void attn_stream(const AttnParams &p, const CtxFn &cf, uint32_t wave_id, uint32_t s_begin,
                                             uint32_t s_end, uint32_t start_b, uint32_t start_cum,
-                                            RL_LDS uint8_t *st0, RL_LDS uint8_t *st1, RL_LDS uint8_t *qs, int lane)
+                                            RL_LDS uint8_t *st, uint32_t st_stride, RL_LDS uint8_t *qs, int lane)
 {
     using C = Cfg<D, G, DT, TPB>;
-    Issuer<D, G, DT, TPB, CtxFn> is;
+    static_assert(NS >= 2 && NS <= 8, "stages");
+    Issuer<D, G, DT, TPB, NS, CtxFn> is;
     is.cf = cf;
     is.init_offsets(lane);
     is.set_rollout(p, start_b);
@@ -461,41 +484,32 @@ __device__ __forceinline__ void attn_stream(const AttnParams &p, const CtxFn &cf
     is.win0 = is.win1 = 0;
 
     RowState<D, G, DT, TPB> rs;
-    StageMeta mc, mn;  // tile to consume next, tile in flight behind it
-    RL_LDS uint8_t *stc = st0;
-    RL_LDS uint8_t *stn = st1;
-    bool has_next = false;
-    is.issue(p, stc, qs, mc, lane);
-    if (is.left) {
-        is.issue(p, stn, qs, mn, lane);
-        has_next = true;
-    }
-    for (;;) {
-        // Copies complete in issue order: once at most one tile's worth is
-        // outstanding, everything older - this tile and its q - has landed.
-        // (A tile that brings a q slot issues one more copy: the wait is then
-        // slightly stronger than needed, never weaker.)
-        if (has_next)
-            rl_wait_vmcnt<C::UNIT_OPS>();
-        else
-            rl_wait_vmcnt<0>();
-        consume<D, G, DT, TPB>(p, rs, stc, qs, mc, wave_id, lane);
-        if (!has_next)
-            break;
-        // the stage just consumed takes the tile after next
-        StageMeta mi;
-        bool has_after = false;
+    StageMeta m[NS];  // indexed with compile-time slots only (the ring loop is unrolled)
+    uint32_t n_in = 0;  // tiles staged and not yet consumed
+#pragma unroll
+    for (int k = 0; k < NS; k++)
         if (is.left) {
-            rl_wait_lgkmcnt0();
-            is.issue(p, stc, qs, mi, lane);
-            has_after = true;
+            is.issue(p, st + k * st_stride, qs, m[k], lane);
+            n_in++;
         }
-        RL_LDS uint8_t *t = stc;
-        stc = stn;
-        stn = t;
-        mc = mn;
-        mn = mi;
-        has_next = has_after;
+    for (;;) {
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            // Once at most n_in - 1 tiles' copies are outstanding, this tile
+            // and its q have landed. (A younger tile that brings a q slot
+            // issues more copies: the wait is then stronger, never weaker.)
+            wait_tiles<C::UNIT_OPS, NS - 1>(n_in - 1);
+            consume<D, G, DT, TPB>(p, rs, st + k * st_stride, qs, m[k], wave_id, lane);
+            n_in--;
+            if (is.left) {
+                // the consumed stage takes the tile NS ahead
+                rl_wait_lgkmcnt0();
+                is.issue(p, st + k * st_stride, qs, m[k], lane);
+                n_in++;
+            } else if (n_in == 0) {
+                return;
+            }
+        }
     }
 }
 

@@ -42,21 +42,30 @@
 #include "rl_dev_common.h"
 #include "rl_hip.h"
 #include "rl_hip_internal.h"
+#include "kv_append_core.h"
 
 namespace {
 
+// Stages of the per-wave tile ring. Two (one tile in flight while one is
+// consumed) with two workgroups per CU measured faster than four stages with
+// one workgroup per CU (120 vs 125 us on the 64-rollout ragged batch): the
+// random-block stream saturates the same ~5.5 TB/s either way, and eight
+// waves per CU overlap the consume phases better than four.
+template <int D, int G, int DT, int TPB>
+constexpr int stages_of()
+{
+    return 2;
+}
 
 template <int D, int G, int DT, int TPB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
 {
     using C = Cfg<D, G, DT, TPB>;
     constexpr int W = C::W;
+    constexpr int NS = stages_of<D, G, DT, TPB>();
     static_assert(W * 64 == 256, "launch bounds");
-    // Separate arrays per stage so the compiler's wait insertion can tell a
-    // copy into one stage from reads of the other.
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_st0[W * C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_st1[W * C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * 2 * C::QSLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_st[NS][W * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * NS * C::QSLOT];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -135,22 +144,27 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
     if (!active)
         return;
 
-    RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_st0 + wave * C::STAGE;
-    RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_st1 + wave * C::STAGE;
-    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * 2 * C::QSLOT;
-    attn_stream<D, G, DT, TPB>(p, CtxFromArray{p.ctx}, wave_id, s_begin, s_end, rb, rcum, st0, st1, qs, lane);
+    RL_LDS uint8_t *st = (RL_LDS uint8_t *)lds_st[0] + wave * C::STAGE;
+    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * NS * C::QSLOT;
+    attn_stream<D, G, DT, TPB, NS>(p, CtxFromArray{p.ctx}, wave_id, s_begin, s_end, rb, rcum, st, W * C::STAGE, qs,
+                                   lane);
 }
 
 // Combines the partials of every row split across waves (merge_row) and
-// writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN).
+// writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN). In a
+// fused decode step (ap.arena set) the workgroup of row (b, g) also appends
+// that row's new K/V token: attn_decode_kernel has read every context
+// already, and the merge reads only the partials.
 template <int D, int G, int DT>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p)
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, AppendParams ap)
 {
     __shared__ float s_f[kMergeLds * G];
     __shared__ float s_l[kMergeLds * G];
     __shared__ float s_L[G];
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
+    if (ap.arena && threadIdx.x < 64)
+        append_row(ap, b, g, threadIdx.x, 64);
     const uint32_t cin = rl_sload(p.ctx + b);
     const bool bad = cin > p.max_ctx;
     const uint32_t nu = tiles_of(p, cin);
@@ -182,9 +196,11 @@ uint32_t waves_of(const rl_attn_decode_args_t *a)
         return a->grid_waves;
     const uint32_t G = a->q_heads / a->kv_heads;
     const uint32_t D = a->layout.head_dim;
-    // LDS per wave: two stages of one tile's K and V, two q slots
-    const uint32_t wave_lds = 2 * (2 * 16 * 2 * D) + 2 * ((G * D * 2 + 1023) / 1024) * 1024;
-    uint32_t wg = (160u * 1024u) / (4 * wave_lds);
+    // LDS per wave: NS stages of one tile's K and V and NS q slots, NS as in
+    // stages_of()
+    const uint32_t per_stage = 2 * 16 * 2 * D + ((G * D * 2 + 1023) / 1024) * 1024;
+    const uint32_t ns = 2;
+    uint32_t wg = (160u * 1024u) / (4 * ns * per_stage);
     wg = wg > 4 ? 4 : wg;
     return rl_cu_count() * wg * 4;
 }
@@ -204,37 +220,38 @@ WsLayout ws_layout(const rl_attn_decode_args_t *a)
 }
 
 template <int D, int G, int DT, int TPB>
-int launch(const AttnParams &p)
+int launch(const AttnParams &p, const AppendParams &ap)
 {
     using C = Cfg<D, G, DT, TPB>;
     const uint32_t wgs = (p.nwaves + C::W - 1) / C::W;
     hipLaunchKernelGGL((attn_decode_kernel<D, G, DT, TPB>), dim3(wgs), dim3(C::W * 64), 0, rl_stream(), p);
     if (rl_check_launch("attn_decode_kernel launch"))
         return -1;
-    hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(), p);
+    hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(), p,
+                       ap);
     return rl_check_launch("attn_merge_kernel launch");
 }
 
 template <int D, int G, int DT>
-int dispatch_tpb(const AttnParams &p, uint32_t tpb)
+int dispatch_tpb(const AttnParams &p, const AppendParams &ap, uint32_t tpb)
 {
-    return tpb == 16 ? launch<D, G, DT, 16>(p) : launch<D, G, DT, 32>(p);
+    return tpb == 16 ? launch<D, G, DT, 16>(p, ap) : launch<D, G, DT, 32>(p, ap);
 }
 
 template <int D, int G>
-int dispatch_dt(const AttnParams &p, uint32_t dt, uint32_t tpb)
+int dispatch_dt(const AttnParams &p, const AppendParams &ap, uint32_t dt, uint32_t tpb)
 {
-    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, tpb) : dispatch_tpb<D, G, 1>(p, tpb);
+    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, ap, tpb) : dispatch_tpb<D, G, 1>(p, ap, tpb);
 }
 
 template <int D>
-int dispatch_g(const AttnParams &p, uint32_t G, uint32_t dt, uint32_t tpb)
+int dispatch_g(const AttnParams &p, const AppendParams &ap, uint32_t G, uint32_t dt, uint32_t tpb)
 {
     switch (G) {
-    case 1: return dispatch_dt<D, 1>(p, dt, tpb);
-    case 2: return dispatch_dt<D, 2>(p, dt, tpb);
-    case 4: return dispatch_dt<D, 4>(p, dt, tpb);
-    default: return dispatch_dt<D, 8>(p, dt, tpb);
+    case 1: return dispatch_dt<D, 1>(p, ap, dt, tpb);
+    case 2: return dispatch_dt<D, 2>(p, ap, dt, tpb);
+    case 4: return dispatch_dt<D, 4>(p, ap, dt, tpb);
+    default: return dispatch_dt<D, 8>(p, ap, dt, tpb);
     }
 }
 
@@ -302,10 +319,10 @@ extern "C" size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *a)
     return ws_layout(a).total;
 }
 
-extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
+namespace {
+
+int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap)
 {
-    if (rl_require_open("rl_hip_attn_decode") || validate(a))
-        return -1;
     const WsLayout w = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < w.total) {
         rl_set_error("rl_hip_attn_decode: workspace %zu bytes < %zu required", a->workspace_bytes, w.total);
@@ -334,6 +351,29 @@ extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
 
     const uint32_t G = a->q_heads / a->kv_heads;
     if (a->layout.head_dim == 128)
-        return dispatch_g<128>(p, G, a->dtype, a->layout.token_count);
-    return dispatch_g<64>(p, G, a->dtype, a->layout.token_count);
+        return dispatch_g<128>(p, ap, G, a->dtype, a->layout.token_count);
+    return dispatch_g<64>(p, ap, G, a->dtype, a->layout.token_count);
+}
+
+}  // namespace
+
+extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
+{
+    if (rl_require_open("rl_hip_attn_decode") || validate(a))
+        return -1;
+    AppendParams none = {};
+    none.arena = nullptr;
+    return attn_run(a, none);
+}
+
+extern "C" int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append)
+{
+    if (rl_require_open("rl_hip_decode_step") || validate(attn) || append_validate(append, "rl_hip_decode_step"))
+        return -1;
+    if (append->batch != attn->batch || append->kv_heads != attn->kv_heads) {
+        rl_set_error("rl_hip_decode_step: append batch %u / kv_heads %u differ from attention %u / %u",
+                     append->batch, append->kv_heads, attn->batch, attn->kv_heads);
+        return -1;
+    }
+    return attn_run(attn, append_params(append));
 }

@@ -101,22 +101,35 @@ __device__ __forceinline__ float wave_sum_f(float v)
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kGreedyBatch = 8;  // 16-byte loads in flight per thread
+constexpr int kGreedyBatch = 16;  // 16-byte loads in flight per thread
 
-// Folds value v at index i into a running (best, bidx, z): best the max,
-// bidx the lowest index holding it, z the sum of exp(v - best) so far.
-__device__ __forceinline__ void greedy_fold(float v, uint32_t i, float &best, uint32_t &bidx, float &z)
+// Folds a batch of n values (at indices idx[j], increasing) into a running
+// (best, bidx, z): best the max, bidx the lowest index holding it, z the sum
+// of exp(v - best). The batch max comes first, so each value costs one exp
+// and no branch.
+template <int N>
+__device__ __forceinline__ void greedy_fold_batch(const float (&v)[N], const uint32_t (&idx)[N], float &best,
+                                                  uint32_t &bidx, float &z)
 {
-    if (v > best) {
-        z = (best == -INFINITY ? 0.f : z * __builtin_amdgcn_exp2f((best - v) * kLog2e)) + 1.f;
-        best = v;
-        bidx = i;
-    } else {
-        if (v == best && i < bidx)
-            bidx = i;
-        if (v != -INFINITY)
-            z += __builtin_amdgcn_exp2f((v - best) * kLog2e);
+    float bm = v[0];
+    uint32_t bi = idx[0];
+#pragma unroll
+    for (int j = 1; j < N; j++) {
+        const bool gt = v[j] > bm;  // strict: the earlier (lower) index keeps a tie
+        bm = gt ? v[j] : bm;
+        bi = gt ? idx[j] : bi;
     }
+    const bool take = bm > best;
+    const float nb = take ? bm : best;
+    bidx = take ? bi : bidx;
+    if (nb != -INFINITY) {
+        float zz = best == -INFINITY ? 0.f : z * __builtin_amdgcn_exp2f((best - nb) * kLog2e);
+#pragma unroll
+        for (int j = 0; j < N; j++)
+            zz += v[j] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((v[j] - nb) * kLog2e);
+        z = zz;
+    }
+    best = nb;
 }
 
 // One thread's share of a greedy scan over lg[0, n): 16-byte loads of
@@ -132,35 +145,56 @@ __device__ void greedy_scan(const float *lg, uint32_t n, uint32_t tid, float &be
     if (((uintptr_t)lg & 15u) == 0 && quads > 0) {
         const RL_GLOBAL rl_f32x4 *l4 = (const RL_GLOBAL rl_f32x4 *)lg;
         for (uint32_t q0 = 0; q0 < quads; q0 += T * kGreedyBatch) {
-            rl_f32x4 v[kGreedyBatch];
+            rl_f32x4 r[kGreedyBatch];
 #pragma unroll
             for (int j = 0; j < kGreedyBatch; j++)
-                v[j] = l4[min(q0 + j * T + tid, quads - 1)];
+                r[j] = l4[min(q0 + j * T + tid, quads - 1)];
+            float v[4 * kGreedyBatch];
+            uint32_t idx[4 * kGreedyBatch];
 #pragma unroll
             for (int j = 0; j < kGreedyBatch; j++) {
                 const uint32_t q = q0 + j * T + tid;
-                if (q >= quads)
-                    v[j] = rl_f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-                const uint32_t i = q * 4;
-                greedy_fold(v[j].x, i, best, bidx, z);
-                greedy_fold(v[j].y, i + 1, best, bidx, z);
-                greedy_fold(v[j].z, i + 2, best, bidx, z);
-                greedy_fold(v[j].w, i + 3, best, bidx, z);
+                const bool in = q < quads;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[4 * j + e] = in ? r[j][e] : -INFINITY;
+                    idx[4 * j + e] = q * 4 + e;
+                }
             }
+            greedy_fold_batch(v, idx, best, bidx, z);
         }
         done = quads * 4;
     }
     for (uint32_t i0 = done; i0 < n; i0 += T * kGreedyBatch) {
         float v[kGreedyBatch];
-#pragma unroll
-        for (int j = 0; j < kGreedyBatch; j++)
-            v[j] = lg[min(i0 + j * T + tid, n - 1)];
+        uint32_t idx[kGreedyBatch];
 #pragma unroll
         for (int j = 0; j < kGreedyBatch; j++) {
             const uint32_t i = i0 + j * T + tid;
-            greedy_fold(i < n ? v[j] : -INFINITY, i, best, bidx, z);
+            v[j] = lg[min(i, n - 1)];
+            v[j] = i < n ? v[j] : -INFINITY;
+            idx[j] = i;
         }
+        greedy_fold_batch(v, idx, best, bidx, z);
     }
+}
+
+// Stages of each wave's tile ring: the worker is one workgroup per ring pair,
+// so a decode step's attention is latency-bound. Four stages measured best
+// on the 8-head d64 plumbing shape (34 us of tile streaming per step against
+// 40 us with seven); fewer when the LDS beside the merge buffers (2 KiB kept
+// free) or the vmcnt range of the copies does not allow four.
+template <int D, int G, int DT, int TPB>
+constexpr int worker_stages()
+{
+    using C = Cfg<D, G, DT, TPB>;
+    constexpr int fixed = 2 * kMergeLds * G * 4 + 2048;
+    constexpr int per = C::W * (C::STAGE + C::QSLOT);
+    int ns = (C::LDS_CU - fixed) / per;
+    ns = ns > 4 ? 4 : ns;
+    while (ns > 2 && (ns - 1) * C::UNIT_OPS >= 64)
+        ns--;
+    return ns < 2 ? 2 : ns;
 }
 
 template <int D, int G, int DT, int TPB>
@@ -168,15 +202,16 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
 {
     using C = Cfg<D, G, DT, TPB>;
     constexpr int W = C::W;
+    constexpr int NS = worker_stages<D, G, DT, TPB>();
     static_assert(W * 64 == kWorkerThreads, "four waves");
     constexpr int PART = C::PART;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_st0[W * C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_st1[W * C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * 2 * C::QSLOT];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_st[NS][W * C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * NS * C::QSLOT];
     __shared__ float s_f[kMergeLds * G];
     __shared__ float s_l[kMergeLds * G];
     __shared__ float s_L[G];
     __shared__ uint32_t s_desc[16];
+    __shared__ uint32_t s_out[16];
     __shared__ uint32_t s_ctl;
     __shared__ float s_red[W];
     __shared__ uint32_t s_redi[W];
@@ -200,38 +235,49 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
         dtail = sys_load(&dq->tail);
     }
 
-    RL_LDS uint8_t *st0 = (RL_LDS uint8_t *)lds_st0 + wave * C::STAGE;
-    RL_LDS uint8_t *st1 = (RL_LDS uint8_t *)lds_st1 + wave * C::STAGE;
-    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * 2 * C::QSLOT;
+    RL_LDS uint8_t *st = (RL_LDS uint8_t *)lds_st[0] + wave * C::STAGE;
+    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds_q + wave * NS * C::QSLOT;
 
     for (;;) {
-        // ---- next descriptor (thread 0), bounded wait ---------------------
-        if (tid == 0) {
-            uint32_t ctl = 0;
-            uint64_t idle = 0;
-            for (;;) {
-                if (sys_load(wp.stop) != 0) {
-                    ctl = 1;
-                    break;
+        // ---- next descriptor (wave 0), bounded wait -------------------------
+        // Lane 0 polls the producer's tail (the stop flag only while the ring
+        // is empty); after the acquire, lanes 0-15 read the 16 dwords of the
+        // descriptor in one load instruction, then lane 0 releases the slot.
+        if (wave == 0) {
+            uint32_t ctl = 0, got = 0;
+            if (lane == 0) {
+                uint64_t idle = 0;
+                for (;;) {
+                    if (sys_load(&cq->tail) != head) {
+                        got = 1;
+                        break;
+                    }
+                    if (sys_load(wp.stop) != 0) {
+                        ctl = 1;
+                        break;
+                    }
+                    if (++idle > wp.max_idle_polls) {
+                        ctl = 1;
+                        status = kStatusIdle;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
                 }
-                if (sys_load(&cq->tail) != head) {
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-                    const volatile uint32_t *src = (const volatile uint32_t *)&cq->desc[head & HW_RING_MASK];
-#pragma unroll
-                    for (int i = 0; i < 16; i++)
-                        s_desc[i] = src[i];
+            }
+            got = rl_readlane(got, 0);
+            if (got) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+                const uint32_t h = rl_readlane(head, 0);
+                if (lane < 16)
+                    s_desc[lane] = ((const volatile uint32_t *)&cq->desc[h & HW_RING_MASK])[lane];
+                rl_wave_lds_fence();
+                if (lane == 0) {
                     head++;
                     sys_store_release(&cq->head, head);
-                    break;
                 }
-                if (++idle > wp.max_idle_polls) {
-                    ctl = 1;
-                    status = kStatusIdle;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
             }
-            s_ctl = ctl;
+            if (lane == 0)
+                s_ctl = ctl;
         }
         __syncthreads();
         if (s_ctl)
@@ -280,7 +326,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                 if ((uint32_t)wave < NW) {
                     const uint32_t sb = (uint32_t)(((uint64_t)wave * U) / NW);
                     const uint32_t se = (uint32_t)(((uint64_t)(wave + 1) * U) / NW);
-                    attn_stream<D, G, DT, TPB>(a, CtxFixed{pos}, wave, sb, se, 0, 0, st0, st1, qs, lane);
+                    attn_stream<D, G, DT, TPB, NS>(a, CtxFixed{pos}, wave, sb, se, 0, 0, st, W * C::STAGE, qs, lane);
                 }
                 __syncthreads();
                 for (uint32_t g = 0; g < kvh; g++)
@@ -374,31 +420,46 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
         if (fail)
             break;
 
-        // ---- publish the completion (thread 0), bounded wait while full ------
-        if (tid == 0) {
-            uint32_t ctl = 1;
-            uint64_t idle = 0;
-            for (;;) {
-                if (dtail - sys_load(&dq->head) < HW_RING_SIZE) {
-                    volatile uint32_t *dst = (volatile uint32_t *)&dq->desc[dtail & HW_RING_MASK];
+        // ---- publish the completion (wave 0), bounded wait while full --------
+        // Lanes 0-15 write the descriptor's 16 dwords with one store
+        // instruction; lane 0 then release-stores the new tail.
+        if (wave == 0) {
+            uint32_t ctl = 1, room = 0;
+            if (lane == 0) {
+                uint64_t idle = 0;
+                for (;;) {
+                    if (dtail - sys_load(&dq->head) < HW_RING_SIZE) {
+                        room = 1;
+                        break;
+                    }
+                    if (sys_load(wp.stop) != 0)
+                        break;
+                    if (++idle > wp.max_idle_polls) {
+                        status = kStatusDoneqFull;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            if (rl_readlane(room, 0)) {
+                const uint32_t t = rl_readlane(dtail, 0);
+                if (lane == 0) {
                     const uint32_t *dw = (const uint32_t *)&d;
 #pragma unroll
                     for (int i = 0; i < 16; i++)
-                        dst[i] = dw[i];
+                        s_out[i] = dw[i];
+                }
+                rl_wave_lds_fence();
+                if (lane < 16)
+                    ((volatile uint32_t *)&dq->desc[t & HW_RING_MASK])[lane] = s_out[lane];
+                if (lane == 0) {
                     dtail++;
                     sys_store_release(&dq->tail, dtail);
-                    ctl = 0;
-                    break;
                 }
-                if (sys_load(wp.stop) != 0)
-                    break;
-                if (++idle > wp.max_idle_polls) {
-                    status = kStatusDoneqFull;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
+                ctl = 0;
             }
-            s_ctl = ctl;
+            if (lane == 0)
+                s_ctl = ctl;
         }
         __syncthreads();
         if (s_ctl)

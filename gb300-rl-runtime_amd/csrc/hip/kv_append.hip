@@ -10,97 +10,23 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "kv_layout.h"
-#include "rl_dev_common.h"
-#include "rl_hip.h"
 #include "rl_hip_internal.h"
+#include "kv_append_core.h"
 
 namespace {
 
-struct AppendParams {
-    uint8_t *arena;
-    uint64_t block_bytes;
-    uint64_t arena_blocks;
-    uint32_t token_count;   // tokens per block
-    uint32_t row_bytes;     // K (and V) bytes per token
-    const uint32_t *table;
-    uint32_t table_stride;
-    uint32_t kv_heads;
-    const uint32_t *positions;
-    const int32_t *cow_src;
-    const uint8_t *k_new;
-    const uint8_t *v_new;
-};
-
 __global__ __launch_bounds__(64) void kv_append_kernel(AppendParams p)
 {
-    const uint32_t g = blockIdx.x;
-    const uint32_t b = blockIdx.y;
-    const int lane = threadIdx.x;
-    const uint32_t row_id = b * p.kv_heads + g;
-    const uint32_t pos = p.positions[b];
-    const uint32_t slot = pos % p.token_count;
-    if (pos / p.token_count >= p.table_stride)
-        return;  // position outside the rollout's table row: nothing written
-    const uint32_t blk = p.table[(size_t)row_id * p.table_stride + pos / p.token_count];
-    if (blk >= p.arena_blocks)
-        return;
-    uint8_t *dst = p.arena + (uint64_t)blk * p.block_bytes;
-    const uint32_t v_plane = p.token_count * p.row_bytes;
-    const uint32_t chunks = p.row_bytes / 16;  // 16-byte chunks per row
-
-    if (p.cow_src) {
-        const int32_t src_blk = p.cow_src[row_id];
-        if (src_blk >= 0 && (uint64_t)src_blk < p.arena_blocks && slot > 0) {
-            const uint8_t *src = p.arena + (uint64_t)(uint32_t)src_blk * p.block_bytes;
-            const uint32_t n = slot * chunks;  // chunks of the filled rows of one plane
-            for (uint32_t i = lane; i < 2 * n; i += 64) {
-                const uint32_t plane = i / n, c = i % n;
-                const uint32_t off = plane * v_plane + c * 16;
-                *(rl_u32x4 *)(dst + off) = *(const rl_u32x4 *)(src + off);
-            }
-        }
-    }
-    const uint8_t *kn = p.k_new + (size_t)row_id * p.row_bytes;
-    const uint8_t *vn = p.v_new + (size_t)row_id * p.row_bytes;
-    for (uint32_t i = lane; i < 2 * chunks; i += 64) {
-        const uint32_t plane = i / chunks, c = i % chunks;
-        const uint8_t *s = (plane ? vn : kn) + c * 16;
-        *(rl_u32x4 *)(dst + plane * v_plane + slot * p.row_bytes + c * 16) = *(const rl_u32x4 *)s;
-    }
+    append_row(p, blockIdx.y, blockIdx.x, threadIdx.x, 64);
 }
 
 }  // namespace
 
 extern "C" int rl_hip_kv_append(const rl_kv_append_args_t *a)
 {
-    if (rl_require_open("rl_hip_kv_append"))
+    if (rl_require_open("rl_hip_kv_append") || append_validate(a, "rl_hip_kv_append"))
         return -1;
-    if (!a || !a->arena_base || !a->block_table || !a->positions || !a->k_new || !a->v_new) {
-        rl_set_error("rl_hip_kv_append: NULL argument");
-        return -1;
-    }
-    if (kv_layout_check_paged(&a->layout) != 0) {
-        rl_set_error("rl_hip_kv_append: unsupported KV layout");
-        return -1;
-    }
-    if (a->batch == 0 || a->kv_heads == 0 || a->batch > 65535 || a->kv_heads > 65535) {
-        rl_set_error("rl_hip_kv_append: batch %u kv_heads %u out of range", a->batch, a->kv_heads);
-        return -1;
-    }
-    AppendParams p;
-    p.arena = (uint8_t *)a->arena_base;
-    p.block_bytes = a->layout.block_bytes;
-    p.arena_blocks = a->arena_bytes / a->layout.block_bytes;
-    p.token_count = a->layout.token_count;
-    p.row_bytes = a->layout.k_stride_bytes;
-    p.table = a->block_table;
-    p.table_stride = a->table_stride;
-    p.kv_heads = a->kv_heads;
-    p.positions = a->positions;
-    p.cow_src = a->cow_src;
-    p.k_new = (const uint8_t *)a->k_new;
-    p.v_new = (const uint8_t *)a->v_new;
+    const AppendParams p = append_params(a);
     hipLaunchKernelGGL(kv_append_kernel, dim3(a->kv_heads, a->batch), dim3(64), 0, rl_stream(), p);
     return rl_check_launch("kv_append_kernel launch");
 }

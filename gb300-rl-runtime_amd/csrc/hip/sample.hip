@@ -937,7 +937,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         ncand = st[lane].n_cand;
         av = st[lane].arg_val;
         ai = st[lane].arg_idx;
-        clo = st[lane].n_cand ? st[lane].cand_lo : 0xFFFFFFFFu;
+        clo = st[lane].cand_lo;
     }
     const float m = wave_max(mx);
     const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
@@ -965,37 +965,32 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     bool exact = k_eff == 0 || split_over || n > (uint32_t)kMergeCap;
     if (!exact) {
         // ---- gather the slices' candidates ----------------------------------
-        // Flat slot f belongs to the split whose inclusive count first exceeds
-        // it; each thread issues all its loads before storing any.
-        constexpr int kGather = 8;
+        // Every slice's bound is below its own k-th largest key, hence below
+        // the row's: the largest bound is a lower bound of the cutoff, and
+        // only candidates at or above it are kept. Wave w copies the lists of
+        // splits w, w + 8, ..., four loads per lane in flight, and appends
+        // the kept ones (order is irrelevant below).
+        const uint32_t key_lo = rl_wave_max_u32(ncand ? clo : 0u);
+        if (tid == 0)
+            bs.cnt[0] = 0;
+        __syncthreads();
         const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandCap;
-        for (uint32_t base = 0; base < n; base += kMergeThreads * kGather) {
-            uint32_t sp[kGather], excl[kGather];
+        const uint32_t wave = tid >> 6;
+        for (uint32_t t = wave; t < p.splits; t += kMergeWaves) {
+            const uint32_t cnt = rl_readlane(ncand, (int)t);
+            const uint2 *src = rbase + (size_t)t * kCandCap;
+            for (uint32_t j0 = 0; j0 < cnt; j0 += 256) {
+                uint2 v[4];
 #pragma unroll
-            for (int r = 0; r < kGather; r++)
-                sp[r] = excl[r] = 0;
-            for (uint32_t t = 0; t < p.splits; t++) {
-                const uint32_t inc = rl_readlane((uint32_t)cum, (int)t);
+                for (int r = 0; r < 4; r++)
+                    v[r] = src[min(j0 + (uint32_t)(r * 64 + lane), cnt - 1)];
 #pragma unroll
-                for (int r = 0; r < kGather; r++) {
-                    const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
-                    if (inc <= f) {
-                        sp[r] = t + 1;
-                        excl[r] = inc;
-                    }
+                for (int r = 0; r < 4; r++) {
+                    const bool take = j0 + (uint32_t)(r * 64 + lane) < cnt && v[r].x >= key_lo;
+                    const uint32_t pos = wave_append(take, &bs.cnt[0]);
+                    if (take)
+                        s_cand[pos] = v[r];  // pos < n <= kMergeCap
                 }
-            }
-            uint2 v[kGather];
-#pragma unroll
-            for (int r = 0; r < kGather; r++) {
-                const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
-                v[r] = f < n ? rbase[(size_t)sp[r] * kCandCap + (f - excl[r])] : make_uint2(0u, 0u);
-            }
-#pragma unroll
-            for (int r = 0; r < kGather; r++) {
-                const uint32_t f = base + tid + (uint32_t)r * kMergeThreads;
-                if (f < n)
-                    s_cand[f] = v[r];
             }
         }
         if (tid == 0)
@@ -1003,6 +998,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         if (tid < 256)
             s_h2[0][tid] = 0;
         __syncthreads();
+        const uint32_t nf = bs.cnt[0];
 
         // ---- exact k_eff-th largest key --------------------------------------
         // Every candidate key lies in [key_lo, key_hi] (the slices' bounds and
@@ -1015,8 +1011,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         // With fewer than k_eff candidates the row has fewer than k_eff finite
         // logits, and every finite one is kept.
         uint32_t cutoff = 0;
-        if (n >= k_eff) {
-            const uint32_t key_lo = rl_wave_min_u32(clo);
+        if (nf >= k_eff) {
             const uint32_t key_hi = rl_float_key(m);
             const uint32_t diff = key_lo ^ key_hi;
             if (diff == 0) {
@@ -1030,7 +1025,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     const int shift = top >= 7 ? top - 7 : 0;
                     const uint32_t above = top >= 31 ? 0u : ~((2u << top) - 1u);
                     uint32_t *H = s_h2[pass & 1];
-                    for (uint32_t i = tid; i < n; i += kMergeThreads) {
+                    for (uint32_t i = tid; i < nf; i += kMergeThreads) {
                         const uint32_t key = s_cand[i].x;
                         if ((key & above) == prefix)
                             atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
@@ -1066,7 +1061,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         }
 
         // ---- kept set K = {key >= cutoff} ------------------------------------
-        for (uint32_t i = tid; i < n; i += kMergeThreads) {
+        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
             const uint2 c = s_cand[i];
             if (c.x >= cutoff) {
                 const uint32_t pos = atomicAdd(&bs.n, 1u);

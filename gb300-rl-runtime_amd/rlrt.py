@@ -209,6 +209,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample_workspace": (sz, [C.POINTER(SampleArgs)]),
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
+        "rl_hip_decode_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
         "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
@@ -396,6 +397,11 @@ def sample(args: SampleArgs) -> None:
 
 def kv_append(args: AppendArgs) -> None:
     check(lib().rl_hip_kv_append(C.byref(args)), "rl_hip_kv_append")
+
+
+def decode_step(attn: AttnArgs, append: AppendArgs) -> None:
+    """Attention, then the KV append, in one call (the append rides in the merge kernel)."""
+    check(lib().rl_hip_decode_step(C.byref(attn), C.byref(append)), "rl_hip_decode_step")
 
 
 # ---------------------------------------------------------------- hw_desc rings

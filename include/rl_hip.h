@@ -314,4 +314,15 @@ typedef struct {
 
 int rl_hip_kv_append(const rl_kv_append_args_t *args);
 
+/* ---- fused decode step: attention, then the KV append ---------------------
+ * Replaces the per-descriptor decode of process_descriptor
+ * (cu/worker.cu:25-64: attention_decode_step_fixed128 over the rollout's
+ * cached tokens) followed by the append of the step's K/V token (the
+ * copy-on-write of cu/kv_prefix.cu:4-23), batched. Results equal
+ * rl_hip_attn_decode(attn) then rl_hip_kv_append(append) byte for byte: the
+ * append runs inside the attention's merge kernel, after every context has
+ * been read, so the step takes one launch less. append->batch and kv_heads
+ * must equal attn's. */
+int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append);
+
 RL_EXTERN_C_END
