@@ -20,10 +20,11 @@ in child processes measure the attention call's HBM traffic, calibrated on a
 256 MiB device copy in the same pass (--no-traffic skips them).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append|copy]
-  python bench.py --workload sample256|longctx|proj|plumbing|rollout
+  python bench.py --workload sample256|longctx|proj|plumbing|rollout|cmdring
       the other synthetic workloads (sampling at 256 rows, long-context
       split-KV decode, the vocabulary projection, the hw_desc ring plumbing
-      decode, the GRPO rollout loop), one JSON line each
+      decode, the GRPO rollout loop, the v0.2 command/completion rings), one
+      JSON line each
 """
 import argparse
 import json
@@ -470,6 +471,94 @@ def wl_plumbing(args):
             "note": "host side polls the completion ring from Python (ctypes)"}
 
 
+def wl_cmdring(args):
+    """The v0.2 path: Descriptors in decode_batch windows of 32 through a
+    CommandRing to the persistent worker (fixed128 decode step per
+    descriptor: one head, d128, fp16 K/V ~N(0,1) in 16 KiB arena blocks,
+    seq_len 32, q from the q buffer) and Completions back. Pipelined: 4,096
+    descriptors submitted as fast as the ring takes them; lock-step: one
+    descriptor at a time, submit to completion."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    nblk, io, total = 256, 64, 4096
+    rng = np.random.default_rng(71)
+    arena = synth.f32_to_f16(rng.standard_normal(nblk * 8192, dtype=np.float32))
+    qf = synth.f32_to_f16(rng.standard_normal((io, 128), dtype=np.float32))
+    darena, dq = rlrt.DeviceBuffer.from_array(arena), rlrt.DeviceBuffer.from_array(qf)
+    do, stats = rlrt.DeviceBuffer(io * 128 * 4), rlrt.DeviceBuffer(32, zero=True)
+    ring, cr = L.ring_create(), L.comp_ring_create()
+
+    def coherent(n):
+        p = L.rl_hip_host_alloc_coherent(n)
+        if not p:
+            raise rlrt.RlrtError("coherent host allocation failed")
+        return p
+
+    pairs, stop = coherent(16), coherent(64)
+    C.cast(pairs, C.POINTER(C.c_void_p))[0] = ring
+    C.cast(pairs, C.POINTER(C.c_void_p))[1] = cr
+    a = rlrt.CmdWorkerArgs(rings=pairs, comp_rings=pairs + 8, groups=1, stop=stop, max_idle_polls=1 << 24,
+                           arena_base=darena.ptr, arena_bytes=darena.nbytes, sample_state=None, q_buffer=dq.ptr,
+                           o_buffer=do.ptr, io_slots=io, stats=stats.ptr)
+    batch = rlrt.DecodeDispatchBatch()
+
+    def submit(first, n):
+        L.decode_batch_reset(C.byref(batch))
+        for k in range(first, first + n):
+            d = rlrt.Descriptor(seq_id=k, kv_block_offset=k % nblk, num_kv_blocks=32, output_token_offset=k,
+                                reward_cookie=k)
+            L.decode_batch_push(C.byref(batch), C.byref(d))
+        return L.decode_batch_submit(ring, C.byref(batch)) == 0
+
+    def drain():
+        n = 0
+        while True:
+            head, tail = L.hw_ring_load_acquire(cr), L.hw_ring_load_acquire(cr + 64)
+            if head == tail:
+                return n
+            n += (tail - head) & 0xFFFFFFFF
+            L.hw_ring_store_release(cr, tail)
+
+    rlrt.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
+    lat = []
+    try:
+        t0 = time.perf_counter()
+        sent = done = 0
+        while done < total and time.perf_counter() - t0 < 30:
+            if sent < total and submit(sent, 32):
+                sent += 32
+            done += drain()
+        pipelined = time.perf_counter() - t0
+        for k in range(200):
+            t1 = time.perf_counter()
+            submit(total + k, 1)
+            while drain() == 0:
+                if time.perf_counter() - t1 > 5:
+                    raise rlrt.RlrtError("lock-step completion timed out")
+            lat.append(time.perf_counter() - t1)
+        submit_sentinel = rlrt.Descriptor(seq_id=2**64 - 1)
+        L.decode_batch_reset(C.byref(batch))
+        L.decode_batch_push(C.byref(batch), C.byref(submit_sentinel))
+        L.decode_batch_submit(ring, C.byref(batch))
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rlrt.sync()
+    st = stats.download(np.uint64, 4)
+    for b in (darena, dq, do, stats):
+        b.close()
+    L.ring_destroy(ring)
+    L.comp_ring_destroy(cr)
+    L.rl_hip_host_free(pairs)
+    L.rl_hip_host_free(stop)
+    lat_us = np.array(lat) * 1e6
+    return {"workload": "cmdring_fixed128_d128_fp16_seq32_windows32", "descriptors": total,
+            "pipelined_descriptors_per_s": total / pipelined, "pipelined_ms": pipelined * 1e3,
+            "lockstep_latency_us": {"p50": float(np.percentile(lat_us, 50)), "p90": float(np.percentile(lat_us, 90)),
+                                    "p99": float(np.percentile(lat_us, 99))},
+            "worker_stats": st.tolist(), "note": "host side in Python (ctypes) on both ends of the rings"}
+
+
 def wl_rollout(args):
     """512 GRPO requests (64 groups of 8, shared 512-token prefix, U[0,512]
     private prompt tokens, 256 generated tokens each) through the request
@@ -491,7 +580,7 @@ def wl_rollout(args):
 
 
 WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
-             "rollout": wl_rollout}
+             "rollout": wl_rollout, "cmdring": wl_cmdring}
 
 
 def main():

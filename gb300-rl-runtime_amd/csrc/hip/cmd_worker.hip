@@ -1,0 +1,369 @@
+// cmd_worker.hip - the persistent gfx950 worker on the v0.2 rings: 32-byte
+// Descriptors in from a CommandRing, 32-byte Completions out to a
+// CompletionRing, both in fine-grained coherent host memory.
+//
+// Replaces decode_worker / process_descriptor (cu/worker.cu:25-131: one warp
+// per SM, lane 0 consumes one descriptor at a time, runs
+// attention_decode_step_fixed128 and pushes the completion) with one
+// persistent workgroup (4 wave64s) per ring pair - the single consumer of its
+// command ring and the single producer of its completion ring, so the SPSC
+// contract of ring.h / completion.h holds on the device side:
+//
+//  poll    lane 0 of wave 0 reads the producer's tail with system-scope loads
+//          (the stop flag only while the ring is empty); after the acquire the
+//          whole window of descriptors already committed - up to 32, the
+//          decode_batch window (src/decode_batch.c:3-51) - is read with one
+//          16-byte load per lane, and the head is released once.
+//  decode  wave w takes descriptors w, w + 4, ... of the window: the fixed128
+//          step of the reference (cu/attention_decode.cu:60-204) - one head,
+//          d128, fp16 K/V of arena block kv_block_offset (K plane, V plane at
+//          +8 KiB, 32 tokens), seq_len = num_kv_blocks clamped to [1, 32]
+//          ("seq_len" is what the reference passes there), q from slot
+//          output_token_offset & (io_slots - 1) of the q buffer or the
+//          reference's synthesized query, fp32 softmax(q K^T / sqrt(128)) V to
+//          the o buffer, token = the lowest index of the output's maximum,
+//          cycles = tiles * 128 * 24.
+//  publish wave 0 writes the window's completions {seq_id, token_id,
+//          kv_block_offset, reward_cookie, cycles} in descriptor order with
+//          one 16-byte store per lane and release-stores tail + n at system
+//          scope. A descriptor with seq_id == UINT64_MAX is consumed and ends
+//          the worker without a completion, as in the reference; the ones
+//          before it in its window are completed first.
+//  exit    also on the host's stop flag, after max_idle_polls empty polls, or
+//          when the completion ring stays full for as long (stats status).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "completion.h"
+#include "descriptor.h"
+#include "ring.h"
+#include "rl_dev_common.h"
+#include "rl_hip.h"
+#include "rl_hip_internal.h"
+#include "sample.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr uint32_t kWindow = 32;          // descriptors per poll at most (the decode_batch window)
+constexpr uint32_t kD = 128;              // fixed128 head dim
+constexpr uint32_t kTokens = 32;          // tokens per fixed128 block
+constexpr uint32_t kRowBytes = kD * 2;    // fp16
+constexpr uint32_t kBlockBytes = 2 * kTokens * kRowBytes;  // 16 KiB: K plane, V plane
+constexpr uint64_t kDefaultIdlePolls = 1ull << 22;
+
+enum : uint32_t { kStatusStopped = 0, kStatusIdle = 1, kStatusCompFull = 3 };
+
+struct CmdParams {
+    CommandRing *const *rings;
+    CompletionRing *const *comp_rings;
+    const volatile uint32_t *stop;
+    uint64_t max_idle_polls;
+    const uint8_t *arena;
+    uint64_t arena_blocks;
+    const SampleState *sample_state;
+    const uint16_t *q;
+    float *o;
+    uint32_t io_mask;
+    uint64_t *stats;
+};
+
+__device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
+{
+    return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ void sys_store_release(volatile uint32_t *p, uint32_t v)
+{
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+    v = rl_row_sum(v);
+    return (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))) +
+           (__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48)));
+}
+
+// The reference's query when no q buffer is given
+// (decode_synth_query_component, cu/attention_decode.cu:16-28).
+__device__ __forceinline__ float synth_query(const Descriptor &d, const SampleState *st, uint32_t idx)
+{
+    uint64_t seed = d.seq_id ^ d.reward_cookie ^ ((uint64_t)(idx + 1u) * 0x9e3779b97f4a7c15ull);
+    if (st)
+        seed ^= st->rng_state[idx & 3u];
+    const uint32_t bits = (uint32_t)(seed ^ (seed >> 32));
+    const int centered = (int)(bits & 0xFFu) - 127;
+    return (float)centered / 127.0f;
+}
+
+// One fixed128 decode step by one wave; lane l owns dims 2l and 2l + 1.
+// Returns the completion record's token and cycle fields.
+__device__ void fixed128_step(const CmdParams &p, const Descriptor &d, int lane, uint32_t &token, uint64_t &cycles)
+{
+    const uint32_t seq = d.num_kv_blocks == 0 ? 1u : (d.num_kv_blocks > kTokens ? kTokens : d.num_kv_blocks);
+    const uint32_t slot = d.output_token_offset & p.io_mask;
+    const bool bad = d.kv_block_offset >= p.arena_blocks;
+    const uint8_t *blk = p.arena + (uint64_t)(bad ? 0u : d.kv_block_offset) * kBlockBytes;
+
+    // every K and V word of the block, issued before the first use
+    uint32_t kw[kTokens], vw[kTokens];
+#pragma unroll
+    for (uint32_t t = 0; t < kTokens; t++) {
+        kw[t] = *(const RL_GLOBAL uint32_t *)(blk + t * kRowBytes + lane * 4u);
+        vw[t] = *(const RL_GLOBAL uint32_t *)(blk + kTokens * kRowBytes + t * kRowBytes + lane * 4u);
+    }
+    float q0, q1;
+    if (p.q) {
+        const uint32_t qw = *(const RL_GLOBAL uint32_t *)(p.q + (size_t)slot * kD + 2u * lane);
+        rl_unpack2<1>(qw, q0, q1);
+    } else {
+        q0 = synth_query(d, p.sample_state, 2u * lane);
+        q1 = synth_query(d, p.sample_state, 2u * lane + 1u);
+    }
+    const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
+    float s[kTokens];
+    float m = -INFINITY;
+#pragma unroll
+    for (uint32_t t = 0; t < kTokens; t++) {
+        float k0, k1;
+        rl_unpack2<1>(kw[t], k0, k1);
+        const float dot = wave_sum(fmaf(q1, k1, q0 * k0)) * scale;
+        s[t] = t < seq ? dot : -INFINITY;
+        m = fmaxf(m, s[t]);
+    }
+    float o0 = 0.f, o1 = 0.f, l = 0.f;
+#pragma unroll
+    for (uint32_t t = 0; t < kTokens; t++) {
+        const float e = t < seq ? __expf(s[t] - m) : 0.f;
+        float v0, v1;
+        rl_unpack2<1>(vw[t], v0, v1);
+        l += e;
+        o0 = fmaf(e, v0, o0);
+        o1 = fmaf(e, v1, o1);
+    }
+    o0 /= l;
+    o1 /= l;
+    if (bad) {
+        o0 = __builtin_nanf("");
+        o1 = o0;
+    }
+    if (p.o) {
+        float *orow = p.o + (size_t)slot * kD;
+        orow[2u * lane] = o0;
+        orow[2u * lane + 1u] = o1;
+    }
+    // lowest index of the maximum (the pair's first element wins a tie)
+    float best = o1 > o0 ? o1 : o0;
+    uint32_t bidx = o1 > o0 ? 2u * lane + 1u : 2u * lane;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ob = __shfl_xor(best, off);
+        const uint32_t oi = __shfl_xor(bidx, off);
+        if (ob > best || (ob == best && oi < bidx)) {
+            best = ob;
+            bidx = oi;
+        }
+    }
+    token = bad ? 0u : bidx;
+    cycles = (uint64_t)((seq + 15u) / 16u) * kD * 24u;
+}
+
+__global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
+{
+    __shared__ __attribute__((aligned(16))) Descriptor s_desc[kWindow];
+    __shared__ __attribute__((aligned(16))) Completion s_comp[kWindow];
+    __shared__ uint32_t s_ctl[2];  // descriptors to run, exit flag
+
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    CommandRing *ring = p.rings[blockIdx.x];
+    CompletionRing *cr = p.comp_rings[blockIdx.x];
+
+    uint64_t descs = 0, completions = 0, windows = 0;
+    uint32_t status = kStatusStopped;
+    uint32_t head = 0, ctail = 0;  // lane 0 of wave 0: this worker owns cons.head and the completion tail
+    if (tid == 0) {
+        head = sys_load(&ring->cons.head);
+        ctail = sys_load(&cr->prod.tail);
+    }
+
+    for (;;) {
+        // ---- the committed window at the head (wave 0) ------------------------
+        if (wave == 0) {
+            uint32_t avail = 0, ctl = 0;
+            if (lane == 0) {
+                uint64_t idle = 0;
+                for (;;) {
+                    avail = sys_load(&ring->prod.tail) - head;
+                    if (avail != 0)
+                        break;
+                    if (sys_load(p.stop) != 0) {
+                        ctl = 1;
+                        break;
+                    }
+                    if (++idle > p.max_idle_polls) {
+                        ctl = 1;
+                        status = kStatusIdle;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            avail = rl_readlane(avail, 0);
+            ctl = rl_readlane(ctl, 0);
+            uint32_t n = 0;
+            if (!ctl) {
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+                const uint32_t h = rl_readlane(head, 0);
+                // the window ends where the ring wraps or after kWindow descriptors
+                n = min(min(avail, kWindow), RING_SIZE - (h & (RING_SIZE - 1)));
+                if ((uint32_t)lane < 2 * n) {
+                    const volatile rl_u32x4 *src = (const volatile rl_u32x4 *)&ring->slots[h & (RING_SIZE - 1)];
+                    ((rl_u32x4 *)s_desc)[lane] = src[lane];
+                }
+                rl_wave_lds_fence();
+                // a shutdown sentinel ends the window (it is consumed, not run)
+                uint32_t run = n;
+                for (uint32_t i = 0; i < n; i++)
+                    if (s_desc[i].seq_id == ~0ull) {
+                        run = i;
+                        ctl = 1;
+                        n = i + 1;
+                        break;
+                    }
+                if (lane == 0) {
+                    head += n;
+                    sys_store_release(&ring->cons.head, head);
+                }
+                n = run;
+            }
+            if (lane == 0) {
+                s_ctl[0] = n;
+                s_ctl[1] = ctl;
+            }
+        }
+        __syncthreads();
+        const uint32_t n = s_ctl[0];
+        const uint32_t stop_now = s_ctl[1];
+
+        // ---- decode: one descriptor per wave at a time ---------------------------
+        for (uint32_t i = wave; i < n; i += kWaves) {
+            const Descriptor d = s_desc[i];
+            uint32_t token;
+            uint64_t cycles;
+            fixed128_step(p, d, lane, token, cycles);
+            if (lane == 0) {
+                Completion c;
+                c.seq_id = d.seq_id;
+                c.token_id = token;
+                c.kv_block_offset = d.kv_block_offset;
+                c.reward_cookie = d.reward_cookie;
+                c.cycles_taken = cycles;
+                s_comp[i] = c;
+            }
+        }
+        __syncthreads();
+
+        // ---- publish the window's completions (wave 0), bounded wait while full --
+        uint32_t fail = 0;
+        if (wave == 0 && n) {
+            uint32_t room = 0;
+            if (lane == 0) {
+                uint64_t idle = 0;
+                for (;;) {
+                    if (ctail - sys_load(&cr->cons.head) <= (uint32_t)COMP_RING_SIZE - n) {
+                        room = 1;
+                        break;
+                    }
+                    if (sys_load(p.stop) != 0)
+                        break;
+                    if (++idle > p.max_idle_polls) {
+                        status = kStatusCompFull;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                }
+            }
+            if (rl_readlane(room, 0)) {
+                const uint32_t t = rl_readlane(ctail, 0);
+                // two lanes per record; records may wrap around the ring
+                if ((uint32_t)lane < 2 * n) {
+                    const uint32_t rec = (uint32_t)lane / 2;
+                    volatile rl_u32x4 *dst = (volatile rl_u32x4 *)&cr->slots[(t + rec) & (COMP_RING_SIZE - 1)];
+                    dst[lane & 1] = ((const rl_u32x4 *)s_comp)[lane];
+                }
+                if (lane == 0) {
+                    ctail += n;
+                    sys_store_release(&cr->prod.tail, ctail);
+                }
+            } else {
+                fail = 1;
+            }
+            if (lane == 0)
+                s_ctl[1] = fail;
+        }
+        if (n) {
+            __syncthreads();
+            fail = s_ctl[1];
+        }
+        descs += n;
+        if (!fail && n) {
+            completions += n;
+            windows++;
+        }
+        if (stop_now || fail)
+            break;
+        __syncthreads();  // s_desc / s_ctl are rewritten by the next poll
+    }
+    if (tid == 0) {
+        uint64_t *st = p.stats + (size_t)blockIdx.x * 4;
+        st[0] = descs;
+        st[1] = completions;
+        st[2] = windows;
+        st[3] = status;
+    }
+}
+
+}  // namespace
+
+extern "C" int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *a)
+{
+    if (rl_require_open("rl_hip_cmd_worker_launch"))
+        return -1;
+    if (!a || !a->rings || !a->comp_rings || !a->stop || !a->stats || !a->arena_base) {
+        rl_set_error("rl_hip_cmd_worker_launch: NULL argument");
+        return -1;
+    }
+    if (a->groups == 0 || a->groups > 65535) {
+        rl_set_error("rl_hip_cmd_worker_launch: groups %u out of range", a->groups);
+        return -1;
+    }
+    if (a->io_slots & (a->io_slots - 1)) {
+        rl_set_error("rl_hip_cmd_worker_launch: io_slots %u is not a power of two", a->io_slots);
+        return -1;
+    }
+    if (a->arena_bytes < kBlockBytes) {
+        rl_set_error("rl_hip_cmd_worker_launch: arena of %llu bytes holds no 16 KiB block",
+                     (unsigned long long)a->arena_bytes);
+        return -1;
+    }
+    CmdParams p;
+    p.rings = a->rings;
+    p.comp_rings = a->comp_rings;
+    p.stop = a->stop;
+    p.max_idle_polls = a->max_idle_polls ? a->max_idle_polls : kDefaultIdlePolls;
+    p.arena = (const uint8_t *)a->arena_base;
+    p.arena_blocks = a->arena_bytes / kBlockBytes;
+    p.sample_state = a->sample_state;
+    p.q = (const uint16_t *)a->q_buffer;
+    p.o = a->o_buffer;
+    p.io_mask = a->io_slots ? a->io_slots - 1 : 0;
+    p.stats = a->stats;
+    hipLaunchKernelGGL(cmd_worker_kernel, dim3(a->groups), dim3(kThreads), 0, rl_stream(), p);
+    return rl_check_launch("cmd_worker_kernel launch");
+}

@@ -184,6 +184,13 @@ class HwWorkerArgs(C.Structure):
                 ("stats", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
 
+class CmdWorkerArgs(C.Structure):
+    _fields_ = [("rings", C.c_void_p), ("comp_rings", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
+                ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
+                ("sample_state", C.c_void_p), ("q_buffer", C.c_void_p), ("o_buffer", C.c_void_p),
+                ("io_slots", C.c_uint32), ("stats", C.c_void_p)]
+
+
 DTYPE_BF16 = 0
 DTYPE_FP16 = 1
 
@@ -215,6 +222,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
         "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
+        "rl_hip_cmd_worker_launch": (i32, [C.POINTER(CmdWorkerArgs)]),
         # reference host API
         "hw_ring_create": (vp, []), "hw_ring_reset": (None, [vp]), "hw_ring_destroy": (None, [vp]),
         "hw_ring_load_acquire": (u32, [vp]), "hw_ring_store_release": (None, [vp, u32]),

@@ -23,6 +23,8 @@
 #include "kv_layout.h"
 #include "request.h"
 #include "reward.h"
+#include "ring.h"
+#include "sample.h"
 
 RL_EXTERN_C_BEGIN
 
@@ -256,6 +258,42 @@ typedef struct {
 
 size_t rl_hip_hw_worker_workspace(const rl_hw_worker_args_t *args);
 int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
+
+/* ---- persistent worker on the v0.2 command / completion rings ---------------
+ * Replaces decode_worker and process_descriptor (cu/worker.cu:25-131): one
+ * persistent workgroup per (CommandRing, CompletionRing) pair - the single
+ * consumer and the single producer of that pair - that takes every window of
+ * committed Descriptors at the head (up to 32, the decode_batch window),
+ * runs the fixed128 decode step of each (attention_decode_step_fixed128,
+ * cu/attention_decode.cu:60-204: one head, d128, fp16 K/V of the 16 KiB arena
+ * block kv_block_offset, seq_len = num_kv_blocks clamped to [1, 32], q from
+ * q_buffer slot output_token_offset & (io_slots - 1) or, with no q buffer,
+ * the reference's synthesized query seeded by seq_id, reward_cookie and
+ * sample_state->rng_state; fp32 output to the o buffer; token = lowest index
+ * of the output's maximum; cycles = ceil(seq_len / 16) * 128 * 24) and
+ * pushes the Completions {seq_id, token_id, kv_block_offset, reward_cookie,
+ * cycles} in descriptor order. seq_id == UINT64_MAX is consumed and stops the
+ * worker without a completion. A block past arena_bytes gives NaN outputs and
+ * token 0 (it is not read). The launch returns at once; rl_hip_sync() waits
+ * for every worker to exit (sentinel, *stop, max_idle_polls empty polls, or
+ * a completion ring full for as long). stats per group: {descriptors run,
+ * completions pushed, windows, status (0 stopped, 1 idle, 3 ring full)}. */
+typedef struct {
+    CommandRing *const *rings;          /* coherent host [groups] (ring_create after rl_hip_open) */
+    CompletionRing *const *comp_rings;  /* coherent host [groups] (comp_ring_create) */
+    uint32_t groups;
+    const volatile uint32_t *stop;      /* coherent host: nonzero ends every worker */
+    uint64_t max_idle_polls;            /* 0 selects 2^22 */
+    const void *arena_base;             /* device: fixed128 blocks of 16,384 bytes */
+    uint64_t arena_bytes;
+    const SampleState *sample_state;    /* device, optional (synthesized queries only) */
+    const void *q_buffer;               /* device fp16 [io_slots][128], or NULL */
+    float *o_buffer;                    /* device fp32 [io_slots][128], or NULL */
+    uint32_t io_slots;                  /* a power of two; 0 uses slot 0 */
+    uint64_t *stats;                    /* device [groups][4] */
+} rl_cmd_worker_args_t;
+
+int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *args);
 
 /* ---- sampling -------------------------------------------------------------
  * Replaces sample_token (cu/sample.cu:41-123) with the specification in

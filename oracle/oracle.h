@@ -96,6 +96,8 @@ void orc_attn_decode_f64(const orc_attn_t *a, double *out);
 /* fp32 online softmax over 16-token tiles, OpenMP over (rollout, kv head):
  * the CPU baseline of the decode step. */
 void orc_attn_decode_f32(const orc_attn_t *a, float *out);
+/* decode_synth_query_component (cu/attention_decode.cu:16-28); rng_state may be NULL */
+float orc_synth_query(uint64_t seq_id, uint64_t reward_cookie, const uint64_t *rng_state, uint32_t idx);
 
 /* ---- sampling (specification in include/sample.h) ----
  * greedy != 0 or temperature <= 0: argmax, lowest index.

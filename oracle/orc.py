@@ -45,6 +45,7 @@ def load_oracle() -> C.CDLL:
     vp, u32, u64, i64, i32 = C.c_void_p, C.c_uint32, C.c_uint64, C.c_int64, C.c_int
     sigs = {
         "orc_hw_ring_push": (i32, [vp, vp]), "orc_hw_ring_pop": (i32, [vp, vp]),
+        "orc_synth_query": (C.c_float, [u64, u64, vp, u32]),
         "orc_submit_decode": (i64, [vp, u32, u32, u32, u64, u64, u32, u32, u32]),
         "orc_worker_sim_drain": (u64, [vp, vp, C.POINTER(u64), C.POINTER(i32)]),
         "orc_ring_acquire": (u32, [vp, C.POINTER(RingShape), u32]),

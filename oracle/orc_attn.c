@@ -160,3 +160,19 @@ orc_attn_decode_f32(const orc_attn_t *a, float *out)
         }
     }
 }
+
+/* The fixed128 step's query when no q buffer is given
+ * (decode_synth_query_component, cu/attention_decode.cu:16-28):
+ * seed = seq_id ^ reward_cookie ^ (idx + 1) * 0x9e3779b97f4a7c15
+ * [^ rng_state[idx & 3]]; bits = low 32 of seed ^ (seed >> 32);
+ * q = ((bits & 0xFF) - 127) / 127. */
+float
+orc_synth_query(uint64_t seq_id, uint64_t reward_cookie, const uint64_t *rng_state, uint32_t idx)
+{
+    uint64_t seed = seq_id ^ reward_cookie ^ ((uint64_t)(idx + 1u) * 0x9e3779b97f4a7c15ULL);
+    if (rng_state)
+        seed ^= rng_state[idx & 3u];
+    const uint32_t bits = (uint32_t)(seed ^ (seed >> 32));
+    const int centered = (int)(bits & 0xFFu) - 127;
+    return (float)centered / 127.0f;
+}

@@ -174,6 +174,25 @@ def test_attention_oracle_fixed128_closed_form(orc, olib, rl):
     assert int(np.argmax(o64)) == int(np.argmax(ref))  # lowest-index argmax token
 
 
+def test_synth_query_known_values(olib):
+    """decode_synth_query_component (cu/attention_decode.cu:16-28), values
+    worked out by hand: with seq_id = cookie = 0 the seed of component idx is
+    (idx + 1) * 0x9e3779b97f4a7c15 mod 2^64; idx 0: 0x9e3779b97f4a7c15, folded
+    0x7f4a7c15 ^ 0x9e3779b9 = 0xe17d05ac, low byte 0xac = 172 -> 45/127;
+    idx 1: 0x3c6ef372fe94f82a, folded 0xc2fa0b58, 0x58 = 88 -> -39/127. A
+    sample state xors rng_state[idx & 3] into the seed: rng_state[0] = 1 turns
+    idx 0's low byte into 0xad -> 46/127, and rng_state[1] = 0x100 leaves
+    idx 1's low byte alone (-39/127)."""
+    f = np.float32
+    assert olib.orc_synth_query(0, 0, None, 0) == f(45) / f(127)
+    assert olib.orc_synth_query(0, 0, None, 1) == f(-39) / f(127)
+    st = np.array([1, 0x100, 0, 0], dtype=np.uint64)
+    assert olib.orc_synth_query(0, 0, st.ctypes.data, 0) == f(46) / f(127)
+    assert olib.orc_synth_query(0, 0, st.ctypes.data, 1) == f(-39) / f(127)
+    # seq_id and cookie enter the seed symmetrically
+    assert olib.orc_synth_query(5, 9, None, 7) == olib.orc_synth_query(9, 5, None, 7)
+
+
 def _numpy_paged(w):
     import synth
     f = synth.bf16_to_f32 if w.dtype == "bf16" else synth.f16_to_f32
