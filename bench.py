@@ -20,7 +20,7 @@ in child processes measure the attention call's HBM traffic, calibrated on a
 256 MiB device copy in the same pass (--no-traffic skips them).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append|copy]
-  python bench.py --workload sample256|longctx|proj|plumbing|rollout|cmdring
+  python bench.py --workload sample256|longctx|proj|plumbing|rollout|rollout_pipeline|cmdring|pipeline
       the other synthetic workloads (sampling at 256 rows, long-context
       split-KV decode, the vocabulary projection, the hw_desc ring plumbing
       decode, the GRPO rollout loop, the v0.2 command/completion rings), one
@@ -579,8 +579,76 @@ def wl_rollout(args):
             "steady_tokens_per_s": grpo.SLOTS / res["window_us_per_step"] * 1e6}
 
 
+def wl_rollout_pipeline(args):
+    """The GRPO run of the rollout workload with its request ring fed by the
+    host rollout pipeline (384 decode credits; retire, admit and send at each
+    done poll) instead of one upfront burst."""
+    import grpo
+
+    cfg = grpo.build_workload(404)
+    loop = grpo.RolloutLoop(cfg)
+    loop.attach_pipeline(decode_credits=384)
+    res = loop.run()
+    st = loop.feeder.stats
+    stats = {k: getattr(st, k) for k, _ in st._fields_}
+    loop.close()
+    gen_tokens = grpo.REQ * grpo.GEN
+    return {"workload": "grpo_512req_pipeline_fed_credits384", "steps": res["steps"], "wall_s": res["wall_s"],
+            "generated_tokens_per_s": gen_tokens / res["wall_s"], "steady_us_per_step": res["window_us_per_step"],
+            "feeder": stats}
+
+
+def wl_pipeline(args):
+    """bench/bench_pipeline.cu's run: 1,000 rollouts x 128 decode tokens
+    through the host rollout pipeline (credits 256/128/128/1024, decode
+    batches of 32 rollouts, decode_batch windows of 32 descriptors) into the
+    command ring, natively (rl_pipeline_cmd_run); the persistent worker runs
+    the fixed128 step of each descriptor (one KV token of one of 128 arena
+    blocks, fp16, synthesized query) and the same host thread drains the
+    completions. Tokens/s = descriptors completed / wall time."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    n, tokens, nblk, io = 1000, 128, 128, 4096
+    rng = np.random.default_rng(81)
+    arena = synth.f32_to_f16(rng.standard_normal(nblk * 8192, dtype=np.float32))
+    import struct
+
+    seed, m64 = 42, 2**64 - 1                   # SampleState as bench/bench_pipeline.cu:108-117 fills it
+    st = np.frombuffer(struct.pack("<4QfH2xfI", seed, seed ^ 0x9E3779B97F4A7C15,
+                                   ((seed << 17) ^ 0x3C6EF372FE94F82A) & m64, ~seed & m64, 1.0, 50, 0.9, 128256),
+                       np.uint8).copy()
+    darena, dst = rlrt.DeviceBuffer.from_array(arena), rlrt.DeviceBuffer.from_array(st)
+    pipe = np.zeros(rlrt.PIPELINE_BYTES, np.uint8)
+    rew = np.zeros(rlrt.REWARD_RING_BYTES, np.uint8)
+    L.pipeline_init(pipe.ctypes.data)
+    L.reward_ring_init(rew.ctypes.data)
+    cfg = rlrt.CmdPipelineCfg(n_rollouts=n, tokens_per_rollout=tokens, batch_max=32, kv_blocks=nblk,
+                              max_decode_credits=256, max_reward_credits=128, max_trajectory_credits=128,
+                              kv_block_limit=1024, seed_base=42, full_wait_ns=10**10, drain_wait_ns=10**10)
+    stats = rlrt.CmdPipelineStats()
+    w = rlrt.CmdWorker(darena, io, sample_state=dst)
+    try:
+        rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, w.ring, w.comp, rew.ctypes.data, C.byref(cfg),
+                                   C.byref(stats), None, 0)
+    finally:
+        wst = w.stop()
+        w.close()
+    darena.close()
+    dst.close()
+    if rc != 0:
+        raise rlrt.RlrtError(f"rl_pipeline_cmd_run: {stats.descriptors_consumed} of {stats.descriptors_posted}")
+    sd = {k: getattr(stats, k) for k, _ in stats._fields_}
+    return {"workload": "pipeline_1000rollouts_x128tok_fixed128_cmdring", "rc": rc,
+            "tokens_per_s": stats.descriptors_consumed / (stats.wall_ns * 1e-9),
+            "rollouts_per_s": stats.rollouts_completed / (stats.wall_ns * 1e-9), "wall_ms": stats.wall_ns * 1e-6,
+            "stats": sd, "worker_stats": wst.tolist(),
+            "note": "host loop native (C); one persistent worker workgroup"}
+
+
 WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
-             "rollout": wl_rollout, "cmdring": wl_cmdring}
+             "rollout": wl_rollout, "cmdring": wl_cmdring, "rollout_pipeline": wl_rollout_pipeline,
+             "pipeline": wl_pipeline}
 
 
 def main():

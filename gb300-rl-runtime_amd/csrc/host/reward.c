@@ -1,10 +1,42 @@
 /*
- * reward.c - reward rule (reference src/reward.c:36-41) and group advantage.
+ * reward.c - the reward handoff ring (reference src/reward.c:5-34), the
+ * reward rule (src/reward.c:36-41) and the group advantage.
  */
 #include <math.h>
 #include <stddef.h>
+#include <string.h>
 
 #include "reward.h"
+#include "spsc_index.h"
+
+void
+reward_ring_init(RewardRing *r)
+{
+    if (r)
+        memset(r, 0, sizeof(*r));
+}
+
+int
+reward_push(RewardRing *r, const RewardDesc *d)
+{
+    uint32_t slot;
+    if (!r || !d || spsc_reserve(&r->prod.head, &r->cons.tail, REWARD_RING_SIZE, &slot) != 0)
+        return -1;
+    r->slots[slot] = *d;
+    spsc_publish(&r->prod.head);
+    return 0;
+}
+
+int
+reward_pop(RewardRing *r, RewardDesc *d)
+{
+    uint32_t slot;
+    if (!r || !d || spsc_peek(&r->prod.head, &r->cons.tail, REWARD_RING_SIZE, &slot) != 0)
+        return -1;
+    *d = r->slots[slot];
+    spsc_retire(&r->cons.tail);
+    return 0;
+}
 
 float
 reward_score_mock(const void *tokens, uint32_t n)

@@ -149,6 +149,7 @@ class RolloutLoop:
         self.kv_row = SLOTS * KVH * D * 2
         self.dones: list[tuple] = []
         self.t = 0
+        self.feeder = None
 
     def submit_requests(self) -> None:
         """512 requests (temperature 1, top-p 0.9, per-request seed) and the end marker."""
@@ -160,6 +161,45 @@ class RolloutLoop:
                 raise rlrt.RlrtError("request ring full")
         if req_ring_push(self.rr, rlrt.RolloutRequest(request_id=2**64 - 1)) != 0:
             raise rlrt.RlrtError("request ring full")
+
+    def attach_pipeline(self, decode_credits: int = 384) -> None:
+        """Feed the request ring from the host rollout pipeline (pipeline.h /
+        pipeline_feed.h) instead of one upfront burst: every request is
+        registered as a rollout (FREE -> PREFILL_READY, Q_PREFILL); each done
+        poll retires the dones (reward handoff on the RewardRing, the rollout
+        freed, its decode credit returned), admits rollouts to Q_DECODE while
+        decode credits last and sends them FIFO. decode_credits bounds the
+        rollouts queued on or running in the device (256 slots)."""
+        L = rlrt.lib()
+        cfg = self.cfg
+        self.pipe = np.zeros(rlrt.PIPELINE_BYTES, np.uint8)
+        self.reward_ring = np.zeros(rlrt.REWARD_RING_BYTES, np.uint8)
+        self.rid_map = np.zeros(REQ, np.uint32)
+        if L.pipeline_init(self.pipe.ctypes.data) != 0:
+            raise rlrt.RlrtError("pipeline_init failed")
+        L.pipeline_credits_set(self.pipe.ctypes.data, decode_credits, 0, 0, 0)
+        L.reward_ring_init(self.reward_ring.ctypes.data)
+        self.feeder = rlrt.PipelineFeeder()
+        fp = rlrt.FeedParams(temperature=1.0, top_k=0, top_p=0.9, block_tokens=TPB)
+        if L.rl_feed_init(C.byref(self.feeder), self.pipe.ctypes.data, self.rr, self.dr,
+                          self.reward_ring.ctypes.data, self.rid_map.ctypes.data, REQ, C.byref(fp)) != 0:
+            raise rlrt.RlrtError("rl_feed_init failed")
+        self.request_of_rid = {}
+        for r in range(REQ):
+            rid = L.rl_feed_register(C.byref(self.feeder), r, int(cfg["prompt"][r]), GEN, int(cfg["seeds"][r]))
+            if rid < 0:
+                raise rlrt.RlrtError(f"rl_feed_register({r}) failed")
+            self.request_of_rid[rid] = r
+        self._pump()
+
+    def _pump(self) -> None:
+        L = rlrt.lib()
+        L.rl_feed_pump(C.byref(self.feeder))
+        if self.feeder.stats.sent == REQ:
+            L.rl_feed_end(C.byref(self.feeder))
+        rd = rlrt.RewardDesc()
+        while L.reward_pop(self.reward_ring.ctypes.data, C.byref(rd)) == 0:
+            self.dones.append((self.request_of_rid[rd.rollout_id], None, rd.token_count, rd.reward, rd.flags))
 
     def schedule(self) -> None:
         self.sched.sampled = self.dev["tok"].ptr if self.t > 0 else None
@@ -181,8 +221,11 @@ class RolloutLoop:
     def drain_dones(self) -> np.ndarray:
         """Pops every published RolloutDone; returns the scheduler counters
         {dones, admitted, end seen, status}."""
-        while (d := done_ring_pop(self.dr)) is not None:
-            self.dones.append((d.request_id, d.rollout_id, d.tokens_generated, d.reward, d.status))
+        if self.feeder is not None:
+            self._pump()
+        else:
+            while (d := done_ring_pop(self.dr)) is not None:
+                self.dones.append((d.request_id, d.rollout_id, d.tokens_generated, d.reward, d.status))
         return self.dev["counters"].download(np.uint32, 4)
 
     def finish(self) -> None:

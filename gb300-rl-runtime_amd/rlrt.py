@@ -88,6 +88,62 @@ class RolloutDone(C.Structure):
                 ("reward", C.c_float), ("status", C.c_uint32)]
 
 
+class PipelineCredits(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("max_decode_credits", "max_reward_credits", "max_trajectory_credits",
+                                          "kv_block_limit", "decode_used", "reward_used", "trajectory_used",
+                                          "kv_blocks_used")]
+
+
+class PipelineSnapshot(C.Structure):
+    _fields_ = [("queue_occupancy", C.c_uint32 * 6), ("stage_credit_headroom", C.c_uint32 * 6),
+                ("credits", PipelineCredits), ("policy", C.c_int)]
+
+
+PIPELINE_BYTES = 493376       # sizeof(RolloutPipeline)
+PIPELINE_SLAB_OFF = 99072     # offsetof(RolloutPipeline, slab)
+PIPELINE_CREDITS_OFF = 493312
+PIPELINE_POLICY_OFF = 493344
+REWARD_RING_BYTES = 24704     # sizeof(RewardRing)
+Q_FREE, Q_PREFILL, Q_DECODE, Q_REWARD, Q_TRAJECTORY, Q_DONE = range(6)
+ROLL_FREE, ROLL_PREFILL_READY, ROLL_DECODING, ROLL_REWARD_PENDING, ROLL_TRAJECTORY_READY, ROLL_DONE = range(6)
+
+
+class RewardDesc(C.Structure):
+    _pack_ = 1
+    _fields_ = [("rollout_id", C.c_uint32), ("token_start", C.c_uint32), ("token_count", C.c_uint32),
+                ("reward_model_id", C.c_uint32), ("reward", C.c_float), ("flags", C.c_uint32)]
+
+
+class FeedParams(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("block_tokens", C.c_uint32)]
+
+
+class FeedStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("registered", "admitted", "sent", "retired", "reward_handoffs",
+                                          "reward_ring_full", "bad_dones", "req_ring_full")]
+
+
+class PipelineFeeder(C.Structure):
+    _fields_ = [("pipeline", C.c_void_p), ("requests", C.c_void_p), ("dones", C.c_void_p),
+                ("rewards", C.c_void_p), ("rid_of_request", C.c_void_p), ("n_requests", C.c_uint32),
+                ("end_sent", C.c_uint32), ("params", FeedParams), ("stats", FeedStats)]
+
+
+class CmdPipelineCfg(C.Structure):
+    _fields_ = [(n, C.c_uint32) for n in ("n_rollouts", "tokens_per_rollout", "batch_max", "kv_blocks",
+                                          "max_decode_credits", "max_reward_credits", "max_trajectory_credits",
+                                          "kv_block_limit")] + \
+               [(n, C.c_uint64) for n in ("seed_base", "full_wait_ns", "drain_wait_ns")]
+
+
+class CmdPipelineStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "rollouts_started", "rollouts_completed", "rollouts_dropped", "descriptors_posted",
+        "descriptors_consumed", "decode_batches", "decode_rollouts_scheduled", "decode_batch_peak",
+        "ring_full_spins", "pipeline_overflow", "reward_handoffs", "reward_ring_full", "wall_ns")]
+
+
 class KVPrefix(C.Structure):
     _pack_ = 1
     _fields_ = [("prefix_id", C.c_uint32), ("refcnt", C.c_uint32), ("kv_block_offset", C.c_int64),
@@ -246,6 +302,27 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "kv_branch_alloc": (i32, [vp, u32, u32, i64, u32, u32, C.POINTER(u32)]),
         "kv_branch_free": (i32, [vp, u32]), "kv_branch_get": (C.POINTER(KVBranch), [vp, u32]),
         "kv_branch_total_offset": (i64, [vp, u32]),
+        "rollout_slab_init": (None, [vp]), "rollout_alloc": (i32, [vp, C.POINTER(u32)]),
+        "rollout_free": (None, [vp, u32]), "rollout_get": (vp, [vp, u32]),
+        "rollout_transition": (i32, [vp, i32, i32]),
+        "pipeline_init": (i32, [vp]), "pipeline_push": (i32, [vp, i32, u32]),
+        "pipeline_pop": (i32, [vp, i32, C.POINTER(u32)]), "pipeline_transition": (i32, [vp, u32, i32, i32]),
+        "pipeline_credits_set": (None, [vp, u32, u32, u32, u32]), "pipeline_try_push": (i32, [vp, i32, u32]),
+        "pipeline_release": (None, [vp, i32, u32]), "pipeline_set_schedule_policy": (i32, [vp, i32]),
+        "pipeline_schedule": (i32, [vp, i32, C.POINTER(u32)]), "pipeline_occupancy": (u32, [vp, i32]),
+        "pipeline_stage_available_credits": (u32, [vp, i32]),
+        "pipeline_stage_target_batch": (u32, [vp, i32, u32]),
+        "pipeline_snapshot": (None, [vp, C.POINTER(PipelineSnapshot)]),
+        "reward_ring_init": (None, [vp]), "reward_push": (i32, [vp, C.POINTER(RewardDesc)]),
+        "reward_pop": (i32, [vp, C.POINTER(RewardDesc)]),
+        "rl_feed_init": (i32, [C.POINTER(PipelineFeeder), vp, vp, vp, vp, vp, u32, C.POINTER(FeedParams)]),
+        "rl_feed_register": (i64, [C.POINTER(PipelineFeeder), u32, u32, u32, u64]),
+        "rl_feed_admit": (u32, [C.POINTER(PipelineFeeder), u32]),
+        "rl_feed_send": (u32, [C.POINTER(PipelineFeeder), u32]),
+        "rl_feed_retire": (u32, [C.POINTER(PipelineFeeder)]), "rl_feed_end": (i32, [C.POINTER(PipelineFeeder)]),
+        "rl_feed_pump": (u32, [C.POINTER(PipelineFeeder)]),
+        "rl_pipeline_cmd_run": (i32, [vp, vp, vp, vp, C.POINTER(CmdPipelineCfg), C.POINTER(CmdPipelineStats),
+                                      vp, u64]),
         "reward_score_mock": (C.c_float, [vp, u32]),
         "reward_match_count": (u32, [vp, vp, u32]),
         "reward_group_advantage": (i32, [vp, u32, u32, vp]),
@@ -335,6 +412,57 @@ def open_device(device: int = 0) -> DeviceInfo:
 
 def sync() -> None:
     check(lib().rl_hip_sync(), "rl_hip_sync")
+
+
+class CmdWorker:
+    """One persistent command-ring worker (rl_hip_cmd_worker_launch) on a
+    fresh CommandRing / CompletionRing pair in coherent host memory. q is the
+    query buffer (None: the synthesized query from seq_id, reward_cookie and
+    the sample state's rng words); the o buffer has io_slots rows of 128
+    floats. stop() raises the stop flag and waits for the worker to exit."""
+
+    def __init__(self, arena: DeviceBuffer, io_slots: int, q: DeviceBuffer | None = None,
+                 sample_state: DeviceBuffer | None = None, max_idle_polls: int = 1 << 24):
+        L = lib()
+        self.ring, self.comp = L.ring_create(), L.comp_ring_create()
+        self.pairs = L.rl_hip_host_alloc_coherent(16)
+        self.stop_flag = L.rl_hip_host_alloc_coherent(64)
+        if not (self.ring and self.comp and self.pairs and self.stop_flag):
+            raise RlrtError(f"command-ring worker rings: {_err()}")
+        C.memset(self.stop_flag, 0, 64)
+        C.cast(self.pairs, C.POINTER(C.c_void_p))[0] = self.ring
+        C.cast(self.pairs, C.POINTER(C.c_void_p))[1] = self.comp
+        self.o = DeviceBuffer(io_slots * 128 * 4, zero=True)
+        self.stats = DeviceBuffer(32, zero=True)
+        self.args = CmdWorkerArgs(rings=self.pairs, comp_rings=self.pairs + 8, groups=1, stop=self.stop_flag,
+                                  max_idle_polls=max_idle_polls, arena_base=arena.ptr, arena_bytes=arena.nbytes,
+                                  sample_state=sample_state.ptr if sample_state is not None else None,
+                                  q_buffer=q.ptr if q is not None else None, o_buffer=self.o.ptr,
+                                  io_slots=io_slots, stats=self.stats.ptr)
+        self.running = False
+        check(L.rl_hip_cmd_worker_launch(C.byref(self.args)), "rl_hip_cmd_worker_launch")
+        self.running = True
+
+    def stop(self) -> np.ndarray:
+        """Stops the worker; returns its counters {descriptors, completions,
+        windows, status}."""
+        if self.running:
+            C.cast(self.stop_flag, C.POINTER(C.c_uint32))[0] = 1
+            sync()
+            self.running = False
+        return self.stats.download(np.uint64, 4)
+
+    def close(self) -> None:
+        L = lib()
+        self.stop()
+        self.o.close()
+        self.stats.close()
+        if self.ring:
+            L.ring_destroy(self.ring)
+            L.comp_ring_destroy(self.comp)
+            L.rl_hip_host_free(self.pairs)
+            L.rl_hip_host_free(self.stop_flag)
+            self.ring = self.comp = None
 
 
 class Timer:

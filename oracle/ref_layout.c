@@ -15,9 +15,11 @@
 #include "hw_worker_sim.h"
 #include "infer_submit.h"
 #include "kv_layout.h"
+#include "pipeline.h"
 #include "request.h"
 #include "reward.h"
 #include "ring.h"
+#include "rollout.h"
 
 static int first = 1;
 #define S(T) emit(#T, "sizeof", sizeof(T))
@@ -62,6 +64,21 @@ main(void)
     S(KVArena); O(KVArena, base); O(KVArena, capacity); O(KVArena, block_size); O(KVArena, bitmap);
     S(KvLayoutDesc); O(KvLayoutDesc, block_bytes); O(KvLayoutDesc, alignment);
     S(RewardDesc); O(RewardDesc, reward); O(RewardDesc, flags);
+    S(rollout_t); O(rollout_t, state); O(rollout_t, kv_arena_id); O(rollout_t, kv_block_idx);
+    O(rollout_t, seq_len); O(rollout_t, max_tokens); O(rollout_t, reward_id); O(rollout_t, flags);
+    O(rollout_t, rng_seed); O(rollout_t, pad);
+    S(rollout_slab_t); O(rollout_slab_t, free_bitmap);
+    S(IdRingIndex); O(IdRingIndex, tail); S(IdRing); O(IdRing, cons); O(IdRing, slots);
+    S(PipelineCredits); O(PipelineCredits, decode_used); O(PipelineCredits, kv_blocks_used);
+    S(RolloutPipeline); O(RolloutPipeline, slab); O(RolloutPipeline, credits); O(RolloutPipeline, policy);
+    S(PipelineSnapshot); O(PipelineSnapshot, stage_credit_headroom); O(PipelineSnapshot, credits);
+    O(PipelineSnapshot, policy);
+    S(RewardIndex); S(RewardRing); O(RewardRing, cons); O(RewardRing, slots);
+    emit("const", "MAX_ROLLOUTS", MAX_ROLLOUTS); emit("const", "PIPELINE_RING_SIZE", PIPELINE_RING_SIZE);
+    emit("const", "REWARD_RING_SIZE", REWARD_RING_SIZE); emit("enum", "ROLL_DONE", ROLL_DONE);
+    emit("enum", "Q_TRAJECTORY", Q_TRAJECTORY); emit("enum", "Q_COUNT", Q_COUNT);
+    emit("enum", "SCHED_FIFO", SCHED_FIFO); emit("enum", "SCHED_SHORTEST_REMAINING", SCHED_SHORTEST_REMAINING);
+    emit("enum", "SCHED_PREFIX_SHARING", SCHED_PREFIX_SHARING);
     printf("\n}\n");
     return 0;
 }

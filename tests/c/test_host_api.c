@@ -7,6 +7,9 @@
  *     completion ring, kv_prefix: the first six asserts; its final
  *     off == 0x1000 contradicts src/kv_prefix.c:83-87 and is replaced by the
  *     code's answer, -1)
+ *   test/test_smoke.c:200-284, test/test_bench.cu:512-581, 739-762 (rollout
+ *     slab, transitions, pipeline queues, credits and snapshot, FIFO without
+ *     work loss, reward ring)
  * Exits non-zero with a message on the first failed check.
  */
 #include <pthread.h>
@@ -23,9 +26,12 @@
 #include "hw_worker_sim.h"
 #include "infer_submit.h"
 #include "kv_prefix.h"
+#include "pipeline.h"
+#include "pipeline_feed.h"
 #include "request.h"
 #include "reward.h"
 #include "ring.h"
+#include "rollout.h"
 
 #define CHECK(c)                                                                 \
     do {                                                                         \
@@ -368,6 +374,158 @@ reward_and_decode_bookkeeping(void)
     printf("reward_and_decode_bookkeeping OK\n");
 }
 
+/* test/test_bench.cu:512-534, plus the lowest-free-id order and the wipe. */
+static void
+rollout_slab_basic(void)
+{
+    static rollout_slab_t slab;
+    uint32_t ids[10], id2;
+    rollout_slab_init(&slab);
+    for (uint32_t i = 0; i < 10; i++) {
+        CHECK(rollout_alloc(&slab, &ids[i]) == 0);
+        CHECK(ids[i] == i);
+        rollout_get(&slab, ids[i])->seq_len = 77;
+    }
+    rollout_free(&slab, ids[3]);
+    rollout_free(&slab, ids[7]);
+    CHECK(rollout_alloc(&slab, &id2) == 0 && id2 == 3);
+    CHECK(rollout_get(&slab, 3)->seq_len == 0 && rollout_get(&slab, 3)->rollout_id == 3);
+    CHECK(rollout_alloc(&slab, &id2) == 0 && id2 == 7);
+    CHECK(rollout_alloc(&slab, &id2) == 0 && id2 == 10);
+    rollout_free(&slab, MAX_ROLLOUTS);          /* out of range: ignored */
+    CHECK(rollout_get(&slab, MAX_ROLLOUTS) == NULL);
+    rollout_slab_init(&slab);
+    for (uint32_t i = 0; i < MAX_ROLLOUTS; i++)
+        CHECK(rollout_alloc(&slab, &id2) == 0 && id2 == i);
+    CHECK(rollout_alloc(&slab, &id2) == -1);
+    rollout_free(&slab, 4097);
+    CHECK(rollout_alloc(&slab, &id2) == 0 && id2 == 4097);
+    printf("rollout_slab_basic OK\n");
+}
+
+/* test/test_bench.cu:536-557, plus the whole 6 x 6 table. */
+static void
+rollout_transitions(void)
+{
+    rollout_t r;
+    memset(&r, 0, sizeof(r));
+    CHECK(rollout_transition(&r, ROLL_FREE, ROLL_DECODING) != 0 && r.state == ROLL_FREE);
+    CHECK(rollout_transition(&r, ROLL_FREE, ROLL_PREFILL_READY) == 0);
+    CHECK(rollout_transition(&r, ROLL_PREFILL_READY, ROLL_DECODING) == 0);
+    CHECK(rollout_transition(&r, ROLL_DECODING, ROLL_REWARD_PENDING) == 0);
+    CHECK(rollout_transition(&r, ROLL_REWARD_PENDING, ROLL_TRAJECTORY_READY) == 0);
+    CHECK(rollout_transition(&r, ROLL_TRAJECTORY_READY, ROLL_DONE) == 0);
+    CHECK(rollout_transition(&r, ROLL_DONE, ROLL_FREE) == 0);
+    CHECK(r.state == ROLL_FREE);
+    /* a valid pair from the wrong current state fails and changes nothing */
+    CHECK(rollout_transition(&r, ROLL_DECODING, ROLL_DONE) != 0 && r.state == ROLL_FREE);
+    static const int allowed[6][6] = {
+        {0, 1, 0, 0, 0, 0}, {0, 0, 1, 0, 0, 0}, {0, 0, 0, 1, 0, 1},
+        {0, 0, 1, 0, 1, 0}, {0, 0, 0, 0, 0, 1}, {1, 0, 0, 0, 0, 0},
+    };
+    for (int f = 0; f < 6; f++)
+        for (int t = 0; t < 6; t++) {
+            CHECK(rollout_is_valid_transition((rollout_state_t)f, (rollout_state_t)t) == allowed[f][t]);
+            r.state = (uint32_t)f;
+            CHECK((rollout_transition(&r, (rollout_state_t)f, (rollout_state_t)t) == 0) == allowed[f][t]);
+            CHECK(r.state == (uint32_t)(allowed[f][t] ? t : f));
+        }
+    printf("rollout_transitions OK\n");
+}
+
+/* test/test_bench.cu:559-581 and test/test_smoke.c:200-284. */
+static void
+pipeline_queues_credits_fifo(void)
+{
+    static RolloutPipeline p;
+    PipelineSnapshot snap;
+    uint32_t rid, rid0, rid1, rid2, out;
+
+    CHECK(pipeline_init(&p) == 0);
+    CHECK(rollout_alloc(&p.slab, &rid) == 0);
+    for (int q = Q_FREE; q <= Q_DONE; q++) {
+        CHECK(pipeline_push(&p, (pipeline_q_t)q, rid) == 0);
+        CHECK(pipeline_pop(&p, (pipeline_q_t)q, &out) == 0 && out == rid);
+    }
+    CHECK(pipeline_pop(&p, Q_FREE, &out) != 0);
+    CHECK(pipeline_push(&p, Q_COUNT, rid) != 0 && pipeline_occupancy(&p, Q_COUNT) == 0);
+    rollout_free(&p.slab, rid);
+
+    /* credits and snapshot (test_smoke.c:200-227) */
+    CHECK(pipeline_init(&p) == 0);
+    CHECK(rollout_alloc(&p.slab, &rid0) == 0 && rollout_alloc(&p.slab, &rid1) == 0);
+    CHECK(rollout_alloc(&p.slab, &rid2) == 0);
+    pipeline_credits_set(&p, 2, 4, 4, 32);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid0) == 0);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid1) == 0);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid2) == -1);
+    pipeline_snapshot(&p, &snap);
+    CHECK(snap.queue_occupancy[Q_DECODE] == 2 && snap.stage_credit_headroom[Q_DECODE] == 0);
+    CHECK(snap.stage_credit_headroom[Q_REWARD] == 4 && snap.stage_credit_headroom[Q_PREFILL] == UINT32_MAX);
+    CHECK(snap.credits.kv_block_limit == 32 && snap.policy == PIPELINE_SCHED_FIFO);
+    CHECK(pipeline_stage_target_batch(&p, Q_DECODE, 8) == 0);
+    pipeline_release(&p, Q_DECODE, 1);
+    pipeline_snapshot(&p, &snap);
+    CHECK(snap.stage_credit_headroom[Q_DECODE] == 1);
+    CHECK(pipeline_stage_target_batch(&p, Q_DECODE, 8) == 1);
+    pipeline_release(&p, Q_DECODE, 9);      /* saturates at 0 used */
+    CHECK(pipeline_stage_available_credits(&p, Q_DECODE) == 2);
+    CHECK(pipeline_stage_target_batch(&p, Q_DECODE, 8) == 2);
+    CHECK(pipeline_stage_target_batch(&p, Q_DECODE, 1) == 1);
+
+    /* FIFO without work loss (test_smoke.c:231-284) */
+    CHECK(pipeline_init(&p) == 0);
+    CHECK(rollout_alloc(&p.slab, &rid0) == 0 && rollout_alloc(&p.slab, &rid1) == 0);
+    CHECK(rollout_alloc(&p.slab, &rid2) == 0);
+    pipeline_credits_set(&p, 3, 4, 4, 32);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid0) == 0 && pipeline_try_push(&p, Q_DECODE, rid1) == 0);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid2) == 0 && pipeline_occupancy(&p, Q_DECODE) == 3);
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) == 0 && out == rid0 && pipeline_occupancy(&p, Q_DECODE) == 2);
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) == 0 && out == rid1);
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) == 0 && out == rid2 && pipeline_occupancy(&p, Q_DECODE) == 0);
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) != 0);
+    pipeline_release(&p, Q_DECODE, 3);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid0) == 0 && pipeline_try_push(&p, Q_DECODE, rid1) == 0);
+    CHECK(pipeline_try_push(&p, Q_DECODE, rid2) == 0 && pipeline_occupancy(&p, Q_DECODE) == 3);
+    p.policy = PIPELINE_SCHED_SHORTEST_REMAINING;
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) != 0 && pipeline_occupancy(&p, Q_DECODE) == 3);
+    CHECK(pipeline_set_schedule_policy(&p, PIPELINE_SCHED_SHORTEST_REMAINING) != 0);
+    p.policy = PIPELINE_SCHED_PREFIX_SHARING;
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) != 0 && pipeline_occupancy(&p, Q_DECODE) == 3);
+    CHECK(pipeline_set_schedule_policy(&p, PIPELINE_SCHED_PREFIX_SHARING) != 0);
+    CHECK(pipeline_set_schedule_policy(&p, PIPELINE_SCHED_FIFO) == 0 && p.policy == PIPELINE_SCHED_FIFO);
+    CHECK(pipeline_schedule(&p, Q_DECODE, &out) == 0 && out == rid0 && pipeline_occupancy(&p, Q_DECODE) == 2);
+
+    /* a queue holds 4,096 ids */
+    CHECK(pipeline_init(&p) == 0);
+    for (uint32_t i = 0; i < PIPELINE_RING_SIZE; i++)
+        CHECK(pipeline_push(&p, Q_REWARD, i) == 0);
+    CHECK(pipeline_push(&p, Q_REWARD, 0) == -1 && pipeline_occupancy(&p, Q_REWARD) == PIPELINE_RING_SIZE);
+    CHECK(pipeline_pop(&p, Q_REWARD, &out) == 0 && out == 0 && pipeline_push(&p, Q_REWARD, 9) == 0);
+    printf("pipeline_queues_credits_fifo OK\n");
+}
+
+/* test/test_bench.cu:739-762, plus full and wrap. */
+static void
+reward_ring_basic(void)
+{
+    static RewardRing rr;
+    RewardDesc d = {1, 0, 128, 0, 0.0f, 0}, got;
+    reward_ring_init(&rr);
+    CHECK(reward_push(&rr, &d) == 0);
+    CHECK(reward_pop(&rr, &got) == 0 && got.rollout_id == 1 && got.token_count == 128);
+    CHECK(reward_pop(&rr, &got) != 0);
+    for (uint32_t i = 0; i < REWARD_RING_SIZE; i++) {
+        d.rollout_id = i;
+        CHECK(reward_push(&rr, &d) == 0);
+    }
+    CHECK(reward_push(&rr, &d) == -1);
+    for (uint32_t i = 0; i < REWARD_RING_SIZE; i++)
+        CHECK(reward_pop(&rr, &got) == 0 && got.rollout_id == i);
+    CHECK(reward_pop(&rr, &got) == -1);
+    printf("reward_ring_basic OK\n");
+}
+
 int
 main(void)
 {
@@ -383,6 +541,10 @@ main(void)
     arena_basic();
     kv_prefix_basic();
     reward_and_decode_bookkeeping();
+    rollout_slab_basic();
+    rollout_transitions();
+    pipeline_queues_credits_fifo();
+    reward_ring_basic();
     printf("ALL OK\n");
     return 0;
 }

@@ -152,3 +152,42 @@ def test_grpo_rollout_loop(rl, gpu, orc, olib):
     for b in (ntok, rew2, adv):
         b.close()
     loop.close()
+
+
+def test_grpo_loop_fed_by_the_rollout_pipeline(rl, gpu, orc, olib):
+    """The same loop with the request ring fed by the host rollout pipeline
+    (pipeline_feed.h) under 384 decode credits: requests 0..383 go out at
+    once, the rest as dones return credits. Every request finishes once with
+    the reference rule's reward on its device tokens; the pipeline ends empty
+    (queues, credits, slab, request map); the RewardRing holds one RewardDesc
+    per done {prompt length, 256 tokens, reward}; at two checkpoint steps the
+    tokens, attention and projection match the host as above."""
+    L = rl.lib()
+    cfg = grpo.build_workload(405)
+    loop = grpo.RolloutLoop(cfg)
+    dev = loop.dev
+    loop.attach_pipeline(decode_credits=384)
+    f = loop.feeder
+    assert (f.stats.registered, f.stats.admitted, f.stats.sent) == (REQ, 384, 384)
+    print("[rollout] running the pipeline-fed loop", flush=True)
+    res = loop.run(check_steps=(0, 300), on_check=lambda t: _check_step(rl, orc, olib, cfg, dev, t))
+    print(f"[rollout] pipeline-fed: {res['steps']} steps in {res['wall_s']:.2f} s", flush=True)
+    assert (f.stats.admitted, f.stats.sent, f.stats.retired, f.stats.reward_handoffs) == (REQ,) * 4
+    assert f.stats.bad_dones == 0 and f.end_sent == 1
+    assert dev["counters"].download(np.uint32, 4).tolist() == [REQ, REQ, 1, 0]
+    dones = loop.dones
+    assert sorted(d[0] for d in dones) == list(range(REQ)) and all(d[2] == GEN and d[4] == 0 for d in dones)
+    gen = dev["gen"].download(np.uint32, (REQ, GEN))
+    rew_dev = dev["rewards"].download(np.float32, REQ)
+    for r, _, _, reward, _ in dones:
+        tgt = np.ascontiguousarray(cfg["targets"][r // GS])
+        row = np.ascontiguousarray(gen[r])
+        want = np.float32(L.reward_match_count(row.ctypes.data, tgt.ctypes.data, GEN) & 0xFF) / np.float32(255.0)
+        assert np.float32(reward) == want and rew_dev[r] == want, r
+    snap = rl.PipelineSnapshot()
+    L.pipeline_snapshot(loop.pipe.ctypes.data, C.byref(snap))
+    assert list(snap.queue_occupancy) == [0] * 6 and snap.credits.decode_used == 0
+    assert np.all(loop.pipe[rl.PIPELINE_SLAB_OFF + 48 * 8192:rl.PIPELINE_SLAB_OFF + 48 * 8192 + 1024] == 0xFF)
+    assert np.all(loop.rid_map == 0xFFFFFFFF)
+    assert L.hw_ring_load_acquire(loop.rr) == REQ + 1 and L.hw_ring_load_acquire(loop.dr) == REQ
+    loop.close()
