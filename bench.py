@@ -20,11 +20,14 @@ in child processes measure the attention call's HBM traffic, calibrated on a
 256 MiB device copy in the same pass (--no-traffic skips them).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append|copy]
-  python bench.py --workload sample256|longctx|proj|plumbing|rollout|rollout_pipeline|cmdring|pipeline
+  python bench.py --workload sample256|longctx|proj|plumbing|rollout|rollout_pipeline|cmdring|pipeline|
+                            pipeline_trace
       the other synthetic workloads (sampling at 256 rows, long-context
       split-KV decode, the vocabulary projection, the hw_desc ring plumbing
-      decode, the GRPO rollout loop, the v0.2 command/completion rings), one
-      JSON line each
+      decode, the GRPO rollout loop with its requests sent at once or fed by
+      the host rollout pipeline, the v0.2 command/completion rings, the host
+      pipeline driving them, and that run traced on both sides), one JSON
+      line each
 """
 import argparse
 import json
@@ -630,7 +633,7 @@ def wl_pipeline(args):
     w = rlrt.CmdWorker(darena, io, sample_state=dst)
     try:
         rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, w.ring, w.comp, rew.ctypes.data, C.byref(cfg),
-                                   C.byref(stats), None, 0)
+                                   C.byref(stats), None, 0, None)
     finally:
         wst = w.stop()
         w.close()
@@ -646,9 +649,77 @@ def wl_pipeline(args):
             "note": "host loop native (C); one persistent worker workgroup"}
 
 
+def wl_pipeline_trace(args):
+    """The pipeline run with tracing on both sides of the rings: the driver's
+    host records (CLOCK_MONOTONIC) and the worker's device records
+    (s_memrealtime, mapped onto the host clock by ping-pong clock samples
+    before and after the run), merged and paired as the reference's trace
+    report does. Latencies in ns."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    n, tokens, nblk, io = 1000, 128, 128, 4096
+    rng = np.random.default_rng(81)
+    arena = synth.f32_to_f16(rng.standard_normal(nblk * 8192, dtype=np.float32))
+    darena = rlrt.DeviceBuffer.from_array(arena)
+    host = np.zeros(rlrt.TRACE_RING_BYTES, np.uint8)
+    L.trace_init(host.ctypes.data)
+    dev_ring = L.rl_hip_host_alloc_coherent(rlrt.TRACE_RING_BYTES)
+    if not dev_ring:
+        raise rlrt.RlrtError("coherent trace ring allocation failed")
+    C.memset(dev_ring, 0, rlrt.TRACE_RING_BYTES)
+
+    def clock():
+        t, h, r = C.c_uint64(), C.c_double(), C.c_uint64()
+        rlrt.check(L.rl_hip_trace_clock_sample(64, C.byref(t), C.byref(h), C.byref(r)), "clock sample")
+        return t.value, h.value, r.value
+
+    pipe = np.zeros(rlrt.PIPELINE_BYTES, np.uint8)
+    rew = np.zeros(rlrt.REWARD_RING_BYTES, np.uint8)
+    L.pipeline_init(pipe.ctypes.data)
+    L.reward_ring_init(rew.ctypes.data)
+    cfg = rlrt.CmdPipelineCfg(n_rollouts=n, tokens_per_rollout=tokens, batch_max=32, kv_blocks=nblk,
+                              max_decode_credits=256, max_reward_credits=128, max_trajectory_credits=128,
+                              kv_block_limit=1024, seed_base=42, full_wait_ns=10**10, drain_wait_ns=10**10)
+    stats = rlrt.CmdPipelineStats()
+    c0 = clock()
+    w = rlrt.CmdWorker(darena, io, trace=dev_ring)
+    try:
+        rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, w.ring, w.comp, rew.ctypes.data, C.byref(cfg),
+                                   C.byref(stats), None, 0, host.ctypes.data)
+    finally:
+        w.stop()
+        w.close()
+        darena.close()
+    c1 = clock()
+    if rc != 0:
+        L.rl_hip_host_free(dev_ring)
+        raise rlrt.RlrtError("rl_pipeline_cmd_run did not complete")
+    m = rlrt.TraceClockMap()
+    L.trace_clock_fit(c0[0], c0[1], c1[0], c1[1], C.byref(m))
+    L.trace_rebase(dev_ring, C.byref(m))
+    merged = np.zeros(rlrt.TRACE_RING_BYTES, np.uint8)
+    events = L.trace_merge(merged.ctypes.data, (C.c_void_p * 2)(host.ctypes.data, dev_ring), 2)
+    L.rl_hip_host_free(dev_ring)
+    T = rlrt.TRACE
+    pairs = {}
+    s = rlrt.TracePairStats()
+    for a, b in (("DESC_POSTED", "DESC_COMMITTED"), ("DESC_POSTED", "DESC_CONSUMED"),
+                 ("DESC_CONSUMED", "COMPLETION_POSTED"), ("COMPLETION_POSTED", "COMPLETION_POLLED"),
+                 ("DESC_POSTED", "COMPLETION_POLLED"), ("DESC_CONSUMED", "COMPLETION_POLLED"),
+                 ("ROLLOUT_ALLOC", "REWARD_POSTED"), ("ROLLOUT_ALLOC", "TRAJECTORY_DONE"),
+                 ("REWARD_POSTED", "REWARD_SCORED"), ("REWARD_POSTED", "TRAJECTORY_DONE")):
+        L.trace_pair_stats(merged.ctypes.data, T[a], T[b], C.byref(s))
+        pairs[f"{a.lower()}->{b.lower()}"] = {"n": s.n, "avg": s.avg_ns, "p50": s.p50_ns, "p90": s.p90_ns,
+                                             "p99": s.p99_ns}
+    return {"workload": "pipeline_trace_1000rollouts_x128tok", "events": events,
+            "tokens_per_s_traced": stats.descriptors_consumed / (stats.wall_ns * 1e-9),
+            "clock": {"ns_per_tick": m.ns_per_tick, "rtt_ns": [c0[2], c1[2]]}, "latency_ns": pairs}
+
+
 WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
              "rollout": wl_rollout, "cmdring": wl_cmdring, "rollout_pipeline": wl_rollout_pipeline,
-             "pipeline": wl_pipeline}
+             "pipeline": wl_pipeline, "pipeline_trace": wl_pipeline_trace}
 
 
 def main():

@@ -31,6 +31,12 @@
 //          before it in its window are completed first.
 //  exit    also on the host's stop flag, after max_idle_polls empty polls, or
 //          when the completion ring stays full for as long (stats status).
+//  trace   optional: wave 0 appends 20-byte trace records (trace.h) to the
+//          worker's own TraceRing in coherent host memory - DESC_CONSUMED per
+//          descriptor once its window is read, COMPLETION_POSTED per
+//          completion before the tail release - stamped with s_memrealtime
+//          (100 MHz) and keyed {low 32 bits of seq_id, output_token_offset};
+//          one 32-bit word per lane, then a release store of the ring head.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -41,6 +47,7 @@
 #include "rl_hip.h"
 #include "rl_hip_internal.h"
 #include "sample.h"
+#include "trace.h"
 
 namespace {
 
@@ -67,6 +74,7 @@ struct CmdParams {
     float *o;
     uint32_t io_mask;
     uint64_t *stats;
+    TraceRing *trace;
 };
 
 __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
@@ -77,6 +85,28 @@ __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
 __device__ __forceinline__ void sys_store_release(volatile uint32_t *p, uint32_t v)
 {
     __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Appends the records {tsc, type, low 32 bits of seq_id, output_token_offset}
+// of descriptors d[0..n) at the ring's head (wave 0; the worker is the ring's
+// only producer), one 32-bit word per lane, and release-stores the new head.
+__device__ void trace_append(TraceRing *tr, uint64_t &thead, const Descriptor *d, uint32_t n, uint32_t type,
+                             int lane)
+{
+    const uint64_t tsc = __builtin_amdgcn_s_memrealtime();
+    volatile uint32_t *words = (volatile uint32_t *)tr->entries;
+    for (uint32_t w = (uint32_t)lane; w < 5u * n; w += 64u) {
+        const uint32_t i = w / 5u, f = w - 5u * i;
+        const uint32_t v = f == 0 ? (uint32_t)tsc
+                         : f == 1 ? (uint32_t)(tsc >> 32)
+                         : f == 2 ? type
+                         : f == 3 ? (uint32_t)d[i].seq_id
+                                  : d[i].output_token_offset;
+        words[((thead + i) & (TRACE_CAPACITY - 1)) * 5u + f] = v;
+    }
+    thead += n;
+    if (lane == 0)
+        __hip_atomic_store((uint64_t *)&tr->head, thead, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ float wave_sum(float v)
@@ -191,6 +221,10 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
         head = sys_load(&ring->cons.head);
         ctail = sys_load(&cr->prod.tail);
     }
+    TraceRing *tr = p.trace ? p.trace + blockIdx.x : nullptr;
+    uint64_t thead = 0;            // wave 0, uniform: the trace ring's head
+    if (tr && wave == 0)
+        thead = __hip_atomic_load((uint64_t *)&tr->head, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 
     for (;;) {
         // ---- the committed window at the head (wave 0) ------------------------
@@ -241,6 +275,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                     sys_store_release(&ring->cons.head, head);
                 }
                 n = run;
+                if (tr && n)
+                    trace_append(tr, thead, s_desc, n, TRACE_DESC_CONSUMED, lane);
             }
             if (lane == 0) {
                 s_ctl[0] = n;
@@ -290,6 +326,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                 }
             }
             if (rl_readlane(room, 0)) {
+                if (tr)
+                    trace_append(tr, thead, s_desc, n, TRACE_COMPLETION_POSTED, lane);
                 const uint32_t t = rl_readlane(ctail, 0);
                 // two lanes per record; records may wrap around the ring
                 if ((uint32_t)lane < 2 * n) {
@@ -364,6 +402,7 @@ extern "C" int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *a)
     p.o = a->o_buffer;
     p.io_mask = a->io_slots ? a->io_slots - 1 : 0;
     p.stats = a->stats;
+    p.trace = a->trace;
     hipLaunchKernelGGL(cmd_worker_kernel, dim3(a->groups), dim3(kThreads), 0, rl_stream(), p);
     return rl_check_launch("cmd_worker_kernel launch");
 }

@@ -19,6 +19,7 @@ typedef struct {
     rl_cmd_pipeline_stats_t *st;
     Completion *log;
     uint64_t log_cap;
+    TraceRing *trace;
 } Run;
 
 static uint64_t
@@ -35,6 +36,8 @@ drain(Run *r)
     Completion c;
     uint64_t n = 0;
     while (comp_ring_poll(r->comp, &c)) {
+        if (r->trace)
+            trace_push(r->trace, TRACE_COMPLETION_POLLED, (uint32_t)c.seq_id, (uint32_t)c.reward_cookie);
         if (r->log && r->st->descriptors_consumed < r->log_cap)
             r->log[r->st->descriptors_consumed] = c;
         r->st->descriptors_consumed++;
@@ -60,6 +63,8 @@ dispatch_window(Run *r, uint32_t rid, uint32_t t0, uint32_t n)
         d.reward_cookie = (uint64_t)rid << 32 | t;
         if (decode_batch_push(&batch, &d) != 0)
             return -1;
+        if (r->trace)
+            trace_push(r->trace, TRACE_DESC_POSTED, rid, t);
     }
     if (decode_batch_submit(r->cmd, &batch) == 0)
         goto posted;
@@ -77,6 +82,9 @@ dispatch_window(Run *r, uint32_t rid, uint32_t t0, uint32_t n)
     }
     return -1;
 posted:
+    if (r->trace)
+        for (uint32_t i = 0; i < n; i++)
+            trace_push(r->trace, TRACE_DESC_COMMITTED, rid, t0 + i);
     r->st->descriptors_posted += n;
     drain(r);
     return 0;
@@ -100,6 +108,8 @@ finish(Run *r, uint32_t rid)
     const uint32_t tokens = r->cfg->tokens_per_rollout;
     rollout_transition(ro, ROLL_DECODING, ROLL_REWARD_PENDING);
     pass_stage(p, Q_REWARD, rid);
+    if (r->trace)
+        trace_push(r->trace, TRACE_REWARD_POSTED, rid, 0);
     if (r->rewards) {
         RewardDesc rd = {rid, 0, tokens, 0, reward_score_mock(NULL, tokens), 0};
         if (reward_push(r->rewards, &rd) == 0)
@@ -107,12 +117,18 @@ finish(Run *r, uint32_t rid)
         else
             r->st->reward_ring_full++;
     }
+    if (r->trace)
+        trace_push(r->trace, TRACE_REWARD_SCORED, rid, 0);
     rollout_transition(ro, ROLL_REWARD_PENDING, ROLL_TRAJECTORY_READY);
     pass_stage(p, Q_TRAJECTORY, rid);
     rollout_transition(ro, ROLL_TRAJECTORY_READY, ROLL_DONE);
     pass_stage(p, Q_DONE, rid);
+    if (r->trace)
+        trace_push(r->trace, TRACE_TRAJECTORY_DONE, rid, 0);
     r->st->rollouts_completed++;
     rollout_free(&p->slab, rid);
+    if (r->trace)
+        trace_push(r->trace, TRACE_ROLLOUT_FREE, rid, 0);
 }
 
 /* One decode batch of pipeline_stage_target_batch rollouts, or with
@@ -137,6 +153,8 @@ decode_batch_run(Run *r, int drain)
         return 0;
     r->st->decode_batches++;
     r->st->decode_rollouts_scheduled += got;
+    if (r->trace)
+        trace_push(r->trace, TRACE_DECODE_BATCH, got, r->cfg->tokens_per_rollout);
     if (got > r->st->decode_batch_peak)
         r->st->decode_batch_peak = got;
     const uint32_t tokens = r->cfg->tokens_per_rollout;
@@ -157,13 +175,13 @@ decode_batch_run(Run *r, int drain)
 int
 rl_pipeline_cmd_run(RolloutPipeline *p, CommandRing *cmd, CompletionRing *comp, RewardRing *rewards,
                     const rl_cmd_pipeline_cfg_t *cfg, rl_cmd_pipeline_stats_t *stats, Completion *log,
-                    uint64_t log_cap)
+                    uint64_t log_cap, TraceRing *trace)
 {
     if (!p || !cmd || !comp || !cfg || !stats || cfg->batch_max == 0 ||
         cfg->batch_max > DECODE_DESCRIPTOR_BATCH_LIMIT || cfg->kv_blocks == 0)
         return -1;
     memset(stats, 0, sizeof(*stats));
-    Run r = {p, cmd, comp, rewards, cfg, stats, log, log_cap};
+    Run r = {p, cmd, comp, rewards, cfg, stats, log, log_cap, trace};
     const uint64_t t0 = now_ns();
     pipeline_credits_set(p, cfg->max_decode_credits, cfg->max_reward_credits, cfg->max_trajectory_credits,
                          cfg->kv_block_limit);
@@ -174,6 +192,8 @@ rl_pipeline_cmd_run(RolloutPipeline *p, CommandRing *cmd, CompletionRing *comp, 
             break;
         }
         stats->rollouts_started++;
+        if (trace)
+            trace_push(trace, TRACE_ROLLOUT_ALLOC, rid, 0);
         rollout_t *ro = rollout_get(&p->slab, rid);
         ro->max_tokens = cfg->tokens_per_rollout;
         ro->rng_seed = cfg->seed_base + i;
@@ -195,6 +215,8 @@ rl_pipeline_cmd_run(RolloutPipeline *p, CommandRing *cmd, CompletionRing *comp, 
         if (!admitted) {
             rollout_transition(ro, ROLL_DECODING, ROLL_DONE);
             rollout_free(&p->slab, rid);
+            if (trace)
+                trace_push(trace, TRACE_ROLLOUT_FREE, rid, 0);
             stats->rollouts_dropped++;
             continue;
         }

@@ -144,6 +144,23 @@ class CmdPipelineStats(C.Structure):
         "ring_full_spins", "pipeline_overflow", "reward_handoffs", "reward_ring_full", "wall_ns")]
 
 
+TRACE_RING_BYTES = 20971528  # sizeof(TraceRing)
+TRACE_CAPACITY = 1 << 20
+TRACE_EVENTS = ("ROLLOUT_ALLOC", "ROLLOUT_FREE", "DESC_POSTED", "DESC_COMMITTED", "DESC_CONSUMED",
+                "COMPLETION_POSTED", "COMPLETION_POLLED", "DECODE_BATCH", "REWARD_POSTED", "REWARD_SCORED",
+                "TRAJECTORY_DONE")
+TRACE = {n: i for i, n in enumerate(TRACE_EVENTS)}
+TRACE_ENTRY = np.dtype([("tsc", "<u8"), ("type", "<u4"), ("rollout_id", "<u4"), ("seq", "<u4")])
+
+
+class TracePairStats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("n", "avg_ns", "p50_ns", "p90_ns", "p99_ns")]
+
+
+class TraceClockMap(C.Structure):
+    _fields_ = [("ns_per_tick", C.c_double), ("offset_ns", C.c_double)]
+
+
 class KVPrefix(C.Structure):
     _pack_ = 1
     _fields_ = [("prefix_id", C.c_uint32), ("refcnt", C.c_uint32), ("kv_block_offset", C.c_int64),
@@ -244,7 +261,7 @@ class CmdWorkerArgs(C.Structure):
     _fields_ = [("rings", C.c_void_p), ("comp_rings", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
                 ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
                 ("sample_state", C.c_void_p), ("q_buffer", C.c_void_p), ("o_buffer", C.c_void_p),
-                ("io_slots", C.c_uint32), ("stats", C.c_void_p)]
+                ("io_slots", C.c_uint32), ("stats", C.c_void_p), ("trace", C.c_void_p)]
 
 
 DTYPE_BF16 = 0
@@ -322,7 +339,14 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_feed_retire": (u32, [C.POINTER(PipelineFeeder)]), "rl_feed_end": (i32, [C.POINTER(PipelineFeeder)]),
         "rl_feed_pump": (u32, [C.POINTER(PipelineFeeder)]),
         "rl_pipeline_cmd_run": (i32, [vp, vp, vp, vp, C.POINTER(CmdPipelineCfg), C.POINTER(CmdPipelineStats),
-                                      vp, u64]),
+                                      vp, u64, vp]),
+        "trace_init": (None, [vp]), "trace_push": (None, [vp, i32, u32, u32]),
+        "trace_push_ts": (None, [vp, u64, i32, u32, u32]),
+        "trace_report_from": (i32, [vp, u64, u64, u64, C.c_char_p]),
+        "trace_pair_stats": (i32, [vp, i32, i32, C.POINTER(TracePairStats)]), "trace_now_ns": (u64, []),
+        "trace_clock_fit": (i32, [u64, C.c_double, u64, C.c_double, C.POINTER(TraceClockMap)]),
+        "trace_rebase": (None, [vp, C.POINTER(TraceClockMap)]), "trace_merge": (u64, [vp, vp, u32]),
+        "rl_hip_trace_clock_sample": (i32, [u32, C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64)]),
         "reward_score_mock": (C.c_float, [vp, u32]),
         "reward_match_count": (u32, [vp, vp, u32]),
         "reward_group_advantage": (i32, [vp, u32, u32, vp]),
@@ -419,10 +443,12 @@ class CmdWorker:
     fresh CommandRing / CompletionRing pair in coherent host memory. q is the
     query buffer (None: the synthesized query from seq_id, reward_cookie and
     the sample state's rng words); the o buffer has io_slots rows of 128
-    floats. stop() raises the stop flag and waits for the worker to exit."""
+    floats; trace, a TraceRing in coherent host memory, receives the worker's
+    device-stamped records. stop() raises the stop flag and waits for the
+    worker to exit."""
 
     def __init__(self, arena: DeviceBuffer, io_slots: int, q: DeviceBuffer | None = None,
-                 sample_state: DeviceBuffer | None = None, max_idle_polls: int = 1 << 24):
+                 sample_state: DeviceBuffer | None = None, max_idle_polls: int = 1 << 24, trace: int | None = None):
         L = lib()
         self.ring, self.comp = L.ring_create(), L.comp_ring_create()
         self.pairs = L.rl_hip_host_alloc_coherent(16)
@@ -438,7 +464,7 @@ class CmdWorker:
                                   max_idle_polls=max_idle_polls, arena_base=arena.ptr, arena_bytes=arena.nbytes,
                                   sample_state=sample_state.ptr if sample_state is not None else None,
                                   q_buffer=q.ptr if q is not None else None, o_buffer=self.o.ptr,
-                                  io_slots=io_slots, stats=self.stats.ptr)
+                                  io_slots=io_slots, stats=self.stats.ptr, trace=trace)
         self.running = False
         check(L.rl_hip_cmd_worker_launch(C.byref(self.args)), "rl_hip_cmd_worker_launch")
         self.running = True

@@ -139,6 +139,7 @@ RL_EXTERN_C_END
  */
 #include "completion.h"
 #include "ring.h"
+#include "trace.h"
 
 typedef struct {
     uint32_t n_rollouts;          /* rollouts to run (1000) */
@@ -173,11 +174,16 @@ typedef struct {
 RL_EXTERN_C_BEGIN
 
 /* Runs the loop above on an initialised pipeline. Completions are copied
- * to log[0 .. log_cap) in arrival order when log is not NULL. 0 when every
- * posted descriptor was completed, -1 on bad arguments or when the final
- * drain gave up (stats are filled either way). */
+ * to log[0 .. log_cap) in arrival order when log is not NULL. With trace set
+ * the host side pushes (trace.h keys): ROLLOUT_ALLOC, DESC_POSTED when a
+ * window is formed, DESC_COMMITTED when its submit succeeds,
+ * COMPLETION_POLLED per completion drained (seq = low 32 bits of its
+ * reward_cookie, the step), DECODE_BATCH {rollouts, tokens}, REWARD_POSTED,
+ * REWARD_SCORED, TRAJECTORY_DONE and ROLLOUT_FREE. 0 when every posted
+ * descriptor was completed, -1 on bad arguments or when the final drain gave
+ * up (stats are filled either way). */
 int rl_pipeline_cmd_run(RolloutPipeline *p, CommandRing *cmd, CompletionRing *comp, RewardRing *rewards,
                         const rl_cmd_pipeline_cfg_t *cfg, rl_cmd_pipeline_stats_t *stats, Completion *log,
-                        uint64_t log_cap);
+                        uint64_t log_cap, TraceRing *trace);
 
 RL_EXTERN_C_END

@@ -25,6 +25,7 @@
 #include "reward.h"
 #include "ring.h"
 #include "sample.h"
+#include "trace.h"
 
 RL_EXTERN_C_BEGIN
 
@@ -277,7 +278,14 @@ int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
  * token 0 (it is not read). The launch returns at once; rl_hip_sync() waits
  * for every worker to exit (sentinel, *stop, max_idle_polls empty polls, or
  * a completion ring full for as long). stats per group: {descriptors run,
- * completions pushed, windows, status (0 stopped, 1 idle, 3 ring full)}. */
+ * completions pushed, windows, status (0 stopped, 1 idle, 3 ring full)}.
+ * With trace set, worker g appends to trace[g] (trace.h records; the worker is
+ * that ring's only producer and starts at its head) a DESC_CONSUMED record per
+ * descriptor when its window has been read and a COMPLETION_POSTED record per
+ * completion just before the completion tail is released, {tsc = the GPU's
+ * 100 MHz s_memrealtime ticks, rollout_id = low 32 bits of seq_id, seq =
+ * output_token_offset}; the ring head is release-stored after each batch of
+ * records. */
 typedef struct {
     CommandRing *const *rings;          /* coherent host [groups] (ring_create after rl_hip_open) */
     CompletionRing *const *comp_rings;  /* coherent host [groups] (comp_ring_create) */
@@ -291,9 +299,20 @@ typedef struct {
     float *o_buffer;                    /* device fp32 [io_slots][128], or NULL */
     uint32_t io_slots;                  /* a power of two; 0 uses slot 0 */
     uint64_t *stats;                    /* device [groups][4] */
+    TraceRing *trace;                   /* coherent host [groups] rings, or NULL (see below) */
 } rl_cmd_worker_args_t;
 
 int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *args);
+
+/* ---- clock samples for device-stamped traces ---------------------------------
+ * No counterpart in the reference (its tracing is host-only; docs/tracing.md
+ * lists device timestamps as future work). Takes `samples` ping-pong rounds
+ * between the host and a one-wave kernel on a private stream and returns the
+ * round with the shortest trip: the GPU's 100 MHz s_memrealtime reading, the
+ * host CLOCK_MONOTONIC ns at the middle of that trip, and the trip (the
+ * sample's uncertainty is at most half of it). Two calls, before and after a
+ * run, feed trace_clock_fit (trace.h). samples 1..1024. */
+int rl_hip_trace_clock_sample(uint32_t samples, uint64_t *ticks, double *host_ns, uint64_t *rtt_ns);
 
 /* ---- sampling -------------------------------------------------------------
  * Replaces sample_token (cu/sample.cu:41-123) with the specification in

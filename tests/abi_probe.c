@@ -19,6 +19,7 @@
 #include "reward.h"
 #include "ring.h"
 #include "rollout.h"
+#include "trace.h"
 #include "sample.h"
 
 static int first = 1;
@@ -79,6 +80,9 @@ main(void)
     emit("enum", "Q_TRAJECTORY", Q_TRAJECTORY); emit("enum", "Q_COUNT", Q_COUNT);
     emit("enum", "SCHED_FIFO", SCHED_FIFO); emit("enum", "SCHED_SHORTEST_REMAINING", SCHED_SHORTEST_REMAINING);
     emit("enum", "SCHED_PREFIX_SHARING", SCHED_PREFIX_SHARING);
+    S(trace_entry_t); O(trace_entry_t, type); O(trace_entry_t, rollout_id); O(trace_entry_t, seq);
+    S(TraceRing); O(TraceRing, head); emit("const", "TRACE_CAPACITY", TRACE_CAPACITY);
+    emit("enum", "TRACE_COMPLETION_POLLED", TRACE_COMPLETION_POLLED); emit("enum", "TRACE_EVENT_COUNT", TRACE_EVENT_COUNT);
     /* not compilable from the reference headers: pinned by packed-layout arithmetic */
     S(KVPrefix); O(KVPrefix, refcnt); O(KVPrefix, kv_block_offset); O(KVPrefix, token_len);
     O(KVPrefix, kv_block_count); O(KVPrefix, flags);

@@ -30,7 +30,7 @@ def _cfg(rl):
                              kv_block_limit=1024, seed_base=42, full_wait_ns=10**10, drain_wait_ns=10**10)
 
 
-def _drive(rl, ring, comp):
+def _drive(rl, ring, comp, trace=None):
     L = rl.lib()
     pipe = np.zeros(rl.PIPELINE_BYTES, np.uint8)
     rew = np.zeros(rl.REWARD_RING_BYTES, np.uint8)
@@ -39,7 +39,7 @@ def _drive(rl, ring, comp):
     st = rl.CmdPipelineStats()
     log = (rl.Completion * (N * TOKENS))()
     rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, ring, comp, rew.ctypes.data, C.byref(_cfg(rl)), C.byref(st),
-                               C.addressof(log), N * TOKENS)
+                               C.addressof(log), N * TOKENS, trace)
     rows = np.frombuffer(log, dtype=np.dtype([("seq", "<u8"), ("tok", "<u4"), ("kv", "<u4"), ("cookie", "<u8"),
                                               ("cycles", "<u8")])).copy()
     return rc, st, rows, pipe
@@ -89,3 +89,80 @@ def test_pipeline_drives_the_gpu_worker(rl, gpu):
     snap = rl.PipelineSnapshot()
     L.pipeline_snapshot(pipe.ctypes.data, C.byref(snap))
     assert list(snap.queue_occupancy) == [0] * 6 and snap.credits.decode_used == 0
+
+
+def _clock(rl):
+    L = rl.lib()
+    ticks, host, rtt = C.c_uint64(), C.c_double(), C.c_uint64()
+    rl.check(L.rl_hip_trace_clock_sample(64, C.byref(ticks), C.byref(host), C.byref(rtt)),
+             "rl_hip_trace_clock_sample")
+    return ticks.value, host.value, rtt.value
+
+
+def test_pipeline_traced_on_both_sides(rl, gpu):
+    """The same run with tracing: host records from the driver, device
+    records (s_memrealtime) from the worker, the device ring mapped onto the
+    host clock through two ping-pong clock samples and merged. Every
+    descriptor has post, commit, device dequeue, device completion and poll
+    records under one (rid, step) key, in stream order on each side; on the
+    host timeline the four stamps of a descriptor are ordered within the
+    clock samples' uncertainty; the report pairs every descriptor."""
+    L = rl.lib()
+    rng = np.random.default_rng(92)
+    arena16 = synth.f32_to_f16(rng.standard_normal(NBLK * 8192, dtype=np.float32))
+    darena = rl.DeviceBuffer.from_array(arena16)
+    host = np.zeros(rl.TRACE_RING_BYTES, np.uint8)
+    L.trace_init(host.ctypes.data)
+    dev_ring = L.rl_hip_host_alloc_coherent(rl.TRACE_RING_BYTES)
+    assert dev_ring, rl._err()
+    C.memset(dev_ring, 0, rl.TRACE_RING_BYTES)
+    c0 = _clock(rl)
+    print(f"[pipeline] clock sample: rtt {c0[2]} ns", flush=True)
+    w = rl.CmdWorker(darena, IO, trace=dev_ring)
+    try:
+        rc, st, got, _ = _drive(rl, w.ring, w.comp, trace=host.ctypes.data)
+    finally:
+        wst = w.stop()
+        w.close()
+        darena.close()
+    c1 = _clock(rl)
+    assert rc == 0 and wst[1] == N * TOKENS
+    m = rl.TraceClockMap()
+    assert L.trace_clock_fit(c0[0], c0[1], c1[0], c1[1], C.byref(m)) == 0
+    print(f"[pipeline] clock map: {m.ns_per_tick:.6f} ns/tick, rtt {c0[2]} / {c1[2]} ns", flush=True)
+    assert abs(m.ns_per_tick - 10.0) < 0.01
+    dbuf = np.frombuffer((C.c_uint8 * rl.TRACE_RING_BYTES).from_address(dev_ring), np.uint8)
+    n_dev = int(dbuf[rl.TRACE_CAPACITY * 20:].view(np.uint64)[0])
+    assert n_dev == 2 * N * TOKENS
+    L.trace_rebase(dev_ring, C.byref(m))
+    dev = dbuf[:n_dev * 20].view(rl.TRACE_ENTRY).copy()
+    n_host = int(host[rl.TRACE_CAPACITY * 20:].view(np.uint64)[0])
+    hst = host[:n_host * 20].view(rl.TRACE_ENTRY)
+    T = rl.TRACE
+
+    def of(e, name):
+        return e[e["type"] == T[name]]
+    post, commit, poll = of(hst, "DESC_POSTED"), of(hst, "DESC_COMMITTED"), of(hst, "COMPLETION_POLLED")
+    deq, done = of(dev, "DESC_CONSUMED"), of(dev, "COMPLETION_POSTED")
+    for x in (commit, poll, deq, done):
+        assert len(x) == N * TOKENS
+        assert np.array_equal(x["rollout_id"], post["rollout_id"]) and np.array_equal(x["seq"], post["seq"])
+    assert np.array_equal(post["rollout_id"], got["seq"].astype(np.uint32))
+    slack = (max(c0[2], c1[2]) + 1) // 2 + 1000
+    t = [x["tsc"].astype(np.int64) for x in (commit, deq, done, poll)]
+    for a, b in zip(t, t[1:]):
+        assert np.all(b - a >= -slack), int((b - a).min())
+    merged = np.zeros(rl.TRACE_RING_BYTES, np.uint8)
+    srcs = (C.c_void_p * 2)(host.ctypes.data, dev_ring)
+    assert L.trace_merge(merged.ctypes.data, srcs, 2) == n_host + n_dev
+    s = rl.TracePairStats()
+    lat = {}
+    for a, b in (("DESC_POSTED", "DESC_COMMITTED"), ("DESC_POSTED", "DESC_CONSUMED"),
+                 ("DESC_CONSUMED", "COMPLETION_POSTED"), ("DESC_POSTED", "COMPLETION_POLLED")):
+        assert L.trace_pair_stats(merged.ctypes.data, T[a], T[b], C.byref(s)) == 0
+        lat[f"{a}->{b}"] = (s.n, s.p50_ns, s.p99_ns)
+    print(f"[pipeline] latency pairs (n, p50 ns, p99 ns): {lat}", flush=True)
+    assert lat["DESC_POSTED->DESC_COMMITTED"][0] == N * TOKENS
+    assert lat["DESC_POSTED->COMPLETION_POLLED"][0] == N * TOKENS
+    assert lat["DESC_POSTED->DESC_CONSUMED"][0] >= 0.99 * N * TOKENS
+    L.rl_hip_host_free(dev_ring)

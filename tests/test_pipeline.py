@@ -246,7 +246,7 @@ def _replay_bench_pipeline(ref, rl, n, tokens, batch_max, kv_blocks, credits):
     return np.array(rows, dtype=np.uint64).reshape(-1, 6), batches[0], counts
 
 
-def _run_cmd_driver(rl, sim, n, tokens, batch_max, kv_blocks, credits):
+def _run_cmd_driver(rl, sim, n, tokens, batch_max, kv_blocks, credits, trace=None):
     L = rl.lib()
     pipe = np.zeros(PIPE, np.uint8)
     rew = np.zeros(rl.REWARD_RING_BYTES, np.uint8)
@@ -262,7 +262,7 @@ def _run_cmd_driver(rl, sim, n, tokens, batch_max, kv_blocks, credits):
     assert sim.sim_start(C.c_void_p(cmd), C.c_void_p(comp)) == 0
     try:
         rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, cmd, comp, rew.ctypes.data, C.byref(cfg), C.byref(st),
-                                   C.addressof(log), n * tokens)
+                                   C.addressof(log), n * tokens, trace)
     finally:
         done = sim.sim_stop()
         L.ring_destroy(cmd)
@@ -323,7 +323,7 @@ def test_cmd_driver_rejects_bad_config(rl):
         kw = dict(n_rollouts=1, tokens_per_rollout=1, batch_max=1, kv_blocks=1)
         kw.update(bad)
         cfg = rl.CmdPipelineCfg(**kw)
-        assert L.rl_pipeline_cmd_run(pipe.ctypes.data, 1, 1, None, C.byref(cfg), C.byref(st), None, 0) == -1
+        assert L.rl_pipeline_cmd_run(pipe.ctypes.data, 1, 1, None, C.byref(cfg), C.byref(st), None, 0, None) == -1
 
 
 # ---------------------------------------------------------------- RequestRing feeder
@@ -453,3 +453,37 @@ def test_feeder_rejects_unknown_dones_and_bad_params(rl, prod_shim):
     assert L.rl_feed_send(C.byref(f), 10) == 0
     L.req_ring_destroy(req_ring)
     L.done_ring_destroy(done_ring)
+
+
+def test_cmd_driver_host_trace(rl, sim):
+    """The host-side trace records of a run: one of each rollout event per
+    rollout, post / commit / poll per descriptor with its (rid, step) key, in
+    an order the report pairs completely."""
+    L = rl.lib()
+    ring = np.zeros(rl.TRACE_RING_BYTES, np.uint8)
+    L.trace_init(ring.ctypes.data)
+    n, tokens = 200, 40
+    rc, st, log, done, pipe, rew = _run_cmd_driver(rl, sim, n, tokens, 32, 128, (256, 128, 128, 1024),
+                                                   trace=ring.ctypes.data)
+    assert rc == 0
+    cnt = int(ring[rl.TRACE_CAPACITY * 20:].view(np.uint64)[0])
+    e = ring[:cnt * 20].view(rl.TRACE_ENTRY)
+    T = rl.TRACE
+    counts = {k: int((e["type"] == v).sum()) for k, v in T.items()}
+    assert counts == {"ROLLOUT_ALLOC": n, "ROLLOUT_FREE": n, "DESC_POSTED": n * tokens,
+                      "DESC_COMMITTED": n * tokens, "DESC_CONSUMED": 0, "COMPLETION_POSTED": 0,
+                      "COMPLETION_POLLED": n * tokens, "DECODE_BATCH": st.decode_batches, "REWARD_POSTED": n,
+                      "REWARD_SCORED": n, "TRAJECTORY_DONE": n}
+    assert np.all(np.diff(e["tsc"].astype(np.int64)) >= 0)
+    posted = e[e["type"] == T["DESC_POSTED"]]
+    polled = e[e["type"] == T["COMPLETION_POLLED"]]
+    assert np.array_equal(posted[["rollout_id", "seq"]], polled[["rollout_id", "seq"]])
+    got = np.array([(c.seq_id, c.reward_cookie & 0xFFFFFFFF) for c in log[:n * tokens]], dtype=np.uint64)
+    assert np.array_equal(got[:, 0], posted["rollout_id"]) and np.array_equal(got[:, 1], posted["seq"])
+    s = rl.TracePairStats()
+    for a, b, want in (("DESC_POSTED", "DESC_COMMITTED", n * tokens), ("DESC_POSTED", "COMPLETION_POLLED", n * tokens),
+                       ("ROLLOUT_ALLOC", "REWARD_POSTED", n), ("ROLLOUT_ALLOC", "TRAJECTORY_DONE", n),
+                       ("REWARD_POSTED", "REWARD_SCORED", n), ("REWARD_POSTED", "TRAJECTORY_DONE", n)):
+        assert L.trace_pair_stats(ring.ctypes.data, T[a], T[b], C.byref(s)) == 0
+        assert s.n == want, (a, b, s.n)
+        assert s.p50_ns <= s.p90_ns <= s.p99_ns
