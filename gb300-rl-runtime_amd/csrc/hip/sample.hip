@@ -12,13 +12,18 @@
 //         largest value. The bound is the minimum over the four waves of each
 //         wave's ceil(k/4)-th largest lane maximum (found with a 32-step ballot
 //         radix select), so at least k distinct elements lie above it.
-//  merge  grid (row): one 256-thread workgroup merges the slices: global max
-//         and log-sum-exp, exact k-th largest among the candidates (4-pass
-//         8-bit radix select on LDS histograms, each wave finding the digit
-//         with DPP scans), rank sort of the kept set by (x desc, index asc),
-//         24-bit integer weights rl_sample_weight(x - max), nucleus prefix,
-//         Philox4x32-10 draw and the ascending-index integer CDF walk - in one
-//         wave when at most 64 elements are kept.
+//  merge  grid (row): one 512-thread workgroup (8 waves) merges the slices:
+//         global max and log-sum-exp; the candidates gathered into LDS, one
+//         wave per slice list, keeping only keys at or above the largest
+//         slice bound (every slice's bound is below the row's k-th largest
+//         key); the exact k-th largest among them (MSB-first 8-bit radix
+//         select on LDS histograms from the highest bit where the candidate
+//         keys differ, each wave finding the digit with DPP scans); rank sort
+//         of the kept set by (x desc, index asc); 24-bit integer weights
+//         rl_sample_weight(x - max), nucleus prefix, Philox4x32-10 draw and
+//         the ascending-index integer CDF walk - in one wave when at most 64
+//         elements are kept. Rows without top-k (a whole-vocabulary nucleus)
+//         or whose candidates overflow take the exact full-row path below.
 // Integer weights make every sum exact, so the token is bit-identical to the
 // host restatement whatever the reduction order.
 #include <hip/hip_runtime.h>
@@ -320,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
 }
 
-// ---- block-wide helpers of the merge (256 threads = 4 waves) ----------------
+// ---- block-wide helpers of the merge (512 threads = 8 waves) ----------------
 
 constexpr int kMergeThreads = 512;  // 8 waves: two per SIMD hide each other's latency
 constexpr int kMergeWaves = kMergeThreads / 64;
