@@ -163,18 +163,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, AppendPar
     __shared__ float s_L[G];
     const uint32_t g = blockIdx.x;
     const uint32_t b = blockIdx.y;
-    if (ap.arena && threadIdx.x < 64)
-        append_row(ap, b, g, threadIdx.x, 64);
+    // the three values the row's partials are located by, loaded together
+    // (cum has batch + 1 entries whatever the context)
     const uint32_t cin = rl_sload(p.ctx + b);
+    const uint32_t U = rl_sload(p.cum + p.batch);
+    const uint32_t cum_b = rl_sload(p.cum + b);
+    if (ap.arena && threadIdx.x >= 192)
+        append_row(ap, b, g, threadIdx.x - 192, 64);
     const bool bad = cin > p.max_ctx;
     const uint32_t nu = tiles_of(p, cin);
     if (nu == 0) {
         empty_row<D, G, DT>(p, b, g, bad, threadIdx.x, 256);
         return;
     }
-    const uint32_t U = rl_sload(p.cum + p.batch);  // > 0: this row has tiles
-    const uint32_t NW = min(p.nwaves, U);
-    const uint32_t R0 = rl_sload(p.cum + b) + g * nu;
+    const uint32_t NW = min(p.nwaves, U);  // U > 0: this row has tiles
+    const uint32_t R0 = cum_b + g * nu;
     merge_row<D, G, DT, 256>(p, b, g, R0, nu, U, NW, bad, threadIdx.x, s_f, s_l, s_L);
 }
 
