@@ -5,7 +5,7 @@
 // Replaces decode_worker / process_descriptor (cu/worker.cu:25-131: one warp
 // per SM, lane 0 consumes one descriptor at a time, runs
 // attention_decode_step_fixed128 and pushes the completion) with one
-// persistent workgroup (4 wave64s) per ring pair - the single consumer of its
+// persistent workgroup (16 wave64s) per ring pair - the single consumer of its
 // command ring and the single producer of its completion ring, so the SPSC
 // contract of ring.h / completion.h holds on the device side:
 //
@@ -14,7 +14,7 @@
 //          whole window of descriptors already committed - up to 32, the
 //          decode_batch window (src/decode_batch.c:3-51) - is read with one
 //          16-byte load per lane, and the head is released once.
-//  decode  wave w takes descriptors w, w + 4, ... of the window: the fixed128
+//  decode  wave w takes descriptors w, w + 16, ... of the window: the fixed128
 //          step of the reference (cu/attention_decode.cu:60-204) - one head,
 //          d128, fp16 K/V of arena block kv_block_offset (K plane, V plane at
 //          +8 KiB, 32 tokens), seq_len = num_kv_blocks clamped to [1, 32]
@@ -51,7 +51,7 @@
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr uint32_t kWindow = 32;          // descriptors per poll at most (the decode_batch window)
 constexpr uint32_t kD = 128;              // fixed128 head dim
