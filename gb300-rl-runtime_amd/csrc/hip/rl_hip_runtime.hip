@@ -280,4 +280,51 @@ int rl_hip_timer_end(float *elapsed_ms)
     return 0;
 }
 
+int rl_hip_capture_begin(void)
+{
+    if (rl_require_open("rl_hip_capture_begin"))
+        return -1;
+    return rl_check_hip(hipStreamBeginCapture(g_session.stream, hipStreamCaptureModeThreadLocal),
+                        "hipStreamBeginCapture");
+}
+
+int rl_hip_capture_end(void **graph)
+{
+    if (rl_require_open("rl_hip_capture_end"))
+        return -1;
+    if (!graph) {
+        rl_set_error("rl_hip_capture_end: NULL output");
+        return -1;
+    }
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    if (rl_check_hip(hipStreamEndCapture(g_session.stream, &g), "hipStreamEndCapture"))
+        return -1;
+    hipGraphExec_t exec = nullptr;
+    const int rc = rl_check_hip(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc)
+        return -1;
+    *graph = exec;
+    return 0;
+}
+
+int rl_hip_graph_launch(void *graph)
+{
+    if (rl_require_open("rl_hip_graph_launch"))
+        return -1;
+    if (!graph) {
+        rl_set_error("rl_hip_graph_launch: NULL graph");
+        return -1;
+    }
+    return rl_check_hip(hipGraphLaunch((hipGraphExec_t)graph, g_session.stream), "hipGraphLaunch");
+}
+
+int rl_hip_graph_destroy(void *graph)
+{
+    if (!graph)
+        return 0;
+    return rl_check_hip(hipGraphExecDestroy((hipGraphExec_t)graph), "hipGraphExecDestroy");
+}
+
 }  // extern "C"

@@ -283,6 +283,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_memcpy_h2d": (i32, [vp, vp, sz]), "rl_hip_memcpy_d2h": (i32, [vp, vp, sz]),
         "rl_hip_memcpy_d2d": (i32, [vp, vp, sz]), "rl_hip_memset_d": (i32, [vp, i32, sz]),
         "rl_hip_sync": (i32, []), "rl_hip_timer_begin": (i32, []),
+        "rl_hip_capture_begin": (i32, []), "rl_hip_capture_end": (i32, [C.POINTER(vp)]),
+        "rl_hip_graph_launch": (i32, [vp]), "rl_hip_graph_destroy": (i32, [vp]),
         "rl_hip_timer_end": (i32, [C.POINTER(C.c_float)]),
         "rl_hip_attn_decode_workspace": (sz, [C.POINTER(AttnArgs)]),
         "rl_hip_attn_decode": (i32, [C.POINTER(AttnArgs)]),
@@ -489,6 +491,29 @@ class CmdWorker:
             L.rl_hip_host_free(self.pairs)
             L.rl_hip_host_free(self.stop_flag)
             self.ring = self.comp = None
+
+
+class Graph:
+    """What fn() launches on the library stream, captured once into a HIP
+    graph and replayed by launch()."""
+
+    def __init__(self, fn):
+        check(lib().rl_hip_capture_begin(), "rl_hip_capture_begin")
+        try:
+            fn()
+        finally:
+            h = C.c_void_p()
+            rc = lib().rl_hip_capture_end(C.byref(h))
+        check(rc, "rl_hip_capture_end")
+        self.handle = h.value
+
+    def launch(self) -> None:
+        check(lib().rl_hip_graph_launch(self.handle), "rl_hip_graph_launch")
+
+    def close(self) -> None:
+        if self.handle:
+            lib().rl_hip_graph_destroy(self.handle)
+            self.handle = None
 
 
 class Timer:

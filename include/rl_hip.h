@@ -71,6 +71,19 @@ int rl_hip_sync(void);
 int rl_hip_timer_begin(void);
 int rl_hip_timer_end(float *elapsed_ms);
 
+/* ---- HIP graphs of the library stream ---------------------------------------
+ * No counterpart in the reference (its decode path launches one kernel per
+ * descriptor). rl_hip_capture_begin records, instead of running, what this
+ * thread launches on the library stream until rl_hip_capture_end, which
+ * instantiates the recording into *graph; rl_hip_graph_launch replays it on
+ * the library stream (same device pointers, same arguments) and
+ * rl_hip_graph_destroy frees it. Only kernel entry points may be called while
+ * capturing: no rl_hip_sync, timers, copies or rl_hip_memset_d. */
+int rl_hip_capture_begin(void);
+int rl_hip_capture_end(void **graph);
+int rl_hip_graph_launch(void *graph);
+int rl_hip_graph_destroy(void *graph);
+
 #define RL_DTYPE_BF16 0u
 #define RL_DTYPE_FP16 1u
 
