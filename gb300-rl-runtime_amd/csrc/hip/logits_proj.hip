@@ -6,16 +6,20 @@
 // like an lm_head weight, one row of K per vocabulary entry, so both
 // operands are K-contiguous.
 //
-//  tiles   128 x 128 output tile per 256-thread workgroup, K in steps of 64;
-//          the four waves each own 64 x 64 (4 x 4 MFMA blocks of 16 x 16).
-//          The M tiles sharing a W tile run together on one XCD, so W
-//          streams from HBM about once.
-//  staging the X and W tiles of a K step (16 KiB each) are copied HBM -> LDS
-//          with global_load_lds_dwordx4, double-buffered; 16-byte chunk c of
-//          row r lands at chunk position c ^ (r & 7) (lanes fetch permuted
-//          sources), so the MFMA operand reads are free of bank conflicts.
+//  tiles   256 x 128 output tile per 512-thread workgroup (8 waves of
+//          64 x 64: 4 x 4 MFMA blocks of 16 x 16), K in steps of 64. At 256
+//          rows every W tile is read by exactly one workgroup and the grid
+//          (one workgroup per 128 vocabulary rows) fits the device in one
+//          round; X (at most 2 MiB per M tile) is read from L2.
+//  staging the X and W tiles of a K step (32 + 16 KiB) are copied HBM -> LDS
+//          with global_load_lds_dwordx4 into a 3-stage ring (144 KiB, one
+//          workgroup per CU), two steps ahead of the MFMAs, with one barrier
+//          per step; 16-byte chunk c of row r lands at chunk position
+//          c ^ (r & 7) (lanes fetch permuted sources), so the MFMA operand
+//          reads are free of bank conflicts.
 //  MFMA    v_mfma_f32_16x16x32_bf16: lane l reads 16 B of row l % 16 at
 //          k-chunk 4 s + l / 16 for both operands; 32 MFMAs per wave and K step.
+//  When several M tiles share a W tile, they run side by side on one XCD.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -28,10 +32,15 @@ namespace {
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int TILE_BYTES = BM * BK * 2;   // 16 KiB per operand tile
-constexpr int OPS = TILE_BYTES / 1024;    // 1 KiB copies per operand tile
-constexpr int OPS_PER_WAVE = OPS / 4;     // per operand, per wave
+constexpr int BM = 256, BN = 128, BK = 64;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
+constexpr int NSTAGE = 3;
+constexpr int XBYTES = BM * BK * 2;          // 32 KiB of X per step
+constexpr int WBYTES = BN * BK * 2;          // 16 KiB of W per step
+constexpr int XOPS = XBYTES / 1024 / kWaves; // 1 KiB copies per wave and step: 4 of X
+constexpr int WOPS = WBYTES / 1024 / kWaves; // ... and 2 of W
+constexpr int STEP_OPS = XOPS + WOPS;
 
 struct ProjParams {
     const uint16_t *x;  // [M][ldx]
@@ -47,33 +56,30 @@ struct ProjParams {
 // run side by side behind one L2 and W leaves HBM about once.
 constexpr uint32_t kXcds = 8;
 
-// Copies rows [row0, row0 + 128) x k [k0, k0 + 64) of a K-contiguous
-// operand into an LDS tile, this wave's share of the 16 copies. Rows past
-// `rows` re-read the last row (in bounds; their results are never stored).
-__device__ __forceinline__ void stage_tile(const uint16_t *src, uint32_t ld, uint32_t rows, uint32_t row0,
-                                           uint32_t k0, RL_LDS uint8_t *dst, int wave, int lane)
+// Copies `nops` 1 KiB pieces (8 rows x 64 k each) of rows [row0, row0 + 8 *
+// total ops) x k [k0, k0 + 64) of a K-contiguous operand into an LDS tile,
+// pieces op0 .. op0 + nops - 1. Rows past `rows` re-read the last row (in
+// bounds; their results are never stored).
+template <int NOPS>
+__device__ __forceinline__ void stage_rows(const uint16_t *src, uint32_t ld, uint32_t rows, uint32_t row0, uint32_t k0,
+                                           RL_LDS uint8_t *dst, int op0, int lane)
 {
+    const uint16_t *base = src + (size_t)min(row0, rows - 1) * ld + k0;  // wave-uniform: the tile's first row
 #pragma unroll
-    for (int j = 0; j < OPS_PER_WAVE; j++) {
-        const int op = wave * OPS_PER_WAVE + j;
+    for (int j = 0; j < NOPS; j++) {
+        const int op = op0 + j;
         const uint32_t r = (uint32_t)op * 8 + (uint32_t)lane / 8;
-        const uint32_t pos = (uint32_t)lane % 8;
-        const uint32_t c = pos ^ (r & 7);
-        const uint32_t grow = min(row0 + r, rows - 1);
-        const uint16_t *rowp = src + (size_t)grow * ld + k0;
-        // wave-uniform base: the tile's first row; per-lane offset to its chunk
-        const uint16_t *base = src + (size_t)min(row0, rows - 1) * ld + k0;
+        const uint32_t c = ((uint32_t)lane % 8) ^ (r & 7);
+        const uint16_t *rowp = src + (size_t)min(row0 + r, rows - 1) * ld + k0;
         const uint32_t off = (uint32_t)((const uint8_t *)(rowp + c * 8) - (const uint8_t *)base);
         rl_g2lds_16_off(base, off, dst + op * 1024);
     }
 }
 
-__global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
+__global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t sA0[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t sB0[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t sA1[TILE_BYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t sB1[TILE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sX[NSTAGE][XBYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t sW[NSTAGE][WBYTES];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -83,7 +89,7 @@ __global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
     if (nt >= p.n_tiles)
         return;
     const uint32_t m0 = mt * BM, n0 = nt * BN;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wm = wave & 3, wn = wave >> 2;
 
     rl_f32x4 acc[4][4];
 #pragma unroll
@@ -96,22 +102,30 @@ __global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
     // fragment addressing inside a tile: row (l % 16) of block i, chunk 4 s + l / 16
     const int fr = lane & 15;
     const int fc = lane >> 4;
+    auto stage = [&](uint32_t kt) {
+        const int buf = (int)(kt % NSTAGE);
+        stage_rows<XOPS>(p.x, p.ldx, p.M, m0, kt * BK, (RL_LDS uint8_t *)sX[buf], wave * XOPS, lane);
+        stage_rows<WOPS>(p.w, p.ldw, p.N, n0, kt * BK, (RL_LDS uint8_t *)sW[buf], wave * WOPS, lane);
+    };
 
-    stage_tile(p.x, p.ldx, p.M, m0, 0, (RL_LDS uint8_t *)sA0, wave, lane);
-    stage_tile(p.w, p.ldw, p.N, n0, 0, (RL_LDS uint8_t *)sB0, wave, lane);
+    stage(0);
+    if (ksteps > 1)
+        stage(1);
     for (uint32_t kt = 0; kt < ksteps; kt++) {
-        RL_LDS uint8_t *a_cur = (kt & 1) ? (RL_LDS uint8_t *)sA1 : (RL_LDS uint8_t *)sA0;
-        RL_LDS uint8_t *b_cur = (kt & 1) ? (RL_LDS uint8_t *)sB1 : (RL_LDS uint8_t *)sB0;
-        if (kt + 1 < ksteps) {
-            RL_LDS uint8_t *a_nxt = (kt & 1) ? (RL_LDS uint8_t *)sA0 : (RL_LDS uint8_t *)sA1;
-            RL_LDS uint8_t *b_nxt = (kt & 1) ? (RL_LDS uint8_t *)sB0 : (RL_LDS uint8_t *)sB1;
-            stage_tile(p.x, p.ldx, p.M, m0, (kt + 1) * BK, a_nxt, wave, lane);
-            stage_tile(p.w, p.ldw, p.N, n0, (kt + 1) * BK, b_nxt, wave, lane);
-            rl_wait_vmcnt<2 * OPS_PER_WAVE>();  // this wave's copies of step kt landed
-        } else {
+        // this wave's copies of step kt have landed once at most the next
+        // step's are outstanding (copies complete in issue order)
+        if (kt + 1 < ksteps)
+            rl_wait_vmcnt<STEP_OPS>();
+        else
             rl_wait_vmcnt<0>();
-        }
-        __syncthreads();  // ... and every other wave's
+        // every wave's copies of step kt have landed, and every wave is done
+        // with step kt - 1, whose buffer step kt + 2 takes
+        __syncthreads();
+        if (kt + 2 < ksteps)
+            stage(kt + 2);
+        const int buf = (int)(kt % NSTAGE);
+        RL_LDS const uint8_t *xs = (RL_LDS const uint8_t *)sX[buf];
+        RL_LDS const uint8_t *ws = (RL_LDS const uint8_t *)sW[buf];
 #pragma unroll
         for (int s = 0; s < BK / 32; s++) {
             s16x8 af[4], bf[4];
@@ -120,8 +134,8 @@ __global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
             for (int i = 0; i < 4; i++) {
                 const int ra = wm * 64 + i * 16 + fr;
                 const int rb = wn * 64 + i * 16 + fr;
-                af[i] = *(RL_LDS const s16x8 *)(a_cur + ra * (BK * 2) + ((c ^ (ra & 7)) << 4));
-                bf[i] = *(RL_LDS const s16x8 *)(b_cur + rb * (BK * 2) + ((c ^ (rb & 7)) << 4));
+                af[i] = *(RL_LDS const s16x8 *)(xs + ra * (BK * 2) + ((c ^ (ra & 7)) << 4));
+                bf[i] = *(RL_LDS const s16x8 *)(ws + rb * (BK * 2) + ((c ^ (rb & 7)) << 4));
             }
 #pragma unroll
             for (int i = 0; i < 4; i++)
@@ -131,7 +145,6 @@ __global__ __launch_bounds__(256) void logits_proj_kernel(ProjParams p)
                                                                         __builtin_bit_cast(bf16x8, bf[j]),
                                                                         acc[i][j], 0, 0, 0);
         }
-        __syncthreads();  // the stage is rewritten two steps later
     }
 
     // C block (i, j): lane holds rows 4 (l / 16) + r, column l % 16
@@ -190,6 +203,6 @@ extern "C" int rl_hip_logits_proj(const rl_logits_proj_args_t *a)
         rl_set_error("rl_hip_logits_proj: %llu workgroups", (unsigned long long)grid);
         return -1;
     }
-    hipLaunchKernelGGL(logits_proj_kernel, dim3((uint32_t)grid), dim3(256), 0, rl_stream(), p);
+    hipLaunchKernelGGL(logits_proj_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, rl_stream(), p);
     return rl_check_launch("logits_proj_kernel launch");
 }
