@@ -51,7 +51,7 @@ struct SplitStat {
     uint32_t arg_idx;
     uint32_t n_cand;  // candidates written (> kCandCap: overflow)
     uint32_t cand_lo; // every candidate key is >= this
-    uint32_t pad[2];
+    uint64_t draw;    // split 0 of a sampled row: the row's Philox draw
 };
 
 struct SampleParams {
@@ -135,6 +135,20 @@ __device__ __forceinline__ void wave_argmax(float &v, uint32_t &i)
     }
 }
 
+// The kw-th largest key held by the 64 lanes (kw in [1, 64]) among keys that
+// equal `prefix` above bit top, exact: MSB-first radix select on ballot counts
+// over bits top .. 0 (smaller keys never count).
+__device__ __forceinline__ uint32_t wave_kth_largest_key_from(uint32_t key, uint32_t kw, uint32_t prefix, int top)
+{
+    for (int bit = top; bit >= 0; bit--) {
+        const uint32_t cand = prefix | (1u << bit);
+        const uint64_t ge = __ballot(key >= cand);
+        if ((uint32_t)__popcll(ge) >= kw)
+            prefix = cand;
+    }
+    return prefix;
+}
+
 // The kw-th largest key held by the 64 lanes (kw in [1, 64]), exact: MSB-first
 // radix select on ballot counts.
 __device__ __forceinline__ uint32_t wave_kth_largest_key(uint32_t key, uint32_t kw)
@@ -160,9 +174,9 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
 
     __shared__ float s_red[4];
     __shared__ uint32_t s_red_i[4];
+    __shared__ float s_z[4];
     __shared__ uint32_t s_key[4];
     __shared__ uint32_t s_wtot[4];
-    __shared__ uint32_t s_ncand;
 
     const float *lrow = p.logits + (size_t)row * p.row_stride;
     const uint32_t c0 = split * kSplitLen;
@@ -172,7 +186,8 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
     // Every load is issued unconditionally (a quad past the end re-reads the
     // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
-    // masked afterwards, so all eight are in flight together.
+    // masked afterwards, so all eight are in flight together. Only the last
+    // slice of a row can reach past the vocabulary (a workgroup-uniform test).
     float x[kPerThread];
     const uint32_t last_quad = (p.vocab - 1) & ~3u;
     rl_f32x4 raw[kPerThread / 4];
@@ -181,13 +196,24 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
         const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
         raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
     }
+    // the row's Philox draw, for the merge (computed while the loads are in flight)
+    uint64_t draw = 0;
+    if (split == 0 && !greedy && wave == 0)
+        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+    if (c0 + (uint32_t)kSplitLen <= p.vocab) {
 #pragma unroll
-    for (int k = 0; k < kPerThread / 4; k++) {
-        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
-        x[k * 4 + 0] = col + 0 < p.vocab ? raw[k].x : -INFINITY;
-        x[k * 4 + 1] = col + 1 < p.vocab ? raw[k].y : -INFINITY;
-        x[k * 4 + 2] = col + 2 < p.vocab ? raw[k].z : -INFINITY;
-        x[k * 4 + 3] = col + 3 < p.vocab ? raw[k].w : -INFINITY;
+        for (int k = 0; k < kPerThread / 4; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                x[k * 4 + e] = raw[k][e];
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++) {
+            const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                x[k * 4 + e] = col + (uint32_t)e < p.vocab ? raw[k][e] : -INFINITY;
+        }
     }
 
     SplitStat *st = p.stats + (size_t)row * p.splits + split;
@@ -227,13 +253,12 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
                 z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
         }
         z = wave_sum(z);
-        __syncthreads();
         if (lane == 0)
-            s_red[wave] = z;
+            s_z[wave] = z;
         __syncthreads();
         if (tid == 0) {
             st->max_x = m;
-            st->sum_exp = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+            st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
             st->arg_val = m;
             st->arg_idx = mi;
             st->n_cand = 0;
@@ -242,6 +267,8 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
 
     // ---- sampling: x = l * inv_t, slice max, sum exp, candidates -------------
+    // Two barriers: (1) wave maxima and k-th bounds, (2) wave sums and
+    // candidate counts; the candidates are then written at their offsets.
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < kPerThread; i++) {
@@ -250,7 +277,6 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
     const float wmax = wave_max(tmax);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
-    uint32_t cand_lo = 0;
     if (k_eff != 0) {
         const uint32_t kw = (k_eff + 3) / 4;
         const uint32_t ck = wave_kth_largest_key(rl_float_key(tmax), kw);
@@ -259,8 +285,6 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
     if (lane == 0)
         s_red[wave] = wmax;
-    if (tid == 0)
-        s_ncand = 0;
     __syncthreads();
     const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
     float z = 0.f;
@@ -271,16 +295,23 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
             z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
     }
     z = wave_sum(z);
+    if (lane == 0)
+        s_z[wave] = z;
 
+    // Candidates: key(x) >= clb and x != -inf. For x not NaN that is x >= t
+    // with t = the float of clb (the key order is the float order with -0 =
+    // +0), t raised to -FLT_MAX when clb is the key of -inf; a NaN x has a key
+    // above every non-NaN key, and !(x < t) keeps it too.
+    uint32_t cand_lo = 0, cnt = 0, incl = 0;
+    float t = 0.f;
     if (k_eff != 0) {
         const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
         cand_lo = clb;
-        // count, block-wide exclusive scan, then write: no per-element ballots
-        uint32_t cnt = 0;
+        t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
 #pragma unroll
         for (int i = 0; i < kPerThread; i++)
-            cnt += (rl_float_key(x[i]) >= clb && x[i] != -INFINITY) ? 1u : 0u;
-        uint32_t incl = cnt;
+            cnt += !(x[i] < t) ? 1u : 0u;
+        incl = cnt;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const uint32_t o = __shfl_up(incl, off);
@@ -289,39 +320,33 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
         }
         if (lane == 63)
             s_wtot[wave] = incl;
-        __syncthreads();
+    }
+    __syncthreads();
+    if (k_eff != 0 && cnt) {
         uint32_t base = incl - cnt;
         for (int w = 0; w < wave; w++)
             base += s_wtot[w];
-        if (tid == 0)
-            s_ncand = s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3];
         uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandCap;
-        if (cnt) {
 #pragma unroll
-            for (int k = 0; k < kPerThread / 4; k++)
+        for (int k = 0; k < kPerThread / 4; k++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float v = x[k * 4 + e];
-                    const uint32_t key = rl_float_key(v);
-                    if (key >= clb && v != -INFINITY) {
-                        if (base < (uint32_t)kCandCap)
-                            cand[base] = make_uint2(key, c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
-                        base++;
-                    }
+            for (int e = 0; e < 4; e++) {
+                const float v = x[k * 4 + e];
+                if (!(v < t)) {
+                    if (base < (uint32_t)kCandCap)
+                        cand[base] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                    base++;
                 }
-        }
+            }
     }
-    __syncthreads();
-    if (lane == 0)
-        s_red[wave] = z;
-    __syncthreads();
     if (tid == 0) {
         st->max_x = m;
-        st->sum_exp = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+        st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
         st->arg_val = m;
         st->arg_idx = 0;
-        st->n_cand = s_ncand;
+        st->n_cand = k_eff != 0 ? s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3] : 0u;
         st->cand_lo = cand_lo;
+        st->draw = draw;
     }
 }
 
@@ -929,6 +954,25 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 
     const SplitStat *st = p.stats + (size_t)row * p.splits;
     const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const uint32_t wave = tid >> 6;
+
+    // Issued before the slice statistics are known, so that the latencies
+    // overlap: this wave's first 256 candidates of the lists of splits w and
+    // w + 8 (in bounds whatever the split wrote; masked by the counts later),
+    // and the row's Philox draw (computed by the row's first split).
+    const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandCap;
+    uint2 pv[8];
+    uint64_t draw = 0;
+    if (!greedy) {
+        draw = st[0].draw;
+        const uint2 *pf1 = rbase + (size_t)min(wave, p.splits - 1) * kCandCap;
+        const uint2 *pf2 = rbase + (size_t)min(wave + kMergeWaves, p.splits - 1) * kCandCap;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            pv[r] = pf1[r * 64 + lane];
+            pv[4 + r] = pf2[r * 64 + lane];
+        }
+    }
 
     // Global max and log-sum-exp over the slices (splits <= 64: one per lane;
     // every wave computes the same values).
@@ -945,10 +989,14 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         clo = st[lane].cand_lo;
     }
     const float m = wave_max(mx);
-    const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
-    const float lse = m + logf(wave_sum(zterm));
+    // the row's log-sum-exp, needed only for the logprob written at the end
+    auto row_lse = [&]() {
+        const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
+        return m + logf(wave_sum(zterm));
+    };
 
     if (greedy) {
+        const float lse = row_lse();
         wave_argmax(av, ai);
         if (tid == 0) {
             const uint32_t i = ai >= p.vocab ? 0u : ai;  // all -inf: lowest index
@@ -976,66 +1024,110 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         // splits w, w + 8, ..., four loads per lane in flight, and appends
         // the kept ones (order is irrelevant below).
         const uint32_t key_lo = rl_wave_max_u32(ncand ? clo : 0u);
-        if (tid == 0)
+        // Every kept candidate key lies in [key_lo, key_hi] (the slices' bounds
+        // and the row max), so the MSB-first radix select below starts at the
+        // highest bit hb where those differ, 8-bit digits. Its first histogram
+        // is filled during the gather.
+        const uint32_t key_hi = rl_float_key(m);
+        const uint32_t diff = key_lo ^ key_hi;
+        const int hb = diff ? 31 - __builtin_clz(diff) : -1;
+        const int shift0 = hb >= 7 ? hb - 7 : 0;
+        const uint32_t above0 = (hb < 0 || hb >= 31) ? 0u : ~((2u << hb) - 1u);
+        const uint32_t prefix0 = key_hi & above0;
+        if (tid == 0) {
             bs.cnt[0] = 0;
+            bs.cnt[1] = 0;
+            bs.n = 0;
+        }
+        if (tid < 256) {
+            s_h2[0][tid] = 0;
+            s_h2[1][tid] = 0;
+        }
         __syncthreads();
-        const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandCap;
-        const uint32_t wave = tid >> 6;
-        for (uint32_t t = wave; t < p.splits; t += kMergeWaves) {
-            const uint32_t cnt = rl_readlane(ncand, (int)t);
-            const uint2 *src = rbase + (size_t)t * kCandCap;
-            for (uint32_t j0 = 0; j0 < cnt; j0 += 256) {
-                uint2 v[4];
+        // Wave w copies the lists of splits w and w + 8 (then w + 16 and
+        // w + 24, ...): both lists' loads in flight together, one LDS atomic
+        // per wave for the eight groups of 64, keeping only keys at or above
+        // key_lo (order is irrelevant below).
+        for (uint32_t t = wave; t < p.splits; t += 2 * kMergeWaves) {
+            const uint32_t t2 = t + kMergeWaves;
+            const bool has2 = t2 < p.splits;
+            const uint32_t cnt1 = rl_readlane(ncand, (int)t);
+            const uint32_t cnt2 = has2 ? rl_readlane(ncand, (int)min(t2, 63u)) : 0u;
+            const uint2 *src1 = rbase + (size_t)t * kCandCap;
+            const uint2 *src2 = has2 ? rbase + (size_t)t2 * kCandCap : src1;
+            const uint32_t last1 = cnt1 ? cnt1 - 1 : 0u, last2 = cnt2 ? cnt2 - 1 : 0u;
+            for (uint32_t j0 = 0; j0 < max(cnt1, cnt2); j0 += 256) {
+                uint2 v[8];
+                if (t == wave && j0 == 0) {
 #pragma unroll
-                for (int r = 0; r < 4; r++)
-                    v[r] = src[min(j0 + (uint32_t)(r * 64 + lane), cnt - 1)];
+                    for (int g = 0; g < 8; g++)
+                        v[g] = pv[g];
+                } else {
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const bool take = j0 + (uint32_t)(r * 64 + lane) < cnt && v[r].x >= key_lo;
-                    const uint32_t pos = wave_append(take, &bs.cnt[0]);
-                    if (take)
-                        s_cand[pos] = v[r];  // pos < n <= kMergeCap
+                    for (int r = 0; r < 4; r++) {
+                        v[r] = src1[min(j0 + (uint32_t)(r * 64 + lane), last1)];
+                        v[4 + r] = src2[min(j0 + (uint32_t)(r * 64 + lane), last2)];
+                    }
+                }
+                bool tk[8];
+                uint64_t bal[8];
+                uint32_t off[8], tot = 0;
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    const uint32_t j = j0 + (uint32_t)((g & 3) * 64 + lane);
+                    tk[g] = j < (g < 4 ? cnt1 : cnt2) && v[g].x >= key_lo;
+                    bal[g] = __ballot(tk[g]);
+                    off[g] = tot;
+                    tot += (uint32_t)__popcll(bal[g]);
+                }
+                uint32_t base = 0;
+                if (lane == 0 && tot)
+                    base = atomicAdd(&bs.cnt[0], tot);
+                base = (uint32_t)__builtin_amdgcn_readfirstlane((int)base);
+#pragma unroll
+                for (int g = 0; g < 8; g++) {
+                    if (tk[g]) {
+                        const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(bal[g] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal[g], 0u));
+                        s_cand[base + off[g] + below] = v[g];  // < n <= kMergeCap
+                        if (hb >= 0 && (v[g].x & above0) == prefix0)
+                            atomicAdd(&s_h2[0][(v[g].x >> shift0) & 0xFFu], 1u);
+                    }
                 }
             }
         }
-        if (tid == 0)
-            bs.n = 0;
-        if (tid < 256)
-            s_h2[0][tid] = 0;
         __syncthreads();
         const uint32_t nf = bs.cnt[0];
 
         // ---- exact k_eff-th largest key --------------------------------------
-        // Every candidate key lies in [key_lo, key_hi] (the slices' bounds and
-        // the row max), so the MSB-first radix select starts at the highest bit
-        // where those differ: 8-bit digits, and the first pass already spreads
-        // the candidates over many bins. The pass's histogram is filled while
-        // the other one is cleared; every wave then finds the digit itself:
-        // lane l holds bins 255-4l .. 252-4l, a DPP scan gives the count in
-        // higher bins, and the digit is the bin where that count reaches need.
-        // With fewer than k_eff candidates the row has fewer than k_eff finite
-        // logits, and every finite one is kept.
+        // Each pass's histogram (after the first) is filled while the other one
+        // is cleared; every wave then finds the digit itself: lane l holds
+        // bins 255-4l .. 252-4l, a DPP scan gives the count in higher bins,
+        // and the digit is the bin where that count reaches need. Once the
+        // chosen bin holds at most 64 keys, they are copied out and one wave
+        // finishes the selection with a ballot radix select. With fewer than
+        // k_eff candidates the row has fewer than k_eff finite logits, and
+        // every finite one is kept.
         uint32_t cutoff = 0;
         if (nf >= k_eff) {
-            const uint32_t key_hi = rl_float_key(m);
-            const uint32_t diff = key_lo ^ key_hi;
-            if (diff == 0) {
+            if (hb < 0) {
                 cutoff = key_hi;
             } else {
-                const int hb = 31 - __builtin_clz(diff);
-                uint32_t prefix = key_hi & ~((2u << hb) - 1u);
+                uint32_t prefix = prefix0;
                 uint32_t need = k_eff;
                 int pass = 0;
                 for (int top = hb; top >= 0; top -= 8, pass++) {
                     const int shift = top >= 7 ? top - 7 : 0;
                     const uint32_t above = top >= 31 ? 0u : ~((2u << top) - 1u);
                     uint32_t *H = s_h2[pass & 1];
-                    for (uint32_t i = tid; i < nf; i += kMergeThreads) {
-                        const uint32_t key = s_cand[i].x;
-                        if ((key & above) == prefix)
-                            atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
+                    if (pass > 0) {
+                        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
+                            const uint32_t key = s_cand[i].x;
+                            if ((key & above) == prefix)
+                                atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
+                        }
+                        __syncthreads();
                     }
-                    __syncthreads();
                     if (tid < 256)
                         s_h2[(pass & 1) ^ 1][tid] = 0;
                     uint32_t h[4], own = 0;
@@ -1046,12 +1138,13 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     }
                     uint32_t acc = rl_wave_incl_scan_u32(own) - own;
                     int found = -1;
-                    uint32_t rem = 0;
+                    uint32_t rem = 0, hcnt = 0;
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         if (found < 0 && acc < need && acc + h[j] >= need) {
                             found = 255 - 4 * lane - j;
                             rem = need - acc;
+                            hcnt = h[j];
                         }
                         acc += h[j];
                     }
@@ -1059,7 +1152,28 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     const int src = hit ? (int)__ffsll((long long)hit) - 1 : 0;
                     prefix |= (uint32_t)__builtin_amdgcn_readlane(found, src) << shift;
                     need = rl_readlane(rem, src);
+                    const uint32_t bin_cnt = rl_readlane(hcnt, src);
                     __syncthreads();
+                    if (shift > 0 && bin_cnt <= 64u) {
+                        // the keys sharing every bit fixed so far (bits >= shift)
+                        const uint32_t above_s = ~((1u << shift) - 1u);
+                        uint32_t *lst = s_h2[pass & 1];  // H is read by no one after the barrier
+                        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
+                            const uint32_t key = s_cand[i].x;
+                            if ((key & above_s) == prefix)
+                                lst[atomicAdd(&bs.cnt[1], 1u)] = key;  // bin_cnt <= 64 of them
+                        }
+                        __syncthreads();
+                        if (tid < 64) {
+                            const uint32_t key = (uint32_t)lane < bin_cnt ? lst[lane] : 0u;
+                            const uint32_t c = wave_kth_largest_key_from(key, need, prefix, shift - 1);
+                            if (tid == 0)
+                                bs.w32[0] = c;
+                        }
+                        __syncthreads();
+                        prefix = bs.w32[0];
+                        break;
+                    }
                 }
                 cutoff = prefix;
             }
@@ -1083,21 +1197,33 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             // ---- one wave: lane i holds sorted element i; with at most 64
             // weights of at most 2^24 every prefix fits in 32 bits ------------
             tok = 0;
+            // rank of kept key i = kept keys above it; thread (i, b) counts
+            // over keys 8b .. 8b + 7 (s_h2 is free after the cutoff)
+            {
+                const uint32_t i = tid & 63u, b = tid >> 6;
+                const uint64_t cki = i < nk ? s_keep[i] : 0ull;
+                uint32_t part = 0;
+#pragma unroll
+                for (uint32_t jj = 0; jj < 8; jj++) {
+                    const uint32_t j = b * 8 + jj;
+                    part += (j < nk && s_keep[j] > cki) ? 1u : 0u;
+                }
+                s_h2[b >> 2][(b & 3) * 64 + i] = part;
+            }
+            __syncthreads();
             if (tid < 64) {
                 const bool valid = (uint32_t)lane < nk;
                 const uint64_t ck = valid ? s_keep[lane] : 0ull;  // real keys are > 0
-                // rank = kept keys above mine (broadcast LDS reads, independent)
                 uint32_t rank = 0;
-                for (uint32_t j = 0; j < nk; j++)
-                    rank += s_keep[j] > ck ? 1u : 0u;
+#pragma unroll
+                for (uint32_t b = 0; b < 8; b++)
+                    rank += s_h2[b >> 2][(b & 3) * 64 + lane];
                 if (valid)
                     s_sort[rank] = ck;
                 rl_wave_lds_fence();
                 const uint64_t cs = valid ? s_sort[lane] : 0ull;
                 const uint32_t idx = 0xFFFFFFFFu - (uint32_t)cs;
                 const uint32_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(cs >> 32)) - m) : 0u;
-                s_idx[lane] = idx;
-                s_w[lane] = w;
                 const uint32_t c = rl_wave_incl_scan_u32(w);
                 const uint32_t wk = rl_readlane(c, 63);
                 uint32_t np = nk;
@@ -1107,12 +1233,12 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
                 }
                 const uint32_t wp = np ? rl_readlane(c, (int)np - 1) : 0u;
-                const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
+                const uint64_t u = rl_mulhi_u64(draw, wp);
                 const bool in_p = (uint32_t)lane < np;
-                rl_wave_lds_fence();
+                // ascending-index prefix weight at my index (lane j holds sorted element j)
                 uint32_t s_le = 0;
                 for (uint32_t j = 0; j < np; j++)
-                    s_le += s_idx[j] <= idx ? s_w[j] : 0u;
+                    s_le += rl_readlane(idx, (int)j) <= idx ? rl_readlane(w, (int)j) : 0u;
                 tok = rl_wave_min_u32(in_p && (uint64_t)s_le > u ? idx : 0xFFFFFFFFu);
                 if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
                     tok = rl_wave_min_u32(in_p ? idx : 0xFFFFFFFFu);
@@ -1167,7 +1293,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             const uint64_t wp = block_sum_u64(wp_own, bs);
 
             // ---- draw; smallest index whose ascending-index prefix weight exceeds u
-            const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
+            const uint64_t u = rl_mulhi_u64(draw, wp);
             uint32_t cand = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
             for (uint32_t i = tid; i < np; i += kMergeThreads) {
                 const uint32_t idx_i = s_idx[i];
@@ -1188,9 +1314,12 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     }
     if (exact)
         tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
-    if (tid == 0) {
-        p.token_out[row] = tok;
-        p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+    if (tid < 64) {
+        const float lse = row_lse();
+        if (tid == 0) {
+            p.token_out[row] = tok;
+            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+        }
     }
 }
 
