@@ -304,6 +304,10 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "infer_submit_decode": (i32, [C.POINTER(InferHwCtx), u32, u64, u64, u32, u32, u32]),
         "hw_worker_sim_run": (None, [C.POINTER(HwWorkerSim)]),
         "hw_worker_apply_decode_rule": (u32, [C.POINTER(HwDesc)]),
+        "rtl_desc_pack": (C.c_int, [C.POINTER(HwDesc), C.POINTER(C.c_uint32)]),
+        "rtl_desc_unpack": (C.c_int, [C.POINTER(C.c_uint32), C.POINTER(HwDesc)]),
+        "rtl_comp_pack": (C.c_int, [C.POINTER(HwDesc), C.POINTER(C.c_uint32)]),
+        "rtl_comp_unpack": (C.c_int, [C.POINTER(C.c_uint32)] + [C.POINTER(C.c_uint32)] * 4),
         "ring_create": (vp, []), "ring_destroy": (None, [vp]),
         "comp_ring_create": (vp, []), "comp_ring_destroy": (None, [vp]),
         "req_ring_create": (vp, []), "req_ring_destroy": (None, [vp]),
