@@ -1,6 +1,6 @@
 /*
  * rtl_wire.c - hw_desc_t <-> RTL desc_t / completion_t word images
- * (rtl/desc_pkg.sv:8-26; word layout of verilator/rtl_bridge.cpp:157-188).
+ * (rtl/desc_pkg.sv:8-27; word layout of verilator/rtl_bridge.cpp:114-146).
  */
 #include "rtl_wire.h"
 

@@ -3,9 +3,9 @@
 
 Pinned independently of the C shifts:
 * the word images equal the SystemVerilog packed-struct rule (first declared
-  field in the most significant bits, rtl/desc_pkg.sv:8-26), restated here as
+  field in the most significant bits, rtl/desc_pkg.sv:8-27), restated here as
   an integer concatenation of the fields and cut into 32-bit words, word i =
-  bits [32i + 31 : 32i] (verilator/rtl_bridge.cpp:157-188);
+  bits [32i + 31 : 32i] (verilator/rtl_bridge.cpp:114-146);
 * the completions of the RTL testbench's own three cases
   (rtl/tb_rl_runtime_top.sv:81-147: rollout 7, seq 0, max 10 -> DONE at 10;
   rollout 9, seq 0, max 40 -> REWARD_NEEDED at 32; rollout 11, seq 8, max 12
