@@ -81,13 +81,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
     uint32_t S = 0;
     for (uint32_t bb = b0; bb < b1; bb++)
         S += tiles_of(p, p.ctx[bb]) * p.kv_heads;
-    uint32_t inc = S;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const uint32_t v = __shfl_up(inc, off);
-        if (lane >= off)
-            inc += v;
-    }
+    // tiles of one rollout: its share of S when the thread has one, else reloaded
+    auto tiles_at = [&](uint32_t bb) { return per == 1 ? S : tiles_of(p, p.ctx[bb]) * p.kv_heads; };
+    const uint32_t inc = rl_wave_incl_scan_u32(S);
     if (lane == 63)
         wave_tot[wave] = inc;
     __syncthreads();
@@ -110,7 +106,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
             if (s >= P0 && s < P0 + S) {
                 uint32_t c = P0;
                 for (uint32_t bb = b0; bb < b1; bb++) {
-                    const uint32_t n = tiles_of(p, p.ctx[bb]) * p.kv_heads;
+                    const uint32_t n = tiles_at(bb);
                     if (s < c + n) {
                         start[2 * v] = bb;
                         start[2 * v + 1] = c;
@@ -125,7 +121,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
         uint32_t c = P0;
         for (uint32_t bb = b0; bb < b1; bb++) {
             p.cum[bb] = c;
-            c += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+            c += tiles_at(bb);
         }
         if (threadIdx.x == T - 1)
             p.cum[p.batch] = U;
