@@ -22,7 +22,11 @@
 //          output_token_offset & (io_slots - 1) of the q buffer or the
 //          reference's synthesized query, fp32 softmax(q K^T / sqrt(128)) V to
 //          the o buffer, token = the lowest index of the output's maximum,
-//          cycles = tiles * 128 * 24.
+//          cycles = tiles * 128 * 24. Scores: lane l takes token l % 32 and
+//          half l / 32 of its K row (one 128-byte line, 16-byte loads), the
+//          halves add across the wave, one max and one sum for the softmax;
+//          the output: lane l owns dims 2l and 2l + 1, the weights broadcast
+//          from the token lanes.
 //  publish wave 0 writes the window's completions {seq_id, token_id,
 //          kv_block_offset, reward_cookie, cycles} in descriptor order with
 //          one 16-byte store per lane and release-stores tail + n at system
@@ -130,22 +134,38 @@ __device__ __forceinline__ float synth_query(const Descriptor &d, const SampleSt
     return (float)centered / 127.0f;
 }
 
-// One fixed128 decode step by one wave; lane l owns dims 2l and 2l + 1.
-// Returns the completion record's token and cycle fields.
-__device__ void fixed128_step(const CmdParams &p, const Descriptor &d, int lane, uint32_t &token, uint64_t &cycles)
+__device__ __forceinline__ float wave_max(float v)
+{
+    v = rl_row_max(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48))));
+}
+
+// One fixed128 decode step by one wave (qs: this wave's 128-float LDS slot,
+// vs: its 8 KiB slot for the V plane). Returns the completion record's token
+// and cycle fields.
+__device__ void fixed128_step(const CmdParams &p, const Descriptor &d, RL_LDS float *qs, RL_LDS uint8_t *vs, int lane,
+                              uint32_t &token, uint64_t &cycles)
 {
     const uint32_t seq = d.num_kv_blocks == 0 ? 1u : (d.num_kv_blocks > kTokens ? kTokens : d.num_kv_blocks);
     const uint32_t slot = d.output_token_offset & p.io_mask;
     const bool bad = d.kv_block_offset >= p.arena_blocks;
     const uint8_t *blk = p.arena + (uint64_t)(bad ? 0u : d.kv_block_offset) * kBlockBytes;
+    const uint32_t t = (uint32_t)lane & (kTokens - 1);   // this lane's token
+    const uint32_t h = (uint32_t)lane / kTokens;         // and half of its K row
 
-    // every K and V word of the block, issued before the first use
-    uint32_t kw[kTokens], vw[kTokens];
+    // every load issued before the first use: the V plane straight to LDS
+    // (eight 1 KiB copies), then the lane's K half row (8 x 16 B)
+    const uint8_t *vp = blk + kTokens * kRowBytes;
 #pragma unroll
-    for (uint32_t t = 0; t < kTokens; t++) {
-        kw[t] = *(const RL_GLOBAL uint32_t *)(blk + t * kRowBytes + lane * 4u);
-        vw[t] = *(const RL_GLOBAL uint32_t *)(blk + kTokens * kRowBytes + t * kRowBytes + lane * 4u);
-    }
+    for (int i = 0; i < 8; i++)
+        rl_g2lds_16_off(vp, (uint32_t)(i * 1024 + lane * 16), vs + i * 1024);
+    rl_u32x4 kq[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        kq[i] = *(const RL_GLOBAL rl_u32x4 *)(blk + t * kRowBytes + h * (kRowBytes / 2) + i * 16);
     float q0, q1;
     if (p.q) {
         const uint32_t qw = *(const RL_GLOBAL uint32_t *)(p.q + (size_t)slot * kD + 2u * lane);
@@ -154,26 +174,48 @@ __device__ void fixed128_step(const CmdParams &p, const Descriptor &d, int lane,
         q0 = synth_query(d, p.sample_state, 2u * lane);
         q1 = synth_query(d, p.sample_state, 2u * lane + 1u);
     }
-    const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
-    float s[kTokens];
-    float m = -INFINITY;
+    qs[2 * lane] = q0;
+    qs[2 * lane + 1] = q1;
+    rl_wave_lds_fence();
+
+    // q . k_t over this half, then the other half's partial
+    float dot = 0.f;
 #pragma unroll
-    for (uint32_t t = 0; t < kTokens; t++) {
-        float k0, k1;
-        rl_unpack2<1>(kw[t], k0, k1);
-        const float dot = wave_sum(fmaf(q1, k1, q0 * k0)) * scale;
-        s[t] = t < seq ? dot : -INFINITY;
-        m = fmaxf(m, s[t]);
+    for (int i = 0; i < 8; i++) {
+        const rl_f32x4 qa = *(RL_LDS const rl_f32x4 *)(qs + h * 64 + 8 * i);
+        const rl_f32x4 qb = *(RL_LDS const rl_f32x4 *)(qs + h * 64 + 8 * i + 4);
+        float k0, k1, k2, k3, k4, k5, k6, k7;
+        rl_unpack2<1>(kq[i].x, k0, k1);
+        rl_unpack2<1>(kq[i].y, k2, k3);
+        rl_unpack2<1>(kq[i].z, k4, k5);
+        rl_unpack2<1>(kq[i].w, k6, k7);
+        dot = fmaf(qa.x, k0, dot);
+        dot = fmaf(qa.y, k1, dot);
+        dot = fmaf(qa.z, k2, dot);
+        dot = fmaf(qa.w, k3, dot);
+        dot = fmaf(qb.x, k4, dot);
+        dot = fmaf(qb.y, k5, dot);
+        dot = fmaf(qb.z, k6, dot);
+        dot = fmaf(qb.w, k7, dot);
+        // two query reads in flight at a time: hoisting all sixteen costs
+        // 64 VGPRs, which the 16-wave workgroup does not have
+        __builtin_amdgcn_sched_barrier(0);
     }
-    float o0 = 0.f, o1 = 0.f, l = 0.f;
+    dot += __shfl_xor(dot, 32);
+    const float scale = 0.08838834764831845f;  // 1 / sqrt(128)
+    const float sc = t < seq ? dot * scale : -INFINITY;
+    const float m = wave_max(sc);
+    const float e = (h == 0 && t < seq) ? __expf(sc - m) : 0.f;
+    const float l = wave_sum(e);
+    rl_wait_vmcnt<0>();  // the V copies have landed (issued first, they retire first)
+    float o0 = 0.f, o1 = 0.f;
 #pragma unroll
-    for (uint32_t t = 0; t < kTokens; t++) {
-        const float e = t < seq ? __expf(s[t] - m) : 0.f;
+    for (uint32_t tt = 0; tt < kTokens; tt++) {
+        const float et = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), (int)tt));
         float v0, v1;
-        rl_unpack2<1>(vw[t], v0, v1);
-        l += e;
-        o0 = fmaf(e, v0, o0);
-        o1 = fmaf(e, v1, o1);
+        rl_unpack2<1>(*(RL_LDS const uint32_t *)(vs + tt * kRowBytes + lane * 4u), v0, v1);
+        o0 = fmaf(et, v0, o0);
+        o1 = fmaf(et, v1, o1);
     }
     o0 /= l;
     o1 /= l;
@@ -206,6 +248,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
 {
     __shared__ __attribute__((aligned(16))) Descriptor s_desc[kWindow];
     __shared__ __attribute__((aligned(16))) Completion s_comp[kWindow];
+    __shared__ __attribute__((aligned(16))) float s_q[kWaves][kD];  // each wave's query
+    __shared__ __attribute__((aligned(1024))) uint8_t s_v[kWaves][kTokens * kRowBytes];  // each wave's V plane
     __shared__ uint32_t s_ctl[2];  // descriptors to run, exit flag
 
     const uint32_t tid = threadIdx.x;
@@ -292,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
             const Descriptor d = s_desc[i];
             uint32_t token;
             uint64_t cycles;
-            fixed128_step(p, d, lane, token, cycles);
+            fixed128_step(p, d, (RL_LDS float *)s_q[wave], (RL_LDS uint8_t *)s_v[wave], lane, token, cycles);
             if (lane == 0) {
                 Completion c;
                 c.seq_id = d.seq_id;
