@@ -13,7 +13,9 @@
 //          (the stop flag only while the ring is empty); after the acquire the
 //          whole window of descriptors already committed - up to 32, the
 //          decode_batch window (src/decode_batch.c:3-51) - is read with one
-//          16-byte load per lane, and the head is released once.
+//          16-byte load per lane, and the head is released once. The tail
+//          and the completion ring's head are read again while each window
+//          decodes, so the next poll and the room check rarely wait.
 //  decode  wave w takes descriptors w, w + 16, ... of the window: the fixed128
 //          step of the reference (cu/attention_decode.cu:60-204) - one head,
 //          d128, fp16 K/V of arena block kv_block_offset (K plane, V plane at
@@ -261,9 +263,16 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
     uint64_t descs = 0, completions = 0, windows = 0;
     uint32_t status = kStatusStopped;
     uint32_t head = 0, ctail = 0;  // lane 0 of wave 0: this worker owns cons.head and the completion tail
+    // lane 0 of wave 0: the producer's tail and the host's completion head as
+    // last read; both are read again while the window decodes, so the next
+    // poll and the room check usually find their answer already there (an
+    // older value only means fewer descriptors or less room, then re-read)
+    uint32_t tail_seen = 0, chead_seen = 0;
     if (tid == 0) {
         head = sys_load(&ring->cons.head);
         ctail = sys_load(&cr->prod.tail);
+        tail_seen = head;
+        chead_seen = sys_load(&cr->cons.head);
     }
     TraceRing *tr = p.trace ? p.trace + blockIdx.x : nullptr;
     uint64_t thead = 0;            // wave 0, uniform: the trace ring's head
@@ -276,7 +285,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
             uint32_t avail = 0, ctl = 0;
             if (lane == 0) {
                 uint64_t idle = 0;
-                for (;;) {
+                avail = tail_seen - head;
+                for (; avail == 0;) {
                     avail = sys_load(&ring->prod.tail) - head;
                     if (avail != 0)
                         break;
@@ -331,6 +341,11 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
         const uint32_t n = s_ctl[0];
         const uint32_t stop_now = s_ctl[1];
 
+        if (tid == 0 && n && !stop_now) {
+            tail_seen = sys_load(&ring->prod.tail);
+            chead_seen = sys_load(&cr->cons.head);
+        }
+
         // ---- decode: one descriptor per wave at a time ---------------------------
         for (uint32_t i = wave; i < n; i += kWaves) {
             const Descriptor d = s_desc[i];
@@ -356,7 +371,12 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
             if (lane == 0) {
                 uint64_t idle = 0;
                 for (;;) {
-                    if (ctail - sys_load(&cr->cons.head) <= (uint32_t)COMP_RING_SIZE - n) {
+                    if (ctail - chead_seen <= (uint32_t)COMP_RING_SIZE - n) {
+                        room = 1;
+                        break;
+                    }
+                    chead_seen = sys_load(&cr->cons.head);
+                    if (ctail - chead_seen <= (uint32_t)COMP_RING_SIZE - n) {
                         room = 1;
                         break;
                     }
