@@ -11,19 +11,28 @@
 //         candidates: every element >= a lower bound of the slice's k-th
 //         largest value. The bound is the minimum over the four waves of each
 //         wave's ceil(k/4)-th largest lane maximum (found with a 32-step ballot
-//         radix select), so at least k distinct elements lie above it.
+//         radix select), so at least k distinct elements lie above it. The
+//         kernel is VALU-bound once its loads land, so the per-element work is
+//         kept small: masking only in a row's last slice, one float compare as
+//         the candidate test, two barriers. Slice 0 of each row also computes
+//         the row's Philox draw while its loads are in flight.
 //  merge  grid (row): one 512-thread workgroup (8 waves) merges the slices:
-//         global max and log-sum-exp; the candidates gathered into LDS, one
-//         wave per slice list, keeping only keys at or above the largest
-//         slice bound (every slice's bound is below the row's k-th largest
-//         key); the exact k-th largest among them (MSB-first 8-bit radix
-//         select on LDS histograms from the highest bit where the candidate
-//         keys differ, each wave finding the digit with DPP scans); rank sort
-//         of the kept set by (x desc, index asc); 24-bit integer weights
-//         rl_sample_weight(x - max), nucleus prefix, Philox4x32-10 draw and
-//         the ascending-index integer CDF walk - in one wave when at most 64
-//         elements are kept. Rows without top-k (a whole-vocabulary nucleus)
-//         or whose candidates overflow take the exact full-row path below.
+//         the global max (the log-sum-exp only at the end, for the logprob);
+//         the candidates gathered into LDS - wave w takes the lists of slices
+//         w and w + 8, their first 256 entries loaded at kernel entry with the
+//         slice records, one LDS atomic per wave for eight groups of 64 -
+//         keeping only keys at or above the largest slice bound (every slice's
+//         bound is below the row's k-th largest key); the exact k-th largest
+//         among them by an MSB-first 8-bit radix select on LDS histograms from
+//         the highest bit where the candidate keys differ (the first
+//         histogram filled during the gather, each wave finding the digit
+//         with DPP scans), finished by one wave's ballot select once the
+//         chosen bin holds at most 64 keys; rank sort of the kept set by
+//         (x desc, index asc); 24-bit integer weights rl_sample_weight(x -
+//         max), nucleus prefix and the ascending-index integer CDF walk - in
+//         one wave when at most 64 elements are kept. Rows without top-k (a
+//         whole-vocabulary nucleus) or whose candidates overflow take the
+//         exact full-row path below.
 // Integer weights make every sum exact, so the token is bit-identical to the
 // host restatement whatever the reduction order.
 #include <hip/hip_runtime.h>
