@@ -9,24 +9,31 @@
 //          records the token sampled for it and counts it;
 //  retire  slots with tokens_generated >= max_tokens get their reward - the
 //          reference rule (count & 0xFF) / 255 applied to the number of
-//          generated tokens equal to the group's target at the same position
-//          - and write their RolloutDone records in parallel, slot s at
-//          done-ring position tail + (retiring slots below s), so the ring
-//          holds them in slot order; after a barrier thread 0 publishes the
-//          new tail with one system-scope release (coherent host memory) and
-//          the slots are freed;
+//          generated tokens equal to the group's target at the same position,
+//          counted by whole waves four slots at a time - and write their
+//          RolloutDone records in parallel, slot s at done-ring position tail
+//          + (retiring slots below s), so the ring holds them in slot order;
+//          after a barrier thread 0 publishes the new tail (coherent host
+//          memory) and the slots are freed;
 //  admit   the free slots (after retirement) are ranked in slot order;
 //          threads read up to that many requests from the ring in parallel,
-//          thread 0 stops at the end marker (request_id UINT64_MAX) or a bad
-//          id and publishes the new head, and the i-th request goes to the
-//          i-th free slot - the lowest free slot first, as in the reference,
-//          whose seeding of the slot fields is kept. Unlike the reference, a
-//          request is never consumed without a free slot, so none is dropped;
+//          the first end marker (request_id UINT64_MAX) or bad id stops the
+//          admission (a ballot finds it), thread 0 publishes the new head, and
+//          the i-th request goes to the i-th free slot - the lowest free slot
+//          first, as in the reference, whose seeding of the slot fields is
+//          kept. Unlike the reference, a request is never consumed without a
+//          free slot, so none is dropped;
 //  prepare every slot writes the next step's arguments: attention context and
 //          append position (prompt tokens + generated tokens), sampler
 //          temperature / top-k / top-p / seed / step (temperature 0 for an
-//          idle slot: the cheap greedy path), and an admitted slot copies its
-//          request's block-table rows.
+//          idle slot: the cheap greedy path), and the admitted slots' rows of
+//          the block table are copied from their requests' rows.
+// Latency is the whole cost of this kernel, so every device input is loaded
+// up front in one batch, the four host-ring indexes a launch needs are read
+// together while the rewards are counted, host records are read and written
+// with relaxed system-scope accesses that stay in flight together (one fence
+// orders them), and work lists are compact: a launch that retires and admits
+// nothing touches no host memory and loops over nothing.
 // Waits on the done ring are bounded by max_spin polls (status 3).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -48,12 +55,19 @@ __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
     return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ void sys_store_release(volatile uint32_t *p, uint32_t v)
+__device__ __forceinline__ uint16_t sys_load16(const volatile uint16_t *p)
 {
-    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load((uint16_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ void sys_store(volatile uint32_t *p, uint32_t v)
+{
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // A packed 34-byte request (2-byte aligned in the ring) read as 17 halves.
+// Relaxed system-scope loads are all in flight together; volatile loads would
+// each wait for the one before, one PCIe round trip apiece.
 __device__ RolloutRequest read_request(const RolloutRequest *src)
 {
     union {
@@ -63,157 +77,230 @@ __device__ RolloutRequest read_request(const RolloutRequest *src)
     const volatile uint16_t *s = (const volatile uint16_t *)src;
 #pragma unroll
     for (int i = 0; i < 17; i++)
-        u.h[i] = s[i];
+        u.h[i] = sys_load16(s + i);
     return u.r;
 }
 
-// Exclusive prefix of v over the workgroup in thread order; total in `total`.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t &total, uint32_t *s_w)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t incl = rl_wave_incl_scan_u32(v);
-    if (lane == 63)
-        s_w[wave] = incl;
-    __syncthreads();
-    uint32_t base = 0, t = 0;
-#pragma unroll
-    for (int w = 0; w < kSlots / 64; w++) {
-        base += w < wave ? s_w[w] : 0u;
-        t += s_w[w];
-    }
-    __syncthreads();
-    total = t;
-    return base + incl - v;
-}
+constexpr int kWaves = kSlots / 64;
+constexpr int kRewardSlots = 4;   // retiring slots a wave counts per round
+constexpr int kCopyDepth = 16;    // block-table entries per thread and round
 
 __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sched_args_t p)
 {
-    __shared__ uint32_t s_w[kSlots / 64];
+    __shared__ uint32_t s_w[kWaves];
+    __shared__ uint32_t s_stop[kWaves];
     __shared__ uint32_t s_ctl[4];
-    __shared__ uint32_t s_admit[kSlots];           // request index admitted into the slot this launch, or ~0
-    __shared__ RolloutRequest s_req[kSlots];       // requests read from the ring this launch, in ring order
+    __shared__ uint32_t s_rslot[kSlots];     // retiring slots in slot order
+    __shared__ uint32_t s_rreq[kSlots];      // ... their request ids
+    __shared__ uint32_t s_rlen[kSlots];      // ... the number of generated tokens the reward compares
+    __shared__ float s_reward[kSlots];       // ... their rewards
+    __shared__ uint32_t s_aslot[kSlots];     // admitted slots in admission order
+    __shared__ RolloutRequest s_req[kSlots]; // requests read from the ring this launch, in ring order
     const uint32_t s = threadIdx.x;
     const int lane = s & 63, wave = s >> 6;
     GpuRolloutSlot *slot = &p.state->slots[s];
     const uint32_t row_entries = p.kv_heads * p.table_stride;
-    const uint32_t status0 = p.counters[3];
+    DoneRing *dr = p.done_ring;
+    RequestRing *rr = p.req_ring;
+
+    // ---- every device-side input of the launch, loaded together -------------
+    const uint32_t cnt_done = p.counters[0], cnt_adm = p.counters[1];
+    const uint32_t ended = p.counters[2], status0 = p.counters[3];
+    const uint64_t bits = p.state->bitmap[wave];
+    const uint32_t active = slot->active;
+    const uint32_t req0 = slot->request_id;
+    uint32_t t = slot->tokens_generated;
+    const uint32_t max_tok = slot->max_tokens;
+    const uint64_t seed0 = slot->rng_state[0];
+    const float temp0 = slot->temperature;
+    const uint32_t topk0 = slot->top_k;
+    const float topp0 = slot->top_p;
+    const uint32_t pos = p.slot_pos[s];
+    const uint32_t tok = p.sampled ? p.sampled[s] : 0u;
+    const uint32_t plen0 = p.prompt_len[min(req0, p.requests - 1)];
 
     // ---- commit the last step's token ------------------------------------
-    uint32_t active = slot->active;
-    if (p.sampled && active && p.slot_pos[s] != 0xFFFFFFFFu) {
-        const uint32_t req = slot->request_id;
-        const uint32_t t = slot->tokens_generated;
-        if (req < p.requests && t < p.gen_stride)
-            p.gen_tokens[(size_t)req * p.gen_stride + t] = p.sampled[s];
-        slot->tokens_generated = t + 1;
+    if (p.sampled && active && pos != 0xFFFFFFFFu) {
+        if (req0 < p.requests && t < p.gen_stride)
+            p.gen_tokens[(size_t)req0 * p.gen_stride + t] = tok;
+        t += 1;
+        slot->tokens_generated = t;
     }
 
-    // ---- retire: reward, then the dones in slot order -------------------------
-    const bool retire = status0 == kOk && active && slot->tokens_generated >= slot->max_tokens;
-    float reward = 0.f;
-    if (retire) {
-        const uint32_t req = slot->request_id;
-        uint32_t count = 0;
-        if (req < p.requests) {
-            const uint32_t *tok = p.gen_tokens + (size_t)req * p.gen_stride;
-            const uint32_t *tgt = p.targets + (size_t)(req / p.group_size) * p.target_len;
-            const uint32_t n = min(min(slot->tokens_generated, p.gen_stride), p.target_len);
-            for (uint32_t i = 0; i < n; i++)
-                count += tok[i] == tgt[i] ? 1u : 0u;
-        }
-        reward = (float)(count & 0xFFu) / 255.0f;
+    // ---- rank the retiring slots and the slots free after retirement -----------
+    // (one scan: retiring count in the low half, free count in the high half)
+    const bool retire = status0 == kOk && active && t >= max_tok;
+    const bool maybe_free = status0 == kOk && ended == 0 && (((bits >> lane) & 1ull) == 0 || retire);
+    const uint32_t v = (retire ? 1u : 0u) | (maybe_free ? 0x10000u : 0u);
+    const uint32_t incl = rl_wave_incl_scan_u32(v);
+    if (lane == 63)
+        s_w[wave] = incl;
+    __syncthreads();
+    uint32_t ex = incl - v, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++) {
+        ex += w < wave ? s_w[w] : 0u;
+        tot += s_w[w];
     }
-    uint32_t n_ret;
-    const uint32_t rank = block_excl_scan(retire ? 1u : 0u, n_ret, s_w);
-    DoneRing *dr = p.done_ring;
+    const uint32_t rank = ex & 0xFFFFu, frank = ex >> 16;
+    const uint32_t n_ret = tot & 0xFFFFu, n_free = tot >> 16;
+    if (retire) {
+        s_rslot[rank] = s;
+        s_rreq[rank] = req0;
+        s_rlen[rank] = req0 < p.requests ? min(min(t, p.gen_stride), p.target_len) : 0u;
+    }
+    // the host-ring indexes this launch needs, in flight while the rewards are counted
+    uint32_t dtail = 0, dhead = 0, rhead = 0, rtail = 0;
     if (s == 0) {
-        uint32_t status = status0;
-        const uint32_t dtail = n_ret ? sys_load(&dr->prod.tail) : 0u;
-        uint64_t spin = 0;
-        while (n_ret && status == kOk && dtail - sys_load(&dr->cons.head) > (uint32_t)REQUEST_RING_SIZE - n_ret) {
-            if (++spin > p.max_spin)
-                status = kDoneFull;
-            else
-                __builtin_amdgcn_s_sleep(8);
+        if (n_ret) {
+            dtail = sys_load(&dr->prod.tail);
+            dhead = sys_load(&dr->cons.head);
         }
-        s_ctl[0] = dtail;
-        s_ctl[1] = status;
+        if (n_free) {
+            rhead = sys_load(&rr->cons.head);
+            rtail = sys_load(&rr->prod.tail);
+        }
     }
     __syncthreads();
-    const uint32_t dtail = s_ctl[0];
-    const bool pushed = retire && s_ctl[1] == kOk;
+
+    // ---- rewards: (count & 0xFF) / 255 over the generated tokens equal to the
+    // group's target; wave w counts retiring slots 4w .. 4w + 3, 4w + 16 .., 256
+    // tokens of four slots per round with all their loads in flight ------------
+    for (uint32_t j0 = (uint32_t)wave * kRewardSlots; j0 < n_ret; j0 += kWaves * kRewardSlots) {
+        const uint32_t *ga[kRewardSlots], *ta[kRewardSlots];
+        uint32_t n[kRewardSlots], cnt[kRewardSlots], nmax = 0;
+#pragma unroll
+        for (int g = 0; g < kRewardSlots; g++) {
+            const uint32_t j = j0 + g;
+            n[g] = j < n_ret ? s_rlen[j] : 0u;
+            const uint32_t rq = j < n_ret ? s_rreq[j] : 0u;
+            // a slot with nothing to compare reads element 0 of gen_tokens, masked out
+            ga[g] = n[g] ? p.gen_tokens + (size_t)rq * p.gen_stride : p.gen_tokens;
+            ta[g] = n[g] ? p.targets + (size_t)(rq / p.group_size) * p.target_len : p.gen_tokens;
+            cnt[g] = 0;
+            nmax = max(nmax, n[g]);
+        }
+        for (uint32_t c0 = 0; c0 < nmax; c0 += 256) {
+            uint32_t a[kRewardSlots][4], b[kRewardSlots][4];
+#pragma unroll
+            for (int g = 0; g < kRewardSlots; g++)
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const uint32_t i = c0 + (uint32_t)u * 64 + (uint32_t)lane;
+                    const uint32_t k = i < n[g] ? i : 0u;
+                    a[g][u] = ga[g][k];
+                    b[g][u] = ta[g][k];
+                }
+#pragma unroll
+            for (int g = 0; g < kRewardSlots; g++)
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    cnt[g] += (c0 + (uint32_t)u * 64 + (uint32_t)lane < n[g] && a[g][u] == b[g][u]) ? 1u : 0u;
+        }
+#pragma unroll
+        for (int g = 0; g < kRewardSlots; g++) {
+            const uint32_t c = rl_wave_sum_u32(cnt[g]);
+            if (lane == 0 && j0 + g < n_ret)
+                s_reward[j0 + g] = (float)(c & 0xFFu) / 255.0f;
+        }
+    }
+
+    // ---- room on the done ring (bounded wait), requests available ------------
+    if (s == 0) {
+        uint32_t st = status0;
+        if (n_ret) {
+            uint64_t spin = 0;
+            while (dtail - dhead > (uint32_t)REQUEST_RING_SIZE - n_ret) {
+                if (++spin > p.max_spin) {
+                    st = kDoneFull;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+                dhead = sys_load(&dr->cons.head);
+            }
+        }
+        uint32_t n_try = 0;
+        if (n_free && st == kOk) {
+            n_try = min(n_free, rtail - rhead);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        }
+        s_ctl[0] = dtail;
+        s_ctl[1] = st;
+        s_ctl[2] = rhead;
+        s_ctl[3] = n_try;
+    }
+    __syncthreads();
+    const uint32_t st = s_ctl[1], n_try = s_ctl[3];
+
+    // ---- retire: RolloutDone records in slot order; read the requests ----------
+    const bool pushed = retire && st == kOk;
     if (pushed) {
-        volatile uint32_t *dst = (volatile uint32_t *)&dr->slots[(dtail + rank) & (REQUEST_RING_SIZE - 1)];
-        const uint32_t req = slot->request_id;
-        dst[0] = req;  // request_id (the slot keeps its low 32 bits, as in the reference)
-        dst[1] = 0;
-        dst[2] = s;    // rollout_id = slot
-        dst[3] = slot->tokens_generated;
-        dst[4] = __float_as_uint(reward);
-        dst[5] = 0;    // status
+        const uint32_t req = req0;
+        const float reward = s_reward[rank];
+        volatile uint32_t *dst = (volatile uint32_t *)&dr->slots[(s_ctl[0] + rank) & (REQUEST_RING_SIZE - 1)];
+        sys_store(dst + 0, req);  // request_id (the slot keeps its low 32 bits, as in the reference)
+        sys_store(dst + 1, 0);
+        sys_store(dst + 2, s);    // rollout_id = slot
+        sys_store(dst + 3, t);
+        sys_store(dst + 4, __float_as_uint(reward));
+        sys_store(dst + 5, 0);    // status
+        // this wave's records are complete before the barrier, ahead of the tail
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
         if (req < p.requests)
             p.rewards[req] = reward;
         slot->active = 0;
     }
-    const uint64_t freed = __ballot(pushed);  // wave w owns bitmap word w
-    if (lane == 0 && freed)
-        p.state->bitmap[wave] &= ~freed;
-    __syncthreads();  // every record is written before the tail moves
-    if (s == 0 && s_ctl[1] == kOk && n_ret) {
-        sys_store_release(&dr->prod.tail, dtail + n_ret);
-        p.counters[0] += n_ret;
+    // requests in ring order; the first end marker or bad id stops the admission
+    bool stop = false, bad = false;
+    if (s < n_try) {
+        const RolloutRequest q = read_request(&rr->slots[(s_ctl[2] + s) & (REQUEST_RING_SIZE - 1)]);
+        s_req[s] = q;
+        stop = q.request_id == ~0ull || (uint32_t)(q.request_id & 0xFFFFFFFFu) >= p.requests;
+        bad = stop && q.request_id != ~0ull;
     }
+    const uint64_t sb = __ballot(stop), bb = __ballot(bad);
+    if (lane == 0) {
+        const uint32_t f = (uint32_t)__builtin_ctzll(sb | (1ull << 63));
+        s_stop[wave] = sb ? (((uint32_t)wave * 64 + f) << 1) | (uint32_t)((bb >> f) & 1ull) : 0xFFFFFFFFu;
+    }
+    __syncthreads();
 
-    // ---- admit: requests in ring order into the free slots in slot order ------
-    const bool is_free = s_ctl[1] == kOk && p.counters[2] == 0 &&
-                         ((p.state->bitmap[wave] >> lane) & 1ull) == 0;
-    uint32_t n_free;
-    const uint32_t frank = block_excl_scan(is_free ? 1u : 0u, n_free, s_w);
-    RequestRing *rr = p.req_ring;
+    // ---- publish, admit: the i-th request into the i-th free slot ---------------
+    uint32_t key = 0xFFFFFFFFu;
+#pragma unroll
+    for (int w = 0; w < kWaves; w++)
+        key = min(key, s_stop[w]);
+    const uint32_t n_adm = key == 0xFFFFFFFFu ? n_try : key >> 1;
+    const uint32_t used = key == 0xFFFFFFFFu ? n_try : (key >> 1) + 1;
     if (s == 0) {
-        uint32_t head = 0, n_try = 0;
-        if (n_free) {
-            head = sys_load(&rr->cons.head);
-            n_try = min(n_free, sys_load(&rr->prod.tail) - head);
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        const bool publish = st == kOk && n_ret;
+        if (publish || used) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+            if (publish)
+                sys_store(&dr->prod.tail, s_ctl[0] + n_ret);
+            if (used)
+                sys_store(&rr->cons.head, s_ctl[2] + used);
         }
-        s_ctl[2] = head;
-        s_ctl[3] = n_try;
+        if (publish)
+            p.counters[0] = cnt_done + n_ret;
+        p.counters[1] = cnt_adm + n_adm;
+        if (key != 0xFFFFFFFFu && !(key & 1u))
+            p.counters[2] = 1;
+        p.counters[3] = key != 0xFFFFFFFFu && (key & 1u) ? (uint32_t)kBadRequest : st;
     }
-    __syncthreads();
-    const uint32_t head = s_ctl[2], n_try = s_ctl[3];
-    if (s < n_try)
-        s_req[s] = read_request(&rr->slots[(head + s) & (REQUEST_RING_SIZE - 1)]);
-    __syncthreads();
-    if (s == 0) {
-        uint32_t status = s_ctl[1], n_adm = 0, used = 0;
-        for (; used < n_try; used++) {
-            const RolloutRequest &q = s_req[used];
-            if (q.request_id == ~0ull) {
-                p.counters[2] = 1;
-                used++;
-                break;
-            }
-            if ((uint32_t)(q.request_id & 0xFFFFFFFFu) >= p.requests) {
-                status = kBadRequest;
-                used++;
-                break;
-            }
-            n_adm++;
-        }
-        if (used)
-            sys_store_release(&rr->cons.head, head + used);
-        p.counters[1] += n_adm;
-        p.counters[3] = status;
-        s_ctl[3] = n_adm;
-    }
-    __syncthreads();
-    const uint32_t n_adm = s_ctl[3];
-    const bool admit = is_free && frank < n_adm;
-    s_admit[s] = 0xFFFFFFFFu;
+    const bool admit = maybe_free && frank < n_adm;
+    uint32_t rid = req0, tg = t;
+    float temp = temp0, topp = topp0;
+    uint32_t topk = topk0;
+    uint64_t seed = seed0;
     if (admit) {
         const RolloutRequest &q = s_req[frank];
-        const uint32_t rid = (uint32_t)(q.request_id & 0xFFFFFFFFu);
+        rid = (uint32_t)(q.request_id & 0xFFFFFFFFu);
+        tg = 0;
+        temp = q.temperature;
+        topk = q.top_k;
+        topp = q.top_p;
+        seed = q.rng_seed;
         slot->active = 1;
         slot->request_id = rid;
         slot->tokens_generated = 0;
@@ -226,36 +313,46 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
         slot->temperature = q.temperature;
         slot->top_k = q.top_k;
         slot->top_p = q.top_p;
-        s_admit[s] = rid;
+        s_aslot[frank] = s;
     }
-    const uint64_t taken = __ballot(admit);
-    if (lane == 0 && taken)
-        p.state->bitmap[wave] |= taken;
-    __syncthreads();
+    const uint64_t freed = __ballot(pushed), taken = __ballot(admit);
+    if (lane == 0 && (freed | taken))
+        p.state->bitmap[wave] = (bits & ~freed) | taken;
 
     // ---- block-table rows of the slots admitted now ---------------------------
-    for (uint32_t i = 0; i < (uint32_t)kSlots; i++) {
-        const uint32_t rid = s_admit[i];
-        if (rid == 0xFFFFFFFFu)
-            continue;
-        const uint32_t *src = p.req_table + (size_t)rid * row_entries;
-        uint32_t *dst = p.slot_table + (size_t)i * row_entries;
-        for (uint32_t e = s; e < row_entries; e += kSlots)
-            dst[e] = src[e];
+    if (n_adm) {
+        __syncthreads();
+        const uint32_t total = n_adm * row_entries;
+        for (uint32_t e0 = s; e0 < total; e0 += kSlots * kCopyDepth) {
+            uint32_t val[kCopyDepth];
+#pragma unroll
+            for (int u = 0; u < kCopyDepth; u++) {
+                const uint32_t e = min(e0 + (uint32_t)u * kSlots, total - 1);
+                const uint32_t i = e / row_entries;
+                const uint32_t r = (uint32_t)(s_req[i].request_id & 0xFFFFFFFFu);
+                val[u] = p.req_table[(size_t)r * row_entries + (e - i * row_entries)];
+            }
+#pragma unroll
+            for (int u = 0; u < kCopyDepth; u++) {
+                const uint32_t e = e0 + (uint32_t)u * kSlots;
+                if (e < total) {
+                    const uint32_t i = e / row_entries;
+                    p.slot_table[(size_t)s_aslot[i] * row_entries + (e - i * row_entries)] = val[u];
+                }
+            }
+        }
     }
 
     // ---- the next step's arguments ------------------------------------------------
-    active = slot->active;
-    if (active) {
-        const uint32_t rid = slot->request_id;
-        const uint32_t ctx = p.prompt_len[rid] + slot->tokens_generated;
+    if (admit || (active && !pushed)) {
+        const uint32_t ctx = (admit ? p.prompt_len[rid] : plen0) + tg;
         p.slot_ctx[s] = ctx;
         p.slot_pos[s] = ctx;
-        p.slot_temp[s] = slot->temperature;
-        p.slot_topk[s] = slot->top_k;
-        p.slot_topp[s] = slot->top_p;
-        p.slot_seed[s] = slot->rng_state[0];
-        p.slot_step[s] = slot->tokens_generated;
+        p.slot_temp[s] = temp;
+        p.slot_topk[s] = topk;
+        p.slot_topp[s] = topp;
+        p.slot_seed[s] = seed;
+        p.slot_step[s] = tg;
     } else {
         p.slot_ctx[s] = 0;
         p.slot_pos[s] = 0xFFFFFFFFu;
@@ -277,6 +374,11 @@ extern "C" int rl_hip_rollout_schedule(const rl_rollout_sched_args_t *a)
         !a->targets || !a->rewards || !a->slot_table || !a->slot_ctx || !a->slot_pos || !a->slot_temp ||
         !a->slot_topk || !a->slot_topp || !a->slot_seed || !a->slot_step || !a->counters) {
         rl_set_error("rl_hip_rollout_schedule: NULL argument");
+        return -1;
+    }
+    if ((uint64_t)a->kv_heads * a->table_stride >= (1ull << 24)) {
+        rl_set_error("rl_hip_rollout_schedule: kv_heads %u x table_stride %u block-table entries per slot "
+                     "(at most 2^24 - 1)", a->kv_heads, a->table_stride);
         return -1;
     }
     if (a->requests == 0 || a->group_size == 0 || a->kv_heads == 0 || a->table_stride == 0 || a->gen_stride == 0) {
