@@ -57,6 +57,18 @@ constexpr int stages_of()
     return 2;
 }
 
+// Workgroup b runs on XCD b % 8, each XCD behind its own L2. The logical
+// index gives XCD x a contiguous eighth of the tile sequence, so rows that
+// read the same KV blocks (the rollouts of a group over a shared prefix, which
+// sit next to each other in the sequence) stream them through one L2.
+__device__ __forceinline__ uint32_t xcd_contiguous_wg()
+{
+    const uint32_t n = gridDim.x;
+    if (n % 8 != 0)
+        return blockIdx.x;
+    return (blockIdx.x % 8) * (n / 8) + blockIdx.x / 8;
+}
+
 template <int D, int G, int DT, int TPB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
 {
@@ -69,6 +81,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t wg = xcd_contiguous_wg();
 
     // ---- plan: tile prefix over rollouts, each wave's starting rollout -------
     // (q slot memory doubles as scratch until the copies start)
@@ -100,7 +113,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
     const uint32_t NW = min(p.nwaves, U);
 #pragma unroll
     for (int v = 0; v < W; v++) {
-        const uint32_t w = blockIdx.x * W + v;
+        const uint32_t w = wg * W + v;
         if (w < NW && S > 0) {
             const uint32_t s = (uint32_t)(((uint64_t)w * U) / NW);
             if (s >= P0 && s < P0 + S) {
@@ -127,7 +140,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
             p.cum[p.batch] = U;
     }
     __syncthreads();
-    const uint32_t wave_id = blockIdx.x * W + wave;
+    const uint32_t wave_id = wg * W + wave;
     const bool active = wave_id < NW;
     const uint32_t s_begin = active ? (uint32_t)(((uint64_t)wave_id * U) / NW) : 0u;
     const uint32_t s_end = active ? (uint32_t)(((uint64_t)(wave_id + 1) * U) / NW) : 0u;
