@@ -189,7 +189,9 @@ int rl_hip_reward_advantage(const rl_reward_args_t *args);
  * memory (req_ring_create / done_ring_create after rl_hip_open).
  * counters: [0] dones pushed, [1] requests admitted, [2] end marker seen,
  * [3] status (0 ok, 2 request id >= requests, 3 done ring full for max_spin
- * polls; sticky). */
+ * polls; sticky). The launch fails (-1, error set) on a NULL pointer, a zero
+ * requests / group_size / kv_heads / table_stride / gen_stride, or kv_heads x
+ * table_stride >= 2^24 block-table entries per slot. */
 typedef struct {
     RequestRing *req_ring;
     DoneRing *done_ring;
