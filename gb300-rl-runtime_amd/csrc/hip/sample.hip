@@ -941,7 +941,7 @@ __device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint
     return tok;
 }
 
-// One workgroup of 256 threads per row.
+// One workgroup of kMergeThreads threads per row.
 __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParams p)
 {
     const uint32_t row = blockIdx.x;
