@@ -83,7 +83,7 @@ __device__ RolloutRequest read_request(const RolloutRequest *src)
 
 constexpr int kWaves = kSlots / 64;
 constexpr int kRewardSlots = 4;   // retiring slots a wave counts per round
-constexpr int kCopyDepth = 16;    // block-table entries per thread and round
+constexpr int kCopyDepth = 32;    // block-table entries per thread and round
 
 __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sched_args_t p)
 {
@@ -95,6 +95,7 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
     __shared__ uint32_t s_rlen[kSlots];      // ... the number of generated tokens the reward compares
     __shared__ float s_reward[kSlots];       // ... their rewards
     __shared__ uint32_t s_aslot[kSlots];     // admitted slots in admission order
+    __shared__ uint32_t s_arid[kSlots];      // request ids read this launch, in ring order
     __shared__ RolloutRequest s_req[kSlots]; // requests read from the ring this launch, in ring order
     const uint32_t s = threadIdx.x;
     const int lane = s & 63, wave = s >> 6;
@@ -255,6 +256,7 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
     if (s < n_try) {
         const RolloutRequest q = read_request(&rr->slots[(s_ctl[2] + s) & (REQUEST_RING_SIZE - 1)]);
         s_req[s] = q;
+        s_arid[s] = (uint32_t)(q.request_id & 0xFFFFFFFFu);
         stop = q.request_id == ~0ull || (uint32_t)(q.request_id & 0xFFFFFFFFu) >= p.requests;
         bad = stop && q.request_id != ~0ull;
     }
@@ -322,23 +324,29 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
     // ---- block-table rows of the slots admitted now ---------------------------
     if (n_adm) {
         __syncthreads();
-        const uint32_t total = n_adm * row_entries;
+        const uint32_t total = n_adm * row_entries;  // < 2^32: row_entries < 2^24
+        // entry e belongs to admitted row e / row_entries < 256: the float
+        // quotient is within 1e-4 of it, and one step either way corrects it
+        const float inv_row = 1.0f / (float)row_entries;
+        auto row_of = [&](uint32_t e) {
+            uint32_t i = (uint32_t)((float)e * inv_row);
+            i -= i * row_entries > e ? 1u : 0u;
+            i += (i + 1) * row_entries <= e ? 1u : 0u;
+            return i;
+        };
         for (uint32_t e0 = s; e0 < total; e0 += kSlots * kCopyDepth) {
-            uint32_t val[kCopyDepth];
+            uint32_t val[kCopyDepth], row[kCopyDepth];
 #pragma unroll
             for (int u = 0; u < kCopyDepth; u++) {
                 const uint32_t e = min(e0 + (uint32_t)u * kSlots, total - 1);
-                const uint32_t i = e / row_entries;
-                const uint32_t r = (uint32_t)(s_req[i].request_id & 0xFFFFFFFFu);
-                val[u] = p.req_table[(size_t)r * row_entries + (e - i * row_entries)];
+                row[u] = row_of(e);
+                val[u] = p.req_table[(size_t)s_arid[row[u]] * row_entries + (e - row[u] * row_entries)];
             }
 #pragma unroll
             for (int u = 0; u < kCopyDepth; u++) {
                 const uint32_t e = e0 + (uint32_t)u * kSlots;
-                if (e < total) {
-                    const uint32_t i = e / row_entries;
-                    p.slot_table[(size_t)s_aslot[i] * row_entries + (e - i * row_entries)] = val[u];
-                }
+                if (e < total)
+                    p.slot_table[(size_t)s_aslot[row[u]] * row_entries + (e - row[u] * row_entries)] = val[u];
             }
         }
     }
