@@ -5,10 +5,10 @@ bench/bench_gpu_scheduler.cu (request ring in, done ring out) with the real
 decode step of cu/worker.cu in between:
 
   request ring -> rl_hip_rollout_schedule (commit / retire / admit / prepare)
-               -> rl_hip_attn_decode (GQA over the block-paged arena)
+               -> rl_hip_decode_step (GQA over the block-paged arena, with the
+                  step's KV append inside the attention's merge kernel)
                -> rl_hip_logits_proj (attn_out . W_vocab on MFMA)
                -> rl_hip_sample (top-p, per-slot Philox seed and step)
-               -> rl_hip_kv_append
                -> done ring, then rl_hip_reward_advantage per group.
 
 Workload: 512 requests in 64 groups of 8. A group shares a 512-token prompt
@@ -206,16 +206,18 @@ class RolloutLoop:
         rlrt.check(rlrt.lib().rl_hip_rollout_schedule(C.byref(self.sched)), "rl_hip_rollout_schedule")
 
     def step(self) -> None:
-        """Schedule, then one batched decode step over the 256 slots."""
+        """Schedule, then one batched decode step over the 256 slots: attention
+        with the step's KV append run inside its merge kernel
+        (rl_hip_decode_step; the append writes position ctx, which the
+        attention does not read), projection, sampling."""
         dev, t = self.dev, self.t
         self.schedule()
         self.attn.q = dev["qpool"].ptr + (t % POOL) * self.q_row
-        rlrt.attn_decode(self.attn)
-        rlrt.check(rlrt.lib().rl_hip_logits_proj(C.byref(self.proj)), "rl_hip_logits_proj")
-        rlrt.sample(self.samp)
         self.app.k_new = dev["kpool"].ptr + (t % POOL) * self.kv_row
         self.app.v_new = dev["vpool"].ptr + (t % POOL) * self.kv_row
-        rlrt.kv_append(self.app)
+        rlrt.decode_step(self.attn, self.app)
+        rlrt.check(rlrt.lib().rl_hip_logits_proj(C.byref(self.proj)), "rl_hip_logits_proj")
+        rlrt.sample(self.samp)
         self.t += 1
 
     def drain_dones(self) -> np.ndarray:
