@@ -239,3 +239,26 @@ def test_done_ring_full_stops_with_status_3(rl, gpu):
     model, steps = _run(rl, 14, 1500, lambda g: 1, lambda t: 1000 if t == 0 else (600 if t == 3 else 0),
                         pop_every=0, max_spin=64)
     assert model.counters[3] == 3 and model.counters[0] == 1024
+
+
+def test_launch_argument_checks(rl, gpu):
+    """Refused on the host, nothing launched: a zero size, or 2^24 or more
+    block-table entries per slot."""
+    L = rl.lib()
+    dev = rl.DeviceBuffer(1 << 16, zero=True)
+    rr, dr = L.req_ring_create(), L.done_ring_create()
+    try:
+        ok = dict(req_ring=rr, done_ring=dr, state=dev.ptr, requests=4, prompt_len=dev.ptr, req_table=dev.ptr,
+                  kv_heads=2, table_stride=5, gen_tokens=dev.ptr, gen_stride=8, targets=dev.ptr, group_size=2,
+                  target_len=8, rewards=dev.ptr, slot_table=dev.ptr, slot_ctx=dev.ptr, slot_pos=dev.ptr,
+                  slot_temp=dev.ptr, slot_topk=dev.ptr, slot_topp=dev.ptr, slot_seed=dev.ptr, slot_step=dev.ptr,
+                  sampled=None, counters=dev.ptr)
+        for bad in (dict(requests=0), dict(group_size=0), dict(gen_stride=0), dict(kv_heads=8, table_stride=1 << 21),
+                    dict(kv_heads=1, table_stride=1 << 24), dict(counters=None)):
+            a = rl.SchedArgs(**{**ok, **bad})
+            assert L.rl_hip_rollout_schedule(C.byref(a)) == -1, bad
+            assert b"rl_hip_rollout_schedule" in L.rl_hip_last_error(), bad
+    finally:
+        L.req_ring_destroy(rr)
+        L.done_ring_destroy(dr)
+        dev.close()
