@@ -378,14 +378,86 @@ extern "C" int rl_hip_attn_decode(const rl_attn_decode_args_t *a)
     return attn_run(a, none);
 }
 
-extern "C" int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append)
+namespace {
+
+int step_validate(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append, const char *who)
 {
-    if (rl_require_open("rl_hip_decode_step") || validate(attn) || append_validate(append, "rl_hip_decode_step"))
+    if (rl_require_open(who) || validate(attn) || append_validate(append, who))
         return -1;
     if (append->batch != attn->batch || append->kv_heads != attn->kv_heads) {
-        rl_set_error("rl_hip_decode_step: append batch %u / kv_heads %u differ from attention %u / %u",
-                     append->batch, append->kv_heads, attn->batch, attn->kv_heads);
+        rl_set_error("%s: append batch %u / kv_heads %u differ from attention %u / %u", who, append->batch,
+                     append->kv_heads, attn->batch, attn->kv_heads);
         return -1;
     }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append)
+{
+    if (step_validate(attn, append, "rl_hip_decode_step"))
+        return -1;
     return attn_run(attn, append_params(append));
+}
+
+// ---- the decode step without allocation ---------------------------------------
+// The workspace of rl_hip_decode_step_noalloc (cum[batch + 1], then the fp32
+// partials) lives in this file-scope array; every device the library runs on
+// holds its own copy until the process ends. On the host, `scratch` names a
+// host-side stand-in, not device memory: kernels get the device address that
+// hipGetSymbolAddress returned for the device at rl_hip_open, kept in
+// g_scratch_dev. Nothing in the workspace has to start at zero: cum is written
+// by attn_decode_kernel's first workgroup and every partial the merge reads is
+// written earlier in the same call.
+static __device__ __align__(256) uint8_t scratch[RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+void *g_scratch_dev[kScratchDevices];
+
+}  // namespace
+
+int rl_attn_scratch_setup(int device)
+{
+    if (device < 0 || device >= kScratchDevices) {
+        rl_set_error("rl_hip_open: device %d beyond the %d devices the decode-step scratch covers", device,
+                     kScratchDevices);
+        return -1;
+    }
+    if (g_scratch_dev[device])
+        return 0;
+    void *p = nullptr;
+    if (rl_check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+        return -1;
+    if (!p) {
+        rl_set_error("hipGetSymbolAddress(scratch) returned NULL on device %d", device);
+        return -1;
+    }
+    g_scratch_dev[device] = p;
+    return 0;
+}
+
+extern "C" int rl_hip_decode_step_noalloc(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append)
+{
+    if (step_validate(attn, append, "rl_hip_decode_step_noalloc"))
+        return -1;
+    const int dev = rl_device();
+    void *ws = dev >= 0 && dev < kScratchDevices ? g_scratch_dev[dev] : nullptr;
+    if (!ws) {
+        rl_set_error("rl_hip_decode_step_noalloc: no scratch address for device %d", dev);
+        return -1;
+    }
+    const size_t need = ws_layout(attn).total;
+    if (need > RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES) {
+        rl_set_error("rl_hip_decode_step_noalloc: the step needs %zu bytes of workspace, above the %u-byte "
+                     "scratch (use rl_hip_decode_step with a caller workspace)",
+                     need, (unsigned)RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES);
+        return -1;
+    }
+    rl_attn_decode_args_t a = *attn;
+    a.workspace = ws;
+    a.workspace_bytes = RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES;
+    return attn_run(&a, append_params(append));
 }

@@ -10,6 +10,11 @@ int rl_require_open(const char *what);
 hipStream_t rl_stream(void);
 // Compute units of the open device (0 when no device is open).
 uint32_t rl_cu_count(void);
+// The open device's ordinal (-1 when no device is open).
+int rl_device(void);
+// Takes the device address of the decode step's scratch array on `device`,
+// which must be current (attn_decode.hip). Called by rl_hip_open.
+int rl_attn_scratch_setup(int device);
 
 // Reports a launch error (or a fault of an earlier asynchronous call).
 static inline int rl_check_launch(const char *what)

@@ -56,6 +56,8 @@ hipStream_t rl_stream(void) { return g_session.stream; }
 
 uint32_t rl_cu_count(void) { return g_session.cu_count; }
 
+int rl_device(void) { return g_session.open ? g_session.device : -1; }
+
 int rl_require_open(const char *what)
 {
     if (g_session.open)
@@ -82,6 +84,8 @@ int rl_hip_open(int device)
         return -1;
     }
     if (rl_check_hip(hipSetDevice(device), "hipSetDevice"))
+        return -1;
+    if (rl_attn_scratch_setup(device))
         return -1;
     if (rl_check_hip(hipStreamCreateWithFlags(&g_session.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags"))
         return -1;

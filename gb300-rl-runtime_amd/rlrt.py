@@ -292,6 +292,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
         "rl_hip_decode_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
+        "rl_hip_decode_step_noalloc": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
         "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
@@ -593,6 +594,14 @@ def kv_append(args: AppendArgs) -> None:
 def decode_step(attn: AttnArgs, append: AppendArgs) -> None:
     """Attention, then the KV append, in one call (the append rides in the merge kernel)."""
     check(lib().rl_hip_decode_step(C.byref(attn), C.byref(append)), "rl_hip_decode_step")
+
+
+DECODE_STEP_NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def decode_step_noalloc(attn: AttnArgs, append: AppendArgs) -> None:
+    """rl_hip_decode_step on the library's fixed scratch: attn.workspace is ignored."""
+    check(lib().rl_hip_decode_step_noalloc(C.byref(attn), C.byref(append)), "rl_hip_decode_step_noalloc")
 
 
 # ---------------------------------------------------------------- hw_desc rings

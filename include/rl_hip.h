@@ -397,4 +397,22 @@ int rl_hip_kv_append(const rl_kv_append_args_t *args);
  * must equal attn's. */
 int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append);
 
+/* ---- fused decode step that allocates nothing ------------------------------
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same kernels and results as rl_hip_decode_step, but
+ * the workspace is a fixed device array of RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES
+ * inside the library (one per device, held until the process ends; its address
+ * is taken at rl_hip_open). attn->workspace and attn->workspace_bytes are
+ * ignored. The call fails (-1, error set) when the step needs more workspace
+ * than that (rl_hip_attn_decode_workspace tells how much): about 2 KiB per
+ * (wave + rollout x kv head) at GQA group 4 and head_dim 128, so 16 MiB covers
+ * every full-device grid up to ~6,000 rows. It calls no hipMalloc, hipFree or
+ * other allocating routine. All calls on one device share its scratch: calls
+ * that overlap on one device (other threads, other streams, graphs replayed
+ * concurrently) race and corrupt each other's results; calls queued on the
+ * library stream one after another do not. */
+#define RL_DECODE_STEP_NOALLOC_SCRATCH_BYTES (16u << 20)
+int rl_hip_decode_step_noalloc(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append);
+
 RL_EXTERN_C_END
