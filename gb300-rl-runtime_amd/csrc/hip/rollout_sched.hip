@@ -24,7 +24,8 @@
 //          kept. Unlike the reference, a request is never consumed without a
 //          free slot, so none is dropped;
 //  prepare every slot writes the next step's arguments: attention context and
-//          append position (prompt tokens + generated tokens), sampler
+//          append position (prompt tokens + generated tokens; none for a slot
+//          parked at max_tokens because the done ring had no room), sampler
 //          temperature / top-k / top-p / seed / step (temperature 0 for an
 //          idle slot: the cheap greedy path), and the admitted slots' rows of
 //          the block table are copied from their requests' rows.
@@ -291,7 +292,7 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
         p.counters[3] = key != 0xFFFFFFFFu && (key & 1u) ? (uint32_t)kBadRequest : st;
     }
     const bool admit = maybe_free && frank < n_adm;
-    uint32_t rid = req0, tg = t;
+    uint32_t rid = req0, tg = t, maxt = max_tok;
     float temp = temp0, topp = topp0;
     uint32_t topk = topk0;
     uint64_t seed = seed0;
@@ -299,6 +300,7 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
         const RolloutRequest &q = s_req[frank];
         rid = (uint32_t)(q.request_id & 0xFFFFFFFFu);
         tg = 0;
+        maxt = q.max_tokens;
         temp = q.temperature;
         topk = q.top_k;
         topp = q.top_p;
@@ -352,7 +354,14 @@ __global__ __launch_bounds__(kSlots) void rollout_schedule_kernel(rl_rollout_sch
     }
 
     // ---- the next step's arguments ------------------------------------------------
-    if (admit || (active && !pushed)) {
+    // A slot decodes the next step while it holds fewer than max_tokens tokens.
+    // One that reached max_tokens and could not be retired (no room on the done
+    // ring) stays active but parked: no context, no append position, so it
+    // neither grows nor writes past its blocks.
+    const bool decodes = (admit || (active && !pushed)) && tg < maxt;
+    if (p.slot_request)
+        p.slot_request[s] = decodes ? rid : 0xFFFFFFFFu;
+    if (decodes) {
         const uint32_t ctx = (admit ? p.prompt_len[rid] : plen0) + tg;
         p.slot_ctx[s] = ctx;
         p.slot_pos[s] = ctx;

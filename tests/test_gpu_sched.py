@@ -102,20 +102,22 @@ class Model:
         self.counters[3] = st
         for s in range(SLOTS):
             a = self.slot[s]
-            self.pos[s] = 0xFFFFFFFF if a is None else self.prompt[a[0]] + a[1]
+            # a slot at max_tokens that could not retire is parked: no append position
+            self.pos[s] = 0xFFFFFFFF if a is None or a[1] >= a[2] else self.prompt[a[0]] + a[1]
 
     def args(self):
         ctx = np.zeros(SLOTS, np.uint32)
         temp, topp = np.zeros(SLOTS, np.float32), np.ones(SLOTS, np.float32)
         topk, seed, step = np.zeros(SLOTS, np.uint32), np.zeros(SLOTS, np.uint64), np.zeros(SLOTS, np.uint64)
         for s, a in enumerate(self.slot):
-            if a is not None:
+            if a is not None and a[1] < a[2]:
                 ctx[s] = self.prompt[a[0]] + a[1]
                 temp[s], topk[s], topp[s], seed[s], step[s] = a[5], a[6], a[7], a[4], a[1]
-        return ctx, self.pos.copy(), temp, topk, topp, seed, step
+        req = np.array([a[0] if a is not None and a[1] < a[2] else 0xFFFFFFFF for a in self.slot], np.uint32)
+        return ctx, self.pos.copy(), temp, topk, topp, seed, step, req
 
 
-def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, steps=400):
+def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, steps=400, after_stop=0):
     L = rl.lib()
     rng = np.random.default_rng(seed)
     kvh, stride, gen_stride, target_len, gs = 2, 5, 32, 16, 4
@@ -136,7 +138,7 @@ def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, 
     for k, n in (("state", grpo.STATE_BYTES), ("counters", 16), ("gen", requests * gen_stride * 4),
                  ("rewards", requests * 4), ("stab", SLOTS * kvh * stride * 4), ("ctx", SLOTS * 4),
                  ("temp", SLOTS * 4), ("topk", SLOTS * 4), ("topp", SLOTS * 4), ("seed", SLOTS * 8),
-                 ("step", SLOTS * 8), ("tok", SLOTS * 4)):
+                 ("step", SLOTS * 8), ("tok", SLOTS * 4), ("req", SLOTS * 4)):
         dev[k] = rl.DeviceBuffer(n, zero=True)
     dev["pos"] = rl.DeviceBuffer.from_array(np.full(SLOTS, 0xFFFFFFFF, np.uint32))
     rr, dr = L.req_ring_create(), L.done_ring_create()
@@ -147,7 +149,8 @@ def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, 
                      target_len=target_len, rewards=dev["rewards"].ptr, slot_table=dev["stab"].ptr,
                      slot_ctx=dev["ctx"].ptr, slot_pos=dev["pos"].ptr, slot_temp=dev["temp"].ptr,
                      slot_topk=dev["topk"].ptr, slot_topp=dev["topp"].ptr, slot_seed=dev["seed"].ptr,
-                     slot_step=dev["step"].ptr, sampled=None, counters=dev["counters"].ptr, max_spin=max_spin)
+                     slot_step=dev["step"].ptr, sampled=None, counters=dev["counters"].ptr, max_spin=max_spin,
+                     slot_request=dev["req"].ptr)
     fed = 0
     try:
         for step in range(steps):
@@ -169,8 +172,9 @@ def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, 
             got = [dev[k].download(dt, SLOTS) for k, dt in (("ctx", np.uint32), ("pos", np.uint32),
                                                              ("temp", np.float32), ("topk", np.uint32),
                                                              ("topp", np.float32), ("seed", np.uint64),
-                                                             ("step", np.uint64))]
-            for name, g, w in zip(("ctx", "pos", "temp", "topk", "topp", "seed", "step"), got, model.args()):
+                                                             ("step", np.uint64), ("req", np.uint32))]
+            for name, g, w in zip(("ctx", "pos", "temp", "topk", "topp", "seed", "step", "request"), got,
+                                  model.args()):
                 np.testing.assert_array_equal(g, w, err_msg=f"{ctx}: slot_{name}")
             raw = dev["state"].download(np.uint8, grpo.STATE_BYTES)
             st = raw[:SLOTS * 72].view(SLOT_DT)
@@ -200,7 +204,11 @@ def _run(rl, seed, requests, max_tok, feed, pop_every, max_spin=0, bad_at=None, 
                     assert np.float32(d.reward) == w[3], ctx
                     model.dhead += 1
             assert not model.pending_dones or not pop_every or step % pop_every != 0
-            if model.counters[3] != 0 or (model.counters[2] and all(m is None for m in model.slot)):
+            if model.counters[3] != 0:
+                after_stop -= 1
+                if after_stop < 0:
+                    break
+            elif model.counters[2] and all(m is None for m in model.slot):
                 break
         np.testing.assert_array_equal(dev["gen"].download(np.uint32, (requests, gen_stride)), model.gen)
         np.testing.assert_array_equal(dev["rewards"].download(np.float32, requests), model.rewards)
@@ -235,10 +243,15 @@ def test_bad_request_id_stops_admission(rl, gpu):
 
 def test_done_ring_full_stops_with_status_3(rl, gpu):
     """No done is ever popped: the fifth turnover of 256 slots finds no room
-    and gives up after a short bounded wait."""
+    and gives up after a short bounded wait. Four more launches after that:
+    the slots at max_tokens stay parked (no context, no append position, no
+    more tokens) instead of decoding past their blocks."""
     model, steps = _run(rl, 14, 1500, lambda g: 1, lambda t: 1000 if t == 0 else (600 if t == 3 else 0),
-                        pop_every=0, max_spin=64)
+                        pop_every=0, max_spin=64, after_stop=4)
     assert model.counters[3] == 3 and model.counters[0] == 1024
+    parked = [m for m in model.slot if m is not None]
+    assert len(parked) == SLOTS and all(m[1] == m[2] for m in parked)
+    assert (model.pos == 0xFFFFFFFF).all()
 
 
 def test_launch_argument_checks(rl, gpu):
