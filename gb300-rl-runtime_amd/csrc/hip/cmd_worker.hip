@@ -441,8 +441,21 @@ extern "C" int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *a)
         rl_set_error("rl_hip_cmd_worker_launch: NULL argument");
         return -1;
     }
-    if (a->groups == 0 || a->groups > 65535) {
-        rl_set_error("rl_hip_cmd_worker_launch: groups %u out of range", a->groups);
+    if (a->groups == 0) {
+        rl_set_error("rl_hip_cmd_worker_launch: groups 0");
+        return -1;
+    }
+    // Every worker must be resident at once: a worker that waits for a free
+    // compute unit leaves its ring pair unserved until another worker exits.
+    int per_cu = 0;
+    if (rl_check_hip(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, cmd_worker_kernel, kThreads, 0),
+                     "hipOccupancyMaxActiveBlocksPerMultiprocessor(cmd_worker_kernel)"))
+        return -1;
+    const uint64_t resident = (uint64_t)(per_cu > 0 ? per_cu : 0) * rl_cu_count();
+    if (a->groups > resident) {
+        rl_set_error("rl_hip_cmd_worker_launch: %u groups exceed the %llu workers the device holds at once "
+                     "(%d per compute unit x %u compute units)",
+                     a->groups, (unsigned long long)resident, per_cu, rl_cu_count());
         return -1;
     }
     if (a->io_slots & (a->io_slots - 1)) {

@@ -192,3 +192,101 @@ def test_synthesized_queries(rl, gpu, olib):
         return np.array([olib.orc_synth_query(d.seq_id, d.reward_cookie, state.ctypes.data, i) for i in range(128)],
                         dtype=np.float32)
     _check(descs, got, o, 16, arena16, qvec)
+
+
+def test_one_worker_per_cu(rl, gpu):
+    """One persistent worker per compute unit, each the only consumer and
+    producer of its own CommandRing / CompletionRing pair: two decode_batch
+    windows (16 and 9 descriptors) per pair, output slots disjoint across
+    pairs. Per pair: completions in order and every row against fp64 as
+    above, ring indices and counters."""
+    L = rl.lib()
+    G = int(gpu.cu_count)
+    rng = np.random.default_rng(63)
+    nblk = 64
+    per = 32
+    io = 1 << int(np.ceil(np.log2(G * per)))
+    arena16 = synth.f32_to_f16(rng.standard_normal(nblk * BLOCK // 2, dtype=np.float32))
+    qf = synth.f32_to_f16(rng.standard_normal((io, 128), dtype=np.float32))
+    lens = [0, 1, 5, 16, 17, 31, 32, 40]
+    windows = []
+    for g in range(G):
+        ws_ = []
+        k = 0
+        for size in (16, 9):
+            win = []
+            for _ in range(size):
+                win.append(rl.Descriptor(seq_id=(g << 20) + k, kv_block_offset=int(rng.integers(0, nblk)),
+                                         num_kv_blocks=lens[int(rng.integers(0, len(lens)))],
+                                         output_token_offset=g * per + k, reward_cookie=int(rng.integers(0, 2**63))))
+                k += 1
+            ws_.append(win)
+        windows.append(ws_)
+    rings = [L.ring_create() for _ in range(G)]
+    comps = [L.comp_ring_create() for _ in range(G)]
+    assert all(rings) and all(comps)
+    pairs = _coherent(rl, 16 * G)
+    for g in range(G):
+        C.cast(pairs, C.POINTER(C.c_void_p))[g] = rings[g]
+        C.cast(pairs, C.POINTER(C.c_void_p))[G + g] = comps[g]
+    stop = _coherent(rl, 64)
+    darena = rl.DeviceBuffer.from_array(arena16.view(np.uint8))
+    dq = rl.DeviceBuffer.from_array(qf)
+    do = rl.DeviceBuffer(io * 128 * 4, zero=True)
+    stats = rl.DeviceBuffer(32 * G, zero=True)
+    a = rl.CmdWorkerArgs(rings=pairs, comp_rings=pairs + 8 * G, groups=G, stop=stop, max_idle_polls=1 << 22,
+                         arena_base=darena.ptr, arena_bytes=darena.nbytes, sample_state=None, q_buffer=dq.ptr,
+                         o_buffer=do.ptr, io_slots=io, stats=stats.ptr)
+    got = [[] for _ in range(G)]
+    print(f"[cmd] launching {G} command-ring workers, one per compute unit", flush=True)
+    rl.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
+    try:
+        batch = rl.DecodeDispatchBatch()
+        for wi in range(2):
+            for g in range(G):
+                L.decode_batch_reset(C.byref(batch))
+                for d in windows[g][wi]:
+                    assert L.decode_batch_push(C.byref(batch), C.byref(d)) == 0
+                assert L.decode_batch_submit(rings[g], C.byref(batch)) == 0
+        deadline = time.perf_counter() + 60
+        n = 0
+        while n < G * 25 and time.perf_counter() < deadline:
+            for g in range(G):
+                c = _comp_pop_all(rl, comps[g])
+                got[g] += c
+                n += len(c)
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rl.sync()
+    st = stats.download(np.uint64, (G, 4))
+    o = do.download(np.float32, (io, 128))
+    for g in range(G):
+        descs = windows[g][0] + windows[g][1]
+        _check(descs, got[g], o, io, arena16, lambda d, slot: synth.f16_to_f32(qf[slot]))
+        assert st[g, 0] == 25 and st[g, 1] == 25 and st[g, 3] == 0, (g, st[g])
+        assert (L.hw_ring_load_acquire(rings[g]), L.hw_ring_load_acquire(rings[g] + 64),
+                L.hw_ring_load_acquire(comps[g]), L.hw_ring_load_acquire(comps[g] + 64)) == (25, 25, 25, 25), g
+    for b in (darena, dq, do, stats):
+        b.close()
+    for r, c in zip(rings, comps):
+        L.ring_destroy(r)
+        L.comp_ring_destroy(c)
+    L.rl_hip_host_free(pairs)
+    L.rl_hip_host_free(stop)
+
+
+def test_launch_refuses_more_workers_than_resident(rl, gpu):
+    """Workers beyond what the device holds at once would leave their ring
+    pairs unserved: the launch is refused on the host, nothing runs. (A
+    1,024-thread worker takes 16 of a compute unit's 32 wave slots, so twice
+    the compute units plus one exceeds the device whatever the LDS use.)"""
+    L = rl.lib()
+    dev = rl.DeviceBuffer(1 << 16, zero=True)
+    a = rl.CmdWorkerArgs(rings=dev.ptr, comp_rings=dev.ptr, groups=2 * int(gpu.cu_count) + 1, stop=dev.ptr,
+                         max_idle_polls=16, arena_base=dev.ptr, arena_bytes=dev.nbytes, sample_state=None,
+                         q_buffer=None, o_buffer=dev.ptr, io_slots=1, stats=dev.ptr)
+    assert L.rl_hip_cmd_worker_launch(C.byref(a)) == -1
+    assert b"exceed" in L.rl_hip_last_error()
+    a.groups = 0
+    assert L.rl_hip_cmd_worker_launch(C.byref(a)) == -1
+    dev.close()

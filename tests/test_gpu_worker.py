@@ -206,3 +206,125 @@ def test_worker_exits_on_idle_limit(rl, gpu):
     L.hw_ring_destroy(dq)
     L.rl_hip_host_free(rings)
     L.rl_hip_host_free(stop)
+
+
+def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
+    """One persistent worker per compute unit (256 on MI355X), each the single
+    consumer / producer of its own ring pair and its own rollout (MHA 8 x d64
+    fp16, KV length 256 at the start): 8 decode steps per pair through
+    infer_submit_decode, submitted while the workers poll. Per pair: the
+    completions and ring indices byte-identical to hw_worker_sim_run fed the
+    same submissions, and the counters; over all pairs: tokens bit-exact,
+    logprobs within 1e-4, every step's attention within 1e-4 of fp64 over the
+    arena as the earlier appends left it, and the final arena byte-identical
+    to the host appends."""
+    L = rl.lib()
+    G = int(gpu.cu_count)
+    S = 8
+    rng = np.random.default_rng(1003)
+    w = synth.make_decode(1002, G, 8, 8, 64, CTX0, CTX0, dtype="fp16", kv_std=0.5, reserve_tokens=CTX0 + S + 1)
+    host_arena0 = w.arena.copy()
+    q_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32))
+    k_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32) * np.float32(0.5))
+    v_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32) * np.float32(0.5))
+    logits = rng.standard_normal((G, S, VOCAB), dtype=np.float32) * np.float32(2.0)
+    layout = rl.KvLayoutDesc.paged(16, 64)
+    bufs = {n: rl.DeviceBuffer.from_array(a) for n, a in
+            (("arena", w.arena), ("table", w.table), ("q", q_all), ("k", k_all), ("v", v_all), ("logits", logits))}
+    attn_out = rl.DeviceBuffer(G * S * 8 * 64 * 4, zero=True)
+    tok = rl.DeviceBuffer(G * S * 4, zero=True)
+    lp = rl.DeviceBuffer(G * S * 4, zero=True)
+    stats = rl.DeviceBuffer(G * 4 * 8, zero=True)
+    cqs = [L.hw_ring_create() for _ in range(G)]
+    dqs = [L.hw_ring_create() for _ in range(G)]
+    assert all(cqs) and all(dqs)
+    rings = _alloc_coherent(rl, 16 * G)
+    for g in range(G):
+        C.cast(rings, C.POINTER(C.c_void_p))[g] = cqs[g]
+        C.cast(rings, C.POINTER(C.c_void_p))[G + g] = dqs[g]
+    stop = _alloc_coherent(rl, 64)
+    doorbells = _alloc_coherent(rl, 64 * G)
+    a = rl.HwWorkerArgs(cmdq=rings, doneq=rings + 8 * G, groups=G, stop=stop, max_idle_polls=1 << 22,
+                        arena_base=bufs["arena"].ptr, arena_bytes=bufs["arena"].nbytes, layout=layout,
+                        block_table=bufs["table"].ptr, table_stride=w.table_stride, rollouts=G, q_heads=8,
+                        kv_heads=8, dtype=rl.DTYPE_FP16, scale=0.0, max_steps=S, q=bufs["q"].ptr,
+                        k_new=bufs["k"].ptr, v_new=bufs["v"].ptr, logits=bufs["logits"].ptr, vocab=VOCAB,
+                        attn_out=attn_out.ptr, token_out=tok.ptr, logprob_out=lp.ptr, stats=stats.ptr)
+    ws = rl.hw_worker_workspace(a)
+    ctxs = [rl.InferHwCtx(cmdq=cqs[g], doneq=dqs[g], doorbell=doorbells + 64 * g, gpu_group_id=g, kv_arena_id=42)
+            for g in range(G)]
+    got = [[] for _ in range(G)]
+    print(f"[worker] launching {G} persistent workers, one per compute unit", flush=True)
+    rl.hw_worker_launch(a)
+    try:
+        t0 = time.perf_counter()
+        for i in range(S):
+            for g in range(G):
+                assert L.infer_submit_decode(C.byref(ctxs[g]), g, 0x1000 * i, 0x40 * i, 0, CTX0 + i,
+                                             CTX0 + i + 1) == 0
+        deadline = time.perf_counter() + 60.0
+        n = 0
+        while n < G * S and time.perf_counter() < deadline:
+            for g in range(G):
+                while (d := rl.hw_ring_pop(dqs[g])) is not None:
+                    got[g].append(bytes(d))
+                    n += 1
+        elapsed = time.perf_counter() - t0
+        for g in range(G):
+            assert rl.hw_ring_push(cqs[g], rl.HwDesc(opcode=255)) == 0
+        print(f"[worker] {n} completions from {G} pairs in {elapsed * 1e3:.1f} ms", flush=True)
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rl.sync()
+    st = stats.download(np.uint64, (G, 4))
+    assert all(len(x) == S for x in got), [len(x) for x in got]
+    assert (st == np.array([S, S, S, 0], np.uint64)).all(), st
+
+    # every pair against the CPU simulator fed the same submissions
+    for g in range(G):
+        cq2 = L.hw_ring_create()
+        sub = []
+        try:
+            c2 = rl.InferHwCtx(cmdq=cq2, doneq=dqs[g], doorbell=doorbells + 64 * g, gpu_group_id=g, kv_arena_id=42)
+            for i in range(S):
+                assert L.infer_submit_decode(C.byref(c2), g, 0x1000 * i, 0x40 * i, 0, CTX0 + i, CTX0 + i + 1) == 0
+                sub.append(rl.hw_ring_pop(cq2))
+        finally:
+            L.hw_ring_destroy(cq2)
+        sim_out, sim_cq, sim_dq, sim_counts = _sim_completions(rl, sub)
+        assert got[g] == sim_out, g
+        assert rl.hw_ring_indices(cqs[g]) == sim_cq == (S + 1, S + 1), g
+        assert rl.hw_ring_indices(dqs[g]) == sim_dq == (S, S), g
+        assert sim_counts == (S, S)
+
+    gt = tok.download(np.uint32, (G, S))
+    glp = lp.download(np.float32, (G, S))
+    ot, olp = orc.sample_rows(olib, logits.reshape(G * S, VOCAB), True, 1.0, 0, 1.0, 0, 0)
+    assert np.array_equal(gt.ravel(), ot)
+    assert np.abs(glp.ravel() - olp).max() < 1e-4
+
+    gout = attn_out.download(np.float32, (G, S, 8, 64))
+    w.arena[:] = host_arena0
+    worst = 0.0
+    tc, rb = w.token_count, 2 * 64
+    for i in range(S):
+        w.ctx = np.full(G, CTX0 + i, dtype=np.uint32)
+        w.q = np.ascontiguousarray(q_all[:, i])
+        ref = orc.attn_f64(olib, w, 1)
+        worst = max(worst, float((np.abs(gout[:, i] - ref).max(axis=-1) / np.abs(ref).max(axis=-1)).max()))
+        pos = CTX0 + i
+        for g in range(G):
+            for h in range(8):
+                blk = int(w.table[g, h, pos // tc])
+                base = blk * w.block_bytes + (pos % tc) * rb
+                w.arena[base:base + rb] = k_all[g, i, h].view(np.uint8)
+                w.arena[base + tc * rb:base + tc * rb + rb] = v_all[g, i, h].view(np.uint8)
+    assert worst < 1e-4, worst
+    assert np.array_equal(bufs["arena"].download(np.uint8, w.arena.size), w.arena)
+
+    for b in list(bufs.values()) + [attn_out, tok, lp, stats, ws]:
+        b.close()
+    for q in cqs + dqs:
+        L.hw_ring_destroy(q)
+    for p in (rings, stop, doorbells):
+        L.rl_hip_host_free(p)
