@@ -13,7 +13,8 @@ decode step of cu/worker.cu in between:
 
 Workload: 512 requests in 64 groups of 8. A group shares a 512-token prompt
 prefix (32 full 16-token blocks per kv head: the same physical blocks in every
-member's table) plus U[0, 512] private prompt tokens; each request generates
+member's table; a kv_prefix with one branch per member, whose table image the
+device reads) plus U[0, 512] private prompt tokens; each request generates
 256 tokens. GQA 32 q / 8 kv heads, d128, bf16 K/V ~N(0,1); queries and new K/V
 rows come from a pool of 8 seeded steps; W_vocab bf16 [32,000 x 4,096]
 ~N(0, 0.02^2); top-p 0.9 at temperature 1. 256 rollout slots.
@@ -63,32 +64,61 @@ def done_ring_pop(ring: int) -> rlrt.RolloutDone | None:
     return d
 
 
-def build_workload(seed: int) -> dict:
+def build_workload(seed: int, prefix: int = PREFIX, priv_zero_every: int = 0) -> dict:
     """Seeded host inputs: prompts, block tables (shared prefix blocks), arena,
-    W_vocab, query / K / V pools, per-group targets and per-request seeds."""
+    W_vocab, query / K / V pools, per-group targets and per-request seeds.
+
+    Group g's prefix occupies KVH * ceil(prefix / TPB) consecutive arena
+    blocks from prefix_base[g], head-major (the layout a KVPrefix's
+    kv_block_offset / kv_block_count describe); the groups' ranges and the
+    private blocks sit at seeded random places. Full prefix blocks are shared
+    by the group's members. When prefix is not a multiple of TPB, its last
+    block is partly filled: each member writes its own tokens into a private
+    block instead (copy-on-write). Members with private prompt tokens hold the
+    prefix's slots of that block already (their prompt was prefilled); those
+    without (every priv_zero_every-th request, when set) still hold random
+    bytes there, and the loop's copy-on-write fills them before their first
+    step."""
     rng = np.random.default_rng(seed)
     priv = rng.integers(0, PRIV_MAX + 1, REQ)
-    prompt = (PREFIX + priv).astype(np.uint32)
-    n_prefix = PREFIX // TPB
-    n_priv = -(-(priv + GEN + 1) // TPB)
-    stride = n_prefix + -(-(PRIV_MAX + GEN + 1) // TPB)   # covers the largest context
-    total = GROUPS * KVH * n_prefix + int(n_priv.sum()) * KVH
-    perm = rng.permutation(total).astype(np.uint32)
+    if priv_zero_every:
+        priv[::priv_zero_every] = 0
+    prompt = (prefix + priv).astype(np.uint32)
+    n_shared = prefix // TPB                    # full prefix blocks, shared
+    n_pb = -(-prefix // TPB)                    # prefix blocks per head (the last maybe partial)
+    first_own = prefix - prefix % TPB           # first position in a private block
+    n_priv = -(-(prompt.astype(np.int64) + GEN + 1 - first_own) // TPB)
+    stride = -(-(prefix + PRIV_MAX + GEN + 1) // TPB)  # covers the largest context
+    n_private = int(n_priv.sum()) * KVH
+    # place the 64 prefix ranges and the private blocks in one seeded shuffle of units
+    units = np.concatenate([np.full(GROUPS, KVH * n_pb), np.ones(n_private, np.int64)])
+    order = rng.permutation(len(units))
+    start = np.zeros(len(units), np.int64)
+    start[order] = np.concatenate([[0], np.cumsum(units[order])[:-1]])
+    total = int(units.sum())
+    prefix_base = start[:GROUPS].astype(np.uint32)
+    private = start[GROUPS:].astype(np.uint32)
+    prefix_blocks = (prefix_base[:, None, None] + np.arange(KVH)[None, :, None] * n_pb
+                     + np.arange(n_pb)[None, None, :]).astype(np.uint32)
     table = np.zeros((REQ, KVH, stride), np.uint32)
     k = 0
-    prefix_blocks = np.zeros((GROUPS, KVH, n_prefix), np.uint32)
-    for g in range(GROUPS):
-        for h in range(KVH):
-            prefix_blocks[g, h] = perm[k:k + n_prefix]
-            k += n_prefix
     for r in range(REQ):
         for h in range(KVH):
-            table[r, h, :n_prefix] = prefix_blocks[r // GS, h]
+            table[r, h, :n_shared] = prefix_blocks[r // GS, h, :n_shared]
             m = int(n_priv[r])
-            table[r, h, n_prefix:n_prefix + m] = perm[k:k + m]
+            table[r, h, n_shared:n_shared + m] = private[k:k + m]
             k += m
     arena = np.empty(total * 2 * TPB * D, np.uint16)
     synth._fill_normal(rng, arena.size, 1.0, "bf16", arena)
+    if prefix % TPB:
+        # prefill of the members with private prompt tokens: the prefix's slots
+        # of the partly filled block copied into their private block (K and V planes)
+        blk = arena.reshape(total, 2, TPB, D)
+        slot = prefix % TPB
+        for r in np.nonzero(priv > 0)[0]:
+            for h in range(KVH):
+                src, dst = prefix_blocks[r // GS, h, n_shared], table[r, h, n_shared]
+                blk[dst, :, :slot] = blk[src, :, :slot]
     w = synth.f32_to_bf16(rng.standard_normal((VOCAB, HID), dtype=np.float32) * np.float32(0.02))
     qpool = synth.f32_to_bf16(rng.standard_normal((POOL, SLOTS, QH, D), dtype=np.float32))
     kpool = synth.f32_to_bf16(rng.standard_normal((POOL, SLOTS, KVH, D), dtype=np.float32))
@@ -97,7 +127,32 @@ def build_workload(seed: int) -> dict:
     seeds = rng.integers(0, 2**63, REQ, dtype=np.uint64)
     return dict(prompt=prompt, table=table, stride=stride, arena=arena.view(np.uint8), w=w, qpool=qpool,
                 kpool=kpool, vpool=vpool, targets=targets, seeds=seeds, prefix_blocks=prefix_blocks,
-                priv=priv, n_blocks=n_prefix + n_priv)
+                prefix_base=prefix_base, prefix=prefix, priv=priv, n_blocks=n_shared + n_priv)
+
+
+def build_prefix_table(cfg: dict) -> tuple[np.ndarray, np.ndarray]:
+    """The host KVPrefixTable of a workload (src/kv_prefix.c rules through the
+    library): group g's prefix registered as id g at block offset
+    prefix_base[g] with KVH * ceil(prefix / TPB) blocks, and one branch per
+    request (rollout id = request id) on its group's prefix, whose delta is the
+    request's first private block. Returns (table image, branch id of each request)."""
+    L = rlrt.lib()
+    ptab = np.zeros(PREFIX_TABLE_BYTES, np.uint8)
+    L.kv_prefix_table_init(ptab.ctypes.data)
+    prefix = cfg["prefix"]
+    n_shared, n_pb = prefix // TPB, -(-prefix // TPB)
+    pid, bid = C.c_uint32(), C.c_uint32()
+    branch = np.zeros(REQ, np.uint32)
+    for g in range(GROUPS):
+        if L.kv_prefix_register(ptab.ctypes.data, int(cfg["prefix_base"][g]), prefix, KVH * n_pb,
+                                C.byref(pid)) != 0 or pid.value != g:
+            raise rlrt.RlrtError(f"kv_prefix_register for group {g} failed")
+    for r in range(REQ):
+        if L.kv_branch_alloc(ptab.ctypes.data, r, r // GS, int(cfg["table"][r, 0, n_shared]), int(cfg["priv"][r]),
+                             int(cfg["n_blocks"][r]) - n_shared, C.byref(bid)) != 0:
+            raise rlrt.RlrtError(f"kv_branch_alloc for request {r} failed")
+        branch[r] = bid.value
+    return ptab, branch
 
 
 class RolloutLoop:
@@ -111,11 +166,14 @@ class RolloutLoop:
             dev[k] = rlrt.DeviceBuffer.from_array(cfg[k])
         dev["rtab"] = rlrt.DeviceBuffer.from_array(cfg["table"])
         stride = self.stride = cfg["stride"]
+        self.ptab, self.branch = build_prefix_table(cfg)
+        dev["ptab"] = rlrt.DeviceBuffer.from_array(self.ptab)
+        dev["branch"] = rlrt.DeviceBuffer.from_array(self.branch)
         for k, n in (("state", STATE_BYTES), ("counters", 16), ("gen", REQ * GEN * 4), ("rewards", REQ * 4),
                      ("stab", SLOTS * KVH * stride * 4), ("ctx", SLOTS * 4), ("temp", SLOTS * 4),
                      ("topk", SLOTS * 4), ("topp", SLOTS * 4), ("seed", SLOTS * 8), ("step", SLOTS * 8),
                      ("out", SLOTS * HID * 2), ("out32", SLOTS * HID * 4), ("logits", SLOTS * VOCAB * 4),
-                     ("tok", SLOTS * 4), ("lp", SLOTS * 4)):
+                     ("tok", SLOTS * 4), ("lp", SLOTS * 4), ("sreq", SLOTS * 4)):
             dev[k] = rlrt.DeviceBuffer(n, zero=True)
         dev["pos"] = rlrt.DeviceBuffer.from_array(np.full(SLOTS, 0xFFFFFFFF, np.uint32))
 
@@ -129,9 +187,17 @@ class RolloutLoop:
             rewards=dev["rewards"].ptr, slot_table=dev["stab"].ptr, slot_ctx=dev["ctx"].ptr,
             slot_pos=dev["pos"].ptr, slot_temp=dev["temp"].ptr, slot_topk=dev["topk"].ptr,
             slot_topp=dev["topp"].ptr, slot_seed=dev["seed"].ptr, slot_step=dev["step"].ptr, sampled=None,
-            counters=dev["counters"].ptr)
+            counters=dev["counters"].ptr, slot_request=dev["sreq"].ptr)
         self.layout = rlrt.KvLayoutDesc.paged(TPB, D)
-        max_ctx = PREFIX + PRIV_MAX + GEN + 1
+        max_ctx = cfg["prefix"] + PRIV_MAX + GEN + 1
+        # copy-on-write of the prefix's partly filled block before a member's
+        # first own token: needed only when the prefix ends inside a block
+        self.cow = None
+        if cfg["prefix"] % TPB:
+            self.cow = rlrt.CowArgs(arena_base=dev["arena"].ptr, arena_bytes=dev["arena"].nbytes, layout=self.layout,
+                                    prefixes=dev["ptab"].ptr, row_key=dev["sreq"].ptr,
+                                    branch_of_key=dev["branch"].ptr, keys=REQ, block_table=dev["stab"].ptr,
+                                    table_stride=stride, batch=SLOTS, kv_heads=KVH, positions=dev["pos"].ptr)
         self.attn = rlrt.attn_args(dev["arena"], self.layout, dev["stab"], stride, SLOTS, QH, KVH,
                                    rlrt.DTYPE_BF16, dev["ctx"], max_ctx, dev["qpool"], dev["out"], dev["out32"])
         self.attn_ws = rlrt.attn_workspace(self.attn)
@@ -206,12 +272,16 @@ class RolloutLoop:
         rlrt.check(rlrt.lib().rl_hip_rollout_schedule(C.byref(self.sched)), "rl_hip_rollout_schedule")
 
     def step(self) -> None:
-        """Schedule, then one batched decode step over the 256 slots: attention
+        """Schedule, the copy-on-write of members at their first own token when
+        the prefix ends inside a block (rl_hip_kv_cow: the device resolves each
+        slot's branch in the prefix table image), then one batched decode step over the 256 slots: attention
         with the step's KV append run inside its merge kernel
         (rl_hip_decode_step; the append writes position ctx, which the
         attention does not read), projection, sampling."""
         dev, t = self.dev, self.t
         self.schedule()
+        if self.cow is not None:
+            rlrt.kv_cow(self.cow)
         self.attn.q = dev["qpool"].ptr + (t % POOL) * self.q_row
         self.app.k_new = dev["kpool"].ptr + (t % POOL) * self.kv_row
         self.app.v_new = dev["vpool"].ptr + (t % POOL) * self.kv_row

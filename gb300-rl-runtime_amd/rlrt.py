@@ -243,7 +243,14 @@ class SchedArgs(C.Structure):
                 ("slot_ctx", C.c_void_p), ("slot_pos", C.c_void_p), ("slot_temp", C.c_void_p),
                 ("slot_topk", C.c_void_p), ("slot_topp", C.c_void_p), ("slot_seed", C.c_void_p),
                 ("slot_step", C.c_void_p), ("sampled", C.c_void_p), ("counters", C.c_void_p),
-                ("max_spin", C.c_uint64)]
+                ("max_spin", C.c_uint64), ("slot_request", C.c_void_p)]
+
+
+class CowArgs(C.Structure):
+    _fields_ = [("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64), ("layout", KvLayoutDesc),
+                ("prefixes", C.c_void_p), ("row_key", C.c_void_p), ("branch_of_key", C.c_void_p),
+                ("keys", C.c_uint32), ("block_table", C.c_void_p), ("table_stride", C.c_uint32),
+                ("batch", C.c_uint32), ("kv_heads", C.c_uint32), ("positions", C.c_void_p)]
 
 
 class HwWorkerArgs(C.Structure):
@@ -291,6 +298,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_sample_workspace": (sz, [C.POINTER(SampleArgs)]),
         "rl_hip_sample": (i32, [C.POINTER(SampleArgs)]),
         "rl_hip_kv_append": (i32, [C.POINTER(AppendArgs)]),
+        "rl_hip_kv_branch_resolve": (i32, [vp, vp, vp, u32]),
+        "rl_hip_kv_cow": (i32, [C.POINTER(CowArgs)]),
         "rl_hip_decode_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
         "rl_hip_decode_step_noalloc": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
@@ -589,6 +598,10 @@ def sample(args: SampleArgs) -> None:
 
 def kv_append(args: AppendArgs) -> None:
     check(lib().rl_hip_kv_append(C.byref(args)), "rl_hip_kv_append")
+
+
+def kv_cow(args: CowArgs) -> None:
+    check(lib().rl_hip_kv_cow(C.byref(args)), "rl_hip_kv_cow")
 
 
 def decode_step(attn: AttnArgs, append: AppendArgs) -> None:

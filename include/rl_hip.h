@@ -21,6 +21,7 @@
 #include <stdint.h>
 #include "hw_ring.h"
 #include "kv_layout.h"
+#include "kv_prefix.h"
 #include "request.h"
 #include "reward.h"
 #include "ring.h"
@@ -183,7 +184,8 @@ int rl_hip_reward_advantage(const rl_reward_args_t *args);
  * request_id UINT64_MAX sets counters[2]); admitted slots copy their
  * request's kv_heads block-table rows into slot_table. Finally every slot
  * writes the next step's per-row arguments: slot_ctx / slot_pos = prompt_len
- * + tokens_generated (0 / UINT32_MAX when idle), and the sampler's
+ * + tokens_generated (0 / UINT32_MAX when idle, and for a slot parked at
+ * max_tokens that could not be retired for want of room on done_ring), and the sampler's
  * temperature (0 when idle), top_k, top_p, seed (the request's rng_seed) and
  * step (the index of the token being generated). Rings live in coherent host
  * memory (req_ring_create / done_ring_create after rl_hip_open).
@@ -218,6 +220,8 @@ typedef struct {
     const uint32_t *sampled;     /* device [256] tokens of the last step, NULL before the first */
     uint32_t *counters;          /* device [4], zero-initialised */
     uint64_t max_spin;           /* 0 selects 2^22 */
+    uint32_t *slot_request;      /* device [256] or NULL: the request id of each slot that decodes
+                                    the next step, UINT32_MAX for the others */
 } rl_rollout_sched_args_t;
 
 int rl_hip_rollout_schedule(const rl_rollout_sched_args_t *args);
@@ -304,7 +308,7 @@ int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
 typedef struct {
     CommandRing *const *rings;          /* coherent host [groups] (ring_create after rl_hip_open) */
     CompletionRing *const *comp_rings;  /* coherent host [groups] (comp_ring_create) */
-    uint32_t groups;
+    uint32_t groups;                    /* 1 .. workers resident at once (one per compute unit) */
     const volatile uint32_t *stop;      /* coherent host: nonzero ends every worker */
     uint64_t max_idle_polls;            /* 0 selects 2^22 */
     const void *arena_base;             /* device: fixed128 blocks of 16,384 bytes */
@@ -369,7 +373,15 @@ int rl_hip_sample(const rl_sample_args_t *args);
  * When cow_src is non-NULL and cow_src[b * kv_heads + g] >= 0, the slots
  * [0, positions[b] % token_count) of that (shared) source block are first
  * copied into the destination block: the copy-on-write of a partially
- * filled prefix block. */
+ * filled prefix block. The reference keeps the sharing state (refcounts of
+ * src/kv_prefix.c:46-133, the offset rule of kv_branch_resolve,
+ * cu/kv_prefix.cu:4-23) but never copies a block; the copy is this library's.
+ * At the copy-on-write step the destination block holds nothing yet: an
+ * attention in the same step must read the prefix through a table that still
+ * maps the shared source block (the append's table maps the private
+ * destination), and from the next step on the private block holds the
+ * prefix slots and the new token. rl_hip_kv_cow (below) instead copies before
+ * the attention, so that one table serves both. */
 typedef struct {
     void *arena_base;            /* device */
     uint64_t arena_bytes;        /* blocks past it are never written */
@@ -386,15 +398,58 @@ typedef struct {
 
 int rl_hip_kv_append(const rl_kv_append_args_t *args);
 
+/* ---- prefix table on the device ------------------------------------------
+ * rl_hip_kv_branch_resolve replaces kv_branch_resolve (cu/kv_prefix.cu:4-23)
+ * on a byte-compatible KVPrefixTable image in device memory (copied from the
+ * host table that kv_prefix_register / kv_branch_alloc maintain):
+ * out_offsets[i] = -1 when branch_ids[i] >= MAX_BRANCHES; the branch's
+ * delta_kv_offset when its prefix_id >= MAX_PREFIXES or that prefix's refcnt
+ * is 0; otherwise the prefix's kv_block_offset. (The host
+ * kv_branch_total_offset ignores the refcount; the device rule does not.)
+ *
+ * rl_hip_kv_cow is the copy-on-write of a shared prefix's partially filled
+ * last block, run before a step whose attention reads it (no reference
+ * function: the reference keeps the refcounts, src/kv_prefix.c:46-133, and
+ * copies nothing). Row b's branch is row_key[b] (or branch_of_key[row_key[b]]
+ * when that side table is given; keys bounds it). When the branch resolves to
+ * a live prefix of token_len P with P % token_count != 0 and positions[b] ==
+ * P (the branch's first own token lands in that block), kv head g's slots
+ * [0, P % token_count) of the prefix block kv_block_offset + g *
+ * (kv_block_count / kv_heads) + P / token_count (prefix blocks head-major
+ * from kv_block_offset, in arena block units) are copied into the row's
+ * block block_table[(b * kv_heads + g) * table_stride + P / token_count].
+ * Every other row is left alone, as are blocks past the arena or the table. */
+int rl_hip_kv_branch_resolve(const KVPrefixTable *table, const uint32_t *branch_ids, int64_t *out_offsets,
+                             uint32_t n);
+
+typedef struct {
+    void *arena_base;               /* device */
+    uint64_t arena_bytes;
+    KvLayoutDesc layout;
+    const KVPrefixTable *prefixes;  /* device image of the host table */
+    const uint32_t *row_key;        /* device [batch] */
+    const uint32_t *branch_of_key;  /* device [keys] branch ids, or NULL: row_key holds the branch id */
+    uint32_t keys;
+    const uint32_t *block_table;    /* device [batch][kv_heads][table_stride]: private blocks */
+    uint32_t table_stride;
+    uint32_t batch;
+    uint32_t kv_heads;
+    const uint32_t *positions;      /* device [batch]: the position the step appends */
+} rl_kv_cow_args_t;
+
+int rl_hip_kv_cow(const rl_kv_cow_args_t *args);
+
 /* ---- fused decode step: attention, then the KV append ---------------------
  * Replaces the per-descriptor decode of process_descriptor
  * (cu/worker.cu:25-64: attention_decode_step_fixed128 over the rollout's
- * cached tokens) followed by the append of the step's K/V token (the
- * copy-on-write of cu/kv_prefix.cu:4-23), batched. Results equal
+ * cached tokens) followed by the append of the step's K/V token (with the
+ * copy-on-write described above), batched. Results equal
  * rl_hip_attn_decode(attn) then rl_hip_kv_append(append) byte for byte: the
  * append runs inside the attention's merge kernel, after every context has
  * been read, so the step takes one launch less. append->batch and kv_heads
- * must equal attn's. */
+ * must equal attn's. The attention reads through attn->block_table and the
+ * append writes through append->block_table: at a copy-on-write step the
+ * first still maps the shared source block, the second the private one. */
 int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append);
 
 /* ---- fused decode step that allocates nothing ------------------------------

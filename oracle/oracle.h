@@ -68,6 +68,15 @@ int orc_kvb_alloc(uint8_t *t, uint32_t rollout, uint32_t prefix, int64_t delta, 
                   uint32_t dblocks, uint32_t *out_id);
 int orc_kvb_free(uint8_t *t, uint32_t id);
 int64_t orc_kvb_total_offset(const uint8_t *t, uint32_t id);
+/* cu/kv_prefix.cu:4-23 (device kv_branch_resolve): like total_offset, but a
+ * prefix whose refcnt is 0 also yields the branch's delta offset. */
+int64_t orc_kvb_resolve(const uint8_t *t, uint32_t id);
+/* The copy-on-write source of one (row, kv head): the prefix block whose
+ * filled slots [0, token_len % tpb) the row's first own token (position ==
+ * token_len) must find in its private block, or -1. Prefix blocks are
+ * head-major from kv_block_offset, kv_block_count / kv_heads per head. */
+int64_t orc_kvb_cow_source(const uint8_t *t, uint32_t branch, uint32_t position, uint32_t tpb,
+                           uint32_t kv_heads, uint32_t head);
 
 /* ---- reward (src/reward.c:36-41, cu/reward.cu:11) and group advantage ---- */
 float orc_reward_score(uint32_t count);

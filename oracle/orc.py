@@ -59,6 +59,7 @@ def load_oracle() -> C.CDLL:
         "orc_kvp_acquire": (i32, [vp, u32]), "orc_kvp_release": (i32, [vp, u32]),
         "orc_kvb_alloc": (i32, [vp, u32, u32, i64, u32, u32, C.POINTER(u32)]),
         "orc_kvb_free": (i32, [vp, u32]), "orc_kvb_total_offset": (i64, [vp, u32]),
+        "orc_kvb_resolve": (i64, [vp, u32]), "orc_kvb_cow_source": (i64, [vp, u32, u32, u32, u32, u32]),
         "orc_reward_score": (C.c_float, [u32]), "orc_match_count": (u32, [vp, vp, u32]),
         "orc_group_advantage": (None, [vp, u32, u32, vp]),
         "orc_philox4x32_10": (None, [vp, vp, vp]),

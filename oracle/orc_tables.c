@@ -166,6 +166,35 @@ orc_kvb_total_offset(const uint8_t *t, uint32_t id)
     return g64(t, P_BASE(prefix) + 8);
 }
 
+/* cu/kv_prefix.cu:4-15 */
+int64_t
+orc_kvb_resolve(const uint8_t *t, uint32_t id)
+{
+    if (id >= N_BRANCH)
+        return -1;
+    const uint32_t prefix = g32(t, B_BASE(id) + 8);
+    if (prefix >= N_PREFIX || g32(t, P_BASE(prefix) + 4) == 0)
+        return g64(t, B_BASE(id) + 12);
+    return g64(t, P_BASE(prefix) + 8);
+}
+
+int64_t
+orc_kvb_cow_source(const uint8_t *t, uint32_t branch, uint32_t position, uint32_t tpb, uint32_t kv_heads,
+                   uint32_t head)
+{
+    if (branch >= N_BRANCH)
+        return -1;
+    const uint32_t prefix = g32(t, B_BASE(branch) + 8);
+    if (prefix >= N_PREFIX || g32(t, P_BASE(prefix) + 4) == 0)
+        return -1;
+    const int64_t off = g64(t, P_BASE(prefix) + 8);
+    const uint32_t len = g32(t, P_BASE(prefix) + 16);
+    const uint32_t per_head = g32(t, P_BASE(prefix) + 20) / kv_heads;
+    if (len % tpb == 0 || position != len || len / tpb >= per_head || off < 0)
+        return -1;
+    return off + (int64_t)head * per_head + len / tpb;
+}
+
 /* src/reward.c:36-41 and cu/reward.cu:11 */
 float
 orc_reward_score(uint32_t count)

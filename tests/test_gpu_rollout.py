@@ -20,6 +20,11 @@ Checked:
     the device logits (the "given identical logits" contract), attention rows
     within 1e-4 of fp64 over the arena as it stands, and projection rows within
     the fp32 summation bound of an fp64 GEMM;
+  * at every step that admitted requests: every row's token against the host
+    sampler on the device logits;
+  * the whole arena at the end byte-equal to the oracle's appends replayed
+    step by step (each step's append positions, the request each slot held,
+    and that step's K/V pool rows), copy-on-write included;
   * kv_prefix refcounts: 9 while the 8 branches live, 1 after they are freed.
 """
 import ctypes as C
@@ -37,7 +42,74 @@ pytestmark = pytest.mark.gpu
 CHECK_STEPS = (0, 137, 306)
 
 
-def _check_step(rl, orc, olib, cfg, dev, t):
+def _check_tokens(olib, dev, t):
+    """Every row's token of step t against the host sampler on the device logits."""
+    logits = dev["logits"].download(np.float32, (SLOTS, VOCAB))
+    tok = dev["tok"].download(np.uint32, SLOTS)
+    temp = dev["temp"].download(np.float32, SLOTS)
+    topk = dev["topk"].download(np.uint32, SLOTS)
+    topp = dev["topp"].download(np.float32, SLOTS)
+    seed = dev["seed"].download(np.uint64, SLOTS)
+    step = dev["step"].download(np.uint64, SLOTS)
+    lp = C.c_double()
+    for r in range(SLOTS):
+        want = olib.orc_sample_row(logits[r].ctypes.data, VOCAB, int(not temp[r] > 0), float(temp[r]), int(topk[r]),
+                                   float(topp[r]), int(seed[r]), int(step[r]), r, C.byref(lp))
+        assert tok[r] == want, (t, r, tok[r], want)
+
+
+class _Recorder:
+    """on_check hook of RolloutLoop.run: after every step, the append positions
+    and the slot -> request map that step used; tokens checked at every step
+    that admitted requests, and the full check at `full_steps`."""
+
+    def __init__(self, rl, orc, olib, cfg, loop, full_steps, pick=None):
+        self.rl, self.orc, self.olib, self.cfg, self.loop = rl, orc, olib, cfg, loop
+        self.full_steps, self.pick = full_steps, pick
+        self.records, self.admitted, self.token_checks = [], 0, []
+
+    def __call__(self, t):
+        dev = self.loop.dev
+        pos, sreq = dev["pos"].download(np.uint32, SLOTS), dev["sreq"].download(np.uint32, SLOTS)
+        self.records.append((t, pos, sreq))
+        adm = int(dev["counters"].download(np.uint32, 4)[1])
+        if t in self.full_steps:
+            _check_step(self.rl, self.orc, self.olib, self.cfg, dev, t, self.pick(sreq) if self.pick else None)
+        elif adm != self.admitted:
+            _check_tokens(self.olib, dev, t)
+            self.token_checks.append(t)
+        self.admitted = adm
+
+
+def _replay_arena(olib, cfg, loop, records):
+    """The arena after the oracle's appends of every recorded step (copy-on-write
+    sources from the oracle's resolve of each slot's branch)."""
+    arena = cfg["arena"].copy()
+    stride, prefix = cfg["stride"], cfg["prefix"]
+    block = 2 * TPB * D * 2
+    cows = 0
+    for t, pos, sreq in records:
+        act = np.nonzero(pos != 0xFFFFFFFF)[0]
+        if len(act) == 0:
+            continue
+        req = sreq[act]
+        assert (req < REQ).all(), t
+        p = np.ascontiguousarray(pos[act])
+        tables = np.ascontiguousarray(cfg["table"][req])
+        cow = np.full((len(act), KVH), -1, np.int32)
+        for i in np.nonzero(p == prefix)[0]:   # the only position a copy-on-write source can have
+            for h in range(KVH):
+                cow[i, h] = olib.orc_kvb_cow_source(loop.ptab.ctypes.data, int(loop.branch[req[i]]), int(p[i]),
+                                                    TPB, KVH, h)
+            cows += int((cow[i] >= 0).all())
+        kn = np.ascontiguousarray(cfg["kpool"][t % POOL][act])
+        vn = np.ascontiguousarray(cfg["vpool"][t % POOL][act])
+        olib.orc_kv_append(arena.ctypes.data, block, TPB, D * 2, tables.ctypes.data, stride, len(act), KVH,
+                           p.ctypes.data, cow.ctypes.data, kn.ctypes.data, vn.ctypes.data)
+    return arena, cows
+
+
+def _check_step(rl, orc, olib, cfg, dev, t, pick=None):
     """Tokens, attention and projection of step t against the host."""
     logits = dev["logits"].download(np.float32, (SLOTS, VOCAB))
     tok = dev["tok"].download(np.uint32, SLOTS)
@@ -59,7 +131,8 @@ def _check_step(rl, orc, olib, cfg, dev, t):
     out32 = dev["out32"].download(np.float32, (SLOTS, QH, D))
     arena = dev["arena"].download(np.uint8, cfg["arena"].size)
     stab = dev["stab"].download(np.uint32, (SLOTS, KVH, cfg["stride"]))
-    pick = active[[0, len(active) // 2]]
+    if pick is None:
+        pick = active[[0, len(active) // 2]]
     wl = synth.DecodeWorkload(len(pick), QH, KVH, D, "bf16", TPB, ctx[pick].copy(), stab[pick].copy(), arena,
                               cfg["qpool"][t % POOL][pick].copy(), 0)
     ref = orc.attn_f64(olib, wl, 0)
@@ -83,32 +156,24 @@ def test_grpo_rollout_loop(rl, gpu, orc, olib):
     print(f"[rollout] inputs built in {time.perf_counter() - t0:.1f}s (arena {cfg['arena'].nbytes / 1e9:.2f} GB)",
           flush=True)
 
-    # kv_prefix bookkeeping of the shared prompts (host, src/kv_prefix.c rules)
-    ptab = (C.c_uint8 * grpo.PREFIX_TABLE_BYTES)()
-    L.kv_prefix_table_init(ptab)
-    pid, bid = C.c_uint32(), C.c_uint32()
-    branch_ids = []
-    for g in range(GROUPS):
-        assert L.kv_prefix_register(ptab, int(cfg["prefix_blocks"][g, 0, 0]) * 8192, PREFIX, PREFIX // TPB,
-                                    C.byref(pid)) == 0
-        assert pid.value == g
-        for m in range(GS):
-            r = g * GS + m
-            assert L.kv_branch_alloc(ptab, r, g, int(cfg["table"][r, 0, PREFIX // TPB]) * 8192,
-                                     int(cfg["priv"][r]), int(cfg["n_blocks"][r]) - PREFIX // TPB, C.byref(bid)) == 0
-            branch_ids.append(bid.value)
-    assert all(L.kv_prefix_get(ptab, g).contents.refcnt == GS + 1 for g in range(GROUPS))
-
     loop = grpo.RolloutLoop(cfg)
     dev = loop.dev
+    # kv_prefix bookkeeping of the shared prompts (host, src/kv_prefix.c rules)
+    ptab = loop.ptab.ctypes.data
+    branch_ids = [int(b) for b in loop.branch]
+    assert all(L.kv_prefix_get(ptab, g).contents.refcnt == GS + 1 for g in range(GROUPS))
     assert L.rl_hip_is_coherent_host(loop.rr) and L.rl_hip_is_coherent_host(loop.dr)
     loop.submit_requests()
     print("[rollout] running the loop", flush=True)
-    res = loop.run(check_steps=CHECK_STEPS, on_check=lambda t: _check_step(rl, orc, olib, cfg, dev, t))
+    rec = _Recorder(rl, orc, olib, cfg, loop, CHECK_STEPS)
+    res = loop.run(check_steps=range(10**6), on_check=rec)
     dones = loop.dones
-    print(f"[rollout] {res['steps']} steps in {res['wall_s']:.2f} s; steps 20-119 (256 active slots): "
-          f"{res['window_us_per_step']:.0f} us/step, {SLOTS / res['window_us_per_step'] * 1e6:.0f} tokens/s",
-          flush=True)
+    print(f"[rollout] tokens checked at admission steps {rec.token_checks}", flush=True)
+    want, cows = _replay_arena(olib, cfg, loop, rec.records)
+    assert cows == 0                                      # a 512-token prefix fills whole blocks
+    assert np.array_equal(dev["arena"].download(np.uint8, cfg["arena"].size), want)
+    print(f"[rollout] arena equals the oracle's replay of {len(rec.records)} steps of appends", flush=True)
+    print(f"[rollout] {res['steps']} steps in {res['wall_s']:.2f} s (synchronised after every step)", flush=True)
 
     counters = dev["counters"].download(np.uint32, 4)
     assert counters.tolist() == [REQ, REQ, 1, 0], counters
@@ -170,8 +235,12 @@ def test_grpo_loop_fed_by_the_rollout_pipeline(rl, gpu, orc, olib):
     f = loop.feeder
     assert (f.stats.registered, f.stats.admitted, f.stats.sent) == (REQ, 384, 384)
     print("[rollout] running the pipeline-fed loop", flush=True)
-    res = loop.run(check_steps=(0, 300), on_check=lambda t: _check_step(rl, orc, olib, cfg, dev, t))
-    print(f"[rollout] pipeline-fed: {res['steps']} steps in {res['wall_s']:.2f} s", flush=True)
+    rec = _Recorder(rl, orc, olib, cfg, loop, (0, 300))
+    res = loop.run(check_steps=range(10**6), on_check=rec)
+    print(f"[rollout] pipeline-fed: {res['steps']} steps in {res['wall_s']:.2f} s; tokens checked at admission "
+          f"steps {rec.token_checks}", flush=True)
+    want, _ = _replay_arena(olib, cfg, loop, rec.records)
+    assert np.array_equal(dev["arena"].download(np.uint8, cfg["arena"].size), want)
     assert (f.stats.admitted, f.stats.sent, f.stats.retired, f.stats.reward_handoffs) == (REQ,) * 4
     assert f.stats.bad_dones == 0 and f.end_sent == 1
     assert dev["counters"].download(np.uint32, 4).tolist() == [REQ, REQ, 1, 0]
@@ -190,4 +259,44 @@ def test_grpo_loop_fed_by_the_rollout_pipeline(rl, gpu, orc, olib):
     assert np.all(loop.pipe[rl.PIPELINE_SLAB_OFF + 48 * 8192:rl.PIPELINE_SLAB_OFF + 48 * 8192 + 1024] == 0xFF)
     assert np.all(loop.rid_map == 0xFFFFFFFF)
     assert L.hw_ring_load_acquire(loop.rr) == REQ + 1 and L.hw_ring_load_acquire(loop.dr) == REQ
+    loop.close()
+
+
+def test_grpo_loop_copy_on_write_prefix(rl, gpu, orc, olib):
+    """The loop with a 520-token shared prefix: 32 full blocks per kv head are
+    shared, and the 33rd holds 8 prefix tokens. Every second request has no
+    private prompt tokens, so its first generated token lands in that block:
+    before its first step rl_hip_kv_cow resolves the slot's branch on the
+    device prefix table and copies the 8 prefix slots into the request's
+    private block, which the step's attention then reads. Checked: 256
+    copy-on-writes happen, the attention at step 0 of two such slots is within
+    1e-4 of fp64 over the copied block, every token at admission steps, every
+    request done once with the reference reward rule, and the final arena
+    byte-equal to the oracle's replay of every step's copy-on-write and append."""
+    L = rl.lib()
+    cfg = grpo.build_workload(406, prefix=520, priv_zero_every=2)
+    loop = grpo.RolloutLoop(cfg)
+    dev = loop.dev
+    assert loop.cow is not None
+    loop.submit_requests()
+    zero = set(int(r) for r in np.nonzero(cfg["priv"] == 0)[0])
+    pick = lambda sreq: np.array([s for s in range(SLOTS) if int(sreq[s]) in zero][:2])
+    rec = _Recorder(rl, orc, olib, cfg, loop, (0, 291), pick=pick)
+    print("[rollout] running the copy-on-write loop (prefix 520)", flush=True)
+    res = loop.run(check_steps=range(10**6), on_check=rec)
+    print(f"[rollout] cow loop: {res['steps']} steps; tokens checked at admission steps {rec.token_checks}",
+          flush=True)
+    assert dev["counters"].download(np.uint32, 4).tolist() == [REQ, REQ, 1, 0]
+    dones = loop.dones
+    assert sorted(d[0] for d in dones) == list(range(REQ)) and all(d[2] == GEN and d[4] == 0 for d in dones)
+    gen = dev["gen"].download(np.uint32, (REQ, GEN))
+    for rid, _, _, reward, _ in dones:
+        tgt = np.ascontiguousarray(cfg["targets"][rid // GS])
+        row = np.ascontiguousarray(gen[rid])
+        want = np.float32(L.reward_match_count(row.ctypes.data, tgt.ctypes.data, GEN) & 0xFF) / np.float32(255.0)
+        assert np.float32(reward) == want, rid
+    want, cows = _replay_arena(olib, cfg, loop, rec.records)
+    assert cows == len(zero) == REQ // 2, (cows, len(zero))
+    assert np.array_equal(dev["arena"].download(np.uint8, cfg["arena"].size), want)
+    print(f"[rollout] {cows} copy-on-writes; arena equals the oracle's replay", flush=True)
     loop.close()

@@ -354,3 +354,33 @@ def test_sampling_all_masked_row(olib):
     for k, p in ((0, 1.0), (0, 0.9), (3, 0.3), (50, 1.0)):
         assert olib.orc_sample_row(x.ctypes.data, 300, 0, 0.7, k, p, 9, 2, 2, C.byref(lp)) == 0
         assert math.isnan(lp.value)
+
+
+def test_branch_resolve_oracle_known_cases(olib):
+    """The device resolve rule (cu/kv_prefix.cu:4-15) on hand-built tables:
+    a live prefix gives its offset; a released prefix (refcount 0) gives the
+    branch's delta, where the host total_offset gives the -1 that release
+    stored; a prefix id past 512 gives the delta; a branch id past 16,384
+    gives -1. The copy-on-write source follows the head-major prefix layout."""
+    t = np.zeros(606280, np.uint8)
+    olib.orc_kvp_init(t.ctypes.data)
+    pid, bid = C.c_uint32(), C.c_uint32()
+    assert olib.orc_kvp_register(t.ctypes.data, 4096, 520, 8 * 33, C.byref(pid)) == 0 and pid.value == 0
+    assert olib.orc_kvb_alloc(t.ctypes.data, 7, 0, 90000, 3, 1, C.byref(bid)) == 0 and bid.value == 0
+    assert olib.orc_kvb_resolve(t.ctypes.data, 0) == 4096
+    assert olib.orc_kvb_total_offset(t.ctypes.data, 0) == 4096
+    # token_len 520 = 32 full blocks + 8 slots: block 32 of head h is 4096 + 33 h + 32
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 520, 16, 8, 0) == 4096 + 32
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 520, 16, 8, 5) == 4096 + 5 * 33 + 32
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 521, 16, 8, 5) == -1      # not the first own token
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 520, 8, 8, 0) == -1       # 520 = 65 whole 8-token blocks
+    # a branch whose prefix id is out of range: the delta
+    assert olib.orc_kvb_alloc(t.ctypes.data, 8, 600, 123456, 3, 1, C.byref(bid)) == 0 and bid.value == 1
+    assert olib.orc_kvb_resolve(t.ctypes.data, 1) == 123456
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 1, 520, 16, 8, 0) == -1
+    # release the prefix to refcount 0 (branch 0 holds one reference, register the other)
+    assert olib.orc_kvp_release(t.ctypes.data, 0) == 0 and olib.orc_kvp_release(t.ctypes.data, 0) == 0
+    assert olib.orc_kvb_total_offset(t.ctypes.data, 0) == -1
+    assert olib.orc_kvb_resolve(t.ctypes.data, 0) == 90000
+    assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 520, 16, 8, 0) == -1
+    assert olib.orc_kvb_resolve(t.ctypes.data, 16384) == -1
