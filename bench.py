@@ -77,7 +77,13 @@ class Step:
         log(f"[bench] inputs generated in {time.time() - t0:.1f}s (arena {self.w.arena.nbytes / 1e6:.0f} MB)")
         w = self.w
         self.layout = rlrt.KvLayoutDesc.paged(TPB, D)
-        self.arena = rlrt.DeviceBuffer.from_array(w.arena)
+        # the KV arena through arena.h (HBM base from arena_init); the
+        # workload's permuted block ids are the ids arena_acquire hands out
+        n_blocks = w.arena.nbytes // w.block_bytes
+        self.arena = rlrt.Arena(w.arena.nbytes, w.block_bytes)
+        if not np.array_equal(self.arena.acquire_n(n_blocks), np.arange(n_blocks)):
+            raise rlrt.RlrtError("arena_acquire did not hand out the lowest free blocks in order")
+        self.arena.upload(w.arena)
         self.table = rlrt.DeviceBuffer.from_array(w.table)
         self.ctx = rlrt.DeviceBuffer.from_array(w.ctx)
         self.q = rlrt.DeviceBuffer.from_array(w.q)

@@ -162,7 +162,17 @@ class RolloutLoop:
         L = rlrt.lib()
         self.cfg = cfg
         self.dev = dev = {}
-        for k in ("arena", "w", "qpool", "kpool", "vpool", "prompt", "targets"):
+        # the KV arena through arena.h: HBM base from arena_init, one arena_acquire
+        # per block (lowest id first, so the workload's block ids are arena ids)
+        block_bytes = 2 * TPB * D * 2
+        n_blocks = cfg["arena"].nbytes // block_bytes
+        arena = rlrt.Arena(n_blocks * block_bytes, block_bytes)
+        ids = arena.acquire_n(n_blocks)
+        if not np.array_equal(ids, np.arange(n_blocks)):
+            raise rlrt.RlrtError("arena_acquire did not hand out the lowest free blocks in order")
+        arena.upload(cfg["arena"])
+        dev["arena"] = arena
+        for k in ("w", "qpool", "kpool", "vpool", "prompt", "targets"):
             dev[k] = rlrt.DeviceBuffer.from_array(cfg[k])
         dev["rtab"] = rlrt.DeviceBuffer.from_array(cfg["table"])
         stride = self.stride = cfg["stride"]

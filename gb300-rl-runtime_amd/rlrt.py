@@ -264,6 +264,20 @@ class HwWorkerArgs(C.Structure):
                 ("stats", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
 
 
+class RingStepArgs(C.Structure):
+    _fields_ = [("cmdq", C.c_void_p), ("doneq", C.c_void_p), ("stop", C.c_void_p), ("max_idle_polls", C.c_uint64),
+                ("batch", C.c_uint32), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
+                ("layout", KvLayoutDesc), ("block_table", C.c_void_p), ("table_stride", C.c_uint32),
+                ("rollouts", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32), ("dtype", C.c_uint32),
+                ("scale", C.c_float), ("max_ctx", C.c_uint32), ("input_slots", C.c_uint32), ("q", C.c_void_p),
+                ("k_new", C.c_void_p), ("v_new", C.c_void_p), ("logits", C.c_void_p), ("vocab", C.c_uint32),
+                ("greedy", C.c_uint32), ("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("seeds", C.c_void_p), ("output_slots", C.c_uint32), ("attn_out", C.c_void_p),
+                ("attn_out_f32", C.c_void_p), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
+                ("row_rollout_out", C.c_void_p), ("stats", C.c_void_p), ("workspace", C.c_void_p),
+                ("workspace_bytes", C.c_size_t)]
+
+
 class CmdWorkerArgs(C.Structure):
     _fields_ = [("rings", C.c_void_p), ("comp_rings", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
                 ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
@@ -308,6 +322,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_hw_worker_workspace": (sz, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_hw_worker_launch": (i32, [C.POINTER(HwWorkerArgs)]),
         "rl_hip_cmd_worker_launch": (i32, [C.POINTER(CmdWorkerArgs)]),
+        "rl_hip_ring_step_workspace": (sz, [C.POINTER(RingStepArgs)]),
+        "rl_hip_ring_step_enqueue": (i32, [C.POINTER(RingStepArgs), u32, u64]),
         # reference host API
         "hw_ring_create": (vp, []), "hw_ring_reset": (None, [vp]), "hw_ring_destroy": (None, [vp]),
         "hw_ring_load_acquire": (u32, [vp]), "hw_ring_store_release": (None, [vp, u32]),
@@ -441,6 +457,43 @@ class DeviceBuffer:
             self.close()
         except Exception:
             pass
+
+
+KV_ARENA_BYTES = 131096  # sizeof(KVArena)
+
+
+class Arena(DeviceBuffer):
+    """The byte-compatible KVArena (arena.h) after rl_hip_open: arena_init
+    takes its base from HBM (zero-filled), arena_acquire hands out block ids
+    lowest-first from the host bitmap, arena_destroy frees the HBM. ptr / nbytes
+    are base / capacity, so the arena passes wherever a DeviceBuffer does."""
+
+    def __init__(self, capacity: int, block_size: int):
+        L = lib()
+        self.struct = np.zeros(KV_ARENA_BYTES, np.uint8)
+        self.nbytes = int(capacity)
+        L.arena_init(self.struct.ctypes.data, self.nbytes, int(block_size))
+        head = KVArenaHead.from_address(self.struct.ctypes.data)
+        self.ptr, self.block_size = head.base, int(block_size)
+        if not L.arena_is_device(self.struct.ctypes.data):
+            raise RlrtError("arena_init did not place the arena in device memory (no device open?)")
+
+    def acquire(self) -> int:
+        return int(lib().arena_acquire(self.struct.ctypes.data))
+
+    def acquire_n(self, n: int) -> np.ndarray:
+        ids = np.array([self.acquire() for _ in range(n)], np.int64)
+        if (ids < 0).any():
+            raise RlrtError(f"arena exhausted after {int((ids >= 0).sum())} of {n} blocks")
+        return ids
+
+    def release(self, idx: int) -> None:
+        lib().arena_release(self.struct.ctypes.data, int(idx))
+
+    def close(self) -> None:
+        if self.ptr:
+            lib().arena_destroy(self.struct.ctypes.data)
+            self.ptr = None
 
 
 def open_device(device: int = 0) -> DeviceInfo:
