@@ -279,6 +279,77 @@ typedef struct {
 size_t rl_hip_hw_worker_workspace(const rl_hw_worker_args_t *args);
 int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
 
+/* ---- the batched decode step driven through the hw_desc rings ---------------
+ * Replaces the one-descriptor-per-SM device worker (cu/worker.cu:66-131) and
+ * applies the hw_worker_sim rule (src/hw_worker_sim.c:23-59) token by token,
+ * with up to `batch` DECODE descriptors sharing one decode step that spans
+ * every compute unit. rl_hip_ring_step_enqueue queues `steps` steps on the
+ * library stream and returns at once; each step:
+ *  - takes descriptors from cmdq into free rows (lowest row first, ring
+ *    order), waiting (bounded by max_idle_polls) only while no row is active:
+ *    DECODE with seq_len < max_tokens decodes; DECODE with seq_len >=
+ *    max_tokens passes through unchanged; STOP, the host *stop flag, an idle
+ *    limit or a rollout_id >= rollouts end admission (stats status 4, 4, 1, 2)
+ *    while active rows finish; other opcodes are dropped;
+ *  - decodes one token for every active row: paged GQA attention of rollout
+ *    rollout_id over its seq_len cached tokens (block_table rows rollout *
+ *    kv_heads + h) with the K/V token appended at position seq_len
+ *    (rl_hip_decode_step), and sampling (rl_hip_sample: greedy, or
+ *    temperature / top_k / top_p with Philox key seeds[rollout] and counter
+ *    seq_len);
+ *  - applies the rule for that token (seq_len++; DONE at max_tokens;
+ *    NEEDS_REWARD at a multiple of 32; otherwise the row decodes again next
+ *    step) and pushes finished descriptors to doneq in row order (bounded
+ *    wait for room; status 3 if it never comes).
+ * Step k (counting from first_step) reads input slot k % input_slots and
+ * writes output slot k % output_slots; row i of a slot belongs to whatever
+ * descriptor holds row i in that step, which row_rollout_out records
+ * (UINT32_MAX for a row that did not decode). The workspace (from
+ * rl_hip_ring_step_workspace) holds the row table and the pipeline's ring
+ * indexes across calls: zero it before the first enqueue of a run. stats =
+ * {tokens decoded, completions pushed, steps with work, status}. */
+typedef struct {
+    hw_ring_t *cmdq;             /* coherent host (hw_ring_create after rl_hip_open) */
+    hw_ring_t *doneq;            /* coherent host */
+    const volatile uint32_t *stop; /* coherent host */
+    uint64_t max_idle_polls;     /* 0 selects 2^22 */
+    uint32_t batch;              /* rows per step, 1..1024 */
+    void *arena_base;            /* device: KVArena.base */
+    uint64_t arena_bytes;
+    KvLayoutDesc layout;
+    const uint32_t *block_table; /* device [rollouts][kv_heads][table_stride] */
+    uint32_t table_stride;
+    uint32_t rollouts;
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t dtype;              /* RL_DTYPE_* of q, K, V and attn_out */
+    float scale;                 /* 0 selects 1/sqrt(head_dim) */
+    uint32_t max_ctx;            /* upper bound of every seq_len */
+    uint32_t input_slots;
+    const void *q;               /* device [input_slots][batch][q_heads][head_dim] */
+    const void *k_new;           /* device [input_slots][batch][kv_heads][head_dim] */
+    const void *v_new;
+    const float *logits;         /* device [input_slots][batch][vocab] */
+    uint32_t vocab;              /* multiple of 4 */
+    uint32_t greedy;
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    const uint64_t *seeds;       /* device [rollouts] or NULL: the rollout id is the seed */
+    uint32_t output_slots;
+    void *attn_out;              /* device [output_slots][batch][q_heads][head_dim] */
+    float *attn_out_f32;         /* device, optional, same shape */
+    uint32_t *token_out;         /* device [output_slots][batch] */
+    float *logprob_out;          /* device [output_slots][batch] */
+    uint32_t *row_rollout_out;   /* device [output_slots][batch] or NULL */
+    uint64_t *stats;             /* device [4] */
+    void *workspace;             /* device, >= rl_hip_ring_step_workspace(), zeroed before the first enqueue */
+    size_t workspace_bytes;
+} rl_ring_step_args_t;
+
+size_t rl_hip_ring_step_workspace(const rl_ring_step_args_t *args);
+int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *args, uint32_t steps, uint64_t first_step);
+
 /* ---- persistent worker on the v0.2 command / completion rings ---------------
  * Replaces decode_worker and process_descriptor (cu/worker.cu:25-131): one
  * persistent workgroup per (CommandRing, CompletionRing) pair - the single
