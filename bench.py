@@ -198,32 +198,77 @@ def cpu_baseline(step, budget_s):
         olib.orc_kv_append(arena.ctypes.data, w.block_bytes, TPB, D * 2, w.table.ctypes.data, w.table_stride, B, KVH,
                            w.ctx.ctypes.data, None, knew.ctypes.data, vnew.ctypes.data)
 
-    one(0)
-    times = []
-    t_start = time.perf_counter()
-    i = 1
-    while (time.perf_counter() - t_start < budget_s or len(times) < 3) and len(times) < 200:
-        t0 = time.perf_counter()
-        one(i)
-        times.append(time.perf_counter() - t0)
-        i += 1
+    threads = int(olib.orc_num_threads())
+
+    def timed(n_warm, n_min, budget, cap):
+        for i in range(n_warm):
+            one(i)
+        times = []
+        t_start = time.perf_counter()
+        i = n_warm
+        while (time.perf_counter() - t_start < budget or len(times) < n_min) and len(times) < cap:
+            t0 = time.perf_counter()
+            one(i)
+            times.append(time.perf_counter() - t0)
+            i += 1
+        return times
+
+    times = timed(2, 10, budget_s, 200)
     med = float(np.median(times))
-    return {"value": B / med, "unit": "tokens/s", "cores": int(olib.orc_num_threads()), "kind": "port",
+    # the same step on one thread: 2 warm-ups, median of 5
+    olib.orc_set_num_threads(1)
+    t1 = timed(2, 5, 0.0, 5)
+    olib.orc_set_num_threads(threads)
+    med1 = float(np.median(t1))
+    return {"value": B / med, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"the full 64-rollout step (fp32 online-softmax attention over the same arena, sampling "
                       f"of the same 64 x {VOCAB} logits, KV append), median of {len(times)} steps "
-                      f"({sum(times):.1f} s of CPU work) after one warm-up, OpenMP over rollout x kv-head / rows",
+                      f"({sum(times):.1f} s of CPU work) after 2 warm-ups, OpenMP over rollout x kv-head / rows "
+                      f"on {threads} threads; one thread: median of {len(t1)} after 2 warm-ups",
             "steps_per_s": 1.0 / med, "ms_per_step": med * 1e3,
-            "cpu_model": _cpu_model()}
+            "one_thread": {"value": B / med1, "ms_per_step": med1 * 1e3},
+            **_host_info(threads)}
 
 
 def _cpu_model():
+    """The CPU model as lscpu and /proc/cpuinfo print it (family / model numbers too)."""
+    import subprocess
+
+    name, fam, mod = None, None, None
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() == "Model name" and v.strip():
+                name = v.strip()
+    except Exception:
+        pass
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k == "model name" and not name:
+                name = v.strip()
+            elif k == "cpu family" and fam is None:
+                fam = v.strip()
+            elif k == "model" and mod is None:
+                mod = v.strip()
     except OSError:
         pass
-    return "unknown"
+    return f"{name or 'unknown'} (family {fam}, model {mod})"
+
+
+def _host_info(threads):
+    """nproc, OpenMP threads, CPU model and NUMA nodes of this host."""
+    import glob
+
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except OSError:
+        nproc = os.cpu_count()
+    return {"nproc": nproc, "omp_threads": threads, "cpu_model": _cpu_model(),
+            "numa_nodes": len(glob.glob("/sys/devices/system/node/node[0-9]*")) or 1,
+            "omp_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")}}
 
 
 # ---------------------------------------------------------------- HBM traffic (rocprofv3 counters)
@@ -472,12 +517,218 @@ def wl_plumbing(args):
     L.hw_ring_destroy(dq)
     for p in (rings, stop, doorbell):
         L.rl_hip_host_free(p)
+    cpu = None
+    if not args.no_cpu:
+        cpu = _plumbing_cpu(w, q, kv, logits, steps, ctx0, vocab)
     return {"workload": "plumbing_mha8_d64_fp16_ctx256_v32000_100steps",
-            "pipelined_steps_per_s": steps / pipelined, "pipelined_ms": pipelined * 1e3,
+            "pipelined_steps_per_s": steps / pipelined, "pipelined_ms": pipelined * 1e3, "cpu_baseline": cpu,
             "lockstep_latency_us": {"p50": float(np.percentile(lat_us, 50)), "p90": float(np.percentile(lat_us, 90)),
                                     "p99": float(np.percentile(lat_us, 99)), "mean": float(lat_us.mean())},
             "lockstep_steps_per_s": 1e6 / float(lat_us.mean()), "worker_stats": st.tolist(),
             "note": "host side polls the completion ring from Python (ctypes)"}
+
+
+def _plumbing_cpu(w, q, kv, logits, steps, ctx0, vocab):
+    """The CPU path of the plumbing decode: the hw_worker_sim loop on a pthread
+    with a real decode step per token (the oracle's fp32 attention, greedy,
+    KV append), fed through ring images, on the same inputs: 100 descriptors
+    back to back, then 100 one at a time."""
+    import ctypes as C
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import orc
+
+    olib = orc.load_oracle()
+    arena = w.arena.copy()
+    out = np.zeros((2 * steps, 8, 64), np.float32)
+    tok = np.zeros(2 * steps, np.uint32)
+    p = orc.OrcPlumbing(arena=arena.ctypes.data, block_bytes=w.block_bytes, token_count=16, head_dim=64, dtype=1,
+                        table=w.table.ctypes.data, table_stride=w.table_stride, q_heads=8, kv_heads=8,
+                        scale=1.0 / 8.0, q=q.ctypes.data, k_new=kv.ctypes.data, v_new=kv.ctypes.data,
+                        logits=logits.ctypes.data, vocab=vocab, steps=2 * steps, attn_out=out.ctypes.data,
+                        tokens=tok.ctypes.data)
+    pipe = C.c_double()
+    lat = np.zeros(steps, np.float64)
+    if olib.orc_plumbing_run(C.byref(p), ctx0, steps, C.byref(pipe), lat.ctypes.data) != 0:
+        return None
+    threads = int(olib.orc_num_threads())
+    lat_us = lat * 1e6
+    return {"value": steps / pipe.value, "unit": "steps/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} descriptors pipelined then {steps} lock-step through hw_desc ring images: the "
+                      f"hw_worker_sim loop on a pthread, per token fp32 attention (OpenMP over the 8 heads), "
+                      f"greedy over {vocab} logits and the KV append",
+            "lockstep_latency_us": {"p50": float(np.percentile(lat_us, 50)), "p99": float(np.percentile(lat_us, 99))},
+            **_host_info(threads)}
+
+
+def wl_plumbing256(args):
+    """One persistent hw_desc worker per compute unit, each with its own ring
+    pair and rollout (MHA 8 heads x d64 fp16 K/V ~N(0, 0.5^2), 16-token
+    blocks, KV length 256 at the start, greedy over 32,000 fp32 logits).
+    Pipelined: 32 one-token descriptors per ring queued through
+    infer_submit_decode before the launch, then STOP; the kernel's duration
+    (HIP events) over all 256 x 32 steps is the aggregate rate. Lock-step:
+    one descriptor per ring per round, the round ends when every ring has its
+    completion (Python polls the 256 completion rings)."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    info = rlrt.DeviceInfo()
+    rlrt.check(L.rl_hip_device_info(C.byref(info)), "rl_hip_device_info")
+    G, S, R, ctx0, vocab = int(info.cu_count), 32, 20, 256, 32000
+    rng = np.random.default_rng(1010)
+    n_steps = S + R
+    w = synth.make_decode(1011, G, 8, 8, 64, ctx0, ctx0, dtype="fp16", kv_std=0.5, reserve_tokens=ctx0 + n_steps + 1)
+    q = synth.f32_to_f16(rng.standard_normal((G, n_steps, 8, 64), dtype=np.float32))
+    kv = synth.f32_to_f16(rng.standard_normal((G, n_steps, 8, 64), dtype=np.float32) * np.float32(0.5))
+    logits = rng.standard_normal((G, n_steps, vocab), dtype=np.float32) * np.float32(2.0)
+    bufs = {n: rlrt.DeviceBuffer.from_array(a) for n, a in
+            (("arena", w.arena), ("table", w.table), ("q", q), ("kv", kv), ("logits", logits))}
+    outs = [rlrt.DeviceBuffer(n, zero=True) for n in (G * n_steps * 8 * 64 * 4, G * n_steps * 4, G * n_steps * 4,
+                                                       G * 32)]
+
+    def coherent(n):
+        p = L.rl_hip_host_alloc_coherent(n)
+        if not p:
+            raise rlrt.RlrtError("coherent host allocation failed")
+        return p
+
+    cqs = [L.hw_ring_create() for _ in range(G)]
+    dqs = [L.hw_ring_create() for _ in range(G)]
+    rings, stop, bells = coherent(16 * G), coherent(64), coherent(64 * G)
+    for g in range(G):
+        C.cast(rings, C.POINTER(C.c_void_p))[g] = cqs[g]
+        C.cast(rings, C.POINTER(C.c_void_p))[G + g] = dqs[g]
+    ctxs = [rlrt.InferHwCtx(cmdq=cqs[g], doneq=dqs[g], doorbell=bells + 64 * g, gpu_group_id=g, kv_arena_id=0)
+            for g in range(G)]
+
+    def make_args():
+        return rlrt.HwWorkerArgs(cmdq=rings, doneq=rings + 8 * G, groups=G, stop=stop, max_idle_polls=1 << 24,
+                                 arena_base=bufs["arena"].ptr, arena_bytes=bufs["arena"].nbytes,
+                                 layout=rlrt.KvLayoutDesc.paged(16, 64), block_table=bufs["table"].ptr,
+                                 table_stride=w.table_stride, rollouts=G, q_heads=8, kv_heads=8,
+                                 dtype=rlrt.DTYPE_FP16, scale=0.0, max_steps=n_steps, q=bufs["q"].ptr,
+                                 k_new=bufs["kv"].ptr, v_new=bufs["kv"].ptr, logits=bufs["logits"].ptr, vocab=vocab,
+                                 attn_out=outs[0].ptr, token_out=outs[1].ptr, logprob_out=outs[2].ptr,
+                                 stats=outs[3].ptr)
+
+    # pipelined: everything queued first, the kernel runs until STOP
+    for i in range(S):
+        for g in range(G):
+            if L.infer_submit_decode(C.byref(ctxs[g]), g, 0, 0, 0, ctx0 + i, ctx0 + i + 1) != 0:
+                raise rlrt.RlrtError("submit failed")
+    for g in range(G):
+        rlrt.hw_ring_push(cqs[g], rlrt.HwDesc(opcode=255))
+    a = make_args()
+    ws = rlrt.hw_worker_workspace(a)
+    timer = rlrt.Timer()
+    rlrt.sync()
+    timer.begin()
+    rlrt.hw_worker_launch(a)
+    ms = timer.end()
+    st = outs[3].download(np.uint64, (G, 4))
+    if not (st[:, 1] == S).all():
+        raise rlrt.RlrtError(f"pipelined: completions per pair {np.unique(st[:, 1]).tolist()}")
+    for g in range(G):
+        while rlrt.hw_ring_pop(dqs[g]) is not None:
+            pass
+    # lock-step rounds on a fresh launch (each worker continues its rollout at step S)
+    for o in outs[3:]:
+        rlrt.check(L.rl_hip_memset_d(o.ptr, 0, o.nbytes), "memset")
+    a2 = make_args()  # a fresh launch counts its steps from 0 again: input rows are reused
+    a2.workspace, a2.workspace_bytes = a.workspace, a.workspace_bytes
+    rlrt.hw_worker_launch(a2)
+    rounds = []
+    try:
+        for i in range(S, S + R):
+            t1 = time.perf_counter()
+            for g in range(G):
+                if L.infer_submit_decode(C.byref(ctxs[g]), g, 0, 0, 0, ctx0 + i, ctx0 + i + 1) != 0:
+                    raise rlrt.RlrtError("submit failed")
+            pending = set(range(G))
+            deadline = t1 + 10
+            while pending:
+                for g in list(pending):
+                    if rlrt.hw_ring_pop(dqs[g]) is not None:
+                        pending.discard(g)
+                if time.perf_counter() > deadline:
+                    raise rlrt.RlrtError(f"lock-step round: {len(pending)} rings without a completion")
+            rounds.append(time.perf_counter() - t1)
+        for g in range(G):
+            rlrt.hw_ring_push(cqs[g], rlrt.HwDesc(opcode=255))
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rlrt.sync()
+    for b in list(bufs.values()) + outs + [ws]:
+        b.close()
+    for r in cqs + dqs:
+        L.hw_ring_destroy(r)
+    for p in (rings, stop, bells):
+        L.rl_hip_host_free(p)
+    r_us = np.array(rounds) * 1e6
+    return {"workload": f"plumbing_{G}pairs_mha8_d64_fp16_ctx256_v32000",
+            "pairs": G, "pipelined_steps": G * S, "pipelined_kernel_ms": ms,
+            "pipelined_steps_per_s": G * S / (ms * 1e-3),
+            "lockstep_round_us": {"p50": float(np.percentile(r_us, 50)), "p99": float(np.percentile(r_us, 99))},
+            "lockstep_steps_per_s": G / (float(np.median(r_us)) * 1e-6),
+            "note": "pipelined: rings filled before the launch, HIP events around the persistent kernel; lock-step: "
+                    "one descriptor per ring per round, submitted and polled from Python"}
+
+
+def wl_ringstep(args):
+    """The headline step (64 rollouts, GQA 32/8, d128, bf16 K/V, ctx
+    U[512,4096], sampling of 64 x 128,256 logits with T 0.8 / top-k 50 /
+    top-p 0.9, KV append) driven through the hw_desc rings
+    (rl_hip_ring_step_enqueue): per step 64 one-token descriptors drained by
+    the poll kernel, the batched step over every compute unit, 64 completions
+    published. The descriptors of every step are queued before the timed
+    region; logits rotate over 4 input slots. The launched step on the same
+    inputs is timed beside it."""
+    import ringstep
+
+    K, W = args.steps, args.warmup
+    if B * (K + W) > 65536:
+        raise SystemExit("ringstep: every step's descriptors and completions are queued up front; "
+                         f"{B} x (steps + warmup) must fit the 65,536-slot rings")
+    st = Step()
+    w = st.w
+    seeds = np.random.default_rng(33).integers(0, 2**63, B, dtype=np.uint64)
+    run = ringstep.RingStepRun(st.arena, st.layout, w.table, QH, MAX_CTX, B, VOCAB, input_slots=LOGIT_COPIES,
+                               output_slots=1, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
+    logits = synth.make_logits(SEED_LOGITS, B, VOCAB, spikes=SPIKES)
+    rng = np.random.default_rng(44)
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), np.float32))
+    for sl in range(LOGIT_COPIES):
+        run.set_inputs(sl, w.q, kn, vn, logits)
+    for _ in range(K + W):
+        for r in range(B):
+            run.submit_decode(r, int(w.ctx[r]), int(w.ctx[r]) + 1)
+    run.enqueue(W)
+    rlrt.sync()
+    timer = rlrt.Timer()
+    timer.begin()
+    run.enqueue(K)
+    ms = timer.end()
+    stats = run.stats()
+    n_comp = len(run.completions())
+    run.stop()
+    run.close()
+    if stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
+        raise rlrt.RlrtError(f"ring step stats {stats}, {n_comp} completions")
+    # the launched step on the same inputs
+    for i in range(W):
+        st.run(i)
+    lms, _ = time_loop(st, K, "step")
+    ring_us, launched_us = ms / K * 1e3, lms / K * 1e3
+    step_bytes = st.attn_bytes() + st.sample_bytes() + st.append_bytes()
+    return {"workload": "ringstep_b64_q32kv8_d128_ctx512-4096_v128256_t0.8_k50_p0.9",
+            "steps": K, "ring_step_us": ring_us, "ring_steps_per_s": 1e6 / ring_us,
+            "ring_tokens_per_s": B * 1e6 / ring_us, "ring_step_hbm_frac": step_bytes / (ring_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "launched_step_us": launched_us, "launched_tokens_per_s": B * 1e6 / launched_us,
+            "stats": stats,
+            "note": "per step: poll kernel (one wave, 64 descriptors over PCIe), gather kernel, fused attention + "
+                    "append, sampler, publish kernel (64 completions); HIP events on the library stream"}
 
 
 def wl_cmdring(args):
@@ -724,6 +975,7 @@ def wl_pipeline_trace(args):
 
 
 WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
+             "plumbing256": wl_plumbing256, "ringstep": wl_ringstep,
              "rollout": wl_rollout, "cmdring": wl_cmdring, "rollout_pipeline": wl_rollout_pipeline,
              "pipeline": wl_pipeline, "pipeline_trace": wl_pipeline_trace}
 

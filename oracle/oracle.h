@@ -29,6 +29,10 @@
 int orc_hw_ring_push(uint8_t *ring, const uint8_t desc[64]);
 int orc_hw_ring_pop(uint8_t *ring, uint8_t out[64]);
 
+/* The 64-byte descriptor infer_submit_decode builds (src/infer_submit.c:12-32). */
+void orc_decode_desc(uint8_t d[64], uint32_t gpu_group_id, uint32_t kv_arena_id, uint32_t rollout_id,
+                     uint64_t kv_offset, uint64_t delta_offset, uint32_t prefix_id, uint32_t seq_len,
+                     uint32_t max_tokens);
 /* infer_submit_decode (src/infer_submit.c:3-37): builds the 64-byte
  * descriptor, pushes it, returns the doorbell value (tail) or -1. */
 int64_t orc_submit_decode(uint8_t *cmdq, uint32_t gpu_group_id, uint32_t kv_arena_id,
@@ -107,6 +111,32 @@ void orc_attn_decode_f64(const orc_attn_t *a, double *out);
 void orc_attn_decode_f32(const orc_attn_t *a, float *out);
 /* decode_synth_query_component (cu/attention_decode.cu:16-28); rng_state may be NULL */
 float orc_synth_query(uint64_t seq_id, uint64_t reward_cookie, const uint64_t *rng_state, uint32_t idx);
+
+/* ---- the plumbing decode on the CPU (orc_plumbing.c): the hw_worker_sim
+ * loop (src/hw_worker_sim.c:23-59) on a pthread with a real decode step per
+ * token of one rollout (fp32 attention, greedy, KV append), fed through
+ * hw_ring images by the calling thread. Step k uses row k of q / k_new /
+ * v_new / logits and writes attn_out[k], tokens[k]. n descriptors (seq ctx0
+ * + i, max ctx0 + i + 1) go in back to back (*pipelined_s = until the last
+ * completion), then n more one at a time (lat_s[i] = submit to completion).
+ * Needs steps >= 2n. ---- */
+typedef struct {
+    const uint8_t *arena;          /* written by the appends */
+    uint64_t block_bytes;
+    uint32_t token_count, head_dim, dtype;
+    const uint32_t *table;         /* [kv_heads][table_stride] of the one rollout */
+    uint32_t table_stride, q_heads, kv_heads;
+    double scale;
+    const uint16_t *q;             /* [steps][q_heads][head_dim] */
+    const uint16_t *k_new, *v_new; /* [steps][kv_heads][head_dim] */
+    const float *logits;           /* [steps][vocab] */
+    uint32_t vocab, steps;
+    float *attn_out;               /* [steps][q_heads][head_dim] */
+    uint32_t *tokens;              /* [steps] */
+} orc_plumbing_t;
+int orc_plumbing_run(const orc_plumbing_t *p, uint32_t ctx0, uint32_t n, double *pipelined_s, double *lat_s);
+/* OpenMP threads of the baseline kernels (omp_set_num_threads). */
+void orc_set_num_threads(int n);
 
 /* ---- sampling (specification in include/sample.h) ----
  * greedy != 0 or temperature <= 0: argmax, lowest index.

@@ -23,6 +23,15 @@ class OrcAttn(C.Structure):
                 ("kv_heads", C.c_uint32), ("ctx", C.c_void_p), ("q", C.c_void_p), ("scale", C.c_double)]
 
 
+class OrcPlumbing(C.Structure):
+    _fields_ = [("arena", C.c_void_p), ("block_bytes", C.c_uint64), ("token_count", C.c_uint32),
+                ("head_dim", C.c_uint32), ("dtype", C.c_uint32), ("table", C.c_void_p),
+                ("table_stride", C.c_uint32), ("q_heads", C.c_uint32), ("kv_heads", C.c_uint32),
+                ("scale", C.c_double), ("q", C.c_void_p), ("k_new", C.c_void_p), ("v_new", C.c_void_p),
+                ("logits", C.c_void_p), ("vocab", C.c_uint32), ("steps", C.c_uint32), ("attn_out", C.c_void_p),
+                ("tokens", C.c_void_p)]
+
+
 class RingShape(C.Structure):
     _fields_ = [("slot_size", C.c_uint32), ("n_slots", C.c_uint32), ("slot_off", C.c_uint32),
                 ("overflow_off", C.c_int32)]
@@ -68,7 +77,8 @@ def load_oracle() -> C.CDLL:
         "orc_sample_row": (u32, [vp, u32, i32, C.c_float, u32, C.c_float, u64, u64, u32, C.POINTER(C.c_double)]),
         "orc_sample_rows": (None, [vp, u32, u32, u32, i32, C.c_float, u32, C.c_float, vp, u64, vp, vp]),
         "orc_kv_append": (None, [vp, u64, u32, u32, vp, u32, u32, u32, vp, vp, vp, vp]),
-        "orc_num_threads": (i32, []),
+        "orc_num_threads": (i32, []), "orc_set_num_threads": (None, [i32]),
+        "orc_plumbing_run": (i32, [C.POINTER(OrcPlumbing), u32, u32, C.POINTER(C.c_double), vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(o, name)

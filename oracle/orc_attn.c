@@ -38,10 +38,37 @@ orc_f16_to_f64(uint16_t v)
     return s ? -r : r;
 }
 
+/* fp16 -> fp32 by fields (exact): zero / subnormal m * 2^-24, inf / NaN, or
+ * the rebiased exponent with the mantissa shifted into place. */
+static inline float
+f16_to_f32(uint16_t v)
+{
+    const uint32_t s = (uint32_t)(v & 0x8000u) << 16, e = (v >> 10) & 31u, m = v & 1023u;
+    uint32_t u;
+    if (e == 0) {
+        const float r = (float)m * 5.9604644775390625e-8f; /* 2^-24 */
+        memcpy(&u, &r, 4);
+        u |= s;
+    } else if (e == 31) {
+        u = s | 0x7F800000u | (m << 13);
+    } else {
+        u = s | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
 static inline float
 to_f32(uint16_t v, uint32_t dtype)
 {
-    return (float)(dtype == 0 ? orc_bf16_to_f64(v) : orc_f16_to_f64(v));
+    if (dtype == 0) {
+        const uint32_t u = (uint32_t)v << 16;
+        float f;
+        memcpy(&f, &u, 4);
+        return f;
+    }
+    return f16_to_f32(v);
 }
 
 /* Address of token t's K (plane 0) or V (plane 1) row for (b, g). */

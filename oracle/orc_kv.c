@@ -37,6 +37,16 @@ orc_kv_append(uint8_t *arena, uint64_t block_bytes, uint32_t token_count, uint32
     }
 }
 
+void
+orc_set_num_threads(int n)
+{
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
 int
 orc_num_threads(void)
 {

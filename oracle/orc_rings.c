@@ -36,13 +36,12 @@ orc_hw_ring_pop(uint8_t *ring, uint8_t out[64])
     return 0;
 }
 
-/* src/infer_submit.c:12-36 */
-int64_t
-orc_submit_decode(uint8_t *cmdq, uint32_t group, uint32_t arena_id, uint32_t rollout, uint64_t kv_off,
-                  uint64_t delta_off, uint32_t prefix, uint32_t seq, uint32_t max_tokens)
+/* src/infer_submit.c:12-32 (the descriptor infer_submit_decode builds) */
+void
+orc_decode_desc(uint8_t d[64], uint32_t group, uint32_t arena_id, uint32_t rollout, uint64_t kv_off,
+                uint64_t delta_off, uint32_t prefix, uint32_t seq, uint32_t max_tokens)
 {
-    uint8_t d[64];
-    memset(d, 0, sizeof(d));
+    memset(d, 0, 64);
     wr16(d + 0, 1);                       /* DESC_OP_DECODE */
     wr16(d + 2, prefix ? 4 : 0);          /* DESC_FLAG_COW_PREFIX */
     wr32(d + 4, rollout);
@@ -56,6 +55,15 @@ orc_submit_decode(uint8_t *cmdq, uint32_t group, uint32_t arena_id, uint32_t rol
     wr32(d + 44, group);
     wr64(d + 48, rollout);
     wr64(d + 56, kv_off ^ delta_off ^ ((uint64_t)rollout << 32));
+}
+
+/* src/infer_submit.c:12-36 */
+int64_t
+orc_submit_decode(uint8_t *cmdq, uint32_t group, uint32_t arena_id, uint32_t rollout, uint64_t kv_off,
+                  uint64_t delta_off, uint32_t prefix, uint32_t seq, uint32_t max_tokens)
+{
+    uint8_t d[64];
+    orc_decode_desc(d, group, arena_id, rollout, kv_off, delta_off, prefix, seq, max_tokens);
     if (orc_hw_ring_push(cmdq, d) != 0)
         return -1;
     return rd32(cmdq + 64);

@@ -384,3 +384,44 @@ def test_branch_resolve_oracle_known_cases(olib):
     assert olib.orc_kvb_resolve(t.ctypes.data, 0) == 90000
     assert olib.orc_kvb_cow_source(t.ctypes.data, 0, 520, 16, 8, 0) == -1
     assert olib.orc_kvb_resolve(t.ctypes.data, 16384) == -1
+
+
+def test_plumbing_cpu_path_equals_sequential_oracle(orc, olib):
+    """The CPU baseline of the plumbing decode (hw_worker_sim loop on a pthread
+    with a real step per token) computes what the oracle computes step by
+    step: greedy tokens equal argmax, each step's fp32 attention equals
+    orc_attn_decode_f32 over the arena as the earlier appends left it, and the
+    final arena equals the sequential appends."""
+    import synth
+
+    n, ctx0, V = 6, 40, 512
+    steps = 2 * n
+    rng = np.random.default_rng(9)
+    w = synth.make_decode(8, 1, 8, 8, 64, ctx0, ctx0, dtype="fp16", kv_std=0.5, reserve_tokens=ctx0 + steps + 1)
+    q = synth.f32_to_f16(rng.standard_normal((steps, 8, 64), dtype=np.float32))
+    kn = synth.f32_to_f16(rng.standard_normal((steps, 8, 64), dtype=np.float32))
+    vn = synth.f32_to_f16(rng.standard_normal((steps, 8, 64), dtype=np.float32))
+    logits = rng.standard_normal((steps, V), dtype=np.float32)
+    arena = w.arena.copy()
+    out = np.zeros((steps, 8, 64), np.float32)
+    tok = np.zeros(steps, np.uint32)
+    p = orc.OrcPlumbing(arena=arena.ctypes.data, block_bytes=w.block_bytes, token_count=16, head_dim=64, dtype=1,
+                        table=w.table.ctypes.data, table_stride=w.table_stride, q_heads=8, kv_heads=8,
+                        scale=1.0 / 8.0, q=q.ctypes.data, k_new=kn.ctypes.data, v_new=vn.ctypes.data,
+                        logits=logits.ctypes.data, vocab=V, steps=steps, attn_out=out.ctypes.data,
+                        tokens=tok.ctypes.data)
+    pipe = C.c_double()
+    lat = np.zeros(n, np.float64)
+    assert olib.orc_plumbing_run(C.byref(p), ctx0, n, C.byref(pipe), lat.ctypes.data) == 0
+    assert pipe.value > 0 and (lat > 0).all()
+    assert np.array_equal(tok, np.argmax(logits, axis=1).astype(np.uint32))
+    host = w.arena.copy()
+    for k in range(steps):
+        wk = synth.DecodeWorkload(1, 8, 8, 64, "fp16", 16, np.array([ctx0 + k], np.uint32), w.table, host,
+                                  q[k].reshape(1, 8, 64), 0)
+        assert np.array_equal(out[k], orc.attn_f32(olib, wk, 1)[0]), k
+        pos = np.array([ctx0 + k], np.uint32)
+        k_row, v_row = np.ascontiguousarray(kn[k]), np.ascontiguousarray(vn[k])
+        olib.orc_kv_append(host.ctypes.data, w.block_bytes, 16, 128, w.table.ctypes.data, w.table_stride, 1, 8,
+                           pos.ctypes.data, None, k_row.ctypes.data, v_row.ctypes.data)
+    assert np.array_equal(arena, host)
