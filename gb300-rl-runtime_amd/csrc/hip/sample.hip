@@ -50,6 +50,12 @@ constexpr int kThreads = 256;
 constexpr int kPerThread = 32;
 constexpr int kSplitLen = kThreads * kPerThread;  // 8,192 elements
 constexpr int kCandCap = 1024;                    // candidates per split
+// Stride of consecutive slices' candidate lists: 16 entries (128 bytes) past
+// the capacity, so that the lists' starts, which every slice writes and every
+// merge reads, fall on different memory channels instead of one 8 KiB period.
+constexpr int kCandStride = kCandCap + 16;
+constexpr int kWaveCand = 256;                    // candidates per wave of a split (LDS list)
+constexpr int kSlicesPerWg = 1;                   // slices of one row per split workgroup
 constexpr int kMergeCap = 8192;                   // candidates per row in the merge
 constexpr int kKeptCap = 1024;                    // kept (top-k with ties) per row
 
@@ -80,7 +86,7 @@ struct SampleParams {
     uint32_t *token_out;
     float *logprob_out;
     SplitStat *stats;       // [rows][splits]
-    uint2 *cand;            // [rows][splits][kCandCap] (key, index)
+    uint2 *cand;            // [rows][splits][kCandStride] (key, index)
 };
 
 __device__ __forceinline__ float row_temperature(const SampleParams &p, uint32_t row)
@@ -173,42 +179,36 @@ __device__ __forceinline__ uint32_t wave_kth_largest_key(uint32_t key, uint32_t 
     return prefix;
 }
 
-__global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
+// The workgroup's LDS for one slice.
+struct SplitLds {
+    float red[4];
+    uint32_t red_i[4];
+    float z[4];
+    uint32_t key[4];
+    uint32_t wtot[4];
+    uint2 cand[4][kWaveCand];  // each wave's candidates, compacted
+};
+
+// One 8,192-element slice of a row, its quads already requested into raw:
+// the slice statistics (greedy: argmax; sampling: max and sum exp of x =
+// l * inv_t, and the candidates at or above the slice's bound).
+__device__ __forceinline__ void split_slice(const SampleParams &p, uint32_t row, uint32_t split, bool greedy,
+                                            float inv_t, const rl_f32x4 (&raw)[kPerThread / 4], uint64_t draw,
+                                            SplitLds &L)
 {
-    const uint32_t split = blockIdx.x;
-    const uint32_t row = blockIdx.y;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-
-    __shared__ float s_red[4];
-    __shared__ uint32_t s_red_i[4];
-    __shared__ float s_z[4];
-    __shared__ uint32_t s_key[4];
-    __shared__ uint32_t s_wtot[4];
-
-    const float *lrow = p.logits + (size_t)row * p.row_stride;
+    float *s_red = L.red;
+    uint32_t *s_red_i = L.red_i;
+    float *s_z = L.z;
+    uint32_t *s_key = L.key;
+    uint32_t *s_wtot = L.wtot;
+    uint2 (*s_cand)[kWaveCand] = L.cand;
     const uint32_t c0 = split * kSplitLen;
-    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
-    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
-
-    // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
-    // Every load is issued unconditionally (a quad past the end re-reads the
-    // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
-    // masked afterwards, so all eight are in flight together. Only the last
-    // slice of a row can reach past the vocabulary (a workgroup-uniform test).
+    // Only the last slice of a row can reach past the vocabulary (a
+    // workgroup-uniform test); its quads past the end are masked to -inf.
     float x[kPerThread];
-    const uint32_t last_quad = (p.vocab - 1) & ~3u;
-    rl_f32x4 raw[kPerThread / 4];
-#pragma unroll
-    for (int k = 0; k < kPerThread / 4; k++) {
-        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
-        raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
-    }
-    // the row's Philox draw, for the merge (computed while the loads are in flight)
-    uint64_t draw = 0;
-    if (split == 0 && !greedy && wave == 0)
-        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
     if (c0 + (uint32_t)kSplitLen <= p.vocab) {
 #pragma unroll
         for (int k = 0; k < kPerThread / 4; k++)
@@ -276,13 +276,31 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
     }
 
     // ---- sampling: x = l * inv_t, slice max, sum exp, candidates -------------
-    // Two barriers: (1) wave maxima and k-th bounds, (2) wave sums and
-    // candidate counts; the candidates are then written at their offsets.
-    float tmax = -INFINITY;
+    // Each quad is consumed as its load lands: x, the lane's running max and
+    // its sum of exp(x - running max), rescaled when the max grows (once per
+    // quad at most), so the exponentials overlap the stream and no second
+    // pass over the slice is needed. After the last quad: the wave's k-th
+    // bound, one barrier for the wave maxima / sums / bounds, the candidate
+    // counts, a second barrier, and the candidate writes.
+    constexpr float kLog2e = 1.4426950408889634f;
+    float tmax = -INFINITY, zl = 0.f;
 #pragma unroll
-    for (int i = 0; i < kPerThread; i++) {
-        x[i] = x[i] * inv_t;
-        tmax = fmaxf(tmax, x[i]);
+    for (int k = 0; k < kPerThread / 4; k++) {
+        float q[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            q[e] = x[k * 4 + e] * inv_t;
+            x[k * 4 + e] = q[e];
+        }
+        const float qm = fmaxf(fmaxf(q[0], q[1]), fmaxf(q[2], q[3]));
+        const float nm = fmaxf(tmax, qm);
+        // rescale the running sum to the new max (a running max of -inf has no sum yet)
+        zl = tmax == -INFINITY ? 0.f : zl * __builtin_amdgcn_exp2f((tmax - nm) * kLog2e);
+        tmax = nm;
+        const float ml = nm == -INFINITY ? 0.f : nm * kLog2e;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            zl += __builtin_amdgcn_exp2f(fmaf(q[e], kLog2e, -ml));
     }
     const float wmax = wave_max(tmax);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
@@ -292,71 +310,125 @@ __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
         if (lane == 0)
             s_key[wave] = ck;
     }
-    if (lane == 0)
+    // the wave's sum relative to the wave max
+    const float wz = wave_sum(tmax == -INFINITY ? 0.f : zl * __builtin_amdgcn_exp2f((tmax - wmax) * kLog2e));
+    if (lane == 0) {
         s_red[wave] = wmax;
+        s_z[wave] = wz;
+    }
     __syncthreads();
     const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float z = 0.f;
-    if (m != -INFINITY) {
-        const float ml = m * 1.4426950408889634f;
-#pragma unroll
-        for (int i = 0; i < kPerThread; i++)
-            z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
-    }
-    z = wave_sum(z);
-    if (lane == 0)
-        s_z[wave] = z;
 
     // Candidates: key(x) >= clb and x != -inf. For x not NaN that is x >= t
     // with t = the float of clb (the key order is the float order with -0 =
     // +0), t raised to -FLT_MAX when clb is the key of -inf; a NaN x has a key
     // above every non-NaN key, and !(x < t) keeps it too.
-    uint32_t cand_lo = 0, cnt = 0, incl = 0;
-    float t = 0.f;
+    // Each wave compacts its candidates into its own LDS list: one ballot per
+    // element position, and the lanes holding a candidate there take
+    // consecutive slots (mbcnt); a position without one costs a scalar branch
+    // and no store. After the barrier each wave copies its list to its offset
+    // in the slice's global list, 64 entries per store. A wave with more than
+    // kWaveCand candidates makes the slice report an overflow (the merge then
+    // takes the exact whole-row path).
+    uint32_t cand_lo = 0, wcount = 0;
     if (k_eff != 0) {
         const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
         cand_lo = clb;
-        t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
-#pragma unroll
-        for (int i = 0; i < kPerThread; i++)
-            cnt += !(x[i] < t) ? 1u : 0u;
-        incl = cnt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t o = __shfl_up(incl, off);
-            if (lane >= off)
-                incl += o;
-        }
-        if (lane == 63)
-            s_wtot[wave] = incl;
-    }
-    __syncthreads();
-    if (k_eff != 0 && cnt) {
-        uint32_t base = incl - cnt;
-        for (int w = 0; w < wave; w++)
-            base += s_wtot[w];
-        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandCap;
+        const float t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
+        uint2 *mine = s_cand[wave];
 #pragma unroll
         for (int k = 0; k < kPerThread / 4; k++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float v = x[k * 4 + e];
-                if (!(v < t)) {
-                    if (base < (uint32_t)kCandCap)
-                        cand[base] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
-                    base++;
+                const bool c = !(v < t);
+                const uint64_t bal = __ballot(c);
+                if (bal) {
+                    if (c) {
+                        const uint32_t slot = wcount + __builtin_amdgcn_mbcnt_hi(
+                                                           (uint32_t)(bal >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                        if (slot < (uint32_t)kWaveCand)
+                            mine[slot] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                    }
+                    wcount += (uint32_t)__popcll(bal);
                 }
             }
+        if (lane == 0)
+            s_wtot[wave] = wcount;
+    }
+    __syncthreads();
+    uint32_t n_cand = 0;
+    if (k_eff != 0) {
+        uint32_t base = 0;
+        bool over = false;
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t c = s_wtot[w];
+            base += w < wave ? c : 0u;
+            n_cand += c;
+            over |= c > (uint32_t)kWaveCand;
+        }
+        if (over)
+            n_cand = kCandCap + 1u;
+        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandStride;
+        const uint2 *mine = s_cand[wave];
+        const uint32_t n = min(wcount, (uint32_t)kWaveCand);
+        for (uint32_t j = lane; j < n; j += 64)
+            if (base + j < (uint32_t)kCandCap)
+                cand[base + j] = mine[j];
     }
     if (tid == 0) {
+        float zsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+            zsum += s_red[w] == -INFINITY ? 0.f : s_z[w] * __builtin_amdgcn_exp2f((s_red[w] - m) * kLog2e);
         st->max_x = m;
-        st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
+        st->sum_exp = zsum;
         st->arg_val = m;
         st->arg_idx = 0;
-        st->n_cand = k_eff != 0 ? s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3] : 0u;
+        st->n_cand = n_cand;
         st->cand_lo = cand_lo;
         st->draw = draw;
     }
+}
+
+
+// Grid (slice pair, row): each workgroup takes two consecutive slices of its
+// row. Both slices' quads are requested at entry (element (k, e) of thread
+// tid in slice s is column s * 8,192 + (k * 256 + tid) * 4 + e; a quad past
+// the end re-reads the row's last quad, which row_stride % 4 == 0 keeps inside
+// the row, and is masked later), so the first slice's data lands early and
+// its reductions and candidate pass run while the second slice still streams;
+// only the second slice's tail is left at the end, with half as many waves per
+// SIMD as one slice per workgroup would leave. Slice 0 of a sampled row also
+// computes the row's Philox draw while the loads are in flight.
+__global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
+{
+    const uint32_t row = blockIdx.y;
+    const uint32_t s0 = blockIdx.x * kSlicesPerWg;
+    const int tid = threadIdx.x;
+    __shared__ SplitLds lds[kSlicesPerWg];
+
+    const float *lrow = p.logits + (size_t)row * p.row_stride;
+    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
+    const uint32_t last_quad = (p.vocab - 1) & ~3u;
+    rl_f32x4 raw[kSlicesPerWg][kPerThread / 4];
+#pragma unroll
+    for (int j = 0; j < kSlicesPerWg; j++)
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++) {
+            const uint32_t col = (s0 + j) * kSplitLen + (uint32_t)(k * kThreads + tid) * 4u;
+            raw[j][k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
+        }
+    uint64_t draw = 0;
+    if (s0 == 0 && !greedy && (tid >> 6) == 0)
+        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+#pragma unroll
+    for (int j = 0; j < kSlicesPerWg; j++)
+        if (s0 + j < p.splits)
+            split_slice(p, row, s0 + j, greedy, inv_t, raw[j], j == 0 ? draw : 0ull, lds[j]);
 }
 
 // ---- block-wide helpers of the merge (512 threads = 8 waves) ----------------
@@ -969,13 +1041,13 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     // overlap: this wave's first 256 candidates of the lists of splits w and
     // w + 8 (in bounds whatever the split wrote; masked by the counts later),
     // and the row's Philox draw (computed by the row's first split).
-    const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandCap;
+    const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandStride;
     uint2 pv[8];
     uint64_t draw = 0;
     if (!greedy) {
         draw = st[0].draw;
-        const uint2 *pf1 = rbase + (size_t)min(wave, p.splits - 1) * kCandCap;
-        const uint2 *pf2 = rbase + (size_t)min(wave + kMergeWaves, p.splits - 1) * kCandCap;
+        const uint2 *pf1 = rbase + (size_t)min(wave, p.splits - 1) * kCandStride;
+        const uint2 *pf2 = rbase + (size_t)min(wave + kMergeWaves, p.splits - 1) * kCandStride;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             pv[r] = pf1[r * 64 + lane];
@@ -1010,7 +1082,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         if (tid == 0) {
             const uint32_t i = ai >= p.vocab ? 0u : ai;  // all -inf: lowest index
             p.token_out[row] = i;
-            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + i] - lse;
+            // av is the logit at i (for a row of -inf, logit 0 is -inf too): no reload
+            p.logprob_out[row] = av - lse;
         }
         return;
     }
@@ -1022,6 +1095,10 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const uint64_t cum = wave_inclusive_scan_u64(ncand);
     const uint32_t n = (uint32_t)__shfl(cum, 63);
     uint32_t tok = 0;
+    // the sampled token's x when the path that chose it holds it (its key is
+    // the float l * inv_t itself), so the logprob needs no reload of the logit
+    float xtok = 0.f;
+    bool xknown = false;
     // the exact whole-row path (one call site, so it is inlined and its
     // pointers stay in their address spaces): no top-k, or too many candidates
     bool exact = k_eff == 0 || split_over || n > (uint32_t)kMergeCap;
@@ -1062,8 +1139,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             const bool has2 = t2 < p.splits;
             const uint32_t cnt1 = rl_readlane(ncand, (int)t);
             const uint32_t cnt2 = has2 ? rl_readlane(ncand, (int)min(t2, 63u)) : 0u;
-            const uint2 *src1 = rbase + (size_t)t * kCandCap;
-            const uint2 *src2 = has2 ? rbase + (size_t)t2 * kCandCap : src1;
+            const uint2 *src1 = rbase + (size_t)t * kCandStride;
+            const uint2 *src2 = has2 ? rbase + (size_t)t2 * kCandStride : src1;
             const uint32_t last1 = cnt1 ? cnt1 - 1 : 0u, last2 = cnt2 ? cnt2 - 1 : 0u;
             for (uint32_t j0 = 0; j0 < max(cnt1, cnt2); j0 += 256) {
                 uint2 v[8];
@@ -1253,6 +1330,12 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
                     tok = rl_wave_min_u32(in_p ? idx : 0xFFFFFFFFu);
                 if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
                     tok = 0;
+                const uint64_t own = __ballot(valid && idx == tok);
+                if (own) {
+                    const int src = (int)__ffsll((long long)own) - 1;
+                    xtok = rl_key_float(rl_readlane((uint32_t)(cs >> 32), src));
+                    xknown = true;
+                }
             }
         } else {
             // ---- rank sort by (x desc, index asc): composite keys are distinct
@@ -1327,7 +1410,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         const float lse = row_lse();
         if (tid == 0) {
             p.token_out[row] = tok;
-            p.logprob_out[row] = p.logits[(size_t)row * p.row_stride + tok] * inv_t - lse;
+            const float x = xknown ? xtok : p.logits[(size_t)row * p.row_stride + tok] * inv_t;
+            p.logprob_out[row] = x - lse;
         }
     }
 }
@@ -1344,7 +1428,7 @@ WsLayout ws_layout(const rl_sample_args_t *a)
     WsLayout w;
     w.stats_off = 0;
     w.cand_off = ((a->rows * splits * sizeof(SplitStat) + 255) / 256) * 256;
-    w.total = w.cand_off + (size_t)a->rows * splits * kCandCap * sizeof(uint2);
+    w.total = w.cand_off + (size_t)a->rows * splits * kCandStride * sizeof(uint2);
     return w;
 }
 
@@ -1414,7 +1498,8 @@ extern "C" int rl_hip_sample(const rl_sample_args_t *a)
     p.stats = (SplitStat *)(ws + w.stats_off);
     p.cand = (uint2 *)(ws + w.cand_off);
 
-    hipLaunchKernelGGL(sample_split_kernel, dim3(p.splits, a->rows), dim3(kThreads), 0, rl_stream(), p);
+    hipLaunchKernelGGL(sample_split_kernel, dim3((p.splits + kSlicesPerWg - 1) / kSlicesPerWg, a->rows),
+                       dim3(kThreads), 0, rl_stream(), p);
     if (rl_check_launch("sample_split_kernel launch"))
         return -1;
     hipLaunchKernelGGL(sample_merge_kernel, dim3(a->rows), dim3(kMergeThreads), 0, rl_stream(), p);
