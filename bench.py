@@ -392,6 +392,40 @@ def wl_sample256(args):
     return {"workload": "sample_r256_v128256_t0.8_k50_p0.9 (+ greedy)", **res}
 
 
+def wl_sample32k(args):
+    """The rollout loop's sampler shape: 256 rows x 32,000 fp32 logits
+    ~N(0, 0.3); top-p 0.9 over the whole vocabulary (T 1, no top-k), then
+    top-k 50 + top-p 0.9, then greedy. Nine copies of the logits (295 MB)
+    rotate past the 256 MB Infinity Cache, so every call reads HBM."""
+    rows, vocab, copies = 256, 32000, 9
+    rng = np.random.default_rng(35)
+    x = rng.standard_normal((rows, vocab), dtype=np.float32) * np.float32(0.3)
+    lg = [rlrt.DeviceBuffer.from_array(x) for _ in range(copies)]
+    seeds = rlrt.DeviceBuffer.from_array(rng.integers(0, 2**63, rows, dtype=np.uint64))
+    tok, lp = rlrt.DeviceBuffer(rows * 4), rlrt.DeviceBuffer(rows * 4)
+    res = {}
+    for name, greedy, k in (("topp", False, 0), ("topk_topp", False, TOPK), ("greedy", True, 0)):
+        ss = [rlrt.sample_args(b, rows, vocab, vocab, tok, lp, greedy=greedy, temperature=1.0, top_k=k,
+                               top_p=TOPP, seeds=seeds) for b in lg]
+        ws = rlrt.sample_workspace(ss[0])
+        for s in ss[1:]:
+            s.workspace, s.workspace_bytes = ws.ptr, ws.nbytes
+
+        def run(i, ss=ss):
+            s = ss[i % copies]
+            s.step = i
+            rlrt.sample(s)
+
+        us = _event_us(run, args.steps)
+        nbytes = rows * vocab * 4 + rows * 8
+        res[name] = {"us_per_call": us, "alg_bytes": nbytes, "alg_gbps": nbytes / (us * 1e-6) / 1e9,
+                     "frac": nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS}
+        ws.close()
+    for b in lg + [seeds, tok, lp]:
+        b.close()
+    return {"workload": "sample_r256_v32000_p0.9 (+ top-k 50, greedy)", **res}
+
+
 def wl_longctx(args):
     """B=8, ctx 32,768, 64 q / 8 kv heads, d128, bf16 K/V ~N(0,1), permuted
     16-token blocks, split-KV over the whole device with the fp32 LSE merge;
@@ -974,8 +1008,8 @@ def wl_pipeline_trace(args):
             "clock": {"ns_per_tick": m.ns_per_tick, "rtt_ns": [c0[2], c1[2]]}, "latency_ns": pairs}
 
 
-WORKLOADS = {"sample256": wl_sample256, "longctx": wl_longctx, "proj": wl_proj, "plumbing": wl_plumbing,
-             "plumbing256": wl_plumbing256, "ringstep": wl_ringstep,
+WORKLOADS = {"sample256": wl_sample256, "sample32k": wl_sample32k, "longctx": wl_longctx, "proj": wl_proj,
+             "plumbing": wl_plumbing, "plumbing256": wl_plumbing256, "ringstep": wl_ringstep,
              "rollout": wl_rollout, "cmdring": wl_cmdring, "rollout_pipeline": wl_rollout_pipeline,
              "pipeline": wl_pipeline, "pipeline_trace": wl_pipeline_trace}
 

@@ -474,7 +474,7 @@ struct BlockShared {
 };
 
 // Exclusive prefix over the block in thread order; `total` gets the block sum.
-__device__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t &total, BlockShared &bs)
+__device__ __forceinline__ uint64_t block_excl_scan_u64_inl(uint64_t v, uint64_t &total, BlockShared &bs)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t incl = wave_inclusive_scan_u64(v);
@@ -491,6 +491,13 @@ __device__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t &total, BlockShared
     __syncthreads();
     total = t;
     return base + incl - v;
+}
+
+// (the merge kernel calls it; the row kernel inlines it, a call there would
+// save and restore the registers that hold the row)
+__device__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t &total, BlockShared &bs)
+{
+    return block_excl_scan_u64_inl(v, total, bs);
 }
 
 __device__ uint64_t block_sum_u64(uint64_t v, BlockShared &bs)
@@ -707,11 +714,11 @@ __device__ uint32_t row_topk_cutoff(const float *l, uint32_t V, float inv_t, uin
 // The radix fallback: nucleus boundary tau as the largest composite key whose
 // suffix weight reaches thr (8 passes of 8-bit digits), then W_P and the
 // ascending-index walk in chunks of 256 threads x 8 elements.
-__device__ uint32_t radix_row_sample(const SampleParams &p, uint32_t row, const float *l, float inv_t, uint32_t cutoff,
-                                     float topp, float m, uint64_t wk, unsigned long long *s_whist, BlockShared &bs)
+__device__ __forceinline__ uint32_t radix_row_sample(uint64_t seed, uint64_t step, uint32_t row, uint32_t V,
+                                                     const float *l, float inv_t, uint32_t cutoff, float topp, float m,
+                                                     uint64_t wk, unsigned long long *s_whist, BlockShared &bs)
 {
     const uint32_t tid = threadIdx.x;
-    const uint32_t V = p.vocab;
     uint64_t tau = 0;
     if (topp > 0.f && topp < 1.f) {
         const uint64_t thr = rl_topp_threshold(topp, wk);
@@ -754,7 +761,7 @@ __device__ uint32_t radix_row_sample(const SampleParams &p, uint32_t row, const 
     const uint64_t wp = block_sum_u64(wp_own, bs);
     lowest = block_min_u32(lowest, bs);
 
-    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(row_seed(p, row), row_step(p, row), row), wp);
+    const uint64_t u = rl_mulhi_u64(rl_sample_draw64(seed, step, row), wp);
     uint64_t carry = 0;
     uint32_t tok = 0xFFFFFFFFu;
     for (uint32_t base = 0; base < V && tok == 0xFFFFFFFFu; base += kMergeThreads * 8) {
@@ -793,9 +800,9 @@ __device__ uint32_t radix_row_sample(const SampleParams &p, uint32_t row, const 
     return tok;
 }
 
-__device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff, float topp,
-                                     float m, RowScratch &rs, uint32_t *s_hist, unsigned long long *s_whist,
-                                     BlockShared &bs)
+__device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint32_t row, float inv_t, uint32_t k_eff,
+                                                     float topp, float m, RowScratch &rs, uint32_t *s_hist,
+                                                     unsigned long long *s_whist, BlockShared &bs)
 {
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -890,7 +897,8 @@ __device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint
     if (trunc) {
         const uint32_t nb = bs.cnt[0];
         if (nb > (uint32_t)kBinCap)
-            return radix_row_sample(p, row, l, inv_t, cutoff, topp, m, wk, s_whist, bs);
+            return radix_row_sample(row_seed(p, row), row_step(p, row), row, V, l, inv_t, cutoff, topp, m, wk, s_whist,
+                                    bs);
 
         // ---- the boundary bin's sub-bins: the one where thr is reached ----------
         for (uint32_t e = tid; e < nb; e += kMergeThreads) {
@@ -936,7 +944,8 @@ __device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint
         __syncthreads();
         const uint32_t ns = bs.cnt[1];
         if (ns > (uint32_t)kSubCap)
-            return radix_row_sample(p, row, l, inv_t, cutoff, topp, m, wk, s_whist, bs);
+            return radix_row_sample(row_seed(p, row), row_step(p, row), row, V, l, inv_t, cutoff, topp, m, wk, s_whist,
+                                    bs);
         if (tid < ns) {
             const uint64_t ck = rs.skey[tid];
             uint64_t s = 0;  // sub-bin weight strictly above this element
@@ -993,9 +1002,10 @@ __device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint
             const float x = quad_at(v, e) * inv_t;
             const uint32_t key = rl_float_key(x);
             const uint32_t b = trunc ? dist_bin(m, x) : 0u;
-            const bool in = key >= cutoff && (b < bstar || (b == bstar && composite_key(key, i0 + e) >= tau));
+            const uint32_t at_tau = (uint32_t)(b == bstar) & (uint32_t)(composite_key(key, i0 + e) >= tau);
+            const uint32_t in = (uint32_t)(key >= cutoff) & ((uint32_t)(b < bstar) | at_tau);
             const uint32_t w = rl_sample_weight_nb(x - m);  // -inf weighs 0
-            w4[e] = in ? w : 0u;
+            w4[e] = w & (0u - in);  // (a mask: no short-circuit branches)
             own += w4[e];
         }
         uint64_t c = before + wave_inclusive_scan_u64(own) - own;
@@ -1416,6 +1426,488 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     }
 }
 
+// ---- one workgroup per row, the whole row in registers (vocab <= 32,768) ----
+// Wave w holds the 4,096 consecutive logits from 4,096 w in 16 rounds of 256:
+// lane l of round j holds the quad at 4,096 w + 256 j + 4 l, so each load
+// instruction reads 1 KiB of consecutive logits and each thread's elements
+// ascend with (j, e). Rows without top-k only (whole-vocabulary nucleus and
+// greedy rows); the host sends batches with top-k to the split and merge
+// kernels. With one row per compute unit the kernel is bound by vector-ALU
+// issue (a wave64 instruction every 4 cycles per SIMD), so the element loops
+// are kept to two passes over the registers:
+//   weights  d = x - m, w = floor(e^d 2^24) (rl_sample_weight_f), the float
+//            e^d 2^24 summed for the log-sum-exp, and the weight histogram
+//            by bin of d
+//   gather   per round, the weight in the bins above the nucleus boundary
+//            bin, and that bin's members appended to an LDS list
+// then, on LDS: the boundary member (members ranked pairwise), the per-round
+// nucleus weights (the lanes' round sums reduced through LDS, plus the
+// boundary bin's members in the nucleus), the round where the cumulative
+// weight first exceeds the draw, and the element inside it (one wave scan).
+// Bins: kRowBins over d in [0, span), span = min(m - min x, 17) (w = 0
+// beyond 16.64), a monotone map of x; u32 weight sums (a bin that wraps
+// shows as a histogram total below W and sends the row to the exact path),
+// one pad word after every 16 bins so that the scan's reads of 16
+// consecutive bins per thread hit distinct banks. The nucleus boundary is the composite key tau (x desc, index asc) at
+// which the weights ranked above tau sum to less than thr = ceil(p W) and
+// with tau to at least thr: the bin where the cumulative weight reaches thr,
+// then its members. A boundary bin with more than kRowList members (massive
+// ties) sends the row to the exact whole-row path above, which reads it
+// again from memory.
+constexpr int kRowRounds = 16;
+constexpr uint32_t kRowVocab = (uint32_t)kMergeWaves * kRowRounds * 256u;  // 32,768
+constexpr int kRowBins = 8192;
+constexpr int kRowPer = kRowBins / kMergeThreads;              // bins per thread in the scan
+constexpr int kRowHistWords = kRowBins + kRowBins / kRowPer;   // with the pad words
+constexpr int kRowList = 256;
+
+struct RowEntry {
+    unsigned long long ck;  // composite key
+    uint32_t val;
+    uint32_t pad;
+};
+
+struct RowLds {
+    union {
+        uint32_t hist[kRowHistWords];                    // bin b at word b + b / 16
+        uint32_t lane_rs[kMergeWaves][kRowRounds][64];  // per-lane round sums
+    };
+    RowEntry list[kRowList];
+    unsigned long long rsum[kMergeWaves * kRowRounds];
+    float f0[kMergeWaves], f1[kMergeWaves];
+    uint32_t u0[kMergeWaves];
+    unsigned long long u1[kMergeWaves];
+};
+
+// Redefines every element as far as the compiler knows (no instruction is
+// emitted): values derived from the elements before this point are computed
+// again after it instead of being held in registers across the phases of the
+// row kernel, whose elements already take 128 registers per lane.
+template <class T>
+__device__ __forceinline__ void row_fence(T (&a)[kRowRounds][4])
+{
+#pragma unroll
+    for (int j = 0; j < kRowRounds; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            asm volatile("" : "+v"(a[j][e]));
+}
+
+// Bin of d = x - m <= 0 (scale = kRowBins / span, or 0): -inf and NaN fall
+// in the last bin.
+__device__ __forceinline__ uint32_t row_bin(float d, float scale)
+{
+    return (uint32_t)fminf(-d * scale, (float)(kRowBins - 1));
+}
+
+__device__ __forceinline__ uint32_t row_hist_word(uint32_t b) { return b + b / kRowPer; }
+
+__device__ __forceinline__ void row_clear_hist(RowLds &L)
+{
+    for (uint32_t b = threadIdx.x; b < (uint32_t)kRowHistWords / 4u; b += kMergeThreads)
+        reinterpret_cast<uint4 *>(L.hist)[b] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// Block max of a and min of b (every thread gets both).
+__device__ __forceinline__ void row_max_min(float &a, float &b, RowLds &L)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    a = wave_max(a);
+    b = -wave_max(-b);
+    if (lane == 0) {
+        L.f0[wave] = a;
+        L.f1[wave] = b;
+    }
+    __syncthreads();
+    a = L.f0[0];
+    b = L.f1[0];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; w++) {
+        a = fmaxf(a, L.f0[w]);
+        b = fminf(b, L.f1[w]);
+    }
+    __syncthreads();
+}
+
+// Block sums of a float and of a per-thread u32 below 2^31 (exact, in 64 bits).
+__device__ __forceinline__ void row_sum_f_u(float &f, uint32_t v, uint64_t &total, RowLds &L)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    f = wave_sum(f);
+    const uint64_t ws = ((uint64_t)rl_wave_sum_u32(v >> 8) << 8) + rl_wave_sum_u32(v & 0xFFu);
+    if (lane == 0) {
+        L.f0[wave] = f;
+        L.u1[wave] = ws;
+    }
+    __syncthreads();
+    f = 0.f;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; w++) {
+        f += L.f0[w];
+        total += L.u1[w];
+    }
+    __syncthreads();
+}
+
+// The bin where the cumulative histogram value (bins in order) reaches need,
+// and the value in the bins before it; need in [1, total]. Returns false when
+// the histogram total is not W (a bin wrapped). Also clears the list counter.
+__device__ __forceinline__ bool row_hist_scan(uint64_t need, uint64_t W, uint32_t &bstar, uint64_t &above,
+                                              RowLds &L, BlockShared &bs)
+{
+    const uint32_t tid = threadIdx.x;
+    uint32_t h[kRowPer];
+    uint64_t own = 0;
+#pragma unroll
+    for (int k = 0; k < kRowPer; k++) {
+        h[k] = L.hist[tid * (kRowPer + 1) + k];
+        own += h[k];
+    }
+    uint64_t total;
+    const uint64_t excl = block_excl_scan_u64_inl(own, total, bs);
+    if (excl < need && excl + own >= need) {  // exactly one thread (when no bin wrapped)
+        uint64_t c = excl;
+        uint32_t b = 0;
+#pragma unroll
+        for (int k = 0; k < kRowPer; k++)
+            if (c + h[k] < need && b == (uint32_t)k) {
+                c += h[k];
+                b++;
+            }
+        bs.n = tid * kRowPer + b;
+        bs.sel64 = c;
+    }
+    if (tid == 0)
+        bs.cnt[0] = 0;
+    __syncthreads();
+    bstar = bs.n;
+    above = bs.sel64;
+    __syncthreads();
+    return total == W;
+}
+
+// Appends this lane's element to the LDS list when `take`: one LDS atomic per
+// wave and round for the four elements of the round.
+__device__ __forceinline__ void row_append4(const bool (&take)[4], const float (&x4)[4], const uint32_t (&v4)[4],
+                                            uint32_t idx0, RowLds &L, BlockShared &bs)
+{
+    uint64_t bal[4];
+    uint32_t off[4], tot = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        bal[e] = __ballot(take[e]);
+        off[e] = tot;
+        tot += (uint32_t)__popcll(bal[e]);
+    }
+    if (tot == 0)
+        return;
+    uint32_t pos0 = 0;
+    if ((threadIdx.x & 63) == 0)
+        pos0 = atomicAdd(&bs.cnt[0], tot);
+    pos0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)pos0);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t pos = pos0 + off[e] +
+                             __builtin_amdgcn_mbcnt_hi((uint32_t)(bal[e] >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo((uint32_t)bal[e], 0u));
+        if (take[e] && pos < (uint32_t)kRowList)
+            L.list[pos] = RowEntry{composite_key(rl_float_key(x4[e]), idx0 + e), v4[e], 0u};
+    }
+}
+
+// Member tid of the list (tid < n): publishes (tau, above + value ranked
+// above tau + tau's value) when it is the boundary. The caller synchronises.
+__device__ __forceinline__ void row_rank(uint32_t n, uint64_t above, uint64_t need, RowLds &L, BlockShared &bs)
+{
+    const uint32_t tid = threadIdx.x;
+    if (tid < n) {
+        const RowEntry me = L.list[tid];
+        uint64_t s = 0;  // value of the members ranked above me
+        // four entries per step, their LDS reads in flight together (the
+        // entries past n, read in bounds, count nothing)
+        for (uint32_t k = 0; k < n; k += 4) {
+            RowEntry o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = L.list[min(k + i, (uint32_t)kRowList - 1u)];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                s += (k + i < n && o[i].ck > me.ck) ? (uint64_t)o[i].val : 0ull;
+        }
+        if (above + s < need && above + s + me.val >= need) {  // exactly one member
+            bs.res64[0] = me.ck;
+            bs.res64[1] = above + s + me.val;
+        }
+    }
+}
+
+__global__ __launch_bounds__(kMergeThreads) void sample_row_kernel(SampleParams p)
+{
+    const uint32_t row = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    __shared__ union {
+        RowLds r;
+        RowScratch x;  // the exact whole-row path
+    } lds;
+    __shared__ uint32_t s_hist[256];
+    __shared__ unsigned long long s_whist[256];
+    __shared__ BlockShared bs;
+    RowLds &L = lds.r;
+
+    const float *l = p.logits + (size_t)row * p.row_stride;
+    const uint32_t V = p.vocab;
+    const uint32_t wave_base = (uint32_t)wave * (kRowRounds * 256u);
+    // (base is redefined, as far as the compiler knows, at every phase, so
+    // that the 64 element indices are formed again where used, not held)
+    uint32_t base = wave_base + (uint32_t)lane * 4u;
+    const uint32_t last_quad = (V - 1) & ~3u;
+    rl_f32x4 raw[kRowRounds];
+#pragma unroll
+    for (int j = 0; j < kRowRounds; j++)
+        raw[j] = __builtin_nontemporal_load((const rl_f32x4 *)(l + min(base + 256u * j, last_quad)));
+    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
+    const uint64_t draw = greedy ? 0ull : rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+    const float topp = row_topp(p, row);
+    const bool trunc = !greedy && topp > 0.f && topp < 1.f;
+    if (trunc)
+        row_clear_hist(L);  // ordered before the atomics by the barriers of the max
+    constexpr float kLog2e = 1.4426950408889634f;
+
+    float x[kRowRounds][4];
+    float m = -INFINITY, xmin = INFINITY;  // (xmin: -inf when the row holds a -inf logit)
+#pragma unroll
+    for (int j = 0; j < kRowRounds; j++) {
+        if (wave_base + 256u * j + 256u <= V) {  // a round inside the vocabulary (wave-uniform)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[j][e] = raw[j][e] * inv_t;
+                xmin = fminf(xmin, x[j][e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool in = base + 256u * j + e < V;
+                x[j][e] = in ? raw[j][e] * inv_t : -INFINITY;
+                xmin = fminf(xmin, in ? x[j][e] : INFINITY);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            m = fmaxf(m, x[j][e]);
+    }
+    row_max_min(m, xmin, L);
+    row_fence(x);
+    asm volatile("" : "+v"(base));
+
+    if (greedy) {  // the lowest index holding the maximum (0 for a row of -inf)
+        uint32_t bi = 0xFFFFFFFFu;
+        float z = 0.f;
+        const float ml = m * kLog2e;
+#pragma unroll
+        for (int j = kRowRounds - 1; j >= 0; j--)
+#pragma unroll
+            for (int e = 3; e >= 0; e--) {
+                bi = x[j][e] == m ? base + 256u * j + e : bi;
+                z += m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(fmaf(x[j][e], kLog2e, -ml));
+            }
+        uint64_t unused;
+        row_sum_f_u(z, 0u, unused, L);
+        bi = rl_wave_min_u32(bi);
+        if (lane == 0)
+            L.u0[wave] = bi;
+        __syncthreads();
+        if (tid == 0) {
+#pragma unroll
+            for (int w = 1; w < kMergeWaves; w++)
+                bi = min(bi, L.u0[w]);
+            p.token_out[row] = bi;
+            p.logprob_out[row] = m - (m + logf(z));
+        }
+        return;
+    }
+
+    // bins over d in [0, span): the row's spread, at most 17
+    const float span = fminf(m - xmin, kBinSpan);
+    const float scale = span > 0.f ? (float)kRowBins / span : 0.f;
+
+    // ---- weights, log-sum-exp terms, the first histogram ------------------------
+    uint32_t w[kRowRounds][4];
+    float zf = 0.f;
+    uint32_t own = 0;  // the weight sum (< 2^31)
+    if (trunc) {
+#pragma unroll
+        for (int j = 0; j < kRowRounds; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float d = x[j][e] - m;
+                float f;
+                w[j][e] = rl_sample_weight_f(d, &f);
+                zf += f;
+                own += w[j][e];
+                atomicAdd(&L.hist[row_hist_word(row_bin(d, scale))], w[j][e]);
+            }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kRowRounds; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float f;
+                w[j][e] = rl_sample_weight_f(x[j][e] - m, &f);
+                zf += f;
+                own += w[j][e];
+            }
+    }
+    uint64_t total;
+    row_sum_f_u(zf, own, total, L);  // (synchronises: the histogram is complete)
+    // log of the sum of e^(x - m) 2^24, less 24 ln 2
+    const float lse = m + (logf(zf) - 16.635532333438686f);
+
+    uint32_t tok = 0;
+    float xtok = 0.f;
+    bool found = false;  // this lane holds the token
+    bool ok = true;
+    if (m == -INFINITY) {  // every logit -inf: token 0
+        found = tid == 0;
+        xtok = x[0][0];
+    } else {
+        const uint64_t wk = total;
+        {
+            // ---- the nucleus boundary bin, then one pass: the round weights
+            // above it and its members -----------------------------------------
+            uint32_t bstar = kRowBins;  // every bin below: no truncation
+            uint64_t above = 0;
+            const uint64_t thr = trunc ? rl_topp_threshold(topp, wk) : 0ull;
+            if (trunc)
+                ok = row_hist_scan(thr, wk, bstar, above, L, bs);
+            row_fence(x);
+            row_fence(w);
+            asm volatile("" : "+v"(base));
+#pragma unroll
+            for (int j = 0; j < kRowRounds; j++) {
+                bool take[4];
+                float x4[4];
+                uint32_t w4[4], s = 0;  // < 2^26
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t b = row_bin(x[j][e] - m, scale);
+                    s += b < bstar ? w[j][e] : 0u;
+                    take[e] = b == bstar;
+                    x4[e] = x[j][e];
+                    w4[e] = w[j][e];
+                }
+                if (trunc)
+                    row_append4(take, x4, w4, base + 256u * j, L, bs);
+                L.lane_rs[wave][j][lane] = s;  // (the histogram is no longer read)
+            }
+            __syncthreads();
+            const uint32_t n = trunc ? bs.cnt[0] : 0u;
+            ok = ok && n <= (uint32_t)kRowList;
+            if (ok) {
+                // round r = 16 wave + j (index order): threads 4r .. 4r + 3
+                // add 16 lanes each
+                {
+                    const uint32_t r = tid >> 2, q = tid & 3u;
+                    const uint32_t *src = &L.lane_rs[r / kRowRounds][r % kRowRounds][q * 16u];
+                    uint32_t part = 0;  // < 2^30
+#pragma unroll
+                    for (int k = 0; k < 16; k += 4) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(src + k);
+                        part += (v.x + v.y) + (v.z + v.w);
+                    }
+                    uint64_t rs = part;
+                    rs += __shfl_xor(rs, 1);
+                    rs += __shfl_xor(rs, 2);
+                    if (q == 0)
+                        L.rsum[r] = rs;
+                }
+                if (trunc)
+                    row_rank(n, above, thr, L, bs);
+                __syncthreads();
+                uint64_t tau = 0, wp = wk;
+                if (trunc) {
+                    tau = bs.res64[0];
+                    wp = bs.res64[1];
+                    // the boundary bin's members in the nucleus join their rounds
+                    if (tid < n) {
+                        const RowEntry me = L.list[tid];
+                        if (me.ck >= tau)
+                            atomicAdd(&L.rsum[(0xFFFFFFFFu - (uint32_t)me.ck) >> 8], (unsigned long long)me.val);
+                    }
+                    __syncthreads();
+                }
+                // ---- the walk: the round where the cumulative weight first
+                // exceeds the draw, then the element in it ------------------------
+                const uint64_t u = rl_mulhi_u64(draw, wp);
+                const uint64_t rv = tid < (uint32_t)(kMergeWaves * kRowRounds) ? L.rsum[tid] : 0ull;
+                uint64_t rtot;
+                const uint64_t rex = block_excl_scan_u64_inl(rv, rtot, bs);
+                if (rex <= u && u < rex + rv) {  // exactly one round: u < W_P
+                    bs.n = tid;
+                    bs.sel64 = rex;
+                }
+                __syncthreads();
+                const uint32_t rstar = bs.n;
+                const uint64_t before = bs.sel64;
+                row_fence(x);
+                row_fence(w);
+                asm volatile("" : "+v"(base));
+                if ((uint32_t)wave == rstar / kRowRounds) {
+                    const uint32_t jstar = rstar % kRowRounds;
+                    uint32_t w4[4] = {0u, 0u, 0u, 0u};
+                    float x4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < kRowRounds; j++)
+                        if ((uint32_t)j == jstar)
+#pragma unroll
+                            for (int e = 0; e < 4; e++) {
+                                w4[e] = w[j][e];
+                                x4[e] = x[j][e];
+                            }
+                    const uint32_t i0 = base + 256u * jstar;
+                    // Nucleus membership as a bit mask: written with || and &&,
+                    // the short-circuit became divergent branches that cleared
+                    // w also for the boundary bin's members inside the nucleus.
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t b = row_bin(x4[e] - m, scale);
+                        const uint64_t ck = composite_key(rl_float_key(x4[e]), i0 + e);
+                        const uint32_t in = (uint32_t)(b < bstar) | ((uint32_t)(b == bstar) & (uint32_t)(ck >= tau));
+                        w4[e] &= 0u - in;
+                    }
+                    const uint32_t mine = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+                    uint64_t c = before + wave_inclusive_scan_u64(mine) - mine;
+                    uint32_t cand = 0xFFFFFFFFu;
+                    float xc = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        c += w4[e];
+                        if (cand == 0xFFFFFFFFu && c > u) {
+                            cand = i0 + e;
+                            xc = x4[e];
+                        }
+                    }
+                    tok = rl_wave_min_u32(cand);
+                    found = cand == tok && cand != 0xFFFFFFFFu;
+                    xtok = xc;
+                }
+            }
+        }
+    }
+    if (!ok) {  // boundary bin too full: the exact path (uniform: ok comes from LDS)
+        __syncthreads();
+        tok = exact_row_sample(p, row, inv_t, 0u, topp, m, lds.x, s_hist, s_whist, bs);
+        found = tid == 0;
+        xtok = l[tok] * inv_t;
+    }
+    if (found) {
+        p.token_out[row] = tok;
+        p.logprob_out[row] = xtok - lse;
+    }
+}
+
 uint32_t splits_for(uint32_t vocab) { return (vocab + kSplitLen - 1) / kSplitLen; }
 
 struct WsLayout {
@@ -1498,6 +1990,13 @@ extern "C" int rl_hip_sample(const rl_sample_args_t *a)
     p.stats = (SplitStat *)(ws + w.stats_off);
     p.cand = (uint2 *)(ws + w.cand_off);
 
+    // Rows without top-k whose whole row fits one workgroup's registers: the
+    // row kernel; otherwise split and merge.
+    const bool no_topk = !a->top_k && (a->top_k_all == 0 || a->top_k_all >= a->vocab);
+    if (a->vocab <= kRowVocab && (no_topk || a->greedy)) {
+        hipLaunchKernelGGL(sample_row_kernel, dim3(a->rows), dim3(kMergeThreads), 0, rl_stream(), p);
+        return rl_check_launch("sample_row_kernel launch");
+    }
     hipLaunchKernelGGL(sample_split_kernel, dim3((p.splits + kSlicesPerWg - 1) / kSlicesPerWg, a->rows),
                        dim3(kThreads), 0, rl_stream(), p);
     if (rl_check_launch("sample_split_kernel launch"))

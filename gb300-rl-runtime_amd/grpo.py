@@ -35,6 +35,7 @@ PREFIX, PRIV_MAX, GEN = 512, 512, 256
 QH, KVH, D, TPB = 32, 8, 128, 16
 HID, VOCAB = QH * D, 32000
 SLOTS = 256
+TEMPERATURE, TOP_K, TOP_P = 1.0, 0, 0.9  # every request's sampling parameters
 POOL = 8
 REQ_RING_SLOTS = 1024
 STATE_BYTES = 18464        # sizeof(GpuRolloutState)
@@ -213,6 +214,8 @@ class RolloutLoop:
         self.attn_ws = rlrt.attn_workspace(self.attn)
         s = rlrt.sample_args(dev["logits"], SLOTS, VOCAB, VOCAB, dev["tok"], dev["lp"])
         s.temperature, s.top_k, s.top_p = dev["temp"].ptr, dev["topk"].ptr, dev["topp"].ptr
+        if TOP_K == 0:  # no request uses top-k: the sampler's whole-row path takes every slot
+            s.top_k, s.top_k_all = None, 0
         s.seed, s.steps = dev["seed"].ptr, dev["step"].ptr
         self.samp = s
         self.samp_ws = rlrt.sample_workspace(s)
@@ -232,7 +235,8 @@ class RolloutLoop:
         cfg = self.cfg
         for r in range(REQ):
             req = rlrt.RolloutRequest(request_id=r, max_tokens=GEN, kv_blocks=int(cfg["n_blocks"][r]),
-                                      temperature=1.0, top_k=0, top_p=0.9, rng_seed=int(cfg["seeds"][r]))
+                                      temperature=TEMPERATURE, top_k=TOP_K, top_p=TOP_P,
+                                      rng_seed=int(cfg["seeds"][r]))
             if req_ring_push(self.rr, req) != 0:
                 raise rlrt.RlrtError("request ring full")
         if req_ring_push(self.rr, rlrt.RolloutRequest(request_id=2**64 - 1)) != 0:
@@ -256,7 +260,7 @@ class RolloutLoop:
         L.pipeline_credits_set(self.pipe.ctypes.data, decode_credits, 0, 0, 0)
         L.reward_ring_init(self.reward_ring.ctypes.data)
         self.feeder = rlrt.PipelineFeeder()
-        fp = rlrt.FeedParams(temperature=1.0, top_k=0, top_p=0.9, block_tokens=TPB)
+        fp = rlrt.FeedParams(temperature=TEMPERATURE, top_k=TOP_K, top_p=TOP_P, block_tokens=TPB)
         if L.rl_feed_init(C.byref(self.feeder), self.pipe.ctypes.data, self.rr, self.dr,
                           self.reward_ring.ctypes.data, self.rid_map.ctypes.data, REQ, C.byref(fp)) != 0:
             raise rlrt.RlrtError("rl_feed_init failed")

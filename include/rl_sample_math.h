@@ -161,6 +161,38 @@ rl_sample_weight_nb(float d)
     return d >= -87.0f ? w : 0u;
 }
 
+/* rl_sample_weight_nb with fewer operations, for d <= 0, -inf and NaN: the
+ * same range reduction and polynomial on max(d, -87) (NaN gives -87), then
+ * one multiply by 2^(n+24) in place of 2^n and 2^24, and no final select.
+ * Equal bit for bit: 2^n p is normal whenever the weight is nonzero, so the
+ * two scalings round alike, and d <= -87 weighs 0 either way. *f receives the
+ * float before the truncation, e^d 2^24 to about an ulp (about 2^-102 for
+ * d <= -87): the terms of the row's log-sum-exp. */
+RL_HD uint32_t
+rl_sample_weight_f(float d, float *f)
+{
+    RL_FP_CONTRACT_OFF
+    const float x = fmaxf(d, -87.0f);
+    const float n = floorf(x * RL_EXP_LOG2E + 0.5f);
+    float r = fmaf(-n, RL_EXP_LN2_HI, x);
+    r = fmaf(-n, RL_EXP_LN2_LO, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    union {
+        uint32_t u;
+        float f;
+    } scale;
+    scale.u = (uint32_t)((int)n + 151) << 23; /* n >= -126 here */
+    *f = p * scale.f;
+    return (uint32_t)*f;
+}
+
 /* Order-preserving u32 key of a non-NaN float; -0 and +0 share a key. */
 RL_HD uint32_t
 rl_float_key(float x)

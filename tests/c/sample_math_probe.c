@@ -15,6 +15,14 @@ void probe_weight_pair_many(const float *d, uint32_t *a, uint32_t *b, uint32_t n
         b[i] = rl_sample_weight_nb(d[i]);
     }
 }
+/* rl_sample_weight_f next to rl_sample_weight: weights a, b and b's float f */
+void probe_weight_f_many(const float *d, uint32_t *a, uint32_t *b, float *f, uint32_t n)
+{
+    for (uint32_t i = 0; i < n; i++) {
+        a[i] = rl_sample_weight(d[i]);
+        b[i] = rl_sample_weight_f(d[i], &f[i]);
+    }
+}
 uint32_t probe_key(float x) { return rl_float_key(x); }
 float probe_key_float(uint32_t k) { return rl_key_float(k); }
 uint64_t probe_topp(float p, uint64_t w) { return rl_topp_threshold(p, w); }

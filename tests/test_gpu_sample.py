@@ -114,3 +114,53 @@ def test_exact_path_edge_rows(rl, gpu, orc, olib, k):
     x[5] = np.random.default_rng(2).standard_normal(20000)
     for p in (1.0, 0.9, 0.3):
         _check(rl, orc, olib, x, temperature=0.7, top_k=k, top_p=p, seeds=np.arange(6, dtype=np.uint64) + 9, step=2)
+
+
+@pytest.mark.parametrize("vocab,stride", [(32768, 32768), (32769, 32772), (32001, 32004), (5, 8)])
+def test_row_kernel_vocab_edges(rl, gpu, orc, olib, vocab, stride):
+    """Whole-vocabulary nucleus at the row kernel's limits: 32,768 logits (the
+    largest row one workgroup holds), 32,769 (the split and merge path), a
+    row ending inside a quad, and a five-logit row; p from 0.05 to 0.999 over
+    the rows, ~N(0, 1) logits with spike ties and -inf entries."""
+    rng = np.random.default_rng(vocab)
+    rows = 24
+    x = np.full((rows, stride), np.float32(7.0))           # padding past vocab never read
+    x[:, :vocab] = rng.standard_normal((rows, vocab), dtype=np.float32)
+    x[1, :vocab:97] = np.float32(3.5)
+    x[2, rng.choice(vocab, max(1, vocab // 4), replace=False)] = -np.inf
+    seeds = rng.integers(0, 2**63, rows, dtype=np.uint64)
+    for p in (0.05, 0.5, 0.9, 0.999):
+        _check(rl, orc, olib, x, vocab=vocab, temperature=0.9, top_k=0, top_p=p, seeds=seeds, step=int(p * 1000))
+    _check(rl, orc, olib, x, vocab=vocab, greedy=True)
+
+
+def test_row_kernel_per_row_parameters(rl, gpu, orc, olib):
+    """Per-row temperature / top-p / seed / step arrays over 32,000 logits with
+    no top-k: greedy rows (temperature 0) next to nucleus rows and rows with
+    top-p 1 in one launch, every row against the oracle with its own
+    parameters."""
+    rows, V = 48, 32000
+    rng = np.random.default_rng(4242)
+    x = rng.standard_normal((rows, V), dtype=np.float32) * np.float32(0.5)
+    temp = rng.choice(np.float32([0.0, 0.6, 1.0, 1.7]), rows).astype(np.float32)
+    topp = rng.choice(np.float32([1.0, 0.95, 0.9, 0.3]), rows).astype(np.float32)
+    seeds = rng.integers(0, 2**63, rows, dtype=np.uint64)
+    steps = rng.integers(0, 2**40, rows, dtype=np.uint64)
+    bufs = [rl.DeviceBuffer.from_array(a) for a in (x, temp, topp, seeds, steps)]
+    tok, lp = rl.DeviceBuffer(rows * 4), rl.DeviceBuffer(rows * 4)
+    args = rl.sample_args(bufs[0], rows, V, V, tok, lp)
+    args.temperature, args.top_p, args.seed, args.steps = bufs[1].ptr, bufs[2].ptr, bufs[3].ptr, bufs[4].ptr
+    ws = rl.sample_workspace(args)
+    print("[sample] per-row parameters, 48 x 32000", flush=True)
+    rl.sample(args)
+    rl.sync()
+    gt, gl = tok.download(np.uint32, rows), lp.download(np.float32, rows)
+    import ctypes as C
+    lpv = C.c_double()
+    for r in range(rows):
+        want = olib.orc_sample_row(x[r].ctypes.data, V, 0, float(temp[r]), 0, float(topp[r]), int(seeds[r]),
+                                   int(steps[r]), r, C.byref(lpv))
+        assert gt[r] == want, (r, temp[r], topp[r], gt[r], want)
+        assert abs(gl[r] - lpv.value) < 1e-4, r
+    for b in bufs + [tok, lp, ws]:
+        b.close()

@@ -24,7 +24,8 @@ def sm():
                             ("probe_mulhi", u64, [u64, u64]), ("probe_expf_cw", f, [f]), ("probe_weight", u32, [f]),
                             ("probe_key", u32, [f]), ("probe_key_float", f, [u32]), ("probe_topp", u64, [f, u64]),
                             ("probe_expf_many", None, [C.c_void_p, C.c_void_p, u32]),
-                            ("probe_weight_pair_many", None, [C.c_void_p, C.c_void_p, C.c_void_p, u32])]:
+                            ("probe_weight_pair_many", None, [C.c_void_p, C.c_void_p, C.c_void_p, u32]),
+                            ("probe_weight_f_many", None, [C.c_void_p] * 4 + [u32])]:
         fn = getattr(lib, name)
         fn.restype, fn.argtypes = res, args
     return lib
@@ -120,6 +121,30 @@ def test_branch_free_weight_equals_weight(sm):
         b = np.zeros(d.size, np.uint32)
         sm.probe_weight_pair_many(d.ctypes.data, a.ctypes.data, b.ctypes.data, d.size)
         assert np.array_equal(a, b), d[np.nonzero(a != b)[0][:5]]
+
+
+def test_weight_with_float_equals_weight(sm):
+    """rl_sample_weight_f (the row kernel's form: one scaling by 2^(n+24),
+    no final select) equals rl_sample_weight bit for bit on the same sweeps
+    as above, and its float is e^d 2^24 to within 2 ulp in double for
+    d in [-87, 0] (the row kernel sums it for the log-sum-exp)."""
+    neg0, m18 = 0x80000000, int(np.float32(-18.0).view(np.uint32))
+    lo87, hi87 = int(np.float32(-86.5).view(np.uint32)), int(np.float32(-87.5).view(np.uint32))
+    pats = np.arange(neg0, 0x100000000, 997, dtype=np.uint64).astype(np.uint32)
+    dense = np.concatenate([np.arange(neg0, m18 + 1, 211, dtype=np.uint64),
+                            np.arange(lo87, hi87 + 1, dtype=np.uint64)]).astype(np.uint32)
+    for u in (pats, dense):
+        d = np.concatenate([u.view(np.float32), np.float32([0.0, -0.0, -np.inf, np.nan])])
+        a = np.zeros(d.size, np.uint32)
+        b = np.zeros(d.size, np.uint32)
+        f = np.zeros(d.size, np.float32)
+        sm.probe_weight_f_many(d.ctypes.data, a.ctypes.data, b.ctypes.data, f.ctypes.data, d.size)
+        assert np.array_equal(a, b), d[np.nonzero(a != b)[0][:5]]
+        sel = (d >= -87.0) & (d <= 0.0)
+        want = np.exp(d[sel].astype(np.float64)) * 2.0**24
+        rel = np.abs(f[sel].astype(np.float64) - want) / want
+        assert rel.max() < 2.0**-22, rel.max()
+    assert sm.probe_weight(-87.0) == 0  # (the clamp itself weighs 0)
 
 
 def test_float_key_orders_like_floats(sm):
