@@ -1443,22 +1443,23 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 // then, on LDS: the boundary member (members ranked pairwise), the per-round
 // nucleus weights (the lanes' round sums reduced through LDS, plus the
 // boundary bin's members in the nucleus), the round where the cumulative
-// weight first exceeds the draw, and the element inside it (one wave scan).
-// Bins: kRowBins over d in [0, span), span = min(m - min x, 17) (w = 0
-// beyond 16.64), a monotone map of x; u32 weight sums (a bin that wraps
-// shows as a histogram total below W and sends the row to the exact path),
-// one pad word after every 16 bins so that the scan's reads of 16
-// consecutive bins per thread hit distinct banks. The nucleus boundary is the composite key tau (x desc, index asc) at
-// which the weights ranked above tau sum to less than thr = ceil(p W) and
-// with tau to at least thr: the bin where the cumulative weight reaches thr,
-// then its members. A boundary bin with more than kRowList members (massive
-// ties) sends the row to the exact whole-row path above, which reads it
-// again from memory.
+// weight first exceeds the draw (one wave), and the element inside it (one
+// wave scan).
+// Bins: the bin coordinate t = (x - m)(-s) >= 0, s = kRowBins / span, span =
+// min(m - min x, 17) (w = 0 beyond 16.64), is a monotone function of x (two
+// correctly rounded steps); bin = min(t, kRowBins - 1) truncated. Both passes
+// compute t the same way, and the gather tests t against the boundary bin
+// as a float. u32 weight sums: a bin that wraps shows as a histogram total
+// below W and sends the row to the exact path. The nucleus boundary is the
+// composite key tau (x desc, index asc) at which the weights ranked above tau
+// sum to less than thr = ceil(p W) and with tau to at least thr: the bin
+// where the cumulative weight reaches thr, then its members. A boundary bin
+// with more than kRowList members (massive ties) sends the row to the exact
+// whole-row path above, which reads it again from memory.
 constexpr int kRowRounds = 16;
 constexpr uint32_t kRowVocab = (uint32_t)kMergeWaves * kRowRounds * 256u;  // 32,768
 constexpr int kRowBins = 8192;
-constexpr int kRowPer = kRowBins / kMergeThreads;              // bins per thread in the scan
-constexpr int kRowHistWords = kRowBins + kRowBins / kRowPer;   // with the pad words
+constexpr int kRowPer = kRowBins / kMergeThreads;  // bins per thread in the scan
 constexpr int kRowList = 256;
 
 struct RowEntry {
@@ -1469,7 +1470,7 @@ struct RowEntry {
 
 struct RowLds {
     union {
-        uint32_t hist[kRowHistWords];                    // bin b at word b + b / 16
+        uint32_t hist[kRowBins];
         uint32_t lane_rs[kMergeWaves][kRowRounds][64];  // per-lane round sums
     };
     RowEntry list[kRowList];
@@ -1493,18 +1494,18 @@ __device__ __forceinline__ void row_fence(T (&a)[kRowRounds][4])
             asm volatile("" : "+v"(a[j][e]));
 }
 
-// Bin of d = x - m <= 0 (scale = kRowBins / span, or 0): -inf and NaN fall
-// in the last bin.
-__device__ __forceinline__ uint32_t row_bin(float d, float scale)
-{
-    return (uint32_t)fminf(-d * scale, (float)(kRowBins - 1));
-}
+// Bin coordinate of x (ns = -s): 0 at the maximum, never negative; +inf for
+// -inf (s > 0).
+__device__ __forceinline__ float row_t(float x, float m, float ns) { return (x - m) * ns; }
 
-__device__ __forceinline__ uint32_t row_hist_word(uint32_t b) { return b + b / kRowPer; }
+__device__ __forceinline__ uint32_t row_bin(float t)
+{
+    return (uint32_t)fminf(t, (float)(kRowBins - 1));  // (NaN: the last bin)
+}
 
 __device__ __forceinline__ void row_clear_hist(RowLds &L)
 {
-    for (uint32_t b = threadIdx.x; b < (uint32_t)kRowHistWords / 4u; b += kMergeThreads)
+    for (uint32_t b = threadIdx.x; b < (uint32_t)kRowBins / 4u; b += kMergeThreads)
         reinterpret_cast<uint4 *>(L.hist)[b] = make_uint4(0u, 0u, 0u, 0u);
 }
 
@@ -1550,9 +1551,17 @@ __device__ __forceinline__ void row_sum_f_u(float &f, uint32_t v, uint64_t &tota
     __syncthreads();
 }
 
+// Inclusive scan of a u32 below 2^26 over the wave, exact in 64 bits: two DPP
+// scans of its high and low parts.
+__device__ __forceinline__ uint64_t row_wave_scan26(uint32_t v)
+{
+    return ((uint64_t)rl_wave_incl_scan_u32(v >> 8) << 8) + rl_wave_incl_scan_u32(v & 0xFFu);
+}
+
 // The bin where the cumulative histogram value (bins in order) reaches need,
 // and the value in the bins before it; need in [1, total]. Returns false when
 // the histogram total is not W (a bin wrapped). Also clears the list counter.
+// (Thread t reads bins 16 t .. 16 t + 15 as four 16-byte reads.)
 __device__ __forceinline__ bool row_hist_scan(uint64_t need, uint64_t W, uint32_t &bstar, uint64_t &above,
                                               RowLds &L, BlockShared &bs)
 {
@@ -1560,9 +1569,13 @@ __device__ __forceinline__ bool row_hist_scan(uint64_t need, uint64_t W, uint32_
     uint32_t h[kRowPer];
     uint64_t own = 0;
 #pragma unroll
-    for (int k = 0; k < kRowPer; k++) {
-        h[k] = L.hist[tid * (kRowPer + 1) + k];
-        own += h[k];
+    for (int k = 0; k < kRowPer; k += 4) {
+        const uint4 v = reinterpret_cast<const uint4 *>(L.hist)[(tid * kRowPer + k) / 4];
+        h[k] = v.x;
+        h[k + 1] = v.y;
+        h[k + 2] = v.z;
+        h[k + 3] = v.w;
+        own += (uint64_t)v.x + v.y + v.z + v.w;
     }
     uint64_t total;
     const uint64_t excl = block_excl_scan_u64_inl(own, total, bs);
@@ -1731,9 +1744,10 @@ __global__ __launch_bounds__(kMergeThreads) void sample_row_kernel(SampleParams 
 
     // bins over d in [0, span): the row's spread, at most 17
     const float span = fminf(m - xmin, kBinSpan);
-    const float scale = span > 0.f ? (float)kRowBins / span : 0.f;
+    const float sc = span > 0.f ? (float)kRowBins / span : 0.f;
+    const float ns = -sc;
 
-    // ---- weights, log-sum-exp terms, the first histogram ------------------------
+    // ---- weights, log-sum-exp terms, the histogram ------------------------------
     uint32_t w[kRowRounds][4];
     float zf = 0.f;
     uint32_t own = 0;  // the weight sum (< 2^31)
@@ -1742,12 +1756,11 @@ __global__ __launch_bounds__(kMergeThreads) void sample_row_kernel(SampleParams 
         for (int j = 0; j < kRowRounds; j++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float d = x[j][e] - m;
                 float f;
-                w[j][e] = rl_sample_weight_f(d, &f);
+                w[j][e] = rl_sample_weight_f(x[j][e] - m, &f);
                 zf += f;
                 own += w[j][e];
-                atomicAdd(&L.hist[row_hist_word(row_bin(d, scale))], w[j][e]);
+                atomicAdd(&L.hist[row_bin(row_t(x[j][e], m, ns))], w[j][e]);
             }
     } else {
 #pragma unroll
@@ -1774,125 +1787,133 @@ __global__ __launch_bounds__(kMergeThreads) void sample_row_kernel(SampleParams 
         xtok = x[0][0];
     } else {
         const uint64_t wk = total;
-        {
-            // ---- the nucleus boundary bin, then one pass: the round weights
-            // above it and its members -----------------------------------------
-            uint32_t bstar = kRowBins;  // every bin below: no truncation
-            uint64_t above = 0;
-            const uint64_t thr = trunc ? rl_topp_threshold(topp, wk) : 0ull;
+        // ---- the nucleus boundary bin, then one pass: the round weights above
+        // it and its members -----------------------------------------------------
+        uint32_t bstar = kRowBins;  // every bin below: no truncation
+        uint64_t above = 0;
+        const uint64_t thr = trunc ? rl_topp_threshold(topp, wk) : 0ull;
+        if (trunc)
+            ok = row_hist_scan(thr, wk, bstar, above, L, bs);
+        // t < lo: a bin below bstar (every t without truncation); lo <= t <
+        // hi: bin bstar (the last bin takes every t above it)
+        const float lo = bstar >= (uint32_t)kRowBins ? INFINITY : (float)bstar;
+        const float hi = bstar >= (uint32_t)(kRowBins - 1) ? INFINITY : (float)(bstar + 1u);
+        row_fence(x);
+        row_fence(w);
+        asm volatile("" : "+v"(base));
+#pragma unroll
+        for (int j = 0; j < kRowRounds; j++) {
+            bool take[4];
+            float x4[4];
+            uint32_t w4[4], s = 0;  // < 2^26
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float t = row_t(x[j][e], m, ns);
+                const bool below = t < lo;
+                s += below ? w[j][e] : 0u;
+                take[e] = !below && t < hi;
+                x4[e] = x[j][e];
+                w4[e] = w[j][e];
+            }
             if (trunc)
-                ok = row_hist_scan(thr, wk, bstar, above, L, bs);
+                row_append4(take, x4, w4, base + 256u * j, L, bs);
+            L.lane_rs[wave][j][lane] = s;  // (the histogram is no longer read)
+        }
+        __syncthreads();
+        const uint32_t n = trunc ? bs.cnt[0] : 0u;
+        ok = ok && n <= (uint32_t)kRowList;
+        if (ok) {
+            // round r = 16 wave + j (index order): threads 4r .. 4r + 3 add 16
+            // lanes each
+            {
+                const uint32_t r = tid >> 2, q = tid & 3u;
+                const uint32_t *src = &L.lane_rs[r / kRowRounds][r % kRowRounds][q * 16u];
+                uint32_t part = 0;  // < 2^30
+#pragma unroll
+                for (int k = 0; k < 16; k += 4) {
+                    const uint4 v = *reinterpret_cast<const uint4 *>(src + k);
+                    part += (v.x + v.y) + (v.z + v.w);
+                }
+                uint64_t rs = part;
+                rs += __shfl_xor(rs, 1);
+                rs += __shfl_xor(rs, 2);
+                if (q == 0)
+                    L.rsum[r] = rs;
+            }
+            if (trunc)
+                row_rank(n, above, thr, L, bs);
+            __syncthreads();
+            uint64_t tau = 0, wp = wk;
+            if (trunc) {
+                tau = bs.res64[0];
+                wp = bs.res64[1];
+                // the boundary bin's members in the nucleus join their rounds
+                if (tid < n) {
+                    const RowEntry me = L.list[tid];
+                    if (me.ck >= tau)
+                        atomicAdd(&L.rsum[(0xFFFFFFFFu - (uint32_t)me.ck) >> 8], (unsigned long long)me.val);
+                }
+                __syncthreads();
+            }
+            // ---- the walk: the round where the cumulative weight first exceeds
+            // the draw (wave 0: rounds 2 l and 2 l + 1 on lane l), then the
+            // element in it ----------------------------------------------------
+            const uint64_t u = rl_mulhi_u64(draw, wp);
+            if (wave == 0) {
+                const uint64_t r0 = L.rsum[2 * lane], r1 = L.rsum[2 * lane + 1];
+                const uint64_t ex = wave_inclusive_scan_u64(r0 + r1) - (r0 + r1);
+                if (ex <= u && u < ex + r0) {  // exactly one lane and round: u < W_P
+                    bs.n = 2 * lane;
+                    bs.sel64 = ex;
+                } else if (ex + r0 <= u && u < ex + r0 + r1) {
+                    bs.n = 2 * lane + 1;
+                    bs.sel64 = ex + r0;
+                }
+            }
+            __syncthreads();
+            const uint32_t rstar = bs.n;
+            const uint64_t before = bs.sel64;
             row_fence(x);
             row_fence(w);
             asm volatile("" : "+v"(base));
+            if ((uint32_t)wave == rstar / kRowRounds) {
+                const uint32_t jstar = rstar % kRowRounds;
+                uint32_t w4[4] = {0u, 0u, 0u, 0u};
+                float x4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int j = 0; j < kRowRounds; j++) {
-                bool take[4];
-                float x4[4];
-                uint32_t w4[4], s = 0;  // < 2^26
+                for (int j = 0; j < kRowRounds; j++)
+                    if ((uint32_t)j == jstar)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            w4[e] = w[j][e];
+                            x4[e] = x[j][e];
+                        }
+                const uint32_t i0 = base + 256u * jstar;
+                // Nucleus membership as a bit mask: written with || and &&,
+                // the short-circuit became divergent branches that cleared w
+                // also for the boundary bin's members inside the nucleus.
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    const uint32_t b = row_bin(x[j][e] - m, scale);
-                    s += b < bstar ? w[j][e] : 0u;
-                    take[e] = b == bstar;
-                    x4[e] = x[j][e];
-                    w4[e] = w[j][e];
+                    const float t = row_t(x4[e], m, ns);
+                    const uint64_t ck = composite_key(rl_float_key(x4[e]), i0 + e);
+                    const uint32_t in = (uint32_t)(t < lo) | ((uint32_t)(t >= lo && t < hi) & (uint32_t)(ck >= tau));
+                    w4[e] &= 0u - in;
                 }
-                if (trunc)
-                    row_append4(take, x4, w4, base + 256u * j, L, bs);
-                L.lane_rs[wave][j][lane] = s;  // (the histogram is no longer read)
-            }
-            __syncthreads();
-            const uint32_t n = trunc ? bs.cnt[0] : 0u;
-            ok = ok && n <= (uint32_t)kRowList;
-            if (ok) {
-                // round r = 16 wave + j (index order): threads 4r .. 4r + 3
-                // add 16 lanes each
-                {
-                    const uint32_t r = tid >> 2, q = tid & 3u;
-                    const uint32_t *src = &L.lane_rs[r / kRowRounds][r % kRowRounds][q * 16u];
-                    uint32_t part = 0;  // < 2^30
+                const uint32_t mine = (w4[0] + w4[1]) + (w4[2] + w4[3]);
+                uint64_t c = before + row_wave_scan26(mine) - mine;
+                uint32_t cand = 0xFFFFFFFFu;
+                float xc = 0.f;
 #pragma unroll
-                    for (int k = 0; k < 16; k += 4) {
-                        const uint4 v = *reinterpret_cast<const uint4 *>(src + k);
-                        part += (v.x + v.y) + (v.z + v.w);
+                for (int e = 0; e < 4; e++) {
+                    c += w4[e];
+                    if (cand == 0xFFFFFFFFu && c > u) {
+                        cand = i0 + e;
+                        xc = x4[e];
                     }
-                    uint64_t rs = part;
-                    rs += __shfl_xor(rs, 1);
-                    rs += __shfl_xor(rs, 2);
-                    if (q == 0)
-                        L.rsum[r] = rs;
                 }
-                if (trunc)
-                    row_rank(n, above, thr, L, bs);
-                __syncthreads();
-                uint64_t tau = 0, wp = wk;
-                if (trunc) {
-                    tau = bs.res64[0];
-                    wp = bs.res64[1];
-                    // the boundary bin's members in the nucleus join their rounds
-                    if (tid < n) {
-                        const RowEntry me = L.list[tid];
-                        if (me.ck >= tau)
-                            atomicAdd(&L.rsum[(0xFFFFFFFFu - (uint32_t)me.ck) >> 8], (unsigned long long)me.val);
-                    }
-                    __syncthreads();
-                }
-                // ---- the walk: the round where the cumulative weight first
-                // exceeds the draw, then the element in it ------------------------
-                const uint64_t u = rl_mulhi_u64(draw, wp);
-                const uint64_t rv = tid < (uint32_t)(kMergeWaves * kRowRounds) ? L.rsum[tid] : 0ull;
-                uint64_t rtot;
-                const uint64_t rex = block_excl_scan_u64_inl(rv, rtot, bs);
-                if (rex <= u && u < rex + rv) {  // exactly one round: u < W_P
-                    bs.n = tid;
-                    bs.sel64 = rex;
-                }
-                __syncthreads();
-                const uint32_t rstar = bs.n;
-                const uint64_t before = bs.sel64;
-                row_fence(x);
-                row_fence(w);
-                asm volatile("" : "+v"(base));
-                if ((uint32_t)wave == rstar / kRowRounds) {
-                    const uint32_t jstar = rstar % kRowRounds;
-                    uint32_t w4[4] = {0u, 0u, 0u, 0u};
-                    float x4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int j = 0; j < kRowRounds; j++)
-                        if ((uint32_t)j == jstar)
-#pragma unroll
-                            for (int e = 0; e < 4; e++) {
-                                w4[e] = w[j][e];
-                                x4[e] = x[j][e];
-                            }
-                    const uint32_t i0 = base + 256u * jstar;
-                    // Nucleus membership as a bit mask: written with || and &&,
-                    // the short-circuit became divergent branches that cleared
-                    // w also for the boundary bin's members inside the nucleus.
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const uint32_t b = row_bin(x4[e] - m, scale);
-                        const uint64_t ck = composite_key(rl_float_key(x4[e]), i0 + e);
-                        const uint32_t in = (uint32_t)(b < bstar) | ((uint32_t)(b == bstar) & (uint32_t)(ck >= tau));
-                        w4[e] &= 0u - in;
-                    }
-                    const uint32_t mine = (w4[0] + w4[1]) + (w4[2] + w4[3]);
-                    uint64_t c = before + wave_inclusive_scan_u64(mine) - mine;
-                    uint32_t cand = 0xFFFFFFFFu;
-                    float xc = 0.f;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        c += w4[e];
-                        if (cand == 0xFFFFFFFFu && c > u) {
-                            cand = i0 + e;
-                            xc = x4[e];
-                        }
-                    }
-                    tok = rl_wave_min_u32(cand);
-                    found = cand == tok && cand != 0xFFFFFFFFu;
-                    xtok = xc;
-                }
+                tok = rl_wave_min_u32(cand);
+                found = cand == tok && cand != 0xFFFFFFFFu;
+                xtok = xc;
             }
         }
     }
