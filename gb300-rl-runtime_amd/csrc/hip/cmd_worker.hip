@@ -302,12 +302,12 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                     __builtin_amdgcn_s_sleep(8);
                 }
             }
-            avail = rl_readlane(avail, 0);
-            ctl = rl_readlane(ctl, 0);
+            avail = rl_wave_bcast_u32(avail, 0);
+            ctl = rl_wave_bcast_u32(ctl, 0);
             uint32_t n = 0;
             if (!ctl) {
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-                const uint32_t h = rl_readlane(head, 0);
+                const uint32_t h = rl_wave_bcast_u32(head, 0);
                 // the window ends where the ring wraps or after kWindow descriptors
                 n = min(min(avail, kWindow), RING_SIZE - (h & (RING_SIZE - 1)));
                 if ((uint32_t)lane < 2 * n) {
@@ -389,10 +389,10 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                     __builtin_amdgcn_s_sleep(8);
                 }
             }
-            if (rl_readlane(room, 0)) {
+            if (rl_wave_bcast_u32(room, 0)) {
                 if (tr)
                     trace_append(tr, thead, s_desc, n, TRACE_COMPLETION_POSTED, lane);
-                const uint32_t t = rl_readlane(ctail, 0);
+                const uint32_t t = rl_wave_bcast_u32(ctail, 0);
                 // two lanes per record; records may wrap around the ring
                 if ((uint32_t)lane < 2 * n) {
                     const uint32_t rec = (uint32_t)lane / 2;

@@ -264,10 +264,10 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                     __builtin_amdgcn_s_sleep(8);
                 }
             }
-            got = rl_readlane(got, 0);
+            got = rl_wave_bcast_u32(got, 0);
             if (got) {
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-                const uint32_t h = rl_readlane(head, 0);
+                const uint32_t h = rl_wave_bcast_u32(head, 0);
                 if (lane < 16)
                     s_desc[lane] = ((const volatile uint32_t *)&cq->desc[h & HW_RING_MASK])[lane];
                 rl_wave_lds_fence();
@@ -441,8 +441,8 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                     __builtin_amdgcn_s_sleep(8);
                 }
             }
-            if (rl_readlane(room, 0)) {
-                const uint32_t t = rl_readlane(dtail, 0);
+            if (rl_wave_bcast_u32(room, 0)) {
+                const uint32_t t = rl_wave_bcast_u32(dtail, 0);
                 if (lane == 0) {
                     const uint32_t *dw = (const uint32_t *)&d;
 #pragma unroll

@@ -97,8 +97,8 @@ __global__ __launch_bounds__(64) void ring_poll_kernel(RingParams p)
     RingCtl *c = p.ctl;
     uint32_t status = c->status, head = c->head;
     if (!c->init) {
-        head = rl_readlane(lane == 0 ? sys_load(&p.cq->head) : 0u, 0);
-        const uint32_t dt = rl_readlane(lane == 0 ? sys_load(&p.dq->tail) : 0u, 0);
+        head = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.cq->head) : 0u, 0);
+        const uint32_t dt = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.dq->tail) : 0u, 0);
         if (lane == 0) {
             c->dtail = dt;
             c->init = 1;
@@ -119,12 +119,12 @@ __global__ __launch_bounds__(64) void ring_poll_kernel(RingParams p)
     rl_wave_lds_fence();
     uint64_t idle = 0;
     while (status == kRunning && taken < nfree) {
-        const uint32_t tail = rl_readlane(lane == 0 ? sys_load(&p.cq->tail) : 0u, 0);
+        const uint32_t tail = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.cq->tail) : 0u, 0);
         const uint32_t avail = tail - head;
         if (avail == 0) {
             if (active > 0)
                 break;  // rows to decode: go with them
-            const uint32_t stop = rl_readlane(lane == 0 ? sys_load(p.stop) : 0u, 0);
+            const uint32_t stop = rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0);
             if (stop) {
                 status = kStopped;
                 break;
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(64) void ring_poll_kernel(RingParams p)
     }
     if (status == kRunning && taken < nfree && active == 0) {
         // nothing admitted and nothing running: the host flag still ends the run
-        if (rl_readlane(lane == 0 ? sys_load(p.stop) : 0u, 0))
+        if (rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0))
             status = kStopped;
     }
     if (lane == 0) {
@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64) void ring_publish_kernel(RingParams p)
                 __builtin_amdgcn_s_sleep(8);
             }
         }
-        room = rl_readlane(ok, 0) != 0;
+        room = rl_wave_bcast_u32(ok, 0) != 0;
         if (!room)
             status = kDoneqFull;
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");

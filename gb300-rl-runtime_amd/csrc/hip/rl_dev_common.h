@@ -138,6 +138,17 @@ __device__ __forceinline__ uint32_t rl_readlane(uint32_t x, int lane)
     return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
 }
 
+// Wave broadcast: every lane gets lane `src`'s value (src wave-uniform), in
+// a scalar register. The ring workers use it for the values one lane reads
+// from a ring (the reference's warp_broadcast_u32 / _u64,
+// include/warp_broadcast.cuh).
+__device__ __forceinline__ uint32_t rl_wave_bcast_u32(uint32_t x, int src) { return rl_readlane(x, src); }
+
+__device__ __forceinline__ uint64_t rl_wave_bcast_u64(uint64_t x, int src)
+{
+    return ((uint64_t)rl_readlane((uint32_t)(x >> 32), src) << 32) | rl_readlane((uint32_t)x, src);
+}
+
 // Wave-uniform min / max / sum of a u32 held by every lane.
 __device__ __forceinline__ uint32_t rl_wave_min_u32(uint32_t x)
 {

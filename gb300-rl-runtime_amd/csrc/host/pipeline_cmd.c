@@ -159,14 +159,26 @@ decode_batch_run(Run *r, int drain)
         r->st->decode_batch_peak = got;
     const uint32_t tokens = r->cfg->tokens_per_rollout;
     for (uint32_t i = 0; i < got; i++) {
+        int posted = 1;
         for (uint32_t t = 0; t < tokens; t += DECODE_DESCRIPTOR_BATCH_LIMIT) {
             const uint32_t n = tokens - t < DECODE_DESCRIPTOR_BATCH_LIMIT ? tokens - t : DECODE_DESCRIPTOR_BATCH_LIMIT;
             if (dispatch_window(r, ids[i], t, n) != 0) {
                 r->st->pipeline_overflow++;
+                posted = 0;
                 break;
             }
         }
-        finish(r, ids[i]);
+        if (posted) {
+            finish(r, ids[i]);
+        } else {
+            /* part of its decode never reached the ring: no reward, no
+             * trajectory; the slot is freed and the rollout counted failed */
+            rollout_transition(rollout_get(&r->p->slab, ids[i]), ROLL_DECODING, ROLL_DONE);
+            rollout_free(&r->p->slab, ids[i]);
+            if (r->trace)
+                trace_push(r->trace, TRACE_ROLLOUT_FREE, ids[i], 0);
+            r->st->rollouts_failed++;
+        }
     }
     pipeline_release(p, Q_DECODE, got);
     return got;

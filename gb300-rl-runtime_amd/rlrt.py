@@ -141,7 +141,8 @@ class CmdPipelineStats(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
         "rollouts_started", "rollouts_completed", "rollouts_dropped", "descriptors_posted",
         "descriptors_consumed", "decode_batches", "decode_rollouts_scheduled", "decode_batch_peak",
-        "ring_full_spins", "pipeline_overflow", "reward_handoffs", "reward_ring_full", "wall_ns")]
+        "ring_full_spins", "pipeline_overflow", "reward_handoffs", "reward_ring_full", "wall_ns",
+        "rollouts_failed")]
 
 
 TRACE_RING_BYTES = 20971528  # sizeof(TraceRing)
@@ -379,6 +380,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "trace_clock_fit": (i32, [u64, C.c_double, u64, C.c_double, C.POINTER(TraceClockMap)]),
         "trace_rebase": (None, [vp, C.POINTER(TraceClockMap)]), "trace_merge": (u64, [vp, vp, u32]),
         "rl_hip_trace_clock_sample": (i32, [u32, C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64)]),
+        "rl_hip_wave_broadcast_selftest": (i32, [vp, vp, vp]),
         "reward_score_mock": (C.c_float, [vp, u32]),
         "reward_match_count": (u32, [vp, vp, u32]),
         "reward_group_advantage": (i32, [vp, u32, u32, vp]),

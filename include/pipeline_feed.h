@@ -169,6 +169,8 @@ typedef struct {
     uint64_t reward_handoffs;
     uint64_t reward_ring_full;
     uint64_t wall_ns;                /* first allocation to the last completion */
+    uint64_t rollouts_failed;        /* a window of theirs was never posted (ring full
+                                        past full_wait_ns): freed, no reward handoff */
 } rl_cmd_pipeline_stats_t;
 
 RL_EXTERN_C_BEGIN

@@ -404,6 +404,17 @@ int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *args);
  * run, feed trace_clock_fit (trace.h). samples 1..1024. */
 int rl_hip_trace_clock_sample(uint32_t samples, uint64_t *ticks, double *host_ns, uint64_t *rtt_ns);
 
+/* ---- wave broadcast self-test ---------------------------------------------
+ * The ring workers hand the values one lane reads from a ring to the whole
+ * wave with a lane broadcast (rl_wave_bcast_u32 / _u64, in place of the
+ * reference's warp_broadcast_u32 / _u64, include/warp_broadcast.cuh). This
+ * runs it in the shape of the reference's test (test/test_bench.cu:47-59,
+ * 623-656) on two 64-lane waves: in wave w, lane (w ? 37 : 0) holds seq
+ * 0x123456789ABCDEF0 + w, offset 77 + w and cookie 0x0FEDCBA987654321 ^ w,
+ * the other lanes zeros, and every lane writes what it receives to element
+ * 64 w + lane of each device array (128 entries each). Synchronous. */
+int rl_hip_wave_broadcast_selftest(uint64_t *seq_out, uint32_t *offset_out, uint64_t *cookie_out);
+
 /* ---- sampling -------------------------------------------------------------
  * Replaces sample_token (cu/sample.cu:41-123) with the specification in
  * sample.h: greedy, or temperature / top-k (k <= 256) / top-p with a

@@ -2,6 +2,7 @@
  * drive them with the same traces as the oracle and the reference build. */
 #include "completion.h"
 #include "hw_ring.h"
+#include "kv_layout.h"
 #include "request.h"
 #include "ring.h"
 
@@ -19,3 +20,7 @@ void prod_req_ring_commit(RequestRing *r) { req_ring_commit(r); }
 int prod_req_ring_consume(RequestRing *r, RolloutRequest *o) { return req_ring_consume(r, o); }
 int prod_done_ring_push(DoneRing *r, const RolloutDone *d) { return done_ring_push(r, d); }
 int prod_done_ring_pop(DoneRing *r, RolloutDone *o) { return done_ring_pop(r, o); }
+void prod_kv_layout_desc_fixed128(KvLayoutDesc *out) { *out = kv_layout_desc_fixed128(); }
+uint32_t prod_kv_layout_block_offset_bytes(uint32_t i) { return kv_layout_block_offset_bytes(i); }
+uint32_t prod_kv_layout_k_offset_bytes(uint32_t t) { return kv_layout_k_offset_bytes(t); }
+uint32_t prod_kv_layout_v_offset_bytes(uint32_t t) { return kv_layout_v_offset_bytes(t); }

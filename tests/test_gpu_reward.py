@@ -1,9 +1,11 @@
-"""Reward rule and group advantage on the device vs the host C (reward.h).
+"""Reward rule and group advantage on the device vs the oracle and the host C
+(reward.h).
 
 count = matches against the group's target at the same positions, reward =
 (count & 0xFF) / 255.0f (src/reward.c:36-41), advantage = (r - mean) / std
 with the population std in double, 0 when std is 0: floats bit-identical to
-reward_match_count / reward_group_advantage.
+the oracle's orc_match_count / orc_reward_score / orc_group_advantage and to
+the runtime's host reward_match_count / reward_group_advantage.
 """
 import ctypes as C
 
@@ -11,6 +13,19 @@ import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
+
+
+def _oracle(olib, tokens, n_tok, targets, gs, tlen):
+    R = tokens.shape[0]
+    rew = np.zeros(R, np.float32)
+    for r in range(R):
+        n = min(int(n_tok[r]), tlen, tokens.shape[1])
+        t = np.ascontiguousarray(tokens[r])
+        g = np.ascontiguousarray(targets[r // gs])
+        rew[r] = olib.orc_reward_score(olib.orc_match_count(t.ctypes.data, g.ctypes.data, n))
+    adv = np.zeros(R, np.float32)
+    olib.orc_group_advantage(rew.ctypes.data, R // gs, gs, adv.ctypes.data)
+    return rew, adv
 
 
 def _host(rl, tokens, n_tok, targets, gs, tlen):
@@ -30,7 +45,7 @@ def _host(rl, tokens, n_tok, targets, gs, tlen):
 
 @pytest.mark.parametrize("groups,gs,T,match", [(64, 8, 256, 0.3), (3, 5, 1000, 0.9), (2, 8, 40, 0.0),
                                                (4, 1, 17, 0.5)])
-def test_reward_advantage_matches_host(rl, gpu, groups, gs, T, match):
+def test_reward_advantage_matches_oracle_and_host(rl, gpu, olib, groups, gs, T, match):
     rng = np.random.default_rng(groups * 100 + gs)
     R = groups * gs
     targets = rng.integers(0, 32000, (groups, T), dtype=np.uint32)
@@ -50,7 +65,10 @@ def test_reward_advantage_matches_host(rl, gpu, groups, gs, T, match):
     rl.check(rl.lib().rl_hip_reward_advantage(C.byref(a)), "rl_hip_reward_advantage")
     rl.sync()
     hr, ha = _host(rl, tokens, n_tok, targets, gs, T)
+    orr, ora = _oracle(olib, tokens, n_tok, targets, gs, T)
     gr, ga = rew.download(np.float32, R), adv.download(np.float32, R)
+    assert np.array_equal(gr.view(np.uint32), orr.view(np.uint32))
+    assert np.array_equal(ga.view(np.uint32), ora.view(np.uint32))
     assert np.array_equal(gr.view(np.uint32), hr.view(np.uint32))
     assert np.array_equal(ga.view(np.uint32), ha.view(np.uint32))
     dd = descs.download(np.uint32, (R, 6))

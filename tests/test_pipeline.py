@@ -314,6 +314,44 @@ def test_cmd_driver_matches_bench_pipeline_loop(rl, ref, sim, n, tokens, batch_m
         assert rd.reward == np.float32((tokens & 0xFF) / 255.0)
 
 
+def test_cmd_driver_ring_never_drains(rl):
+    """No consumer on the command ring: the first 4,096 descriptors (64
+    rollouts of 64 tokens) fill it, then every window times out after
+    full_wait_ns. Those rollouts are counted failed, freed and never handed to
+    the reward ring; only the 64 fully posted ones complete, and the final
+    drain gives up (rc -1) with the pipeline left empty."""
+    L = rl.lib()
+    n, tokens = 200, 64
+    pipe = np.zeros(PIPE, np.uint8)
+    rew = np.zeros(rl.REWARD_RING_BYTES, np.uint8)
+    assert L.pipeline_init(pipe.ctypes.data) == 0
+    L.reward_ring_init(rew.ctypes.data)
+    cmd, comp = L.ring_create(), L.comp_ring_create()
+    cfg = rl.CmdPipelineCfg(n_rollouts=n, tokens_per_rollout=tokens, batch_max=32, kv_blocks=128, seed_base=42,
+                            full_wait_ns=10**6, drain_wait_ns=10**6)
+    st = rl.CmdPipelineStats()
+    try:
+        rc = L.rl_pipeline_cmd_run(pipe.ctypes.data, cmd, comp, rew.ctypes.data, C.byref(cfg), C.byref(st), None, 0,
+                                   None)
+    finally:
+        L.ring_destroy(cmd)
+        L.comp_ring_destroy(comp)
+    assert rc == -1
+    assert (st.descriptors_posted, st.descriptors_consumed) == (4096, 0)
+    assert (st.rollouts_started, st.rollouts_completed, st.rollouts_failed, st.rollouts_dropped) == (n, 64, n - 64, 0)
+    assert st.reward_handoffs == 64 and st.pipeline_overflow == n - 64
+    rd = rl.RewardDesc()
+    got = []
+    while L.reward_pop(rew.ctypes.data, C.byref(rd)) == 0:
+        got.append(rd.rollout_id)
+    assert len(got) == 64
+    snap = rl.PipelineSnapshot()
+    L.pipeline_snapshot(pipe.ctypes.data, C.byref(snap))
+    assert list(snap.queue_occupancy) == [0] * 6
+    assert (snap.credits.decode_used, snap.credits.reward_used, snap.credits.trajectory_used) == (0, 0, 0)
+    assert np.all(pipe[SLAB + 48 * MAXR:SLAB + 48 * MAXR + 1024] == 0xFF)
+
+
 def test_cmd_driver_rejects_bad_config(rl):
     L = rl.lib()
     pipe = np.zeros(PIPE, np.uint8)

@@ -282,3 +282,32 @@ def test_kv_prefix_trace(rl, olib):
         if step % 5000 == 0:
             assert np.array_equal(t0, t1), step
     assert np.array_equal(t0, t1)
+
+
+def test_kv_layout_fixed128_known_answers(prod_shim, orc):
+    """The fixed128 block math: the runtime's header against the values the
+    reference's layout bench prints (bench/bench_kv_layout.cu:20-22: block[3]
+    = 49,152, K token 7 = 1,792, V token 7 = 9,984) and the descriptor of
+    kv_layout_desc_fixed128, then against the reference's own header
+    compiled into oracle/_ref over every block and token index used."""
+    import rlrt
+
+    u32 = C.c_uint32
+    fns = {}
+    libs = [(prod_shim, "prod_")]
+    r = orc.load_ref()
+    if r is not None:
+        libs.append((r, "ref_"))
+    for lib, pre in libs:
+        fns[pre] = [_setup(lib, pre + n, u32, [u32]) for n in
+                    ("kv_layout_block_offset_bytes", "kv_layout_k_offset_bytes", "kv_layout_v_offset_bytes")]
+        d = rlrt.KvLayoutDesc()
+        _setup(lib, pre + "kv_layout_desc_fixed128", None, [C.c_void_p])(C.addressof(d))
+        assert (d.token_count, d.head_dim, d.scalar_bytes, d.vec_bytes, d.k_stride_bytes, d.v_stride_bytes,
+                d.block_bytes, d.alignment) == (32, 128, 2, 16, 256, 256, 16384, 128), pre
+        blk, k, v = fns[pre]
+        assert (blk(3), k(7), v(7)) == (49152, 1792, 9984), pre
+    if r is None:
+        pytest.skip("oracle/_ref not built: known answers checked, reference header not compared")
+    for i in range(4096):
+        assert [f(i) for f in fns["prod_"]] == [f(i) for f in fns["ref_"]], i
