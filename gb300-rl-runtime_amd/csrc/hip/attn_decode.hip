@@ -18,8 +18,10 @@
 //         global_load_lds_dwordx4 (16 B per lane, 1 KiB per instruction,
 //         coalesced), double-buffered per wave and continuing across row
 //         boundaries. Lanes fetch the 16-byte chunks of a row in XOR-permuted
-//         order (chunk c of row t lands at position c ^ t), which makes both
-//         MFMA operand reads below free of LDS bank conflicts. The query of a
+//         order (chunk c of row t lands at position c ^ t in the K plane and
+//         c ^ rotl4(t) in the V plane), which makes both MFMA operand reads
+//         below free of LDS bank conflicts (the row-major K reads and the
+//         transposed V reads need different permutations). The query of a
 //         new row rides in the same copy stream into one of two q slots.
 //  QK     v_mfma_f32_16x16x32_{bf16,f16}: A = the tile's 16 K rows, B = q^T
 //         with the G heads of the group padded to 16 columns, so each K byte
