@@ -56,24 +56,34 @@ struct ProjParams {
 // run side by side behind one L2 and W leaves HBM about once.
 constexpr uint32_t kXcds = 8;
 
-// Copies `nops` 1 KiB pieces (8 rows x 64 k each) of rows [row0, row0 + 8 *
-// total ops) x k [k0, k0 + 64) of a K-contiguous operand into an LDS tile,
-// pieces op0 .. op0 + nops - 1. Rows past `rows` re-read the last row (in
-// bounds; their results are never stored).
+// Per-lane source offsets of the `nops` 1 KiB pieces op0 .. op0 + nops - 1
+// (8 rows x 64 k each) of a tile of a K-contiguous operand, relative to the
+// tile's first row at the step's k: piece op, lane l fetches chunk
+// (l % 8) ^ (r & 7) of row r = 8 op + l / 8, so chunk c of row r lands at
+// c ^ (r & 7). Rows past `rows` re-read the last row (in bounds; their
+// results are never stored). The same for every K step: computed once.
 template <int NOPS>
-__device__ __forceinline__ void stage_rows(const uint16_t *src, uint32_t ld, uint32_t rows, uint32_t row0, uint32_t k0,
-                                           RL_LDS uint8_t *dst, int op0, int lane)
+__device__ __forceinline__ void piece_offsets(uint32_t ld, uint32_t rows, uint32_t row0, int op0, int lane,
+                                              uint32_t (&off)[NOPS])
 {
-    const uint16_t *base = src + (size_t)min(row0, rows - 1) * ld + k0;  // wave-uniform: the tile's first row
+    const uint32_t first = min(row0, rows - 1);
 #pragma unroll
     for (int j = 0; j < NOPS; j++) {
-        const int op = op0 + j;
-        const uint32_t r = (uint32_t)op * 8 + (uint32_t)lane / 8;
+        const uint32_t r = (uint32_t)(op0 + j) * 8 + (uint32_t)lane / 8;
         const uint32_t c = ((uint32_t)lane % 8) ^ (r & 7);
-        const uint16_t *rowp = src + (size_t)min(row0 + r, rows - 1) * ld + k0;
-        const uint32_t off = (uint32_t)((const uint8_t *)(rowp + c * 8) - (const uint8_t *)base);
-        rl_g2lds_16_off(base, off, dst + op * 1024);
+        off[j] = (min(row0 + r, rows - 1) - first) * ld * 2u + c * 16u;
     }
+}
+
+// Copies the pieces of one K step: base is the tile's first row at the
+// step's k (wave-uniform).
+template <int NOPS>
+__device__ __forceinline__ void stage_rows(const uint16_t *base, const uint32_t (&off)[NOPS], RL_LDS uint8_t *dst,
+                                           int op0)
+{
+#pragma unroll
+    for (int j = 0; j < NOPS; j++)
+        rl_g2lds_16_off(base, off[j], dst + (op0 + j) * 1024);
 }
 
 __global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
@@ -102,10 +112,15 @@ __global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
     // fragment addressing inside a tile: row (l % 16) of block i, chunk 4 s + l / 16
     const int fr = lane & 15;
     const int fc = lane >> 4;
+    uint32_t xoff[XOPS], woff[WOPS];
+    piece_offsets<XOPS>(p.ldx, p.M, m0, wave * XOPS, lane, xoff);
+    piece_offsets<WOPS>(p.ldw, p.N, n0, wave * WOPS, lane, woff);
+    const uint16_t *xbase = p.x + (size_t)min(m0, p.M - 1) * p.ldx;
+    const uint16_t *wbase = p.w + (size_t)min(n0, p.N - 1) * p.ldw;
     auto stage = [&](uint32_t kt) {
         const int buf = (int)(kt % NSTAGE);
-        stage_rows<XOPS>(p.x, p.ldx, p.M, m0, kt * BK, (RL_LDS uint8_t *)sX[buf], wave * XOPS, lane);
-        stage_rows<WOPS>(p.w, p.ldw, p.N, n0, kt * BK, (RL_LDS uint8_t *)sW[buf], wave * WOPS, lane);
+        stage_rows<XOPS>(xbase + kt * BK, xoff, (RL_LDS uint8_t *)sX[buf], wave * XOPS);
+        stage_rows<WOPS>(wbase + kt * BK, woff, (RL_LDS uint8_t *)sW[buf], wave * WOPS);
     };
 
     stage(0);
