@@ -1,8 +1,10 @@
 // sample.hip - on-device token sampling for gfx950 (specification: sample.h).
 //
 // Replaces the reference's serial sample_token (cu/sample.cu:41-123: one
-// thread, O(V*k) insertion top-k, xoshiro256** draw, float CDF walk) with a
-// two-kernel, HBM-streaming design:
+// thread, O(V*k) insertion top-k, xoshiro256** draw, float CDF walk) with
+// HBM-streaming kernels: batches with top-k, or vocabularies above 32,768,
+// take split + merge; the others (whole-vocabulary nucleus, greedy) one
+// workgroup per row holding the row in registers (sample_row_kernel, below).
 //
 //  split  grid (split, row): each 256-thread workgroup streams an 8,192-
 //         element slice of one row (32 fp32 per thread, 16-byte loads) and
@@ -54,8 +56,6 @@ constexpr int kCandCap = 1024;                    // candidates per split
 // the capacity, so that the lists' starts, which every slice writes and every
 // merge reads, fall on different memory channels instead of one 8 KiB period.
 constexpr int kCandStride = kCandCap + 16;
-constexpr int kWaveCand = 256;                    // candidates per wave of a split (LDS list)
-constexpr int kSlicesPerWg = 1;                   // slices of one row per split workgroup
 constexpr int kMergeCap = 8192;                   // candidates per row in the merge
 constexpr int kKeptCap = 1024;                    // kept (top-k with ties) per row
 
@@ -179,36 +179,42 @@ __device__ __forceinline__ uint32_t wave_kth_largest_key(uint32_t key, uint32_t 
     return prefix;
 }
 
-// The workgroup's LDS for one slice.
-struct SplitLds {
-    float red[4];
-    uint32_t red_i[4];
-    float z[4];
-    uint32_t key[4];
-    uint32_t wtot[4];
-    uint2 cand[4][kWaveCand];  // each wave's candidates, compacted
-};
-
-// One 8,192-element slice of a row, its quads already requested into raw:
-// the slice statistics (greedy: argmax; sampling: max and sum exp of x =
-// l * inv_t, and the candidates at or above the slice's bound).
-__device__ __forceinline__ void split_slice(const SampleParams &p, uint32_t row, uint32_t split, bool greedy,
-                                            float inv_t, const rl_f32x4 (&raw)[kPerThread / 4], uint64_t draw,
-                                            SplitLds &L)
+__global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
 {
+    const uint32_t split = blockIdx.x;
+    const uint32_t row = blockIdx.y;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    float *s_red = L.red;
-    uint32_t *s_red_i = L.red_i;
-    float *s_z = L.z;
-    uint32_t *s_key = L.key;
-    uint32_t *s_wtot = L.wtot;
-    uint2 (*s_cand)[kWaveCand] = L.cand;
+
+    __shared__ float s_red[4];
+    __shared__ uint32_t s_red_i[4];
+    __shared__ float s_z[4];
+    __shared__ uint32_t s_key[4];
+    __shared__ uint32_t s_wtot[4];
+
+    const float *lrow = p.logits + (size_t)row * p.row_stride;
     const uint32_t c0 = split * kSplitLen;
-    // Only the last slice of a row can reach past the vocabulary (a
-    // workgroup-uniform test); its quads past the end are masked to -inf.
+    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
+
+    // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
+    // Every load is issued unconditionally (a quad past the end re-reads the
+    // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
+    // masked afterwards, so all eight are in flight together. Only the last
+    // slice of a row can reach past the vocabulary (a workgroup-uniform test).
     float x[kPerThread];
+    const uint32_t last_quad = (p.vocab - 1) & ~3u;
+    rl_f32x4 raw[kPerThread / 4];
+#pragma unroll
+    for (int k = 0; k < kPerThread / 4; k++) {
+        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
+        raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
+    }
+    // the row's Philox draw, for the merge (computed while the loads are in flight)
+    uint64_t draw = 0;
+    if (split == 0 && !greedy && wave == 0)
+        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
     if (c0 + (uint32_t)kSplitLen <= p.vocab) {
 #pragma unroll
         for (int k = 0; k < kPerThread / 4; k++)
@@ -276,31 +282,13 @@ __device__ __forceinline__ void split_slice(const SampleParams &p, uint32_t row,
     }
 
     // ---- sampling: x = l * inv_t, slice max, sum exp, candidates -------------
-    // Each quad is consumed as its load lands: x, the lane's running max and
-    // its sum of exp(x - running max), rescaled when the max grows (once per
-    // quad at most), so the exponentials overlap the stream and no second
-    // pass over the slice is needed. After the last quad: the wave's k-th
-    // bound, one barrier for the wave maxima / sums / bounds, the candidate
-    // counts, a second barrier, and the candidate writes.
-    constexpr float kLog2e = 1.4426950408889634f;
-    float tmax = -INFINITY, zl = 0.f;
+    // Two barriers: (1) wave maxima and k-th bounds, (2) wave sums and
+    // candidate counts; the candidates are then written at their offsets.
+    float tmax = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kPerThread / 4; k++) {
-        float q[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            q[e] = x[k * 4 + e] * inv_t;
-            x[k * 4 + e] = q[e];
-        }
-        const float qm = fmaxf(fmaxf(q[0], q[1]), fmaxf(q[2], q[3]));
-        const float nm = fmaxf(tmax, qm);
-        // rescale the running sum to the new max (a running max of -inf has no sum yet)
-        zl = tmax == -INFINITY ? 0.f : zl * __builtin_amdgcn_exp2f((tmax - nm) * kLog2e);
-        tmax = nm;
-        const float ml = nm == -INFINITY ? 0.f : nm * kLog2e;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            zl += __builtin_amdgcn_exp2f(fmaf(q[e], kLog2e, -ml));
+    for (int i = 0; i < kPerThread; i++) {
+        x[i] = x[i] * inv_t;
+        tmax = fmaxf(tmax, x[i]);
     }
     const float wmax = wave_max(tmax);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
@@ -310,125 +298,71 @@ __device__ __forceinline__ void split_slice(const SampleParams &p, uint32_t row,
         if (lane == 0)
             s_key[wave] = ck;
     }
-    // the wave's sum relative to the wave max
-    const float wz = wave_sum(tmax == -INFINITY ? 0.f : zl * __builtin_amdgcn_exp2f((tmax - wmax) * kLog2e));
-    if (lane == 0) {
+    if (lane == 0)
         s_red[wave] = wmax;
-        s_z[wave] = wz;
-    }
     __syncthreads();
     const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float z = 0.f;
+    if (m != -INFINITY) {
+        const float ml = m * 1.4426950408889634f;
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++)
+            z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
+    }
+    z = wave_sum(z);
+    if (lane == 0)
+        s_z[wave] = z;
 
     // Candidates: key(x) >= clb and x != -inf. For x not NaN that is x >= t
     // with t = the float of clb (the key order is the float order with -0 =
     // +0), t raised to -FLT_MAX when clb is the key of -inf; a NaN x has a key
     // above every non-NaN key, and !(x < t) keeps it too.
-    // Each wave compacts its candidates into its own LDS list: one ballot per
-    // element position, and the lanes holding a candidate there take
-    // consecutive slots (mbcnt); a position without one costs a scalar branch
-    // and no store. After the barrier each wave copies its list to its offset
-    // in the slice's global list, 64 entries per store. A wave with more than
-    // kWaveCand candidates makes the slice report an overflow (the merge then
-    // takes the exact whole-row path).
-    uint32_t cand_lo = 0, wcount = 0;
+    uint32_t cand_lo = 0, cnt = 0, incl = 0;
+    float t = 0.f;
     if (k_eff != 0) {
         const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
         cand_lo = clb;
-        const float t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
-        uint2 *mine = s_cand[wave];
+        t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++)
+            cnt += !(x[i] < t) ? 1u : 0u;
+        incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off);
+            if (lane >= off)
+                incl += o;
+        }
+        if (lane == 63)
+            s_wtot[wave] = incl;
+    }
+    __syncthreads();
+    if (k_eff != 0 && cnt) {
+        uint32_t base = incl - cnt;
+        for (int w = 0; w < wave; w++)
+            base += s_wtot[w];
+        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandStride;
 #pragma unroll
         for (int k = 0; k < kPerThread / 4; k++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const float v = x[k * 4 + e];
-                const bool c = !(v < t);
-                const uint64_t bal = __ballot(c);
-                if (bal) {
-                    if (c) {
-                        const uint32_t slot = wcount + __builtin_amdgcn_mbcnt_hi(
-                                                           (uint32_t)(bal >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-                        if (slot < (uint32_t)kWaveCand)
-                            mine[slot] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
-                    }
-                    wcount += (uint32_t)__popcll(bal);
+                if (!(v < t)) {
+                    if (base < (uint32_t)kCandCap)
+                        cand[base] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                    base++;
                 }
             }
-        if (lane == 0)
-            s_wtot[wave] = wcount;
-    }
-    __syncthreads();
-    uint32_t n_cand = 0;
-    if (k_eff != 0) {
-        uint32_t base = 0;
-        bool over = false;
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const uint32_t c = s_wtot[w];
-            base += w < wave ? c : 0u;
-            n_cand += c;
-            over |= c > (uint32_t)kWaveCand;
-        }
-        if (over)
-            n_cand = kCandCap + 1u;
-        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandStride;
-        const uint2 *mine = s_cand[wave];
-        const uint32_t n = min(wcount, (uint32_t)kWaveCand);
-        for (uint32_t j = lane; j < n; j += 64)
-            if (base + j < (uint32_t)kCandCap)
-                cand[base + j] = mine[j];
     }
     if (tid == 0) {
-        float zsum = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-            zsum += s_red[w] == -INFINITY ? 0.f : s_z[w] * __builtin_amdgcn_exp2f((s_red[w] - m) * kLog2e);
         st->max_x = m;
-        st->sum_exp = zsum;
+        st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
         st->arg_val = m;
         st->arg_idx = 0;
-        st->n_cand = n_cand;
+        st->n_cand = k_eff != 0 ? s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3] : 0u;
         st->cand_lo = cand_lo;
         st->draw = draw;
     }
-}
-
-
-// Grid (slice pair, row): each workgroup takes two consecutive slices of its
-// row. Both slices' quads are requested at entry (element (k, e) of thread
-// tid in slice s is column s * 8,192 + (k * 256 + tid) * 4 + e; a quad past
-// the end re-reads the row's last quad, which row_stride % 4 == 0 keeps inside
-// the row, and is masked later), so the first slice's data lands early and
-// its reductions and candidate pass run while the second slice still streams;
-// only the second slice's tail is left at the end, with half as many waves per
-// SIMD as one slice per workgroup would leave. Slice 0 of a sampled row also
-// computes the row's Philox draw while the loads are in flight.
-__global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
-{
-    const uint32_t row = blockIdx.y;
-    const uint32_t s0 = blockIdx.x * kSlicesPerWg;
-    const int tid = threadIdx.x;
-    __shared__ SplitLds lds[kSlicesPerWg];
-
-    const float *lrow = p.logits + (size_t)row * p.row_stride;
-    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
-    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
-    const uint32_t last_quad = (p.vocab - 1) & ~3u;
-    rl_f32x4 raw[kSlicesPerWg][kPerThread / 4];
-#pragma unroll
-    for (int j = 0; j < kSlicesPerWg; j++)
-#pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++) {
-            const uint32_t col = (s0 + j) * kSplitLen + (uint32_t)(k * kThreads + tid) * 4u;
-            raw[j][k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
-        }
-    uint64_t draw = 0;
-    if (s0 == 0 && !greedy && (tid >> 6) == 0)
-        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
-#pragma unroll
-    for (int j = 0; j < kSlicesPerWg; j++)
-        if (s0 + j < p.splits)
-            split_slice(p, row, s0 + j, greedy, inv_t, raw[j], j == 0 ? draw : 0ull, lds[j]);
 }
 
 // ---- block-wide helpers of the merge (512 threads = 8 waves) ----------------
@@ -2018,7 +1952,7 @@ extern "C" int rl_hip_sample(const rl_sample_args_t *a)
         hipLaunchKernelGGL(sample_row_kernel, dim3(a->rows), dim3(kMergeThreads), 0, rl_stream(), p);
         return rl_check_launch("sample_row_kernel launch");
     }
-    hipLaunchKernelGGL(sample_split_kernel, dim3((p.splits + kSlicesPerWg - 1) / kSlicesPerWg, a->rows),
+    hipLaunchKernelGGL(sample_split_kernel, dim3(p.splits, a->rows),
                        dim3(kThreads), 0, rl_stream(), p);
     if (rl_check_launch("sample_split_kernel launch"))
         return -1;
