@@ -6,19 +6,23 @@
 // like an lm_head weight, one row of K per vocabulary entry, so both
 // operands are K-contiguous.
 //
-//  tiles   256 x 128 output tile per 512-thread workgroup (8 waves of
-//          64 x 64: 4 x 4 MFMA blocks of 16 x 16), K in steps of 64. At 256
-//          rows every W tile is read by exactly one workgroup and the grid
-//          (one workgroup per 128 vocabulary rows) fits the device in one
-//          round; X (at most 2 MiB per M tile) is read from L2.
-//  staging the X and W tiles of a K step (32 + 16 KiB) are copied HBM -> LDS
-//          with global_load_lds_dwordx4 into a 3-stage ring (144 KiB, one
-//          workgroup per CU), two steps ahead of the MFMAs, with one barrier
-//          per step; 16-byte chunk c of row r lands at chunk position
+//  tiles   one 512-thread workgroup (8 waves, 4 along M x 2 along N) per
+//          output tile, K in steps of 64:
+//          - up to 256 rows: 256 x 128 tiles, waves of 64 x 64 (4 x 4 MFMA
+//            blocks of 16 x 16), a 3-stage LDS ring (144 KiB). Every W tile
+//            is read by exactly one workgroup, and the grid (one workgroup
+//            per 128 vocabulary rows) fits the device in one round.
+//          - above 256 rows: 256 x 256 tiles, waves of 64 x 128, a 2-stage
+//            ring (128 KiB). The larger wave tile reads fewer LDS bytes per
+//            MFMA, and at 512 rows the grid is again one round.
+//          X (at most 2 MiB per M tile) is read from L2.
+//  staging the X and W tiles of a K step are copied HBM -> LDS with
+//          global_load_lds_dwordx4, NS - 1 steps ahead of the MFMAs, with one
+//          barrier per step; 16-byte chunk c of row r lands at chunk position
 //          c ^ (r & 7) (lanes fetch permuted sources), so the MFMA operand
 //          reads are free of bank conflicts.
 //  MFMA    v_mfma_f32_16x16x32_bf16: lane l reads 16 B of row l % 16 at
-//          k-chunk 4 s + l / 16 for both operands; 32 MFMAs per wave and K step.
+//          k-chunk 4 s + l / 16 for both operands.
 //  When several M tiles share a W tile, they run side by side on one XCD.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -32,15 +36,24 @@ namespace {
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 256, BN = 128, BK = 64;
+constexpr int BM = 256, BK = 64;
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int NSTAGE = 3;
-constexpr int XBYTES = BM * BK * 2;          // 32 KiB of X per step
-constexpr int WBYTES = BN * BK * 2;          // 16 KiB of W per step
-constexpr int XOPS = XBYTES / 1024 / kWaves; // 1 KiB copies per wave and step: 4 of X
-constexpr int WOPS = WBYTES / 1024 / kWaves; // ... and 2 of W
-constexpr int STEP_OPS = XOPS + WOPS;
+constexpr int kWavesM = 4, kWavesN = 2;
+constexpr int TM = BM / kWavesM / 16;        // 16-row MFMA blocks per wave along M: 4
+
+// Tile shape by TN, the 16-column MFMA blocks per wave along N.
+template <int TN>
+struct Tile {
+    static constexpr int BN = kWavesN * TN * 16;          // 128 or 256
+    static constexpr int NSTAGE = TN == 4 ? 3 : 2;        // 144 or 128 KiB of LDS
+    static constexpr int XBYTES = BM * BK * 2;            // 32 KiB of X per step
+    static constexpr int WBYTES = BN * BK * 2;            // 16 or 32 KiB of W per step
+    static constexpr int XOPS = XBYTES / 1024 / kWaves;   // 1 KiB copies per wave and step: 4 of X
+    static constexpr int WOPS = WBYTES / 1024 / kWaves;   // ... and 2 or 4 of W
+    static constexpr int STEP_OPS = XOPS + WOPS;
+    static constexpr int STAGE = XBYTES + WBYTES;
+};
 
 struct ProjParams {
     const uint16_t *x;  // [M][ldx]
@@ -52,7 +65,7 @@ struct ProjParams {
 
 // Workgroups are dispatched to the 8 XCDs round-robin (workgroup b on XCD
 // b % 8), each XCD with its own L2. The M tiles of one N tile (which share
-// the 128-row W tile) are given consecutive workgroups of one XCD, so they
+// the N tile's W rows) are given consecutive workgroups of one XCD, so they
 // run side by side behind one L2 and W leaves HBM about once.
 constexpr uint32_t kXcds = 8;
 
@@ -86,10 +99,11 @@ __device__ __forceinline__ void stage_rows(const uint16_t *base, const uint32_t 
         rl_g2lds_16_off(base, off[j], dst + (op0 + j) * 1024);
 }
 
+template <int TN>
 __global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
 {
-    __shared__ __attribute__((aligned(1024))) uint8_t sX[NSTAGE][XBYTES];
-    __shared__ __attribute__((aligned(1024))) uint8_t sW[NSTAGE][WBYTES];
+    using T = Tile<TN>;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[T::NSTAGE * T::STAGE];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -98,64 +112,71 @@ __global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
     const uint32_t nt = xcd + kXcds * (local / p.m_tiles);
     if (nt >= p.n_tiles)
         return;
-    const uint32_t m0 = mt * BM, n0 = nt * BN;
-    const int wm = wave & 3, wn = wave >> 2;
+    const uint32_t m0 = mt * BM, n0 = nt * T::BN;
+    const int wm = wave % kWavesM, wn = wave / kWavesM;
 
-    rl_f32x4 acc[4][4];
+    rl_f32x4 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int j = 0; j < TN; j++)
             acc[i][j] = rl_f32x4{0.f, 0.f, 0.f, 0.f};
 
     const uint32_t ksteps = p.K / BK;
     // fragment addressing inside a tile: row (l % 16) of block i, chunk 4 s + l / 16
     const int fr = lane & 15;
     const int fc = lane >> 4;
-    uint32_t xoff[XOPS], woff[WOPS];
-    piece_offsets<XOPS>(p.ldx, p.M, m0, wave * XOPS, lane, xoff);
-    piece_offsets<WOPS>(p.ldw, p.N, n0, wave * WOPS, lane, woff);
+    uint32_t xoff[T::XOPS], woff[T::WOPS];
+    piece_offsets<T::XOPS>(p.ldx, p.M, m0, wave * T::XOPS, lane, xoff);
+    piece_offsets<T::WOPS>(p.ldw, p.N, n0, wave * T::WOPS, lane, woff);
     const uint16_t *xbase = p.x + (size_t)min(m0, p.M - 1) * p.ldx;
     const uint16_t *wbase = p.w + (size_t)min(n0, p.N - 1) * p.ldw;
+    auto sx = [&](int b) { return (RL_LDS uint8_t *)(smem + b * T::STAGE); };
+    auto sw = [&](int b) { return (RL_LDS uint8_t *)(smem + b * T::STAGE + T::XBYTES); };
     auto stage = [&](uint32_t kt) {
-        const int buf = (int)(kt % NSTAGE);
-        stage_rows<XOPS>(xbase + kt * BK, xoff, (RL_LDS uint8_t *)sX[buf], wave * XOPS);
-        stage_rows<WOPS>(wbase + kt * BK, woff, (RL_LDS uint8_t *)sW[buf], wave * WOPS);
+        const int b = (int)(kt % T::NSTAGE);
+        stage_rows<T::XOPS>(xbase + kt * BK, xoff, sx(b), wave * T::XOPS);
+        stage_rows<T::WOPS>(wbase + kt * BK, woff, sw(b), wave * T::WOPS);
     };
 
-    stage(0);
-    if (ksteps > 1)
-        stage(1);
+#pragma unroll
+    for (int s = 0; s < T::NSTAGE - 1; s++)
+        if ((uint32_t)s < ksteps)
+            stage(s);
     for (uint32_t kt = 0; kt < ksteps; kt++) {
-        // this wave's copies of step kt have landed once at most the next
-        // step's are outstanding (copies complete in issue order)
-        if (kt + 1 < ksteps)
-            rl_wait_vmcnt<STEP_OPS>();
+        // this wave's copies of step kt have landed once at most the ones
+        // issued after them (steps kt + 1 .. kt + NSTAGE - 2) are outstanding:
+        // copies complete in issue order
+        if (T::NSTAGE == 3 && kt + 1 < ksteps)
+            rl_wait_vmcnt<(T::NSTAGE == 3 ? T::STEP_OPS : 0)>();
         else
             rl_wait_vmcnt<0>();
         // every wave's copies of step kt have landed, and every wave is done
-        // with step kt - 1, whose buffer step kt + 2 takes
+        // with step kt - 1, whose buffer step kt + NSTAGE - 1 takes
         __syncthreads();
-        if (kt + 2 < ksteps)
-            stage(kt + 2);
-        const int buf = (int)(kt % NSTAGE);
-        RL_LDS const uint8_t *xs = (RL_LDS const uint8_t *)sX[buf];
-        RL_LDS const uint8_t *ws = (RL_LDS const uint8_t *)sW[buf];
+        if (kt + T::NSTAGE - 1 < ksteps)
+            stage(kt + T::NSTAGE - 1);
+        const int buf = (int)(kt % T::NSTAGE);
+        RL_LDS const uint8_t *xs = sx(buf);
+        RL_LDS const uint8_t *ws = sw(buf);
 #pragma unroll
         for (int s = 0; s < BK / 32; s++) {
-            s16x8 af[4], bf[4];
+            s16x8 af[TM], bf[TN];
             const int c = 4 * s + fc;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int ra = wm * 64 + i * 16 + fr;
-                const int rb = wn * 64 + i * 16 + fr;
+            for (int i = 0; i < TM; i++) {
+                const int ra = wm * TM * 16 + i * 16 + fr;
                 af[i] = *(RL_LDS const s16x8 *)(xs + ra * (BK * 2) + ((c ^ (ra & 7)) << 4));
-                bf[i] = *(RL_LDS const s16x8 *)(ws + rb * (BK * 2) + ((c ^ (rb & 7)) << 4));
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int j = 0; j < TN; j++) {
+                const int rb = wn * TN * 16 + j * 16 + fr;
+                bf[j] = *(RL_LDS const s16x8 *)(ws + rb * (BK * 2) + ((c ^ (rb & 7)) << 4));
+            }
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
                                                                         __builtin_bit_cast(bf16x8, bf[j]),
                                                                         acc[i][j], 0, 0, 0);
@@ -164,20 +185,34 @@ __global__ __launch_bounds__(kThreads) void logits_proj_kernel(ProjParams p)
 
     // C block (i, j): lane holds rows 4 (l / 16) + r, column l % 16
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t m = m0 + wm * 64 + i * 16 + 4 * fc + r;
+            const uint32_t m = m0 + wm * TM * 16 + i * 16 + 4 * fc + r;
             if (m >= p.M)
                 continue;
             float *orow = p.out + (size_t)m * p.ldo;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t n = n0 + wn * 64 + j * 16 + fr;
+            for (int j = 0; j < TN; j++) {
+                const uint32_t n = n0 + wn * TN * 16 + j * 16 + fr;
                 if (n < p.N)
                     orow[n] = acc[i][j][r];
             }
         }
+}
+
+template <int TN>
+int launch_proj(ProjParams p)
+{
+    p.m_tiles = (p.M + BM - 1) / BM;
+    p.n_tiles = (p.N + Tile<TN>::BN - 1) / Tile<TN>::BN;
+    const uint64_t grid = (uint64_t)(p.n_tiles + kXcds - 1) / kXcds * kXcds * p.m_tiles;
+    if (grid > 0x7FFFFFFFull) {
+        rl_set_error("rl_hip_logits_proj: %llu workgroups", (unsigned long long)grid);
+        return -1;
+    }
+    hipLaunchKernelGGL(logits_proj_kernel<TN>, dim3((uint32_t)grid), dim3(kThreads), 0, rl_stream(), p);
+    return rl_check_launch("logits_proj_kernel launch");
 }
 
 }  // namespace
@@ -211,13 +246,7 @@ extern "C" int rl_hip_logits_proj(const rl_logits_proj_args_t *a)
     p.ldx = a->x_stride;
     p.ldw = a->w_stride;
     p.ldo = a->logits_stride;
-    p.m_tiles = (a->rows + BM - 1) / BM;
-    p.n_tiles = (a->vocab + BN - 1) / BN;
-    const uint64_t grid = (uint64_t)(p.n_tiles + kXcds - 1) / kXcds * kXcds * p.m_tiles;
-    if (grid > 0x7FFFFFFFull) {
-        rl_set_error("rl_hip_logits_proj: %llu workgroups", (unsigned long long)grid);
-        return -1;
-    }
-    hipLaunchKernelGGL(logits_proj_kernel, dim3((uint32_t)grid), dim3(kThreads), 0, rl_stream(), p);
-    return rl_check_launch("logits_proj_kernel launch");
+    // above 256 rows the 256 x 256 tile (more MFMA work per LDS byte); up to
+    // 256 rows the 256 x 128 tile, whose grid still fills the device
+    return a->rows > (uint32_t)BM ? launch_proj<8>(p) : launch_proj<4>(p);
 }

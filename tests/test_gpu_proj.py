@@ -45,8 +45,10 @@ def _case(rl, rows, vocab, hidden, seed, check_rows=None, check_cols=None, repea
         b.close()
 
 
+# up to 256 rows the 256 x 128 tile, above it the 256 x 256 tile (three M
+# tiles and a partial N tile at 700 x 777)
 @pytest.mark.parametrize("rows,vocab,hidden", [(1, 129, 64), (130, 1000, 128), (64, 32000, 256),
-                                               (257, 300, 4096)])
+                                               (257, 300, 4096), (700, 777, 192)])
 def test_projection_shapes(rl, gpu, rows, vocab, hidden):
     _case(rl, rows, vocab, hidden, seed=rows + vocab + hidden)
 
