@@ -27,6 +27,7 @@ struct AttnParams {
     uint64_t arena_blocks;  // blocks at or past this index are never read
     const uint32_t *table;
     uint32_t table_stride;
+    const uint32_t *row_map;  // [batch]: the table row (rollout) of batch row b, or NULL: b itself
     const uint32_t *ctx;
     uint32_t max_ctx;
     uint32_t batch;
@@ -157,6 +158,7 @@ struct Issuer {
     using C = Cfg<D, G, DT, TPB>;
     CtxFn cf;
     uint32_t b, g, u, nu, ctx;
+    uint32_t tb;       // table row of rollout b
     bool ctx_bad;
     bool first;
     uint32_t left;     // tiles still to issue
@@ -179,6 +181,7 @@ struct Issuer {
     __device__ __forceinline__ void set_rollout(const AttnParams &p, uint32_t nb)
     {
         b = nb;
+        tb = p.row_map ? rl_sload(p.row_map + nb) : nb;
         const uint32_t cin = cf(nb);
         ctx_bad = cin > p.max_ctx;
         ctx = ctx_bad ? p.max_ctx : cin;
@@ -188,7 +191,7 @@ struct Issuer {
     __device__ __forceinline__ void issue(const AttnParams &p, RL_LDS uint8_t *st, RL_LDS uint8_t *qslots,
                                           StageMeta &m, int lane)
     {
-        const uint32_t row = b * p.kv_heads + g;
+        const uint32_t row = tb * p.kv_heads + g;
         const uint32_t lb = u / C::SUB;
         if (row != wrow || lb < wfirst || lb >= wfirst + 128u) {
             // New row or past the window: reload 128 table entries. The wait

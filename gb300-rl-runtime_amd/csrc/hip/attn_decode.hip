@@ -335,7 +335,7 @@ extern "C" size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *a)
 
 namespace {
 
-int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap)
+int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap, const uint32_t *row_map = nullptr)
 {
     const WsLayout w = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < w.total) {
@@ -348,6 +348,7 @@ int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap)
     p.arena_blocks = a->arena_bytes / a->layout.block_bytes;
     p.table = a->block_table;
     p.table_stride = a->table_stride;
+    p.row_map = row_map;
     p.ctx = a->ctx_lens;
     p.max_ctx = a->max_ctx;
     p.batch = a->batch;
@@ -401,6 +402,19 @@ extern "C" int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv
     if (step_validate(attn, append, "rl_hip_decode_step"))
         return -1;
     return attn_run(attn, append_params(append));
+}
+
+int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                          const uint32_t *row_map)
+{
+    if (step_validate(attn, append, "rl_hip_decode_step") || !row_map) {
+        if (!row_map)
+            rl_set_error("rl_hip_decode_step: NULL row map");
+        return -1;
+    }
+    AppendParams ap = append_params(append);
+    ap.row_map = row_map;
+    return attn_run(attn, ap, row_map);
 }
 
 // ---- the decode step without allocation ---------------------------------------

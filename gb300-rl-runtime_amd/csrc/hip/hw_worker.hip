@@ -591,6 +591,7 @@ extern "C" int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *a)
     p.arena_blocks = a->arena_bytes / a->layout.block_bytes;
     p.table = a->block_table;
     p.table_stride = a->table_stride;
+    p.row_map = nullptr;
     p.ctx = nullptr;
     p.max_ctx = 0;
     p.batch = 1;

@@ -20,6 +20,7 @@ struct AppendParams {
     uint32_t row_bytes;     // K (and V) bytes per token
     const uint32_t *table;
     uint32_t table_stride;
+    const uint32_t *row_map;  // [batch]: the table row (rollout) of batch row b, or NULL: b itself
     uint32_t kv_heads;
     const uint32_t *positions;
     const int32_t *cow_src;
@@ -37,6 +38,7 @@ inline AppendParams append_params(const rl_kv_append_args_t *a)
     p.row_bytes = a->layout.k_stride_bytes;
     p.table = a->block_table;
     p.table_stride = a->table_stride;
+    p.row_map = nullptr;
     p.kv_heads = a->kv_heads;
     p.positions = a->positions;
     p.cow_src = a->cow_src;
@@ -57,7 +59,8 @@ __device__ __forceinline__ void append_row(const AppendParams &p, uint32_t b, ui
     const uint32_t slot = pos % p.token_count;
     if (pos / p.token_count >= p.table_stride)
         return;  // position outside the rollout's table row: nothing written
-    const uint32_t blk = p.table[(size_t)row_id * p.table_stride + pos / p.token_count];
+    const uint32_t trow = (p.row_map ? p.row_map[b] : b) * p.kv_heads + g;
+    const uint32_t blk = p.table[(size_t)trow * p.table_stride + pos / p.token_count];
     if (blk >= p.arena_blocks)
         return;
     uint8_t *dst = p.arena + (uint64_t)blk * p.block_bytes;

@@ -4,34 +4,37 @@
 // (cu/worker.cu:66-131) and its CPU model applies the hw_worker_sim rule per
 // descriptor (src/hw_worker_sim.c:23-59). Here up to `batch` DECODE
 // descriptors share one decode step that spreads over every compute unit,
-// in a stream-ordered pipeline the host enqueues ahead of time:
+// in a stream-ordered pipeline the host enqueues ahead of time. Per step:
 //
-//  poll     one wave drains the command ring (coherent host memory, system-
-//           scope loads) into free rows of a device row table, lowest row
-//           first, in ring order: DECODE descriptors with seq_len <
-//           max_tokens decode, those at max_tokens pass through unchanged,
-//           other opcodes are dropped, STOP ends admission. It waits (bounded)
-//           only while no row is active; once rows are active it takes what
-//           the ring holds and goes.
-//  gather   one wave per (row, kv head): the row's block-table row (by the
-//           descriptor's rollout_id) into a batch-ordered table, and the
-//           row's context (= seq_len), append position, Philox seed and
-//           counter.
-//  step     rl_hip_decode_step (paged GQA attention over all compute units,
-//           the KV append in its merge kernel) and rl_hip_sample over the
-//           batch rows.
-//  publish  one wave applies the hw_worker_sim rule for the token just
-//           decoded to every active row (seq_len++, DONE at max_tokens,
-//           NEEDS_REWARD at a multiple of 32, else the row stays for the next
-//           step), pushes the finished descriptors to the completion ring in
-//           row order (bounded wait for room) and frees their rows.
+//  turn     one wave (ring_turn_kernel). First the publish of the step just
+//           decoded: the hw_worker_sim rule for its token on every active
+//           row (seq_len++, DONE at max_tokens, NEEDS_REWARD at a multiple of
+//           32, else the row stays for the next step), the finished
+//           descriptors pushed to the completion ring in row order (bounded
+//           wait for room) and their rows freed. Then the admission: the
+//           command ring (coherent host memory, system-scope loads) drained
+//           into the free rows, lowest row first, in ring order: DECODE
+//           descriptors with seq_len < max_tokens decode, those at
+//           max_tokens pass through unchanged, other opcodes are dropped,
+//           STOP ends admission. It waits (bounded) only while no row is
+//           active; once rows are active it takes what the ring holds and
+//           goes. Last, every row's step arguments: its rollout (the
+//           block-table row the step reads), context (= seq_len), append
+//           position, Philox seed and counter. The three ring indexes and
+//           the stop flag it needs are read in one round trip, and both
+//           ring releases share one fence.
+//  step     the decode step (paged GQA attention over all compute units, the
+//           KV append in its merge kernel) reading the rollout-ordered block
+//           table through the row map, and rl_hip_sample over the batch rows.
 //
-// Each kernel boundary makes the previous kernel's writes visible on every
-// XCD, which an in-kernel hand-off between workgroups would have to buy with
-// L2 write-backs and invalidations. Waits are bounded: the poll gives up after
-// max_idle_polls empty polls (status 1), the publish after as many polls of a
-// full completion ring (status 3); a STOP, the host stop flag, an idle limit
-// or a bad rollout id end admission while active rows finish.
+// A call of `steps` steps launches steps + 1 turns: the last one only
+// publishes. Each kernel boundary makes the previous kernel's writes visible
+// on every XCD, which an in-kernel hand-off between workgroups would have to
+// buy with L2 write-backs and invalidations. Waits are bounded: the
+// admission gives up after max_idle_polls empty polls (status 1), the publish
+// after as many polls of a full completion ring (status 3); a STOP, the host
+// stop flag, an idle limit or a bad rollout id end admission while active
+// rows finish.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -61,14 +64,11 @@ struct RingParams {
     uint64_t max_idle;
     uint32_t batch;
     uint32_t rollouts;
-    uint32_t kv_heads;
-    uint32_t table_stride;
-    const uint32_t *table;      // [rollouts][kv_heads][table_stride]
     const uint64_t *seeds;      // [rollouts] or NULL (seed = rollout id)
     RingCtl *ctl;
     hw_desc_t *rows;            // [batch]
     uint32_t *kind;             // [batch]
-    uint32_t *btab;             // [batch][kv_heads][table_stride]
+    uint32_t *rmap;             // [batch] rollout of each row (the block-table row the step reads)
     uint32_t *ctx;              // [batch]
     uint32_t *pos;              // [batch]
     uint64_t *rseed;            // [batch]
@@ -82,183 +82,114 @@ __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
     return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ void sys_store_release(volatile uint32_t *p, uint32_t v)
+__device__ __forceinline__ void sys_store(volatile uint32_t *p, uint32_t v)
 {
-    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 constexpr int kMaxBatch = 1024;
 
-// One wave: admission of ring descriptors into free rows.
-__global__ __launch_bounds__(64) void ring_poll_kernel(RingParams p)
+__device__ __forceinline__ uint32_t lanes_below(uint64_t m)
+{
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
+
+// Step arguments of a row that decodes seq_len next (rollout r), or of a row
+// that does not decode.
+__device__ __forceinline__ void set_row_args(const RingParams &p, uint32_t i, bool dec, uint32_t r, uint32_t seq)
+{
+    p.ctx[i] = dec ? seq : 0u;
+    p.pos[i] = dec ? seq : 0xFFFFFFFFu;
+    p.rstep[i] = dec ? (uint64_t)seq : 0ull;
+    if (p.row_rollout)
+        p.row_rollout[i] = dec ? r : 0xFFFFFFFFu;
+}
+
+// One wave, between two decode steps: the publish of the step just decoded
+// (the hw_worker_sim rule for its token, completions in row order, finished
+// rows freed), then the admission of ring descriptors into the free rows for
+// the next step. Every row's step arguments are written where the row is
+// updated: continuing rows in the publish pass, new rows at admission, rows
+// left free at the end. The producer's tail, the consumer's head and the
+// stop flag are read together in one round trip; ring records move as
+// relaxed system-scope 8-byte accesses issued back to back; the completion
+// ring's tail and the command ring's head are released together behind one
+// fence at the end - or the completions first, when the admission has to
+// wait for the host.
+__global__ __launch_bounds__(64) void ring_turn_kernel(RingParams p, uint32_t do_publish, uint32_t do_poll)
 {
     __shared__ uint16_t s_free[kMaxBatch];  // free rows, ascending
     const uint32_t lane = threadIdx.x;
     RingCtl *c = p.ctl;
-    uint32_t status = c->status, head = c->head;
+    uint32_t status = c->status, head = c->head, dtail = c->dtail;
     if (!c->init) {
-        head = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.cq->head) : 0u, 0);
-        const uint32_t dt = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.dq->tail) : 0u, 0);
-        if (lane == 0) {
-            c->dtail = dt;
-            c->init = 1;
-        }
+        const volatile uint32_t *ia = lane == 0 ? &p.cq->head : &p.dq->tail;
+        const uint32_t iv = lane < 2 ? sys_load(ia) : 0u;
+        head = rl_wave_bcast_u32(iv, 0);
+        dtail = rl_wave_bcast_u32(iv, 1);
     }
-    // free rows in ascending order, active count
-    uint32_t nfree = 0;
-    for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
-        const uint32_t i = i0 + lane;
-        const bool f = i < p.batch && p.kind[i] == kFree;
-        const uint64_t m = __ballot(f);
-        if (f)
-            s_free[nfree + __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0))] =
-                (uint16_t)i;
-        nfree += (uint32_t)__builtin_popcountll(m);
-    }
-    uint32_t active = p.batch - nfree, taken = 0;
-    rl_wave_lds_fence();
-    uint64_t idle = 0;
-    while (status == kRunning && taken < nfree) {
-        const uint32_t tail = rl_wave_bcast_u32(lane == 0 ? sys_load(&p.cq->tail) : 0u, 0);
-        const uint32_t avail = tail - head;
-        if (avail == 0) {
-            if (active > 0)
-                break;  // rows to decode: go with them
-            const uint32_t stop = rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0);
-            if (stop) {
-                status = kStopped;
-                break;
-            }
-            if (++idle > p.max_idle) {
-                status = kIdle;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-            continue;
-        }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
-        const uint32_t take = min(min(avail, 64u), nfree - taken);
-        hw_desc_t d;
-        const bool in = lane < take;
-        if (in) {
-            const volatile rl_u32x4 *src = (const volatile rl_u32x4 *)&p.cq->desc[(head + lane) & HW_RING_MASK];
-            rl_u32x4 w[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                w[j] = src[j];
-            __builtin_memcpy(&d, w, sizeof(d));
-        } else {
-            __builtin_memset(&d, 0, sizeof(d));
-        }
-        const bool is_stop = in && d.opcode == DESC_OP_STOP;
-        const bool is_dec = in && d.opcode == DESC_OP_DECODE;
-        const bool bad = is_dec && d.rollout_id >= p.rollouts;
-        const uint64_t ends = __ballot(is_stop || bad);
-        const uint32_t f = ends ? (uint32_t)__builtin_ctzll(ends) : take;  // first STOP or bad id
-        const uint32_t consumed = ends ? f + 1 : take;
-        const bool use = is_dec && lane < f;
-        const uint64_t um = __ballot(use);
-        if (use) {
-            const uint32_t k = __builtin_amdgcn_mbcnt_hi((uint32_t)(um >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)um, 0));
-            const uint32_t row = s_free[taken + k];
-            p.rows[row] = d;
-            p.kind[row] = d.seq_len < d.max_tokens ? kDecode : kPass;
-        }
-        const uint32_t n = (uint32_t)__builtin_popcountll(um);
-        taken += n;
-        active += n;
-        head += consumed;
-        if (lane == 0)
-            sys_store_release(&p.cq->head, head);
-        if (ends) {
-            const bool was_bad = ((__ballot(bad) >> f) & 1ull) != 0;
-            status = was_bad ? kBadInput : kStopped;
-        }
-        idle = 0;
-    }
-    if (status == kRunning && taken < nfree && active == 0) {
-        // nothing admitted and nothing running: the host flag still ends the run
-        if (rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0))
-            status = kStopped;
-    }
-    if (lane == 0) {
-        c->status = status;
-        c->head = head;
-    }
-}
+    const uint32_t head0 = head;
+    // the first 64 rows, loaded before the ring indexes so that the two
+    // round trips overlap
+    const uint32_t k_first = lane < p.batch ? p.kind[lane] : kFree;
+    const hw_desc_t d_first = p.rows[lane < p.batch ? lane : 0];
+    // the command ring's tail, the completion ring's head and the stop flag
+    const volatile uint32_t *ra = lane == 0 ? &p.cq->tail : lane == 1 ? &p.dq->head : p.stop;
+    const uint32_t rv = lane < 3 ? sys_load(ra) : 0u;
+    const uint32_t cq_tail = rl_wave_bcast_u32(rv, 0);
+    const uint32_t dq_head = rl_wave_bcast_u32(rv, 1);
+    const uint32_t stop0 = rl_wave_bcast_u32(rv, 2);
 
-// One wave per (row, kv head): the batch-ordered step arguments.
-__global__ __launch_bounds__(64) void ring_gather_kernel(RingParams p)
-{
-    const uint32_t g = blockIdx.x, i = blockIdx.y, lane = threadIdx.x;
-    const uint32_t k = p.kind[i];
-    const uint32_t r = p.rows[i].rollout_id;
-    const uint32_t seq = p.rows[i].seq_len;
-    if (k == kDecode) {
-        const uint32_t *src = p.table + ((size_t)r * p.kv_heads + g) * p.table_stride;
-        uint32_t *dst = p.btab + ((size_t)i * p.kv_heads + g) * p.table_stride;
-        for (uint32_t e = lane; e < p.table_stride; e += 64)
-            dst[e] = src[e];
-    }
-    if (g == 0 && lane == 0) {
-        const bool dec = k == kDecode;
-        p.ctx[i] = dec ? seq : 0u;
-        p.pos[i] = dec ? seq : 0xFFFFFFFFu;
-        p.rseed[i] = dec ? (p.seeds ? p.seeds[r] : (uint64_t)r) : 0ull;
-        p.rstep[i] = dec ? (uint64_t)seq : 0ull;
-        if (p.row_rollout)
-            p.row_rollout[i] = dec ? r : 0xFFFFFFFFu;
-    }
-}
-
-// One wave: the hw_worker_sim rule for the decoded token, completions in row order.
-__global__ __launch_bounds__(64) void ring_publish_kernel(RingParams p)
-{
-    const uint32_t lane = threadIdx.x;
-    RingCtl *c = p.ctl;
-    uint32_t status = c->status;
-    uint32_t dtail = c->dtail;
-    // pass 1: how many rows finish, how many decoded
-    uint32_t n_done = 0, n_dec = 0;
-    for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
-        const uint32_t i = i0 + lane;
-        uint32_t k = i < p.batch ? p.kind[i] : kFree;
-        bool fin = k == kPass;
-        if (k == kDecode) {
-            const uint32_t s = p.rows[i].seq_len + 1;
-            fin = s >= p.rows[i].max_tokens || (s & 31u) == 0u;
-        }
-        n_done += (uint32_t)__builtin_popcountll(__ballot(fin));
-        n_dec += (uint32_t)__builtin_popcountll(__ballot(k == kDecode));
-    }
-    // room on the completion ring (bounded wait)
+    // ---- room on the completion ring -----------------------------------------
+    // A whole batch of completions fits (the usual case): no count needed.
+    // Otherwise count the rows that finish and wait (bounded) for their room.
     bool room = true;
-    if (n_done) {
-        uint32_t ok = 1;
-        if (lane == 0) {
-            uint64_t spin = 0;
-            while (dtail - sys_load(&p.dq->head) > HW_RING_SIZE - n_done) {
-                if (++spin > p.max_idle) {
-                    ok = 0;
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(8);
-            }
+    if (do_publish && HW_RING_SIZE - (dtail - dq_head) < p.batch) {
+        uint32_t need = 0;
+        for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
+            const uint32_t i = i0 + lane;
+            const uint32_t k = i < p.batch ? p.kind[i] : kFree;
+            const uint32_t s1 = i < p.batch ? p.rows[i].seq_len + 1 : 0u;
+            const uint32_t mt = i < p.batch ? p.rows[i].max_tokens : 0u;
+            const bool fin = k == kPass || (k == kDecode && (s1 >= mt || (s1 & 31u) == 0u));
+            need += (uint32_t)__builtin_popcountll(__ballot(fin));
         }
-        room = rl_wave_bcast_u32(ok, 0) != 0;
-        if (!room)
-            status = kDoneqFull;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+        if (need) {
+            uint32_t ok = 1;
+            if (lane == 0) {
+                uint64_t spin = 0;
+                uint32_t h = dq_head;
+                while (dtail - h > HW_RING_SIZE - need) {
+                    if (++spin > p.max_idle) {
+                        ok = 0;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(8);
+                    h = sys_load(&p.dq->head);
+                }
+            }
+            room = rl_wave_bcast_u32(ok, 0) != 0;
+            if (!room)
+                status = kDoneqFull;
+        }
     }
-    // pass 2: apply the rule, write the completions, free finished rows
-    uint32_t rank0 = 0;
+    // Every access to the rings' host memory is a system-scope atomic, which
+    // bypasses the caches, and each one is issued after the index it depends
+    // on has returned: the completions are written after the consumer's head
+    // was read, the descriptors read after the producer's tail. No cache
+    // needs invalidating for that, so the acquire sides are wavefront-scope
+    // fences (the order of this wave's own accesses).
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- publish: the rule, the completions, the free-row list ---------------
+    uint32_t nfree = 0, n_done = 0, n_dec = 0;
     for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
         const uint32_t i = i0 + lane;
-        const uint32_t k = i < p.batch ? p.kind[i] : kFree;
-        hw_desc_t d;
+        const bool valid = i < p.batch;
+        const uint32_t k = i0 == 0 ? k_first : valid ? p.kind[i] : kFree;
+        hw_desc_t d = i0 == 0 ? d_first : p.rows[valid ? i : 0];
         bool fin = false;
-        if (k != kFree) {
-            d = p.rows[i];
+        if (do_publish && k != kFree) {
             fin = k == kPass;
             if (k == kDecode) {
                 d.seq_len++;
@@ -274,32 +205,134 @@ __global__ __launch_bounds__(64) void ring_publish_kernel(RingParams p)
         }
         const uint64_t fm = __ballot(fin);
         if (fin) {
-            const uint32_t rk = rank0 + __builtin_amdgcn_mbcnt_hi((uint32_t)(fm >> 32),
-                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)fm, 0));
             if (room) {
-                volatile rl_u32x4 *dst = (volatile rl_u32x4 *)&p.dq->desc[(dtail + rk) & HW_RING_MASK];
-                rl_u32x4 w[4];
+                uint64_t w[8];
                 __builtin_memcpy(w, &d, sizeof(d));
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    dst[j] = w[j];
+                rl_sys_store_64B(&p.dq->desc[(dtail + n_done + lanes_below(fm)) & HW_RING_MASK], w);
             }
             p.kind[i] = kFree;  // a finished row is freed even when its completion is lost
+        } else if (k == kDecode) {
+            set_row_args(p, i, true, d.rollout_id, d.seq_len);  // the row decodes again
         }
-        rank0 += (uint32_t)__builtin_popcountll(fm);
+        n_done += (uint32_t)__builtin_popcountll(fm);
+        n_dec += do_publish ? (uint32_t)__builtin_popcountll(__ballot(k == kDecode)) : 0u;
+        const bool f = valid && (k == kFree || fin);
+        const uint64_t m = __ballot(f);
+        if (f)
+            s_free[nfree + lanes_below(m)] = (uint16_t)i;
+        nfree += (uint32_t)__builtin_popcountll(m);
     }
+    bool dq_pending = false;
     if (n_done && room) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
         dtail += n_done;
-        if (lane == 0)
-            sys_store_release(&p.dq->tail, dtail);
+        dq_pending = true;
+    }
+    rl_wave_lds_fence();
+
+    // ---- admission -----------------------------------------------------------
+    uint32_t active = p.batch - nfree, taken = 0;
+    if (do_poll) {
+        uint64_t idle = 0;
+        bool fresh = true;  // cq_tail and stop0 were read at entry
+        while (status == kRunning && taken < nfree) {
+            const uint32_t tail = fresh ? cq_tail : rl_wave_bcast_u32(lane == 0 ? sys_load(&p.cq->tail) : 0u, 0);
+            const uint32_t avail = tail - head;
+            if (avail == 0) {
+                if (active > 0)
+                    break;  // rows to decode: go with them
+                if (dq_pending) {
+                    // the host may wait for these completions before it submits more
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+                    if (lane == 0)
+                        sys_store(&p.dq->tail, dtail);
+                    dq_pending = false;
+                }
+                const uint32_t stop = fresh ? stop0 : rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0);
+                fresh = false;
+                if (stop) {
+                    status = kStopped;
+                    break;
+                }
+                if (++idle > p.max_idle) {
+                    status = kIdle;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(8);
+                continue;
+            }
+            fresh = false;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            const uint32_t take = min(min(avail, 64u), nfree - taken);
+            hw_desc_t d;
+            const bool in = lane < take;
+            if (in) {
+                uint64_t w[8];
+                rl_sys_load_64B(&p.cq->desc[(head + lane) & HW_RING_MASK], w);
+                __builtin_memcpy(&d, w, sizeof(d));
+            } else {
+                __builtin_memset(&d, 0, sizeof(d));
+            }
+            const bool is_stop = in && d.opcode == DESC_OP_STOP;
+            const bool is_dec = in && d.opcode == DESC_OP_DECODE;
+            const bool bad = is_dec && d.rollout_id >= p.rollouts;
+            const uint64_t ends = __ballot(is_stop || bad);
+            const uint32_t f = ends ? (uint32_t)__builtin_ctzll(ends) : take;  // first STOP or bad id
+            const uint32_t consumed = ends ? f + 1 : take;
+            const bool use = is_dec && lane < f;
+            const uint64_t um = __ballot(use);
+            if (use) {
+                const uint32_t row = s_free[taken + lanes_below(um)];
+                const bool dec = d.seq_len < d.max_tokens;
+                p.rows[row] = d;
+                p.kind[row] = dec ? kDecode : kPass;
+                p.rmap[row] = dec ? d.rollout_id : 0u;
+                p.rseed[row] = dec ? (p.seeds ? p.seeds[d.rollout_id] : (uint64_t)d.rollout_id) : 0ull;
+                set_row_args(p, row, dec, d.rollout_id, d.seq_len);
+            }
+            const uint32_t n = (uint32_t)__builtin_popcountll(um);
+            taken += n;
+            active += n;
+            head += consumed;
+            if (ends) {
+                const bool was_bad = ((__ballot(bad) >> f) & 1ull) != 0;
+                status = was_bad ? kBadInput : kStopped;
+            }
+            idle = 0;
+        }
+        if (status == kRunning && taken < nfree && active == 0) {
+            // nothing admitted and nothing running: the host flag still ends the run
+            if (rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0))
+                status = kStopped;
+        }
+    }
+
+    // ---- releases: the completions, then the consumed descriptors ------------
+    if (dq_pending || head != head0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+        if (lane == 0) {
+            if (dq_pending)
+                sys_store(&p.dq->tail, dtail);
+            if (head != head0)
+                sys_store(&p.cq->head, head);
+        }
+    }
+
+    // ---- rows left free decode nothing next step --------------------------------
+    for (uint32_t j = taken + lane; j < nfree; j += 64) {
+        const uint32_t i = s_free[j];
+        p.rmap[i] = 0u;
+        set_row_args(p, i, false, 0u, 0u);
     }
     if (lane == 0) {
+        c->init = 1;
         c->status = status;
+        c->head = head;
         c->dtail = dtail;
-        c->decoded += n_dec;
-        c->completions += room ? n_done : 0u;
-        c->steps += n_dec || n_done ? 1u : 0u;
+        if (do_publish) {
+            c->decoded += n_dec;
+            c->completions += room ? n_done : 0u;
+            c->steps += n_dec || n_done ? 1u : 0u;
+        }
         p.stats[0] = c->decoded;
         p.stats[1] = c->completions;
         p.stats[2] = c->steps;
@@ -310,7 +343,7 @@ __global__ __launch_bounds__(64) void ring_publish_kernel(RingParams p)
 // ---- host side -------------------------------------------------------------
 
 struct RingWs {
-    size_t ctl, rows, kind, btab, ctx, pos, rseed, rstep, attn, samp, total;
+    size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, attn, samp, total;
     size_t attn_bytes, samp_bytes;
 };
 
@@ -387,8 +420,8 @@ int ring_layout(const rl_ring_step_args_t *a, RingWs &w)
     w.ctl = 0;
     w.rows = 256;
     w.kind = w.rows + up256(B * sizeof(hw_desc_t));
-    w.btab = w.kind + up256(B * 4);
-    w.ctx = w.btab + up256(B * a->kv_heads * (size_t)a->table_stride * 4);
+    w.rmap = w.kind + up256(B * 4);
+    w.ctx = w.rmap + up256(B * 4);
     w.pos = w.ctx + up256(B * 4);
     w.rseed = w.pos + up256(B * 4);
     w.rstep = w.rseed + up256(B * 8);
@@ -437,14 +470,11 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
     p.max_idle = a->max_idle_polls ? a->max_idle_polls : (1ull << 22);
     p.batch = a->batch;
     p.rollouts = a->rollouts;
-    p.kv_heads = a->kv_heads;
-    p.table_stride = a->table_stride;
-    p.table = a->block_table;
     p.seeds = a->seeds;
     p.ctl = (RingCtl *)(ws + w.ctl);
     p.rows = (hw_desc_t *)(ws + w.rows);
     p.kind = (uint32_t *)(ws + w.kind);
-    p.btab = (uint32_t *)(ws + w.btab);
+    p.rmap = (uint32_t *)(ws + w.rmap);
     p.ctx = (uint32_t *)(ws + w.ctx);
     p.pos = (uint32_t *)(ws + w.pos);
     p.rseed = (uint64_t *)(ws + w.rseed);
@@ -454,18 +484,18 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
     const size_t B = a->batch;
     const size_t qrow = (size_t)a->q_heads * a->layout.head_dim * 2;
     const size_t kvrow = (size_t)a->kv_heads * a->layout.head_dim * 2;
+    if (steps == 0)
+        return 0;
     for (uint32_t n = 0; n < steps; n++) {
         const uint64_t k = first_step + n;
         const size_t si = k % a->input_slots, so = k % a->output_slots;
         p.row_rollout = a->row_rollout_out ? a->row_rollout_out + so * B : nullptr;
-        hipLaunchKernelGGL(ring_poll_kernel, dim3(1), dim3(64), 0, rl_stream(), p);
-        if (rl_check_launch("ring_poll_kernel launch"))
-            return -1;
-        hipLaunchKernelGGL(ring_gather_kernel, dim3(a->kv_heads, a->batch), dim3(64), 0, rl_stream(), p);
-        if (rl_check_launch("ring_gather_kernel launch"))
+        // publish the previous step of this call (if any), admit for this one
+        hipLaunchKernelGGL(ring_turn_kernel, dim3(1), dim3(64), 0, rl_stream(), p, n > 0 ? 1u : 0u, 1u);
+        if (rl_check_launch("ring_turn_kernel launch"))
             return -1;
         rl_attn_decode_args_t t = attn_of(a, ws + w.attn, w.attn_bytes);
-        t.block_table = p.btab;
+        t.block_table = a->block_table;
         t.ctx_lens = p.ctx;
         t.q = (const uint8_t *)a->q + si * B * qrow;
         t.out = (uint8_t *)a->attn_out + so * B * qrow;
@@ -474,7 +504,7 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         ap.arena_base = a->arena_base;
         ap.arena_bytes = a->arena_bytes;
         ap.layout = a->layout;
-        ap.block_table = p.btab;
+        ap.block_table = a->block_table;
         ap.table_stride = a->table_stride;
         ap.batch = a->batch;
         ap.kv_heads = a->kv_heads;
@@ -482,7 +512,8 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         ap.cow_src = nullptr;
         ap.k_new = (const uint8_t *)a->k_new + si * B * kvrow;
         ap.v_new = (const uint8_t *)a->v_new + si * B * kvrow;
-        if (rl_hip_decode_step(&t, &ap))
+        // batch row i reads the block-table row of the rollout it holds
+        if (rl_decode_step_mapped(&t, &ap, p.rmap))
             return -1;
         rl_sample_args_t s = samp_of(a);
         s.logits = a->logits + si * B * a->vocab;
@@ -494,9 +525,11 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         s.workspace_bytes = w.samp_bytes;
         if (rl_hip_sample(&s))
             return -1;
-        hipLaunchKernelGGL(ring_publish_kernel, dim3(1), dim3(64), 0, rl_stream(), p);
-        if (rl_check_launch("ring_publish_kernel launch"))
-            return -1;
     }
+    // publish the last step
+    p.row_rollout = nullptr;
+    hipLaunchKernelGGL(ring_turn_kernel, dim3(1), dim3(64), 0, rl_stream(), p, 1u, 0u);
+    if (rl_check_launch("ring_turn_kernel launch"))
+        return -1;
     return 0;
 }

@@ -149,6 +149,27 @@ __device__ __forceinline__ uint64_t rl_wave_bcast_u64(uint64_t x, int src)
     return ((uint64_t)rl_readlane((uint32_t)(x >> 32), src) << 32) | rl_readlane((uint32_t)x, src);
 }
 
+// One 64-byte ring record between registers and fine-grained host memory as
+// eight relaxed system-scope 8-byte accesses. They are issued back to back
+// with one wait for the loads, where a volatile access would wait for the
+// previous one to complete: four PCIe round trips for a record in 16-byte
+// volatile pieces, one here.
+__device__ __forceinline__ void rl_sys_load_64B(const void *src, uint64_t (&w)[8])
+{
+    const uint64_t *s = (const uint64_t *)src;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        w[j] = __hip_atomic_load((uint64_t *)(s + j), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ void rl_sys_store_64B(void *dst, const uint64_t (&w)[8])
+{
+    uint64_t *d = (uint64_t *)dst;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        __hip_atomic_store(d + j, w[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // Wave-uniform min / max / sum of a u32 held by every lane.
 __device__ __forceinline__ uint32_t rl_wave_min_u32(uint32_t x)
 {

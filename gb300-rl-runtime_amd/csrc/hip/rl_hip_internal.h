@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "rl_hip.h"
+
 void rl_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int rl_check_hip(hipError_t e, const char *what);
 int rl_require_open(const char *what);
@@ -15,6 +17,13 @@ int rl_device(void);
 // Takes the device address of the decode step's scratch array on `device`,
 // which must be current (attn_decode.hip). Called by rl_hip_open.
 int rl_attn_scratch_setup(int device);
+
+// rl_hip_decode_step with the block table indexed through row_map: batch row
+// b reads the table row of rollout row_map[b] (device [batch]); queries,
+// outputs, contexts, positions and new K/V rows stay batch-ordered
+// (attn_decode.hip; the ring-driven step uses it).
+int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                          const uint32_t *row_map);
 
 // Reports a launch error (or a fault of an earlier asynchronous call).
 static inline int rl_check_launch(const char *what)
