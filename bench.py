@@ -769,9 +769,12 @@ def wl_cmdring(args):
     """The v0.2 path: Descriptors in decode_batch windows of 32 through a
     CommandRing to the persistent worker (fixed128 decode step per
     descriptor: one head, d128, fp16 K/V ~N(0,1) in 16 KiB arena blocks,
-    seq_len 32, q from the q buffer) and Completions back. Pipelined: 4,096
-    descriptors submitted as fast as the ring takes them; lock-step: one
-    descriptor at a time, submit to completion."""
+    seq_len 32, q from the q buffer) and Completions back. Prefilled: 127
+    windows and the shutdown sentinel committed before the launch, the
+    persistent kernel timed with HIP events (the worker's own rate, no host in
+    the loop); pipelined: 4,096 descriptors submitted from Python as fast as
+    the ring takes them; lock-step: one descriptor at a time, submit to
+    completion."""
     import ctypes as C
 
     L = rlrt.lib()
@@ -814,6 +817,25 @@ def wl_cmdring(args):
             n += (tail - head) & 0xFFFFFFFF
             L.hw_ring_store_release(cr, tail)
 
+    # prefilled: the worker drains a full ring on its own (twice; the second
+    # pass is reported)
+    pre_windows = 127
+    timer = rlrt.Timer()
+    for _ in range(2):
+        for w in range(pre_windows):
+            if not submit(w * 32, 32):
+                raise rlrt.RlrtError("prefill: command ring full")
+        L.decode_batch_reset(C.byref(batch))
+        L.decode_batch_push(C.byref(batch), C.byref(rlrt.Descriptor(seq_id=2**64 - 1)))
+        L.decode_batch_submit(ring, C.byref(batch))
+        timer.begin()
+        rlrt.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
+        pre_ms = timer.end()
+        rlrt.sync()
+        if drain() != pre_windows * 32:
+            raise rlrt.RlrtError("prefill: completions missing")
+        pre_st = stats.download(np.uint64, 4)
+
     rlrt.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
     lat = []
     try:
@@ -847,10 +869,14 @@ def wl_cmdring(args):
     L.rl_hip_host_free(stop)
     lat_us = np.array(lat) * 1e6
     return {"workload": "cmdring_fixed128_d128_fp16_seq32_windows32", "descriptors": total,
+            "prefilled_descriptors_per_s": pre_windows * 32 / (pre_ms * 1e-3), "prefilled_ms": pre_ms,
+            "prefilled_us_per_window": pre_ms * 1e3 / pre_windows, "prefilled_worker_stats": pre_st.tolist(),
             "pipelined_descriptors_per_s": total / pipelined, "pipelined_ms": pipelined * 1e3,
             "lockstep_latency_us": {"p50": float(np.percentile(lat_us, 50)), "p90": float(np.percentile(lat_us, 90)),
                                     "p99": float(np.percentile(lat_us, 99))},
-            "worker_stats": st.tolist(), "note": "host side in Python (ctypes) on both ends of the rings"}
+            "worker_stats": st.tolist(),
+            "note": "prefilled: kernel time of one worker draining 127 committed windows; pipelined and lock-step: "
+                    "host side in Python (ctypes) on both ends of the rings"}
 
 
 def wl_rollout(args):

@@ -306,7 +306,11 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
             ctl = rl_wave_bcast_u32(ctl, 0);
             uint32_t n = 0;
             if (!ctl) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+                // The slots are read with system-scope (volatile) loads, which
+                // bypass the caches, after the tail that covers them has
+                // returned: no cache needs invalidating, so the acquire is a
+                // wavefront-scope fence.
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 const uint32_t h = rl_wave_bcast_u32(head, 0);
                 // the window ends where the ring wraps or after kWindow descriptors
                 n = min(min(avail, kWindow), RING_SIZE - (h & (RING_SIZE - 1)));
