@@ -540,16 +540,36 @@ __device__ __forceinline__ void attn_stream(const AttnParams &p, const CtxFn &cf
 // [R0, R0 + nu) of a sequence of U tiles shared by NW waves, the partials of
 // waves wf..wl at p.part[(w + row)]: M = max_w m_w, L = sum_w l_w 2^(m_w - M),
 // O = sum_w o_w 2^(m_w - M), out = O / L. Threads tid, tid + NTHR, ... of the
-// caller take the output elements; s_f / s_l hold kMergeLds * G floats and
-// s_L G floats of LDS. Returns without writing when one wave covered the row.
+// caller take the output elements (NTHR a multiple of 64); s_f holds
+// kMergeLds * G floats and s_L G floats of LDS. Returns without writing when one wave covered the row.
 constexpr int kMergeLds = 256;
 
-template <int D, int G, int DT, int NTHR>
-__device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t R0, uint32_t nu,
-                                          uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f, float *s_l,
+// Wave-wide max / sum of a float (butterfly: every lane ends with the same
+// value).
+__device__ __forceinline__ float wave_max_f32(float x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float x)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        x += __shfl_xor(x, o);
+    return x;
+}
+
+template <int D, int G, int DT, int NTHR, int GH>
+__device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, uint32_t R0,
+                                          uint32_t nu, uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f,
                                           float *s_L)
 {
+    static_assert(G % GH == 0, "head subset");
     constexpr int PART = G * D + 2 * G;
+    constexpr int NE = GH * D;  // output elements of the head subset: global element h0 * D + e
     constexpr uint32_t nthr = NTHR;
     const uint32_t row = b * p.kv_heads + g;
     const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
@@ -571,7 +591,7 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
             p.out_f32[obase + e] = v;
     };
     constexpr int NPR = 8;                              // partials merged from registers
-    constexpr int EPT = (G * D + NTHR - 1) / NTHR;      // output elements per thread
+    constexpr int EPT = (NE + NTHR - 1) / NTHR;         // output elements per thread
     if (np <= (uint32_t)NPR) {
         // few partials: every load is issued before the first use
         float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
@@ -580,17 +600,18 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
 #pragma unroll
             for (int k = 0; k < EPT; k++) {
                 const uint32_t e = tid + nthr * k;
-                const bool ok = (uint32_t)i < np && e < (uint32_t)(G * D);
+                const bool ok = (uint32_t)i < np && e < (uint32_t)NE;
                 const float *pp = part + (size_t)(ok ? i : 0) * PART;
-                const int h = (ok ? e : 0) / D;
-                o[i][k] = ok ? pp[e] : 0.f;
+                const uint32_t eg = h0 * D + (ok ? e : 0);
+                const int h = eg / D;
+                o[i][k] = ok ? pp[eg] : 0.f;
                 mm[i][k] = ok ? pp[G * D + 2 * h] : -INFINITY;
                 ll[i][k] = ok ? pp[G * D + 2 * h + 1] : 0.f;
             }
 #pragma unroll
         for (int k = 0; k < EPT; k++) {
             const uint32_t e = tid + nthr * k;
-            if (e >= (uint32_t)(G * D))
+            if (e >= (uint32_t)NE)
                 break;
             float M = -INFINITY;
 #pragma unroll
@@ -603,46 +624,85 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
                 L = fmaf(ll[i][k], f, L);
                 O = fmaf(o[i][k], f, O);
             }
-            store(e, O, L);
+            store(h0 * D + e, O, L);
         }
         return;
     }
     if (np <= (uint32_t)kMergeLds) {
-        for (uint32_t t = tid; t < np * G; t += nthr) {
-            const uint32_t i = t / G, h = t % G;
-            s_f[t] = part[(size_t)i * PART + G * D + 2 * h];
-            s_l[t] = part[(size_t)i * PART + G * D + 2 * h + 1];
-        }
-        __syncthreads();
-        if (tid < (uint32_t)G) {
-            const int h = tid;
-            float M = -INFINITY;
-            for (uint32_t i = 0; i < np; i++)
-                M = fmaxf(M, s_f[i * G + h]);
-            float L = 0.f;
-            for (uint32_t i = 0; i < np; i++) {
-                const float mi = s_f[i * G + h];
-                const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
-                s_f[i * G + h] = f;
-                L = fmaf(s_l[i * G + h], f, L);
+        // the weights 2^(m_w - M) of each head's partials: wave v takes heads
+        // h0 + v, h0 + v + NTHR / 64, ..., lane j partials j, j + 64, ... (all
+        // loaded at once), with M and L reduced across the wave
+        constexpr uint32_t nwav = nthr / 64;
+        constexpr int PL = kMergeLds / 64;  // partials per lane at most
+        const uint32_t wv = tid / 64, ln = tid % 64;
+        for (uint32_t h = h0 + wv; h < h0 + (uint32_t)GH; h += nwav) {
+            float mv[PL], lv[PL];
+#pragma unroll
+            for (int j = 0; j < PL; j++) {
+                const uint32_t i = ln + 64u * (uint32_t)j;
+                const bool ok = i < np;
+                const float *pp = part + (size_t)(ok ? i : 0) * PART + G * D + 2 * h;
+                mv[j] = ok ? pp[0] : -INFINITY;
+                lv[j] = ok ? pp[1] : 0.f;
             }
-            s_L[h] = L;
+            float M = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < PL; j++)
+                M = fmaxf(M, mv[j]);
+            M = wave_max_f32(M);
+            float L = 0.f;
+#pragma unroll
+            for (int j = 0; j < PL; j++) {
+                const uint32_t i = ln + 64u * (uint32_t)j;
+                const float f = mv[j] == -INFINITY ? 0.f : exp2f(mv[j] - M);
+                if (i < np)
+                    s_f[i * G + h] = f;
+                L = fmaf(lv[j], f, L);
+            }
+            L = wave_sum_f32(L);
+            if (ln == 0)
+                s_L[h] = L;
         }
         __syncthreads();
-        for (uint32_t e = tid; e < (uint32_t)(G * D); e += nthr) {
-            const int h = e / D;
-            float O = 0.f;
-#pragma unroll 8
-            for (uint32_t i = 0; i < np; i++)
-                O = fmaf(part[(size_t)i * PART + e], s_f[i * G + h], O);
-            store(e, O, s_L[h]);
+        // the outputs, kC partials at a time: the loads of all of a thread's
+        // elements for the chunk (16 in all) are issued before the first use
+        constexpr int kC = EPT >= 8 ? 2 : 16 / EPT;
+        float O[EPT];
+#pragma unroll
+        for (int k = 0; k < EPT; k++)
+            O[k] = 0.f;
+        for (uint32_t i0 = 0; i0 < np; i0 += kC) {
+            float v[kC][EPT];
+#pragma unroll
+            for (int c = 0; c < kC; c++)
+#pragma unroll
+                for (int k = 0; k < EPT; k++) {
+                    const uint32_t i = i0 + (uint32_t)c, e = tid + nthr * (uint32_t)k;
+                    const bool ok = i < np && e < (uint32_t)NE;
+                    v[c][k] = ok ? part[(size_t)i * PART + h0 * D + e] : 0.f;
+                }
+#pragma unroll
+            for (int c = 0; c < kC; c++)
+#pragma unroll
+                for (int k = 0; k < EPT; k++) {
+                    const uint32_t i = i0 + (uint32_t)c, e = tid + nthr * (uint32_t)k;
+                    if (i < np && e < (uint32_t)NE)
+                        O[k] = fmaf(v[c][k], s_f[i * G + h0 + e / D], O[k]);
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < EPT; k++) {
+            const uint32_t e = tid + nthr * (uint32_t)k;
+            if (e < (uint32_t)NE)
+                store(h0 * D + e, O[k], s_L[h0 + e / D]);
         }
         __syncthreads();
         return;
     }
     // very long rows: stream the partials per element
-    for (uint32_t e = tid; e < (uint32_t)(G * D); e += nthr) {
-        const int h = e / D;
+    for (uint32_t e = tid; e < (uint32_t)NE; e += nthr) {
+        const uint32_t eg = h0 * D + e;
+        const int h = eg / D;
         float M = -INFINITY;
         for (uint32_t i = 0; i < np; i++)
             M = fmaxf(M, part[(size_t)i * PART + G * D + 2 * h]);
@@ -652,19 +712,20 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
             const float mi = pp[G * D + 2 * h];
             const float f = mi == -INFINITY ? 0.f : exp2f(mi - M);
             L = fmaf(pp[G * D + 2 * h + 1], f, L);
-            O = fmaf(pp[e], f, O);
+            O = fmaf(pp[eg], f, O);
         }
-        store(e, O, L);
+        store(eg, O, L);
     }
 }
 
-// Writes a row without tiles: zeros (ctx 0) or NaN (ctx beyond max_ctx).
-template <int D, int G, int DT>
-__device__ __forceinline__ void empty_row(const AttnParams &p, uint32_t b, uint32_t g, bool bad, uint32_t tid,
-                                          uint32_t nthr)
+// Writes heads h0 .. h0 + GH - 1 of a row without tiles: zeros (ctx 0) or
+// NaN (ctx beyond max_ctx).
+template <int D, int G, int DT, int GH>
+__device__ __forceinline__ void empty_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, bool bad,
+                                          uint32_t tid, uint32_t nthr)
 {
-    const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
-    for (uint32_t e = tid; e < (uint32_t)(G * D); e += nthr) {
+    const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G + h0) * D;
+    for (uint32_t e = tid; e < (uint32_t)(GH * D); e += nthr) {
         const float v = bad ? __builtin_nanf("") : 0.f;
         if (p.out)
             p.out[obase + e] = rl_from_f32<DT>(v);

@@ -162,36 +162,45 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
 }
 
 // Combines the partials of every row split across waves (merge_row) and
-// writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN). In a
-// fused decode step (ap.arena set) the workgroup of row (b, g) also appends
-// that row's new K/V token: attn_decode_kernel has read every context
-// already, and the merge reads only the partials.
-template <int D, int G, int DT>
+// writes rows without tiles (ctx 0: zeros; ctx beyond max_ctx: NaN). With
+// HS > 1 each row's heads are shared by HS workgroups of G / HS heads
+// (workgroup x of the grid: kv head x / HS, heads (x % HS) G / HS ... of its
+// group), so the many partials of long rows are read through that many
+// compute units. In a fused decode step (ap.arena set) the first workgroup
+// of row (b, g) also appends that row's new K/V token: attn_decode_kernel has
+// read every context already, and the merge reads only the partials.
+template <int G>
+constexpr int merge_heads_of()
+{
+    return G >= 2 ? G / 2 : 1;
+}
+
+template <int D, int G, int DT, int HS>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, AppendParams ap)
 {
+    constexpr int GH = G / HS;
     __shared__ float s_f[kMergeLds * G];
-    __shared__ float s_l[kMergeLds * G];
     __shared__ float s_L[G];
-    const uint32_t g = blockIdx.x;
+    const uint32_t g = blockIdx.x / HS;
+    const uint32_t h0 = (blockIdx.x % HS) * GH;
     const uint32_t b = blockIdx.y;
     // the three values the row's partials are located by, loaded together
     // (cum has batch + 1 entries whatever the context)
     const uint32_t cin = rl_sload(p.ctx + b);
     const uint32_t U = rl_sload(p.cum + p.batch);
     const uint32_t cum_b = rl_sload(p.cum + b);
-    if (ap.arena && threadIdx.x >= 192)
+    if (ap.arena && h0 == 0 && threadIdx.x >= 192)
         append_row(ap, b, g, threadIdx.x - 192, 64);
     const bool bad = cin > p.max_ctx;
     const uint32_t nu = tiles_of(p, cin);
     if (nu == 0) {
-        empty_row<D, G, DT>(p, b, g, bad, threadIdx.x, 256);
+        empty_row<D, G, DT, GH>(p, b, g, h0, bad, threadIdx.x, 256);
         return;
     }
     const uint32_t NW = min(p.nwaves, U);  // U > 0: this row has tiles
     const uint32_t R0 = cum_b + g * nu;
-    merge_row<D, G, DT, 256>(p, b, g, R0, nu, U, NW, bad, threadIdx.x, s_f, s_l, s_L);
+    merge_row<D, G, DT, 256, GH>(p, b, g, h0, R0, nu, U, NW, bad, threadIdx.x, s_f, s_L);
 }
-
 }  // namespace
 
 // ---- launcher ------------------------------------------------------------------
@@ -241,8 +250,16 @@ int launch(const AttnParams &p, const AppendParams &ap)
     hipLaunchKernelGGL((attn_decode_kernel<D, G, DT, TPB>), dim3(wgs), dim3(C::W * 64), 0, rl_stream(), p);
     if (rl_check_launch("attn_decode_kernel launch"))
         return -1;
-    hipLaunchKernelGGL((attn_merge_kernel<D, G, DT>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(), p,
-                       ap);
+    // Rows averaging 8 or more partials (waves per row) take workgroups of
+    // two heads; shorter rows one workgroup per row, whose partials arrive
+    // in one batch of loads.
+    constexpr int HS = merge_heads_of<G>();
+    if (HS > 1 && (uint64_t)p.nwaves >= 8ull * p.batch * p.kv_heads)
+        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, HS>), dim3(p.kv_heads * HS, p.batch), dim3(256), 0,
+                           rl_stream(), p, ap);
+    else
+        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, 1>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(),
+                           p, ap);
     return rl_check_launch("attn_merge_kernel launch");
 }
 

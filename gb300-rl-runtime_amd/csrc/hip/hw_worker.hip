@@ -208,7 +208,6 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
     __shared__ __attribute__((aligned(1024))) uint8_t lds_st[NS][W * C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * NS * C::QSLOT];
     __shared__ float s_f[kMergeLds * G];
-    __shared__ float s_l[kMergeLds * G];
     __shared__ float s_L[G];
     __shared__ uint32_t s_desc[16];
     __shared__ uint32_t s_out[16];
@@ -320,7 +319,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
             const uint32_t U = kvh * nu;
             if (U == 0) {
                 for (uint32_t g = 0; g < kvh; g++)
-                    empty_row<D, G, DT>(a, 0, g, false, tid, kWorkerThreads);
+                    empty_row<D, G, DT, G>(a, 0, g, 0, false, tid, kWorkerThreads);
             } else {
                 const uint32_t NW = min((uint32_t)W, U);
                 if ((uint32_t)wave < NW) {
@@ -330,7 +329,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                 }
                 __syncthreads();
                 for (uint32_t g = 0; g < kvh; g++)
-                    merge_row<D, G, DT, kWorkerThreads>(a, 0, g, g * nu, nu, U, NW, false, tid, s_f, s_l, s_L);
+                    merge_row<D, G, DT, kWorkerThreads, G>(a, 0, g, 0, g * nu, nu, U, NW, false, tid, s_f, s_L);
             }
 
             // greedy token (lowest index among maxima) and its logprob: one
