@@ -99,7 +99,9 @@ def make_decode(seed: int, batch: int, q_heads: int, kv_heads: int, head_dim: in
                 ctx: np.ndarray | None = None, spare_blocks: int = 0,
                 reserve_tokens: int = 0) -> DecodeWorkload:
     """Ragged contexts uniform in [ctx_lo, ctx_hi] (or given), permuted blocks;
-    every row owns blocks for max(ctx + 1, reserve_tokens) tokens."""
+    every row owns blocks for max(ctx + 1, reserve_tokens) tokens. The
+    spare_blocks spare blocks are the last ids of the arena, owned by no row
+    (copy-on-write sources read while rows append)."""
     rng = np.random.default_rng(seed)
     if ctx is None:
         ctx = rng.integers(ctx_lo, ctx_hi + 1, size=batch, dtype=np.int64)
@@ -108,8 +110,9 @@ def make_decode(seed: int, batch: int, q_heads: int, kv_heads: int, head_dim: in
     cap = max(cap, reserve_tokens - 1)
     stride = max(1, -(-(cap + 1) // token_count))
     nblk = -(-np.maximum(ctx.astype(np.int64) + 1, reserve_tokens) // token_count)  # blocks per (b, g)
-    total = int(nblk.sum()) * kv_heads + spare_blocks
-    perm = rng.permutation(total).astype(np.uint32)
+    owned = int(nblk.sum()) * kv_heads
+    total = owned + spare_blocks
+    perm = rng.permutation(total if spare_blocks == 0 else owned).astype(np.uint32)
     table = np.zeros((batch, kv_heads, stride), dtype=np.uint32)
     k = 0
     for b in range(batch):

@@ -450,3 +450,19 @@ def test_plumbing_cpu_path_equals_sequential_oracle(orc, olib):
         olib.orc_kv_append(host.ctypes.data, w.block_bytes, 16, 128, w.table.ctypes.data, w.table_stride, 1, 8,
                            pos.ctypes.data, None, k_row.ctypes.data, v_row.ctypes.data)
     assert np.array_equal(arena, host)
+
+
+def test_decode_workload_spare_blocks_owned_by_no_row():
+    """The synthetic decode workload's spare blocks (the copy-on-write sources
+    of the append tests) are the arena's last ids and no row's table holds
+    them; every owned block belongs to exactly one (rollout, kv head, block)."""
+    import synth
+
+    for spare in (0, 8, 40):
+        w = synth.make_decode(31, 24, 32, 8, 128, 200, 1500, spare_blocks=spare)
+        total = w.arena.size // w.block_bytes
+        nblk = -(-(w.ctx.astype(np.int64) + 1) // w.token_count)
+        owned = np.concatenate([w.table[b, g, :nblk[b]] for b in range(w.batch) for g in range(w.table.shape[1])])
+        assert len(np.unique(owned)) == len(owned)
+        assert owned.max() < total - spare
+        assert total - spare == len(owned)
