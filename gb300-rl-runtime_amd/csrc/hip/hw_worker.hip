@@ -2,7 +2,7 @@
 //
 // Replaces the CPU worker hw_worker_sim_run (src/hw_worker_sim.c:23-59) and
 // the reference's per-SM device worker (cu/worker.cu:66-131) with one
-// persistent workgroup (4 wave64s) per ring pair. Each workgroup is the
+// persistent workgroup (8 wave64s) per ring pair. Each workgroup is the
 // single consumer of its command ring and the single producer of its
 // completion ring, both in fine-grained coherent host memory, so the SPSC
 // contract of hw_ring.h holds on the device side too:
@@ -14,7 +14,7 @@
 //          max_tokens: one decode step, seq_len++, stop at max_tokens (DONE)
 //          or at a multiple of 32 (NEEDS_REWARD) - with a real step for every
 //          token: paged attention of the rollout over its seq_len tokens (the
-//          batched kernel's MFMA tile stream, four waves, split rows merged in
+//          batched kernel's MFMA tile stream, eight waves, split rows merged in
 //          the workgroup), the greedy token and its logprob over the step's
 //          logits, and the append of the step's K/V token at position seq_len.
 //  publish thread 0 writes the updated descriptor into the completion ring
@@ -37,7 +37,8 @@
 
 namespace {
 
-constexpr int kWorkerThreads = 256;
+constexpr int kWorkerWavesMax = 8;  // a step's tiles are shared by up to this many waves
+constexpr int kWorkerThreadsMax = kWorkerWavesMax * 64;
 constexpr uint64_t kDefaultIdlePolls = 1ull << 22;
 
 enum : uint32_t {
@@ -65,7 +66,7 @@ struct WorkerParams {
     uint32_t *token_out;
     float *logprob_out;
     uint64_t *stats;
-    float *part;  // [groups][W + kv_heads][G * D + 2 * G]
+    float *part;  // [groups][kWorkerWavesMax + kv_heads][G * D + 2 * G]
 };
 
 __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
@@ -101,7 +102,7 @@ __device__ __forceinline__ float wave_sum_f(float v)
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kGreedyBatch = 16;  // 16-byte loads in flight per thread
+constexpr int kGreedyBatch = 8;  // 16-byte loads in flight per thread
 
 // Folds a batch of n values (at indices idx[j], increasing) into a running
 // (best, bidx, z): best the max, bidx the lowest index holding it, z the sum
@@ -137,9 +138,9 @@ __device__ __forceinline__ void greedy_fold_batch(const float (&v)[N], const uin
 // aligned, kGreedyBatch of them issued before any is used (a quad past the
 // end re-reads the last whole quad and is masked, so no load is
 // conditional); scalar loads for the remainder or an unaligned row.
+template <uint32_t T>
 __device__ void greedy_scan(const float *lg, uint32_t n, uint32_t tid, float &best, uint32_t &bidx, float &z)
 {
-    constexpr uint32_t T = kWorkerThreads;
     uint32_t done = 0;
     const uint32_t quads = n / 4;
     if (((uintptr_t)lg & 15u) == 0 && quads > 0) {
@@ -179,31 +180,51 @@ __device__ void greedy_scan(const float *lg, uint32_t n, uint32_t tid, float &be
     }
 }
 
-// Stages of each wave's tile ring: the worker is one workgroup per ring pair,
-// so a decode step's attention is latency-bound. Four stages measured best
-// on the 8-head d64 plumbing shape (34 us of tile streaming per step against
-// 40 us with seven); fewer when the LDS beside the merge buffers (2 KiB kept
-// free) or the vmcnt range of the copies does not allow four.
+// LDS of the worker beside the tile stages: the merge weights and the small
+// per-step buffers.
+template <int G>
+constexpr int worker_fixed_lds()
+{
+    return kMergeLds * G * 4 + 2048;
+}
+
+// Waves of the worker: a decode step's attention is latency-bound (one
+// workgroup per ring pair), so its tiles are shared by eight waves when two
+// tile stages per wave fit the LDS, else by four.
+template <int D, int G, int DT, int TPB>
+constexpr int worker_waves()
+{
+    using C = Cfg<D, G, DT, TPB>;
+    return (C::LDS_CU - worker_fixed_lds<G>()) / (kWorkerWavesMax * (C::STAGE + C::QSLOT)) >= 2 ? kWorkerWavesMax
+                                                                                                : 4;
+}
+
+// Stages of each wave's tile ring: two with eight waves; with four, up to
+// four as the LDS and the vmcnt range of the copies allow. Beyond two stages
+// the stream's per-stage state is indexed at run time and lives in scratch
+// memory, so eight waves of two stages keep the same 16 tiles in flight
+// without it.
 template <int D, int G, int DT, int TPB>
 constexpr int worker_stages()
 {
     using C = Cfg<D, G, DT, TPB>;
-    constexpr int fixed = 2 * kMergeLds * G * 4 + 2048;
-    constexpr int per = C::W * (C::STAGE + C::QSLOT);
-    int ns = (C::LDS_CU - fixed) / per;
-    ns = ns > 4 ? 4 : ns;
+    constexpr int W = worker_waves<D, G, DT, TPB>();
+    constexpr int per = W * (C::STAGE + C::QSLOT);
+    int ns = (C::LDS_CU - worker_fixed_lds<G>()) / per;
+    const int cap = W == kWorkerWavesMax ? 2 : 4;
+    ns = ns > cap ? cap : ns;
     while (ns > 2 && (ns - 1) * C::UNIT_OPS >= 64)
         ns--;
     return ns < 2 ? 2 : ns;
 }
 
 template <int D, int G, int DT, int TPB>
-__global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams wp)
+__global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerParams wp)
 {
     using C = Cfg<D, G, DT, TPB>;
-    constexpr int W = C::W;
+    constexpr int W = worker_waves<D, G, DT, TPB>();
+    constexpr uint32_t kThreads = W * 64;
     constexpr int NS = worker_stages<D, G, DT, TPB>();
-    static_assert(W * 64 == kWorkerThreads, "four waves");
     constexpr int PART = C::PART;
     __shared__ __attribute__((aligned(1024))) uint8_t lds_st[NS][W * C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * NS * C::QSLOT];
@@ -314,12 +335,12 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
             a.q = wp.q + step_row * qh * D;
             a.out = nullptr;
             a.out_f32 = wp.attn_out + step_row * qh * D;
-            a.part = wp.part + (size_t)grp * (W + kvh) * PART;
+            a.part = wp.part + (size_t)grp * (kWorkerWavesMax + kvh) * PART;
             const uint32_t nu = (pos + kTile - 1) / kTile;
             const uint32_t U = kvh * nu;
             if (U == 0) {
                 for (uint32_t g = 0; g < kvh; g++)
-                    empty_row<D, G, DT, G>(a, 0, g, 0, false, tid, kWorkerThreads);
+                    empty_row<D, G, DT, G>(a, 0, g, 0, false, tid, kThreads);
             } else {
                 const uint32_t NW = min((uint32_t)W, U);
                 if ((uint32_t)wave < NW) {
@@ -329,7 +350,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                 }
                 __syncthreads();
                 for (uint32_t g = 0; g < kvh; g++)
-                    merge_row<D, G, DT, kWorkerThreads, G>(a, 0, g, 0, g * nu, nu, U, NW, false, tid, s_f, s_L);
+                    merge_row<D, G, DT, kThreads, G>(a, 0, g, 0, g * nu, nu, U, NW, false, tid, s_f, s_L);
             }
 
             // greedy token (lowest index among maxima) and its logprob: one
@@ -340,7 +361,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
                 const float *lg = wp.logits + step_row * wp.vocab;
                 float best = -INFINITY, z = 0.f;
                 uint32_t bidx = 0xFFFFFFFFu;
-                greedy_scan(lg, wp.vocab, tid, best, bidx, z);
+                greedy_scan<kThreads>(lg, wp.vocab, tid, best, bidx, z);
                 // combine (best, bidx, z) over the workgroup; z is relative to best
                 float m = best;
                 wave_argmax(m, bidx);
@@ -375,7 +396,7 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
             {
                 constexpr int CH = D * 2 / 16;  // 16-byte chunks per row
                 bool bad = false;
-                for (uint32_t t = tid; t < kvh * CH * 2; t += kWorkerThreads) {
+                for (uint32_t t = tid; t < kvh * CH * 2; t += kThreads) {
                     const uint32_t h = t / (CH * 2);
                     const uint32_t c = t % (CH * 2);
                     const bool isv = c >= (uint32_t)CH;
@@ -479,13 +500,14 @@ __global__ __launch_bounds__(kWorkerThreads) void hw_worker_kernel(WorkerParams 
 size_t part_bytes(const rl_hw_worker_args_t *a)
 {
     const uint32_t G = a->q_heads / a->kv_heads;
-    return (size_t)a->groups * (4 + a->kv_heads) * (G * a->layout.head_dim + 2 * G) * 4;
+    return (size_t)a->groups * (kWorkerWavesMax + a->kv_heads) * (G * a->layout.head_dim + 2 * G) * 4;
 }
 
 template <int D, int G, int DT, int TPB>
 int launch(const WorkerParams &wp, uint32_t groups)
 {
-    hipLaunchKernelGGL((hw_worker_kernel<D, G, DT, TPB>), dim3(groups), dim3(kWorkerThreads), 0, rl_stream(), wp);
+    hipLaunchKernelGGL((hw_worker_kernel<D, G, DT, TPB>), dim3(groups), dim3(worker_waves<D, G, DT, TPB>() * 64), 0,
+                       rl_stream(), wp);
     return rl_check_launch("hw_worker_kernel launch");
 }
 
