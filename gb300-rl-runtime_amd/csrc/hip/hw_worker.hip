@@ -286,7 +286,10 @@ __global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerPara
             }
             got = rl_wave_bcast_u32(got, 0);
             if (got) {
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "");
+                // the descriptor's dwords are read with system-scope
+                // (volatile) loads, which bypass the caches, after the tail
+                // that covers them: no cache needs invalidating
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 const uint32_t h = rl_wave_bcast_u32(head, 0);
                 if (lane < 16)
                     s_desc[lane] = ((const volatile uint32_t *)&cq->desc[h & HW_RING_MASK])[lane];
@@ -416,13 +419,16 @@ __global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerPara
                                    (pos % TPB) * C::RB;
                     *(rl_u32x4 *)(dst + cc * 16) = *(const rl_u32x4 *)((const uint8_t *)srcp + cc * 16);
                 }
+                // the next step's copies, issued by the waves of this
+                // workgroup, read the appended token: release before the
+                // barrier, acquire after it, both at workgroup scope
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
                 if (__syncthreads_or(bad)) {
                     status = kStatusAppend;
                     fail = true;
                     break;
                 }
-                // the next step's copies read the appended token
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
             }
 
             d.seq_len++;
