@@ -2,9 +2,13 @@
 //
 // Replaces the reference's serial sample_token (cu/sample.cu:41-123: one
 // thread, O(V*k) insertion top-k, xoshiro256** draw, float CDF walk) with
-// HBM-streaming kernels: batches with top-k, or vocabularies above 32,768,
-// take split + merge; the others (whole-vocabulary nucleus, greedy) one
-// workgroup per row holding the row in registers (sample_row_kernel, below).
+// HBM-streaming kernels. Batches with top-k take one workgroup per row that
+// streams the row in chunks (sample_stream_kernel, below) when the rows are at
+// most 32,768 logits or number at least kStreamMinRows, and split + merge when
+// fewer long rows would leave most compute units idle. Vocabularies above
+// 32,768 without top-k (or greedy) take split + merge too; the others
+// (whole-vocabulary nucleus, greedy) one workgroup per row holding the row in
+// registers (sample_row_kernel, below).
 //
 //  split  grid (split, row): each 256-thread workgroup streams an 8,192-
 //         element slice of one row (32 fp32 per thread, 16-byte loads) and
@@ -957,6 +961,266 @@ __device__ __forceinline__ uint32_t exact_row_sample(const SampleParams &p, uint
     return tok;
 }
 
+// ---- one-wave top-k pick -------------------------------------------------------
+// Lane j holds the j-th kept composite key in (x desc, index asc) order (j <
+// nk <= 64): integer weights, the nucleus prefix, the draw and the smallest
+// index whose ascending-index cumulative weight exceeds it. With at most 64
+// weights of at most 2^24 every prefix fits in 32 bits. Every lane of the
+// wave returns the token; xtok / xknown: its x from the kept key.
+__device__ __forceinline__ void wave_draw_sorted(uint64_t cs, uint32_t nk, float m, float topp, uint64_t draw,
+                                                 uint32_t vocab, uint32_t &tok, float &xtok, bool &xknown)
+{
+    const int lane = threadIdx.x & 63;
+    const bool valid = (uint32_t)lane < nk;
+    const uint32_t idx = 0xFFFFFFFFu - (uint32_t)cs;
+    const uint32_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(cs >> 32)) - m) : 0u;
+    const uint32_t c = rl_wave_incl_scan_u32(w);
+    const uint32_t wk = rl_readlane(c, 63);
+    uint32_t np = nk;
+    if (topp > 0.f && topp < 1.f) {
+        const uint64_t thr = rl_topp_threshold(topp, wk);
+        const uint64_t hit = __ballot(valid && (uint64_t)c >= thr);
+        np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
+    }
+    const uint32_t wp = np ? rl_readlane(c, (int)np - 1) : 0u;
+    const uint64_t u = rl_mulhi_u64(draw, wp);
+    const bool in_p = (uint32_t)lane < np;
+    // ascending-index prefix weight at my index (lane j holds sorted element j)
+    uint32_t s_le = 0;
+    for (uint32_t j = 0; j < np; j++)
+        s_le += rl_readlane(idx, (int)j) <= idx ? rl_readlane(w, (int)j) : 0u;
+    tok = rl_wave_min_u32(in_p && (uint64_t)s_le > u ? idx : 0xFFFFFFFFu);
+    if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
+        tok = rl_wave_min_u32(in_p ? idx : 0xFFFFFFFFu);
+    if (tok >= vocab)        // empty kept set (every logit -inf): token 0
+        tok = 0;
+    const uint64_t own = __ballot(valid && idx == tok);
+    if (own) {
+        const int src = (int)__ffsll((long long)own) - 1;
+        xtok = rl_key_float(rl_readlane((uint32_t)(cs >> 32), src));
+        xknown = true;
+    }
+}
+
+// ---- the top-k tail shared by the merge and the stream kernels ---------------
+// Input: the candidates s_cand[0, nf), among them every key of the row's
+// k_eff largest (every candidate key lies in [key_lo, key_hi], key_hi the
+// key of the row max m); s_h2[0] holding the histogram of the first radix
+// digit, bits hb .. hb - 7 (bits 7 .. 0 when hb < 7), of the candidate keys
+// equal to prefix0 above bit hb (hb < 0: every candidate key equals key_hi);
+// bs.cnt[1] and bs.n zero; all of it visible to the block. Returns the
+// sampled token, or overflow when the kept set exceeds kKeptCap (the caller
+// then takes the exact whole-row path).
+struct TopkPick {
+    uint32_t tok;
+    float xtok;    // the token's x when the path that chose it holds it
+    bool xknown;
+    bool overflow;
+};
+
+__device__ __forceinline__ TopkPick topk_pick(uint32_t nf, uint32_t k_eff, int hb, uint32_t key_hi, uint32_t prefix0,
+                                              float m, float topp, uint64_t draw, uint32_t vocab, uint2 *s_cand,
+                                              uint32_t (*s_h2)[256], uint64_t *s_keep, uint64_t *s_sort,
+                                              uint32_t *s_w, uint32_t *s_idx, BlockShared &bs)
+{
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63;
+    uint32_t tok = 0;
+    float xtok = 0.f;
+    bool xknown = false, exact = false;
+    // ---- exact k_eff-th largest key --------------------------------------
+    // Each pass's histogram (after the first) is filled while the other one
+    // is cleared; every wave then finds the digit itself: lane l holds
+    // bins 255-4l .. 252-4l, a DPP scan gives the count in higher bins,
+    // and the digit is the bin where that count reaches need. Once the
+    // chosen bin holds at most 64 keys, they are copied out and one wave
+    // finishes the selection with a ballot radix select. With fewer than
+    // k_eff candidates the row has fewer than k_eff finite logits, and
+    // every finite one is kept.
+    uint32_t cutoff = 0;
+    if (nf >= k_eff) {
+        if (hb < 0) {
+            cutoff = key_hi;
+        } else {
+            uint32_t prefix = prefix0;
+            uint32_t need = k_eff;
+            int pass = 0;
+            for (int top = hb; top >= 0; top -= 8, pass++) {
+                const int shift = top >= 7 ? top - 7 : 0;
+                const uint32_t above = top >= 31 ? 0u : ~((2u << top) - 1u);
+                uint32_t *H = s_h2[pass & 1];
+                if (pass > 0) {
+                    for (uint32_t i = tid; i < nf; i += kMergeThreads) {
+                        const uint32_t key = s_cand[i].x;
+                        if ((key & above) == prefix)
+                            atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
+                    }
+                    __syncthreads();
+                }
+                if (tid < 256)
+                    s_h2[(pass & 1) ^ 1][tid] = 0;
+                uint32_t h[4], own = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    h[j] = H[255 - 4 * lane - j];
+                    own += h[j];
+                }
+                uint32_t acc = rl_wave_incl_scan_u32(own) - own;
+                int found = -1;
+                uint32_t rem = 0, hcnt = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    if (found < 0 && acc < need && acc + h[j] >= need) {
+                        found = 255 - 4 * lane - j;
+                        rem = need - acc;
+                        hcnt = h[j];
+                    }
+                    acc += h[j];
+                }
+                const uint64_t hit = __ballot(found >= 0);  // never empty: need <= matching keys
+                const int src = hit ? (int)__ffsll((long long)hit) - 1 : 0;
+                prefix |= (uint32_t)__builtin_amdgcn_readlane(found, src) << shift;
+                need = rl_readlane(rem, src);
+                const uint32_t bin_cnt = rl_readlane(hcnt, src);
+                __syncthreads();
+                if (shift > 0 && bin_cnt <= 64u) {
+                    // the keys sharing every bit fixed so far (bits >= shift)
+                    const uint32_t above_s = ~((1u << shift) - 1u);
+                    uint32_t *lst = s_h2[pass & 1];  // H is read by no one after the barrier
+                    for (uint32_t i = tid; i < nf; i += kMergeThreads) {
+                        const uint32_t key = s_cand[i].x;
+                        if ((key & above_s) == prefix)
+                            lst[atomicAdd(&bs.cnt[1], 1u)] = key;  // bin_cnt <= 64 of them
+                    }
+                    __syncthreads();
+                    if (tid < 64) {
+                        const uint32_t key = (uint32_t)lane < bin_cnt ? lst[lane] : 0u;
+                        const uint32_t c = wave_kth_largest_key_from(key, need, prefix, shift - 1);
+                        if (tid == 0)
+                            bs.w32[0] = c;
+                    }
+                    __syncthreads();
+                    prefix = bs.w32[0];
+                    break;
+                }
+            }
+            cutoff = prefix;
+        }
+    }
+
+    // ---- kept set K = {key >= cutoff} ------------------------------------
+    for (uint32_t i = tid; i < nf; i += kMergeThreads) {
+        const uint2 c = s_cand[i];
+        if (c.x >= cutoff) {
+            const uint32_t pos = atomicAdd(&bs.n, 1u);
+            if (pos < (uint32_t)kKeptCap)
+                s_keep[pos] = composite_key(c.x, c.y);
+        }
+    }
+    __syncthreads();
+    const uint32_t nk = bs.n;
+    __syncthreads();
+    if (nk > (uint32_t)kKeptCap) {
+        exact = true;
+    } else if (nk <= 64u) {
+        // ---- one wave: lane i holds sorted element i; with at most 64
+        // weights of at most 2^24 every prefix fits in 32 bits ------------
+        tok = 0;
+        // rank of kept key i = kept keys above it; thread (i, b) counts
+        // over keys 8b .. 8b + 7 (s_h2 is free after the cutoff)
+        {
+            const uint32_t i = tid & 63u, b = tid >> 6;
+            const uint64_t cki = i < nk ? s_keep[i] : 0ull;
+            uint32_t part = 0;
+#pragma unroll
+            for (uint32_t jj = 0; jj < 8; jj++) {
+                const uint32_t j = b * 8 + jj;
+                part += (j < nk && s_keep[j] > cki) ? 1u : 0u;
+            }
+            s_h2[b >> 2][(b & 3) * 64 + i] = part;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            const bool valid = (uint32_t)lane < nk;
+            const uint64_t ck = valid ? s_keep[lane] : 0ull;  // real keys are > 0
+            uint32_t rank = 0;
+#pragma unroll
+            for (uint32_t b = 0; b < 8; b++)
+                rank += s_h2[b >> 2][(b & 3) * 64 + lane];
+            if (valid)
+                s_sort[rank] = ck;
+            rl_wave_lds_fence();
+            wave_draw_sorted(valid ? s_sort[lane] : 0ull, nk, m, topp, draw, vocab, tok, xtok, xknown);
+        }
+    } else {
+        // ---- rank sort by (x desc, index asc): composite keys are distinct
+        for (uint32_t i = tid; i < nk; i += kMergeThreads) {
+            const uint64_t ck = s_keep[i];
+            uint32_t rank = 0;
+            for (uint32_t j = 0; j < nk; j++)
+                rank += s_keep[j] > ck ? 1u : 0u;
+            s_sort[rank] = ck;
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < nk; i += kMergeThreads) {
+            const uint64_t ck = s_sort[i];
+            s_w[i] = rl_sample_weight(rl_key_float((uint32_t)(ck >> 32)) - m);
+            s_idx[i] = 0xFFFFFFFFu - (uint32_t)ck;
+        }
+        __syncthreads();
+
+        // ---- nucleus prefix over the sorted order -----------------------
+        // thread t owns the contiguous sorted positions [t*per, (t+1)*per)
+        const uint32_t per = (nk + kMergeThreads - 1) / kMergeThreads;
+        const uint32_t i0 = min(nk, tid * per), i1 = min(nk, (tid + 1) * per);
+        uint64_t own = 0;
+        for (uint32_t i = i0; i < i1; i++)
+            own += s_w[i];
+        uint64_t wk;
+        const uint64_t excl = block_excl_scan_u64(own, wk, bs);
+        uint32_t np = nk;
+        if (topp > 0.f && topp < 1.f) {
+            const uint64_t thr = rl_topp_threshold(topp, wk);
+            // first sorted position whose inclusive prefix reaches thr
+            uint32_t first = 0xFFFFFFFFu;
+            uint64_t c = excl;
+            for (uint32_t i = i0; i < i1; i++) {
+                c += s_w[i];
+                if (c >= thr) {
+                    first = i;
+                    break;
+                }
+            }
+            first = block_min_u32(first, bs);
+            np = (first == 0xFFFFFFFFu) ? nk : first + 1;
+        }
+        uint64_t wp_own = 0;
+        for (uint32_t i = i0; i < min(i1, np); i++)
+            wp_own += s_w[i];
+        const uint64_t wp = block_sum_u64(wp_own, bs);
+
+        // ---- draw; smallest index whose ascending-index prefix weight exceeds u
+        const uint64_t u = rl_mulhi_u64(draw, wp);
+        uint32_t cand = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
+        for (uint32_t i = tid; i < np; i += kMergeThreads) {
+            const uint32_t idx_i = s_idx[i];
+            lowest = min(lowest, idx_i);
+            uint64_t s_le = 0;
+            for (uint32_t j = 0; j < np; j++)
+                s_le += s_idx[j] <= idx_i ? (uint64_t)s_w[j] : 0ull;
+            if (s_le > u)
+                cand = min(cand, idx_i);
+        }
+        tok = block_min_u32(cand, bs);
+        lowest = block_min_u32(lowest, bs);
+        if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
+            tok = lowest;
+        if (tok >= vocab)      // empty kept set (every logit -inf): token 0
+            tok = 0;
+    }
+    return TopkPick{tok, xtok, xknown, exact};
+}
+
 // One workgroup of kMergeThreads threads per row.
 __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParams p)
 {
@@ -1129,224 +1393,12 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         __syncthreads();
         const uint32_t nf = bs.cnt[0];
 
-        // ---- exact k_eff-th largest key --------------------------------------
-        // Each pass's histogram (after the first) is filled while the other one
-        // is cleared; every wave then finds the digit itself: lane l holds
-        // bins 255-4l .. 252-4l, a DPP scan gives the count in higher bins,
-        // and the digit is the bin where that count reaches need. Once the
-        // chosen bin holds at most 64 keys, they are copied out and one wave
-        // finishes the selection with a ballot radix select. With fewer than
-        // k_eff candidates the row has fewer than k_eff finite logits, and
-        // every finite one is kept.
-        uint32_t cutoff = 0;
-        if (nf >= k_eff) {
-            if (hb < 0) {
-                cutoff = key_hi;
-            } else {
-                uint32_t prefix = prefix0;
-                uint32_t need = k_eff;
-                int pass = 0;
-                for (int top = hb; top >= 0; top -= 8, pass++) {
-                    const int shift = top >= 7 ? top - 7 : 0;
-                    const uint32_t above = top >= 31 ? 0u : ~((2u << top) - 1u);
-                    uint32_t *H = s_h2[pass & 1];
-                    if (pass > 0) {
-                        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
-                            const uint32_t key = s_cand[i].x;
-                            if ((key & above) == prefix)
-                                atomicAdd(&H[(key >> shift) & 0xFFu], 1u);
-                        }
-                        __syncthreads();
-                    }
-                    if (tid < 256)
-                        s_h2[(pass & 1) ^ 1][tid] = 0;
-                    uint32_t h[4], own = 0;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        h[j] = H[255 - 4 * lane - j];
-                        own += h[j];
-                    }
-                    uint32_t acc = rl_wave_incl_scan_u32(own) - own;
-                    int found = -1;
-                    uint32_t rem = 0, hcnt = 0;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        if (found < 0 && acc < need && acc + h[j] >= need) {
-                            found = 255 - 4 * lane - j;
-                            rem = need - acc;
-                            hcnt = h[j];
-                        }
-                        acc += h[j];
-                    }
-                    const uint64_t hit = __ballot(found >= 0);  // never empty: need <= matching keys
-                    const int src = hit ? (int)__ffsll((long long)hit) - 1 : 0;
-                    prefix |= (uint32_t)__builtin_amdgcn_readlane(found, src) << shift;
-                    need = rl_readlane(rem, src);
-                    const uint32_t bin_cnt = rl_readlane(hcnt, src);
-                    __syncthreads();
-                    if (shift > 0 && bin_cnt <= 64u) {
-                        // the keys sharing every bit fixed so far (bits >= shift)
-                        const uint32_t above_s = ~((1u << shift) - 1u);
-                        uint32_t *lst = s_h2[pass & 1];  // H is read by no one after the barrier
-                        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
-                            const uint32_t key = s_cand[i].x;
-                            if ((key & above_s) == prefix)
-                                lst[atomicAdd(&bs.cnt[1], 1u)] = key;  // bin_cnt <= 64 of them
-                        }
-                        __syncthreads();
-                        if (tid < 64) {
-                            const uint32_t key = (uint32_t)lane < bin_cnt ? lst[lane] : 0u;
-                            const uint32_t c = wave_kth_largest_key_from(key, need, prefix, shift - 1);
-                            if (tid == 0)
-                                bs.w32[0] = c;
-                        }
-                        __syncthreads();
-                        prefix = bs.w32[0];
-                        break;
-                    }
-                }
-                cutoff = prefix;
-            }
-        }
-
-        // ---- kept set K = {key >= cutoff} ------------------------------------
-        for (uint32_t i = tid; i < nf; i += kMergeThreads) {
-            const uint2 c = s_cand[i];
-            if (c.x >= cutoff) {
-                const uint32_t pos = atomicAdd(&bs.n, 1u);
-                if (pos < (uint32_t)kKeptCap)
-                    s_keep[pos] = composite_key(c.x, c.y);
-            }
-        }
-        __syncthreads();
-        const uint32_t nk = bs.n;
-        __syncthreads();
-        if (nk > (uint32_t)kKeptCap) {
-            exact = true;
-        } else if (nk <= 64u) {
-            // ---- one wave: lane i holds sorted element i; with at most 64
-            // weights of at most 2^24 every prefix fits in 32 bits ------------
-            tok = 0;
-            // rank of kept key i = kept keys above it; thread (i, b) counts
-            // over keys 8b .. 8b + 7 (s_h2 is free after the cutoff)
-            {
-                const uint32_t i = tid & 63u, b = tid >> 6;
-                const uint64_t cki = i < nk ? s_keep[i] : 0ull;
-                uint32_t part = 0;
-#pragma unroll
-                for (uint32_t jj = 0; jj < 8; jj++) {
-                    const uint32_t j = b * 8 + jj;
-                    part += (j < nk && s_keep[j] > cki) ? 1u : 0u;
-                }
-                s_h2[b >> 2][(b & 3) * 64 + i] = part;
-            }
-            __syncthreads();
-            if (tid < 64) {
-                const bool valid = (uint32_t)lane < nk;
-                const uint64_t ck = valid ? s_keep[lane] : 0ull;  // real keys are > 0
-                uint32_t rank = 0;
-#pragma unroll
-                for (uint32_t b = 0; b < 8; b++)
-                    rank += s_h2[b >> 2][(b & 3) * 64 + lane];
-                if (valid)
-                    s_sort[rank] = ck;
-                rl_wave_lds_fence();
-                const uint64_t cs = valid ? s_sort[lane] : 0ull;
-                const uint32_t idx = 0xFFFFFFFFu - (uint32_t)cs;
-                const uint32_t w = valid ? rl_sample_weight(rl_key_float((uint32_t)(cs >> 32)) - m) : 0u;
-                const uint32_t c = rl_wave_incl_scan_u32(w);
-                const uint32_t wk = rl_readlane(c, 63);
-                uint32_t np = nk;
-                if (topp > 0.f && topp < 1.f) {
-                    const uint64_t thr = rl_topp_threshold(topp, wk);
-                    const uint64_t hit = __ballot(valid && (uint64_t)c >= thr);
-                    np = hit ? (uint32_t)__ffsll((long long)hit) : nk;  // first reaching lane + 1
-                }
-                const uint32_t wp = np ? rl_readlane(c, (int)np - 1) : 0u;
-                const uint64_t u = rl_mulhi_u64(draw, wp);
-                const bool in_p = (uint32_t)lane < np;
-                // ascending-index prefix weight at my index (lane j holds sorted element j)
-                uint32_t s_le = 0;
-                for (uint32_t j = 0; j < np; j++)
-                    s_le += rl_readlane(idx, (int)j) <= idx ? rl_readlane(w, (int)j) : 0u;
-                tok = rl_wave_min_u32(in_p && (uint64_t)s_le > u ? idx : 0xFFFFFFFFu);
-                if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
-                    tok = rl_wave_min_u32(in_p ? idx : 0xFFFFFFFFu);
-                if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
-                    tok = 0;
-                const uint64_t own = __ballot(valid && idx == tok);
-                if (own) {
-                    const int src = (int)__ffsll((long long)own) - 1;
-                    xtok = rl_key_float(rl_readlane((uint32_t)(cs >> 32), src));
-                    xknown = true;
-                }
-            }
-        } else {
-            // ---- rank sort by (x desc, index asc): composite keys are distinct
-            for (uint32_t i = tid; i < nk; i += kMergeThreads) {
-                const uint64_t ck = s_keep[i];
-                uint32_t rank = 0;
-                for (uint32_t j = 0; j < nk; j++)
-                    rank += s_keep[j] > ck ? 1u : 0u;
-                s_sort[rank] = ck;
-            }
-            __syncthreads();
-            for (uint32_t i = tid; i < nk; i += kMergeThreads) {
-                const uint64_t ck = s_sort[i];
-                s_w[i] = rl_sample_weight(rl_key_float((uint32_t)(ck >> 32)) - m);
-                s_idx[i] = 0xFFFFFFFFu - (uint32_t)ck;
-            }
-            __syncthreads();
-
-            // ---- nucleus prefix over the sorted order -----------------------
-            // thread t owns the contiguous sorted positions [t*per, (t+1)*per)
-            const uint32_t per = (nk + kMergeThreads - 1) / kMergeThreads;
-            const uint32_t i0 = min(nk, tid * per), i1 = min(nk, (tid + 1) * per);
-            uint64_t own = 0;
-            for (uint32_t i = i0; i < i1; i++)
-                own += s_w[i];
-            uint64_t wk;
-            const uint64_t excl = block_excl_scan_u64(own, wk, bs);
-            uint32_t np = nk;
-            if (topp > 0.f && topp < 1.f) {
-                const uint64_t thr = rl_topp_threshold(topp, wk);
-                // first sorted position whose inclusive prefix reaches thr
-                uint32_t first = 0xFFFFFFFFu;
-                uint64_t c = excl;
-                for (uint32_t i = i0; i < i1; i++) {
-                    c += s_w[i];
-                    if (c >= thr) {
-                        first = i;
-                        break;
-                    }
-                }
-                first = block_min_u32(first, bs);
-                np = (first == 0xFFFFFFFFu) ? nk : first + 1;
-            }
-            uint64_t wp_own = 0;
-            for (uint32_t i = i0; i < min(i1, np); i++)
-                wp_own += s_w[i];
-            const uint64_t wp = block_sum_u64(wp_own, bs);
-
-            // ---- draw; smallest index whose ascending-index prefix weight exceeds u
-            const uint64_t u = rl_mulhi_u64(draw, wp);
-            uint32_t cand = 0xFFFFFFFFu, lowest = 0xFFFFFFFFu;
-            for (uint32_t i = tid; i < np; i += kMergeThreads) {
-                const uint32_t idx_i = s_idx[i];
-                lowest = min(lowest, idx_i);
-                uint64_t s_le = 0;
-                for (uint32_t j = 0; j < np; j++)
-                    s_le += s_idx[j] <= idx_i ? (uint64_t)s_w[j] : 0ull;
-                if (s_le > u)
-                    cand = min(cand, idx_i);
-            }
-            tok = block_min_u32(cand, bs);
-            lowest = block_min_u32(lowest, bs);
-            if (tok == 0xFFFFFFFFu)  // zero total weight: lowest index of P
-                tok = lowest;
-            if (tok >= p.vocab)      // empty kept set (every logit -inf): token 0
-                tok = 0;
-        }
+        const TopkPick pk = topk_pick(nf, k_eff, hb, key_hi, prefix0, m, topp, draw, p.vocab, s_cand, s_h2, s_keep,
+                                      s_sort, s_w, s_idx, bs);
+        tok = pk.tok;
+        xtok = pk.xtok;
+        xknown = pk.xknown;
+        exact = pk.overflow;
     }
     if (exact)
         tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
@@ -1357,6 +1409,300 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
             const float x = xknown ? xtok : p.logits[(size_t)row * p.row_stride + tok] * inv_t;
             p.logprob_out[row] = x - lse;
         }
+    }
+}
+
+// ---- one workgroup per row, the row streamed in chunks (rows with top-k) -----
+// Thread t's quad j of chunk c holds the logits from c * kStreamChunk +
+// (512 j + t) * 4, so each load instruction reads 1 KiB of consecutive logits
+// and each thread's elements ascend in (c, j, e). Two register buffers of
+// kStreamQuads quads alternate: the next chunk's loads are in flight while the
+// current chunk is processed, so the vector-ALU work overlaps the stream, and
+// no slice statistics or candidate lists go through memory. Per chunk:
+//   max     x = l * inv_t (masked past the row's end), the quad maxima and the
+//           thread's running max;
+//   bound   (the first kStreamRefresh chunks) the minimum over the waves of
+//           each wave's ceil(k/8)-th largest running lane max. At least k
+//           elements seen so far lie at or above it, so it is a lower bound
+//           of the row's k-th largest key, and it only grows;
+//   sum     sum exp(x - running max) in four partial sums, rescaled when the
+//           max grows (the log-sum-exp of the logprob). A NaN or +inf logit
+//           turns the sum NaN;
+//   append  the elements at or above the bound (a quad is tested by its max
+//           first) into the thread's own LDS list of kStreamList entries, so
+//           appends need no atomics. An element below the bound in force at
+//           its chunk is below the final bound too, hence outside the top k.
+// After the last chunk: the block max and log-sum-exp; the lists compacted
+// into the candidate buffer, keeping the keys at or above the final bound and
+// filling the first radix histogram on the way; then the top-k tail shared
+// with the merge kernel. A list overflow, a NaN sum, a kept set beyond
+// kKeptCap and rows without top-k take the exact whole-row path. Greedy rows
+// keep the (value desc, index asc) argmax instead of candidates.
+constexpr int kStreamQuads = 16;                                          // quads per thread per chunk
+constexpr uint32_t kStreamChunk = (uint32_t)kMergeThreads * 4u * kStreamQuads;  // 32,768 logits
+constexpr uint32_t kStreamRefresh = 2;                                    // chunks that raise the bound
+constexpr uint32_t kStreamList = 8;                                       // list entries per thread
+// Long rows (above 32,768 logits) take the stream kernel from this many rows
+// on: at 128,256 logits, 144 rows (9/16 of the 256 compute units) is where
+// one row per compute unit overtakes split and merge.
+constexpr uint32_t kStreamMinRows = 144;
+constexpr float kLog2e = 1.4426950408889634f;
+// Third dword of a gfx9 buffer descriptor for raw (unswizzled) 32-bit data,
+// and the load's cache-policy operand for a nontemporal load.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kBufferNontemporal = 2;
+
+__global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SampleParams p)
+{
+    const uint32_t row = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+
+    __shared__ uint2 s_cand[kMergeCap];
+    __shared__ uint2 s_list[kStreamList][kMergeThreads];  // thread t's entries: column t
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_h2[2][256];
+    __shared__ unsigned long long s_whist[256];
+    __shared__ uint64_t s_keep[kKeptCap];
+    __shared__ uint64_t s_sort[kKeptCap];
+    __shared__ uint32_t s_w[kKeptCap];
+    __shared__ uint32_t s_idx[kKeptCap];
+    __shared__ BlockShared bs;
+    __shared__ uint32_t s_bound[kStreamRefresh][kMergeWaves];
+    __shared__ float s_wm[kMergeWaves], s_wz[kMergeWaves], s_wv[kMergeWaves];
+    __shared__ uint32_t s_wi[kMergeWaves], s_wflag[kMergeWaves];
+    // the whole-row path's scratch reuses the candidate buffer
+    static_assert(sizeof(RowScratch) <= sizeof(s_cand), "row scratch fits the candidate buffer");
+    RowScratch &rs = *reinterpret_cast<RowScratch *>(s_cand);
+
+    const float *lrow = p.logits + (size_t)row * p.row_stride;
+    const uint32_t V = p.vocab;
+    const uint32_t nch = (V + kStreamChunk - 1) / kStreamChunk;
+
+    // Buffer loads over the row's stride: the per-load offset is one scalar
+    // and the thread's offset one register, so the loads of two chunks fit
+    // beside the data; quads past the stride (the chunk after the last one,
+    // which the pipeline below also loads) read as 0 without a memory access,
+    // and everything past the vocabulary is masked before use.
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)lrow, (short)0, (int)(p.row_stride * 4u), kBufferWord3);
+    const uint32_t voff = tid * 16u;
+    auto load = [&](rl_f32x4 (&v)[kStreamQuads], uint32_t c) {
+#pragma unroll
+        for (int j = 0; j < kStreamQuads; j++)
+            v[j] = __builtin_bit_cast(rl_f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rsrc, (int)voff, (int)(c * kStreamChunk * 4u + j * kMergeThreads * 16u),
+                                                    kBufferNontemporal));
+    };
+
+    rl_f32x4 A[kStreamQuads], B[kStreamQuads];
+    load(A, 0);
+    // the row's parameters and Philox draw, while the first loads are in flight
+    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
+    const uint32_t k_eff = greedy ? 0u : effective_k(row_topk(p, row), V);
+    const uint64_t draw = greedy ? 0ull : rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+
+    float mt = -INFINITY, zt = 0.f;  // running max of x and sum exp(x - mt)
+    float bv = -INFINITY;            // greedy: the running argmax
+    uint32_t bi = 0xFFFFFFFFu;
+    uint32_t nt = 0;                 // list entries appended (> kStreamList: overflow)
+    uint32_t bound = 0;              // key lower bound of the row's k_eff-th largest
+    float t = INFINITY;              // candidates: !(x < t)
+
+    auto process = [&](rl_f32x4 (&v)[kStreamQuads], uint32_t c) {
+        const uint32_t c0 = c * kStreamChunk;
+        if (c0 + kStreamChunk > V) {  // workgroup-uniform: the chunk reaches past the row
+#pragma unroll
+            for (int j = 0; j < kStreamQuads; j++) {
+                const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    v[j][e] = col + (uint32_t)e < V ? v[j][e] : -INFINITY;
+            }
+        }
+        float qm[kStreamQuads];
+#pragma unroll
+        for (int j = 0; j < kStreamQuads; j++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                v[j][e] = v[j][e] * inv_t;
+            qm[j] = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+        }
+        float m4[kStreamQuads / 4];
+#pragma unroll
+        for (int a = 0; a < kStreamQuads / 4; a++)
+            m4[a] = fmaxf(fmaxf(qm[4 * a], qm[4 * a + 1]), fmaxf(qm[4 * a + 2], qm[4 * a + 3]));
+        float cm = m4[0];
+#pragma unroll
+        for (int a = 1; a < kStreamQuads / 4; a++)
+            cm = fmaxf(cm, m4[a]);
+        const float mnew = fmaxf(mt, cm);
+
+        if (greedy) {
+#pragma unroll
+            for (int j = 0; j < kStreamQuads; j++) {
+                if (qm[j] > bv) {  // the quad's lowest index holding its max
+                    const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
+                    bi = col + (v[j][0] == qm[j] ? 0u : v[j][1] == qm[j] ? 1u : v[j][2] == qm[j] ? 2u : 3u);
+                    bv = qm[j];
+                }
+            }
+        } else if (k_eff != 0 && c < kStreamRefresh) {
+            const uint32_t kw = (k_eff + kMergeWaves - 1) / kMergeWaves;
+            const uint32_t ck = wave_kth_largest_key(rl_float_key(mnew), kw);
+            if (lane == 0)
+                s_bound[c][wave] = ck;
+            __syncthreads();
+            uint32_t b = s_bound[c][0];
+#pragma unroll
+            for (int w = 1; w < kMergeWaves; w++)
+                b = min(b, s_bound[c][w]);
+            bound = b;
+            // x >= t selects the keys >= bound (the key order is the float
+            // order with -0 = +0); the key of -inf admits every finite x
+            t = b == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(b);
+        }
+
+        // sum exp(x - mt): ml = 0 while every element so far is -inf (or
+        // NaN), so that a NaN still reaches the sum
+        const float sc = mt == mnew ? 1.0f : __builtin_amdgcn_exp2f((mt - mnew) * kLog2e);
+        zt *= sc;
+        mt = mnew;
+        const float ml = mt == -INFINITY ? 0.f : mt * kLog2e;
+        float z4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kStreamQuads; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                z4[e] += __builtin_amdgcn_exp2f(fmaf(v[j][e], kLog2e, -ml));
+        zt += (z4[0] + z4[1]) + (z4[2] + z4[3]);
+
+        if (k_eff != 0) {
+#pragma unroll
+            for (int j = 0; j < kStreamQuads; j++) {
+                if (!(qm[j] < t)) {
+                    const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float x = v[j][e];
+                        if (!(x < t)) {
+                            if (nt < kStreamList)
+                                s_list[nt][tid] = make_uint2(rl_float_key(x), col + (uint32_t)e);
+                            nt++;
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+    for (uint32_t c = 0; c < nch; c += 2) {
+        load(B, c + 1);
+        process(A, c);
+        load(A, c + 2);
+        if (c + 1 < nch)
+            process(B, c + 1);
+    }
+
+    // ---- the row's max, log-sum-exp, flags and (greedy) argmax ---------------
+    const float wm = wave_max(mt);
+    const uint32_t wflag = (__ballot(zt != zt) ? 1u : 0u) | (__ballot(nt > kStreamList) ? 2u : 0u);
+    if (greedy)
+        wave_argmax(bv, bi);
+    if (lane == 0) {
+        s_wm[wave] = wm;
+        s_wflag[wave] = wflag;
+        s_wv[wave] = bv;
+        s_wi[wave] = bi;
+    }
+    __syncthreads();
+    float m = s_wm[0];
+    uint32_t flags = s_wflag[0];
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; w++) {
+        m = fmaxf(m, s_wm[w]);
+        flags |= s_wflag[w];
+    }
+    const float zterm = mt == -INFINITY ? 0.f : zt * exp2f((mt - m) * kLog2e);
+    const float wz = wave_sum(zterm);
+    if (lane == 0)
+        s_wz[wave] = wz;
+    __syncthreads();
+    float zs = 0.f;
+#pragma unroll
+    for (int w = 0; w < kMergeWaves; w++)
+        zs += s_wz[w];
+    const float lse = m + logf(zs);
+
+    if (greedy) {
+        if (tid == 0) {
+            float v = s_wv[0];
+            uint32_t i = s_wi[0];
+#pragma unroll
+            for (int w = 1; w < kMergeWaves; w++)
+                if (s_wv[w] > v || (s_wv[w] == v && s_wi[w] < i)) {
+                    v = s_wv[w];
+                    i = s_wi[w];
+                }
+            p.token_out[row] = i >= V ? 0u : i;  // all -inf: lowest index
+            p.logprob_out[row] = v - lse;
+        }
+        return;
+    }
+
+    const float topp = row_topp(p, row);
+    uint32_t tok = 0;
+    float xtok = 0.f;
+    bool xknown = false;
+    bool exact = k_eff == 0 || flags != 0;
+    if (!exact) {
+        // ---- compact the lists: keys at or above the final bound ------------
+        const uint32_t key_lo = bound;
+        const uint32_t key_hi = rl_float_key(m);
+        const uint32_t diff = key_lo ^ key_hi;
+        const int hb = diff ? 31 - __builtin_clz(diff) : -1;
+        const int shift0 = hb >= 7 ? hb - 7 : 0;
+        const uint32_t above0 = (hb < 0 || hb >= 31) ? 0u : ~((2u << hb) - 1u);
+        const uint32_t prefix0 = key_hi & above0;
+        if (tid == 0) {
+            bs.cnt[1] = 0;
+            bs.n = 0;
+        }
+        if (tid < 256)
+            s_h2[0][tid] = 0;
+        uint32_t own = 0;
+#pragma unroll
+        for (uint32_t e = 0; e < kStreamList; e++)
+            own += (e < nt && s_list[e][tid].x >= key_lo) ? 1u : 0u;
+        uint64_t total;
+        uint32_t pos = (uint32_t)block_excl_scan_u64_inl(own, total, bs);  // (synchronises)
+        const uint32_t nf = (uint32_t)total;                           // <= kMergeThreads * kStreamList
+#pragma unroll
+        for (uint32_t e = 0; e < kStreamList; e++) {
+            if (e < nt) {
+                const uint2 cd = s_list[e][tid];
+                if (cd.x >= key_lo) {
+                    s_cand[pos++] = cd;
+                    if (hb >= 0 && (cd.x & above0) == prefix0)
+                        atomicAdd(&s_h2[0][(cd.x >> shift0) & 0xFFu], 1u);
+                }
+            }
+        }
+        __syncthreads();
+        const TopkPick pk = topk_pick(nf, k_eff, hb, key_hi, prefix0, m, topp, draw, V, s_cand, s_h2, s_keep, s_sort,
+                                      s_w, s_idx, bs);
+        tok = pk.tok;
+        xtok = pk.xtok;
+        xknown = pk.xknown;
+        exact = pk.overflow;
+    }
+    if (exact)
+        tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
+    if (tid == 0) {
+        p.token_out[row] = tok;
+        const float x = xknown ? xtok : p.logits[(size_t)row * p.row_stride + tok] * inv_t;
+        p.logprob_out[row] = x - lse;
     }
 }
 
@@ -1946,11 +2292,18 @@ extern "C" int rl_hip_sample(const rl_sample_args_t *a)
     p.cand = (uint2 *)(ws + w.cand_off);
 
     // Rows without top-k whose whole row fits one workgroup's registers: the
-    // row kernel; otherwise split and merge.
+    // row kernel. Batches with top-k: the stream kernel when the rows are
+    // short or fill most of the device (one row per compute unit, so fewer
+    // long rows leave it idle), else split and merge. Everything else: split
+    // and merge.
     const bool no_topk = !a->top_k && (a->top_k_all == 0 || a->top_k_all >= a->vocab);
     if (a->vocab <= kRowVocab && (no_topk || a->greedy)) {
         hipLaunchKernelGGL(sample_row_kernel, dim3(a->rows), dim3(kMergeThreads), 0, rl_stream(), p);
         return rl_check_launch("sample_row_kernel launch");
+    }
+    if (!no_topk && !a->greedy && (a->vocab <= kRowVocab || a->rows >= kStreamMinRows)) {
+        hipLaunchKernelGGL(sample_stream_kernel, dim3(a->rows), dim3(kMergeThreads), 0, rl_stream(), p);
+        return rl_check_launch("sample_stream_kernel launch");
     }
     hipLaunchKernelGGL(sample_split_kernel, dim3(p.splits, a->rows),
                        dim3(kThreads), 0, rl_stream(), p);

@@ -164,3 +164,51 @@ def test_row_kernel_per_row_parameters(rl, gpu, orc, olib):
         assert abs(gl[r] - lpv.value) < 1e-4, r
     for b in bufs + [tok, lp, ws]:
         b.close()
+
+
+@pytest.mark.parametrize("rows,vocab,stride", [(160, 50257, 50260), (144, 128256, 128256)])
+def test_stream_kernel_mixed_rows(rl, gpu, orc, olib, rows, vocab, stride):
+    """Per-row arrays over enough long rows for the one-workgroup-per-row
+    stream kernel: greedy rows (temperature 0) next to top-k 1 / 7 / 50 / 256 /
+    300 rows and rows without top-k (its exact whole-row path); rows of heavy
+    ties, all equal (candidate lists overflow), all -inf, one finite logit,
+    spike ties and a row ending in -inf. Every row against the oracle with its
+    own parameters."""
+    rng = np.random.default_rng(rows + vocab)
+    x = np.full((rows, stride), np.float32(9.0))          # padding past vocab never read
+    x[:, :vocab] = rng.standard_normal((rows, vocab), dtype=np.float32) * np.float32(1.5)
+    x[1, :vocab] = np.round(x[1, :vocab])
+    x[2, :vocab] = 0.25
+    x[3, :vocab] = -np.inf
+    x[4, :vocab] = -np.inf
+    x[4, vocab - 3] = 2.0
+    x[5, rng.choice(vocab, 6, replace=False)] = np.float32(7.0)
+    x[6, vocab // 2:vocab] = -np.inf
+    temp = rng.choice(np.float32([0.0, 0.7, 1.0, 1.3]), rows).astype(np.float32)
+    temp[1:7] = np.float32(0.9)
+    topk = rng.choice(np.uint32([0, 1, 7, 50, 50, 256, 300]), rows).astype(np.uint32)
+    topk[1:7] = np.uint32(50)
+    topk[8] = 0
+    temp[8] = np.float32(1.0)
+    topp = rng.choice(np.float32([1.0, 0.95, 0.9, 0.3]), rows).astype(np.float32)
+    seeds = rng.integers(0, 2**63, rows, dtype=np.uint64)
+    steps = rng.integers(0, 2**40, rows, dtype=np.uint64)
+    bufs = [rl.DeviceBuffer.from_array(a) for a in (x, temp, topk, topp, seeds, steps)]
+    tok, lp = rl.DeviceBuffer(rows * 4), rl.DeviceBuffer(rows * 4)
+    args = rl.sample_args(bufs[0], rows, vocab, stride, tok, lp)
+    args.temperature, args.top_k, args.top_p = bufs[1].ptr, bufs[2].ptr, bufs[3].ptr
+    args.seed, args.steps = bufs[4].ptr, bufs[5].ptr
+    ws = rl.sample_workspace(args)
+    print(f"[sample] stream kernel, mixed rows, {rows} x {vocab}", flush=True)
+    rl.sample(args)
+    rl.sync()
+    gt, gl = tok.download(np.uint32, rows), lp.download(np.float32, rows)
+    import ctypes as C
+    lpv = C.c_double()
+    for r in range(rows):
+        want = olib.orc_sample_row(x[r].ctypes.data, vocab, int(not temp[r] > 0), float(temp[r]), int(topk[r]),
+                                   float(topp[r]), int(seeds[r]), int(steps[r]), r, C.byref(lpv))
+        assert gt[r] == want, (r, temp[r], topk[r], topp[r], gt[r], want)
+        assert gl[r] == pytest.approx(lpv.value, abs=1e-4, nan_ok=True), (r, gl[r], lpv.value)
+    for b in bufs + [tok, lp, ws]:
+        b.close()
