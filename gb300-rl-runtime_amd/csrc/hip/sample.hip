@@ -1424,7 +1424,10 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 //   bound   (the first kStreamRefresh chunks) the minimum over the waves of
 //           each wave's ceil(k/8)-th largest running lane max. At least k
 //           elements seen so far lie at or above it, so it is a lower bound
-//           of the row's k-th largest key, and it only grows;
+//           of the row's k-th largest key, and it only grows. Only the first
+//           chunk waits for every wave's entry; later refreshes read whatever
+//           entries are there, and the final bound is the largest of the
+//           waves' own;
 //   sum     sum exp(x - running max) in four partial sums, rescaled when the
 //           max grows (the log-sum-exp of the logprob). A NaN or +inf logit
 //           turns the sum NaN;
@@ -1468,9 +1471,9 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
     __shared__ uint32_t s_w[kKeptCap];
     __shared__ uint32_t s_idx[kKeptCap];
     __shared__ BlockShared bs;
-    __shared__ uint32_t s_bound[kStreamRefresh][kMergeWaves];
+    __shared__ uint32_t s_bound[kMergeWaves];      // each wave's latest candidate bound
     __shared__ float s_wm[kMergeWaves], s_wz[kMergeWaves], s_wv[kMergeWaves];
-    __shared__ uint32_t s_wi[kMergeWaves], s_wflag[kMergeWaves];
+    __shared__ uint32_t s_wi[kMergeWaves], s_wflag[kMergeWaves], s_wb[kMergeWaves];
     // the whole-row path's scratch reuses the candidate buffer
     static_assert(sizeof(RowScratch) <= sizeof(s_cand), "row scratch fits the candidate buffer");
     RowScratch &rs = *reinterpret_cast<RowScratch *>(s_cand);
@@ -1549,15 +1552,23 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
                 }
             }
         } else if (k_eff != 0 && c < kStreamRefresh) {
+            // Each wave's entry certifies kw elements of that wave at or above
+            // it, so the minimum over the entries bounds the row's k_eff-th
+            // largest from below. After the first chunk's barrier the waves
+            // refresh without one: entries only grow, and any mix of older
+            // and newer entries still certifies 8 kw >= k_eff elements.
             const uint32_t kw = (k_eff + kMergeWaves - 1) / kMergeWaves;
             const uint32_t ck = wave_kth_largest_key(rl_float_key(mnew), kw);
             if (lane == 0)
-                s_bound[c][wave] = ck;
-            __syncthreads();
-            uint32_t b = s_bound[c][0];
+                __hip_atomic_store(&s_bound[wave], ck, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (c == 0)
+                __syncthreads();
+            uint32_t b = ck;
 #pragma unroll
-            for (int w = 1; w < kMergeWaves; w++)
-                b = min(b, s_bound[c][w]);
+            for (int w = 0; w < kMergeWaves; w++)
+                if (w != wave)
+                    b = min(b, __hip_atomic_load(&s_bound[w], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            b = max(bound, b);
             bound = b;
             // x >= t selects the keys >= bound (the key order is the float
             // order with -0 = +0); the key of -inf admits every finite x
@@ -1615,14 +1626,17 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
         s_wflag[wave] = wflag;
         s_wv[wave] = bv;
         s_wi[wave] = bi;
+        s_wb[wave] = bound;
     }
     __syncthreads();
     float m = s_wm[0];
     uint32_t flags = s_wflag[0];
+    uint32_t key_lo = s_wb[0];  // the largest of the waves' bounds, each a valid one
 #pragma unroll
     for (int w = 1; w < kMergeWaves; w++) {
         m = fmaxf(m, s_wm[w]);
         flags |= s_wflag[w];
+        key_lo = max(key_lo, s_wb[w]);
     }
     const float zterm = mt == -INFINITY ? 0.f : zt * exp2f((mt - m) * kLog2e);
     const float wz = wave_sum(zterm);
@@ -1658,7 +1672,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
     bool exact = k_eff == 0 || flags != 0;
     if (!exact) {
         // ---- compact the lists: keys at or above the final bound ------------
-        const uint32_t key_lo = bound;
+        // (every wave's elements at or above it were tested against a bound
+        // no higher, so they are all listed)
         const uint32_t key_hi = rl_float_key(m);
         const uint32_t diff = key_lo ^ key_hi;
         const int hb = diff ? 31 - __builtin_clz(diff) : -1;
