@@ -1413,8 +1413,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 }
 
 // ---- one workgroup per row, the row streamed in chunks (rows with top-k) -----
-// Thread t's quad j of chunk c holds the logits from c * kStreamChunk +
-// (512 j + t) * 4, so each load instruction reads 1 KiB of consecutive logits
+// Thread t's quad j of chunk c holds the logits from 32,768 c + (512 j + t) *
+// 4, so each load instruction reads 1 KiB of consecutive logits
 // and each thread's elements ascend in (c, j, e). Two register buffers of
 // kStreamQuads quads alternate: the next chunk's loads are in flight while the
 // current chunk is processed, so the vector-ALU work overlaps the stream, and
@@ -1442,7 +1442,6 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
 // kKeptCap and rows without top-k take the exact whole-row path. Greedy rows
 // keep the (value desc, index asc) argmax instead of candidates.
 constexpr int kStreamQuads = 16;                                          // quads per thread per chunk
-constexpr uint32_t kStreamChunk = (uint32_t)kMergeThreads * 4u * kStreamQuads;  // 32,768 logits
 constexpr uint32_t kStreamRefresh = 2;                                    // chunks that raise the bound
 constexpr uint32_t kStreamList = 8;                                       // list entries per thread
 // Long rows (above 32,768 logits) take the stream kernel from this many rows
@@ -1455,32 +1454,32 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kBufferNontemporal = 2;
 
-__global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SampleParams p)
+// What one thread holds after streaming its part of a row.
+struct StreamOut {
+    bool greedy;
+    float inv_t;
+    uint32_t k_eff;
+    uint64_t draw;    // the row's Philox draw (when asked for and sampled)
+    float mt, zt;     // running max of x and sum exp(x - mt)
+    float bv;         // greedy: the running (value desc, index asc) argmax
+    uint32_t bi;
+    uint32_t nt;      // list entries appended (> kStreamList: overflow)
+    uint32_t bound;   // key lower bound of the k_eff-th largest of what was streamed
+};
+
+// The streaming part of the stream kernel: nch chunks of Q quads per thread
+// from column col0 (see the stream kernel's description), the candidates into
+// s_list, the wave bounds through s_bound. Called by every thread of the
+// workgroup.
+template <int Q>
+__device__ __forceinline__ StreamOut stream_row(const SampleParams &p, uint32_t row, uint32_t col0, uint32_t nch,
+                                                bool want_draw, uint2 (*s_list)[kMergeThreads], uint32_t *s_bound)
 {
-    const uint32_t row = blockIdx.x;
+    constexpr uint32_t chunk = (uint32_t)kMergeThreads * 4u * Q;
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-
-    __shared__ uint2 s_cand[kMergeCap];
-    __shared__ uint2 s_list[kStreamList][kMergeThreads];  // thread t's entries: column t
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_h2[2][256];
-    __shared__ unsigned long long s_whist[256];
-    __shared__ uint64_t s_keep[kKeptCap];
-    __shared__ uint64_t s_sort[kKeptCap];
-    __shared__ uint32_t s_w[kKeptCap];
-    __shared__ uint32_t s_idx[kKeptCap];
-    __shared__ BlockShared bs;
-    __shared__ uint32_t s_bound[kMergeWaves];      // each wave's latest candidate bound
-    __shared__ float s_wm[kMergeWaves], s_wz[kMergeWaves], s_wv[kMergeWaves];
-    __shared__ uint32_t s_wi[kMergeWaves], s_wflag[kMergeWaves], s_wb[kMergeWaves];
-    // the whole-row path's scratch reuses the candidate buffer
-    static_assert(sizeof(RowScratch) <= sizeof(s_cand), "row scratch fits the candidate buffer");
-    RowScratch &rs = *reinterpret_cast<RowScratch *>(s_cand);
-
     const float *lrow = p.logits + (size_t)row * p.row_stride;
     const uint32_t V = p.vocab;
-    const uint32_t nch = (V + kStreamChunk - 1) / kStreamChunk;
 
     // Buffer loads over the row's stride: the per-load offset is one scalar
     // and the thread's offset one register, so the loads of two chunks fit
@@ -1490,61 +1489,65 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void *)lrow, (short)0, (int)(p.row_stride * 4u), kBufferWord3);
     const uint32_t voff = tid * 16u;
-    auto load = [&](rl_f32x4 (&v)[kStreamQuads], uint32_t c) {
+    auto load = [&](rl_f32x4 (&v)[Q], uint32_t c) {
 #pragma unroll
-        for (int j = 0; j < kStreamQuads; j++)
+        for (int j = 0; j < Q; j++)
             v[j] = __builtin_bit_cast(rl_f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rsrc, (int)voff, (int)(c * kStreamChunk * 4u + j * kMergeThreads * 16u),
+                                                    rsrc, (int)voff, (int)((col0 + c * chunk) * 4u + j * kMergeThreads * 16u),
                                                     kBufferNontemporal));
     };
 
-    rl_f32x4 A[kStreamQuads], B[kStreamQuads];
+    StreamOut o;
+    rl_f32x4 A[Q], B[Q];
     load(A, 0);
     // the row's parameters and Philox draw, while the first loads are in flight
-    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
-    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
-    const uint32_t k_eff = greedy ? 0u : effective_k(row_topk(p, row), V);
-    const uint64_t draw = greedy ? 0ull : rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+    o.greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    o.inv_t = o.greedy ? 1.0f : 1.0f / row_temperature(p, row);
+    o.k_eff = o.greedy ? 0u : effective_k(row_topk(p, row), V);
+    o.draw = (o.greedy || !want_draw) ? 0ull : rl_sample_draw64(row_seed(p, row), row_step(p, row), row);
+    const bool greedy = o.greedy;
+    const float inv_t = o.inv_t;
+    const uint32_t k_eff = o.k_eff;
 
-    float mt = -INFINITY, zt = 0.f;  // running max of x and sum exp(x - mt)
-    float bv = -INFINITY;            // greedy: the running argmax
+    float mt = -INFINITY, zt = 0.f;
+    float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    uint32_t nt = 0;                 // list entries appended (> kStreamList: overflow)
-    uint32_t bound = 0;              // key lower bound of the row's k_eff-th largest
-    float t = INFINITY;              // candidates: !(x < t)
+    uint32_t nt = 0;
+    uint32_t bound = 0;
+    float t = INFINITY;  // candidates: !(x < t)
 
-    auto process = [&](rl_f32x4 (&v)[kStreamQuads], uint32_t c) {
-        const uint32_t c0 = c * kStreamChunk;
-        if (c0 + kStreamChunk > V) {  // workgroup-uniform: the chunk reaches past the row
+    auto process = [&](rl_f32x4 (&v)[Q], uint32_t c) {
+        const uint32_t c0 = col0 + c * chunk;
+        if (c0 + chunk > V) {  // workgroup-uniform: the chunk reaches past the row
 #pragma unroll
-            for (int j = 0; j < kStreamQuads; j++) {
+            for (int j = 0; j < Q; j++) {
                 const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     v[j][e] = col + (uint32_t)e < V ? v[j][e] : -INFINITY;
             }
         }
-        float qm[kStreamQuads];
+        float qm[Q];
 #pragma unroll
-        for (int j = 0; j < kStreamQuads; j++) {
+        for (int j = 0; j < Q; j++) {
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 v[j][e] = v[j][e] * inv_t;
             qm[j] = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
         }
-        float m4[kStreamQuads / 4];
+        float m4[Q / 4];
 #pragma unroll
-        for (int a = 0; a < kStreamQuads / 4; a++)
+        for (int a = 0; a < Q / 4; a++)
             m4[a] = fmaxf(fmaxf(qm[4 * a], qm[4 * a + 1]), fmaxf(qm[4 * a + 2], qm[4 * a + 3]));
         float cm = m4[0];
 #pragma unroll
-        for (int a = 1; a < kStreamQuads / 4; a++)
+        for (int a = 1; a < Q / 4; a++)
             cm = fmaxf(cm, m4[a]);
         const float mnew = fmaxf(mt, cm);
 
         if (greedy) {
 #pragma unroll
-            for (int j = 0; j < kStreamQuads; j++) {
+            for (int j = 0; j < Q; j++) {
                 if (qm[j] > bv) {  // the quad's lowest index holding its max
                     const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
                     bi = col + (v[j][0] == qm[j] ? 0u : v[j][1] == qm[j] ? 1u : v[j][2] == qm[j] ? 2u : 3u);
@@ -1553,10 +1556,10 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
             }
         } else if (k_eff != 0 && c < kStreamRefresh) {
             // Each wave's entry certifies kw elements of that wave at or above
-            // it, so the minimum over the entries bounds the row's k_eff-th
-            // largest from below. After the first chunk's barrier the waves
-            // refresh without one: entries only grow, and any mix of older
-            // and newer entries still certifies 8 kw >= k_eff elements.
+            // it, so the minimum over the entries bounds the k_eff-th largest
+            // from below. After the first chunk's barrier the waves refresh
+            // without one: entries only grow, and any mix of older and newer
+            // entries still certifies 8 kw >= k_eff elements.
             const uint32_t kw = (k_eff + kMergeWaves - 1) / kMergeWaves;
             const uint32_t ck = wave_kth_largest_key(rl_float_key(mnew), kw);
             if (lane == 0)
@@ -1583,7 +1586,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
         const float ml = mt == -INFINITY ? 0.f : mt * kLog2e;
         float z4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < kStreamQuads; j++)
+        for (int j = 0; j < Q; j++)
 #pragma unroll
             for (int e = 0; e < 4; e++)
                 z4[e] += __builtin_amdgcn_exp2f(fmaf(v[j][e], kLog2e, -ml));
@@ -1591,7 +1594,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
 
         if (k_eff != 0) {
 #pragma unroll
-            for (int j = 0; j < kStreamQuads; j++) {
+            for (int j = 0; j < Q; j++) {
                 if (!(qm[j] < t)) {
                     const uint32_t col = c0 + (uint32_t)(j * kMergeThreads + tid) * 4u;
 #pragma unroll
@@ -1615,65 +1618,113 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
         if (c + 1 < nch)
             process(B, c + 1);
     }
+    o.mt = mt;
+    o.zt = zt;
+    o.bv = bv;
+    o.bi = bi;
+    o.nt = nt;
+    o.bound = bound;
+    return o;
+}
 
-    // ---- the row's max, log-sum-exp, flags and (greedy) argmax ---------------
-    const float wm = wave_max(mt);
-    const uint32_t wflag = (__ballot(zt != zt) ? 1u : 0u) | (__ballot(nt > kStreamList) ? 2u : 0u);
-    if (greedy)
+// The workgroup's max, exp-sum relative to it, flags (1: a NaN sum, 2: a list
+// overflow), largest wave bound and (greedy) argmax, through one barrier.
+struct StreamTotals {
+    float m, zs, av;
+    uint32_t ai, flags, key_lo;
+};
+
+__device__ __forceinline__ StreamTotals stream_totals(const StreamOut &o, float *s_wm, float *s_wz, float *s_wv,
+                                                      uint32_t *s_wi, uint32_t *s_wflag, uint32_t *s_wb)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float wm = wave_max(o.mt);
+    const float wz = wave_sum(o.mt == -INFINITY ? 0.f : o.zt * exp2f((o.mt - wm) * kLog2e));
+    const uint32_t wflag = (__ballot(o.zt != o.zt) ? 1u : 0u) | (__ballot(o.nt > kStreamList) ? 2u : 0u);
+    float bv = o.bv;
+    uint32_t bi = o.bi;
+    if (o.greedy)
         wave_argmax(bv, bi);
     if (lane == 0) {
         s_wm[wave] = wm;
+        s_wz[wave] = wz;
         s_wflag[wave] = wflag;
         s_wv[wave] = bv;
         s_wi[wave] = bi;
-        s_wb[wave] = bound;
+        s_wb[wave] = o.bound;
     }
     __syncthreads();
-    float m = s_wm[0];
-    uint32_t flags = s_wflag[0];
-    uint32_t key_lo = s_wb[0];  // the largest of the waves' bounds, each a valid one
+    StreamTotals r;
+    r.m = s_wm[0];
+    r.flags = s_wflag[0];
+    r.key_lo = s_wb[0];  // the largest of the waves' bounds, each a valid one
+    r.av = s_wv[0];
+    r.ai = s_wi[0];
 #pragma unroll
     for (int w = 1; w < kMergeWaves; w++) {
-        m = fmaxf(m, s_wm[w]);
-        flags |= s_wflag[w];
-        key_lo = max(key_lo, s_wb[w]);
+        r.m = fmaxf(r.m, s_wm[w]);
+        r.flags |= s_wflag[w];
+        r.key_lo = max(r.key_lo, s_wb[w]);
+        if (s_wv[w] > r.av || (s_wv[w] == r.av && s_wi[w] < r.ai)) {
+            r.av = s_wv[w];
+            r.ai = s_wi[w];
+        }
     }
-    const float zterm = mt == -INFINITY ? 0.f : zt * exp2f((mt - m) * kLog2e);
-    const float wz = wave_sum(zterm);
-    if (lane == 0)
-        s_wz[wave] = wz;
-    __syncthreads();
-    float zs = 0.f;
+    r.zs = 0.f;
 #pragma unroll
     for (int w = 0; w < kMergeWaves; w++)
-        zs += s_wz[w];
-    const float lse = m + logf(zs);
+        r.zs += s_wm[w] == -INFINITY ? 0.f : s_wz[w] * exp2f((s_wm[w] - r.m) * kLog2e);
+    return r;
+}
 
-    if (greedy) {
+__global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SampleParams p)
+{
+    const uint32_t row = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+
+    __shared__ uint2 s_cand[kMergeCap];
+    __shared__ uint2 s_list[kStreamList][kMergeThreads];  // thread t's entries: column t
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint32_t s_h2[2][256];
+    __shared__ unsigned long long s_whist[256];
+    __shared__ uint64_t s_keep[kKeptCap];
+    __shared__ uint64_t s_sort[kKeptCap];
+    __shared__ uint32_t s_w[kKeptCap];
+    __shared__ uint32_t s_idx[kKeptCap];
+    __shared__ BlockShared bs;
+    __shared__ uint32_t s_bound[kMergeWaves];      // each wave's latest candidate bound
+    __shared__ float s_wm[kMergeWaves], s_wz[kMergeWaves], s_wv[kMergeWaves];
+    __shared__ uint32_t s_wi[kMergeWaves], s_wflag[kMergeWaves], s_wb[kMergeWaves];
+    // the whole-row path's scratch reuses the candidate buffer
+    static_assert(sizeof(RowScratch) <= sizeof(s_cand), "row scratch fits the candidate buffer");
+    RowScratch &rs = *reinterpret_cast<RowScratch *>(s_cand);
+
+    constexpr uint32_t chunk = (uint32_t)kMergeThreads * 4u * kStreamQuads;  // 32,768 logits
+    const uint32_t V = p.vocab;
+    const StreamOut so = stream_row<kStreamQuads>(p, row, 0u, (V + chunk - 1) / chunk, true, s_list, s_bound);
+    const StreamTotals tt = stream_totals(so, s_wm, s_wz, s_wv, s_wi, s_wflag, s_wb);
+    const float m = tt.m;
+    const float lse = m + logf(tt.zs);
+
+    if (so.greedy) {
         if (tid == 0) {
-            float v = s_wv[0];
-            uint32_t i = s_wi[0];
-#pragma unroll
-            for (int w = 1; w < kMergeWaves; w++)
-                if (s_wv[w] > v || (s_wv[w] == v && s_wi[w] < i)) {
-                    v = s_wv[w];
-                    i = s_wi[w];
-                }
-            p.token_out[row] = i >= V ? 0u : i;  // all -inf: lowest index
-            p.logprob_out[row] = v - lse;
+            p.token_out[row] = tt.ai >= V ? 0u : tt.ai;  // all -inf: lowest index
+            p.logprob_out[row] = tt.av - lse;
         }
         return;
     }
 
+    const uint32_t k_eff = so.k_eff;
     const float topp = row_topp(p, row);
     uint32_t tok = 0;
     float xtok = 0.f;
     bool xknown = false;
-    bool exact = k_eff == 0 || flags != 0;
+    bool exact = k_eff == 0 || tt.flags != 0;
     if (!exact) {
         // ---- compact the lists: keys at or above the final bound ------------
         // (every wave's elements at or above it were tested against a bound
         // no higher, so they are all listed)
+        const uint32_t key_lo = tt.key_lo;
         const uint32_t key_hi = rl_float_key(m);
         const uint32_t diff = key_lo ^ key_hi;
         const int hb = diff ? 31 - __builtin_clz(diff) : -1;
@@ -1686,6 +1737,7 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
         }
         if (tid < 256)
             s_h2[0][tid] = 0;
+        const uint32_t nt = so.nt;
         uint32_t own = 0;
 #pragma unroll
         for (uint32_t e = 0; e < kStreamList; e++)
@@ -1705,18 +1757,18 @@ __global__ __launch_bounds__(kMergeThreads) void sample_stream_kernel(SamplePara
             }
         }
         __syncthreads();
-        const TopkPick pk = topk_pick(nf, k_eff, hb, key_hi, prefix0, m, topp, draw, V, s_cand, s_h2, s_keep, s_sort,
-                                      s_w, s_idx, bs);
+        const TopkPick pk = topk_pick(nf, k_eff, hb, key_hi, prefix0, m, topp, so.draw, V, s_cand, s_h2, s_keep,
+                                      s_sort, s_w, s_idx, bs);
         tok = pk.tok;
         xtok = pk.xtok;
         xknown = pk.xknown;
         exact = pk.overflow;
     }
     if (exact)
-        tok = exact_row_sample(p, row, inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
+        tok = exact_row_sample(p, row, so.inv_t, k_eff, topp, m, rs, s_hist, s_whist, bs);
     if (tid == 0) {
         p.token_out[row] = tok;
-        const float x = xknown ? xtok : p.logits[(size_t)row * p.row_stride + tok] * inv_t;
+        const float x = xknown ? xtok : p.logits[(size_t)row * p.row_stride + tok] * so.inv_t;
         p.logprob_out[row] = x - lse;
     }
 }

@@ -166,14 +166,16 @@ def test_row_kernel_per_row_parameters(rl, gpu, orc, olib):
         b.close()
 
 
-@pytest.mark.parametrize("rows,vocab,stride", [(160, 50257, 50260), (144, 128256, 128256)])
+@pytest.mark.parametrize("rows,vocab,stride", [(160, 50257, 50260), (144, 128256, 128256), (40, 128256, 128256),
+                                                (24, 70001, 70004)])
 def test_stream_kernel_mixed_rows(rl, gpu, orc, olib, rows, vocab, stride):
-    """Per-row arrays over enough long rows for the one-workgroup-per-row
-    stream kernel: greedy rows (temperature 0) next to top-k 1 / 7 / 50 / 256 /
-    300 rows and rows without top-k (its exact whole-row path); rows of heavy
-    ties, all equal (candidate lists overflow), all -inf, one finite logit,
-    spike ties and a row ending in -inf. Every row against the oracle with its
-    own parameters."""
+    """Per-row arrays over long rows: 144 or more rows take the
+    one-workgroup-per-row stream kernel, fewer the split and merge kernels.
+    Greedy rows (temperature 0) next to top-k 1 / 7 / 50 / 256 / 300 rows and
+    rows without top-k (the exact whole-row path); rows of heavy ties, all
+    equal (candidate lists overflow), all -inf, one finite logit, spike ties
+    and a row ending in -inf. Every row against the oracle with its own
+    parameters."""
     rng = np.random.default_rng(rows + vocab)
     x = np.full((rows, stride), np.float32(9.0))          # padding past vocab never read
     x[:, :vocab] = rng.standard_normal((rows, vocab), dtype=np.float32) * np.float32(1.5)
