@@ -214,3 +214,22 @@ def test_stream_kernel_mixed_rows(rl, gpu, orc, olib, rows, vocab, stride):
         assert gl[r] == pytest.approx(lpv.value, abs=1e-4, nan_ok=True), (r, gl[r], lpv.value)
     for b in bufs + [tok, lp, ws]:
         b.close()
+
+
+def test_greedy_long_rows_repeated_calls(rl, gpu, orc, olib):
+    """Greedy batches of rows above 32,768 logits take one kernel whose
+    last-arriving slice per row combines the row and resets the row's arrival
+    counter: calls of different shapes back to back (more and fewer rows and
+    slices than the call before) must each match the oracle, ties to the
+    lowest index and all -inf rows included."""
+    rng = np.random.default_rng(515)
+    for it, (rows, vocab, stride) in enumerate([(8, 128256, 128256), (3, 50001, 50004), (40, 40000, 40000),
+                                                (8, 128256, 128256), (1, 524288, 524288), (40, 40000, 40000)]):
+        x = np.full((rows, stride), np.float32(50.0))          # padding past vocab never read
+        x[:, :vocab] = rng.standard_normal((rows, vocab), dtype=np.float32)
+        x[0, rng.choice(vocab, 4, replace=False)] = np.float32(6.0)   # a 4-way tie: lowest index
+        if rows > 2:
+            x[2, :vocab] = -np.inf
+        print(f"[sample] greedy call {it}: {rows} x {vocab}", flush=True)
+        tok = _check(rl, orc, olib, x, vocab=vocab, greedy=True)
+        assert tok[0] == np.flatnonzero(x[0, :vocab] == np.float32(6.0)).min()
