@@ -590,8 +590,10 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
         if (p.out_f32)
             p.out_f32[obase + e] = v;
     };
-    constexpr int NPR = 8;                              // partials merged from registers
     constexpr int EPT = (NE + NTHR - 1) / NTHR;         // output elements per thread
+    // partials merged from registers, all loaded in one round: up to 40 when
+    // a thread has one output element (long rows over a head subset), 8 else
+    constexpr int NPR = EPT == 1 ? 40 : 8;
     if (np <= (uint32_t)NPR) {
         // few partials: every load is issued before the first use
         float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
