@@ -167,10 +167,12 @@ def test_row_kernel_per_row_parameters(rl, gpu, orc, olib):
 
 
 @pytest.mark.parametrize("rows,vocab,stride", [(160, 50257, 50260), (144, 128256, 128256), (40, 128256, 128256),
-                                                (24, 70001, 70004)])
+                                                (24, 70001, 70004), (150, 32769, 32772), (144, 65537, 65540)])
 def test_stream_kernel_mixed_rows(rl, gpu, orc, olib, rows, vocab, stride):
     """Per-row arrays over long rows: 144 or more rows take the
     one-workgroup-per-row stream kernel, fewer the split and merge kernels.
+    32,769 and 65,537 logits end one logit into the stream kernel's second
+    and third 32,768-logit chunk (an odd chunk count, the pipeline's tail).
     Greedy rows (temperature 0) next to top-k 1 / 7 / 50 / 256 / 300 rows and
     rows without top-k (the exact whole-row path); rows of heavy ties, all
     equal (candidate lists overflow), all -inf, one finite logit, spike ties
