@@ -48,9 +48,21 @@ def _case(rl, rows, vocab, hidden, seed, check_rows=None, check_cols=None, repea
 # up to 256 rows the 256 x 128 tile, above it the 256 x 256 tile (three M
 # tiles and a partial N tile at 700 x 777)
 @pytest.mark.parametrize("rows,vocab,hidden", [(1, 129, 64), (130, 1000, 128), (64, 32000, 256),
-                                               (257, 300, 4096), (700, 777, 192)])
+                                               (256, 130, 192), (200, 4000, 128), (257, 300, 4096),
+                                               (700, 777, 192)])
 def test_projection_shapes(rl, gpu, rows, vocab, hidden):
     _case(rl, rows, vocab, hidden, seed=rows + vocab + hidden)
+
+
+def test_projection_loop_shape(rl, gpu):
+    """256 x 4096 -> 32,000 (the rollout loop's 256 slots, the tile whose
+    waves split the X and W copies): every column of 24 rows, every row of
+    64 columns."""
+    rng = np.random.default_rng(6)
+    rows = np.sort(rng.choice(256, 24, replace=False))
+    _case(rl, 256, 32000, 4096, seed=8, check_rows=rows, repeats=5)
+    cols = np.sort(rng.choice(32000, 64, replace=False))
+    _case(rl, 256, 32000, 4096, seed=8, check_cols=cols)
 
 
 def test_projection_rollout_shape(rl, gpu):
