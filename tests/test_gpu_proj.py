@@ -72,3 +72,36 @@ def test_projection_rollout_shape(rl, gpu):
     _case(rl, 512, 32000, 4096, seed=4, check_rows=rows, repeats=5)
     cols = np.sort(rng.choice(32000, 64, replace=False))
     _case(rl, 512, 32000, 4096, seed=4, check_cols=cols)
+
+
+@pytest.mark.parametrize("rows,vocab,hidden,pad_x,pad_w,pad_o", [(130, 1000, 128, 8, 24, 3), (300, 517, 192, 64, 8, 1)])
+def test_projection_padded_strides(rl, gpu, rows, vocab, hidden, pad_x, pad_w, pad_o):
+    """Row strides past the data (x, w padded by multiples of 8 elements, the
+    logits by any count): the padding is never read as data, the logits'
+    padding is never written, and the result meets the same bound as the
+    contiguous case. Both tiles (up to and above 256 rows)."""
+    import ctypes as C
+    print(f"[proj] padded strides rows={rows} vocab={vocab} hidden={hidden}", flush=True)
+    rng = np.random.default_rng(rows + pad_w)
+    xs, ws, los = hidden + pad_x, hidden + pad_w, vocab + pad_o
+    x = np.full((rows, xs), synth.f32_to_bf16(np.float32([1e4]))[0], dtype=np.uint16)
+    w = np.full((vocab, ws), synth.f32_to_bf16(np.float32([-1e4]))[0], dtype=np.uint16)
+    x[:, :hidden] = synth.f32_to_bf16(rng.standard_normal((rows, hidden), dtype=np.float32))
+    w[:, :hidden] = synth.f32_to_bf16(rng.standard_normal((vocab, hidden), dtype=np.float32) * np.float32(0.02))
+    sentinel = np.float32(-12345.5)
+    dx, dw = rl.DeviceBuffer.from_array(x), rl.DeviceBuffer.from_array(w)
+    out = rl.DeviceBuffer.from_array(np.full((rows, los), sentinel, np.float32))
+    a = rl.ProjArgs(x=dx.ptr, w=dw.ptr, logits=out.ptr, rows=rows, vocab=vocab, hidden=hidden, x_stride=xs,
+                    w_stride=ws, logits_stride=los)
+    rl.check(rl.lib().rl_hip_logits_proj(C.byref(a)), "rl_hip_logits_proj")
+    rl.sync()
+    got = out.download(np.float32, (rows, los))
+    assert (got[:, vocab:] == sentinel).all()
+    xf = synth.bf16_to_f32(x[:, :hidden]).astype(np.float64)
+    wf = synth.bf16_to_f32(w[:, :hidden]).astype(np.float64)
+    ref = xf @ wf.T
+    bound = 2.0 * (hidden - 1) * 2.0**-24 * (np.abs(xf) @ np.abs(wf).T)
+    err = np.abs(got[:, :vocab] - ref)
+    assert np.all(err <= bound + 1e-30), float((err / np.maximum(bound, 1e-30)).max())
+    for b in (dx, dw, out):
+        b.close()
