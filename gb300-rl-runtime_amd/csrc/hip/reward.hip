@@ -101,6 +101,11 @@ extern "C" int rl_hip_reward_advantage(const rl_reward_args_t *a)
                      a->rollouts, a->group_size, kMaxGroup);
         return -1;
     }
+    if (a->target_len > a->target_stride) {
+        rl_set_error("rl_hip_reward_advantage: target_len %u exceeds target_stride %u", a->target_len,
+                     a->target_stride);
+        return -1;
+    }
     RewardParams p;
     p.tokens = a->tokens;
     p.n_tokens = a->n_tokens;

@@ -153,7 +153,8 @@ int rl_hip_logits_proj(const rl_logits_proj_args_t *args);
  * tokens[r][i] == targets[group][i]}; reward_r = (count_r & 0xFF) / 255.0f;
  * advantage_r = (reward_r - mean) / std over the group, population std, 0 when
  * std is 0 - bit-identical to reward_match_count / reward_group_advantage in
- * reward.h. descs, when given, receives one RewardDesc per rollout. */
+ * reward.h. descs, when given, receives one RewardDesc per rollout.
+ * target_len <= target_stride (a target row holds target_len tokens). */
 typedef struct {
     const uint32_t *tokens;      /* device [rollouts][token_stride] */
     const uint32_t *n_tokens;    /* device [rollouts] */

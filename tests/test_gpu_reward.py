@@ -77,3 +77,51 @@ def test_reward_advantage_matches_oracle_and_host(rl, gpu, olib, groups, gs, T, 
         assert np.all(ga[gs:2 * gs] == 0)
     for b in list(d.values()) + [rew, adv, descs]:
         b.close()
+
+
+def test_reward_distinct_strides_largest_group(rl, gpu, olib):
+    """Token rows of 300, target rows of 260 holding 256 target tokens, groups
+    of 64 (the largest): counts stop at min(n_tokens, target_len,
+    token_stride), with n_tokens past both; bit-identical to the oracle."""
+    groups, gs, TS, GS_, TL = 2, 64, 300, 260, 256
+    rng = np.random.default_rng(64)
+    R = groups * gs
+    targets = rng.integers(0, 32000, (groups, GS_), dtype=np.uint32)
+    tokens = rng.integers(0, 32000, (R, TS), dtype=np.uint32)
+    full = np.zeros((R, TS), np.uint32)
+    full[:, :GS_] = np.repeat(targets, gs, axis=0)
+    hit = rng.random((R, TS)) < 0.7
+    tokens[hit] = full[hit]
+    tokens[:, TL:GS_] = full[:, TL:GS_]                       # matches past target_len never count
+    n_tok = rng.integers(200, 330, R).astype(np.uint32)
+    d = {k: rl.DeviceBuffer.from_array(v) for k, v in (("tok", tokens), ("n", n_tok), ("tgt", targets))}
+    rew, adv = rl.DeviceBuffer(R * 4, zero=True), rl.DeviceBuffer(R * 4, zero=True)
+    a = rl.RewardArgs(tokens=d["tok"].ptr, n_tokens=d["n"].ptr, targets=d["tgt"].ptr, rollouts=R, group_size=gs,
+                      token_stride=TS, target_stride=GS_, target_len=TL, descs=None, reward=rew.ptr,
+                      advantage=adv.ptr)
+    rl.check(rl.lib().rl_hip_reward_advantage(C.byref(a)), "rl_hip_reward_advantage")
+    rl.sync()
+    orr = np.zeros(R, np.float32)
+    for r in range(R):
+        n = min(int(n_tok[r]), TL, TS)
+        t = np.ascontiguousarray(tokens[r])
+        g = np.ascontiguousarray(targets[r // gs])
+        orr[r] = olib.orc_reward_score(olib.orc_match_count(t.ctypes.data, g.ctypes.data, n))
+    ora = np.zeros(R, np.float32)
+    olib.orc_group_advantage(orr.ctypes.data, groups, gs, ora.ctypes.data)
+    assert np.array_equal(rew.download(np.float32, R).view(np.uint32), orr.view(np.uint32))
+    assert np.array_equal(adv.download(np.float32, R).view(np.uint32), ora.view(np.uint32))
+    for b in list(d.values()) + [rew, adv]:
+        b.close()
+
+
+def test_reward_argument_checks(rl, gpu):
+    """Refused before any launch: target_len past target_stride, groups of 0
+    or more than 64, rollouts not a multiple of the group size."""
+    buf = rl.DeviceBuffer(4096, zero=True)
+    base = dict(tokens=buf.ptr, n_tokens=buf.ptr, targets=buf.ptr, rollouts=8, group_size=4, token_stride=8,
+                target_stride=8, target_len=8, descs=None, reward=buf.ptr, advantage=buf.ptr)
+    for bad in ({"target_len": 9}, {"group_size": 0}, {"group_size": 65, "rollouts": 130}, {"rollouts": 6}):
+        a = rl.RewardArgs(**{**base, **bad})
+        assert rl.lib().rl_hip_reward_advantage(C.byref(a)) != 0, bad
+    buf.close()
