@@ -562,10 +562,12 @@ __device__ __forceinline__ float wave_sum_f32(float x)
     return x;
 }
 
+// The merge of row (b, g) from the partials of streams wf .. wl at
+// p.part[(w + row)] (a stream being a wave of an even split or a piece of
+// the fused step); nothing to do when one stream covered the row.
 template <int D, int G, int DT, int NTHR, int GH>
-__device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, uint32_t R0,
-                                          uint32_t nu, uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f,
-                                          float *s_L)
+__device__ __forceinline__ void merge_span(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, uint32_t wf,
+                                           uint32_t wl, bool bad, uint32_t tid, float *s_f, float *s_L)
 {
     static_assert(G % GH == 0, "head subset");
     constexpr int PART = G * D + 2 * G;
@@ -573,10 +575,6 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
     constexpr uint32_t nthr = NTHR;
     const uint32_t row = b * p.kv_heads + g;
     const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
-    const uint32_t R1 = R0 + nu;
-    // wave holding tile R0 / tile R1 - 1: the largest w with floor(w U / NW) <= tile
-    const uint32_t wf = (uint32_t)((((uint64_t)R0 + 1) * NW - 1) / U);
-    const uint32_t wl = (uint32_t)(((uint64_t)R1 * NW - 1) / U);
     if (wf == wl)
         return;
     const float *part = p.part + (size_t)(wf + row) * PART;
@@ -592,8 +590,9 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
     };
     constexpr int EPT = (NE + NTHR - 1) / NTHR;         // output elements per thread
     // partials merged from registers, all loaded in one round: up to 40 when
-    // a thread has one output element (long rows over a head subset), 8 else
-    constexpr int NPR = EPT == 1 ? 40 : 8;
+    // a thread has one output element (long rows over a head subset), 16 with
+    // two, 8 else
+    constexpr int NPR = EPT == 1 ? 40 : EPT == 2 ? 16 : 8;
     if (np <= (uint32_t)NPR) {
         // few partials: every load is issued before the first use
         float o[NPR][EPT], mm[NPR][EPT], ll[NPR][EPT];
@@ -718,6 +717,17 @@ __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint3
         }
         store(eg, O, L);
     }
+}
+
+template <int D, int G, int DT, int NTHR, int GH>
+__device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, uint32_t R0,
+                                          uint32_t nu, uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f,
+                                          float *s_L)
+{
+    // wave holding tile R0 / tile R0 + nu - 1: the largest w with floor(w U / NW) <= tile
+    const uint32_t wf = (uint32_t)((((uint64_t)R0 + 1) * NW - 1) / U);
+    const uint32_t wl = (uint32_t)((((uint64_t)R0 + nu) * NW - 1) / U);
+    merge_span<D, G, DT, NTHR, GH>(p, b, g, h0, wf, wl, bad, tid, s_f, s_L);
 }
 
 // Writes heads h0 .. h0 + GH - 1 of a row without tiles: zeros (ctx 0) or

@@ -421,6 +421,16 @@ extern "C" int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv
     return attn_run(attn, append_params(append));
 }
 
+int rl_attn_check(const rl_attn_decode_args_t *a)
+{
+    return validate(a);
+}
+
+int rl_decode_step_check(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append, const char *who)
+{
+    return step_validate(attn, append, who);
+}
+
 int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                           const uint32_t *row_map)
 {

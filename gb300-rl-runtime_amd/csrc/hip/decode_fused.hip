@@ -1,0 +1,499 @@
+// decode_fused.hip - one decode step of a micro-batch and the sampling of
+// another micro-batch's logits in one persistent gfx950 launch, then the
+// log-sum-exp merge of split rows with the KV append.
+//
+// In a rollout loop that keeps two micro-batches of rollouts in flight, step
+// t runs the attention of micro-batch t % 2 while the tokens of the other
+// micro-batch are drawn from the logits its previous step produced (the
+// projection runs between the two). Both halves are HBM streams with no data
+// dependence between them, so one launch runs them side by side:
+//
+//  grid     one 512-thread workgroup (8 waves) per compute unit. Workgroup w
+//           runs on XCD w % 8.
+//  sample   workgroups 0 .. sample_wgs - 1 (a multiple of 8, so each XCD
+//           gets the same number) each sample rows w, w + sample_wgs, ...
+//           with the streamed one-workgroup-per-row sampler
+//           (stream_sample_row, sample_core.h), then stream attention tiles.
+//  attend   the tile sequence of the attention (rows (b, g) in order, 16-token
+//           tiles, as in attn_decode.hip) is cut into 8 contiguous XCD ranges
+//           and each range into one piece per wave of that XCD, weighted: a
+//           sampling wave's piece is smaller by the time its workgroup spends
+//           sampling, so that both kinds of wave end together. Tiles stream
+//           through LDS exactly as in attn_decode.hip (attn_stream,
+//           attn_core.h); a row split between pieces leaves one fp32 partial
+//           per piece at slot piece + row. The pieces depend only on the
+//           step's tile count, so results do not depend on which compute unit
+//           streams what.
+//  merge    merge_pieces_kernel: the split rows' partials combined by the
+//           same log-sum-exp as attn_merge_kernel, and the step's K/V token
+//           appended.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rl_hip.h"
+#include "rl_hip_internal.h"
+#include "attn_core.h"
+#include "kv_append_core.h"
+#include "kv_layout.h"
+#include "rl_dev_common.h"
+#include "sample_core.h"
+
+namespace {
+
+constexpr uint32_t kXcds = 8;                  // MI355X: workgroup w runs on XCD w % 8
+constexpr int kFWaves = 8;                     // waves per workgroup
+constexpr int kFThreads = kFWaves * 64;
+constexpr int kFStages = 2;                    // tile stages per wave (as attn_decode_kernel)
+constexpr uint32_t kFusedMaxBatch = 1024;      // rollouts whose tile prefix fits the LDS
+static_assert(kFThreads == kMergeThreads, "the sampling role runs the stream sampler's workgroup shape");
+// Quads per thread of the sampling role's chunks (16,384 logits): half the
+// stream kernel's, so that the two register buffers beside the attention
+// role's state stay within the 256 VGPRs of two waves per SIMD.
+constexpr int kFusedQuads = 8;
+
+// ---- the split of the tiles among the waves ------------------------------------
+// What the split follows from, identically in both kernels once the step's
+// tile count U is known.
+struct SplitIn {
+    uint32_t wgs, sample_wgs;   // workgroups, of which sampling first (multiples of 8)
+    uint32_t tile_bytes;        // K and V bytes of one tile
+    uint64_t sample_bytes;      // logits bytes one sampling workgroup streams
+    float sample_cost;          // its time per byte over an attention workgroup's
+};
+
+// A sampling workgroup streams its logits slower than an attention workgroup
+// streams the same bytes of KV: the top-k tail and the per-chunk processing
+// sit on one compute unit. Measured on the 64 x 128,256 (top-k 50, top-p 0.9)
+// batch beside the 64-rollout attention: 36-40 us per row, the attention
+// workgroups' tiles at about 2.7 us per wave; a factor of 1.8 ended both kinds
+// of wave together best (1.0, 1.4, 1.8 and 2.2 tried).
+constexpr float kSampleCost = 1.8f;
+
+// The pieces of one XCD's N tiles, one per wave of the XCD: the Aa attention
+// waves' first (weight 256 each), then the As sampling waves' (weight ws).
+// Piece k is [floor(N c_k / W), floor(N c_{k+1} / W)), c_k the weight of the
+// pieces before k, W the total. With fewer than 4 tiles per wave the weights
+// are equal and only min(waves, N) pieces exist (waves past them idle), so no
+// piece is empty.
+struct Sched {
+    uint32_t N, np, Aw, ws;  // tiles, pieces, pieces of weight 256, weight of the others
+    uint64_t W;
+};
+
+__host__ __device__ inline Sched sched_of(uint32_t N, uint32_t Aa, uint32_t As, uint32_t ws)
+{
+    Sched s;
+    s.N = N;
+    const uint32_t n = Aa + As;
+    if (n > 0 && N >= 4u * n) {
+        s.np = n;
+        s.Aw = Aa;
+        s.ws = ws;
+    } else {
+        s.np = n < N ? n : N;
+        s.Aw = s.np;
+        s.ws = 256u;
+    }
+    s.W = 256ull * s.Aw + (uint64_t)s.ws * (s.np - s.Aw);
+    return s;
+}
+
+__host__ __device__ inline uint32_t piece_start(const Sched &s, uint32_t k)
+{
+    const uint64_t c = 256ull * (k < s.Aw ? k : s.Aw) + (uint64_t)s.ws * (k > s.Aw ? k - s.Aw : 0u);
+    return (uint32_t)(((uint64_t)s.N * c) / s.W);
+}
+
+// The piece holding offset o (o < N): the largest k with start(k) <= o, i.e.
+// N c_k < (o + 1) W.
+__host__ __device__ inline uint32_t piece_at(const Sched &s, uint32_t o)
+{
+    const uint64_t t = ((uint64_t)o + 1) * s.W;
+    if (o < piece_start(s, s.Aw))
+        return (uint32_t)((t - 1) / (256ull * s.N));
+    return s.Aw + (uint32_t)((t - 256ull * s.Aw * s.N - 1) / ((uint64_t)s.ws * s.N));
+}
+
+// XCD x's range of the U tiles: [floor(x U / 8), floor((x + 1) U / 8)).
+__host__ __device__ inline uint32_t xcd_start(uint32_t x, uint32_t U)
+{
+    return (uint32_t)(((uint64_t)x * U) / kXcds);
+}
+
+// The schedule of XCD x: a sampling wave's weight is 1 - sample_cost x (its
+// workgroup's logits bytes / a workgroup's share of all bytes), at least 1/4.
+__host__ __device__ inline Sched sched_x(uint32_t x, uint32_t U, const SplitIn &in)
+{
+    const uint32_t Aa = (in.wgs - in.sample_wgs) / kXcds * kFWaves;
+    const uint32_t As = in.sample_wgs / kXcds * kFWaves;
+    const double fair = ((double)U * in.tile_bytes + (double)in.sample_bytes * in.sample_wgs) / in.wgs;
+    double w = fair > 0.0 ? 1.0 - (double)in.sample_cost * (double)in.sample_bytes / fair : 1.0;
+    w = w < 0.25 ? 0.25 : (w > 1.0 ? 1.0 : w);
+    return sched_of(xcd_start(x + 1, U) - xcd_start(x, U), Aa, As, (uint32_t)(w * 256.0 + 0.5));
+}
+
+// Global index of the first piece of XCD x: pieces are numbered XCD by XCD,
+// so the index grows with the tile position.
+__device__ inline uint32_t xcd_base(uint32_t x, uint32_t U, const SplitIn &in)
+{
+    uint32_t base = 0;
+    for (uint32_t y = 0; y < x; y++)
+        base += sched_x(y, U, in).np;
+    return base;
+}
+
+// Global index of the piece holding tile t (t < U).
+__device__ inline uint32_t global_piece_of(uint32_t t, uint32_t U, const SplitIn &in)
+{
+    const uint32_t x = (uint32_t)((((uint64_t)t + 1) * kXcds - 1) / U);
+    return xcd_base(x, U, in) + piece_at(sched_x(x, U, in), t - xcd_start(x, U));
+}
+
+// ---- the kernels ---------------------------------------------------------------------
+
+struct FusedParams {
+    AttnParams p;          // p.part: partials at (piece + row); p.cum: [batch + 1] (written by workgroup 0)
+    SampleParams sp;       // the sampled micro-batch
+    SplitIn si;
+};
+
+template <int D, int G, int DT, int TPB>
+struct FusedLayout {
+    using C = Cfg<D, G, DT, TPB>;
+    static constexpr int ST_BYTES = kFStages * kFWaves * C::STAGE;
+    static constexpr int Q_OFF = ST_BYTES;
+    static constexpr int Q_BYTES = kFWaves * kFStages * C::QSLOT;
+    static constexpr int CUM_OFF = Q_OFF + Q_BYTES;
+    static constexpr int ATTN_END = CUM_OFF + (int)((kFusedMaxBatch + 1) * 4);
+    static constexpr int TOTAL = ATTN_END > (int)sizeof(StreamLds) ? ATTN_END : (int)sizeof(StreamLds);
+    static constexpr bool FITS = TOTAL <= 160 * 1024;
+};
+
+// Largest b < batch with cum[b] <= s (the rollout holding tile s < U; rollouts
+// without tiles share their successor's prefix and are skipped).
+__device__ __forceinline__ uint32_t rollout_of(RL_LDS const uint32_t *cum, uint32_t batch, uint32_t s)
+{
+    uint32_t lo = 0, hi = batch;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (cum[mid] <= s)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+template <int D, int G, int DT, int TPB>
+__global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
+{
+    using C = Cfg<D, G, DT, TPB>;
+    using LY = FusedLayout<D, G, DT, TPB>;
+    static_assert(LY::FITS, "fused step LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
+    const AttnParams &p = f.p;
+    const uint32_t wg = blockIdx.x;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    const bool sampler = wg < f.si.sample_wgs;
+
+    // ---- sampling role ----------------------------------------------------------
+    if (sampler) {
+        StreamLds &L = *reinterpret_cast<StreamLds *>(lds);
+        for (uint32_t row = wg; row < f.sp.rows; row += f.si.sample_wgs) {
+            stream_sample_row<kFusedQuads>(f.sp, row, L);
+            __syncthreads();  // L is rewritten by the next row or by the attention below
+        }
+    }
+
+    // ---- tile prefix over the rollouts, in LDS -----------------------------------
+    RL_LDS uint32_t *cum = (RL_LDS uint32_t *)(lds + LY::CUM_OFF);
+    RL_LDS uint32_t *wtot = (RL_LDS uint32_t *)(lds + LY::Q_OFF);  // q slots as scratch until the copies start
+    {
+        const uint32_t per = (p.batch + kFThreads - 1) / kFThreads;
+        const uint32_t b0 = min(tid * per, p.batch), b1 = min(b0 + per, p.batch);
+        uint32_t S = 0;
+        for (uint32_t bb = b0; bb < b1; bb++)
+            S += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+        const uint32_t inc = rl_wave_incl_scan_u32(S);
+        if (lane == 63)
+            wtot[wave] = inc;
+        __syncthreads();
+        uint32_t before = 0, U = 0;
+#pragma unroll
+        for (int v = 0; v < kFWaves; v++) {
+            const uint32_t t = wtot[v];
+            before += v < wave ? t : 0u;
+            U += t;
+        }
+        uint32_t c = before + inc - S;
+        for (uint32_t bb = b0; bb < b1; bb++) {
+            cum[bb] = c;
+            if (wg == 0)
+                p.cum[bb] = c;
+            c += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+        }
+        if (tid == 0) {
+            cum[p.batch] = U;
+            if (wg == 0)
+                p.cum[p.batch] = U;
+        }
+        __syncthreads();  // prefix and scratch reads done before any copy lands in the q slots
+    }
+
+    // ---- attention role: this wave's piece ---------------------------------------
+    const uint32_t U = cum[p.batch];
+    if (U == 0)
+        return;
+    const uint32_t x = wg % kXcds;
+    const uint32_t Aa = (f.si.wgs - f.si.sample_wgs) / kXcds * kFWaves;
+    const uint32_t k = sampler ? Aa + (wg / kXcds) * kFWaves + (uint32_t)wave
+                               : ((wg - f.si.sample_wgs) / kXcds) * kFWaves + (uint32_t)wave;
+    const Sched s = sched_x(x, U, f.si);
+    if (k >= s.np)
+        return;
+    const uint32_t x0 = xcd_start(x, U);
+    const uint32_t s_begin = x0 + piece_start(s, k);
+    const uint32_t s_end = x0 + piece_start(s, k + 1);
+    const uint32_t b = rollout_of(cum, p.batch, s_begin);
+    RL_LDS uint8_t *st = (RL_LDS uint8_t *)lds + wave * C::STAGE;
+    RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds + LY::Q_OFF + wave * kFStages * C::QSLOT;
+    attn_stream<D, G, DT, TPB, kFStages>(p, CtxFromArray{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b,
+                                         cum[b], st, kFWaves * C::STAGE, qs, lane);
+}
+
+// Combines the partials of every row split across pieces (merge_span), writes
+// rows without tiles and appends the step's K/V token (the row's first
+// workgroup). HS workgroups of G / HS heads per row, as attn_merge_kernel.
+template <int D, int G, int DT, int HS>
+__global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendParams ap, SplitIn si)
+{
+    constexpr int GH = G / HS;
+    __shared__ float s_f[kMergeLds * G];
+    __shared__ float s_L[G];
+    const uint32_t g = blockIdx.x / HS;
+    const uint32_t h0 = (blockIdx.x % HS) * GH;
+    const uint32_t b = blockIdx.y;
+    const uint32_t cin = rl_sload(p.ctx + b);
+    const uint32_t U = rl_sload(p.cum + p.batch);
+    const uint32_t cum_b = rl_sload(p.cum + b);
+    if (ap.arena && h0 == 0 && threadIdx.x >= 192)
+        append_row(ap, b, g, threadIdx.x - 192, 64);
+    const bool bad = cin > p.max_ctx;
+    const uint32_t nu = tiles_of(p, cin);
+    if (nu == 0) {
+        empty_row<D, G, DT, GH>(p, b, g, h0, bad, threadIdx.x, 256);
+        return;
+    }
+    const uint32_t R0 = cum_b + g * nu;
+    const uint32_t wf = global_piece_of(R0, U, si);
+    const uint32_t wl = global_piece_of(R0 + nu - 1, U, si);
+    merge_span<D, G, DT, 256, GH>(p, b, g, h0, wf, wl, bad, threadIdx.x, s_f, s_L);
+}
+
+// ---- launcher ----------------------------------------------------------------------
+
+struct FusedWs {
+    size_t cum_off, part_off, total;
+};
+
+// Partials: at most one per wave-piece plus one per row (slot piece + row).
+FusedWs fused_ws(const rl_attn_decode_args_t *a, const SplitIn &si)
+{
+    FusedWs w;
+    const uint32_t G = a->q_heads / a->kv_heads;
+    const size_t part = (size_t)G * a->layout.head_dim + 2 * G;
+    const size_t rows = (size_t)a->batch * a->kv_heads;
+    w.cum_off = 0;
+    w.part_off = (((size_t)a->batch + 1) * 4 + 255) / 256 * 256;
+    w.total = w.part_off + ((size_t)si.wgs * kFWaves + rows) * part * 4;
+    return w;
+}
+
+template <int D, int G, int DT, int TPB>
+bool fits()
+{
+    return FusedLayout<D, G, DT, TPB>::FITS;
+}
+
+template <int D, int G, int DT, int TPB>
+int launch_fused(const FusedParams &f, const AppendParams &ap, uint32_t wgs)
+{
+    if constexpr (!FusedLayout<D, G, DT, TPB>::FITS) {
+        rl_set_error("rl_hip_decode_sample_step: shape does not fit the fused step");
+        return -1;
+    } else {
+        hipLaunchKernelGGL((decode_fused_kernel<D, G, DT, TPB>), dim3(wgs), dim3(kFThreads), 0, rl_stream(), f);
+        if (rl_check_launch("decode_fused_kernel launch"))
+            return -1;
+        constexpr int HS = G >= 2 ? G / 2 : 1;
+        // rows averaging more partials than the one-workgroup register path
+        // holds (16 at two output elements per thread) take workgroups of two
+        // heads, as attn_merge_kernel
+        const uint64_t rows = (uint64_t)f.p.batch * f.p.kv_heads;
+        if (HS > 1 && (uint64_t)wgs * kFWaves >= 16ull * rows)
+            hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, HS>), dim3(f.p.kv_heads * HS, f.p.batch), dim3(256), 0,
+                               rl_stream(), f.p, ap, f.si);
+        else
+            hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, 1>), dim3(f.p.kv_heads, f.p.batch), dim3(256), 0,
+                               rl_stream(), f.p, ap, f.si);
+        return rl_check_launch("merge_pieces_kernel launch");
+    }
+}
+
+template <int D, int G>
+bool fits_dt(uint32_t dt, uint32_t tpb)
+{
+    return dt == RL_DTYPE_BF16 ? (tpb == 16 ? fits<D, G, 0, 16>() : fits<D, G, 0, 32>())
+                               : (tpb == 16 ? fits<D, G, 1, 16>() : fits<D, G, 1, 32>());
+}
+
+bool shape_fits(uint32_t D, uint32_t G, uint32_t dt, uint32_t tpb)
+{
+    if (D == 128) {
+        switch (G) {
+        case 1: return fits_dt<128, 1>(dt, tpb);
+        case 2: return fits_dt<128, 2>(dt, tpb);
+        case 4: return fits_dt<128, 4>(dt, tpb);
+        default: return fits_dt<128, 8>(dt, tpb);
+        }
+    }
+    switch (G) {
+    case 1: return fits_dt<64, 1>(dt, tpb);
+    case 2: return fits_dt<64, 2>(dt, tpb);
+    case 4: return fits_dt<64, 4>(dt, tpb);
+    default: return fits_dt<64, 8>(dt, tpb);
+    }
+}
+
+template <int D, int G>
+int launch_dt(const FusedParams &f, const AppendParams &ap, uint32_t wgs, uint32_t dt, uint32_t tpb)
+{
+    if (dt == RL_DTYPE_BF16)
+        return tpb == 16 ? launch_fused<D, G, 0, 16>(f, ap, wgs) : launch_fused<D, G, 0, 32>(f, ap, wgs);
+    return tpb == 16 ? launch_fused<D, G, 1, 16>(f, ap, wgs) : launch_fused<D, G, 1, 32>(f, ap, wgs);
+}
+
+template <int D>
+int launch_g(const FusedParams &f, const AppendParams &ap, uint32_t wgs, uint32_t G, uint32_t dt, uint32_t tpb)
+{
+    switch (G) {
+    case 1: return launch_dt<D, 1>(f, ap, wgs, dt, tpb);
+    case 2: return launch_dt<D, 2>(f, ap, wgs, dt, tpb);
+    case 4: return launch_dt<D, 4>(f, ap, wgs, dt, tpb);
+    default: return launch_dt<D, 8>(f, ap, wgs, dt, tpb);
+    }
+}
+
+// Workgroups of the fused grid (one per compute unit, a multiple of 8) and
+// of them the sampling ones: one per row up to 64, never more than half.
+void grid_of(uint32_t rows, uint32_t &wgs, uint32_t &sample_wgs)
+{
+    wgs = rl_cu_count() / kXcds * kXcds;
+    if (wgs < 2 * kXcds)
+        wgs = 2 * kXcds;
+    uint32_t s = (rows + kXcds - 1) / kXcds * kXcds;
+    if (s > 64)
+        s = 64;
+    if (s > wgs / 2)
+        s = wgs / 2 / kXcds * kXcds;
+    sample_wgs = s;
+}
+
+SplitIn split_in_of(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp)
+{
+    SplitIn si;
+    grid_of(samp->rows, si.wgs, si.sample_wgs);
+    si.tile_bytes = 2u * 16u * attn->layout.head_dim * 2u;
+    const uint32_t rows_per_wg = (samp->rows + si.sample_wgs - 1) / si.sample_wgs;
+    si.sample_bytes = (uint64_t)rows_per_wg * samp->vocab * 4u;
+    si.sample_cost = kSampleCost;
+    return si;
+}
+
+bool fused_eligible(const rl_attn_decode_args_t *a)
+{
+    const uint32_t G = a->q_heads / a->kv_heads;
+    return a->batch <= kFusedMaxBatch && shape_fits(a->layout.head_dim, G, a->dtype, a->layout.token_count);
+}
+
+int fused_validate(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                   const rl_sample_args_t *samp, const char *who)
+{
+    if (rl_require_open(who) || rl_decode_step_check(attn, append, who) || rl_sample_check(samp))
+        return -1;
+    return 0;
+}
+
+}  // namespace
+
+extern "C" size_t rl_hip_decode_sample_step_workspace(const rl_attn_decode_args_t *attn,
+                                                      const rl_sample_args_t *samp)
+{
+    if (rl_require_open("rl_hip_decode_sample_step_workspace") || rl_attn_check(attn) || rl_sample_check(samp))
+        return 0;
+    const size_t fused = fused_ws(attn, split_in_of(attn, samp)).total;
+    // the shapes outside the fused kernel run the two steps one after the other
+    const size_t a = rl_hip_attn_decode_workspace(attn);
+    const size_t s = rl_hip_sample_workspace(samp);
+    const size_t split = (a + 255) / 256 * 256 + s;
+    return fused_eligible(attn) ? fused : split;
+}
+
+extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                                         const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes)
+{
+    const char *who = "rl_hip_decode_sample_step";
+    if (fused_validate(attn, append, samp, who))
+        return -1;
+    const size_t need = rl_hip_decode_sample_step_workspace(attn, samp);
+    if (!workspace || workspace_bytes < need) {
+        rl_set_error("%s: workspace %zu bytes < %zu required", who, workspace_bytes, need);
+        return -1;
+    }
+    if (!fused_eligible(attn)) {
+        // one decode step, then the sampling, on the library stream
+        const size_t a_bytes = (rl_hip_attn_decode_workspace(attn) + 255) / 256 * 256;
+        rl_attn_decode_args_t a = *attn;
+        a.workspace = workspace;
+        a.workspace_bytes = a_bytes;
+        if (rl_hip_decode_step(&a, append))
+            return -1;
+        rl_sample_args_t s = *samp;
+        s.workspace = (uint8_t *)workspace + a_bytes;
+        s.workspace_bytes = workspace_bytes - a_bytes;
+        return rl_hip_sample(&s);
+    }
+    FusedParams f;
+    f.si = split_in_of(attn, samp);
+    const uint32_t wgs = f.si.wgs;
+    const FusedWs w = fused_ws(attn, f.si);
+    uint8_t *ws = (uint8_t *)workspace;
+    AttnParams &p = f.p;
+    p.arena = (const uint8_t *)attn->arena_base;
+    p.block_bytes = attn->layout.block_bytes;
+    p.arena_blocks = attn->arena_bytes / attn->layout.block_bytes;
+    p.table = attn->block_table;
+    p.table_stride = attn->table_stride;
+    p.row_map = nullptr;
+    p.ctx = attn->ctx_lens;
+    p.max_ctx = attn->max_ctx;
+    p.batch = attn->batch;
+    p.q_heads = attn->q_heads;
+    p.kv_heads = attn->kv_heads;
+    p.q = (const uint16_t *)attn->q;
+    p.out = (uint16_t *)attn->out;
+    p.out_f32 = attn->out_f32;
+    const float scale = attn->scale != 0.f ? attn->scale : 1.0f / sqrtf((float)attn->layout.head_dim);
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.nwaves = 0;  // the pieces replace the even split
+    p.cum = (uint32_t *)(ws + w.cum_off);
+    p.part = (float *)(ws + w.part_off);
+    f.sp = sample_params_of(samp);
+    const AppendParams ap = append_params(append);
+    const uint32_t G = attn->q_heads / attn->kv_heads;
+    if (attn->layout.head_dim == 128)
+        return launch_g<128>(f, ap, wgs, G, attn->dtype, attn->layout.token_count);
+    return launch_g<64>(f, ap, wgs, G, attn->dtype, attn->layout.token_count);
+}

@@ -519,6 +519,7 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         s.logits = a->logits + si * B * a->vocab;
         s.seed = p.rseed;
         s.steps = p.rstep;
+        s.draw_ids = p.rmap;  // the draw follows the rollout, not the row it was admitted into
         s.token_out = a->token_out + so * B;
         s.logprob_out = a->logprob_out + so * B;
         s.workspace = ws + w.samp;

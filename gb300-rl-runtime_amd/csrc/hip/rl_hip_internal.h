@@ -25,6 +25,12 @@ int rl_attn_scratch_setup(int device);
 int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                           const uint32_t *row_map);
 
+// Argument checks of the attention, the decode step and the sampler (0, or
+// -1 with the error set), for entry points that combine them.
+int rl_attn_check(const rl_attn_decode_args_t *a);
+int rl_decode_step_check(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append, const char *who);
+int rl_sample_check(const rl_sample_args_t *a);
+
 // Reports a launch error (or a fault of an earlier asynchronous call).
 static inline int rl_check_launch(const char *what)
 {

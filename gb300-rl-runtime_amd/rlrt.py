@@ -212,7 +212,7 @@ class SampleArgs(C.Structure):
                 ("top_p", C.c_void_p), ("seed", C.c_void_p), ("temperature_all", C.c_float),
                 ("top_k_all", C.c_uint32), ("top_p_all", C.c_float), ("seed_all", C.c_uint64),
                 ("step", C.c_uint64), ("steps", C.c_void_p), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
-                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+                ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("draw_ids", C.c_void_p)]
 
 
 class AppendArgs(C.Structure):
@@ -317,6 +317,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_kv_cow": (i32, [C.POINTER(CowArgs)]),
         "rl_hip_decode_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
         "rl_hip_decode_step_noalloc": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs)]),
+        "rl_hip_decode_sample_step_workspace": (C.c_size_t, [C.POINTER(AttnArgs), C.POINTER(SampleArgs)]),
+        "rl_hip_decode_sample_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs), C.POINTER(SampleArgs),
+                                             C.c_void_p, C.c_size_t]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
         "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
@@ -627,14 +630,16 @@ def attn_decode(args: AttnArgs) -> None:
 def sample_args(logits: DeviceBuffer, rows: int, vocab: int, row_stride: int, tokens: DeviceBuffer,
                 logprobs: DeviceBuffer, greedy: bool = False, temperature: float = 1.0, top_k: int = 0,
                 top_p: float = 1.0, seed: int = 0, step: int = 0,
-                seeds: DeviceBuffer | None = None) -> SampleArgs:
-    """Scalar parameters for every row; `seeds` (device u64[rows]) overrides `seed`."""
+                seeds: DeviceBuffer | None = None, draw_ids: DeviceBuffer | None = None) -> SampleArgs:
+    """Scalar parameters for every row; `seeds` (device u64[rows]) overrides `seed`,
+    `draw_ids` (device u32[rows]) replaces the row index in the Philox counter."""
     s = SampleArgs()
     s.logits, s.rows, s.vocab, s.row_stride, s.greedy = logits.ptr, rows, vocab, row_stride, int(greedy)
     s.temperature = s.top_k = s.top_p = None
     s.seed = seeds.ptr if seeds is not None else None
     s.temperature_all, s.top_k_all, s.top_p_all, s.seed_all, s.step = temperature, top_k, top_p, seed, step
     s.token_out, s.logprob_out = tokens.ptr, logprobs.ptr
+    s.draw_ids = draw_ids.ptr if draw_ids is not None else None
     return s
 
 
@@ -665,6 +670,21 @@ def decode_step(attn: AttnArgs, append: AppendArgs) -> None:
 
 
 DECODE_STEP_NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def decode_sample_step_workspace(attn: AttnArgs, samp: SampleArgs) -> DeviceBuffer:
+    """The workspace of rl_hip_decode_sample_step."""
+    n = lib().rl_hip_decode_sample_step_workspace(C.byref(attn), C.byref(samp))
+    if n == 0:
+        raise RlrtError(f"rl_hip_decode_sample_step_workspace: {_err()}")
+    return DeviceBuffer(n, zero=True)
+
+
+def decode_sample_step(attn: AttnArgs, append: AppendArgs, samp: SampleArgs, ws: DeviceBuffer) -> None:
+    """The decode step of one micro-batch (attention + KV append) and the
+    sampling of another micro-batch's logits in one launch (plus the merge)."""
+    check(lib().rl_hip_decode_sample_step(C.byref(attn), C.byref(append), C.byref(samp), ws.ptr, ws.nbytes),
+          "rl_hip_decode_sample_step")
 
 
 def decode_step_noalloc(attn: AttnArgs, append: AppendArgs) -> None:

@@ -297,7 +297,8 @@ int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
  *    kv_heads + h) with the K/V token appended at position seq_len
  *    (rl_hip_decode_step), and sampling (rl_hip_sample: greedy, or
  *    temperature / top_k / top_p with Philox key seeds[rollout] and counter
- *    seq_len);
+ *    (seq_len, rollout): the draw depends on the descriptor, never on the
+ *    batch row it was admitted into);
  *  - applies the rule for that token (seq_len++; DONE at max_tokens;
  *    NEEDS_REWARD at a multiple of 32; otherwise the row decodes again next
  *    step) and pushes finished descriptors to doneq in row order (bounded
@@ -444,6 +445,9 @@ typedef struct {
     float *logprob_out;          /* device [rows] */
     void *workspace;             /* device, >= rl_hip_sample_workspace() */
     size_t workspace_bytes;
+    const uint32_t *draw_ids;    /* device [rows] or NULL: row r's Philox counter is (step, draw_ids[r])
+                                    instead of (step, r), so a sampling stream (a rollout) draws the
+                                    same numbers whichever batch row it occupies */
 } rl_sample_args_t;
 
 size_t rl_hip_sample_workspace(const rl_sample_args_t *args);
@@ -534,6 +538,26 @@ int rl_hip_kv_cow(const rl_kv_cow_args_t *args);
  * append writes through append->block_table: at a copy-on-write step the
  * first still maps the shared source block, the second the private one. */
 int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append);
+
+/* ---- decode step of one micro-batch with the sampling of another ----------
+ * Replaces, for a rollout loop that keeps two micro-batches in flight, the
+ * per-descriptor decode (cu/worker.cu:25-64) of one micro-batch together with
+ * sample_token (cu/sample.cu:41-123) of the other, whose logits the previous
+ * step produced: rl_hip_decode_step(attn, append) and rl_hip_sample(samp) in
+ * one persistent launch that streams both from HBM side by side, plus the
+ * attention merge with the append. samp must not read what attn writes (its
+ * logits are the other micro-batch's). Tokens, logprobs and the appended
+ * KV equal the two calls'; the attention is the same fp32 online-softmax
+ * math with the rows split at other tile positions (fixed for a given set
+ * of contexts, so repeated calls give the same bits), within 1e-4 of fp64
+ * like rl_hip_attn_decode. The workspace (size from
+ * rl_hip_decode_sample_step_workspace) holds the step's tile prefix and
+ * partials; it needs no initialisation. Shapes whose tiles do not fit the
+ * fused kernel's LDS (or batches above 1,024) run rl_hip_decode_step and
+ * then rl_hip_sample on the same workspace, with exactly their results. */
+size_t rl_hip_decode_sample_step_workspace(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp);
+int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                              const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes);
 
 /* ---- fused decode step that allocates nothing ------------------------------
  * No counterpart in the reference. For callers that cannot allocate device

@@ -22,7 +22,9 @@
  *     prefix P whose weight sum reaches ceil(p * W_K) (computed in double),
  *     at least one element. Otherwise P = K.
  *  6. draw: (r0, r1, r2, r3) = Philox4x32-10(key = (seed lo, seed hi),
- *     ctr = (step lo, step hi, row, 0)); r64 = r0 | r1 << 32;
+ *     ctr = (step lo, step hi, id, 0)), id the row's draw id (the row
+ *     index unless the caller names the stream, e.g. by its rollout id);
+ *     r64 = r0 | r1 << 32;
  *     u = floor(r64 * W_P / 2^64). The token is the smallest index i in P
  *     whose ascending-index prefix weight sum exceeds u.
  *  7. logprob = x_tok - logsumexp(x) over the whole vocabulary (the

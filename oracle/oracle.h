@@ -147,6 +147,10 @@ uint32_t orc_sample_row(const float *logits, uint32_t vocab, int greedy, float t
 void orc_sample_rows(const float *logits, uint32_t rows, uint32_t vocab, uint32_t stride, int greedy,
                      float temperature, uint32_t top_k, float top_p, const uint64_t *seeds, uint64_t step,
                      uint32_t *tokens, double *logprobs);
+void orc_sample_rows_v(const float *logits, uint32_t rows, uint32_t vocab, uint32_t stride, const float *temperature,
+                       const uint32_t *top_k, const float *top_p, const uint64_t *seeds, const uint64_t *steps,
+                       const uint32_t *draw_ids, float temperature_all, uint32_t top_k_all, float top_p_all,
+                       uint64_t step_all, uint32_t *tokens, double *logprobs);
 
 /* ---- KV append with copy-on-write (see rl_hip_kv_append) ---- */
 void orc_kv_append(uint8_t *arena, uint64_t block_bytes, uint32_t token_count, uint32_t row_bytes,

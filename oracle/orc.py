@@ -76,6 +76,8 @@ def load_oracle() -> C.CDLL:
         "orc_attn_decode_f32": (None, [C.POINTER(OrcAttn), vp]),
         "orc_sample_row": (u32, [vp, u32, i32, C.c_float, u32, C.c_float, u64, u64, u32, C.POINTER(C.c_double)]),
         "orc_sample_rows": (None, [vp, u32, u32, u32, i32, C.c_float, u32, C.c_float, vp, u64, vp, vp]),
+        "orc_sample_rows_v": (None, [vp, u32, u32, u32, vp, vp, vp, vp, vp, vp, C.c_float, u32, C.c_float, u64, vp,
+                                     vp]),
         "orc_kv_append": (None, [vp, u64, u32, u32, vp, u32, u32, u32, vp, vp, vp, vp]),
         "orc_num_threads": (i32, []), "orc_set_num_threads": (None, [i32]),
         "orc_plumbing_run": (i32, [C.POINTER(OrcPlumbing), u32, u32, C.POINTER(C.c_double), vp]),
@@ -130,4 +132,23 @@ def sample_rows(o: C.CDLL, logits: np.ndarray, greedy: bool, temperature: float,
     lp = np.zeros(rows, dtype=np.float64)
     o.orc_sample_rows(_p(logits), rows, vocab, stride, int(greedy), temperature, top_k, top_p, _p(seeds), step,
                       _p(tok), _p(lp))
+    return tok, lp
+
+
+def sample_rows_v(o: C.CDLL, logits: np.ndarray, temperature=None, top_k=None, top_p=None, seeds=None, steps=None,
+                  draw_ids=None, temperature_all: float = 1.0, top_k_all: int = 0, top_p_all: float = 1.0,
+                  step_all: int = 0):
+    """Per-row parameters (arrays of `rows` entries, or None for the scalar)."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, stride = logits.shape
+
+    def arr(a, dt):
+        return None if a is None else np.ascontiguousarray(a, dtype=dt)
+    t, k, p = arr(temperature, np.float32), arr(top_k, np.uint32), arr(top_p, np.float32)
+    s, st, di = arr(seeds, np.uint64), arr(steps, np.uint64), arr(draw_ids, np.uint32)
+    tok = np.zeros(rows, dtype=np.uint32)
+    lp = np.zeros(rows, dtype=np.float64)
+    ptr = lambda a: None if a is None else _p(a)  # noqa: E731
+    o.orc_sample_rows_v(_p(logits), rows, stride, stride, ptr(t), ptr(k), ptr(p), ptr(s), ptr(st), ptr(di),
+                        temperature_all, top_k_all, top_p_all, step_all, _p(tok), _p(lp))
     return tok, lp

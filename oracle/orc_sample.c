@@ -189,3 +189,21 @@ orc_sample_rows(const float *logits, uint32_t rows, uint32_t vocab, uint32_t str
         tokens[r] = orc_sample_row(logits + (size_t)r * stride, vocab, greedy, temperature, top_k, top_p, seeds[r],
                                    step, r, &logprobs[r]);
 }
+
+/* orc_sample_rows with per-row parameters (any of the arrays may be NULL: the
+ * scalar then serves every row) and per-row draw ids (NULL: the row index),
+ * OpenMP over rows. */
+void
+orc_sample_rows_v(const float *logits, uint32_t rows, uint32_t vocab, uint32_t stride, const float *temperature,
+                  const uint32_t *top_k, const float *top_p, const uint64_t *seeds, const uint64_t *steps,
+                  const uint32_t *draw_ids, float temperature_all, uint32_t top_k_all, float top_p_all,
+                  uint64_t step_all, uint32_t *tokens, double *logprobs)
+{
+#pragma omp parallel for schedule(dynamic)
+    for (uint32_t r = 0; r < rows; r++) {
+        const float t = temperature ? temperature[r] : temperature_all;
+        tokens[r] = orc_sample_row(logits + (size_t)r * stride, vocab, !(t > 0.f), t, top_k ? top_k[r] : top_k_all,
+                                   top_p ? top_p[r] : top_p_all, seeds ? seeds[r] : 0u, steps ? steps[r] : step_all,
+                                   draw_ids ? draw_ids[r] : r, &logprobs[r]);
+    }
+}

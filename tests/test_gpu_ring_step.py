@@ -112,7 +112,7 @@ def test_ring_step_batch64(rl, gpu, orc, olib):
     lp = C.c_double()
     for i in range(B):
         r = int(perm[i])
-        want = olib.orc_sample_row(logits[i].ctypes.data, V, 0, 0.8, 50, 0.9, int(seeds[r]), int(w.ctx[r]), i,
+        want = olib.orc_sample_row(logits[i].ctypes.data, V, 0, 0.8, 50, 0.9, int(seeds[r]), int(w.ctx[r]), r,
                                    C.byref(lp))
         assert o["tok"][i] == want, (i, o["tok"][i], want)
         assert abs(o["lp"][i] - lp.value) < 1e-4, i
@@ -183,7 +183,7 @@ def test_ring_step_control_rule_over_steps(rl, gpu, orc, olib):
         gh.check_attn(o["out"][rows], o["out32"][rows], orc.attn_f64(olib, wb, 0), "bf16")
         for j, i in enumerate(rows):
             want = olib.orc_sample_row(logits[s][i].ctypes.data, V, 0, 1.0, 20, 0.8, int(seeds[rs[j]]), int(ctx[j]),
-                                       i, C.byref(lp))
+                                       rs[j], C.byref(lp))
             assert o["tok"][i] == want, (s, i)
             assert abs(o["lp"][i] - lp.value) < 1e-4, (s, i)
         k_rows, v_rows = np.ascontiguousarray(kn[s][rows]), np.ascontiguousarray(vn[s][rows])  # alive across the call
@@ -198,3 +198,45 @@ def test_ring_step_control_rule_over_steps(rl, gpu, orc, olib):
     assert np.array_equal(arena.download(np.uint8, arena.nbytes), host)
     run.close()
     arena.close()
+
+
+def test_ring_step_draw_follows_rollout(rl, gpu, orc, olib):
+    """The Philox counter of a decoded token is (seq_len, rollout): the same
+    descriptors submitted in two different orders land in different batch
+    rows, and every rollout still draws the same token. All rows see the same
+    logits, so only the draw could tell the rows apart."""
+    import ringstep
+
+    B, V = 16, 4096
+    rng = np.random.default_rng(7170)
+    w = synth.make_decode(7171, B, QH, KVH, D, 40, 300)
+    seeds = rng.integers(0, 2**63, B, dtype=np.uint64)
+    q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    logits = np.repeat(rng.standard_normal((1, V), dtype=np.float32) * np.float32(0.5), B, axis=0)
+    tok_of = []
+    for order in (np.arange(B), rng.permutation(B)):
+        arena = rl.DeviceBuffer.from_array(w.arena)
+        run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
+                                   output_slots=2, temperature=1.0, top_k=200, top_p=0.95, seeds=seeds)
+        run.set_inputs(0, q, kn, vn, logits)
+        for r in order:
+            run.submit_decode(int(r), int(w.ctx[r]), int(w.ctx[r]) + 1)
+        run.push(rl.HwDesc(opcode=255))
+        print(f"[ring] one step, rollouts admitted in order {order.tolist()}", flush=True)
+        run.enqueue(2)
+        rl.sync()
+        o = run.outputs(0)
+        assert np.array_equal(o["rows"], order.astype(np.uint32))
+        t = np.zeros(B, dtype=np.uint32)
+        t[o["rows"]] = o["tok"]
+        tok_of.append(t)
+        run.close()
+        arena.close()
+    assert np.array_equal(tok_of[0], tok_of[1])
+    lp = C.c_double()
+    want = [olib.orc_sample_row(logits[0].ctypes.data, V, 0, 1.0, 200, 0.95, int(seeds[r]), int(w.ctx[r]), r,
+                                C.byref(lp)) for r in range(B)]
+    assert tok_of[0].tolist() == want
+    assert len(set(want)) > 1  # the rollouts' draws differ, so a row-keyed draw would show

@@ -16,12 +16,14 @@ Checked:
     advantage equals the host reward_group_advantage bit for bit;
   * scheduler state, counters and ring indices at the end (all slots free,
     513 requests consumed with the end marker, 512 dones);
-  * at three checkpoint steps: every row's token equals the host sampler's on
-    the device logits (the "given identical logits" contract), attention rows
-    within 1e-4 of fp64 over the arena as it stands, and projection rows within
-    the fp32 summation bound of an fp64 GEMM;
-  * at every step that admitted requests: every row's token against the host
-    sampler on the device logits;
+  * at every step (every 8th step, and every step that admitted requests, in
+    the pipeline-fed and copy-on-write variants): every row's token and
+    logprob against the host sampler on the device logits (the "given
+    identical logits" contract), so the rewards below, computed from the
+    device's generated tokens, rest on checked tokens;
+  * at three checkpoint steps: 16 attention rows within 1e-4 of fp64 over the
+    arena as it stands, and 16 projection rows within the fp32 summation bound
+    of an fp64 GEMM;
   * the whole arena at the end byte-equal to the oracle's appends replayed
     step by step (each step's append positions, the request each slot held,
     and that step's K/V pool rows), copy-on-write included;
@@ -42,30 +44,31 @@ pytestmark = pytest.mark.gpu
 CHECK_STEPS = (0, 137, 306)
 
 
-def _check_tokens(olib, dev, t):
-    """Every row's token of step t against the host sampler on the device logits."""
+def _check_tokens(orc, olib, dev, t):
+    """Every row's token and logprob of step t against the host sampler on the
+    device logits (per-row temperature, top-k, top-p, seed and step)."""
     logits = dev["logits"].download(np.float32, (SLOTS, VOCAB))
     tok = dev["tok"].download(np.uint32, SLOTS)
-    temp = dev["temp"].download(np.float32, SLOTS)
-    topk = dev["topk"].download(np.uint32, SLOTS)
-    topp = dev["topp"].download(np.float32, SLOTS)
-    seed = dev["seed"].download(np.uint64, SLOTS)
-    step = dev["step"].download(np.uint64, SLOTS)
-    lp = C.c_double()
-    for r in range(SLOTS):
-        want = olib.orc_sample_row(logits[r].ctypes.data, VOCAB, int(not temp[r] > 0), float(temp[r]), int(topk[r]),
-                                   float(topp[r]), int(seed[r]), int(step[r]), r, C.byref(lp))
-        assert tok[r] == want, (t, r, tok[r], want)
+    glp = dev["lp"].download(np.float32, SLOTS)
+    want, wlp = orc.sample_rows_v(olib, logits, temperature=dev["temp"].download(np.float32, SLOTS),
+                                  top_k=dev["topk"].download(np.uint32, SLOTS),
+                                  top_p=dev["topp"].download(np.float32, SLOTS),
+                                  seeds=dev["seed"].download(np.uint64, SLOTS),
+                                  steps=dev["step"].download(np.uint64, SLOTS))
+    bad = np.nonzero(tok != want)[0]
+    assert len(bad) == 0, (t, bad[:8], tok[bad[:8]], want[bad[:8]])
+    assert np.abs(glp - wlp).max() < 1e-4, t
 
 
 class _Recorder:
     """on_check hook of RolloutLoop.run: after every step, the append positions
-    and the slot -> request map that step used; tokens checked at every step
-    that admitted requests, and the full check at `full_steps`."""
+    and the slot -> request map that step used; tokens checked at every
+    `every`-th step and every step that admitted requests, and the full check
+    at `full_steps`."""
 
-    def __init__(self, rl, orc, olib, cfg, loop, full_steps, pick=None):
+    def __init__(self, rl, orc, olib, cfg, loop, full_steps, pick=None, every=8):
         self.rl, self.orc, self.olib, self.cfg, self.loop = rl, orc, olib, cfg, loop
-        self.full_steps, self.pick = full_steps, pick
+        self.full_steps, self.pick, self.every = full_steps, pick, every
         self.records, self.admitted, self.token_checks = [], 0, []
 
     def __call__(self, t):
@@ -73,11 +76,11 @@ class _Recorder:
         pos, sreq = dev["pos"].download(np.uint32, SLOTS), dev["sreq"].download(np.uint32, SLOTS)
         self.records.append((t, pos, sreq))
         adm = int(dev["counters"].download(np.uint32, 4)[1])
+        if t in self.full_steps or adm != self.admitted or t % self.every == 0:
+            _check_tokens(self.orc, self.olib, dev, t)
+            self.token_checks.append(t)
         if t in self.full_steps:
             _check_step(self.rl, self.orc, self.olib, self.cfg, dev, t, self.pick(sreq) if self.pick else None)
-        elif adm != self.admitted:
-            _check_tokens(self.olib, dev, t)
-            self.token_checks.append(t)
         self.admitted = adm
 
 
@@ -110,43 +113,32 @@ def _replay_arena(olib, cfg, loop, records):
 
 
 def _check_step(rl, orc, olib, cfg, dev, t, pick=None):
-    """Tokens, attention and projection of step t against the host."""
+    """Attention and projection of step t against the host (tokens: _check_tokens)."""
     logits = dev["logits"].download(np.float32, (SLOTS, VOCAB))
-    tok = dev["tok"].download(np.uint32, SLOTS)
-    temp = dev["temp"].download(np.float32, SLOTS)
-    topk = dev["topk"].download(np.uint32, SLOTS)
-    topp = dev["topp"].download(np.float32, SLOTS)
-    seed = dev["seed"].download(np.uint64, SLOTS)
-    step = dev["step"].download(np.uint64, SLOTS)
     ctx = dev["ctx"].download(np.uint32, SLOTS)
-    lp = C.c_double()
     active = np.nonzero(ctx)[0]
     assert len(active) > 0
-    for r in range(SLOTS):
-        greedy = int(not temp[r] > 0)
-        want = olib.orc_sample_row(logits[r].ctypes.data, VOCAB, greedy, float(temp[r]), int(topk[r]),
-                                   float(topp[r]), int(seed[r]), int(step[r]), r, C.byref(lp))
-        assert tok[r] == want, (t, r, tok[r], want)
-    # attention of two active slots over the arena as the step saw it
+    # attention of 16 active slots (spread over the batch) over the arena as the step saw it
     out32 = dev["out32"].download(np.float32, (SLOTS, QH, D))
     arena = dev["arena"].download(np.uint8, cfg["arena"].size)
     stab = dev["stab"].download(np.uint32, (SLOTS, KVH, cfg["stride"]))
-    if pick is None:
-        pick = active[[0, len(active) // 2]]
+    if pick is None or len(pick) == 0:
+        pick = active[np.unique(np.linspace(0, len(active) - 1, 16).astype(np.int64))]
     wl = synth.DecodeWorkload(len(pick), QH, KVH, D, "bf16", TPB, ctx[pick].copy(), stab[pick].copy(), arena,
                               cfg["qpool"][t % POOL][pick].copy(), 0)
     ref = orc.attn_f64(olib, wl, 0)
     err = (np.abs(out32[pick] - ref).max(axis=-1) / np.abs(ref).max(axis=-1)).max()
     assert err < 1e-4, (t, err)
-    # projection of four rows
+    # projection of 16 rows
     x = dev["out"].download(np.uint16, (SLOTS, HID))
-    rows = active[:4]
+    rows = active[np.unique(np.linspace(0, len(active) - 1, 16).astype(np.int64))]
     xf = synth.bf16_to_f32(x[rows]).astype(np.float64)
     wf = synth.bf16_to_f32(cfg["w"]).astype(np.float64)
     ref = xf @ wf.T
     bound = 2.0 * (HID - 1) * 2.0**-24 * (np.abs(xf) @ np.abs(wf).T)
     assert np.all(np.abs(logits[rows] - ref) <= bound + 1e-30), t
-    print(f"[rollout] step {t}: {len(active)} active slots, tokens and attention ({err:.1e}) match", flush=True)
+    print(f"[rollout] step {t}: {len(active)} active slots, attention of {len(pick)} rows ({err:.1e}) and "
+          f"projection of {len(rows)} rows match", flush=True)
 
 
 def test_grpo_rollout_loop(rl, gpu, orc, olib):
@@ -165,10 +157,11 @@ def test_grpo_rollout_loop(rl, gpu, orc, olib):
     assert L.rl_hip_is_coherent_host(loop.rr) and L.rl_hip_is_coherent_host(loop.dr)
     loop.submit_requests()
     print("[rollout] running the loop", flush=True)
-    rec = _Recorder(rl, orc, olib, cfg, loop, CHECK_STEPS)
+    rec = _Recorder(rl, orc, olib, cfg, loop, CHECK_STEPS, every=1)
     res = loop.run(check_steps=range(10**6), on_check=rec)
     dones = loop.dones
-    print(f"[rollout] tokens checked at admission steps {rec.token_checks}", flush=True)
+    assert rec.token_checks == list(range(res["steps"]))
+    print(f"[rollout] tokens and logprobs checked at all {len(rec.token_checks)} steps", flush=True)
     want, cows = _replay_arena(olib, cfg, loop, rec.records)
     assert cows == 0                                      # a 512-token prefix fills whole blocks
     assert np.array_equal(dev["arena"].download(np.uint8, cfg["arena"].size), want)
@@ -237,8 +230,8 @@ def test_grpo_loop_fed_by_the_rollout_pipeline(rl, gpu, orc, olib):
     print("[rollout] running the pipeline-fed loop", flush=True)
     rec = _Recorder(rl, orc, olib, cfg, loop, (0, 300))
     res = loop.run(check_steps=range(10**6), on_check=rec)
-    print(f"[rollout] pipeline-fed: {res['steps']} steps in {res['wall_s']:.2f} s; tokens checked at admission "
-          f"steps {rec.token_checks}", flush=True)
+    print(f"[rollout] pipeline-fed: {res['steps']} steps in {res['wall_s']:.2f} s; tokens checked at "
+          f"{len(rec.token_checks)} steps", flush=True)
     want, _ = _replay_arena(olib, cfg, loop, rec.records)
     assert np.array_equal(dev["arena"].download(np.uint8, cfg["arena"].size), want)
     assert (f.stats.admitted, f.stats.sent, f.stats.retired, f.stats.reward_handoffs) == (REQ,) * 4
@@ -269,9 +262,10 @@ def test_grpo_loop_copy_on_write_prefix(rl, gpu, orc, olib):
     before its first step rl_hip_kv_cow resolves the slot's branch on the
     device prefix table and copies the 8 prefix slots into the request's
     private block, which the step's attention then reads. Checked: 256
-    copy-on-writes happen, the attention at step 0 of two such slots is within
-    1e-4 of fp64 over the copied block, every token at admission steps, every
-    request done once with the reference reward rule, and the final arena
+    copy-on-writes happen, the attention at step 0 of 16 such slots is within
+    1e-4 of fp64 over the copied block, every token at admission steps and
+    every 8th step, every request done once with the reference reward rule,
+    and the final arena
     byte-equal to the oracle's replay of every step's copy-on-write and append."""
     L = rl.lib()
     cfg = grpo.build_workload(406, prefix=520, priv_zero_every=2)
@@ -280,12 +274,11 @@ def test_grpo_loop_copy_on_write_prefix(rl, gpu, orc, olib):
     assert loop.cow is not None
     loop.submit_requests()
     zero = set(int(r) for r in np.nonzero(cfg["priv"] == 0)[0])
-    pick = lambda sreq: np.array([s for s in range(SLOTS) if int(sreq[s]) in zero][:2])
+    pick = lambda sreq: np.array([s for s in range(SLOTS) if int(sreq[s]) in zero][:16])
     rec = _Recorder(rl, orc, olib, cfg, loop, (0, 291), pick=pick)
     print("[rollout] running the copy-on-write loop (prefix 520)", flush=True)
     res = loop.run(check_steps=range(10**6), on_check=rec)
-    print(f"[rollout] cow loop: {res['steps']} steps; tokens checked at admission steps {rec.token_checks}",
-          flush=True)
+    print(f"[rollout] cow loop: {res['steps']} steps; tokens checked at {len(rec.token_checks)} steps", flush=True)
     assert dev["counters"].download(np.uint32, 4).tolist() == [REQ, REQ, 1, 0]
     dones = loop.dones
     assert sorted(d[0] for d in dones) == list(range(REQ)) and all(d[2] == GEN and d[4] == 0 for d in dones)

@@ -208,30 +208,36 @@ def test_worker_exits_on_idle_limit(rl, gpu):
     L.rl_hip_host_free(stop)
 
 
-def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
+def _pairs_run(rl, gpu, orc, olib, *, seed, S, q_heads, kv_heads, head_dim, dtype, tc, ctx_lo, ctx_hi, kv_std,
+               vocab=VOCAB):
     """One persistent worker per compute unit (256 on MI355X), each the single
-    consumer / producer of its own ring pair and its own rollout (MHA 8 x d64
-    fp16, KV length 256 at the start): 8 decode steps per pair through
-    infer_submit_decode, submitted while the workers poll. Per pair: the
-    completions and ring indices byte-identical to hw_worker_sim_run fed the
-    same submissions, and the counters; over all pairs: tokens bit-exact,
-    logprobs within 1e-4, every step's attention within 1e-4 of fp64 over the
-    arena as the earlier appends left it, and the final arena byte-identical
-    to the host appends."""
+    consumer / producer of its own ring pair and its own rollout, rollout g
+    starting at KV length ctx_g ~ U[ctx_lo, ctx_hi]: S decode steps per pair
+    through infer_submit_decode (seq_len ctx_g + i, max_tokens ctx_g + i + 1),
+    submitted while the workers poll. Per pair: the completions and ring
+    indices byte-identical to hw_worker_sim_run fed the same submissions, and
+    the counters; over all pairs: tokens bit-exact, logprobs within 1e-4,
+    every step's attention within 1e-4 of fp64 over the arena as the earlier
+    appends left it, and the final arena byte-identical to the host appends."""
     L = rl.lib()
     G = int(gpu.cu_count)
-    S = 8
-    rng = np.random.default_rng(1003)
-    w = synth.make_decode(1002, G, 8, 8, 64, CTX0, CTX0, dtype="fp16", kv_std=0.5, reserve_tokens=CTX0 + S + 1)
+    code = rl.DTYPE_BF16 if dtype == "bf16" else rl.DTYPE_FP16
+    rng = np.random.default_rng(seed + 1)
+    ctx0 = np.random.default_rng(seed + 2).integers(ctx_lo, ctx_hi + 1, size=G).astype(np.uint32)
+    # every row owns blocks for ctx0 + S + 1 tokens: the S appended slots are in its table
+    w = synth.make_decode(seed, G, q_heads, kv_heads, head_dim, 0, 0, dtype=dtype, kv_std=kv_std, token_count=tc,
+                          ctx=ctx0 + S)
     host_arena0 = w.arena.copy()
-    q_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32))
-    k_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32) * np.float32(0.5))
-    v_all = synth.f32_to_f16(rng.standard_normal((G, S, 8, 64), dtype=np.float32) * np.float32(0.5))
-    logits = rng.standard_normal((G, S, VOCAB), dtype=np.float32) * np.float32(2.0)
-    layout = rl.KvLayoutDesc.paged(16, 64)
+    q_all = synth.to_scalar16(rng.standard_normal((G, S, q_heads, head_dim), dtype=np.float32), dtype)
+    k_all = synth.to_scalar16(rng.standard_normal((G, S, kv_heads, head_dim), dtype=np.float32)
+                              * np.float32(kv_std), dtype)
+    v_all = synth.to_scalar16(rng.standard_normal((G, S, kv_heads, head_dim), dtype=np.float32)
+                              * np.float32(kv_std), dtype)
+    logits = rng.standard_normal((G, S, vocab), dtype=np.float32) * np.float32(2.0)
+    layout = rl.KvLayoutDesc.paged(tc, head_dim)
     bufs = {n: rl.DeviceBuffer.from_array(a) for n, a in
             (("arena", w.arena), ("table", w.table), ("q", q_all), ("k", k_all), ("v", v_all), ("logits", logits))}
-    attn_out = rl.DeviceBuffer(G * S * 8 * 64 * 4, zero=True)
+    attn_out = rl.DeviceBuffer(G * S * q_heads * head_dim * 4, zero=True)
     tok = rl.DeviceBuffer(G * S * 4, zero=True)
     lp = rl.DeviceBuffer(G * S * 4, zero=True)
     stats = rl.DeviceBuffer(G * 4 * 8, zero=True)
@@ -246,22 +252,26 @@ def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
     doorbells = _alloc_coherent(rl, 64 * G)
     a = rl.HwWorkerArgs(cmdq=rings, doneq=rings + 8 * G, groups=G, stop=stop, max_idle_polls=1 << 22,
                         arena_base=bufs["arena"].ptr, arena_bytes=bufs["arena"].nbytes, layout=layout,
-                        block_table=bufs["table"].ptr, table_stride=w.table_stride, rollouts=G, q_heads=8,
-                        kv_heads=8, dtype=rl.DTYPE_FP16, scale=0.0, max_steps=S, q=bufs["q"].ptr,
-                        k_new=bufs["k"].ptr, v_new=bufs["v"].ptr, logits=bufs["logits"].ptr, vocab=VOCAB,
+                        block_table=bufs["table"].ptr, table_stride=w.table_stride, rollouts=G, q_heads=q_heads,
+                        kv_heads=kv_heads, dtype=code, scale=0.0, max_steps=S, q=bufs["q"].ptr,
+                        k_new=bufs["k"].ptr, v_new=bufs["v"].ptr, logits=bufs["logits"].ptr, vocab=vocab,
                         attn_out=attn_out.ptr, token_out=tok.ptr, logprob_out=lp.ptr, stats=stats.ptr)
     ws = rl.hw_worker_workspace(a)
     ctxs = [rl.InferHwCtx(cmdq=cqs[g], doneq=dqs[g], doorbell=doorbells + 64 * g, gpu_group_id=g, kv_arena_id=42)
             for g in range(G)]
+
+    def submit(c, g, i):
+        return L.infer_submit_decode(C.byref(c), g, 0x1000 * i, 0x40 * i, 0, int(ctx0[g]) + i, int(ctx0[g]) + i + 1)
+
     got = [[] for _ in range(G)]
-    print(f"[worker] launching {G} persistent workers, one per compute unit", flush=True)
+    print(f"[worker] launching {G} persistent workers, one per compute unit: {q_heads}/{kv_heads} heads, "
+          f"d{head_dim} {dtype}, {tc}-token blocks, ctx U[{ctx_lo}, {ctx_hi}], {S} steps each", flush=True)
     rl.hw_worker_launch(a)
     try:
         t0 = time.perf_counter()
         for i in range(S):
             for g in range(G):
-                assert L.infer_submit_decode(C.byref(ctxs[g]), g, 0x1000 * i, 0x40 * i, 0, CTX0 + i,
-                                             CTX0 + i + 1) == 0
+                assert submit(ctxs[g], g, i) == 0
         deadline = time.perf_counter() + 60.0
         n = 0
         while n < G * S and time.perf_counter() < deadline:
@@ -287,7 +297,7 @@ def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
         try:
             c2 = rl.InferHwCtx(cmdq=cq2, doneq=dqs[g], doorbell=doorbells + 64 * g, gpu_group_id=g, kv_arena_id=42)
             for i in range(S):
-                assert L.infer_submit_decode(C.byref(c2), g, 0x1000 * i, 0x40 * i, 0, CTX0 + i, CTX0 + i + 1) == 0
+                assert submit(c2, g, i) == 0
                 sub.append(rl.hw_ring_pop(cq2))
         finally:
             L.hw_ring_destroy(cq2)
@@ -299,22 +309,22 @@ def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
 
     gt = tok.download(np.uint32, (G, S))
     glp = lp.download(np.float32, (G, S))
-    ot, olp = orc.sample_rows(olib, logits.reshape(G * S, VOCAB), True, 1.0, 0, 1.0, 0, 0)
+    ot, olp = orc.sample_rows(olib, logits.reshape(G * S, vocab), True, 1.0, 0, 1.0, 0, 0)
     assert np.array_equal(gt.ravel(), ot)
     assert np.abs(glp.ravel() - olp).max() < 1e-4
 
-    gout = attn_out.download(np.float32, (G, S, 8, 64))
+    gout = attn_out.download(np.float32, (G, S, q_heads, head_dim))
     w.arena[:] = host_arena0
     worst = 0.0
-    tc, rb = w.token_count, 2 * 64
+    rb = 2 * head_dim
     for i in range(S):
-        w.ctx = np.full(G, CTX0 + i, dtype=np.uint32)
+        w.ctx = ctx0 + np.uint32(i)
         w.q = np.ascontiguousarray(q_all[:, i])
-        ref = orc.attn_f64(olib, w, 1)
+        ref = orc.attn_f64(olib, w, code)
         worst = max(worst, float((np.abs(gout[:, i] - ref).max(axis=-1) / np.abs(ref).max(axis=-1)).max()))
-        pos = CTX0 + i
         for g in range(G):
-            for h in range(8):
+            pos = int(ctx0[g]) + i
+            for h in range(kv_heads):
                 blk = int(w.table[g, h, pos // tc])
                 base = blk * w.block_bytes + (pos % tc) * rb
                 w.arena[base:base + rb] = k_all[g, i, h].view(np.uint8)
@@ -328,3 +338,25 @@ def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
         L.hw_ring_destroy(q)
     for p in (rings, stop, doorbells):
         L.rl_hip_host_free(p)
+
+
+def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
+    """The plumbing rollout shape (MHA 8 x d64 fp16, KV length 256) on one
+    worker per compute unit, 8 steps per pair."""
+    _pairs_run(rl, gpu, orc, olib, seed=1002, S=8, q_heads=8, kv_heads=8, head_dim=64, dtype="fp16", tc=16,
+               ctx_lo=CTX0, ctx_hi=CTX0, kv_std=0.5)
+
+
+# The worker's other instantiations at one worker per compute unit:
+#  - the batched-decode rollout shape: GQA 32/8 (group 4), d128 bf16, ctx U[512, 4096], 16-token blocks;
+#  - group 8 at d128 (GQA 64/8, the long-context head shape): four waves with up to four tile stages;
+#  - 32-token blocks (GQA 16/8 d64 fp16, group 2) and a d128 fp16 MHA case.
+@pytest.mark.parametrize("shape", [
+    dict(seed=2101, S=4, q_heads=32, kv_heads=8, head_dim=128, dtype="bf16", tc=16, ctx_lo=512, ctx_hi=4096, kv_std=1.0),
+    dict(seed=2102, S=4, q_heads=64, kv_heads=8, head_dim=128, dtype="bf16", tc=16, ctx_lo=512, ctx_hi=2048,
+         kv_std=1.0),
+    dict(seed=2103, S=6, q_heads=16, kv_heads=8, head_dim=64, dtype="fp16", tc=32, ctx_lo=100, ctx_hi=900, kv_std=0.5),
+    dict(seed=2104, S=4, q_heads=8, kv_heads=8, head_dim=128, dtype="fp16", tc=32, ctx_lo=31, ctx_hi=700, kv_std=0.5),
+], ids=["gqa4_d128_bf16_tc16", "gqa8_d128_bf16_tc16", "gqa2_d64_fp16_tc32", "mha_d128_fp16_tc32"])
+def test_worker_shapes_one_per_cu(rl, gpu, orc, olib, shape):
+    _pairs_run(rl, gpu, orc, olib, **shape)

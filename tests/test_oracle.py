@@ -466,3 +466,30 @@ def test_decode_workload_spare_blocks_owned_by_no_row():
         assert len(np.unique(owned)) == len(owned)
         assert owned.max() < total - spare
         assert total - spare == len(owned)
+
+
+def test_sample_rows_v_matches_per_row_calls(olib):
+    """orc_sample_rows_v (per-row parameters, OpenMP over rows) returns what
+    orc_sample_row returns row by row with the same parameters, draw ids
+    included."""
+    import orc
+    rng = np.random.default_rng(91)
+    rows, V = 24, 3000
+    x = rng.standard_normal((rows, V), dtype=np.float32)
+    temp = np.where(rng.random(rows) < 0.25, 0.0, rng.uniform(0.5, 1.5, rows)).astype(np.float32)
+    topk = rng.choice([0, 5, 50, 300], rows).astype(np.uint32)
+    topp = rng.choice([1.0, 0.9, 0.5], rows).astype(np.float32)
+    seeds = rng.integers(0, 2**63, rows, dtype=np.uint64)
+    steps = rng.integers(0, 1000, rows, dtype=np.uint64)
+    ids = rng.integers(0, 1 << 20, rows).astype(np.uint32)
+    tok, lp = orc.sample_rows_v(olib, x, temperature=temp, top_k=topk, top_p=topp, seeds=seeds, steps=steps,
+                                draw_ids=ids)
+    one = C.c_double()
+    for r in range(rows):
+        want = olib.orc_sample_row(x[r].ctypes.data, V, int(not temp[r] > 0), float(temp[r]), int(topk[r]),
+                                   float(topp[r]), int(seeds[r]), int(steps[r]), int(ids[r]), C.byref(one))
+        assert tok[r] == want and lp[r] == one.value, r
+    # scalar parameters and the row index as the draw id
+    tok2, _ = orc.sample_rows_v(olib, x, seeds=seeds, temperature_all=1.0, top_k_all=50, top_p_all=0.9, step_all=7)
+    want2, _ = orc.sample_rows(olib, x, False, 1.0, 50, 0.9, seeds, 7)
+    assert np.array_equal(tok2, want2)
