@@ -719,6 +719,95 @@ __device__ __forceinline__ void merge_span(const AttnParams &p, uint32_t b, uint
     }
 }
 
+// merge_span of one whole row (all G heads) by one wave, with the arithmetic
+// of merge_span's register path in the same order: M = max_w m_w per head,
+// then L = sum l_w f_w and O = sum o_w f_w over w ascending (fmaf), f_w =
+// 2^(m_w - M), out = O / L. Lane j < np first loads partial j's (m, l) of
+// every head, which gives M by a wave reduction and each f_w by readlane;
+// lane l owns output elements l + 64 k. The O loads of up to 8 partials are
+// in flight together with the (m, l) loads. Rows of up to 64 partials.
+template <int D, int G, int DT>
+__device__ __forceinline__ void merge_row_wave(const AttnParams &p, uint32_t b, uint32_t g, uint32_t wf, uint32_t wl,
+                                               bool bad, int lane)
+{
+    constexpr int PART = G * D + 2 * G;
+    constexpr int EPL = G * D / 64;  // output elements per lane
+    constexpr int CH = 8;            // partials per round of O loads
+    static_assert(G * D % 64 == 0, "lane mapping");
+    if (wf == wl)
+        return;
+    const uint32_t row = b * p.kv_heads + g;
+    const uint32_t np = wl - wf + 1;
+    const float *part = p.part + (size_t)(wf + row) * PART;
+    // lane j < np: partial j's (m, l) per head (clamped addresses, masked)
+    float mj[G], lj[G];
+    const float *pj = part + (size_t)min((uint32_t)lane, np - 1) * PART + G * D;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        mj[h] = pj[2 * h];
+        lj[h] = pj[2 * h + 1];
+    }
+    float ov[CH][EPL];
+    auto load_o = [&](uint32_t i0) {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const float *pc = part + (size_t)min(i0 + (uint32_t)c, np - 1) * PART;
+#pragma unroll
+            for (int k = 0; k < EPL; k++)
+                ov[c][k] = pc[lane + 64 * k];
+        }
+    };
+    load_o(0);
+    float M[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        M[h] = wave_max_f32((uint32_t)lane < np ? mj[h] : -INFINITY);
+        if ((uint32_t)lane >= np)
+            lj[h] = 0.f;
+    }
+    float L[G], O[EPL];
+#pragma unroll
+    for (int h = 0; h < G; h++)
+        L[h] = 0.f;
+#pragma unroll
+    for (int k = 0; k < EPL; k++)
+        O[k] = 0.f;
+    for (uint32_t i0 = 0; i0 < np; i0 += CH) {
+        if (i0 > 0)
+            load_o(i0);
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const uint32_t i = i0 + (uint32_t)c;
+            if (i >= np)
+                break;
+            float f[G];
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mj[h]), (int)i));
+                const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj[h]), (int)i));
+                f[h] = m == -INFINITY ? 0.f : exp2f(m - M[h]);
+                L[h] = fmaf(l, f[h], L[h]);
+            }
+#pragma unroll
+            for (int k = 0; k < EPL; k++)
+                O[k] = fmaf(ov[c][k], f[(lane + 64 * k) / D], O[k]);
+        }
+    }
+    const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        const uint32_t e = (uint32_t)lane + 64u * k;
+        const float Lh = L[e / D];
+        float v = (Lh > 0.f || Lh != Lh) ? O[k] / Lh : 0.f;
+        if (bad)
+            v = __builtin_nanf("");
+        if (p.out)
+            p.out[obase + e] = rl_from_f32<DT>(v);
+        if (p.out_f32)
+            p.out_f32[obase + e] = v;
+    }
+}
+
 template <int D, int G, int DT, int NTHR, int GH>
 __device__ __forceinline__ void merge_row(const AttnParams &p, uint32_t b, uint32_t g, uint32_t h0, uint32_t R0,
                                           uint32_t nu, uint32_t U, uint32_t NW, bool bad, uint32_t tid, float *s_f,

@@ -57,6 +57,7 @@ constexpr int kFusedQuads = 8;
 struct SplitIn {
     uint32_t wgs, sample_wgs;   // workgroups, of which sampling first (multiples of 8)
     uint32_t tile_bytes;        // K and V bytes of one tile
+    uint32_t merge_rounds;      // rows of the previous step each sampling wave merges first
     uint64_t sample_bytes;      // logits bytes one sampling workgroup streams
     float sample_cost;          // its time per byte over an attention workgroup's
 };
@@ -68,6 +69,10 @@ struct SplitIn {
 // workgroups' tiles at about 2.7 us per wave; a factor of 1.8 ended both kinds
 // of wave together best (1.0, 1.4, 1.8 and 2.2 tried).
 constexpr float kSampleCost = 1.8f;
+// A wave's merge of one row of the previous step (pipelined calls) costs
+// about as long as an attention workgroup takes to stream this many bytes:
+// one round trip for the partials (about 4 us) at a workgroup's share of HBM.
+constexpr uint64_t kMergeRoundBytes = 96u * 1024u;
 
 // The pieces of one XCD's N tiles, one per wave of the XCD: the Aa attention
 // waves' first (weight 256 each), then the As sampling waves' (weight ws).
@@ -120,14 +125,16 @@ __host__ __device__ inline uint32_t xcd_start(uint32_t x, uint32_t U)
     return (uint32_t)(((uint64_t)x * U) / kXcds);
 }
 
-// The schedule of XCD x: a sampling wave's weight is 1 - sample_cost x (its
-// workgroup's logits bytes / a workgroup's share of all bytes), at least 1/4.
+// The schedule of XCD x: a sampling wave's weight is 1 - (sample_cost x its
+// workgroup's logits bytes + its merge rounds' equivalent bytes) / a
+// workgroup's share of all bytes, at least 1/4.
 __host__ __device__ inline Sched sched_x(uint32_t x, uint32_t U, const SplitIn &in)
 {
     const uint32_t Aa = (in.wgs - in.sample_wgs) / kXcds * kFWaves;
     const uint32_t As = in.sample_wgs / kXcds * kFWaves;
     const double fair = ((double)U * in.tile_bytes + (double)in.sample_bytes * in.sample_wgs) / in.wgs;
-    double w = fair > 0.0 ? 1.0 - (double)in.sample_cost * (double)in.sample_bytes / fair : 1.0;
+    const double pre = (double)in.sample_cost * (double)in.sample_bytes + (double)in.merge_rounds * kMergeRoundBytes;
+    double w = fair > 0.0 ? 1.0 - pre / fair : 1.0;
     w = w < 0.25 ? 0.25 : (w > 1.0 ? 1.0 : w);
     return sched_of(xcd_start(x + 1, U) - xcd_start(x, U), Aa, As, (uint32_t)(w * 256.0 + 0.5));
 }
@@ -155,6 +162,13 @@ struct FusedParams {
     AttnParams p;          // p.part: partials at (piece + row); p.cum: [batch + 1] (written by workgroup 0)
     SampleParams sp;       // the sampled micro-batch
     SplitIn si;
+    SplitIn *si_out;       // the workspace's record of si (workgroup 0 writes it)
+    // the previous step of a pipeline: its rows merged and its K/V appended
+    // by the sampling waves before they sample (has_prev 0: none)
+    uint32_t has_prev;
+    AttnParams pp;         // its attention, partials and prefix in its workspace
+    AppendParams pap;
+    const SplitIn *psi;    // its split, recorded by its own call
 };
 
 template <int D, int G, int DT, int TPB>
@@ -197,6 +211,33 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
     const bool sampler = wg < f.si.sample_wgs;
+
+    if (wg == 0 && tid == 0)
+        *f.si_out = f.si;  // read by the merge kernel, or by the next call of a pipeline
+
+    // ---- the previous step's rows: merge and append, one row per sampling wave ---
+    if (sampler && f.has_prev) {
+        const AttnParams &pp = f.pp;
+        const uint32_t nsw = f.si.sample_wgs * kFWaves;
+        const uint32_t rows = pp.batch * pp.kv_heads;
+        const uint32_t Up = rl_sload(pp.cum + pp.batch);
+        const SplitIn psi = *f.psi;
+        for (uint32_t r = wg * kFWaves + (uint32_t)wave; r < rows; r += nsw) {
+            const uint32_t b = r / pp.kv_heads, g = r % pp.kv_heads;
+            const uint32_t cin = pp.ctx[b];
+            const bool bad = cin > pp.max_ctx;
+            const uint32_t nu = tiles_of(pp, cin);
+            if (nu == 0) {
+                empty_row<D, G, DT, G>(pp, b, g, 0, bad, (uint32_t)lane, 64);
+            } else {
+                const uint32_t R0 = pp.cum[b] + g * nu;
+                merge_row_wave<D, G, DT>(pp, b, g, global_piece_of(R0, Up, psi),
+                                         global_piece_of(R0 + nu - 1, Up, psi), bad, lane);
+            }
+            if (f.pap.arena)
+                append_row(f.pap, b, g, (uint32_t)lane, 64);
+        }
+    }
 
     // ---- sampling role ----------------------------------------------------------
     if (sampler) {
@@ -267,7 +308,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
 // rows without tiles and appends the step's K/V token (the row's first
 // workgroup). HS workgroups of G / HS heads per row, as attn_merge_kernel.
 template <int D, int G, int DT, int HS>
-__global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendParams ap, SplitIn si)
+__global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendParams ap, const SplitIn *psi)
 {
     constexpr int GH = G / HS;
     __shared__ float s_f[kMergeLds * G];
@@ -286,6 +327,7 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
         empty_row<D, G, DT, GH>(p, b, g, h0, bad, threadIdx.x, 256);
         return;
     }
+    const SplitIn si = *psi;
     const uint32_t R0 = cum_b + g * nu;
     const uint32_t wf = global_piece_of(R0, U, si);
     const uint32_t wl = global_piece_of(R0 + nu - 1, U, si);
@@ -295,7 +337,7 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 // ---- launcher ----------------------------------------------------------------------
 
 struct FusedWs {
-    size_t cum_off, part_off, total;
+    size_t si_off, cum_off, part_off, total;
 };
 
 // Partials: at most one per wave-piece plus one per row (slot piece + row).
@@ -305,8 +347,9 @@ FusedWs fused_ws(const rl_attn_decode_args_t *a, const SplitIn &si)
     const uint32_t G = a->q_heads / a->kv_heads;
     const size_t part = (size_t)G * a->layout.head_dim + 2 * G;
     const size_t rows = (size_t)a->batch * a->kv_heads;
-    w.cum_off = 0;
-    w.part_off = (((size_t)a->batch + 1) * 4 + 255) / 256 * 256;
+    w.si_off = 0;
+    w.cum_off = 256;
+    w.part_off = w.cum_off + (((size_t)a->batch + 1) * 4 + 255) / 256 * 256;
     w.total = w.part_off + ((size_t)si.wgs * kFWaves + rows) * part * 4;
     return w;
 }
@@ -317,28 +360,36 @@ bool fits()
     return FusedLayout<D, G, DT, TPB>::FITS;
 }
 
+enum : int { kRunFused = 1, kRunMerge = 2 };
+
 template <int D, int G, int DT, int TPB>
-int launch_fused(const FusedParams &f, const AppendParams &ap, uint32_t wgs)
+int launch(int what, const FusedParams &f, const AppendParams &ap, hipStream_t stream)
 {
     if constexpr (!FusedLayout<D, G, DT, TPB>::FITS) {
         rl_set_error("rl_hip_decode_sample_step: shape does not fit the fused step");
         return -1;
     } else {
-        hipLaunchKernelGGL((decode_fused_kernel<D, G, DT, TPB>), dim3(wgs), dim3(kFThreads), 0, rl_stream(), f);
-        if (rl_check_launch("decode_fused_kernel launch"))
-            return -1;
-        constexpr int HS = G >= 2 ? G / 2 : 1;
-        // rows averaging more partials than the one-workgroup register path
-        // holds (16 at two output elements per thread) take workgroups of two
-        // heads, as attn_merge_kernel
-        const uint64_t rows = (uint64_t)f.p.batch * f.p.kv_heads;
-        if (HS > 1 && (uint64_t)wgs * kFWaves >= 16ull * rows)
-            hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, HS>), dim3(f.p.kv_heads * HS, f.p.batch), dim3(256), 0,
-                               rl_stream(), f.p, ap, f.si);
-        else
-            hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, 1>), dim3(f.p.kv_heads, f.p.batch), dim3(256), 0,
-                               rl_stream(), f.p, ap, f.si);
-        return rl_check_launch("merge_pieces_kernel launch");
+        if (what & kRunFused) {
+            hipLaunchKernelGGL((decode_fused_kernel<D, G, DT, TPB>), dim3(f.si.wgs), dim3(kFThreads), 0, stream, f);
+            if (rl_check_launch("decode_fused_kernel launch"))
+                return -1;
+        }
+        if (what & kRunMerge) {
+            constexpr int HS = G >= 2 ? G / 2 : 1;
+            // rows averaging more partials than the one-workgroup register path
+            // holds (16 at two output elements per thread) take workgroups of
+            // two heads, as attn_merge_kernel
+            const uint64_t rows = (uint64_t)f.p.batch * f.p.kv_heads;
+            if (HS > 1 && (uint64_t)f.si.wgs * kFWaves >= 16ull * rows)
+                hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, HS>), dim3(f.p.kv_heads * HS, f.p.batch), dim3(256),
+                                   0, stream, f.p, ap, (const SplitIn *)f.si_out);
+            else
+                hipLaunchKernelGGL((merge_pieces_kernel<D, G, DT, 1>), dim3(f.p.kv_heads, f.p.batch), dim3(256), 0,
+                                   stream, f.p, ap, (const SplitIn *)f.si_out);
+            if (rl_check_launch("merge_pieces_kernel launch"))
+                return -1;
+        }
+        return 0;
     }
 }
 
@@ -368,22 +419,32 @@ bool shape_fits(uint32_t D, uint32_t G, uint32_t dt, uint32_t tpb)
 }
 
 template <int D, int G>
-int launch_dt(const FusedParams &f, const AppendParams &ap, uint32_t wgs, uint32_t dt, uint32_t tpb)
+int launch_dt(int what, const FusedParams &f, const AppendParams &ap, hipStream_t st, uint32_t dt, uint32_t tpb)
 {
     if (dt == RL_DTYPE_BF16)
-        return tpb == 16 ? launch_fused<D, G, 0, 16>(f, ap, wgs) : launch_fused<D, G, 0, 32>(f, ap, wgs);
-    return tpb == 16 ? launch_fused<D, G, 1, 16>(f, ap, wgs) : launch_fused<D, G, 1, 32>(f, ap, wgs);
+        return tpb == 16 ? launch<D, G, 0, 16>(what, f, ap, st) : launch<D, G, 0, 32>(what, f, ap, st);
+    return tpb == 16 ? launch<D, G, 1, 16>(what, f, ap, st) : launch<D, G, 1, 32>(what, f, ap, st);
 }
 
 template <int D>
-int launch_g(const FusedParams &f, const AppendParams &ap, uint32_t wgs, uint32_t G, uint32_t dt, uint32_t tpb)
+int launch_g(int what, const FusedParams &f, const AppendParams &ap, hipStream_t st, uint32_t G, uint32_t dt,
+             uint32_t tpb)
 {
     switch (G) {
-    case 1: return launch_dt<D, 1>(f, ap, wgs, dt, tpb);
-    case 2: return launch_dt<D, 2>(f, ap, wgs, dt, tpb);
-    case 4: return launch_dt<D, 4>(f, ap, wgs, dt, tpb);
-    default: return launch_dt<D, 8>(f, ap, wgs, dt, tpb);
+    case 1: return launch_dt<D, 1>(what, f, ap, st, dt, tpb);
+    case 2: return launch_dt<D, 2>(what, f, ap, st, dt, tpb);
+    case 4: return launch_dt<D, 4>(what, f, ap, st, dt, tpb);
+    default: return launch_dt<D, 8>(what, f, ap, st, dt, tpb);
     }
+}
+
+int launch_shape(int what, const rl_attn_decode_args_t *attn, const FusedParams &f, const AppendParams &ap,
+                 hipStream_t st)
+{
+    const uint32_t G = attn->q_heads / attn->kv_heads;
+    if (attn->layout.head_dim == 128)
+        return launch_g<128>(what, f, ap, st, G, attn->dtype, attn->layout.token_count);
+    return launch_g<64>(what, f, ap, st, G, attn->dtype, attn->layout.token_count);
 }
 
 // Workgroups of the fused grid (one per compute unit, a multiple of 8) and
@@ -441,6 +502,63 @@ extern "C" size_t rl_hip_decode_sample_step_workspace(const rl_attn_decode_args_
     return fused_eligible(attn) ? fused : split;
 }
 
+namespace {
+
+// The kernel view of an attention call whose prefix and partials live in
+// workspace ws (layout w).
+AttnParams attn_params_of(const rl_attn_decode_args_t *attn, uint8_t *ws, const FusedWs &w)
+{
+    AttnParams p;
+    p.arena = (const uint8_t *)attn->arena_base;
+    p.block_bytes = attn->layout.block_bytes;
+    p.arena_blocks = attn->arena_bytes / attn->layout.block_bytes;
+    p.table = attn->block_table;
+    p.table_stride = attn->table_stride;
+    p.row_map = nullptr;
+    p.ctx = attn->ctx_lens;
+    p.max_ctx = attn->max_ctx;
+    p.batch = attn->batch;
+    p.q_heads = attn->q_heads;
+    p.kv_heads = attn->kv_heads;
+    p.q = (const uint16_t *)attn->q;
+    p.out = (uint16_t *)attn->out;
+    p.out_f32 = attn->out_f32;
+    const float scale = attn->scale != 0.f ? attn->scale : 1.0f / sqrtf((float)attn->layout.head_dim);
+    p.scale_log2 = scale * 1.4426950408889634f;
+    p.nwaves = 0;  // the pieces replace the even split
+    p.cum = (uint32_t *)(ws + w.cum_off);
+    p.part = (float *)(ws + w.part_off);
+    return p;
+}
+
+// The fused kernel's arguments for attention `attn` and sampling `samp` on
+// workspace ws; the previous pipeline step, if any, filled in by the caller.
+FusedParams fused_params_of(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp, void *workspace,
+                            uint32_t merge_rounds)
+{
+    FusedParams f;
+    f.si = split_in_of(attn, samp);
+    f.si.merge_rounds = merge_rounds;
+    const FusedWs w = fused_ws(attn, f.si);
+    uint8_t *ws = (uint8_t *)workspace;
+    f.si_out = (SplitIn *)(ws + w.si_off);
+    f.p = attn_params_of(attn, ws, w);
+    f.sp = sample_params_of(samp);
+    f.has_prev = 0;
+    f.psi = nullptr;
+    f.pp = f.p;
+    f.pap.arena = nullptr;
+    return f;
+}
+
+bool same_shape(const rl_attn_decode_args_t *a, const rl_attn_decode_args_t *b)
+{
+    return a->q_heads == b->q_heads && a->kv_heads == b->kv_heads && a->dtype == b->dtype &&
+           a->layout.head_dim == b->layout.head_dim && a->layout.token_count == b->layout.token_count;
+}
+
+}  // namespace
+
 extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                                          const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes)
 {
@@ -465,35 +583,122 @@ extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, cons
         s.workspace_bytes = workspace_bytes - a_bytes;
         return rl_hip_sample(&s);
     }
+    const FusedParams f = fused_params_of(attn, samp, workspace, 0);
+    return launch_shape(kRunFused | kRunMerge, attn, f, append_params(append), rl_stream());
+}
+
+namespace {
+
+int pipeline_step_on(hipStream_t stream, const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp,
+                     const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append, void *workspace,
+                     void *prev_workspace, size_t workspace_bytes, const char *who)
+{
+    if (rl_require_open(who) || rl_attn_check(attn) || rl_sample_check(samp))
+        return -1;
+    if (!fused_eligible(attn)) {
+        rl_set_error("%s: the shape does not fit the fused kernel (use rl_hip_decode_sample_step)", who);
+        return -1;
+    }
+    const size_t need = rl_hip_decode_sample_step_workspace(attn, samp);
+    if (!workspace || workspace_bytes < need) {
+        rl_set_error("%s: workspace %zu bytes < %zu required", who, workspace_bytes, need);
+        return -1;
+    }
+    uint32_t merge_rounds = 0;
+    if (prev_attn) {
+        if (rl_decode_step_check(prev_attn, prev_append, who))
+            return -1;
+        if (!same_shape(attn, prev_attn)) {
+            rl_set_error("%s: the previous step's heads, dtype or layout differ from this step's", who);
+            return -1;
+        }
+        if (!prev_workspace || prev_workspace == workspace ||
+            workspace_bytes < fused_ws(prev_attn, split_in_of(prev_attn, samp)).total) {
+            rl_set_error("%s: the previous step needs its own workspace of this size", who);
+            return -1;
+        }
+        const uint32_t rows = prev_attn->batch * prev_attn->kv_heads;
+        uint32_t wgs, sample_wgs;
+        grid_of(samp->rows, wgs, sample_wgs);
+        merge_rounds = (rows + sample_wgs * kFWaves - 1) / (sample_wgs * kFWaves);
+    }
+    FusedParams f = fused_params_of(attn, samp, workspace, merge_rounds);
+    if (prev_attn) {
+        const FusedWs pw = fused_ws(prev_attn, f.si);
+        f.has_prev = 1;
+        f.pp = attn_params_of(prev_attn, (uint8_t *)prev_workspace, pw);
+        f.pap = append_params(prev_append);
+        f.psi = (const SplitIn *)((uint8_t *)prev_workspace + pw.si_off);
+    }
+    return launch_shape(kRunFused, attn, f, f.pap, stream);
+}
+
+int pipeline_flush_on(hipStream_t stream, const rl_attn_decode_args_t *prev_attn,
+                      const rl_kv_append_args_t *prev_append, void *prev_workspace, size_t workspace_bytes,
+                      const char *who)
+{
+    if (rl_require_open(who) || rl_decode_step_check(prev_attn, prev_append, who))
+        return -1;
+    if (!fused_eligible(prev_attn)) {
+        rl_set_error("%s: the shape does not fit the fused kernel", who);
+        return -1;
+    }
+    // the workspace layout depends only on the attention and the grid
+    rl_sample_args_t any = {};
+    any.rows = 1;
+    any.vocab = 1;
+    const SplitIn si = split_in_of(prev_attn, &any);
+    const FusedWs w = fused_ws(prev_attn, si);
+    if (!prev_workspace || workspace_bytes < w.total) {
+        rl_set_error("%s: workspace %zu bytes < %zu required", who, workspace_bytes, w.total);
+        return -1;
+    }
     FusedParams f;
-    f.si = split_in_of(attn, samp);
-    const uint32_t wgs = f.si.wgs;
-    const FusedWs w = fused_ws(attn, f.si);
-    uint8_t *ws = (uint8_t *)workspace;
-    AttnParams &p = f.p;
-    p.arena = (const uint8_t *)attn->arena_base;
-    p.block_bytes = attn->layout.block_bytes;
-    p.arena_blocks = attn->arena_bytes / attn->layout.block_bytes;
-    p.table = attn->block_table;
-    p.table_stride = attn->table_stride;
-    p.row_map = nullptr;
-    p.ctx = attn->ctx_lens;
-    p.max_ctx = attn->max_ctx;
-    p.batch = attn->batch;
-    p.q_heads = attn->q_heads;
-    p.kv_heads = attn->kv_heads;
-    p.q = (const uint16_t *)attn->q;
-    p.out = (uint16_t *)attn->out;
-    p.out_f32 = attn->out_f32;
-    const float scale = attn->scale != 0.f ? attn->scale : 1.0f / sqrtf((float)attn->layout.head_dim);
-    p.scale_log2 = scale * 1.4426950408889634f;
-    p.nwaves = 0;  // the pieces replace the even split
-    p.cum = (uint32_t *)(ws + w.cum_off);
-    p.part = (float *)(ws + w.part_off);
-    f.sp = sample_params_of(samp);
-    const AppendParams ap = append_params(append);
-    const uint32_t G = attn->q_heads / attn->kv_heads;
-    if (attn->layout.head_dim == 128)
-        return launch_g<128>(f, ap, wgs, G, attn->dtype, attn->layout.token_count);
-    return launch_g<64>(f, ap, wgs, G, attn->dtype, attn->layout.token_count);
+    f.si = si;
+    f.si_out = (SplitIn *)((uint8_t *)prev_workspace + w.si_off);  // recorded by the step that wrote the partials
+    f.p = attn_params_of(prev_attn, (uint8_t *)prev_workspace, w);
+    return launch_shape(kRunMerge, prev_attn, f, append_params(prev_append), stream);
+}
+
+}  // namespace
+
+extern "C" int rl_hip_decode_pipeline_step(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp,
+                                           const rl_attn_decode_args_t *prev_attn,
+                                           const rl_kv_append_args_t *prev_append, void *workspace,
+                                           void *prev_workspace, size_t workspace_bytes)
+{
+    return pipeline_step_on(rl_stream(), attn, samp, prev_attn, prev_append, workspace, prev_workspace,
+                            workspace_bytes, "rl_hip_decode_pipeline_step");
+}
+
+
+
+extern "C" int rl_hip_decode_lane_step(int lane, const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp,
+                                       const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append,
+                                       void *workspace, void *prev_workspace, size_t workspace_bytes)
+{
+    const char *who = "rl_hip_decode_lane_step";
+    hipStream_t st = rl_lane_stream(lane, who);
+    if (!st)
+        return -1;
+    return pipeline_step_on(st, attn, samp, prev_attn, prev_append, workspace, prev_workspace, workspace_bytes, who);
+}
+
+extern "C" int rl_hip_decode_lane_flush(int lane, const rl_attn_decode_args_t *prev_attn,
+                                        const rl_kv_append_args_t *prev_append, void *prev_workspace,
+                                        size_t workspace_bytes)
+{
+    const char *who = "rl_hip_decode_lane_flush";
+    hipStream_t st = rl_lane_stream(lane, who);
+    if (!st)
+        return -1;
+    return pipeline_flush_on(st, prev_attn, prev_append, prev_workspace, workspace_bytes, who);
+}
+
+extern "C" int rl_hip_decode_pipeline_flush(const rl_attn_decode_args_t *prev_attn,
+                                            const rl_kv_append_args_t *prev_append, void *prev_workspace,
+                                            size_t workspace_bytes)
+{
+    return pipeline_flush_on(rl_stream(), prev_attn, prev_append, prev_workspace, workspace_bytes,
+                             "rl_hip_decode_pipeline_flush");
 }

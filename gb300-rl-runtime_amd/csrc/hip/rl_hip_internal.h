@@ -10,6 +10,9 @@ void rl_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
 int rl_check_hip(hipError_t e, const char *what);
 int rl_require_open(const char *what);
 hipStream_t rl_stream(void);
+// Lane `lane`'s stream, or nullptr (error set) when no device is open or the
+// lane is out of range.
+hipStream_t rl_lane_stream(int lane, const char *what);
 // Compute units of the open device (0 when no device is open).
 uint32_t rl_cu_count(void);
 // The open device's ordinal (-1 when no device is open).

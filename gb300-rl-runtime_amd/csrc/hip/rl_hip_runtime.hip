@@ -1,5 +1,6 @@
 // rl_hip_runtime.hip - session, memory and timing half of the thin C ABI
-// (rl_hip.h). One device, one non-blocking stream, one host thread.
+// (rl_hip.h). One device, one non-blocking library stream plus two lane
+// streams for overlapped decode steps, one host thread.
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -24,8 +25,11 @@ struct Session {
     int device = -1;
     uint32_t cu_count = 0;
     hipStream_t stream = nullptr;
+    hipStream_t lanes[RL_HIP_LANES] = {};
     hipEvent_t ev_begin = nullptr;
     hipEvent_t ev_end = nullptr;
+    hipEvent_t ev_fork = nullptr;
+    hipEvent_t ev_lane[RL_HIP_LANES] = {};
     std::mutex mu;
     CoherentBlock coherent[kMaxCoherent];
     int n_coherent = 0;
@@ -53,6 +57,17 @@ int rl_check_hip(hipError_t e, const char *what)
 }
 
 hipStream_t rl_stream(void) { return g_session.stream; }
+
+hipStream_t rl_lane_stream(int lane, const char *what)
+{
+    if (rl_require_open(what))
+        return nullptr;
+    if (lane < 0 || lane >= RL_HIP_LANES) {
+        rl_set_error("%s: lane %d out of range [0, %d)", what, lane, RL_HIP_LANES);
+        return nullptr;
+    }
+    return g_session.lanes[lane];
+}
 
 uint32_t rl_cu_count(void) { return g_session.cu_count; }
 
@@ -92,6 +107,16 @@ int rl_hip_open(int device)
     if (rl_check_hip(hipEventCreate(&g_session.ev_begin), "hipEventCreate") ||
         rl_check_hip(hipEventCreate(&g_session.ev_end), "hipEventCreate"))
         return -1;
+    // lanes keep the default priority, like the library stream; their events
+    // only order work, so they record no timestamps
+    if (rl_check_hip(hipEventCreateWithFlags(&g_session.ev_fork, hipEventDisableTiming), "hipEventCreateWithFlags"))
+        return -1;
+    for (int l = 0; l < RL_HIP_LANES; l++)
+        if (rl_check_hip(hipStreamCreateWithFlags(&g_session.lanes[l], hipStreamNonBlocking),
+                         "hipStreamCreateWithFlags") ||
+            rl_check_hip(hipEventCreateWithFlags(&g_session.ev_lane[l], hipEventDisableTiming),
+                         "hipEventCreateWithFlags"))
+            return -1;
     int cus = 0;
     if (rl_check_hip(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device),
                      "hipDeviceGetAttribute(MultiprocessorCount)"))
@@ -107,6 +132,15 @@ int rl_hip_close(void)
     if (!g_session.open)
         return 0;
     int rc = rl_check_hip(hipStreamSynchronize(g_session.stream), "hipStreamSynchronize");
+    for (int l = 0; l < RL_HIP_LANES; l++) {
+        if (rl_check_hip(hipStreamSynchronize(g_session.lanes[l]), "hipStreamSynchronize"))
+            rc = -1;
+        (void)hipEventDestroy(g_session.ev_lane[l]);
+        (void)hipStreamDestroy(g_session.lanes[l]);
+        g_session.lanes[l] = nullptr;
+        g_session.ev_lane[l] = nullptr;
+    }
+    (void)hipEventDestroy(g_session.ev_fork);
     (void)hipEventDestroy(g_session.ev_begin);
     (void)hipEventDestroy(g_session.ev_end);
     (void)hipStreamDestroy(g_session.stream);
@@ -259,7 +293,33 @@ int rl_hip_sync(void)
 {
     if (rl_require_open("rl_hip_sync"))
         return -1;
+    for (int l = 0; l < RL_HIP_LANES; l++)
+        if (rl_check_hip(hipStreamSynchronize(g_session.lanes[l]), "hipStreamSynchronize"))
+            return -1;
     return rl_check_hip(hipStreamSynchronize(g_session.stream), "hipStreamSynchronize");
+}
+
+int rl_hip_lanes_fork(void)
+{
+    if (rl_require_open("rl_hip_lanes_fork"))
+        return -1;
+    if (rl_check_hip(hipEventRecord(g_session.ev_fork, g_session.stream), "hipEventRecord"))
+        return -1;
+    for (int l = 0; l < RL_HIP_LANES; l++)
+        if (rl_check_hip(hipStreamWaitEvent(g_session.lanes[l], g_session.ev_fork, 0), "hipStreamWaitEvent"))
+            return -1;
+    return 0;
+}
+
+int rl_hip_lanes_join(void)
+{
+    if (rl_require_open("rl_hip_lanes_join"))
+        return -1;
+    for (int l = 0; l < RL_HIP_LANES; l++)
+        if (rl_check_hip(hipEventRecord(g_session.ev_lane[l], g_session.lanes[l]), "hipEventRecord") ||
+            rl_check_hip(hipStreamWaitEvent(g_session.stream, g_session.ev_lane[l], 0), "hipStreamWaitEvent"))
+            return -1;
+    return 0;
 }
 
 int rl_hip_timer_begin(void)

@@ -320,6 +320,15 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_decode_sample_step_workspace": (C.c_size_t, [C.POINTER(AttnArgs), C.POINTER(SampleArgs)]),
         "rl_hip_decode_sample_step": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs), C.POINTER(SampleArgs),
                                              C.c_void_p, C.c_size_t]),
+        "rl_hip_decode_pipeline_step": (i32, [C.POINTER(AttnArgs), C.POINTER(SampleArgs), C.POINTER(AttnArgs),
+                                               C.POINTER(AppendArgs), C.c_void_p, C.c_void_p, C.c_size_t]),
+        "rl_hip_decode_pipeline_flush": (i32, [C.POINTER(AttnArgs), C.POINTER(AppendArgs), C.c_void_p,
+                                                C.c_size_t]),
+        "rl_hip_lanes_fork": (i32, []), "rl_hip_lanes_join": (i32, []),
+        "rl_hip_decode_lane_step": (i32, [i32, C.POINTER(AttnArgs), C.POINTER(SampleArgs), C.POINTER(AttnArgs),
+                                           C.POINTER(AppendArgs), C.c_void_p, C.c_void_p, C.c_size_t]),
+        "rl_hip_decode_lane_flush": (i32, [i32, C.POINTER(AttnArgs), C.POINTER(AppendArgs), C.c_void_p,
+                                            C.c_size_t]),
         "rl_hip_logits_proj": (i32, [C.POINTER(ProjArgs)]),
         "rl_hip_reward_advantage": (i32, [C.POINTER(RewardArgs)]),
         "rl_hip_rollout_schedule": (i32, [C.POINTER(SchedArgs)]),
@@ -672,12 +681,16 @@ def decode_step(attn: AttnArgs, append: AppendArgs) -> None:
 DECODE_STEP_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 
-def decode_sample_step_workspace(attn: AttnArgs, samp: SampleArgs) -> DeviceBuffer:
-    """The workspace of rl_hip_decode_sample_step."""
+def decode_sample_step_workspace_bytes(attn: AttnArgs, samp: SampleArgs) -> int:
     n = lib().rl_hip_decode_sample_step_workspace(C.byref(attn), C.byref(samp))
     if n == 0:
         raise RlrtError(f"rl_hip_decode_sample_step_workspace: {_err()}")
-    return DeviceBuffer(n, zero=True)
+    return int(n)
+
+
+def decode_sample_step_workspace(attn: AttnArgs, samp: SampleArgs) -> DeviceBuffer:
+    """The workspace of rl_hip_decode_sample_step (and of one micro-batch of its pipelined form)."""
+    return DeviceBuffer(decode_sample_step_workspace_bytes(attn, samp), zero=True)
 
 
 def decode_sample_step(attn: AttnArgs, append: AppendArgs, samp: SampleArgs, ws: DeviceBuffer) -> None:
@@ -685,6 +698,49 @@ def decode_sample_step(attn: AttnArgs, append: AppendArgs, samp: SampleArgs, ws:
     sampling of another micro-batch's logits in one launch (plus the merge)."""
     check(lib().rl_hip_decode_sample_step(C.byref(attn), C.byref(append), C.byref(samp), ws.ptr, ws.nbytes),
           "rl_hip_decode_sample_step")
+
+
+def decode_pipeline_step(attn: AttnArgs, samp: SampleArgs, ws: DeviceBuffer, prev_attn: AttnArgs | None = None,
+                         prev_append: AppendArgs | None = None, prev_ws: DeviceBuffer | None = None) -> None:
+    """One step of the two-micro-batch pipeline: attn's partials into ws, the
+    sampling of samp, and the merge + append of the previous step."""
+    check(lib().rl_hip_decode_pipeline_step(
+        C.byref(attn), C.byref(samp), C.byref(prev_attn) if prev_attn is not None else None,
+        C.byref(prev_append) if prev_append is not None else None, ws.ptr,
+        prev_ws.ptr if prev_ws is not None else None, ws.nbytes), "rl_hip_decode_pipeline_step")
+
+
+def decode_pipeline_flush(prev_attn: AttnArgs, prev_append: AppendArgs, prev_ws: DeviceBuffer) -> None:
+    check(lib().rl_hip_decode_pipeline_flush(C.byref(prev_attn), C.byref(prev_append), prev_ws.ptr, prev_ws.nbytes),
+          "rl_hip_decode_pipeline_flush")
+
+
+LANES = 2
+
+
+def lanes_fork() -> None:
+    """Every lane waits for the work queued so far on the library stream."""
+    check(lib().rl_hip_lanes_fork(), "rl_hip_lanes_fork")
+
+
+def lanes_join() -> None:
+    """The library stream waits for the work queued so far on every lane."""
+    check(lib().rl_hip_lanes_join(), "rl_hip_lanes_join")
+
+
+def decode_lane_step(lane: int, attn: AttnArgs, samp: SampleArgs, ws: DeviceBuffer, prev_attn: AttnArgs | None = None,
+                     prev_append: AppendArgs | None = None, prev_ws: DeviceBuffer | None = None) -> None:
+    """decode_pipeline_step on lane `lane` (0 or 1): steps on the two lanes may
+    run at the same time, so each lane carries its own micro-batches."""
+    check(lib().rl_hip_decode_lane_step(
+        lane, C.byref(attn), C.byref(samp), C.byref(prev_attn) if prev_attn is not None else None,
+        C.byref(prev_append) if prev_append is not None else None, ws.ptr,
+        prev_ws.ptr if prev_ws is not None else None, ws.nbytes), "rl_hip_decode_lane_step")
+
+
+def decode_lane_flush(lane: int, prev_attn: AttnArgs, prev_append: AppendArgs, prev_ws: DeviceBuffer) -> None:
+    check(lib().rl_hip_decode_lane_flush(lane, C.byref(prev_attn), C.byref(prev_append), prev_ws.ptr,
+                                         prev_ws.nbytes), "rl_hip_decode_lane_flush")
 
 
 def decode_step_noalloc(attn: AttnArgs, append: AppendArgs) -> None:

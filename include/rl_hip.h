@@ -66,7 +66,7 @@ int rl_hip_memcpy_h2d(void *dst_device, const void *src, size_t bytes);
 int rl_hip_memcpy_d2h(void *dst, const void *src_device, size_t bytes);
 int rl_hip_memcpy_d2d(void *dst_device, const void *src_device, size_t bytes);
 int rl_hip_memset_d(void *dst_device, int value, size_t bytes);
-int rl_hip_sync(void);
+int rl_hip_sync(void);  /* waits for the library stream and both lanes */
 
 /* ---- timing on the library stream (HIP events) --------------------------- */
 int rl_hip_timer_begin(void);
@@ -558,6 +558,57 @@ int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_arg
 size_t rl_hip_decode_sample_step_workspace(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp);
 int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                               const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes);
+
+/* ---- the same step pipelined over two micro-batches ------------------------
+ * The launch of rl_hip_decode_sample_step without its second kernel: step t
+ * streams attn's tiles (partials into `workspace`) and samples `samp`, and
+ * its sampling waves first merge the previous step's split rows and append
+ * its K/V token (prev_attn / prev_append, partials in prev_workspace, which
+ * that step was given as its workspace). So the rows of attn are complete
+ * only after the next step (or rl_hip_decode_pipeline_flush) has run; rows
+ * that one piece covered are written at once. Tokens, logprobs and the
+ * appended KV equal rl_hip_decode_sample_step's; the attention is its fp32
+ * math (bit for bit when the split is the same, as at the first step: the
+ * merge work of the sampling waves shifts the split otherwise), within 1e-4
+ * of fp64. prev_attn NULL: nothing to merge (the first step). The two micro-batches alternate, each with its own
+ * workspace of rl_hip_decode_sample_step_workspace bytes; prev_attn must
+ * have attn's heads, dtype and layout, and prev_append must not write what
+ * attn reads (the other micro-batch's blocks; a slot at or past a row's
+ * context is never read). Shapes outside the fused kernel are refused.
+ * rl_hip_decode_pipeline_flush merges and appends the last step. Replaces
+ * the same reference functions as rl_hip_decode_sample_step. */
+int rl_hip_decode_pipeline_step(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp,
+                                const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append,
+                                void *workspace, void *prev_workspace, size_t workspace_bytes);
+int rl_hip_decode_pipeline_flush(const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append,
+                                 void *prev_workspace, size_t workspace_bytes);
+
+/* ---- two lanes of pipelined steps ------------------------------------------
+ * No counterpart in the reference (its worker runs one descriptor at a time).
+ * The session owns RL_HIP_LANES extra streams (default priority). Work queued
+ * on different lanes may run at the same time: a step's launch fills the
+ * compute units that the other lane's step leaves idle while its last waves
+ * drain, which one stream cannot do (each launch waits for the previous one
+ * to finish). rl_hip_lanes_fork makes every lane wait for what was queued on
+ * the library stream so far; rl_hip_lanes_join makes the library stream wait
+ * for what was queued on the lanes so far (so rl_hip_timer_end, copies and
+ * rl_hip_sync after it see the lanes' results). rl_hip_decode_lane_step and
+ * rl_hip_decode_lane_flush are rl_hip_decode_pipeline_step and
+ * rl_hip_decode_pipeline_flush on lane `lane` (0 or 1), with the same
+ * arguments and results. Lanes are ordered only by fork and join, so each
+ * lane runs its own pipeline: a micro-batch's steps, the step that merges
+ * them and its flush go to one lane, and the lanes' micro-batches, workspaces,
+ * logits and outputs are disjoint. Four micro-batches m = 0..3 at steps
+ * t = 0, 1, 2, ...: step t runs micro-batch t % 4 on lane t % 2 and merges
+ * step t - 2 (the same lane's previous step). */
+#define RL_HIP_LANES 2
+int rl_hip_lanes_fork(void);
+int rl_hip_lanes_join(void);
+int rl_hip_decode_lane_step(int lane, const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp,
+                            const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append,
+                            void *workspace, void *prev_workspace, size_t workspace_bytes);
+int rl_hip_decode_lane_flush(int lane, const rl_attn_decode_args_t *prev_attn, const rl_kv_append_args_t *prev_append,
+                             void *prev_workspace, size_t workspace_bytes);
 
 /* ---- fused decode step that allocates nothing ------------------------------
  * No counterpart in the reference. For callers that cannot allocate device

@@ -103,8 +103,11 @@ def _check(orc, olib, w, max_ctx, pos, cow, kn, vn, logits, res, want_tok, want_
 
 
 def _kv_rows(rng, w):
-    kn = rng.integers(0, 256, (w.batch, w.kv_heads, w.head_dim * 2), dtype=np.uint8)
-    vn = rng.integers(0, 256, (w.batch, w.kv_heads, w.head_dim * 2), dtype=np.uint8)
+    """The step's new K and V rows, N(0, 1) in the workload's 16-bit format
+    (finite: a later step's attention reads them), as bytes."""
+    shape = (w.batch, w.kv_heads, w.head_dim)
+    kn = synth.to_scalar16(rng.standard_normal(shape, dtype=np.float32), w.dtype).view(np.uint8)
+    vn = synth.to_scalar16(rng.standard_normal(shape, dtype=np.float32), w.dtype).view(np.uint8)
     return kn, vn
 
 
@@ -208,3 +211,223 @@ def test_fused_step_outside_the_kernel_equals_two_calls(rl, gpu, orc, olib):
     assert np.array_equal(lp.download(np.float32, B), res[0][4])
     for b in (lg, tok, lp, sws):
         b.close()
+
+
+class _Batch:
+    """One micro-batch's device buffers: arena, table, ctx, q, outputs, the
+    append's positions and K/V rows."""
+
+    def __init__(self, rl, w, max_ctx, pos, kn, vn):
+        self.rl, self.w = rl, w
+        self.n = w.batch * w.q_heads * w.head_dim
+        self.buf = {k: rl.DeviceBuffer.from_array(v) for k, v in
+                    (("arena", w.arena), ("table", w.table), ("ctx", w.ctx), ("q", w.q), ("pos", pos), ("kn", kn),
+                     ("vn", vn))}
+        self.out, self.out32 = rl.DeviceBuffer(self.n * 2), rl.DeviceBuffer(self.n * 4)
+        layout = rl.KvLayoutDesc.paged(w.token_count, w.head_dim)
+        code = rl.DTYPE_BF16 if w.dtype == "bf16" else rl.DTYPE_FP16
+        b = self.buf
+        self.attn = rl.attn_args(b["arena"], layout, b["table"], w.table_stride, w.batch, w.q_heads, w.kv_heads, code,
+                                 b["ctx"], max_ctx, b["q"], self.out, self.out32)
+        self.app = rl.AppendArgs(arena_base=b["arena"].ptr, arena_bytes=b["arena"].nbytes, layout=layout,
+                                 block_table=b["table"].ptr, table_stride=w.table_stride, batch=w.batch,
+                                 kv_heads=w.kv_heads, positions=b["pos"].ptr, cow_src=None, k_new=b["kn"].ptr,
+                                 v_new=b["vn"].ptr)
+
+    def outputs(self):
+        w = self.w
+        sh = (w.batch, w.q_heads, w.head_dim)
+        return self.out.download(np.uint16, sh), self.out32.download(np.float32, sh)
+
+    def close(self):
+        for x in list(self.buf.values()) + [self.out, self.out32]:
+            x.close()
+
+
+def test_fused_pipeline_two_microbatches(rl, gpu, orc, olib):
+    """Three pipelined steps over micro-batches A, B, A (the second A step at
+    context + 1, so it reads the token the first one appended) and a flush.
+    Every micro-batch's attention is within 1e-4 of fp64; the first step's
+    (nothing to merge before it, so the same split) equals
+    rl_hip_decode_sample_step's bit for bit, which pins the wave-level merge
+    to the merge kernel's arithmetic; the arenas equal the oracle's appends;
+    every step's tokens equal the oracle's."""
+    QH, KVH, D, V = 32, 8, 128, 32000
+    rng = np.random.default_rng(8151)
+    # A: 64 rollouts of up to 1,200 tokens, so that no row spans more than 16
+    # pieces (the merge kernel's register path, which the bit check compares)
+    wa = synth.make_decode(8152, 64, QH, KVH, D, 300, 1200, reserve_tokens=1300)
+    wb = synth.make_decode(8153, 40, QH, KVH, D, 1, 1200, max_ctx=1300)
+    mc = 1300
+    pa1, pb = wa.ctx.copy(), wb.ctx.copy()
+    ka1, va1 = _kv_rows(rng, wa)
+    ka2, va2 = _kv_rows(rng, wa)
+    kb, vb = _kv_rows(rng, wb)
+    qa2 = synth.f32_to_bf16(rng.standard_normal(wa.q.shape, dtype=np.float32))
+    lg = [rng.standard_normal((64, V), dtype=np.float32) for _ in range(3)]
+    seeds = rng.integers(0, 2**63, 64, dtype=np.uint64)
+
+    A1 = _Batch(rl, wa, mc, pa1, ka1, va1)
+    B = _Batch(rl, wb, mc, pb, kb, vb)
+    # A's second step shares A's arena and table: its own ctx (+1), q, positions, rows, outputs
+    A2 = _Batch(rl, synth.DecodeWorkload(wa.batch, QH, KVH, D, "bf16", 16, wa.ctx + np.uint32(1), wa.table,
+                                         wa.arena, qa2, 0), mc, pa1 + np.uint32(1), ka2, va2)
+    for k in ("arena", "table"):
+        A2.buf[k].close()
+        A2.buf[k] = A1.buf[k]
+    A2.attn.arena_base, A2.attn.block_table = A1.attn.arena_base, A1.attn.block_table
+    A2.app.arena_base, A2.app.block_table = A1.app.arena_base, A1.app.block_table
+    seed_buf = rl.DeviceBuffer.from_array(seeds)
+    lgb = [rl.DeviceBuffer.from_array(x) for x in lg]
+    tok = [rl.DeviceBuffer(64 * 4) for _ in range(3)]
+    lp = [rl.DeviceBuffer(64 * 4) for _ in range(3)]
+    samp = [rl.sample_args(lgb[i], 64, V, V, tok[i], lp[i], temperature=0.9, top_k=64, top_p=0.9, seeds=seed_buf,
+                           step=i) for i in range(3)]
+    # one workspace per micro-batch, both of the larger size (the call takes one size for both)
+    n_ws = max(rl.decode_sample_step_workspace_bytes(bt.attn, samp[0]) for bt in (A1, B))
+    ws = [rl.DeviceBuffer(n_ws) for _ in range(2)]
+    print("[fused] pipeline: A, B, A, flush", flush=True)
+    rl.decode_pipeline_step(A1.attn, samp[0], ws[0])
+    rl.decode_pipeline_step(B.attn, samp[1], ws[1], A1.attn, A1.app, ws[0])
+    rl.decode_pipeline_step(A2.attn, samp[2], ws[0], B.attn, B.app, ws[1])
+    rl.decode_pipeline_flush(A2.attn, A2.app, ws[0])
+    rl.sync()
+    outs = {name: bt.outputs() for name, bt in (("A1", A1), ("B", B), ("A2", A2))}
+    arena_a = A1.buf["arena"].download(np.uint8, wa.arena.size)
+    arena_b = B.buf["arena"].download(np.uint8, wb.arena.size)
+    toks = [(t.download(np.uint32, 64), l.download(np.float32, 64)) for t, l in zip(tok, lp)]
+
+    # the first step's attention through rl_hip_decode_sample_step, bit for bit
+    res = _run(rl, wa, mc, pa1, None, ka1, va1, lg[0], repeats=1, temperature=0.9, top_k=64, top_p=0.9,
+               seed=seeds.copy(), step=0)
+    assert np.array_equal(res[0][0], outs["A1"][0]) and np.array_equal(res[0][1], outs["A1"][1])
+    for name, w in (("A1", wa), ("B", wb)):
+        gh.check_attn(outs[name][0], outs[name][1], orc.attn_f64(olib, w, 0), "bf16")
+    # A's second step read the token A's first step appended
+    arena_a1 = wa.arena.copy()
+    olib.orc_kv_append(arena_a1.ctypes.data, wa.block_bytes, 16, D * 2, wa.table.ctypes.data, wa.table_stride,
+                       wa.batch, KVH, pa1.ctypes.data, None, ka1.ctypes.data, va1.ctypes.data)
+    w2 = synth.DecodeWorkload(wa.batch, QH, KVH, D, "bf16", 16, wa.ctx + np.uint32(1), wa.table, arena_a1, qa2, 0)
+    gh.check_attn(outs["A2"][0], outs["A2"][1], orc.attn_f64(olib, w2, 0), "bf16")
+    pa2 = pa1 + np.uint32(1)
+    olib.orc_kv_append(arena_a1.ctypes.data, wa.block_bytes, 16, D * 2, wa.table.ctypes.data, wa.table_stride,
+                       wa.batch, KVH, pa2.ctypes.data, None, ka2.ctypes.data, va2.ctypes.data)
+    assert np.array_equal(arena_a, arena_a1)
+    arena_b1 = wb.arena.copy()
+    olib.orc_kv_append(arena_b1.ctypes.data, wb.block_bytes, 16, D * 2, wb.table.ctypes.data, wb.table_stride,
+                       wb.batch, KVH, pb.ctypes.data, None, kb.ctypes.data, vb.ctypes.data)
+    assert np.array_equal(arena_b, arena_b1)
+    for i in range(3):
+        want, wlp = orc.sample_rows(olib, lg[i], False, 0.9, 64, 0.9, seeds, i)
+        assert np.array_equal(toks[i][0], want), i
+        assert np.abs(toks[i][1] - wlp).max() < 1e-4, i
+    for x in lgb + tok + lp + ws + [seed_buf]:
+        x.close()
+    A2.buf.pop("arena"), A2.buf.pop("table")
+    for bt in (A1, B, A2):
+        bt.close()
+
+
+def _next_step(rl, first, w, mc, q2, pos2, k2, v2):
+    """The micro-batch's next step: the first step's arena and table, ctx + 1,
+    its own queries, positions, K/V rows and outputs."""
+    w2 = synth.DecodeWorkload(w.batch, w.q_heads, w.kv_heads, w.head_dim, w.dtype, w.token_count,
+                              w.ctx + np.uint32(1), w.table, w.arena, q2, 0)
+    nxt = _Batch(rl, w2, mc, pos2, k2, v2)
+    for k in ("arena", "table"):
+        nxt.buf[k].close()
+        nxt.buf[k] = first.buf[k]
+    nxt.attn.arena_base, nxt.attn.block_table = first.attn.arena_base, first.attn.block_table
+    nxt.app.arena_base, nxt.app.block_table = first.app.arena_base, first.app.block_table
+    return nxt
+
+
+def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
+    """Four micro-batches (64, 48, 64 and 33 rollouts) for two steps each on
+    the two lanes: step t runs micro-batch t % 4 on lane t % 2 and merges step
+    t - 2; the last two steps are flushed on their lanes, then joined. The
+    outputs, arenas and tokens equal the same sequence of
+    rl_hip_decode_pipeline_step calls on the library stream bit for bit (the
+    lanes change where steps run, not what they compute), every attention is
+    within 1e-4 of fp64, the arenas equal the oracle's two appends and every
+    step's tokens equal the oracle's."""
+    QH, KVH, D, V, mc = 32, 8, 128, 32000, 1300
+    rng = np.random.default_rng(9161)
+    sizes = (64, 48, 64, 33)
+    ws_ = [synth.make_decode(9162 + m, n, QH, KVH, D, 1 if m % 2 else 300, 1200, reserve_tokens=1300)
+           for m, n in enumerate(sizes)]
+    pos1 = [w.ctx.copy() for w in ws_]
+    rows1 = [_kv_rows(rng, w) for w in ws_]
+    rows2 = [_kv_rows(rng, w) for w in ws_]
+    q2 = [synth.f32_to_bf16(rng.standard_normal(w.q.shape, dtype=np.float32)) for w in ws_]
+    lg = [rng.standard_normal((64, V), dtype=np.float32) for _ in range(8)]
+    seeds = rng.integers(0, 2**63, 64, dtype=np.uint64)
+    seed_buf = rl.DeviceBuffer.from_array(seeds)
+    lgb = [rl.DeviceBuffer.from_array(x) for x in lg]
+
+    def run(on_lanes):
+        first = [_Batch(rl, w, mc, p, k, v) for w, p, (k, v) in zip(ws_, pos1, rows1)]
+        second = [_next_step(rl, f, w, mc, q, p + np.uint32(1), k, v)
+                  for f, w, q, p, (k, v) in zip(first, ws_, q2, pos1, rows2)]
+        steps = first + second                      # step t runs micro-batch t % 4
+        tok = [rl.DeviceBuffer(64 * 4) for _ in range(8)]
+        lp = [rl.DeviceBuffer(64 * 4) for _ in range(8)]
+        samp = [rl.sample_args(lgb[t], 64, V, V, tok[t], lp[t], temperature=0.9, top_k=64, top_p=0.9,
+                               seeds=seed_buf, step=t) for t in range(8)]
+        n_ws = max(rl.decode_sample_step_workspace_bytes(bt.attn, samp[0]) for bt in first)
+        ws = [rl.DeviceBuffer(n_ws) for _ in range(4)]
+        print(f"[fused] four micro-batches, two steps each, {'on the lanes' if on_lanes else 'one stream'}",
+              flush=True)
+        if on_lanes:
+            rl.lanes_fork()
+        for t in range(8):
+            prev = (steps[t - 2].attn, steps[t - 2].app, ws[(t - 2) % 4]) if t >= 2 else (None, None, None)
+            if on_lanes:
+                rl.decode_lane_step(t % 2, steps[t].attn, samp[t], ws[t % 4], *prev)
+            else:
+                rl.decode_pipeline_step(steps[t].attn, samp[t], ws[t % 4], *prev)
+        for t in (6, 7):
+            if on_lanes:
+                rl.decode_lane_flush(t % 2, steps[t].attn, steps[t].app, ws[t % 4])
+            else:
+                rl.decode_pipeline_flush(steps[t].attn, steps[t].app, ws[t % 4])
+        if on_lanes:
+            rl.lanes_join()
+        rl.sync()
+        res = {"out": [bt.outputs() for bt in steps],
+               "arena": [f.buf["arena"].download(np.uint8, w.arena.size) for f, w in zip(first, ws_)],
+               "tok": [(t.download(np.uint32, 64), l.download(np.float32, 64)) for t, l in zip(tok, lp)]}
+        for x in tok + lp + ws:
+            x.close()
+        for bt in second:
+            bt.buf.pop("arena"), bt.buf.pop("table")
+        for bt in first + second:
+            bt.close()
+        return res
+
+    lanes, one = run(True), run(False)
+    for t in range(8):
+        assert np.array_equal(lanes["out"][t][0], one["out"][t][0]), t
+        assert np.array_equal(lanes["out"][t][1], one["out"][t][1]), t
+        assert np.array_equal(lanes["tok"][t][0], one["tok"][t][0]), t
+        assert np.array_equal(lanes["tok"][t][1], one["tok"][t][1]), t
+    for m, w in enumerate(ws_):
+        assert np.array_equal(lanes["arena"][m], one["arena"][m]), m
+        gh.check_attn(lanes["out"][m][0], lanes["out"][m][1], orc.attn_f64(olib, w, 0), "bf16")
+        arena1 = w.arena.copy()
+        k1, v1 = rows1[m]
+        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, 16, D * 2, w.table.ctypes.data, w.table_stride,
+                           w.batch, KVH, pos1[m].ctypes.data, None, k1.ctypes.data, v1.ctypes.data)
+        w2 = synth.DecodeWorkload(w.batch, QH, KVH, D, "bf16", 16, w.ctx + np.uint32(1), w.table, arena1, q2[m], 0)
+        gh.check_attn(lanes["out"][4 + m][0], lanes["out"][4 + m][1], orc.attn_f64(olib, w2, 0), "bf16")
+        k2, v2 = rows2[m]
+        p2 = pos1[m] + np.uint32(1)
+        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, 16, D * 2, w.table.ctypes.data, w.table_stride,
+                           w.batch, KVH, p2.ctypes.data, None, k2.ctypes.data, v2.ctypes.data)
+        assert np.array_equal(lanes["arena"][m], arena1), m
+    for t in range(8):
+        want, wlp = orc.sample_rows(olib, lg[t], False, 0.9, 64, 0.9, seeds, t)
+        assert np.array_equal(lanes["tok"][t][0], want), t
+        assert np.abs(lanes["tok"][t][1] - wlp).max() < 1e-4, t
+    for x in lgb + [seed_buf]:
+        x.close()
