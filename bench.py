@@ -8,18 +8,26 @@ One step = the batched decode work of 64 rollouts with inputs resident in HBM:
   2. sampling of 64 rows x 128,256 fp32 logits ~N(0,1) with 5 spike tokens per
      row at +8.0: temperature 0.8, top-k 50, top-p 0.9, Philox per-row seed,
      step counter = step index;
-  3. KV append of one token per rollout and KV head (rl_hip_decode_step runs
-     it inside the attention's merge kernel, after every context was read).
-value = tokens/s = 64 x steps/s (whole job, one GPU). The dominant kernel's
-roofline (attention, HBM-bound) is measured over its own launches with HIP
-events on the library stream. The CPU baseline is the oracle's OpenMP
-restatement of the same step, timed on this host.
+  3. KV append of one token per rollout and KV head.
+Four such micro-batches (256 rollouts in flight, each with its own copy of
+the arena in HBM) take turns: step t is one launch of decode_fused_kernel
+that streams micro-batch t % 4's attention tiles and samples its logits,
+while its sampling waves first merge step t - 2's split rows and append that
+step's K/V token; steps alternate between the library's two lanes (streams),
+so one launch fills the compute units the other leaves idle as it drains.
+value = tokens/s = 64 x steps/s (whole job, one GPU). The dominant (only)
+kernel's roofline is measured over the same launches back to back on one
+stream with HIP events. Beside it: the same pipeline on one stream and the
+unfused step (rl_hip_decode_step + rl_hip_sample). The CPU baseline is the
+oracle's OpenMP restatement of the step, timed on this host.
 
 Before the timed run, two rocprofv3 counter passes (FETCH_SIZE, WRITE_SIZE)
-in child processes measure the attention call's HBM traffic, calibrated on a
-256 MiB device copy in the same pass (--no-traffic skips them).
+in child processes measure the fused kernel's HBM traffic per step,
+calibrated on a 256 MiB device copy in the same pass (--no-traffic skips
+them).
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--only step|attn|sample|append|copy]
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+                  [--only step|pipeline|unfused|attn|sample|append|copy]
   python bench.py --workload sample256|longctx|proj|plumbing|rollout|rollout_pipeline|cmdring|pipeline|
                             pipeline_trace
       the other synthetic workloads (sampling at 256 rows, long-context
@@ -36,6 +44,16 @@ import sys
 import time
 
 import numpy as np
+
+# the CPU baseline's OpenMP threads: one per core, packed (read when the
+# oracle's library loads libgomp)
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+# the CPUs this process may run on, read before OpenMP binds the main thread
+try:
+    NPROC = len(os.sched_getaffinity(0))
+except OSError:
+    NPROC = os.cpu_count()
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(ROOT, "gb300-rl-runtime_amd")
@@ -59,8 +77,9 @@ B, QH, KVH, D, TPB = 64, 32, 8, 128, 16
 CTX_LO, CTX_HI, MAX_CTX = 512, 4096, 4096
 VOCAB, SPIKES, TEMP, TOPK, TOPP = 128256, 5, 0.8, 50, 0.9
 LOGIT_COPIES = 4
+MICRO_BATCHES = 4
 SEED_KV, SEED_LOGITS = 2, 3
-PMC_CALLS, PMC_COPY_BYTES = 3, 256 << 20
+PMC_CALLS, PMC_COPY_BYTES = 4, 256 << 20
 
 
 def log(msg):
@@ -129,17 +148,105 @@ class Step:
         return B * KVH * D * 2 * 2 * 2  # read new K/V rows, write them into the arena
 
     def run(self, i, only="step"):
-        if only == "step":
+        if only == "unfused":
             # attention, then the KV append inside the attention's merge kernel
             rlrt.decode_step(self.attn, self.app)
         elif only == "attn":
             rlrt.attn_decode(self.attn)
         elif only == "append":
             rlrt.kv_append(self.app)
-        if only in ("step", "sample"):
+        if only in ("unfused", "sample"):
             s = self.samp[i % LOGIT_COPIES]
             s.step = i
             rlrt.sample(s)
+
+
+class Pipeline:
+    """The headline step: four micro-batches of 64 rollouts (256 in flight),
+    each with its own arena, table, queries, outputs, logits and workspace
+    (the arena and contexts are copies of the same seeded draw, so every step
+    streams the same bytes from its own HBM). Step t runs micro-batch t % 4:
+    its attention's tiles and the sampling of its logits in one launch whose
+    sampling waves first merge step t - 2's split rows and append its K/V
+    token, on lane t % 2 (or all on the library stream). The sampled logits
+    are not the step's own attention's output: in an engine they come from
+    the forward pass of a micro-batch whose attention an earlier step ran."""
+
+    def __init__(self, step):
+        w = step.w
+        self.step = step
+        self.attn, self.app, self.keep = [step.attn], [step.app], []
+        for m in range(1, MICRO_BATCHES):
+            arena = rlrt.DeviceBuffer.from_array(w.arena)
+            table = rlrt.DeviceBuffer.from_array(w.table)
+            ctx = rlrt.DeviceBuffer.from_array(w.ctx)
+            q = rlrt.DeviceBuffer.from_array(w.q)
+            out = rlrt.DeviceBuffer(B * QH * D * 2)
+            pos = rlrt.DeviceBuffer.from_array(w.ctx.copy())
+            self.keep += [arena, table, ctx, q, out, pos]
+            self.attn.append(rlrt.attn_args(arena, step.layout, table, w.table_stride, B, QH, KVH, rlrt.DTYPE_BF16,
+                                            ctx, MAX_CTX, q, out))
+            self.app.append(rlrt.AppendArgs(arena_base=arena.ptr, arena_bytes=arena.nbytes, layout=step.layout,
+                                            block_table=table.ptr, table_stride=w.table_stride, batch=B,
+                                            kv_heads=KVH, positions=pos.ptr, cow_src=None, k_new=step.knew.ptr,
+                                            v_new=step.vnew.ptr))
+        self.tok = [rlrt.DeviceBuffer(B * 4) for _ in range(MICRO_BATCHES)]
+        self.lp = [rlrt.DeviceBuffer(B * 4) for _ in range(MICRO_BATCHES)]
+        self.samp = [rlrt.sample_args(step.logits[m], B, VOCAB, VOCAB, self.tok[m], self.lp[m], temperature=TEMP,
+                                      top_k=TOPK, top_p=TOPP, seeds=step.seeds) for m in range(MICRO_BATCHES)]
+        self.ws = [rlrt.decode_sample_step_workspace(self.attn[m], self.samp[m]) for m in range(MICRO_BATCHES)]
+        self.t = 0
+        rlrt.sync()
+
+    def launch(self, n, on_lanes):
+        """Steps self.t .. self.t + n - 1, each merging step t - 2."""
+        for _ in range(n):
+            t, m = self.t, self.t % MICRO_BATCHES
+            s = self.samp[m]
+            s.step = t
+            prev = ()
+            if t >= 2:
+                pm = (t - 2) % MICRO_BATCHES
+                prev = (self.attn[pm], self.app[pm], self.ws[pm])
+            if on_lanes:
+                rlrt.decode_lane_step(t % 2, self.attn[m], s, self.ws[m], *prev)
+            else:
+                rlrt.decode_pipeline_step(self.attn[m], s, self.ws[m], *prev)
+            self.t += 1
+
+    def flush(self, on_lanes):
+        """Merges and appends the last two steps; the next step starts a new pipeline."""
+        for t in range(max(self.t - 2, 0), self.t):
+            m = t % MICRO_BATCHES
+            if on_lanes:
+                rlrt.decode_lane_flush(t % 2, self.attn[m], self.app[m], self.ws[m])
+            else:
+                rlrt.decode_pipeline_flush(self.attn[m], self.app[m], self.ws[m])
+        if on_lanes:
+            rlrt.lanes_join()
+        rlrt.sync()
+        self.t = 0
+
+    def timed(self, k, warmup, on_lanes):
+        """ms for k steps after `warmup` steps of the same pipeline: the timed
+        steps merge the two steps before them, the flush after is not timed."""
+        timer = rlrt.Timer()
+        if on_lanes:
+            rlrt.lanes_fork()
+        self.launch(warmup, on_lanes)
+        if on_lanes:
+            rlrt.lanes_join()
+        timer.begin()
+        if on_lanes:
+            rlrt.lanes_fork()
+        t0 = time.perf_counter()
+        self.launch(k, on_lanes)
+        if on_lanes:
+            rlrt.lanes_join()
+        ms = timer.end()
+        wall = (time.perf_counter() - t0) * 1e3
+        self.flush(on_lanes)
+        return ms, wall
 
 
 def time_loop(step, k, only):
@@ -262,11 +369,7 @@ def _host_info(threads):
     """nproc, OpenMP threads, CPU model and NUMA nodes of this host."""
     import glob
 
-    try:
-        nproc = len(os.sched_getaffinity(0))
-    except OSError:
-        nproc = os.cpu_count()
-    return {"nproc": nproc, "omp_threads": threads, "cpu_model": _cpu_model(),
+    return {"nproc": NPROC, "omp_threads": threads, "cpu_model": _cpu_model(),
             "numa_nodes": len(glob.glob("/sys/devices/system/node/node[0-9]*")) or 1,
             "omp_env": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")}}
 
@@ -297,7 +400,7 @@ def _pmc_pass(counter, tmp):
 
 
 def measure_traffic():
-    """HBM bytes per attention call from FETCH_SIZE and WRITE_SIZE (KiB per
+    """HBM bytes per pipeline step from FETCH_SIZE and WRITE_SIZE (KiB per
     dispatch), each scaled by what the counter reads for a device copy of
     256 MiB (read 256 MiB, write 256 MiB) run in the same pass. The runtime
     may split one copy into several blit dispatches, so both the calls and
@@ -322,12 +425,12 @@ def measure_traffic():
 
     copy_kib = PMC_COPY_BYTES / 1024.0
     cf, cw = pick(fetch, "copyBuffer"), pick(write, "copyBuffer")
-    af, aw = pick(fetch, "attn_decode_kernel"), pick(write, "attn_decode_kernel")
-    mf, mw = pick(fetch, "attn_merge_kernel") or 0.0, pick(write, "attn_merge_kernel") or 0.0
+    af, aw = pick(fetch, "decode_fused_kernel"), pick(write, "decode_fused_kernel")
+    mf, mw = pick(fetch, "merge_pieces_kernel") or 0.0, pick(write, "merge_pieces_kernel") or 0.0
     if not (cf and cw and af is not None and aw is not None):
         return None, f"kernels missing from the counter output: {sorted(fetch)}"
     cf, cw = cf / PMC_CALLS, cw / PMC_CALLS                     # per 256 MiB copy
-    af, aw = (af + mf) / PMC_CALLS, (aw + mw) / PMC_CALLS       # per attention call (both kernels)
+    af, aw = (af + mf) / PMC_CALLS, (aw + mw) / PMC_CALLS       # per pipeline step
     kf, kw = copy_kib / cf, copy_kib / cw
     total = (af * kf + aw * kw) * 1024.0
     return {"bytes": total, "fetch_kib": af, "write_kib": aw, "fetch_scale": kf, "write_scale": kw,
@@ -335,12 +438,14 @@ def measure_traffic():
 
 
 def pmc_target():
-    """What the counter passes profile: 3 attention calls and 3 device copies
-    of 256 MiB (the calibration kernel)."""
+    """What the counter passes profile: PMC_CALLS steps of the pipeline on
+    the library stream and its flush (the merges of the first two steps run
+    in the flush's kernels instead of a later step's), then PMC_CALLS device
+    copies of 256 MiB (the calibration kernel)."""
     rlrt.open_device(0)
-    step = Step()
-    for i in range(PMC_CALLS):
-        rlrt.attn_decode(step.attn)
+    pipe = Pipeline(Step())
+    pipe.launch(PMC_CALLS, False)
+    pipe.flush(False)
     n = PMC_COPY_BYTES
     a, b = rlrt.DeviceBuffer(n), rlrt.DeviceBuffer(n)
     rlrt.check(rlrt.lib().rl_hip_memset_d(a.ptr, 1, n), "memset")
@@ -1045,7 +1150,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="step", choices=["step", "attn", "sample", "append", "copy", "pmc"])
+    ap.add_argument("--only", default="step",
+                    choices=["step", "pipeline", "unfused", "attn", "sample", "append", "copy", "pmc"],
+                    help="step: the headline JSON line; pipeline: only the lane and one-stream pipeline passes; "
+                         "unfused: rl_hip_decode_step + rl_hip_sample; attn/sample/append: one entry point alone")
     ap.add_argument("--workload", default="step", choices=["step"] + sorted(WORKLOADS),
                     help="step: the headline decode step; the others print one JSON line of their own")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1095,33 +1203,48 @@ def main():
     step.attn.grid_waves = args.grid_waves
     if args.grid_waves:
         step.attn_ws = rlrt.attn_workspace(step.attn)
+    attn_bytes = step.attn_bytes()
+    step_bytes = attn_bytes + step.sample_bytes() + step.append_bytes()
 
-    for i in range(args.warmup):
-        step.run(i, args.only)
-    rlrt.sync()
-
-    ms, wall = time_loop(step, args.steps, args.only)
-    ms_step = ms / args.steps
-    log(f"[bench] {args.only}: {args.steps} steps in {ms:.2f} ms (events), {wall:.2f} ms (host wall)")
-
-    if args.only != "step":
-        per = {"attn": step.attn_bytes(), "sample": step.sample_bytes(), "append": step.append_bytes()}[args.only]
+    if args.only not in ("step", "pipeline"):
+        for i in range(args.warmup):
+            step.run(i, args.only)
+        rlrt.sync()
+        ms, wall = time_loop(step, args.steps, args.only)
+        ms_step = ms / args.steps
+        log(f"[bench] {args.only}: {args.steps} steps in {ms:.2f} ms (events), {wall:.2f} ms (host wall)")
+        per = {"attn": attn_bytes, "sample": step.sample_bytes(), "append": step.append_bytes(),
+               "unfused": step_bytes}[args.only]
         print(json.dumps({"only": args.only, "avg_launch_us": ms_step * 1e3,
                           "alg_gbps": per / (ms_step * 1e-3) / 1e9, "alg_bytes": per}), flush=True)
         return
 
-    # per-kernel averages (each over its own back-to-back launches, HIP events)
+    # the headline: the pipeline on the two lanes, then the same launches on
+    # the library stream alone (back to back: the fused kernel's own rate)
+    pipe = Pipeline(step)
+    ms, wall = pipe.timed(args.steps, args.warmup, True)
+    ms_one, _ = pipe.timed(args.steps, args.warmup, False)
+    ms_step, one_us = ms / args.steps, ms_one / args.steps * 1e3
+    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
+    achieved = step_bytes / (one_us * 1e-6) / 1e9
+    log(f"[bench] lanes: {args.steps} steps in {ms:.2f} ms (events), {wall:.2f} ms (host wall): "
+        f"{ms_step * 1e3:.1f} us/step ({step_gbps:.0f} GB/s); one stream {one_us:.1f} us/step ({achieved:.0f} GB/s)")
+    if args.only == "pipeline":
+        print(json.dumps({"only": "pipeline", "lanes_us_per_step": ms_step * 1e3, "one_stream_us_per_step": one_us,
+                          "alg_bytes": step_bytes}), flush=True)
+        return
+
+    # the unfused step of the same micro-batch and its kernels, each over its
+    # own back-to-back launches (HIP events on the library stream)
     kern = {}
-    for k in ("attn", "sample", "append"):
+    for k in ("unfused", "attn", "sample", "append"):
+        for i in range(args.warmup):
+            step.run(i, k)
         kms, _ = time_loop(step, args.steps, k)
         kern[k] = kms / args.steps * 1e3
-    attn_bytes = step.attn_bytes()
-    achieved = attn_bytes / (kern["attn"] * 1e-6) / 1e9
-    step_bytes = attn_bytes + step.sample_bytes() + step.append_bytes()
-    step_gbps = step_bytes / (ms_step * 1e-3) / 1e9
     copy_gbps = stream_copy_gbps()
-    log(f"[bench] attn {kern['attn']:.1f} us ({achieved:.0f} GB/s), sample {kern['sample']:.1f} us, "
-        f"append {kern['append']:.1f} us, stream copy {copy_gbps:.0f} GB/s")
+    log(f"[bench] unfused step {kern['unfused']:.1f} us: attn {kern['attn']:.1f} us, sample {kern['sample']:.1f} us, "
+        f"append {kern['append']:.1f} us; stream copy {copy_gbps:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -1143,20 +1266,30 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded numpy N(0,1) bf16 K/V and queries, fp32 logits N(0,1) with 5 spikes/row",
         "config": {"workload": "gqa_decode_b64_q32kv8_d128_ctx512-4096 + sample_b64_v128256_t0.8_k50_p0.9 + "
-                               "kv_append_b64",
+                               "kv_append_b64, 4 micro-batches on 2 lanes",
                    "batch": B, "q_heads": QH, "kv_heads": KVH, "head_dim": D, "block_tokens": TPB,
                    "ctx": f"U[{CTX_LO},{CTX_HI}] seed {SEED_KV}: mean {ctx.mean():.0f}, sum {int(ctx.sum())}",
-                   "vocab": VOCAB, "temperature": TEMP, "top_k": TOPK, "top_p": TOPP},
+                   "vocab": VOCAB, "temperature": TEMP, "top_k": TOPK, "top_p": TOPP,
+                   "micro_batches": MICRO_BATCHES, "rollouts_in_flight": MICRO_BATCHES * B, "lanes": 2,
+                   "step": "one launch per step: micro-batch t % 4's attention tiles and the sampling of its "
+                           "logits; its sampling waves first merge step t - 2's split rows and append that "
+                           "step's K/V token; steps alternate between two streams"},
         "steps_per_s": 1e3 / ms_step,
         "step_alg_bytes": step_bytes,
         "step_hbm_gbps": step_gbps,
         "step_hbm_frac": step_gbps / PEAK_HBM_GBPS,
+        "one_stream_us_per_step": one_us,
+        "unfused_us_per_step": kern["unfused"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBPS,
                      "traffic": traffic["bytes"] if traffic else None,
                      "traffic_detail": traffic if traffic else traffic_note,
-                     "kernel": "attn_decode_kernel<128,4,bf16,16> + attn_merge_kernel (one call)",
-                     "alg_bytes_per_launch": attn_bytes, "avg_launch_us": kern["attn"]},
+                     "kernel": "decode_fused_kernel<128,4,bf16,16> (one launch per step, with the merge of "
+                               "step t - 2)",
+                     "alg_bytes_per_launch": step_bytes, "avg_launch_us": one_us,
+                     "avg_launch_note": "launches back to back on one stream (HIP events over the timed "
+                                        "steps / steps); on the two lanes launches overlap, so their rate is "
+                                        "the headline step_hbm_gbps instead"},
         "kernels_us": kern,
         "stream_copy_gbps": copy_gbps,
         "device": {"arch": info.arch.decode(), "cu": info.cu_count, "clock_mhz": info.clock_khz / 1e3},

@@ -219,11 +219,11 @@ def test_stream_kernel_mixed_rows(rl, gpu, orc, olib, rows, vocab, stride):
 
 
 def test_greedy_long_rows_repeated_calls(rl, gpu, orc, olib):
-    """Greedy batches of rows above 32,768 logits take one kernel whose
-    last-arriving slice per row combines the row and resets the row's arrival
-    counter: calls of different shapes back to back (more and fewer rows and
-    slices than the call before) must each match the oracle, ties to the
-    lowest index and all -inf rows included."""
+    """Greedy batches of rows above 32,768 logits take the split kernel (each
+    slice's argmax into the workspace) and the merge kernel (the row's argmax
+    over its slices): calls of different shapes back to back (more and fewer
+    rows and slices than the call before) must each match the oracle, ties
+    to the lowest index and all -inf rows included."""
     rng = np.random.default_rng(515)
     for it, (rows, vocab, stride) in enumerate([(8, 128256, 128256), (3, 50001, 50004), (40, 40000, 40000),
                                                 (8, 128256, 128256), (1, 524288, 524288), (40, 40000, 40000)]):
