@@ -1036,8 +1036,9 @@ __device__ __forceinline__ TopkPick topk_pick(uint32_t nf, uint32_t k_eff, int h
 }
 
 // ---- one workgroup per row, the row streamed in chunks (rows with top-k) -----
-// Thread t's quad j of chunk c holds the logits from 32,768 c + (512 j + t) *
-// 4, so each load instruction reads 1 KiB of consecutive logits
+// Thread t's quad j of chunk c holds the logits from 2,048 Q c + (512 j + t)
+// * 4 (Q quads per thread per chunk), so each wave's load instruction reads
+// 1 KiB of consecutive logits
 // and each thread's elements ascend in (c, j, e). Two register buffers of
 // kStreamQuads quads alternate: the next chunk's loads are in flight while the
 // current chunk is processed, so the vector-ALU work overlaps the stream, and
@@ -1065,8 +1066,15 @@ __device__ __forceinline__ TopkPick topk_pick(uint32_t nf, uint32_t k_eff, int h
 // with the merge kernel. A list overflow, a NaN sum, a kept set beyond
 // kKeptCap and rows without top-k take the exact whole-row path. Greedy rows
 // keep the (value desc, index asc) argmax instead of candidates.
-constexpr int kStreamQuads = 16;                                          // quads per thread per chunk
-constexpr uint32_t kStreamRefreshQuads = 32;  // quads per thread over which the bound is raised (two 16-quad chunks)
+// Quads per thread per chunk: 16,384 logits (64 KiB) per chunk. At 256 rows of
+// 128,256 logits this streams a row ~2.5 us sooner than chunks of 16 quads
+// (the last chunk's processing, exposed after the stream, is half as long);
+// chunks of 4 quads, or three buffers in flight, were no faster.
+constexpr int kStreamQuads = 8;
+// Quads per thread over which the bound is raised (four 8-quad chunks). A
+// bound raised over 16 quads only lets so many candidates through that the
+// lists overflow into the exact path.
+constexpr uint32_t kStreamRefreshQuads = 32;
 constexpr uint32_t kStreamList = 8;                                       // list entries per thread
 // Long rows (above 32,768 logits) take the stream kernel from this many rows
 // on: at 128,256 logits, 144 rows (9/16 of the 256 compute units) is where
@@ -1331,7 +1339,7 @@ __device__ __forceinline__ void stream_sample_row(const SampleParams &p, uint32_
     const uint32_t tid = threadIdx.x;
     RowScratch &rs = *reinterpret_cast<RowScratch *>(L.s_cand);
 
-    constexpr uint32_t chunk = (uint32_t)kMergeThreads * 4u * Q;  // 32,768 logits at Q = 16
+    constexpr uint32_t chunk = (uint32_t)kMergeThreads * 4u * Q;  // 16,384 logits at Q = 8
     const uint32_t V = p.vocab;
     const StreamOut so = stream_row<Q>(p, row, 0u, (V + chunk - 1) / chunk, true, L.s_list, L.s_bound);
     const StreamTotals tt = stream_totals(so, L.s_wm, L.s_wz, L.s_wv, L.s_wi, L.s_wflag, L.s_wb);
