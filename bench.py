@@ -1139,10 +1139,178 @@ def wl_pipeline_trace(args):
             "clock": {"ns_per_tick": m.ns_per_tick, "rtt_ns": [c0[2], c1[2]]}, "latency_ns": pairs}
 
 
+def _lat_stats(samples, m, n):
+    """Latencies in ns of the first n lock-step samples under clock map m."""
+    sub = np.array([s.submit_ns for s in samples[:n]], np.float64)
+    con = np.array([s.consume_tick for s in samples[:n]], np.float64)
+    com = np.array([s.complete_tick for s in samples[:n]], np.float64)
+    pol = np.array([s.poll_ns for s in samples[:n]], np.float64)
+    to_ns = lambda t: m.offset_ns + t * m.ns_per_tick
+
+    def pct(x):
+        return {"p50": float(np.percentile(x, 50)), "p99": float(np.percentile(x, 99)), "min": float(x.min()),
+                "mean": float(x.mean())}
+
+    return {"n": int(n), "submit_to_consume_ns": pct(to_ns(con) - sub), "complete_to_poll_ns": pct(pol - to_ns(com)),
+            "round_trip_ns": pct(pol - sub), "device_consume_to_complete_ns": pct((com - con) * m.ns_per_tick)}
+
+
+def _lat_run(L, launch, drive, pairs, n):
+    """Clock samples, workers launched, a warm-up of 2 descriptors per pair,
+    n lock-step samples, workers stopped, clock samples again."""
+    import ctypes as C
+
+    def clock():
+        t, h, r = C.c_uint64(), C.c_double(), C.c_uint64()
+        rlrt.check(L.rl_hip_trace_clock_sample(64, C.byref(t), C.byref(h), C.byref(r)), "clock sample")
+        return t.value, h.value, r.value
+
+    c0 = clock()
+    stop = launch()
+    try:
+        warm = (rlrt.RingLockstepSample * (2 * pairs))()
+        if drive(2 * pairs, warm, 0, 10**10) != 2 * pairs:
+            raise rlrt.RlrtError("latency warm-up: a completion did not arrive")
+        out = (rlrt.RingLockstepSample * n)()
+        got = drive(n, out, 2 * pairs, 10**9)
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rlrt.sync()
+    c1 = clock()
+    if got != n:
+        raise rlrt.RlrtError(f"latency: {got} of {n} lock-step samples")
+    m = rlrt.TraceClockMap()
+    L.trace_clock_fit(c0[0], c0[1], c1[0], c1[1], C.byref(m))
+    res = _lat_stats(out, m, n)
+    res["clock"] = {"ns_per_tick": m.ns_per_tick, "rtt_ns": [c0[2], c1[2]],
+                    "split_error_ns_at_most": max(c0[2], c1[2]) / 2}
+    return res
+
+
+def wl_latency(args):
+    """Unloaded latency across the ring boundary from device stamps, for the
+    hw_desc worker and the command-ring worker at 1 pair and at one pair per
+    compute unit: descriptor i goes to pair i % pairs only after the previous
+    one's completion was polled (native lock-step driver, ring_latency.h), so
+    every ring holds at most one descriptor while the other workers poll
+    empty rings. submit -> consume: host CLOCK_MONOTONIC just before the
+    command tail's release to the worker's s_memrealtime when its poll saw
+    it; complete -> poll: the worker's stamp just before the completion
+    tail's release to the host's poll seeing it. GPU ticks map to host ns by
+    ping-pong clock samples before and after (the split between the two
+    halves is good to half the best sample's round trip; their sum, the round
+    trip, needs no map). hw_desc descriptors have seq_len = max_tokens (no
+    decode step: a pure ring round trip); command-ring descriptors run the
+    fixed128 step (one head, 32 tokens). The reference's targets (H100,
+    docs/metrics.md:70-72): worker poll latency < 100 ns, completion
+    notification < 200 ns."""
+    import ctypes as C
+
+    L = rlrt.lib()
+    info = rlrt.DeviceInfo()
+    rlrt.check(L.rl_hip_device_info(C.byref(info)), "rl_hip_device_info")
+    G = int(info.cu_count)
+
+    def coherent(n):
+        p = L.rl_hip_host_alloc_coherent(n)
+        if not p:
+            raise rlrt.RlrtError("coherent host allocation failed")
+        return p
+
+    res = {"workload": "ring_latency_unloaded", "pairs": [1, G]}
+    # ---- hw_desc worker: one rollout, MHA 8 x d64 fp16 (no step is run)
+    w = synth.make_decode(1201, 1, 8, 8, 64, 16, 16, dtype="fp16", kv_std=0.5, reserve_tokens=32)
+    bufs = [rlrt.DeviceBuffer.from_array(x) for x in (w.arena, w.table)]
+    small = [rlrt.DeviceBuffer(1 << 16, zero=True) for _ in range(6)]
+    for pairs in (1, G):
+        cqs = [L.hw_ring_create() for _ in range(pairs)]
+        dqs = [L.hw_ring_create() for _ in range(pairs)]
+        rings, stop, stamps = coherent(16 * pairs), coherent(64), coherent(16 * pairs)
+        for g in range(pairs):
+            C.cast(rings, C.POINTER(C.c_void_p))[g] = cqs[g]
+            C.cast(rings, C.POINTER(C.c_void_p))[pairs + g] = dqs[g]
+        stats = rlrt.DeviceBuffer(pairs * 32, zero=True)
+        a = rlrt.HwWorkerArgs(cmdq=rings, doneq=rings + 8 * pairs, groups=pairs, stop=stop, max_idle_polls=1 << 26,
+                              arena_base=bufs[0].ptr, arena_bytes=bufs[0].nbytes,
+                              layout=rlrt.KvLayoutDesc.paged(16, 64), block_table=bufs[1].ptr,
+                              table_stride=w.table_stride, rollouts=1, q_heads=8, kv_heads=8, dtype=rlrt.DTYPE_FP16,
+                              scale=0.0, max_steps=1, q=small[0].ptr, k_new=small[1].ptr, v_new=small[2].ptr,
+                              logits=small[3].ptr, vocab=16, attn_out=small[4].ptr, token_out=small[5].ptr,
+                              logprob_out=small[5].ptr, stats=stats.ptr, stamps=stamps)
+        ws = rlrt.hw_worker_workspace(a)
+        desc = rlrt.HwDesc(opcode=1, rollout_id=0, seq_len=16, max_tokens=16)
+
+        def launch(a=a, stop=stop):
+            C.cast(stop, C.POINTER(C.c_uint32))[0] = 0
+            rlrt.hw_worker_launch(a)
+            return stop
+
+        def drive(n, out, first, timeout, rings=rings, pairs=pairs, stamps=stamps, desc=desc):
+            return L.ring_lockstep_hw(rings, rings + 8 * pairs, pairs, C.byref(desc), n, stamps, timeout, out)
+
+        log(f"[bench] latency: hw_desc worker, {pairs} pair(s)")
+        res[f"hw_desc_{pairs}pairs"] = _lat_run(L, launch, drive, pairs, max(2000, 8 * pairs))
+        st = stats.download(np.uint64, (pairs, 4))
+        res[f"hw_desc_{pairs}pairs"]["worker_status"] = np.unique(st[:, 3]).tolist()
+        for r in cqs + dqs:
+            L.hw_ring_destroy(r)
+        for p in (rings, stop, stamps):
+            L.rl_hip_host_free(p)
+        stats.close()
+        ws.close()
+    for b in bufs + small:
+        b.close()
+    # ---- command-ring worker: fixed128 step per descriptor
+    nblk, io = 64, 64
+    rng = np.random.default_rng(1202)
+    darena = rlrt.DeviceBuffer.from_array(synth.f32_to_f16(rng.standard_normal(nblk * 8192, dtype=np.float32)))
+    dq = rlrt.DeviceBuffer.from_array(synth.f32_to_f16(rng.standard_normal((io, 128), dtype=np.float32)))
+    do = rlrt.DeviceBuffer(io * 128 * 4)
+    for pairs in (1, G):
+        rs = [L.ring_create() for _ in range(pairs)]
+        crs = [L.comp_ring_create() for _ in range(pairs)]
+        tab, stop, stamps = coherent(16 * pairs), coherent(64), coherent(16 * pairs)
+        for g in range(pairs):
+            C.cast(tab, C.POINTER(C.c_void_p))[g] = rs[g]
+            C.cast(tab, C.POINTER(C.c_void_p))[pairs + g] = crs[g]
+        stats = rlrt.DeviceBuffer(pairs * 32, zero=True)
+        a = rlrt.CmdWorkerArgs(rings=tab, comp_rings=tab + 8 * pairs, groups=pairs, stop=stop,
+                               max_idle_polls=1 << 26, arena_base=darena.ptr, arena_bytes=darena.nbytes,
+                               sample_state=None, q_buffer=dq.ptr, o_buffer=do.ptr, io_slots=io, stats=stats.ptr,
+                               stamps=stamps)
+        desc = rlrt.Descriptor(seq_id=0, kv_block_offset=0, num_kv_blocks=32, output_token_offset=0,
+                               reward_cookie=0)
+
+        def launch(a=a, stop=stop):
+            C.cast(stop, C.POINTER(C.c_uint32))[0] = 0
+            rlrt.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
+            return stop
+
+        def drive(n, out, first, timeout, tab=tab, pairs=pairs, stamps=stamps, desc=desc):
+            return L.ring_lockstep_cmd(tab, tab + 8 * pairs, pairs, C.byref(desc), first, n, stamps, timeout, out)
+
+        log(f"[bench] latency: command-ring worker, {pairs} pair(s)")
+        res[f"cmd_{pairs}pairs"] = _lat_run(L, launch, drive, pairs, max(2000, 8 * pairs))
+        st = stats.download(np.uint64, (pairs, 4))
+        res[f"cmd_{pairs}pairs"]["worker_status"] = np.unique(st[:, 3]).tolist()
+        for r in rs:
+            L.ring_destroy(r)
+        for r in crs:
+            L.comp_ring_destroy(r)
+        for p in (tab, stop, stamps):
+            L.rl_hip_host_free(p)
+        stats.close()
+    for b in (darena, dq, do):
+        b.close()
+    res["reference_targets_ns"] = {"worker_poll_latency": 100, "completion_notification": 200,
+                                   "source": "docs/metrics.md:70-72 (H100 targets; context only)"}
+    return res
+
+
 WORKLOADS = {"sample256": wl_sample256, "sample32k": wl_sample32k, "longctx": wl_longctx, "proj": wl_proj,
              "plumbing": wl_plumbing, "plumbing256": wl_plumbing256, "ringstep": wl_ringstep,
              "rollout": wl_rollout, "cmdring": wl_cmdring, "rollout_pipeline": wl_rollout_pipeline,
-             "pipeline": wl_pipeline, "pipeline_trace": wl_pipeline_trace}
+             "pipeline": wl_pipeline, "pipeline_trace": wl_pipeline_trace, "latency": wl_latency}
 
 
 def main():

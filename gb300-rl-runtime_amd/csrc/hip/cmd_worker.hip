@@ -10,7 +10,10 @@
 // contract of ring.h / completion.h holds on the device side:
 //
 //  poll    lane 0 of wave 0 reads the producer's tail with system-scope loads
-//          (the stop flag only while the ring is empty); after the acquire the
+//          (the stop flag only while the ring is empty, on every 16th empty
+//          poll: each idle worker's loads cross PCIe, and with one worker per
+//          compute unit a stop read on every poll slowed the busy ring's
+//          round trip from 8.4 to 44 us); after the acquire the
 //          whole window of descriptors already committed - up to 32, the
 //          decode_batch window (src/decode_batch.c:3-51) - is read with one
 //          16-byte load per lane, and the head is released once. The tail
@@ -43,6 +46,10 @@
 //          completion before the tail release - stamped with s_memrealtime
 //          (100 MHz) and keyed {low 32 bits of seq_id, output_token_offset};
 //          one 32-bit word per lane, then a release store of the ring head.
+//  stamps  optional: lane 0 of wave 0 writes s_memrealtime when a poll finds
+//          a new tail and just before a window's completions are released,
+//          to stamps[g][0] and [1] in coherent host memory, for the host's
+//          unloaded-latency measurement.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -81,6 +88,7 @@ struct CmdParams {
     uint32_t io_mask;
     uint64_t *stats;
     TraceRing *trace;
+    uint64_t *stamps;  // coherent host [groups][2] or nullptr
 };
 
 __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
@@ -290,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                     avail = sys_load(&ring->prod.tail) - head;
                     if (avail != 0)
                         break;
-                    if (sys_load(p.stop) != 0) {
+                    if ((idle & 15) == 15 && sys_load(p.stop) != 0) {
                         ctl = 1;
                         break;
                     }
@@ -301,6 +309,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                     }
                     __builtin_amdgcn_s_sleep(8);
                 }
+                if (avail != 0 && p.stamps)
+                    p.stamps[(size_t)blockIdx.x * 2] = __builtin_amdgcn_s_memrealtime();
             }
             avail = rl_wave_bcast_u32(avail, 0);
             ctl = rl_wave_bcast_u32(ctl, 0);
@@ -405,6 +415,8 @@ __global__ __launch_bounds__(kThreads) void cmd_worker_kernel(CmdParams p)
                 }
                 if (lane == 0) {
                     ctail += n;
+                    if (p.stamps)
+                        p.stamps[(size_t)blockIdx.x * 2 + 1] = __builtin_amdgcn_s_memrealtime();
                     sys_store_release(&cr->prod.tail, ctail);
                 }
             } else {
@@ -484,6 +496,7 @@ extern "C" int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *a)
     p.io_mask = a->io_slots ? a->io_slots - 1 : 0;
     p.stats = a->stats;
     p.trace = a->trace;
+    p.stamps = a->stamps;
     hipLaunchKernelGGL(cmd_worker_kernel, dim3(a->groups), dim3(kThreads), 0, rl_stream(), p);
     return rl_check_launch("cmd_worker_kernel launch");
 }

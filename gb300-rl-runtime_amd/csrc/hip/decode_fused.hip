@@ -482,9 +482,19 @@ bool fused_eligible(const rl_attn_decode_args_t *a)
 int fused_validate(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                    const rl_sample_args_t *samp, const char *who)
 {
-    if (rl_require_open(who) || rl_decode_step_check(attn, append, who) || rl_sample_check(samp))
+    if (rl_require_open(who) || rl_sample_check(samp))
         return -1;
-    return 0;
+    return append ? rl_decode_step_check(attn, append, who) : rl_attn_check(attn);
+}
+
+// The append of a step, or none (arena NULL: the kernels skip it).
+AppendParams append_or_none(const rl_kv_append_args_t *append)
+{
+    if (append)
+        return append_params(append);
+    AppendParams ap = {};
+    ap.arena = nullptr;
+    return ap;
 }
 
 }  // namespace
@@ -571,12 +581,15 @@ extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, cons
         return -1;
     }
     if (!fused_eligible(attn)) {
-        // one decode step, then the sampling, on the library stream
+        // one decode step (or the attention alone), then the sampling, on
+        // the library stream. (Running the sampler on a second stream beside
+        // the attention or its merge made the step slower: the cross-stream
+        // event waits cost more than the overlap saved.)
         const size_t a_bytes = (rl_hip_attn_decode_workspace(attn) + 255) / 256 * 256;
         rl_attn_decode_args_t a = *attn;
         a.workspace = workspace;
         a.workspace_bytes = a_bytes;
-        if (rl_hip_decode_step(&a, append))
+        if (append ? rl_hip_decode_step(&a, append) : rl_hip_attn_decode(&a))
             return -1;
         rl_sample_args_t s = *samp;
         s.workspace = (uint8_t *)workspace + a_bytes;
@@ -584,7 +597,7 @@ extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, cons
         return rl_hip_sample(&s);
     }
     const FusedParams f = fused_params_of(attn, samp, workspace, 0);
-    return launch_shape(kRunFused | kRunMerge, attn, f, append_params(append), rl_stream());
+    return launch_shape(kRunFused | kRunMerge, attn, f, append_or_none(append), rl_stream());
 }
 
 namespace {

@@ -8,8 +8,12 @@
 // contract of hw_ring.h holds on the device side too:
 //
 //  poll    thread 0 reads the producer's tail with system-scope loads
-//          (s_sleep between empty polls), acquires, copies the 64-byte
-//          descriptor and release-stores head + 1.
+//          (s_sleep between empty polls, the host's stop flag on every 16th
+//          of them), acquires, copies the 64-byte descriptor and
+//          release-stores head + 1. Every load of an idle worker crosses
+//          PCIe: with one worker per compute unit, reading the stop flag on
+//          every poll as well loaded the link enough to slow the one busy
+//          ring's round trip from 6.7 to 39 us.
 //  decode  for DECODE, the control rule of hw_worker_sim - while seq_len <
 //          max_tokens: one decode step, seq_len++, stop at max_tokens (DONE)
 //          or at a multiple of 32 (NEEDS_REWARD) - with a real step for every
@@ -19,6 +23,11 @@
 //          logits, and the append of the step's K/V token at position seq_len.
 //  publish thread 0 writes the updated descriptor into the completion ring
 //          and release-stores tail + 1 at system scope.
+//  stamps  optional: thread 0 writes the GPU's 100 MHz clock (s_memrealtime)
+//          when a poll first sees a new descriptor and just before the
+//          completion's tail is released, to stamps[g][0] and [1] in
+//          coherent host memory (the release orders both before the tail),
+//          for the host's unloaded-latency measurement.
 //  exit    on STOP (no completion, like the simulator), when the host sets
 //          *stop, or - so that no wave can spin forever - after
 //          max_idle_polls consecutive empty polls or a completion ring that
@@ -67,6 +76,7 @@ struct WorkerParams {
     float *logprob_out;
     uint64_t *stats;
     float *part;  // [groups][kWorkerWavesMax + kv_heads][G * D + 2 * G]
+    uint64_t *stamps;  // coherent host [groups][2] or nullptr
 };
 
 __device__ __forceinline__ uint32_t sys_load(const volatile uint32_t *p)
@@ -261,7 +271,7 @@ __global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerPara
     for (;;) {
         // ---- next descriptor (wave 0), bounded wait -------------------------
         // Lane 0 polls the producer's tail (the stop flag only while the ring
-        // is empty); after the acquire, lanes 0-15 read the 16 dwords of the
+        // is empty, on every 16th empty poll); after the acquire, lanes 0-15 read the 16 dwords of the
         // descriptor in one load instruction, then lane 0 releases the slot.
         if (wave == 0) {
             uint32_t ctl = 0, got = 0;
@@ -270,9 +280,11 @@ __global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerPara
                 for (;;) {
                     if (sys_load(&cq->tail) != head) {
                         got = 1;
+                        if (wp.stamps)
+                            wp.stamps[(size_t)grp * 2] = __builtin_amdgcn_s_memrealtime();
                         break;
                     }
-                    if (sys_load(wp.stop) != 0) {
+                    if ((idle & 15) == 15 && sys_load(wp.stop) != 0) {
                         ctl = 1;
                         break;
                     }
@@ -480,6 +492,8 @@ __global__ __launch_bounds__(kWorkerThreadsMax) void hw_worker_kernel(WorkerPara
                     ((volatile uint32_t *)&dq->desc[t & HW_RING_MASK])[lane] = s_out[lane];
                 if (lane == 0) {
                     dtail++;
+                    if (wp.stamps)
+                        wp.stamps[(size_t)grp * 2 + 1] = __builtin_amdgcn_s_memrealtime();
                     sys_store_release(&dq->tail, dtail);
                 }
                 ctl = 0;
@@ -643,6 +657,7 @@ extern "C" int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *a)
     wp.token_out = a->token_out;
     wp.logprob_out = a->logprob_out;
     wp.stats = a->stats;
+    wp.stamps = a->stamps;
     wp.part = (float *)a->workspace;
 
     const uint32_t G = a->q_heads / a->kv_heads;

@@ -162,6 +162,11 @@ class TraceClockMap(C.Structure):
     _fields_ = [("ns_per_tick", C.c_double), ("offset_ns", C.c_double)]
 
 
+class RingLockstepSample(C.Structure):
+    _fields_ = [("submit_ns", C.c_uint64), ("consume_tick", C.c_uint64), ("complete_tick", C.c_uint64),
+                ("poll_ns", C.c_uint64)]
+
+
 class KVPrefix(C.Structure):
     _pack_ = 1
     _fields_ = [("prefix_id", C.c_uint32), ("refcnt", C.c_uint32), ("kv_block_offset", C.c_int64),
@@ -262,7 +267,8 @@ class HwWorkerArgs(C.Structure):
                 ("dtype", C.c_uint32), ("scale", C.c_float), ("max_steps", C.c_uint32), ("q", C.c_void_p),
                 ("k_new", C.c_void_p), ("v_new", C.c_void_p), ("logits", C.c_void_p), ("vocab", C.c_uint32),
                 ("attn_out", C.c_void_p), ("token_out", C.c_void_p), ("logprob_out", C.c_void_p),
-                ("stats", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+                ("stats", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+                ("stamps", C.c_void_p)]
 
 
 class RingStepArgs(C.Structure):
@@ -283,7 +289,7 @@ class CmdWorkerArgs(C.Structure):
     _fields_ = [("rings", C.c_void_p), ("comp_rings", C.c_void_p), ("groups", C.c_uint32), ("stop", C.c_void_p),
                 ("max_idle_polls", C.c_uint64), ("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64),
                 ("sample_state", C.c_void_p), ("q_buffer", C.c_void_p), ("o_buffer", C.c_void_p),
-                ("io_slots", C.c_uint32), ("stats", C.c_void_p), ("trace", C.c_void_p)]
+                ("io_slots", C.c_uint32), ("stats", C.c_void_p), ("trace", C.c_void_p), ("stamps", C.c_void_p)]
 
 
 DTYPE_BF16 = 0
@@ -392,6 +398,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "trace_clock_fit": (i32, [u64, C.c_double, u64, C.c_double, C.POINTER(TraceClockMap)]),
         "trace_rebase": (None, [vp, C.POINTER(TraceClockMap)]), "trace_merge": (u64, [vp, vp, u32]),
         "rl_hip_trace_clock_sample": (i32, [u32, C.POINTER(u64), C.POINTER(C.c_double), C.POINTER(u64)]),
+        "ring_lockstep_hw": (u32, [vp, vp, u32, vp, u32, vp, u64, vp]),
+        "ring_lockstep_cmd": (u32, [vp, vp, u32, vp, u64, u32, vp, u64, vp]),
         "rl_hip_wave_broadcast_selftest": (i32, [vp, vp, vp]),
         "reward_score_mock": (C.c_float, [vp, u32]),
         "reward_match_count": (u32, [vp, vp, u32]),
@@ -693,11 +701,13 @@ def decode_sample_step_workspace(attn: AttnArgs, samp: SampleArgs) -> DeviceBuff
     return DeviceBuffer(decode_sample_step_workspace_bytes(attn, samp), zero=True)
 
 
-def decode_sample_step(attn: AttnArgs, append: AppendArgs, samp: SampleArgs, ws: DeviceBuffer) -> None:
-    """The decode step of one micro-batch (attention + KV append) and the
-    sampling of another micro-batch's logits in one launch (plus the merge)."""
-    check(lib().rl_hip_decode_sample_step(C.byref(attn), C.byref(append), C.byref(samp), ws.ptr, ws.nbytes),
-          "rl_hip_decode_sample_step")
+def decode_sample_step(attn: AttnArgs, append: AppendArgs | None, samp: SampleArgs, ws: DeviceBuffer) -> None:
+    """The decode step of one micro-batch (attention + KV append, or no append
+    when append is None) and the sampling of another micro-batch's logits in
+    one launch (plus the merge), or the two calls for shapes outside the
+    fused kernel."""
+    check(lib().rl_hip_decode_sample_step(C.byref(attn), C.byref(append) if append is not None else None,
+                                          C.byref(samp), ws.ptr, ws.nbytes), "rl_hip_decode_sample_step")
 
 
 def decode_pipeline_step(attn: AttnArgs, samp: SampleArgs, ws: DeviceBuffer, prev_attn: AttnArgs | None = None,

@@ -246,7 +246,10 @@ int rl_hip_rollout_schedule(const rl_rollout_sched_args_t *args);
  * empty polls (a full completion ring likewise). stats[g] = {decoded tokens,
  * completions, steps, status}; status 0 stopped, 1 idle limit, 2 inputs
  * exhausted or rollout id >= rollouts, 3 completion ring full, 4 appended
- * token outside the block table or arena. */
+ * token outside the block table or arena. With stamps set, worker g writes
+ * the GPU's 100 MHz clock (s_memrealtime ticks) to stamps[g][0] when a poll
+ * first sees a new descriptor and to stamps[g][1] just before it releases
+ * that descriptor's completion (ring_lockstep_hw in trace.h reads them). */
 typedef struct {
     hw_ring_t *const *cmdq;      /* device-readable [groups] */
     hw_ring_t *const *doneq;     /* device-readable [groups] */
@@ -275,6 +278,7 @@ typedef struct {
     uint64_t *stats;             /* device or coherent [groups][4] */
     void *workspace;             /* device, >= rl_hip_hw_worker_workspace() */
     size_t workspace_bytes;
+    uint64_t *stamps;            /* coherent host [groups][2] or NULL: see below */
 } rl_hw_worker_args_t;
 
 size_t rl_hip_hw_worker_workspace(const rl_hw_worker_args_t *args);
@@ -377,7 +381,10 @@ int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *args, uint32_t steps, ui
  * completion just before the completion tail is released, {tsc = the GPU's
  * 100 MHz s_memrealtime ticks, rollout_id = low 32 bits of seq_id, seq =
  * output_token_offset}; the ring head is release-stored after each batch of
- * records. */
+ * records. With stamps set, worker g writes the GPU's 100 MHz clock to
+ * stamps[g][0] when a poll first sees a new tail and to stamps[g][1] just
+ * before it releases a window's completions (ring_lockstep_cmd in trace.h
+ * reads them). */
 typedef struct {
     CommandRing *const *rings;          /* coherent host [groups] (ring_create after rl_hip_open) */
     CompletionRing *const *comp_rings;  /* coherent host [groups] (comp_ring_create) */
@@ -392,6 +399,7 @@ typedef struct {
     uint32_t io_slots;                  /* a power of two; 0 uses slot 0 */
     uint64_t *stats;                    /* device [groups][4] */
     TraceRing *trace;                   /* coherent host [groups] rings, or NULL (see below) */
+    uint64_t *stamps;                   /* coherent host [groups][2] or NULL (see below) */
 } rl_cmd_worker_args_t;
 
 int rl_hip_cmd_worker_launch(const rl_cmd_worker_args_t *args);
@@ -552,9 +560,11 @@ int rl_hip_decode_step(const rl_attn_decode_args_t *attn, const rl_kv_append_arg
  * of contexts, so repeated calls give the same bits), within 1e-4 of fp64
  * like rl_hip_attn_decode. The workspace (size from
  * rl_hip_decode_sample_step_workspace) holds the step's tile prefix and
- * partials; it needs no initialisation. Shapes whose tiles do not fit the
- * fused kernel's LDS (or batches above 1,024) run rl_hip_decode_step and
- * then rl_hip_sample on the same workspace, with exactly their results. */
+ * partials; it needs no initialisation. append may be NULL: the attention
+ * and the sampling without a KV append. Shapes whose tiles do not fit the
+ * fused kernel's LDS (GQA groups of 8 at head_dim 128, batches above 1,024)
+ * run rl_hip_decode_step (rl_hip_attn_decode without an append) and then
+ * rl_hip_sample on the same workspace, with exactly their results. */
 size_t rl_hip_decode_sample_step_workspace(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp);
 int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                               const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes);

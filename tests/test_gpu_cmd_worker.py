@@ -290,3 +290,58 @@ def test_launch_refuses_more_workers_than_resident(rl, gpu):
     a.groups = 0
     assert L.rl_hip_cmd_worker_launch(C.byref(a)) == -1
     dev.close()
+
+
+def test_stamps_lockstep(rl, gpu):
+    """Four workers with stamps set, 64 descriptors one at a time through
+    ring_lockstep_cmd: every completion carries its seq_id, each worker's
+    consume stamp precedes its completion stamp, successive samples' stamps
+    ascend on the device's common clock, the outputs are the fixed128 step's
+    (checked against fp64 like the other cases), and the workers end on the
+    stop flag with 16 descriptors each."""
+    L = rl.lib()
+    pairs, n, io = 4, 64, 64
+    rng = np.random.default_rng(4401)
+    arena16 = synth.f32_to_f16(rng.standard_normal(4 * BLOCK // 2, dtype=np.float32))
+    q = synth.f32_to_f16(rng.standard_normal((io, 128), dtype=np.float32))
+    darena, dq = rl.DeviceBuffer.from_array(arena16.view(np.uint8)), rl.DeviceBuffer.from_array(q)
+    do = rl.DeviceBuffer(io * 128 * 4, zero=True)
+    stats = rl.DeviceBuffer(pairs * 32, zero=True)
+    rs = [L.ring_create() for _ in range(pairs)]
+    crs = [L.comp_ring_create() for _ in range(pairs)]
+    tab = _coherent(rl, 16 * pairs)
+    for g in range(pairs):
+        C.cast(tab, C.POINTER(C.c_void_p))[g] = rs[g]
+        C.cast(tab, C.POINTER(C.c_void_p))[pairs + g] = crs[g]
+    stop, stamps = _coherent(rl, 64), _coherent(rl, 16 * pairs)
+    a = rl.CmdWorkerArgs(rings=tab, comp_rings=tab + 8 * pairs, groups=pairs, stop=stop, max_idle_polls=1 << 24,
+                         arena_base=darena.ptr, arena_bytes=darena.nbytes, sample_state=None, q_buffer=dq.ptr,
+                         o_buffer=do.ptr, io_slots=io, stats=stats.ptr, stamps=stamps)
+    out = (rl.RingLockstepSample * n)()
+    d = rl.Descriptor(kv_block_offset=2, num_kv_blocks=32, output_token_offset=5, reward_cookie=9)
+    print(f"[cmd] {pairs} workers with stamps, {n} lock-step descriptors", flush=True)
+    rl.check(L.rl_hip_cmd_worker_launch(C.byref(a)), "rl_hip_cmd_worker_launch")
+    try:
+        got = L.ring_lockstep_cmd(tab, tab + 8 * pairs, pairs, C.byref(d), 1000, n, stamps, 10**10, out)
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rl.sync()
+    st = stats.download(np.uint64, (pairs, 4))
+    o = do.download(np.float32, (io, 128))
+    assert got == n
+    assert (st[:, 0] == n // pairs).all() and (st[:, 3] == 0).all(), st
+    for i, s in enumerate(out):
+        assert s.consume_tick <= s.complete_tick and s.submit_ns < s.poll_ns, i
+        if i:
+            assert out[i - 1].complete_tick <= s.consume_tick, i
+    # every descriptor wrote slot 5 from block 2 and q slot 5
+    want = _ref_row(arena16, 2, 32, synth.f16_to_f32(q[5]))
+    assert np.abs(o[5] - want).max() < 1e-4
+    for b in (darena, dq, do, stats):
+        b.close()
+    for r in rs:
+        L.ring_destroy(r)
+    for r in crs:
+        L.comp_ring_destroy(r)
+    for p in (tab, stop, stamps):
+        L.rl_hip_host_free(p)

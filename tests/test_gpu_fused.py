@@ -12,7 +12,7 @@ Checked on every shape:
   * a second call on the same workspace gives the same bits (the pieces are
     cut at tile positions that depend only on the contexts).
 Shapes whose tiles do not fit the fused kernel run rl_hip_decode_step then
-rl_hip_sample: there the results equal those two calls bit for bit.
+rl_hip_sample: there the results equal those two calls bit for bit. Without an append (append NULL) the arena is unchanged.
 """
 import numpy as np
 import pytest
@@ -23,10 +23,11 @@ import synth
 pytestmark = pytest.mark.gpu
 
 
-def _run(rl, w, max_ctx, pos, cow, kn, vn, logits, repeats=2, **samp):
+def _run(rl, w, max_ctx, pos, cow, kn, vn, logits, repeats=2, append=True, **samp):
     """Uploads the decode workload and the logits, runs the fused step
-    `repeats` times on one workspace (re-uploading the arena each time), and
-    returns a list of (out16, out32, arena, tok, lp) per call."""
+    `repeats` times on one workspace (re-uploading the arena each time; with
+    append False the step has no KV append), and returns a list of (out16,
+    out32, arena, tok, lp) per call."""
     B, QH, D = w.batch, w.q_heads, w.head_dim
     layout = rl.KvLayoutDesc.paged(w.token_count, D)
     code = rl.DTYPE_BF16 if w.dtype == "bf16" else rl.DTYPE_FP16
@@ -64,7 +65,7 @@ def _run(rl, w, max_ctx, pos, cow, kn, vn, logits, repeats=2, **samp):
             bufs["arena"].upload(w.arena)
         print(f"[fused] call {i}: batch {B}, {QH}/{w.kv_heads} heads d{D} {w.dtype}, sampling {rows} x {V}",
               flush=True)
-        rl.decode_sample_step(a, ap, s, ws)
+        rl.decode_sample_step(a, ap if append else None, s, ws)
         rl.sync()
         res.append((out.download(np.uint16, (B, QH, D)), out32.download(np.float32, (B, QH, D)),
                     bufs["arena"].download(np.uint8, w.arena.size), tok.download(np.uint32, rows),
@@ -93,9 +94,10 @@ def _check(orc, olib, w, max_ctx, pos, cow, kn, vn, logits, res, want_tok, want_
         if (~empty).any():
             gh.check_attn(o16[ok][~empty], o32[ok][~empty], ref[~empty], w.dtype)
     want_arena = w.arena.copy()
-    olib.orc_kv_append(want_arena.ctypes.data, w.block_bytes, w.token_count, w.head_dim * 2, w.table.ctypes.data,
-                       w.table_stride, w.batch, w.kv_heads, pos.ctypes.data,
-                       cow.ctypes.data if cow is not None else None, kn.ctypes.data, vn.ctypes.data)
+    if pos is not None:  # None: a step without append
+        olib.orc_kv_append(want_arena.ctypes.data, w.block_bytes, w.token_count, w.head_dim * 2,
+                           w.table.ctypes.data, w.table_stride, w.batch, w.kv_heads, pos.ctypes.data,
+                           cow.ctypes.data if cow is not None else None, kn.ctypes.data, vn.ctypes.data)
     assert np.array_equal(arena, want_arena)
     bad = np.nonzero(tok != want_tok)[0]
     assert len(bad) == 0, (bad[:8], tok[bad[:8]], want_tok[bad[:8]])
@@ -431,3 +433,39 @@ def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
         assert np.abs(lanes["tok"][t][1] - wlp).max() < 1e-4, t
     for x in lgb + [seed_buf]:
         x.close()
+
+
+def test_fused_step_without_append(rl, gpu, orc, olib):
+    """append NULL: the fused kernel (GQA 32/8) and the two-call path (GQA
+    64/8, 8 rollouts of up to 3,000 tokens with greedy over 8 x 128,256, the
+    long-context step's sampler) leave the arena untouched, the attention is
+    within 1e-4 of fp64, a second call on the same workspace gives the same
+    bits and the tokens equal the oracle's; on the two-call path everything
+    equals rl_hip_attn_decode and rl_hip_sample bit for bit."""
+    rng = np.random.default_rng(8171)
+    w = synth.make_decode(8172, 48, 32, 8, 128, 1, 2500)
+    kn, vn = _kv_rows(rng, w)
+    logits = rng.standard_normal((48, 32000), dtype=np.float32)
+    res = _run(rl, w, int(w.ctx.max()), w.ctx.copy(), None, kn, vn, logits, append=False, temperature=0.7, top_k=40,
+               top_p=0.95, seed=11, step=5)
+    want, wlp = orc.sample_rows(olib, logits, False, 0.7, 40, 0.95, 11, 5)
+    _check(orc, olib, w, int(w.ctx.max()), None, None, kn, vn, logits, res, want, wlp)
+
+    V = 128256
+    w8 = synth.make_decode(8173, 8, 64, 8, 128, 1000, 3000)
+    kn8, vn8 = _kv_rows(rng, w8)
+    lg8 = rng.standard_normal((8, V), dtype=np.float32)
+    res8 = _run(rl, w8, int(w8.ctx.max()), w8.ctx.copy(), None, kn8, vn8, lg8, append=False, greedy=True)
+    want8, wlp8 = orc.sample_rows(olib, lg8, True, 1.0, 0, 1.0, 0, 0)
+    _check(orc, olib, w8, int(w8.ctx.max()), None, None, kn8, vn8, lg8, res8, want8, wlp8)
+    o16, o32 = gh.run_attn(rl, w8)
+    assert np.array_equal(res8[0][0], o16) and np.array_equal(res8[0][1], o32)
+    lg, tok, lp = rl.DeviceBuffer.from_array(lg8), rl.DeviceBuffer(8 * 4), rl.DeviceBuffer(8 * 4)
+    s = rl.sample_args(lg, 8, V, V, tok, lp, greedy=True)
+    sws = rl.sample_workspace(s)
+    rl.sample(s)
+    rl.sync()
+    assert np.array_equal(tok.download(np.uint32, 8), res8[0][3])
+    assert np.array_equal(lp.download(np.float32, 8), res8[0][4])
+    for b in (lg, tok, lp, sws):
+        b.close()

@@ -360,3 +360,55 @@ def test_plumbing_one_worker_per_cu(rl, gpu, orc, olib):
 ], ids=["gqa4_d128_bf16_tc16", "gqa8_d128_bf16_tc16", "gqa2_d64_fp16_tc32", "mha_d128_fp16_tc32"])
 def test_worker_shapes_one_per_cu(rl, gpu, orc, olib, shape):
     _pairs_run(rl, gpu, orc, olib, **shape)
+
+
+def test_worker_stamps_lockstep(rl, gpu):
+    """Four workers with stamps set, 64 descriptors one at a time through
+    ring_lockstep_hw (seq_len = max_tokens: no decode step, the completion is
+    the descriptor unchanged): every sample arrives with its tag, each
+    worker's consume stamp precedes its completion stamp, the stamps of
+    successive samples ascend on the device's common clock, and the workers
+    end on the stop flag (status 0) with 16 completions each."""
+    L = rl.lib()
+    pairs, n = 4, 64
+    w = synth.make_decode(7, 1, 8, 8, 64, 16, 16, dtype="fp16")
+    layout = rl.KvLayoutDesc.paged(16, 64)
+    arena, table = rl.DeviceBuffer.from_array(w.arena), rl.DeviceBuffer.from_array(w.table)
+    scratch = rl.DeviceBuffer(1 << 20, zero=True)
+    stats = rl.DeviceBuffer(pairs * 32, zero=True)
+    cqs = [L.hw_ring_create() for _ in range(pairs)]
+    dqs = [L.hw_ring_create() for _ in range(pairs)]
+    rings = _alloc_coherent(rl, 16 * pairs)
+    for g in range(pairs):
+        C.cast(rings, C.POINTER(C.c_void_p))[g] = cqs[g]
+        C.cast(rings, C.POINTER(C.c_void_p))[pairs + g] = dqs[g]
+    stop, stamps = _alloc_coherent(rl, 64), _alloc_coherent(rl, 16 * pairs)
+    a = rl.HwWorkerArgs(cmdq=rings, doneq=rings + 8 * pairs, groups=pairs, stop=stop, max_idle_polls=1 << 24,
+                        arena_base=arena.ptr, arena_bytes=arena.nbytes, layout=layout, block_table=table.ptr,
+                        table_stride=w.table_stride, rollouts=1, q_heads=8, kv_heads=8, dtype=rl.DTYPE_FP16,
+                        max_steps=1, q=scratch.ptr, k_new=scratch.ptr, v_new=scratch.ptr, logits=scratch.ptr,
+                        vocab=16, attn_out=scratch.ptr, token_out=scratch.ptr, logprob_out=scratch.ptr,
+                        stats=stats.ptr, stamps=stamps)
+    ws = rl.hw_worker_workspace(a)
+    out = (rl.RingLockstepSample * n)()
+    d = rl.HwDesc(opcode=1, rollout_id=0, seq_len=16, max_tokens=16)
+    print(f"[worker] {pairs} workers with stamps, {n} lock-step descriptors", flush=True)
+    rl.hw_worker_launch(a)
+    try:
+        got = L.ring_lockstep_hw(rings, rings + 8 * pairs, pairs, C.byref(d), n, stamps, 10**10, out)
+    finally:
+        C.cast(stop, C.POINTER(C.c_uint32))[0] = 1
+        rl.sync()
+    st = stats.download(np.uint64, (pairs, 4))
+    assert got == n
+    assert (st[:, 1] == n // pairs).all() and (st[:, 3] == 0).all(), st
+    for i, s in enumerate(out):
+        assert s.consume_tick <= s.complete_tick and s.submit_ns < s.poll_ns, i
+        if i:
+            assert out[i - 1].complete_tick <= s.consume_tick, i
+    for b in (arena, table, scratch, stats, ws):
+        b.close()
+    for r in cqs + dqs:
+        L.hw_ring_destroy(r)
+    for p in (rings, stop, stamps):
+        L.rl_hip_host_free(p)
