@@ -147,7 +147,9 @@ class Step:
     def append_bytes():
         return B * KVH * D * 2 * 2 * 2  # read new K/V rows, write them into the arena
 
-    def run(self, i, only="step"):
+    def run(self, i, only):
+        """One launch of `only`: the unfused step (rl_hip_decode_step, then
+        rl_hip_sample), or one of its entry points alone."""
         if only == "unfused":
             # attention, then the KV append inside the attention's merge kernel
             rlrt.decode_step(self.attn, self.app)
@@ -821,8 +823,10 @@ def wl_ringstep(args):
     (rl_hip_ring_step_enqueue): per step 64 one-token descriptors drained by
     the poll kernel, the batched step over every compute unit, 64 completions
     published. The descriptors of every step are queued before the timed
-    region; logits rotate over 4 input slots. The launched step on the same
-    inputs is timed beside it."""
+    region; logits rotate over 4 input slots. Beside it, on the same inputs:
+    the launched fused step (rl_hip_decode_sample_step: the same two kernels
+    without the rings) and the unfused one (rl_hip_decode_step +
+    rl_hip_sample)."""
     import ringstep
 
     K, W = args.steps, args.warmup
@@ -855,19 +859,30 @@ def wl_ringstep(args):
     run.close()
     if stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
         raise rlrt.RlrtError(f"ring step stats {stats}, {n_comp} completions")
-    # the launched step on the same inputs
+    # the launched steps on the same inputs
+    fws = rlrt.decode_sample_step_workspace(st.attn, st.samp[0])
+
+    def fused(i):
+        s = st.samp[i % LOGIT_COPIES]
+        s.step = i
+        rlrt.decode_sample_step(st.attn, st.app, s, fws)
+
+    fused_us = _event_us(fused, K, W)
     for i in range(W):
-        st.run(i)
-    lms, _ = time_loop(st, K, "step")
+        st.run(i, "unfused")
+    lms, _ = time_loop(st, K, "unfused")
     ring_us, launched_us = ms / K * 1e3, lms / K * 1e3
     step_bytes = st.attn_bytes() + st.sample_bytes() + st.append_bytes()
     return {"workload": "ringstep_b64_q32kv8_d128_ctx512-4096_v128256_t0.8_k50_p0.9",
             "steps": K, "ring_step_us": ring_us, "ring_steps_per_s": 1e6 / ring_us,
             "ring_tokens_per_s": B * 1e6 / ring_us, "ring_step_hbm_frac": step_bytes / (ring_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "launched_fused_step_us": fused_us, "ring_over_launched_fused": ring_us / fused_us,
             "launched_step_us": launched_us, "launched_tokens_per_s": B * 1e6 / launched_us,
             "stats": stats,
-            "note": "per step: poll kernel (one wave, 64 descriptors over PCIe), gather kernel, fused attention + "
-                    "append, sampler, publish kernel (64 completions); HIP events on the library stream"}
+            "note": "per step: the turn kernel (one wave: the previous step's 64 completions published and 64 "
+                    "descriptors admitted over PCIe), the fused attention + sampling launch and its merge + append "
+                    "kernel; launched_fused_step_us: the same two kernels called directly; launched_step_us: "
+                    "rl_hip_decode_step + rl_hip_sample; HIP events on the library stream"}
 
 
 def wl_cmdring(args):

@@ -444,6 +444,19 @@ int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_
     return attn_run(attn, ap, row_map);
 }
 
+int rl_attn_mapped(const rl_attn_decode_args_t *attn, const uint32_t *row_map)
+{
+    if (rl_require_open("rl_hip_attn_decode") || validate(attn))
+        return -1;
+    if (!row_map) {
+        rl_set_error("rl_hip_attn_decode: NULL row map");
+        return -1;
+    }
+    AppendParams none = {};
+    none.arena = nullptr;
+    return attn_run(attn, none, row_map);
+}
+
 // ---- the decode step without allocation ---------------------------------------
 // The workspace of rl_hip_decode_step_noalloc (cum[batch + 1], then the fp32
 // partials) lives in this file-scope array; every device the library runs on

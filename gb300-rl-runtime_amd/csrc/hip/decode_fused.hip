@@ -569,10 +569,14 @@ bool same_shape(const rl_attn_decode_args_t *a, const rl_attn_decode_args_t *b)
 
 }  // namespace
 
-extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
-                                         const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes)
+namespace {
+
+// rl_hip_decode_sample_step with batch row b reading the block-table row
+// row_map[b] (row_map NULL: b itself), for the attention and the append.
+int decode_sample_step_rows(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                            const rl_sample_args_t *samp, const uint32_t *row_map, void *workspace,
+                            size_t workspace_bytes, const char *who)
 {
-    const char *who = "rl_hip_decode_sample_step";
     if (fused_validate(attn, append, samp, who))
         return -1;
     const size_t need = rl_hip_decode_sample_step_workspace(attn, samp);
@@ -589,15 +593,43 @@ extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, cons
         rl_attn_decode_args_t a = *attn;
         a.workspace = workspace;
         a.workspace_bytes = a_bytes;
-        if (append ? rl_hip_decode_step(&a, append) : rl_hip_attn_decode(&a))
+        int rc;
+        if (row_map)
+            rc = append ? rl_decode_step_mapped(&a, append, row_map) : rl_attn_mapped(&a, row_map);
+        else
+            rc = append ? rl_hip_decode_step(&a, append) : rl_hip_attn_decode(&a);
+        if (rc)
             return -1;
         rl_sample_args_t s = *samp;
         s.workspace = (uint8_t *)workspace + a_bytes;
         s.workspace_bytes = workspace_bytes - a_bytes;
         return rl_hip_sample(&s);
     }
-    const FusedParams f = fused_params_of(attn, samp, workspace, 0);
-    return launch_shape(kRunFused | kRunMerge, attn, f, append_or_none(append), rl_stream());
+    FusedParams f = fused_params_of(attn, samp, workspace, 0);
+    f.p.row_map = row_map;
+    AppendParams ap = append_or_none(append);
+    ap.row_map = row_map;
+    return launch_shape(kRunFused | kRunMerge, attn, f, ap, rl_stream());
+}
+
+}  // namespace
+
+extern "C" int rl_hip_decode_sample_step(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                                         const rl_sample_args_t *samp, void *workspace, size_t workspace_bytes)
+{
+    return decode_sample_step_rows(attn, append, samp, nullptr, workspace, workspace_bytes,
+                                   "rl_hip_decode_sample_step");
+}
+
+int rl_decode_sample_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                                 const rl_sample_args_t *samp, const uint32_t *row_map, void *workspace,
+                                 size_t workspace_bytes, const char *who)
+{
+    if (!row_map) {
+        rl_set_error("%s: NULL row map", who);
+        return -1;
+    }
+    return decode_sample_step_rows(attn, append, samp, row_map, workspace, workspace_bytes, who);
 }
 
 namespace {

@@ -23,9 +23,13 @@
 //           position, Philox seed and counter. The three ring indexes and
 //           the stop flag it needs are read in one round trip, and both
 //           ring releases share one fence.
-//  step     the decode step (paged GQA attention over all compute units, the
-//           KV append in its merge kernel) reading the rollout-ordered block
-//           table through the row map, and rl_hip_sample over the batch rows.
+//  step     rl_hip_decode_sample_step over the batch rows with the
+//           rollout-ordered block table read through the row map: one launch
+//           streams the paged GQA attention's tiles beside the sampling of
+//           the step's logits (an input of the step, not the attention's
+//           output), a second merges the split rows and appends the K/V
+//           token. Shapes outside the fused kernel take rl_hip_decode_step
+//           and rl_hip_sample.
 //
 // A call of `steps` steps launches steps + 1 turns: the last one only
 // publishes. Each kernel boundary makes the previous kernel's writes visible
@@ -209,14 +213,19 @@ __global__ __launch_bounds__(64) void ring_turn_kernel(RingParams p, uint32_t do
                 uint64_t w[8];
                 __builtin_memcpy(w, &d, sizeof(d));
                 rl_sys_store_64B(&p.dq->desc[(dtail + n_done + lanes_below(fm)) & HW_RING_MASK], w);
+                p.kind[i] = kFree;
+            } else {
+                // no room: the finished descriptor stays in its row as a
+                // pass-through, which a later turn's publish pushes
+                p.kind[i] = kPass;
+                set_row_args(p, i, false, 0u, 0u);
             }
-            p.kind[i] = kFree;  // a finished row is freed even when its completion is lost
         } else if (k == kDecode) {
             set_row_args(p, i, true, d.rollout_id, d.seq_len);  // the row decodes again
         }
         n_done += (uint32_t)__builtin_popcountll(fm);
         n_dec += do_publish ? (uint32_t)__builtin_popcountll(__ballot(k == kDecode)) : 0u;
-        const bool f = valid && (k == kFree || fin);
+        const bool f = valid && (k == kFree || (fin && room));
         const uint64_t m = __ballot(f);
         if (f)
             s_free[nfree + lanes_below(m)] = (uint16_t)i;
@@ -343,8 +352,8 @@ __global__ __launch_bounds__(64) void ring_turn_kernel(RingParams p, uint32_t do
 // ---- host side -------------------------------------------------------------
 
 struct RingWs {
-    size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, attn, samp, total;
-    size_t attn_bytes, samp_bytes;
+    size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, step, total;
+    size_t step_bytes;
 };
 
 size_t up256(size_t x) { return (x + 255) / 256 * 256; }
@@ -425,17 +434,13 @@ int ring_layout(const rl_ring_step_args_t *a, RingWs &w)
     w.pos = w.ctx + up256(B * 4);
     w.rseed = w.pos + up256(B * 4);
     w.rstep = w.rseed + up256(B * 8);
-    w.attn = w.rstep + up256(B * 8);
+    w.step = w.rstep + up256(B * 8);
     rl_attn_decode_args_t t = attn_of(a, nullptr, 0);
-    w.attn_bytes = rl_hip_attn_decode_workspace(&t);
-    if (w.attn_bytes == 0)
-        return -1;
-    w.samp = w.attn + up256(w.attn_bytes);
     rl_sample_args_t s = samp_of(a);
-    w.samp_bytes = rl_hip_sample_workspace(&s);
-    if (w.samp_bytes == 0)
+    w.step_bytes = rl_hip_decode_sample_step_workspace(&t, &s);
+    if (w.step_bytes == 0)
         return -1;
-    w.total = w.samp + up256(w.samp_bytes);
+    w.total = w.step + up256(w.step_bytes);
     return 0;
 }
 
@@ -494,7 +499,7 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         hipLaunchKernelGGL(ring_turn_kernel, dim3(1), dim3(64), 0, rl_stream(), p, n > 0 ? 1u : 0u, 1u);
         if (rl_check_launch("ring_turn_kernel launch"))
             return -1;
-        rl_attn_decode_args_t t = attn_of(a, ws + w.attn, w.attn_bytes);
+        rl_attn_decode_args_t t = attn_of(a, nullptr, 0);
         t.block_table = a->block_table;
         t.ctx_lens = p.ctx;
         t.q = (const uint8_t *)a->q + si * B * qrow;
@@ -512,9 +517,6 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         ap.cow_src = nullptr;
         ap.k_new = (const uint8_t *)a->k_new + si * B * kvrow;
         ap.v_new = (const uint8_t *)a->v_new + si * B * kvrow;
-        // batch row i reads the block-table row of the rollout it holds
-        if (rl_decode_step_mapped(&t, &ap, p.rmap))
-            return -1;
         rl_sample_args_t s = samp_of(a);
         s.logits = a->logits + si * B * a->vocab;
         s.seed = p.rseed;
@@ -522,9 +524,9 @@ extern "C" int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *a, uint32_t s
         s.draw_ids = p.rmap;  // the draw follows the rollout, not the row it was admitted into
         s.token_out = a->token_out + so * B;
         s.logprob_out = a->logprob_out + so * B;
-        s.workspace = ws + w.samp;
-        s.workspace_bytes = w.samp_bytes;
-        if (rl_hip_sample(&s))
+        // batch row i reads the block-table row of the rollout it holds
+        if (rl_decode_sample_step_mapped(&t, &ap, &s, p.rmap, ws + w.step, w.step_bytes,
+                                         "rl_hip_ring_step_enqueue"))
             return -1;
     }
     // publish the last step

@@ -27,6 +27,13 @@ int rl_attn_scratch_setup(int device);
 // (attn_decode.hip; the ring-driven step uses it).
 int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
                           const uint32_t *row_map);
+// rl_hip_attn_decode with the same row map (attn_decode.hip).
+int rl_attn_mapped(const rl_attn_decode_args_t *attn, const uint32_t *row_map);
+// rl_hip_decode_sample_step with the same row map for the attention and the
+// append (decode_fused.hip; errors name `who`).
+int rl_decode_sample_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                                 const rl_sample_args_t *samp, const uint32_t *row_map, void *workspace,
+                                 size_t workspace_bytes, const char *who);
 
 // Argument checks of the attention, the decode step and the sampler (0, or
 // -1 with the error set), for entry points that combine them.

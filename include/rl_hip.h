@@ -298,15 +298,18 @@ int rl_hip_hw_worker_launch(const rl_hw_worker_args_t *args);
  *    while active rows finish; other opcodes are dropped;
  *  - decodes one token for every active row: paged GQA attention of rollout
  *    rollout_id over its seq_len cached tokens (block_table rows rollout *
- *    kv_heads + h) with the K/V token appended at position seq_len
- *    (rl_hip_decode_step), and sampling (rl_hip_sample: greedy, or
- *    temperature / top_k / top_p with Philox key seeds[rollout] and counter
- *    (seq_len, rollout): the draw depends on the descriptor, never on the
- *    batch row it was admitted into);
+ *    kv_heads + h) with the K/V token appended at position seq_len, and
+ *    sampling of the step's logits (greedy, or temperature / top_k / top_p
+ *    with Philox key seeds[rollout] and counter (seq_len, rollout): the draw
+ *    depends on the descriptor, never on the batch row it was admitted
+ *    into), together as rl_hip_decode_sample_step (one launch streams the
+ *    attention beside the sampling, a second merges and appends; its
+ *    results on the rows of the step);
  *  - applies the rule for that token (seq_len++; DONE at max_tokens;
  *    NEEDS_REWARD at a multiple of 32; otherwise the row decodes again next
  *    step) and pushes finished descriptors to doneq in row order (bounded
- *    wait for room; status 3 if it never comes).
+ *    wait for room; status 3 if it never comes, and the finished descriptors
+ *    then stay in their rows, unchanged, for a later step or call to push).
  * Step k (counting from first_step) reads input slot k % input_slots and
  * writes output slot k % output_slots; row i of a slot belongs to whatever
  * descriptor holds row i in that step, which row_rollout_out records

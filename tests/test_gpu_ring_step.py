@@ -8,7 +8,9 @@ ring, checked against the CPU path.
    = the rollout's seed, counter = seq_len), one token per descriptor,
    submitted in a shuffled rollout order. Completions byte-identical to
    hw_worker_sim_run fed the same submissions; every row's attention bit-equal
-   to rl_hip_decode_step launched on the same batch and within 1e-4 of fp64;
+   to rl_hip_decode_sample_step launched on the same rows (the same fused
+   launch: the split depends only on the contexts and the sampled rows'
+   shape) and within 1e-4 of fp64;
    tokens bit-exact and logprobs within 1e-4 against the oracle; the arena
    after the step byte-equal to the oracle's append.
 2. The control rule over many steps with 8 rows for 13 descriptors:
@@ -17,7 +19,11 @@ ring, checked against the CPU path.
    rows refilled as they free, then STOP. Each rollout's completion equals the
    simulator's; for every step, every row that decoded (by the recorded row
    map) is checked against the oracle with the rollout's context at that
-   step, and the final arena against the oracle's replay of every append."""
+   step, and the final arena against the oracle's replay of every append.
+3. The exit paths of admission, each a bounded wait: an idle limit (status
+   1), a rollout id past the table (2), the host's stop flag (4), and a full
+   completion ring (3), where the finished descriptor stays in its row and a
+   later call pushes it once the host has made room."""
 import ctypes as C
 
 import numpy as np
@@ -68,6 +74,28 @@ def _as_submitted(rl, calls):
     return out
 
 
+def _launched_fused(rl, w, logits, max_ctx):
+    """rl_hip_decode_sample_step (no append) on a gathered batch with the
+    step's logits shape: the attention outputs (bf16 bits, fp32)."""
+    layout = rl.KvLayoutDesc.paged(w.token_count, w.head_dim)
+    n = w.batch * w.q_heads * w.head_dim
+    bufs = [rl.DeviceBuffer.from_array(x) for x in (w.arena, w.table, w.ctx, w.q, logits)]
+    out, out32 = rl.DeviceBuffer(n * 2), rl.DeviceBuffer(n * 4)
+    tok, lp = rl.DeviceBuffer(w.batch * 4), rl.DeviceBuffer(w.batch * 4)
+    a = rl.attn_args(bufs[0], layout, bufs[1], w.table_stride, w.batch, w.q_heads, w.kv_heads, rl.DTYPE_BF16,
+                     bufs[2], max_ctx, bufs[3], out, out32)
+    rows, V = logits.shape
+    s = rl.sample_args(bufs[4], rows, V, V, tok, lp, temperature=0.8, top_k=50, top_p=0.9)
+    ws = rl.decode_sample_step_workspace(a, s)
+    rl.decode_sample_step(a, None, s, ws)
+    rl.sync()
+    sh = (w.batch, w.q_heads, w.head_dim)
+    res = out.download(np.uint16, sh), out32.download(np.float32, sh)
+    for b in bufs + [out, out32, tok, lp, ws]:
+        b.close()
+    return res
+
+
 def test_ring_step_batch64(rl, gpu, orc, olib):
     import ringstep
 
@@ -101,11 +129,11 @@ def test_ring_step_batch64(rl, gpu, orc, olib):
     o = run.outputs(0)
     assert np.array_equal(o["rows"], perm.astype(np.uint32))
 
-    # the launched path on the same batch: bit-equal attention
+    # the launched path on the same rows: bit-equal attention
     ref_arena = w.arena.copy()
     wb = synth.DecodeWorkload(B, QH, KVH, D, "bf16", TPB, w.ctx[perm].copy(), np.ascontiguousarray(w.table[perm]),
                               w.arena, q, 0)
-    o16, o32 = gh.run_attn(rl, wb)
+    o16, o32 = _launched_fused(rl, wb, logits, 4096)
     assert np.array_equal(o["out"], o16) and np.array_equal(o["out32"], o32)
     gh.check_attn(o["out"], o["out32"], orc.attn_f64(olib, wb, 0), "bf16")
     # tokens and logprobs
@@ -240,3 +268,68 @@ def test_ring_step_draw_follows_rollout(rl, gpu, orc, olib):
                                 C.byref(lp)) for r in range(B)]
     assert tok_of[0].tolist() == want
     assert len(set(want)) > 1  # the rollouts' draws differ, so a row-keyed draw would show
+
+
+def test_ring_step_exit_paths(rl, gpu):
+    """Each end of admission is a bounded wait that leaves its status: no
+    descriptor within max_idle_polls (1), a rollout id past the block table
+    (2, nothing decoded), the host's stop flag (4), and a completion ring the
+    host keeps full (3): the finished descriptor then stays in its row, and
+    the next call pushes it, unchanged, once the host has made room."""
+    import ringstep
+
+    B, V = 4, 4096
+    rng = np.random.default_rng(7180)
+    w = synth.make_decode(7181, B, QH, KVH, D, 40, 300)
+    q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    logits = rng.standard_normal((B, V), dtype=np.float32)
+
+    def run_of(arena):
+        r = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
+                                 greedy=True, max_idle_polls=2000)
+        r.set_inputs(0, q, kn, vn, logits)
+        return r
+
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    for case in ("idle", "bad_id", "stop"):
+        run = run_of(arena)
+        if case == "bad_id":
+            run.submit_decode(B + 3, 10, 11)
+        if case == "stop":
+            run.stop()
+        print(f"[ring] exit path: {case}", flush=True)
+        run.enqueue(1)
+        rl.sync()
+        st = run.stats()
+        assert st == [0, 0, 0, {"idle": 1, "bad_id": 2, "stop": 4}[case]], (case, st)
+        assert run.completions() == []
+        run.close()
+
+    # a full completion ring: the host fills it with 65,536 entries of its own
+    run = run_of(arena)
+    L = rl.lib()
+    filler = rl.HwDesc(opcode=7)
+    for _ in range(65536):
+        assert rl.hw_ring_push(run.dq, filler) == 0
+    r0 = 1
+    run.submit_decode(r0, int(w.ctx[r0]), int(w.ctx[r0]) + 1)
+    print("[ring] exit path: completion ring full", flush=True)
+    run.enqueue(1)
+    rl.sync()
+    assert run.stats() == [1, 0, 1, 3]
+    assert L.hw_ring_load_acquire(run.dq + 64) == 65536   # nothing pushed
+    got = run.completions()                                # the host drains its entries
+    assert len(got) == 65536 and all(g == bytes(filler) for g in got)
+    run.enqueue(1)                                         # admission stays closed; the row is pushed
+    rl.sync()
+    got = run.completions()
+    assert len(got) == 1
+    d = rl.HwDesc.from_buffer_copy(got[0])
+    assert (d.rollout_id, d.seq_len, d.max_tokens) == (r0, int(w.ctx[r0]) + 1, int(w.ctx[r0]) + 1)
+    assert d.flags & 2 and d.opcode == 1                   # DONE (rule of src/hw_worker_sim.c:23-59)
+    st = run.stats()
+    assert st[0] == 1 and st[1] == 1 and st[3] == 3, st
+    run.close()
+    arena.close()
