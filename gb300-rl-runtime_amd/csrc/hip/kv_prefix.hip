@@ -91,6 +91,7 @@ struct CowParams {
     uint32_t table_stride;
     uint32_t kv_heads;
     const uint32_t *positions;
+    uint32_t *row_status;  // [batch][kv_heads] or nullptr
 };
 
 __global__ __launch_bounds__(64) void kv_cow_kernel(CowParams p)
@@ -100,24 +101,42 @@ __global__ __launch_bounds__(64) void kv_cow_kernel(CowParams p)
     uint32_t br = key;
     if (p.branch_of_key)
         br = key < p.keys ? p.branch_of_key[key] : 0xFFFFFFFFu;
+    uint32_t *status = p.row_status ? p.row_status + (size_t)b * p.kv_heads + g : nullptr;
+    auto report = [&](uint32_t v) {
+        if (status && threadIdx.x == 0)
+            *status = v;
+    };
     bool live;
     uint32_t pid = 0;
     const int64_t off = resolve(p.table, br, &live, &pid);
-    if (!live)
-        return;  // no shared prefix: nothing to copy
+    if (!live) {
+        report(RL_COW_NONE);  // no shared prefix: nothing to copy
+        return;
+    }
     const uint32_t pbase = pid * kPrefixBytes;
     const uint32_t len = tab32(p.table, pbase + 16);    // token_len
     const uint32_t count = tab32(p.table, pbase + 20);  // kv_block_count
     const uint32_t slot = len % p.token_count, j = len / p.token_count;
-    if (slot == 0 || p.positions[b] != len)
-        return;  // the prefix ends on a block boundary, or this is not the branch's first own token
-    const uint32_t per_head = count / p.kv_heads;
-    if (j >= per_head || j >= p.table_stride || off < 0)
+    if (slot == 0 || p.positions[b] != len) {
+        report(RL_COW_NONE);  // the prefix ends on a block boundary, or this is not the branch's first own token
         return;
+    }
+    const uint32_t per_head = count / p.kv_heads;
+    if (j >= per_head || j >= p.table_stride || off < 0) {
+        report(RL_COW_OUT_OF_RANGE);
+        return;
+    }
     const uint64_t src = (uint64_t)off + (uint64_t)g * per_head + j;
     const uint32_t dst = p.block_table[((size_t)b * p.kv_heads + g) * p.table_stride + j];
-    if (src >= p.arena_blocks || dst >= p.arena_blocks || src == dst)
+    if (src >= p.arena_blocks || dst >= p.arena_blocks) {
+        report(RL_COW_OUT_OF_RANGE);
         return;
+    }
+    if (src == dst) {
+        report(RL_COW_SHARED);  // the row maps the prefix block itself: no private copy to make
+        return;
+    }
+    report(RL_COW_COPIED);
     const uint8_t *s = p.arena + src * p.block_bytes;
     uint8_t *d = p.arena + (uint64_t)dst * p.block_bytes;
     const uint32_t chunks = slot * p.row_bytes / 16;  // 16-byte chunks of the filled rows of one plane
@@ -181,6 +200,7 @@ extern "C" int rl_hip_kv_cow(const rl_kv_cow_args_t *a)
     p.table_stride = a->table_stride;
     p.kv_heads = a->kv_heads;
     p.positions = a->positions;
+    p.row_status = a->row_status;
     hipLaunchKernelGGL(kv_cow_kernel, dim3(a->kv_heads, a->batch), dim3(64), 0, rl_stream(), p);
     return rl_check_launch("kv_cow_kernel launch");
 }

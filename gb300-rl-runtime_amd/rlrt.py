@@ -256,7 +256,10 @@ class CowArgs(C.Structure):
     _fields_ = [("arena_base", C.c_void_p), ("arena_bytes", C.c_uint64), ("layout", KvLayoutDesc),
                 ("prefixes", C.c_void_p), ("row_key", C.c_void_p), ("branch_of_key", C.c_void_p),
                 ("keys", C.c_uint32), ("block_table", C.c_void_p), ("table_stride", C.c_uint32),
-                ("batch", C.c_uint32), ("kv_heads", C.c_uint32), ("positions", C.c_void_p)]
+                ("batch", C.c_uint32), ("kv_heads", C.c_uint32), ("positions", C.c_void_p),
+                ("row_status", C.c_void_p)]
+
+COW_NONE, COW_COPIED, COW_SHARED, COW_OUT_OF_RANGE = 0, 1, 2, 3
 
 
 class HwWorkerArgs(C.Structure):

@@ -516,7 +516,20 @@ int rl_hip_kv_append(const rl_kv_append_args_t *args);
  * (kv_block_count / kv_heads) + P / token_count (prefix blocks head-major
  * from kv_block_offset, in arena block units) are copied into the row's
  * block block_table[(b * kv_heads + g) * table_stride + P / token_count].
- * Every other row is left alone, as are blocks past the arena or the table. */
+ * Every other row is left alone, as are blocks past the arena or the table.
+ * That table entry must be a private block: when it is the prefix block
+ * itself, nothing is copied and the step's append would write the branch's
+ * token into the block every sibling reads. With row_status set, entry
+ * b * kv_heads + g reports what happened to (row b, kv head g):
+ * RL_COW_NONE (nothing to copy: no live prefix, a prefix ending on a block
+ * boundary, or not the branch's first own token), RL_COW_COPIED,
+ * RL_COW_SHARED (the row's entry is the prefix block: not copied) or
+ * RL_COW_OUT_OF_RANGE (a block past the arena, or P / token_count past the
+ * table or the prefix's blocks: not copied). */
+#define RL_COW_NONE 0u
+#define RL_COW_COPIED 1u
+#define RL_COW_SHARED 2u
+#define RL_COW_OUT_OF_RANGE 3u
 int rl_hip_kv_branch_resolve(const KVPrefixTable *table, const uint32_t *branch_ids, int64_t *out_offsets,
                              uint32_t n);
 
@@ -533,6 +546,7 @@ typedef struct {
     uint32_t batch;
     uint32_t kv_heads;
     const uint32_t *positions;      /* device [batch]: the position the step appends */
+    uint32_t *row_status;           /* device [batch][kv_heads] RL_COW_*, or NULL */
 } rl_kv_cow_args_t;
 
 int rl_hip_kv_cow(const rl_kv_cow_args_t *args);

@@ -136,11 +136,13 @@ def test_cow_before_attention_then_decode_step(rl, gpu, orc, olib):
     dev = {k: rl.DeviceBuffer.from_array(v) for k, v in
            (("arena", arena), ("table", table), ("ptab", t), ("branch", branch), ("pos", pos), ("ctx", ctx),
             ("q0", q[0]), ("q1", q[1]), ("k0", kn[0]), ("v0", vn[0]), ("k1", kn[1]), ("v1", vn[1]))}
+    dev["status"] = rl.DeviceBuffer(B * KVH * 4, zero=True)
     layout = rl.KvLayoutDesc.paged(TPB, D)
     out, out32 = rl.DeviceBuffer(B * QH * D * 2), rl.DeviceBuffer(B * QH * D * 4)
     cw = rl.CowArgs(arena_base=dev["arena"].ptr, arena_bytes=dev["arena"].nbytes, layout=layout,
                     prefixes=dev["ptab"].ptr, row_key=dev["branch"].ptr, branch_of_key=None, keys=0,
-                    block_table=dev["table"].ptr, table_stride=stride, batch=B, kv_heads=KVH, positions=dev["pos"].ptr)
+                    block_table=dev["table"].ptr, table_stride=stride, batch=B, kv_heads=KVH, positions=dev["pos"].ptr,
+                    row_status=dev["status"].ptr)
     a = rl.attn_args(dev["arena"], layout, dev["table"], stride, B, QH, KVH, rl.DTYPE_BF16, dev["ctx"],
                      int(pos2.max()), dev["q0"], out, out32)
     ws = rl.attn_workspace(a)
@@ -154,6 +156,11 @@ def test_cow_before_attention_then_decode_step(rl, gpu, orc, olib):
         rl.sync()
         got = dev["arena"].download(np.uint8, arena.size)
         assert np.array_equal(got, ref1 if step == 0 else ref2), step
+        status = dev["status"].download(np.uint32, (B, KVH))
+        want = np.full((B, KVH), rl.COW_NONE, np.uint32)
+        if step == 0:
+            want[:12] = rl.COW_COPIED                          # rows 12-15: no copy due (see above)
+        assert np.array_equal(status, want), (step, status)
         w = synth.DecodeWorkload(B, QH, KVH, D, "bf16", TPB, ctx + step, table, got, q[step], 0)
         gh.check_attn(out.download(np.uint16, (B, QH, D)), out32.download(np.float32, (B, QH, D)),
                       orc.attn_f64(olib, w, 0), "bf16")
@@ -162,4 +169,63 @@ def test_cow_before_attention_then_decode_step(rl, gpu, orc, olib):
         dev["ctx"].upload(ctx + 1)
         a.q, ap.k_new, ap.v_new = dev["q1"].ptr, dev["k1"].ptr, dev["v1"].ptr
     for b in list(dev.values()) + [out, out32, ws]:
+        b.close()
+
+
+def test_cow_reports_shared_and_out_of_range(rl, gpu):
+    """Four rows on four prefixes of 20 tokens (2 KV heads, d64, 16-token
+    blocks: slot 4 of block 1 is each branch's first own token): row 0 maps a
+    private block (copied), row 1 maps the prefix's own block 1 (RL_COW_SHARED,
+    nothing copied), row 2 maps a block id past the arena (RL_COW_OUT_OF_RANGE,
+    nothing written), row 3 is one token past its first own token (no copy due).
+    The arena changes only in row 0's private blocks, by the 4 filled slots of
+    each plane of the prefix block."""
+    L = rl.lib()
+    rng = np.random.default_rng(93)
+    B, KVH, D, TPB, P = 4, 2, 64, 16, 20
+    per_head = 2
+    n_prefix_blocks = B * KVH * per_head
+    nblk = n_prefix_blocks + B * KVH * 2
+    block = 2 * TPB * D * 2
+    arena = rng.integers(0, 256, nblk * block, dtype=np.uint8)
+    t = np.zeros(TABLE_BYTES, np.uint8)
+    L.kv_prefix_table_init(t.ctypes.data)
+    table = np.zeros((B, KVH, 3), np.uint32)
+    branch = np.zeros(B, np.uint32)
+    pid, bid = C.c_uint32(), C.c_uint32()
+    for b in range(B):
+        base = b * KVH * per_head
+        assert L.kv_prefix_register(t.ctypes.data, base, P, KVH * per_head, C.byref(pid)) == 0
+        assert L.kv_branch_alloc(t.ctypes.data, b, pid.value, 5, 0, 1, C.byref(bid)) == 0
+        branch[b] = bid.value
+        for h in range(KVH):
+            table[b, h, 0] = base + h * per_head
+            table[b, h, 1] = n_prefix_blocks + b * KVH + h        # private
+            table[b, h, 2] = n_prefix_blocks + B * KVH + b * KVH + h
+    table[1, :, 1] = [1 * KVH * per_head + h * per_head + 1 for h in range(KVH)]   # the prefix block itself
+    table[2, :, 1] = nblk + 5                                                        # past the arena
+    pos = np.array([P, P, P, P + 1], np.uint32)
+    dev = {k: rl.DeviceBuffer.from_array(v) for k, v in
+           (("arena", arena), ("table", table), ("ptab", t), ("branch", branch), ("pos", pos))}
+    status = rl.DeviceBuffer(B * KVH * 4, zero=True)
+    cw = rl.CowArgs(arena_base=dev["arena"].ptr, arena_bytes=dev["arena"].nbytes, layout=rl.KvLayoutDesc.paged(TPB, D),
+                    prefixes=dev["ptab"].ptr, row_key=dev["branch"].ptr, branch_of_key=None, keys=0,
+                    block_table=dev["table"].ptr, table_stride=3, batch=B, kv_heads=KVH, positions=dev["pos"].ptr,
+                    row_status=status.ptr)
+    print("[prefix] copy-on-write with a shared and an out-of-range entry", flush=True)
+    rl.kv_cow(cw)
+    rl.sync()
+    st = status.download(np.uint32, (B, KVH))
+    assert st.tolist() == [[rl.COW_COPIED] * KVH, [rl.COW_SHARED] * KVH, [rl.COW_OUT_OF_RANGE] * KVH,
+                           [rl.COW_NONE] * KVH], st
+    got = dev["arena"].download(np.uint8, arena.size)
+    want = arena.copy().reshape(nblk, block)
+    filled = (P % TPB) * D * 2
+    for h in range(KVH):
+        src = want[0 * KVH * per_head + h * per_head + 1]
+        dst = want[table[0, h, 1]]
+        dst[:filled] = src[:filled]                                    # K plane
+        dst[TPB * D * 2:TPB * D * 2 + filled] = src[TPB * D * 2:TPB * D * 2 + filled]   # V plane
+    assert np.array_equal(got, want.reshape(-1))
+    for b in list(dev.values()) + [status]:
         b.close()
