@@ -722,10 +722,11 @@ __device__ __forceinline__ void merge_span(const AttnParams &p, uint32_t b, uint
 // merge_span of one whole row (all G heads) by one wave, with the arithmetic
 // of merge_span's register path in the same order: M = max_w m_w per head,
 // then L = sum l_w f_w and O = sum o_w f_w over w ascending (fmaf), f_w =
-// 2^(m_w - M), out = O / L. Lane j < np first loads partial j's (m, l) of
-// every head, which gives M by a wave reduction and each f_w by readlane;
-// lane l owns output elements l + 64 k. The O loads of up to 8 partials are
-// in flight together with the (m, l) loads. Rows of up to 64 partials.
+// 2^(m_w - M), out = O / L. The partials go 64 at a time: lane j of a round
+// loads partial (round start + j)'s (m, l) of every head, which gives M by a
+// wave reduction and each f_w by readlane (a row of at most 64 partials, the
+// usual case, loads them once); lane l owns output elements l + 64 k. The O
+// loads of up to 8 partials are in flight together with the (m, l) loads.
 template <int D, int G, int DT>
 __device__ __forceinline__ void merge_row_wave(const AttnParams &p, uint32_t b, uint32_t g, uint32_t wf, uint32_t wl,
                                                bool bad, int lane)
@@ -739,14 +740,17 @@ __device__ __forceinline__ void merge_row_wave(const AttnParams &p, uint32_t b, 
     const uint32_t row = b * p.kv_heads + g;
     const uint32_t np = wl - wf + 1;
     const float *part = p.part + (size_t)(wf + row) * PART;
-    // lane j < np: partial j's (m, l) per head (clamped addresses, masked)
+    // lane j: partial c0 + j's (m, l) per head (clamped addresses, masked)
     float mj[G], lj[G];
-    const float *pj = part + (size_t)min((uint32_t)lane, np - 1) * PART + G * D;
+    auto load_ml = [&](uint32_t c0) {
+        const float *pj = part + (size_t)min(c0 + (uint32_t)lane, np - 1) * PART + G * D;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        mj[h] = pj[2 * h];
-        lj[h] = pj[2 * h + 1];
-    }
+        for (int h = 0; h < G; h++) {
+            mj[h] = pj[2 * h];
+            lj[h] = pj[2 * h + 1];
+        }
+    };
+    load_ml(0);
     float ov[CH][EPL];
     auto load_o = [&](uint32_t i0) {
 #pragma unroll
@@ -760,10 +764,13 @@ __device__ __forceinline__ void merge_row_wave(const AttnParams &p, uint32_t b, 
     load_o(0);
     float M[G];
 #pragma unroll
-    for (int h = 0; h < G; h++) {
+    for (int h = 0; h < G; h++)
         M[h] = wave_max_f32((uint32_t)lane < np ? mj[h] : -INFINITY);
-        if ((uint32_t)lane >= np)
-            lj[h] = 0.f;
+    for (uint32_t c0 = 64; c0 < np; c0 += 64) {  // rows of more than 64 partials
+        const float *pj = part + (size_t)min(c0 + (uint32_t)lane, np - 1) * PART + G * D;
+#pragma unroll
+        for (int h = 0; h < G; h++)
+            M[h] = fmaxf(M[h], wave_max_f32(c0 + (uint32_t)lane < np ? pj[2 * h] : -INFINITY));
     }
     float L[G], O[EPL];
 #pragma unroll
@@ -772,25 +779,30 @@ __device__ __forceinline__ void merge_row_wave(const AttnParams &p, uint32_t b, 
 #pragma unroll
     for (int k = 0; k < EPL; k++)
         O[k] = 0.f;
-    for (uint32_t i0 = 0; i0 < np; i0 += CH) {
-        if (i0 > 0)
-            load_o(i0);
+    for (uint32_t c0 = 0; c0 < np; c0 += 64) {
+        if (c0 > 0)
+            load_ml(c0);
+        const uint32_t n = min(np - c0, 64u);
+        for (uint32_t i0 = 0; i0 < n; i0 += CH) {
+            if (c0 + i0 > 0)
+                load_o(c0 + i0);
 #pragma unroll
-        for (int c = 0; c < CH; c++) {
-            const uint32_t i = i0 + (uint32_t)c;
-            if (i >= np)
-                break;
-            float f[G];
+            for (int c = 0; c < CH; c++) {
+                const uint32_t i = i0 + (uint32_t)c;
+                if (i >= n)
+                    break;
+                float f[G];
 #pragma unroll
-            for (int h = 0; h < G; h++) {
-                const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mj[h]), (int)i));
-                const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj[h]), (int)i));
-                f[h] = m == -INFINITY ? 0.f : exp2f(m - M[h]);
-                L[h] = fmaf(l, f[h], L[h]);
+                for (int h = 0; h < G; h++) {
+                    const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mj[h]), (int)i));
+                    const float l = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lj[h]), (int)i));
+                    f[h] = m == -INFINITY ? 0.f : exp2f(m - M[h]);
+                    L[h] = fmaf(l, f[h], L[h]);
+                }
+#pragma unroll
+                for (int k = 0; k < EPL; k++)
+                    O[k] = fmaf(ov[c][k], f[(lane + 64 * k) / D], O[k]);
             }
-#pragma unroll
-            for (int k = 0; k < EPL; k++)
-                O[k] = fmaf(ov[c][k], f[(lane + 64 * k) / D], O[k]);
         }
     }
     const size_t obase = ((size_t)b * p.q_heads + (size_t)g * G) * D;

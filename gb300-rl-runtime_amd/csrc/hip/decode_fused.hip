@@ -27,6 +27,14 @@
 //  merge    merge_pieces_kernel: the split rows' partials combined by the
 //           same log-sum-exp as attn_merge_kernel, and the step's K/V token
 //           appended.
+//  pipeline rl_hip_decode_pipeline_step launches the fused kernel alone: its
+//           sampling waves first merge the previous step's split rows (one
+//           wave per row, merge_row_wave) and append that step's K/V token,
+//           so a step costs one launch. The lanes (two session streams) let
+//           the launch of step t + 1 start on the compute units that step t's
+//           last pieces leave idle: the end of a launch is uneven across the
+//           XCDs, and on one stream each launch waits for the previous one to
+//           finish.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -46,9 +54,9 @@ constexpr int kFThreads = kFWaves * 64;
 constexpr int kFStages = 2;                    // tile stages per wave (as attn_decode_kernel)
 constexpr uint32_t kFusedMaxBatch = 1024;      // rollouts whose tile prefix fits the LDS
 static_assert(kFThreads == kMergeThreads, "the sampling role runs the stream sampler's workgroup shape");
-// Quads per thread of the sampling role's chunks (16,384 logits): half the
-// stream kernel's, so that the two register buffers beside the attention
-// role's state stay within the 256 VGPRs of two waves per SIMD.
+// Quads per thread of the sampling role's chunks (16,384 logits, as the stream
+// kernel's): the two register buffers beside the attention role's state stay
+// within the 256 VGPRs of two waves per SIMD (16 quads spilled).
 constexpr int kFusedQuads = 8;
 
 // ---- the split of the tiles among the waves ------------------------------------

@@ -469,3 +469,52 @@ def test_fused_step_without_append(rl, gpu, orc, olib):
     assert np.array_equal(lp.download(np.float32, 8), res8[0][4])
     for b in (lg, tok, lp, sws):
         b.close()
+
+
+def test_fused_pipeline_long_rows(rl, gpu, orc, olib):
+    """Few rollouts with long contexts: 2 rollouts of ~4,000 tokens (16 rows
+    of ~250 tiles over 2,048 pieces, so every row is split over ~128 pieces,
+    more than one wave's 64 lanes) then 3 rollouts of ~3,000, pipelined and
+    flushed. The sampling waves' merge of the first step takes its partials
+    64 at a time: both steps' attention within 1e-4 of fp64, the arenas equal
+    the oracle's appends and the tokens the oracle's."""
+    QH, KVH, D, V = 32, 8, 128, 32000
+    rng = np.random.default_rng(8191)
+    wa = synth.make_decode(8192, 2, QH, KVH, D, 3900, 4100, reserve_tokens=4200)
+    wb = synth.make_decode(8193, 3, QH, KVH, D, 2900, 3100, reserve_tokens=4200)
+    mc = 4200
+    pa, pb = wa.ctx.copy(), wb.ctx.copy()
+    ka, va = _kv_rows(rng, wa)
+    kb, vb = _kv_rows(rng, wb)
+    A, Bt = _Batch(rl, wa, mc, pa, ka, va), _Batch(rl, wb, mc, pb, kb, vb)
+    lg = [rng.standard_normal((64, V), dtype=np.float32) for _ in range(2)]
+    seeds = rng.integers(0, 2**63, 64, dtype=np.uint64)
+    seed_buf = rl.DeviceBuffer.from_array(seeds)
+    lgb = [rl.DeviceBuffer.from_array(x) for x in lg]
+    tok = [rl.DeviceBuffer(64 * 4) for _ in range(2)]
+    lp = [rl.DeviceBuffer(64 * 4) for _ in range(2)]
+    samp = [rl.sample_args(lgb[i], 64, V, V, tok[i], lp[i], temperature=0.9, top_k=64, top_p=0.9, seeds=seed_buf,
+                           step=i) for i in range(2)]
+    n_ws = max(rl.decode_sample_step_workspace_bytes(bt.attn, samp[0]) for bt in (A, Bt))
+    ws = [rl.DeviceBuffer(n_ws) for _ in range(2)]
+    print("[fused] pipeline over long rows: A (2 x ~4,000), B (3 x ~3,000), flush", flush=True)
+    rl.decode_pipeline_step(A.attn, samp[0], ws[0])
+    rl.decode_pipeline_step(Bt.attn, samp[1], ws[1], A.attn, A.app, ws[0])
+    rl.decode_pipeline_flush(Bt.attn, Bt.app, ws[1])
+    rl.sync()
+    for name, bt, w in (("A", A, wa), ("B", Bt, wb)):
+        o16, o32 = bt.outputs()
+        gh.check_attn(o16, o32, orc.attn_f64(olib, w, 0), "bf16")
+    for bt, w, pos, k, v in ((A, wa, pa, ka, va), (Bt, wb, pb, kb, vb)):
+        want = w.arena.copy()
+        olib.orc_kv_append(want.ctypes.data, w.block_bytes, 16, D * 2, w.table.ctypes.data, w.table_stride,
+                           w.batch, KVH, pos.ctypes.data, None, k.ctypes.data, v.ctypes.data)
+        assert np.array_equal(bt.buf["arena"].download(np.uint8, w.arena.size), want)
+    for i in range(2):
+        want, wlp = orc.sample_rows(olib, lg[i], False, 0.9, 64, 0.9, seeds, i)
+        assert np.array_equal(tok[i].download(np.uint32, 64), want), i
+        assert np.abs(lp[i].download(np.float32, 64) - wlp).max() < 1e-4, i
+    for x in lgb + tok + lp + ws + [seed_buf]:
+        x.close()
+    A.close()
+    Bt.close()
