@@ -536,7 +536,12 @@ def wl_sample32k(args):
 def wl_longctx(args):
     """B=8, ctx 32,768, 64 q / 8 kv heads, d128, bf16 K/V ~N(0,1), permuted
     16-token blocks, split-KV over the whole device with the fp32 LSE merge;
-    then greedy over 8 x 128,256 fp32 logits ~N(0,1)."""
+    then greedy over 8 x 128,256 fp32 logits ~N(0,1). The step is
+    rl_hip_decode_sample_step without an append: GQA 64/8 is outside the fused
+    kernel, so the greedy sampler's slices ride in the attention's launch (as
+    workgroups after the attention's) and its row merges in the attention
+    merge's; the logits are an input, not the attention's output. The same
+    two calls one after the other are timed beside it."""
     bb, qh = 8, 64
     w = synth.make_decode(5, bb, qh, KVH, D, 32768, 32768, dtype="bf16")
     layout = rlrt.KvLayoutDesc.paged(TPB, D)
@@ -552,13 +557,17 @@ def wl_longctx(args):
     sws = rlrt.sample_workspace(s)
     attn_bytes = w.kv_bytes() + bb * qh * D * 2 * 2 + int((-(-w.ctx.astype(np.int64) // TPB)).sum()) * KVH * 4
     us_attn = _event_us(lambda i: rlrt.attn_decode(a), args.steps)
-    us_step = _event_us(lambda i: (rlrt.attn_decode(a), rlrt.sample(s)), args.steps)
+    us_seq = _event_us(lambda i: (rlrt.attn_decode(a), rlrt.sample(s)), args.steps)
+    fws = rlrt.decode_sample_step_workspace(a, s)
+    us_step = _event_us(lambda i: rlrt.decode_sample_step(a, None, s, fws), args.steps)
     step_bytes = attn_bytes + bb * VOCAB * 4
     return {"workload": "gqa_decode_b8_q64kv8_d128_ctx32768 + greedy_b8_v128256",
             "attn_us": us_attn, "attn_alg_bytes": attn_bytes, "attn_gbps": attn_bytes / (us_attn * 1e-6) / 1e9,
             "attn_frac": attn_bytes / (us_attn * 1e-6) / 1e9 / PEAK_HBM_GBPS,
             "step_us": us_step, "steps_per_s": 1e6 / us_step, "tokens_per_s": bb * 1e6 / us_step,
-            "step_gbps": step_bytes / (us_step * 1e-6) / 1e9}
+            "step_gbps": step_bytes / (us_step * 1e-6) / 1e9, "step_two_calls_us": us_seq,
+            "step": "rl_hip_decode_sample_step(attn, NULL append, greedy): the sampler's slices ride in the "
+                    "attention launch, its row merges in the attention merge launch"}
 
 
 def wl_proj(args):

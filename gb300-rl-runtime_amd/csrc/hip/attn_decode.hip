@@ -45,8 +45,20 @@
 #include "rl_hip.h"
 #include "rl_hip_internal.h"
 #include "kv_append_core.h"
+#include "sample_core.h"
 
 namespace {
+
+// Greedy sampling that rides in the attention's launches (sp.splits == 0:
+// none): workgroups attn_wgs and up of the attention kernel each run one
+// slice of a row (split_slice), after every attention workgroup has been
+// placed, so they take compute units as the attention's last waves retire;
+// rows of the merge grid past the batch each merge greedy rows, one wave per
+// row (greedy_merge_row). The kernel boundary between the two orders them.
+struct SideSample {
+    SampleParams sp;
+    uint32_t attn_wgs;
+};
 
 // Stages of the per-wave tile ring. Two (one tile in flight while one is
 // consumed) with two workgroups per CU measured faster than four stages with
@@ -63,16 +75,15 @@ constexpr int stages_of()
 // index gives XCD x a contiguous eighth of the tile sequence, so rows that
 // read the same KV blocks (the rollouts of a group over a shared prefix, which
 // sit next to each other in the sequence) stream them through one L2.
-__device__ __forceinline__ uint32_t xcd_contiguous_wg()
+__device__ __forceinline__ uint32_t xcd_contiguous_wg(uint32_t n)
 {
-    const uint32_t n = gridDim.x;
     if (n % 8 != 0)
         return blockIdx.x;
     return (blockIdx.x % 8) * (n / 8) + blockIdx.x / 8;
 }
 
 template <int D, int G, int DT, int TPB>
-__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
+__global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p, SideSample ss)
 {
     using C = Cfg<D, G, DT, TPB>;
     constexpr int W = C::W;
@@ -81,9 +92,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(AttnParams p)
     __shared__ __attribute__((aligned(1024))) uint8_t lds_st[NS][W * C::STAGE];
     __shared__ __attribute__((aligned(1024))) uint8_t lds_q[W * NS * C::QSLOT];
 
+    if (blockIdx.x >= ss.attn_wgs) {  // a slice of the greedy sampling riding in this launch
+        const uint32_t e = blockIdx.x - ss.attn_wgs;
+        split_slice(ss.sp, e % ss.sp.splits, e / ss.sp.splits, *reinterpret_cast<SplitLds *>(lds_q));
+        return;
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t wg = xcd_contiguous_wg();
+    const uint32_t wg = xcd_contiguous_wg(ss.attn_wgs);
 
     // ---- plan: tile prefix over rollouts, each wave's starting rollout -------
     // (q slot memory doubles as scratch until the copies start)
@@ -176,9 +192,15 @@ constexpr int merge_heads_of()
 }
 
 template <int D, int G, int DT, int HS>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, AppendParams ap)
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, AppendParams ap, SideSample ss)
 {
     constexpr int GH = G / HS;
+    if (blockIdx.y >= p.batch) {  // greedy rows of the sampling riding in this launch, one wave each
+        const uint32_t r = ((blockIdx.y - p.batch) * gridDim.x + blockIdx.x) * 4 + (threadIdx.x >> 6);
+        if (r < ss.sp.rows)
+            greedy_merge_row(ss.sp, r, (int)(threadIdx.x & 63), true);
+        return;
+    }
     __shared__ float s_f[kMergeLds * G];
     __shared__ float s_L[G];
     const uint32_t g = blockIdx.x / HS;
@@ -243,46 +265,52 @@ WsLayout ws_layout(const rl_attn_decode_args_t *a)
 }
 
 template <int D, int G, int DT, int TPB>
-int launch(const AttnParams &p, const AppendParams &ap)
+int launch(const AttnParams &p, const AppendParams &ap, SideSample ss)
 {
     using C = Cfg<D, G, DT, TPB>;
     const uint32_t wgs = (p.nwaves + C::W - 1) / C::W;
-    hipLaunchKernelGGL((attn_decode_kernel<D, G, DT, TPB>), dim3(wgs), dim3(C::W * 64), 0, rl_stream(), p);
+    ss.attn_wgs = wgs;
+    const uint32_t slices = ss.sp.splits * ss.sp.rows;  // 0 without a side sampling
+    hipLaunchKernelGGL((attn_decode_kernel<D, G, DT, TPB>), dim3(wgs + slices), dim3(C::W * 64), 0, rl_stream(), p,
+                       ss);
     if (rl_check_launch("attn_decode_kernel launch"))
         return -1;
     // Rows averaging 8 or more partials (waves per row) take workgroups of
     // two heads; shorter rows one workgroup per row, whose partials arrive
-    // in one batch of loads.
+    // in one batch of loads. Greedy rows of a side sampling: four per
+    // workgroup in extra grid rows.
     constexpr int HS = merge_heads_of<G>();
-    if (HS > 1 && (uint64_t)p.nwaves >= 8ull * p.batch * p.kv_heads)
-        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, HS>), dim3(p.kv_heads * HS, p.batch), dim3(256), 0,
-                           rl_stream(), p, ap);
+    const bool hs = HS > 1 && (uint64_t)p.nwaves >= 8ull * p.batch * p.kv_heads;
+    const uint32_t gx = hs ? p.kv_heads * HS : p.kv_heads;
+    const uint32_t gy = p.batch + (slices ? (ss.sp.rows + 4 * gx - 1) / (4 * gx) : 0u);
+    if (hs)
+        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, HS>), dim3(gx, gy), dim3(256), 0, rl_stream(), p, ap, ss);
     else
-        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, 1>), dim3(p.kv_heads, p.batch), dim3(256), 0, rl_stream(),
-                           p, ap);
+        hipLaunchKernelGGL((attn_merge_kernel<D, G, DT, 1>), dim3(gx, gy), dim3(256), 0, rl_stream(), p, ap, ss);
     return rl_check_launch("attn_merge_kernel launch");
 }
 
 template <int D, int G, int DT>
-int dispatch_tpb(const AttnParams &p, const AppendParams &ap, uint32_t tpb)
+int dispatch_tpb(const AttnParams &p, const AppendParams &ap, const SideSample &ss, uint32_t tpb)
 {
-    return tpb == 16 ? launch<D, G, DT, 16>(p, ap) : launch<D, G, DT, 32>(p, ap);
+    return tpb == 16 ? launch<D, G, DT, 16>(p, ap, ss) : launch<D, G, DT, 32>(p, ap, ss);
 }
 
 template <int D, int G>
-int dispatch_dt(const AttnParams &p, const AppendParams &ap, uint32_t dt, uint32_t tpb)
+int dispatch_dt(const AttnParams &p, const AppendParams &ap, const SideSample &ss, uint32_t dt, uint32_t tpb)
 {
-    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, ap, tpb) : dispatch_tpb<D, G, 1>(p, ap, tpb);
+    return dt == RL_DTYPE_BF16 ? dispatch_tpb<D, G, 0>(p, ap, ss, tpb) : dispatch_tpb<D, G, 1>(p, ap, ss, tpb);
 }
 
 template <int D>
-int dispatch_g(const AttnParams &p, const AppendParams &ap, uint32_t G, uint32_t dt, uint32_t tpb)
+int dispatch_g(const AttnParams &p, const AppendParams &ap, const SideSample &ss, uint32_t G, uint32_t dt,
+               uint32_t tpb)
 {
     switch (G) {
-    case 1: return dispatch_dt<D, 1>(p, ap, dt, tpb);
-    case 2: return dispatch_dt<D, 2>(p, ap, dt, tpb);
-    case 4: return dispatch_dt<D, 4>(p, ap, dt, tpb);
-    default: return dispatch_dt<D, 8>(p, ap, dt, tpb);
+    case 1: return dispatch_dt<D, 1>(p, ap, ss, dt, tpb);
+    case 2: return dispatch_dt<D, 2>(p, ap, ss, dt, tpb);
+    case 4: return dispatch_dt<D, 4>(p, ap, ss, dt, tpb);
+    default: return dispatch_dt<D, 8>(p, ap, ss, dt, tpb);
     }
 }
 
@@ -352,7 +380,18 @@ extern "C" size_t rl_hip_attn_decode_workspace(const rl_attn_decode_args_t *a)
 
 namespace {
 
-int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap, const uint32_t *row_map = nullptr)
+SideSample no_side()
+{
+    SideSample ss;
+    ss.sp = SampleParams{};
+    ss.sp.splits = 0;
+    ss.sp.rows = 0;
+    ss.attn_wgs = 0;
+    return ss;
+}
+
+int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap, const uint32_t *row_map = nullptr,
+             const SideSample &ss = no_side())
 {
     const WsLayout w = ws_layout(a);
     if (!a->workspace || a->workspace_bytes < w.total) {
@@ -383,8 +422,8 @@ int attn_run(const rl_attn_decode_args_t *a, const AppendParams &ap, const uint3
 
     const uint32_t G = a->q_heads / a->kv_heads;
     if (a->layout.head_dim == 128)
-        return dispatch_g<128>(p, ap, G, a->dtype, a->layout.token_count);
-    return dispatch_g<64>(p, ap, G, a->dtype, a->layout.token_count);
+        return dispatch_g<128>(p, ap, ss, G, a->dtype, a->layout.token_count);
+    return dispatch_g<64>(p, ap, ss, G, a->dtype, a->layout.token_count);
 }
 
 }  // namespace
@@ -442,6 +481,29 @@ int rl_decode_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_append_
     AppendParams ap = append_params(append);
     ap.row_map = row_map;
     return attn_run(attn, ap, row_map);
+}
+
+int rl_decode_step_greedy_side(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                               const rl_sample_args_t *samp)
+{
+    const char *who = "rl_hip_decode_sample_step";
+    if (append ? step_validate(attn, append, who) : (rl_require_open(who) || validate(attn)))
+        return -1;
+    uint32_t splits = 0;
+    size_t cand_off = 0;
+    const int k = rl_sample_greedy_split(samp, &splits, &cand_off);
+    if (k <= 0)
+        return k < 0 ? -1 : 1;
+    SideSample ss = no_side();
+    ss.sp = sample_params_of(samp);
+    ss.sp.splits = splits;
+    ss.sp.stats = (SplitStat *)samp->workspace;  // the slice records start the sampler's workspace
+    ss.sp.cand = (uint2 *)((uint8_t *)samp->workspace + cand_off);
+    AppendParams ap = {};
+    ap.arena = nullptr;
+    if (append)
+        ap = append_params(append);
+    return attn_run(attn, ap, nullptr, ss);
 }
 
 int rl_attn_mapped(const rl_attn_decode_args_t *attn, const uint32_t *row_map)

@@ -593,14 +593,26 @@ int decode_sample_step_rows(const rl_attn_decode_args_t *attn, const rl_kv_appen
         return -1;
     }
     if (!fused_eligible(attn)) {
-        // one decode step (or the attention alone), then the sampling, on
-        // the library stream. (Running the sampler on a second stream beside
-        // the attention or its merge made the step slower: the cross-stream
-        // event waits cost more than the overlap saved.)
+        // One decode step (or the attention alone), then the sampling, on
+        // the library stream. A greedy batch that the sampler splits rides
+        // in the attention's two launches instead: its slices as workgroups
+        // after the attention's (they take compute units as the attention's
+        // last waves retire), its row merges in the attention merge's grid.
+        // (Running the sampler on a second stream beside the attention or
+        // its merge made the step slower: the cross-stream event waits cost
+        // more than the overlap saved.)
         const size_t a_bytes = (rl_hip_attn_decode_workspace(attn) + 255) / 256 * 256;
         rl_attn_decode_args_t a = *attn;
         a.workspace = workspace;
         a.workspace_bytes = a_bytes;
+        if (!row_map) {
+            rl_sample_args_t s = *samp;
+            s.workspace = (uint8_t *)workspace + a_bytes;
+            s.workspace_bytes = workspace_bytes - a_bytes;
+            const int k = rl_decode_step_greedy_side(&a, append, &s);
+            if (k <= 0)
+                return k;
+        }
         int rc;
         if (row_map)
             rc = append ? rl_decode_step_mapped(&a, append, row_map) : rl_attn_mapped(&a, row_map);

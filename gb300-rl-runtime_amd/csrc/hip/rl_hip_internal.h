@@ -40,6 +40,18 @@ int rl_decode_sample_step_mapped(const rl_attn_decode_args_t *attn, const rl_kv_
 int rl_attn_check(const rl_attn_decode_args_t *a);
 int rl_decode_step_check(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append, const char *who);
 int rl_sample_check(const rl_sample_args_t *a);
+// For a greedy batch (a->greedy set) that rl_hip_sample runs as split +
+// merge: 1, with the slices per row and the offset of the candidate lists in
+// its workspace (the slice records start at 0); 0 when the batch takes
+// another path; -1 (error set) for invalid arguments or a short workspace.
+int rl_sample_greedy_split(const rl_sample_args_t *a, uint32_t *splits, size_t *cand_off);
+// rl_hip_decode_step (rl_hip_attn_decode when append is NULL) with the greedy
+// sampling of `samp` riding in its launches: the slices as extra workgroups
+// after the attention's, the row merges as extra workgroups of the attention
+// merge. Results equal the two calls'. 1 when samp is not such a batch
+// (nothing launched), 0 on success, -1 on error (attn_decode.hip).
+int rl_decode_step_greedy_side(const rl_attn_decode_args_t *attn, const rl_kv_append_args_t *append,
+                               const rl_sample_args_t *samp);
 
 // Reports a launch error (or a fault of an earlier asynchronous call).
 static inline int rl_check_launch(const char *what)

@@ -55,188 +55,8 @@ namespace {
 
 __global__ __launch_bounds__(kThreads) void sample_split_kernel(SampleParams p)
 {
-    const uint32_t split = blockIdx.x;
-    const uint32_t row = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    __shared__ float s_red[4];
-    __shared__ uint32_t s_red_i[4];
-    __shared__ float s_z[4];
-    __shared__ uint32_t s_key[4];
-    __shared__ uint32_t s_wtot[4];
-
-    const float *lrow = p.logits + (size_t)row * p.row_stride;
-    const uint32_t c0 = split * kSplitLen;
-    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
-    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
-
-    // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
-    // Every load is issued unconditionally (a quad past the end re-reads the
-    // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
-    // masked afterwards, so all eight are in flight together. Only the last
-    // slice of a row can reach past the vocabulary (a workgroup-uniform test).
-    float x[kPerThread];
-    const uint32_t last_quad = (p.vocab - 1) & ~3u;
-    rl_f32x4 raw[kPerThread / 4];
-#pragma unroll
-    for (int k = 0; k < kPerThread / 4; k++) {
-        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
-        raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
-    }
-    // the row's Philox draw, for the merge (computed while the loads are in flight)
-    uint64_t draw = 0;
-    if (split == 0 && !greedy && wave == 0)
-        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row_draw_id(p, row));
-    if (c0 + (uint32_t)kSplitLen <= p.vocab) {
-#pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++)
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                x[k * 4 + e] = raw[k][e];
-    } else {
-#pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++) {
-            const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                x[k * 4 + e] = col + (uint32_t)e < p.vocab ? raw[k][e] : -INFINITY;
-        }
-    }
-
-    SplitStat *st = p.stats + (size_t)row * p.splits + split;
-
-    if (greedy) {
-        float best = -INFINITY;
-        uint32_t bidx = 0xFFFFFFFFu;
-#pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float v = x[k * 4 + e];
-                if (v > best) {
-                    best = v;
-                    bidx = c0 + (uint32_t)(k * kThreads + tid) * 4u + e;
-                }
-            }
-        wave_argmax(best, bidx);
-        if (lane == 0) {
-            s_red[wave] = best;
-            s_red_i[wave] = bidx;
-        }
-        __syncthreads();
-        float m = s_red[0];
-        uint32_t mi = s_red_i[0];
-#pragma unroll
-        for (int w = 1; w < 4; w++)
-            if (s_red[w] > m || (s_red[w] == m && s_red_i[w] < mi)) {
-                m = s_red[w];
-                mi = s_red_i[w];
-            }
-        float z = 0.f;
-        if (m != -INFINITY) {
-            const float ml = m * 1.4426950408889634f;
-#pragma unroll
-            for (int i = 0; i < kPerThread; i++)
-                z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
-        }
-        z = wave_sum(z);
-        if (lane == 0)
-            s_z[wave] = z;
-        __syncthreads();
-        if (tid == 0) {
-            st->max_x = m;
-            st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
-            st->arg_val = m;
-            st->arg_idx = mi;
-            st->n_cand = 0;
-        }
-        return;
-    }
-
-    // ---- sampling: x = l * inv_t, slice max, sum exp, candidates -------------
-    // Two barriers: (1) wave maxima and k-th bounds, (2) wave sums and
-    // candidate counts; the candidates are then written at their offsets.
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kPerThread; i++) {
-        x[i] = x[i] * inv_t;
-        tmax = fmaxf(tmax, x[i]);
-    }
-    const float wmax = wave_max(tmax);
-    const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
-    if (k_eff != 0) {
-        const uint32_t kw = (k_eff + 3) / 4;
-        const uint32_t ck = wave_kth_largest_key(rl_float_key(tmax), kw);
-        if (lane == 0)
-            s_key[wave] = ck;
-    }
-    if (lane == 0)
-        s_red[wave] = wmax;
-    __syncthreads();
-    const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-    float z = 0.f;
-    if (m != -INFINITY) {
-        const float ml = m * 1.4426950408889634f;
-#pragma unroll
-        for (int i = 0; i < kPerThread; i++)
-            z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
-    }
-    z = wave_sum(z);
-    if (lane == 0)
-        s_z[wave] = z;
-
-    // Candidates: key(x) >= clb and x != -inf. For x not NaN that is x >= t
-    // with t = the float of clb (the key order is the float order with -0 =
-    // +0), t raised to -FLT_MAX when clb is the key of -inf; a NaN x has a key
-    // above every non-NaN key, and !(x < t) keeps it too.
-    uint32_t cand_lo = 0, cnt = 0, incl = 0;
-    float t = 0.f;
-    if (k_eff != 0) {
-        const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
-        cand_lo = clb;
-        t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
-#pragma unroll
-        for (int i = 0; i < kPerThread; i++)
-            cnt += !(x[i] < t) ? 1u : 0u;
-        incl = cnt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const uint32_t o = __shfl_up(incl, off);
-            if (lane >= off)
-                incl += o;
-        }
-        if (lane == 63)
-            s_wtot[wave] = incl;
-    }
-    __syncthreads();
-    if (k_eff != 0 && cnt) {
-        uint32_t base = incl - cnt;
-        for (int w = 0; w < wave; w++)
-            base += s_wtot[w];
-        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandStride;
-#pragma unroll
-        for (int k = 0; k < kPerThread / 4; k++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const float v = x[k * 4 + e];
-                if (!(v < t)) {
-                    if (base < (uint32_t)kCandCap)
-                        cand[base] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
-                    base++;
-                }
-            }
-    }
-    if (tid == 0) {
-        st->max_x = m;
-        st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
-        st->arg_val = m;
-        st->arg_idx = 0;
-        st->n_cand = k_eff != 0 ? s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3] : 0u;
-        st->cand_lo = cand_lo;
-        st->draw = draw;
-    }
+    __shared__ SplitLds L;
+    split_slice(p, blockIdx.x, blockIdx.y, L);
 }
 
 // One workgroup of kMergeThreads threads per row.
@@ -262,6 +82,10 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     const SplitStat *st = p.stats + (size_t)row * p.splits;
     const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
     const uint32_t wave = tid >> 6;
+    if (greedy) {
+        greedy_merge_row(p, row, lane, tid == 0);
+        return;
+    }
 
     // Issued before the slice statistics are known, so that the latencies
     // overlap: this wave's first 256 candidates of the lists of splits w and
@@ -269,9 +93,8 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     // and the row's Philox draw (computed by the row's first split).
     const uint2 *rbase = p.cand + (size_t)row * p.splits * kCandStride;
     uint2 pv[8];
-    uint64_t draw = 0;
-    if (!greedy) {
-        draw = st[0].draw;
+    const uint64_t draw = st[0].draw;
+    {
         const uint2 *pf1 = rbase + (size_t)min(wave, p.splits - 1) * kCandStride;
         const uint2 *pf2 = rbase + (size_t)min(wave + kMergeWaves, p.splits - 1) * kCandStride;
 #pragma unroll
@@ -285,14 +108,11 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
     // every wave computes the same values).
     float mx = -INFINITY, zs = 0.f;
     uint32_t ncand = 0;
-    float av = -INFINITY;
-    uint32_t ai = 0xFFFFFFFFu, clo = 0xFFFFFFFFu;
+    uint32_t clo = 0xFFFFFFFFu;
     if ((uint32_t)lane < p.splits) {
         mx = st[lane].max_x;
         zs = st[lane].sum_exp;
         ncand = st[lane].n_cand;
-        av = st[lane].arg_val;
-        ai = st[lane].arg_idx;
         clo = st[lane].cand_lo;
     }
     const float m = wave_max(mx);
@@ -301,18 +121,6 @@ __global__ __launch_bounds__(kMergeThreads) void sample_merge_kernel(SampleParam
         const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
         return m + logf(wave_sum(zterm));
     };
-
-    if (greedy) {
-        const float lse = row_lse();
-        wave_argmax(av, ai);
-        if (tid == 0) {
-            const uint32_t i = ai >= p.vocab ? 0u : ai;  // all -inf: lowest index
-            p.token_out[row] = i;
-            // av is the logit at i (for a row of -inf, logit 0 is -inf too): no reload
-            p.logprob_out[row] = av - lse;
-        }
-        return;
-    }
 
     const float inv_t = 1.0f / row_temperature(p, row);
     const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
@@ -985,6 +793,24 @@ int validate(const rl_sample_args_t *a)
 int rl_sample_check(const rl_sample_args_t *a)
 {
     return validate(a);
+}
+
+int rl_sample_greedy_split(const rl_sample_args_t *a, uint32_t *splits, size_t *cand_off)
+{
+    if (validate(a))
+        return -1;
+    const WsLayout w = ws_layout(a);
+    if (!a->workspace || a->workspace_bytes < w.total) {
+        rl_set_error("rl_hip_sample: workspace %zu bytes < %zu required", a->workspace_bytes, w.total);
+        return -1;
+    }
+    // rl_hip_sample's choice: greedy batches of rows above kRowVocab logits
+    // take split + merge
+    if (!a->greedy || a->vocab <= kRowVocab)
+        return 0;
+    *splits = splits_for(a->vocab);
+    *cand_off = w.cand_off;
+    return 1;
 }
 
 extern "C" size_t rl_hip_sample_workspace(const rl_sample_args_t *a)

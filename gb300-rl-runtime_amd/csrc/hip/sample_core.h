@@ -1035,6 +1035,231 @@ __device__ __forceinline__ TopkPick topk_pick(uint32_t nf, uint32_t k_eff, int h
     return TopkPick{tok, xtok, xknown, exact};
 }
 
+// ---- split: one slice of a row per workgroup (sample_split_kernel) -----------
+// LDS of one slice's workgroup: per-wave maxima, argmax indexes, exp sums,
+// candidate bounds and candidate counts.
+struct SplitLds {
+    float s_red[4];
+    uint32_t s_red_i[4];
+    float s_z[4];
+    uint32_t s_key[4];
+    uint32_t s_wtot[4];
+};
+
+// One slice of the split kernel: slice `split` of row `row`, by the calling
+// workgroup of kThreads threads (every thread calls it); L in LDS.
+__device__ __forceinline__ void split_slice(const SampleParams &p, uint32_t split, uint32_t row, SplitLds &L)
+{
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    float *s_red = L.s_red;
+    uint32_t *s_red_i = L.s_red_i;
+    float *s_z = L.s_z;
+    uint32_t *s_key = L.s_key;
+    uint32_t *s_wtot = L.s_wtot;
+
+    const float *lrow = p.logits + (size_t)row * p.row_stride;
+    const uint32_t c0 = split * kSplitLen;
+    const bool greedy = p.greedy != 0 || !(row_temperature(p, row) > 0.f);
+    const float inv_t = greedy ? 1.0f : 1.0f / row_temperature(p, row);
+
+    // Stream the slice: element (k, e) of thread tid is column c0 + (k*256 + tid)*4 + e.
+    // Every load is issued unconditionally (a quad past the end re-reads the
+    // row's last quad, which row_stride % 4 == 0 keeps inside the row) and
+    // masked afterwards, so all eight are in flight together. Only the last
+    // slice of a row can reach past the vocabulary (a workgroup-uniform test).
+    float x[kPerThread];
+    const uint32_t last_quad = (p.vocab - 1) & ~3u;
+    rl_f32x4 raw[kPerThread / 4];
+#pragma unroll
+    for (int k = 0; k < kPerThread / 4; k++) {
+        const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
+        raw[k] = __builtin_nontemporal_load((const rl_f32x4 *)(lrow + min(col, last_quad)));
+    }
+    // the row's Philox draw, for the merge (computed while the loads are in flight)
+    uint64_t draw = 0;
+    if (split == 0 && !greedy && wave == 0)
+        draw = rl_sample_draw64(row_seed(p, row), row_step(p, row), row_draw_id(p, row));
+    if (c0 + (uint32_t)kSplitLen <= p.vocab) {
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                x[k * 4 + e] = raw[k][e];
+    } else {
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++) {
+            const uint32_t col = c0 + (uint32_t)(k * kThreads + tid) * 4u;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                x[k * 4 + e] = col + (uint32_t)e < p.vocab ? raw[k][e] : -INFINITY;
+        }
+    }
+
+    SplitStat *st = p.stats + (size_t)row * p.splits + split;
+
+    if (greedy) {
+        float best = -INFINITY;
+        uint32_t bidx = 0xFFFFFFFFu;
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v = x[k * 4 + e];
+                if (v > best) {
+                    best = v;
+                    bidx = c0 + (uint32_t)(k * kThreads + tid) * 4u + e;
+                }
+            }
+        wave_argmax(best, bidx);
+        if (lane == 0) {
+            s_red[wave] = best;
+            s_red_i[wave] = bidx;
+        }
+        __syncthreads();
+        float m = s_red[0];
+        uint32_t mi = s_red_i[0];
+#pragma unroll
+        for (int w = 1; w < 4; w++)
+            if (s_red[w] > m || (s_red[w] == m && s_red_i[w] < mi)) {
+                m = s_red[w];
+                mi = s_red_i[w];
+            }
+        float z = 0.f;
+        if (m != -INFINITY) {
+            const float ml = m * 1.4426950408889634f;
+#pragma unroll
+            for (int i = 0; i < kPerThread; i++)
+                z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
+        }
+        z = wave_sum(z);
+        if (lane == 0)
+            s_z[wave] = z;
+        __syncthreads();
+        if (tid == 0) {
+            st->max_x = m;
+            st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
+            st->arg_val = m;
+            st->arg_idx = mi;
+            st->n_cand = 0;
+        }
+        return;
+    }
+
+    // ---- sampling: x = l * inv_t, slice max, sum exp, candidates -------------
+    // Two barriers: (1) wave maxima and k-th bounds, (2) wave sums and
+    // candidate counts; the candidates are then written at their offsets.
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kPerThread; i++) {
+        x[i] = x[i] * inv_t;
+        tmax = fmaxf(tmax, x[i]);
+    }
+    const float wmax = wave_max(tmax);
+    const uint32_t k_eff = effective_k(row_topk(p, row), p.vocab);
+    if (k_eff != 0) {
+        const uint32_t kw = (k_eff + 3) / 4;
+        const uint32_t ck = wave_kth_largest_key(rl_float_key(tmax), kw);
+        if (lane == 0)
+            s_key[wave] = ck;
+    }
+    if (lane == 0)
+        s_red[wave] = wmax;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+    float z = 0.f;
+    if (m != -INFINITY) {
+        const float ml = m * 1.4426950408889634f;
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++)
+            z += __builtin_amdgcn_exp2f(fmaf(x[i], 1.4426950408889634f, -ml));
+    }
+    z = wave_sum(z);
+    if (lane == 0)
+        s_z[wave] = z;
+
+    // Candidates: key(x) >= clb and x != -inf. For x not NaN that is x >= t
+    // with t = the float of clb (the key order is the float order with -0 =
+    // +0), t raised to -FLT_MAX when clb is the key of -inf; a NaN x has a key
+    // above every non-NaN key, and !(x < t) keeps it too.
+    uint32_t cand_lo = 0, cnt = 0, incl = 0;
+    float t = 0.f;
+    if (k_eff != 0) {
+        const uint32_t clb = min(min(s_key[0], s_key[1]), min(s_key[2], s_key[3]));
+        cand_lo = clb;
+        t = clb == rl_float_key(-INFINITY) ? -__FLT_MAX__ : rl_key_float(clb);
+#pragma unroll
+        for (int i = 0; i < kPerThread; i++)
+            cnt += !(x[i] < t) ? 1u : 0u;
+        incl = cnt;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const uint32_t o = __shfl_up(incl, off);
+            if (lane >= off)
+                incl += o;
+        }
+        if (lane == 63)
+            s_wtot[wave] = incl;
+    }
+    __syncthreads();
+    if (k_eff != 0 && cnt) {
+        uint32_t base = incl - cnt;
+        for (int w = 0; w < wave; w++)
+            base += s_wtot[w];
+        uint2 *cand = p.cand + ((size_t)row * p.splits + split) * kCandStride;
+#pragma unroll
+        for (int k = 0; k < kPerThread / 4; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float v = x[k * 4 + e];
+                if (!(v < t)) {
+                    if (base < (uint32_t)kCandCap)
+                        cand[base] = make_uint2(rl_float_key(v), c0 + (uint32_t)(k * kThreads + tid) * 4u + e);
+                    base++;
+                }
+            }
+    }
+    if (tid == 0) {
+        st->max_x = m;
+        st->sum_exp = s_z[0] + s_z[1] + s_z[2] + s_z[3];
+        st->arg_val = m;
+        st->arg_idx = 0;
+        st->n_cand = k_eff != 0 ? s_wtot[0] + s_wtot[1] + s_wtot[2] + s_wtot[3] : 0u;
+        st->cand_lo = cand_lo;
+        st->draw = draw;
+    }
+}
+
+// The merge of a greedy row split into p.splits slices (at most 64), by one
+// wave: the row's log-sum-exp from the slices' (max, exp-sum) and the lowest
+// index holding the row's maximum; lane 0 writes the token and logprob when
+// `writer` is set.
+__device__ __forceinline__ void greedy_merge_row(const SampleParams &p, uint32_t row, int lane, bool writer)
+{
+    const SplitStat *st = p.stats + (size_t)row * p.splits;
+    float mx = -INFINITY, zs = 0.f;
+    float av = -INFINITY;
+    uint32_t ai = 0xFFFFFFFFu;
+    if ((uint32_t)lane < p.splits) {
+        mx = st[lane].max_x;
+        zs = st[lane].sum_exp;
+        av = st[lane].arg_val;
+        ai = st[lane].arg_idx;
+    }
+    const float m = wave_max(mx);
+    const float zterm = (mx == -INFINITY) ? 0.f : zs * exp2f((mx - m) * 1.4426950408889634f);
+    const float lse = m + logf(wave_sum(zterm));
+    wave_argmax(av, ai);
+    if (writer && lane == 0) {
+        const uint32_t i = ai >= p.vocab ? 0u : ai;  // all -inf: lowest index
+        p.token_out[row] = i;
+        // av is the logit at i (for a row of -inf, logit 0 is -inf too): no reload
+        p.logprob_out[row] = av - lse;
+    }
+}
+
 // ---- one workgroup per row, the row streamed in chunks (rows with top-k) -----
 // Thread t's quad j of chunk c holds the logits from 2,048 Q c + (512 j + t)
 // * 4 (Q quads per thread per chunk), so each wave's load instruction reads

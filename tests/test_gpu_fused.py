@@ -518,3 +518,36 @@ def test_fused_pipeline_long_rows(rl, gpu, orc, olib):
         x.close()
     A.close()
     Bt.close()
+
+
+def test_fused_greedy_rides_in_the_attention(rl, gpu, orc, olib):
+    """GQA 64/8 (outside the fused kernel) with the KV append and greedy over
+    12 rows of 50,000 logits: the sampler's slices run as workgroups after
+    the attention's and its row merges in the attention merge's grid (three
+    rows per extra workgroup row). Attention, arena, tokens and logprobs
+    equal rl_hip_decode_step then rl_hip_sample bit for bit (attention within
+    1e-4 of fp64, the arena equal to the oracle's append, tokens equal to the
+    oracle's), on two calls in a row."""
+    B, V, R = 8, 50000, 12
+    w = synth.make_decode(8201, B, 64, 8, 128, 100, 2000)
+    rng = np.random.default_rng(8202)
+    pos = w.ctx.copy()
+    kn, vn = _kv_rows(rng, w)
+    logits = rng.standard_normal((R, V), dtype=np.float32)
+    logits[3, [5, 17, 49999]] = np.float32(9.0)          # a tie: lowest index
+    logits[7, :40000] = -np.inf                           # -inf over the first slices
+    res = _run(rl, w, int(w.ctx.max()), pos, None, kn, vn, logits, repeats=2, greedy=True)
+    want, wlp = orc.sample_rows(olib, logits, True, 1.0, 0, 1.0, 0, 0)
+    _check(orc, olib, w, int(w.ctx.max()), pos, None, kn, vn, logits, res, want, wlp)
+    assert res[0][3][3] == 5 and res[0][3][7] >= 40000
+    o16, o32 = gh.run_attn(rl, w)
+    assert np.array_equal(res[0][0], o16) and np.array_equal(res[0][1], o32)
+    lg, tok, lp = rl.DeviceBuffer.from_array(logits), rl.DeviceBuffer(R * 4), rl.DeviceBuffer(R * 4)
+    s = rl.sample_args(lg, R, V, V, tok, lp, greedy=True)
+    sws = rl.sample_workspace(s)
+    rl.sample(s)
+    rl.sync()
+    assert np.array_equal(tok.download(np.uint32, R), res[0][3])
+    assert np.array_equal(lp.download(np.float32, R).view(np.uint32), res[0][4].view(np.uint32))
+    for b in (lg, tok, lp, sws):
+        b.close()
