@@ -344,24 +344,22 @@ def _next_step(rl, first, w, mc, q2, pos2, k2, v2):
     return nxt
 
 
-def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
-    """Four micro-batches (64, 48, 64 and 33 rollouts) for two steps each on
-    the two lanes: step t runs micro-batch t % 4 on lane t % 2 and merges step
-    t - 2; the last two steps are flushed on their lanes, then joined. The
-    outputs, arenas and tokens equal the same sequence of
-    rl_hip_decode_pipeline_step calls on the library stream bit for bit (the
-    lanes change where steps run, not what they compute), every attention is
-    within 1e-4 of fp64, the arenas equal the oracle's two appends and every
-    step's tokens equal the oracle's."""
-    QH, KVH, D, V, mc = 32, 8, 128, 32000, 1300
-    rng = np.random.default_rng(9161)
-    sizes = (64, 48, 64, 33)
-    ws_ = [synth.make_decode(9162 + m, n, QH, KVH, D, 1 if m % 2 else 300, 1200, reserve_tokens=1300)
-           for m, n in enumerate(sizes)]
+def _lanes_case(rl, orc, olib, QH, KVH, D, dtype, tc, sizes, ctx_hi, seed, V=32000):
+    """Four micro-batches (batches `sizes`, ctx U[1 or 300, ctx_hi]) for two
+    steps each on the two lanes (step t: micro-batch t % 4 on lane t % 2,
+    merging step t - 2; the last two flushed, then joined), against the same
+    calls on the library stream bit for bit, fp64, the oracle's appends and
+    the oracle's tokens."""
+    code = rl.DTYPE_BF16 if dtype == "bf16" else rl.DTYPE_FP16
+    ocode = 0 if dtype == "bf16" else 1
+    mc = ctx_hi + 100
+    rng = np.random.default_rng(seed)
+    ws_ = [synth.make_decode(seed + 1 + m, n, QH, KVH, D, 1 if m % 2 else min(300, ctx_hi), ctx_hi, dtype=dtype,
+                             token_count=tc, reserve_tokens=mc) for m, n in enumerate(sizes)]
     pos1 = [w.ctx.copy() for w in ws_]
     rows1 = [_kv_rows(rng, w) for w in ws_]
     rows2 = [_kv_rows(rng, w) for w in ws_]
-    q2 = [synth.f32_to_bf16(rng.standard_normal(w.q.shape, dtype=np.float32)) for w in ws_]
+    q2 = [synth.to_scalar16(rng.standard_normal(w.q.shape, dtype=np.float32), dtype) for w in ws_]
     lg = [rng.standard_normal((64, V), dtype=np.float32) for _ in range(8)]
     seeds = rng.integers(0, 2**63, 64, dtype=np.uint64)
     seed_buf = rl.DeviceBuffer.from_array(seeds)
@@ -378,8 +376,8 @@ def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
                                seeds=seed_buf, step=t) for t in range(8)]
         n_ws = max(rl.decode_sample_step_workspace_bytes(bt.attn, samp[0]) for bt in first)
         ws = [rl.DeviceBuffer(n_ws) for _ in range(4)]
-        print(f"[fused] four micro-batches, two steps each, {'on the lanes' if on_lanes else 'one stream'}",
-              flush=True)
+        print(f"[fused] four micro-batches {sizes} ({QH}/{KVH} d{D} {dtype} tc{tc}), two steps each, "
+              f"{'on the lanes' if on_lanes else 'one stream'}", flush=True)
         if on_lanes:
             rl.lanes_fork()
         for t in range(8):
@@ -413,18 +411,19 @@ def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
         assert np.array_equal(lanes["out"][t][1], one["out"][t][1]), t
         assert np.array_equal(lanes["tok"][t][0], one["tok"][t][0]), t
         assert np.array_equal(lanes["tok"][t][1], one["tok"][t][1]), t
+    rb = D * 2
     for m, w in enumerate(ws_):
         assert np.array_equal(lanes["arena"][m], one["arena"][m]), m
-        gh.check_attn(lanes["out"][m][0], lanes["out"][m][1], orc.attn_f64(olib, w, 0), "bf16")
+        gh.check_attn(lanes["out"][m][0], lanes["out"][m][1], orc.attn_f64(olib, w, ocode), dtype)
         arena1 = w.arena.copy()
         k1, v1 = rows1[m]
-        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, 16, D * 2, w.table.ctypes.data, w.table_stride,
+        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, tc, rb, w.table.ctypes.data, w.table_stride,
                            w.batch, KVH, pos1[m].ctypes.data, None, k1.ctypes.data, v1.ctypes.data)
-        w2 = synth.DecodeWorkload(w.batch, QH, KVH, D, "bf16", 16, w.ctx + np.uint32(1), w.table, arena1, q2[m], 0)
-        gh.check_attn(lanes["out"][4 + m][0], lanes["out"][4 + m][1], orc.attn_f64(olib, w2, 0), "bf16")
+        w2 = synth.DecodeWorkload(w.batch, QH, KVH, D, dtype, tc, w.ctx + np.uint32(1), w.table, arena1, q2[m], 0)
+        gh.check_attn(lanes["out"][4 + m][0], lanes["out"][4 + m][1], orc.attn_f64(olib, w2, ocode), dtype)
         k2, v2 = rows2[m]
         p2 = pos1[m] + np.uint32(1)
-        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, 16, D * 2, w.table.ctypes.data, w.table_stride,
+        olib.orc_kv_append(arena1.ctypes.data, w.block_bytes, tc, rb, w.table.ctypes.data, w.table_stride,
                            w.batch, KVH, p2.ctypes.data, None, k2.ctypes.data, v2.ctypes.data)
         assert np.array_equal(lanes["arena"][m], arena1), m
     for t in range(8):
@@ -433,6 +432,26 @@ def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
         assert np.abs(lanes["tok"][t][1] - wlp).max() < 1e-4, t
     for x in lgb + [seed_buf]:
         x.close()
+
+
+def test_fused_lanes_four_microbatches(rl, gpu, orc, olib):
+    """Four micro-batches of the benchmark's shape (64, 48, 64 and 33
+    rollouts of GQA 32/8, d128, bf16, 16-token blocks) on the two lanes
+    against the same calls on one stream: outputs, arenas and tokens bit for
+    bit (the lanes change where steps run, not what they compute), every
+    attention within 1e-4 of fp64, the arenas equal to the oracle's two
+    appends, every step's tokens equal to the oracle's."""
+    _lanes_case(rl, orc, olib, 32, 8, 128, "bf16", 16, (64, 48, 64, 33), 1200, 9161)
+
+
+@pytest.mark.parametrize("shape", [(16, 8, 64, "fp16", 32), (8, 8, 128, "fp16", 32), (16, 8, 128, "bf16", 16),
+                                   (8, 2, 64, "bf16", 16)],
+                         ids=["gqa2_d64_fp16_tc32", "mha_d128_fp16_tc32", "gqa2_d128_bf16", "gqa4_d64_bf16_kv2"])
+def test_fused_lanes_shapes(rl, gpu, orc, olib, shape):
+    """The lanes case on the other shapes the fused kernel takes: GQA groups
+    1, 2 and 4, head_dim 64 and 128, fp16 and bf16, 16- and 32-token blocks."""
+    QH, KVH, D, dtype, tc = shape
+    _lanes_case(rl, orc, olib, QH, KVH, D, dtype, tc, (24, 17, 24, 9), 700, 9300 + QH * 10 + KVH + D)
 
 
 def test_fused_step_without_append(rl, gpu, orc, olib):
