@@ -832,8 +832,9 @@ def wl_ringstep(args):
     (rl_hip_ring_step_enqueue): per step 64 one-token descriptors drained by
     the poll kernel, the batched step over every compute unit, 64 completions
     published. The descriptors of every step are queued before the timed
-    region; logits rotate over 4 input slots. Beside it, on the same inputs:
-    the launched fused step (rl_hip_decode_sample_step: the same two kernels
+    region; logits rotate over 4 input slots. Then the same pipeline as one
+    persistent launch of K steps (rl_hip_ring_loop_launch). Beside them, on
+    the same inputs: the launched fused step (rl_hip_decode_sample_step: the same two kernels
     without the rings) and the unfused one (rl_hip_decode_step +
     rl_hip_sample)."""
     import ringstep
@@ -868,6 +869,26 @@ def wl_ringstep(args):
     run.close()
     if stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
         raise rlrt.RlrtError(f"ring step stats {stats}, {n_comp} completions")
+    # the same pipeline as one persistent launch per call (rl_hip_ring_loop_launch)
+    run = ringstep.RingStepRun(st.arena, st.layout, w.table, QH, MAX_CTX, B, VOCAB, input_slots=LOGIT_COPIES,
+                               output_slots=1, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
+    for sl in range(LOGIT_COPIES):
+        run.set_inputs(sl, w.q, kn, vn, logits)
+    for _ in range(K + W):
+        for r in range(B):
+            run.submit_decode(r, int(w.ctx[r]), int(w.ctx[r]) + 1)
+    if run.loop(W) != W:
+        raise rlrt.RlrtError("ring loop warm-up ended early")
+    timer.begin()
+    run.loop_launch(K)
+    loop_ms = timer.end()
+    loop_ran = run.loop_done()
+    loop_stats = run.stats()
+    n_comp = len(run.completions())
+    run.stop()
+    run.close()
+    if loop_ran != K or loop_stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
+        raise rlrt.RlrtError(f"ring loop ran {loop_ran}, stats {loop_stats}, {n_comp} completions")
     # the launched steps on the same inputs
     fws = rlrt.decode_sample_step_workspace(st.attn, st.samp[0])
 
@@ -880,18 +901,22 @@ def wl_ringstep(args):
     for i in range(W):
         st.run(i, "unfused")
     lms, _ = time_loop(st, K, "unfused")
-    ring_us, launched_us = ms / K * 1e3, lms / K * 1e3
+    ring_us, launched_us, loop_us = ms / K * 1e3, lms / K * 1e3, loop_ms / K * 1e3
     step_bytes = st.attn_bytes() + st.sample_bytes() + st.append_bytes()
     return {"workload": "ringstep_b64_q32kv8_d128_ctx512-4096_v128256_t0.8_k50_p0.9",
             "steps": K, "ring_step_us": ring_us, "ring_steps_per_s": 1e6 / ring_us,
             "ring_tokens_per_s": B * 1e6 / ring_us, "ring_step_hbm_frac": step_bytes / (ring_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
+            "loop_step_us": loop_us, "loop_tokens_per_s": B * 1e6 / loop_us,
+            "loop_step_hbm_frac": step_bytes / (loop_us * 1e-6) / 1e9 / PEAK_HBM_GBPS, "loop_over_ring": loop_us / ring_us,
             "launched_fused_step_us": fused_us, "ring_over_launched_fused": ring_us / fused_us,
             "launched_step_us": launched_us, "launched_tokens_per_s": B * 1e6 / launched_us,
             "stats": stats,
             "note": "per step: the turn kernel (one wave: the previous step's 64 completions published and 64 "
                     "descriptors admitted over PCIe), the fused attention + sampling launch and its merge + append "
-                    "kernel; launched_fused_step_us: the same two kernels called directly; launched_step_us: "
-                    "rl_hip_decode_step + rl_hip_sample; HIP events on the library stream"}
+                    "kernel; loop_step_us: the same turns and steps in one persistent launch of K steps "
+                    "(rl_hip_ring_loop_launch: grid barriers between turn, step and merge); launched_fused_step_us: "
+                    "the same two kernels called directly; launched_step_us: rl_hip_decode_step + rl_hip_sample; "
+                    "HIP events on the library stream"}
 
 
 def wl_cmdring(args):

@@ -140,14 +140,22 @@ struct StageMeta {
 };
 
 // Context length of rollout b: from the ctx array (scalar load), or one
-// value fixed by the caller.
+// value fixed by the caller, or from a ctx array that the same launch
+// rewrites between steps (CtxLive; the row map is then read the same way).
 struct CtxFromArray {
+    static constexpr bool kLive = false;
     const uint32_t *ctx;
     __device__ __forceinline__ uint32_t operator()(uint32_t b) const { return rl_sload(ctx + b); }
 };
 struct CtxFixed {
+    static constexpr bool kLive = false;
     uint32_t value;
     __device__ __forceinline__ uint32_t operator()(uint32_t) const { return value; }
+};
+struct CtxLive {
+    static constexpr bool kLive = true;
+    const uint32_t *ctx;
+    __device__ __forceinline__ uint32_t operator()(uint32_t b) const { return rl_live_u32(ctx + b); }
 };
 
 // Issue side of a wave: walks the wave's tile range and starts the copies.
@@ -181,7 +189,7 @@ struct Issuer {
     __device__ __forceinline__ void set_rollout(const AttnParams &p, uint32_t nb)
     {
         b = nb;
-        tb = p.row_map ? rl_sload(p.row_map + nb) : nb;
+        tb = !p.row_map ? nb : CtxFn::kLive ? rl_live_u32(p.row_map + nb) : rl_sload(p.row_map + nb);
         const uint32_t cin = cf(nb);
         ctx_bad = cin > p.max_ctx;
         ctx = ctx_bad ? p.max_ctx : cin;

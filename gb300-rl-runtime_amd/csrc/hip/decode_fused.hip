@@ -44,6 +44,7 @@
 #include "kv_append_core.h"
 #include "kv_layout.h"
 #include "rl_dev_common.h"
+#include "ring_core.h"
 #include "sample_core.h"
 
 namespace {
@@ -206,13 +207,41 @@ __device__ __forceinline__ uint32_t rollout_of(RL_LDS const uint32_t *cum, uint3
     return lo;
 }
 
-template <int D, int G, int DT, int TPB>
-__global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
+// The previous step's split rows merged and its K/V token appended, one row
+// per wave: rows w0, w0 + nw, ... of pp (its partials and tile prefix in its
+// workspace, its split psi). LIVE: the prefix was written by this launch.
+template <int D, int G, int DT, bool LIVE = false>
+__device__ __forceinline__ void merge_rows_waves(const AttnParams &pp, const AppendParams &pap, const SplitIn &psi,
+                                                 uint32_t w0, uint32_t nw, int lane)
+{
+    const uint32_t rows = pp.batch * pp.kv_heads;
+    const uint32_t Up = LIVE ? rl_live_u32(pp.cum + pp.batch) : rl_sload(pp.cum + pp.batch);
+    for (uint32_t r = w0; r < rows; r += nw) {
+        const uint32_t b = r / pp.kv_heads, g = r % pp.kv_heads;
+        const uint32_t cin = pp.ctx[b];
+        const bool bad = cin > pp.max_ctx;
+        const uint32_t nu = tiles_of(pp, cin);
+        if (nu == 0) {
+            empty_row<D, G, DT, G>(pp, b, g, 0, bad, (uint32_t)lane, 64);
+        } else {
+            const uint32_t R0 = pp.cum[b] + g * nu;
+            merge_row_wave<D, G, DT>(pp, b, g, global_piece_of(R0, Up, psi), global_piece_of(R0 + nu - 1, Up, psi),
+                                     bad, lane);
+        }
+        if (pap.arena)
+            append_row(pap, b, g, (uint32_t)lane, 64);
+    }
+}
+
+// One fused step by the calling workgroup (blockIdx.x), every thread of it;
+// lds is its LDS of FusedLayout::TOTAL bytes. LIVE: the contexts and the row
+// map were written by this launch (a persistent kernel's earlier steps), so
+// they are read past the scalar cache.
+template <int D, int G, int DT, int TPB, bool LIVE = false>
+__device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *lds)
 {
     using C = Cfg<D, G, DT, TPB>;
     using LY = FusedLayout<D, G, DT, TPB>;
-    static_assert(LY::FITS, "fused step LDS");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
     const AttnParams &p = f.p;
     const uint32_t wg = blockIdx.x;
     const uint32_t tid = threadIdx.x;
@@ -224,28 +253,9 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
         *f.si_out = f.si;  // read by the merge kernel, or by the next call of a pipeline
 
     // ---- the previous step's rows: merge and append, one row per sampling wave ---
-    if (sampler && f.has_prev) {
-        const AttnParams &pp = f.pp;
-        const uint32_t nsw = f.si.sample_wgs * kFWaves;
-        const uint32_t rows = pp.batch * pp.kv_heads;
-        const uint32_t Up = rl_sload(pp.cum + pp.batch);
-        const SplitIn psi = *f.psi;
-        for (uint32_t r = wg * kFWaves + (uint32_t)wave; r < rows; r += nsw) {
-            const uint32_t b = r / pp.kv_heads, g = r % pp.kv_heads;
-            const uint32_t cin = pp.ctx[b];
-            const bool bad = cin > pp.max_ctx;
-            const uint32_t nu = tiles_of(pp, cin);
-            if (nu == 0) {
-                empty_row<D, G, DT, G>(pp, b, g, 0, bad, (uint32_t)lane, 64);
-            } else {
-                const uint32_t R0 = pp.cum[b] + g * nu;
-                merge_row_wave<D, G, DT>(pp, b, g, global_piece_of(R0, Up, psi),
-                                         global_piece_of(R0 + nu - 1, Up, psi), bad, lane);
-            }
-            if (f.pap.arena)
-                append_row(f.pap, b, g, (uint32_t)lane, 64);
-        }
-    }
+    if (sampler && f.has_prev)
+        merge_rows_waves<D, G, DT>(f.pp, f.pap, *f.psi, wg * kFWaves + (uint32_t)wave, f.si.sample_wgs * kFWaves,
+                                   lane);
 
     // ---- sampling role ----------------------------------------------------------
     if (sampler) {
@@ -308,8 +318,21 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
     const uint32_t b = rollout_of(cum, p.batch, s_begin);
     RL_LDS uint8_t *st = (RL_LDS uint8_t *)lds + wave * C::STAGE;
     RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds + LY::Q_OFF + wave * kFStages * C::QSLOT;
-    attn_stream<D, G, DT, TPB, kFStages>(p, CtxFromArray{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b,
-                                         cum[b], st, kFWaves * C::STAGE, qs, lane);
+    if constexpr (LIVE)
+        attn_stream<D, G, DT, TPB, kFStages>(p, CtxLive{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b, cum[b],
+                                             st, kFWaves * C::STAGE, qs, lane);
+    else
+        attn_stream<D, G, DT, TPB, kFStages>(p, CtxFromArray{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b,
+                                             cum[b], st, kFWaves * C::STAGE, qs, lane);
+}
+
+template <int D, int G, int DT, int TPB>
+__global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
+{
+    using LY = FusedLayout<D, G, DT, TPB>;
+    static_assert(LY::FITS, "fused step LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
+    fused_step_body<D, G, DT, TPB>(f, lds);
 }
 
 // Combines the partials of every row split across pieces (merge_span), writes
@@ -343,6 +366,207 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 }
 
 // ---- launcher ----------------------------------------------------------------------
+
+// ---- the self-scheduled ring loop ----------------------------------------------
+// One cooperative launch of one workgroup per compute unit runs the
+// ring-driven batched step for as many steps as the rings call for, with no
+// launch between steps. Per step:
+//  turn    workgroup 0's first wave runs the ring turn (ring_core.h: publish
+//          the step just decoded, admit descriptors into free rows, write the
+//          rows' step arguments), then releases a flag; the other workgroups
+//          wait for it (bounded) and acquire. The turn also decides the end:
+//          admission has ended and no row decodes next step, or the step
+//          count reached max_steps.
+//  step    fused_step_body over the step's slots: attention tiles beside the
+//          sampling of the step's logits; rows read the rollout-ordered block
+//          table through the row map.
+//  merge   after a grid barrier, every wave merges split rows (one row per
+//          wave) and appends the step's K/V token; then a second barrier, so
+//          the next turn and step see every write.
+// Grid barriers: each workgroup releases its writes device-wide, adds one to
+// a counter and waits (bounded, acquire) until all workgroups of this epoch
+// have; a wait that runs out sets an error word that ends every workgroup's
+// loop at its next barrier. Cooperative launch keeps every workgroup
+// resident, so the waits are never for a workgroup that cannot run.
+struct LoopParams {
+    RingParams rp;
+    FusedParams f;            // the step over input / output slot 0 (the slots are offsets from it)
+    AppendParams ap;          // the append over input slot 0
+    size_t q_slot, out_slot;  // bytes per input slot of q, per output slot of the 16-bit outputs
+    size_t out32_slot;        // floats per output slot of the fp32 outputs
+    size_t logits_slot;       // floats per input slot of the logits
+    size_t tok_slot;          // entries per output slot of tokens and logprobs
+    size_t kv_slot;           // bytes per input slot of the new K (and V) rows
+    uint32_t *row_rollout;    // [output_slots][batch] or nullptr
+    uint32_t *steps_run;      // steps the loop ran, written at its end (or nullptr)
+    uint32_t input_slots, output_slots;
+    uint64_t first_step;
+    uint32_t max_steps;
+    uint32_t *sync;           // device [4], zeroed: go flag, barrier count, error, spare
+    uint64_t go_ticks;        // longest wait for the turn, in 100 MHz clock ticks
+    uint64_t bar_ticks;       // longest wait at a grid barrier
+};
+
+enum : uint32_t { kLoopSyncTimeout = 5 };  // stats[3] when a wait of the loop ran out
+
+// The loop's arguments, read from the kernel-argument segment through a
+// pointer the optimizer cannot see through: each phase reloads (scalar loads
+// of memory that never changes) the fields it uses, instead of every phase's
+// fields being hoisted out of the loop and held in registers across all of
+// it, which spills.
+__device__ __forceinline__ const RL_CONST LoopParams &loop_args()
+{
+    uint64_t a = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(a));
+    return *(const RL_CONST LoopParams *)a;
+}
+
+template <class T>
+__device__ __forceinline__ T kcopy(const RL_CONST T &x)
+{
+    T v;
+    __builtin_memcpy(&v, (const void *)&x, sizeof(T));
+    return v;
+}
+
+// Grid barrier number `epoch` (all gridDim.x workgroups): this workgroup's
+// writes released device-wide, the count raised, a bounded wait (acquire)
+// for every workgroup of the epoch. False when the wait ran out or another
+// workgroup's did (the error word), which ends the loop.
+__device__ bool loop_barrier(uint32_t *sync, uint64_t limit_ticks, uint32_t epoch, uint32_t *s_ok)
+{
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();  // this workgroup's writes, device-wide, before it counts in
+        atomicAdd(&sync[1], 1u);
+        const uint32_t target = epoch * gridDim.x;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        uint32_t ok = 1;
+        while (__hip_atomic_load(&sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (__hip_atomic_load(&sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                __builtin_amdgcn_s_memrealtime() - t0 > limit_ticks) {
+                ok = 0;
+                __hip_atomic_store(&sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __threadfence();  // the others' writes are visible to this workgroup
+        *s_ok = ok;
+    }
+    __syncthreads();
+    return *s_ok != 0;
+}
+
+template <int D, int G, int DT, int TPB>
+__global__ __launch_bounds__(kFThreads) void ring_loop_kernel(LoopParams)
+{
+    using LY = FusedLayout<D, G, DT, TPB>;
+    static_assert(LY::FITS, "fused step LDS");
+    static_assert(2 * kMaxBatch <= LY::TOTAL, "the turn's free-row list fits the stage buffers");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
+    __shared__ uint32_t s_end;  // the turn's decision, read after it
+    __shared__ uint32_t s_ok;   // a barrier's outcome (its own word: s_end is rewritten while it is read)
+    const uint32_t wg = blockIdx.x, nwg = gridDim.x;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
+    uint32_t epoch = 0;
+    uint32_t n = 0;
+    for (;; n++) {
+        // ---- the turn, and the decision to go on -------------------------------
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            const bool last = n >= L.max_steps;  // this turn only publishes
+            uint32_t *sync = L.sync;
+            if (wg == 0 && wave == 0) {
+                RingParams rp = kcopy(L.rp);
+                const size_t so = (L.first_step + n) % L.output_slots;
+                rp.row_rollout = L.row_rollout && !last ? L.row_rollout + so * rp.batch : nullptr;
+                uint32_t status = 0;
+                // the stage buffers hold the free-row list: no tile is in flight
+                const uint32_t held = ring_turn(rp, n > 0 ? 1u : 0u, last ? 0u : 1u,
+                                               reinterpret_cast<uint16_t *>(lds), &status);
+                // admission over and every row free: later steps would decode nothing
+                const bool end = last || (status != kRunning && held == 0);
+                if (lane == 0) {
+                    __threadfence();  // the rows' step arguments before the flag
+                    __hip_atomic_store(&sync[0], (n + 1) | (end ? 0x80000000u : 0u), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                    s_end = end ? 1u : 0u;
+                }
+            } else if (wg != 0 && tid == 0) {
+                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                const uint64_t limit = L.go_ticks;
+                uint32_t v;
+                for (;;) {
+                    v = __hip_atomic_load(&sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if ((v & 0x7FFFFFFFu) >= n + 1)
+                        break;
+                    if (__hip_atomic_load(&sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
+                        __builtin_amdgcn_s_memrealtime() - t0 > limit) {
+                        __hip_atomic_store(&sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        v = 0x80000000u;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                __threadfence();  // the turn's writes are visible to this workgroup
+                s_end = v >> 31;
+            }
+            __syncthreads();
+            if (s_end)
+                break;
+        }
+
+        // ---- the step over this step's slots -------------------------------------
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            const uint64_t k = L.first_step + n;
+            const size_t si = k % L.input_slots, so = k % L.output_slots;
+            FusedParams f = kcopy(L.f);
+            f.p.q = (const uint16_t *)((const uint8_t *)f.p.q + si * L.q_slot);
+            f.p.out = (uint16_t *)((uint8_t *)f.p.out + so * L.out_slot);
+            f.p.out_f32 = f.p.out_f32 ? f.p.out_f32 + so * L.out32_slot : nullptr;
+            f.sp.logits = f.sp.logits + si * L.logits_slot;
+            f.sp.token_out = f.sp.token_out + so * L.tok_slot;
+            f.sp.logprob_out = f.sp.logprob_out + so * L.tok_slot;
+            fused_step_body<D, G, DT, TPB, true>(f, lds);
+        }
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            if (!loop_barrier(L.sync, L.bar_ticks, ++epoch, &s_ok))
+                break;
+        }
+
+        // ---- merge the split rows, append the step's token --------------------------
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            const uint64_t k = L.first_step + n;
+            const size_t si = k % L.input_slots, so = k % L.output_slots;
+            AttnParams pp = kcopy(L.f.p);
+            pp.out = (uint16_t *)((uint8_t *)pp.out + so * L.out_slot);
+            pp.out_f32 = pp.out_f32 ? pp.out_f32 + so * L.out32_slot : nullptr;
+            AppendParams ap = kcopy(L.ap);
+            ap.k_new = ap.k_new + si * L.kv_slot;
+            ap.v_new = ap.v_new + si * L.kv_slot;
+            const SplitIn psi = kcopy(L.f.si);
+            merge_rows_waves<D, G, DT, true>(pp, ap, psi, wg * kFWaves + (uint32_t)wave, nwg * kFWaves, lane);
+        }
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            if (!loop_barrier(L.sync, L.bar_ticks, ++epoch, &s_ok))
+                break;
+        }
+    }
+    if (wg == 0 && tid == 0) {
+        const RL_CONST LoopParams &L = loop_args();
+        if (L.steps_run)
+            *L.steps_run = n;
+        if (__hip_atomic_load(&L.sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+            L.rp.stats[3] = kLoopSyncTimeout;
+    }
+}
 
 struct FusedWs {
     size_t si_off, cum_off, part_off, total;
@@ -766,4 +990,141 @@ extern "C" int rl_hip_decode_pipeline_flush(const rl_attn_decode_args_t *prev_at
 {
     return pipeline_flush_on(rl_stream(), prev_attn, prev_append, prev_workspace, workspace_bytes,
                              "rl_hip_decode_pipeline_flush");
+}
+
+// ---- the self-scheduled ring loop: host side ---------------------------------------
+
+namespace {
+
+template <int D, int G, int DT, int TPB>
+int loop_launch(LoopParams &L, uint32_t grid)
+{
+    if constexpr (!FusedLayout<D, G, DT, TPB>::FITS) {
+        rl_set_error("rl_hip_ring_loop_launch: shape does not fit the fused step");
+        return -1;
+    } else {
+        void *args[] = {&L};
+        return rl_check_hip(
+            hipLaunchCooperativeKernel(reinterpret_cast<const void *>(&ring_loop_kernel<D, G, DT, TPB>), dim3(grid),
+                                       dim3(kFThreads), args, 0, rl_stream()),
+            "hipLaunchCooperativeKernel(ring_loop_kernel)");
+    }
+}
+
+template <int D, int G>
+int loop_dt(LoopParams &L, uint32_t grid, uint32_t dt, uint32_t tpb)
+{
+    if (dt == RL_DTYPE_BF16)
+        return tpb == 16 ? loop_launch<D, G, 0, 16>(L, grid) : loop_launch<D, G, 0, 32>(L, grid);
+    return tpb == 16 ? loop_launch<D, G, 1, 16>(L, grid) : loop_launch<D, G, 1, 32>(L, grid);
+}
+
+template <int D>
+int loop_g(LoopParams &L, uint32_t grid, uint32_t G, uint32_t dt, uint32_t tpb)
+{
+    switch (G) {
+    case 1: return loop_dt<D, 1>(L, grid, dt, tpb);
+    case 2: return loop_dt<D, 2>(L, grid, dt, tpb);
+    case 4: return loop_dt<D, 4>(L, grid, dt, tpb);
+    default: return loop_dt<D, 8>(L, grid, dt, tpb);
+    }
+}
+
+}  // namespace
+
+extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t max_steps, uint64_t first_step,
+                                       uint32_t *steps_run)
+{
+    const char *who = "rl_hip_ring_loop_launch";
+    if (rl_require_open(who) || ring_validate(a, who))
+        return -1;
+    RingWs w;
+    if (ring_layout(a, w))
+        return -1;
+    if (!a->workspace || a->workspace_bytes < w.total) {
+        rl_set_error("%s: workspace %zu bytes < %zu required", who, a->workspace_bytes, w.total);
+        return -1;
+    }
+    int coop = 0;
+    if (rl_check_hip(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, rl_device()),
+                     "hipDeviceGetAttribute(CooperativeLaunch)"))
+        return -1;
+    if (!coop) {
+        rl_set_error("%s: the device does not support cooperative launches", who);
+        return -1;
+    }
+    uint8_t *ws = (uint8_t *)a->workspace;
+    LoopParams L;
+    L.rp = ring_params_of(a, ws, w);
+
+    const size_t B = a->batch;
+    const size_t qrow = (size_t)a->q_heads * a->layout.head_dim * 2;
+    const size_t kvrow = (size_t)a->kv_heads * a->layout.head_dim * 2;
+    rl_attn_decode_args_t t = attn_of(a, nullptr, 0);
+    t.block_table = a->block_table;
+    t.ctx_lens = L.rp.ctx;
+    t.q = a->q;
+    t.out = a->attn_out;
+    t.out_f32 = a->attn_out_f32;
+    if (!fused_eligible(&t)) {
+        rl_set_error("%s: the shape does not fit the fused kernel (use rl_hip_ring_step_enqueue)", who);
+        return -1;
+    }
+    rl_sample_args_t s = samp_of(a);
+    s.seed = L.rp.rseed;
+    s.steps = L.rp.rstep;
+    s.draw_ids = L.rp.rmap;  // the draw follows the rollout, not the row it was admitted into
+    if (rl_attn_check(&t) || rl_sample_check(&s))
+        return -1;
+    L.f = fused_params_of(&t, &s, ws + w.step, 0);
+    L.f.p.row_map = L.rp.rmap;
+    if (L.f.si.wgs > rl_cu_count()) {
+        rl_set_error("%s: %u workgroups for %u compute units", who, L.f.si.wgs, rl_cu_count());
+        return -1;
+    }
+    // two barriers a step count to epoch * workgroups in 32 bits
+    if (max_steps == 0 || 2ull * (max_steps + 1ull) * L.f.si.wgs >= (1ull << 32)) {
+        rl_set_error("%s: max_steps %u not in 1 .. %llu", who, max_steps,
+                     (unsigned long long)((1ull << 32) / (2ull * L.f.si.wgs) - 2));
+        return -1;
+    }
+    rl_kv_append_args_t apa = {};
+    apa.arena_base = a->arena_base;
+    apa.arena_bytes = a->arena_bytes;
+    apa.layout = a->layout;
+    apa.block_table = a->block_table;
+    apa.table_stride = a->table_stride;
+    apa.batch = a->batch;
+    apa.kv_heads = a->kv_heads;
+    apa.positions = L.rp.pos;
+    apa.cow_src = nullptr;
+    apa.k_new = a->k_new;
+    apa.v_new = a->v_new;
+    L.ap = append_params(&apa);
+    L.ap.row_map = L.rp.rmap;
+    L.q_slot = B * qrow;
+    L.out_slot = B * qrow;
+    L.out32_slot = B * qrow / 2;
+    L.logits_slot = B * a->vocab;
+    L.tok_slot = B;
+    L.kv_slot = B * kvrow;
+    L.row_rollout = a->row_rollout_out;
+    L.steps_run = steps_run;
+    L.input_slots = a->input_slots;
+    L.output_slots = a->output_slots;
+    L.first_step = first_step;
+    L.max_steps = max_steps;
+    L.sync = (uint32_t *)(ws + w.ctl + kLoopSyncOff);
+    // A turn waits at most max_idle polls for room on the completion ring and
+    // as many for a descriptor, each poll one PCIe round trip and a short
+    // sleep (10 us is a generous bound); a step and its merge stream at most
+    // the device's memory once, far below 2 s.
+    L.go_ticks = 2000ull * L.rp.max_idle + 100000000ull;
+    L.bar_ticks = 200000000ull;
+    if (rl_check_hip(hipMemsetAsync(L.sync, 0, 4 * sizeof(uint32_t), rl_stream()), "hipMemsetAsync(loop sync)"))
+        return -1;
+    const uint32_t G = a->q_heads / a->kv_heads;
+    if (a->layout.head_dim == 128)
+        return loop_g<128>(L, L.f.si.wgs, G, a->dtype, a->layout.token_count);
+    return loop_g<64>(L, L.f.si.wgs, G, a->dtype, a->layout.token_count);
 }

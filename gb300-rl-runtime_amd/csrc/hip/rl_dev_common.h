@@ -22,6 +22,16 @@ __device__ __forceinline__ T rl_sload(const T *p)
     return *(const RL_CONST T *)p;
 }
 
+// Wave-uniform load of a word that the same launch rewrites between reads (a
+// persistent kernel's per-step arguments): a relaxed device-scope atomic
+// load, which is never a scalar-cache access and never moved out of a loop,
+// broadcast from the first lane. Ordering comes from the caller's fences.
+__device__ __forceinline__ uint32_t rl_live_u32(const uint32_t *p)
+{
+    return __builtin_amdgcn_readfirstlane(
+        __hip_atomic_load(const_cast<uint32_t *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
 // ---- scalar conversions ---------------------------------------------------
 
 __device__ __forceinline__ float rl_bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }

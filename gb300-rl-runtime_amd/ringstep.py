@@ -99,6 +99,25 @@ class RingStepRun:
                    "rl_hip_ring_step_enqueue")
         self.next_step += steps
 
+    def loop_launch(self, max_steps: int) -> None:
+        """rl_hip_ring_loop_launch: up to max_steps steps in one persistent
+        launch, queued on the library stream (loop_done collects it)."""
+        if "steps_run" not in self.dev:
+            self.dev["steps_run"] = rlrt.DeviceBuffer(256, zero=True)
+        rlrt.check(rlrt.lib().rl_hip_ring_loop_launch(C.byref(self.args), max_steps, self.next_step,
+                                                      self.dev["steps_run"].ptr), "rl_hip_ring_loop_launch")
+
+    def loop_done(self) -> int:
+        """Waits for the loop; returns the steps it ran (the next call starts after them)."""
+        rlrt.sync()
+        n = int(self.dev["steps_run"].download(np.uint32, 1)[0])
+        self.next_step += n
+        return n
+
+    def loop(self, max_steps: int) -> int:
+        self.loop_launch(max_steps)
+        return self.loop_done()
+
     def completions(self) -> list[bytes]:
         out = []
         while (d := rlrt.hw_ring_pop(self.dq)) is not None:

@@ -346,6 +346,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         "rl_hip_cmd_worker_launch": (i32, [C.POINTER(CmdWorkerArgs)]),
         "rl_hip_ring_step_workspace": (sz, [C.POINTER(RingStepArgs)]),
         "rl_hip_ring_step_enqueue": (i32, [C.POINTER(RingStepArgs), u32, u64]),
+        "rl_hip_ring_loop_launch": (i32, [C.POINTER(RingStepArgs), u32, u64, vp]),
         # reference host API
         "hw_ring_create": (vp, []), "hw_ring_reset": (None, [vp]), "hw_ring_destroy": (None, [vp]),
         "hw_ring_load_acquire": (u32, [vp]), "hw_ring_store_release": (None, [vp, u32]),

@@ -1,0 +1,219 @@
+"""The self-scheduled ring loop (rl_hip_ring_loop_launch): the ring-driven
+batched decode step as one persistent launch, held to the launched pipeline
+(rl_hip_ring_step_enqueue), which the ring-step tests pin to the oracle and
+to hw_worker_sim_run. Each case runs the same submissions through both on
+copies of the same arena and compares everything the host can see:
+
+1. The control rule over many steps (8 rows, 13 descriptors of 1-8 tokens,
+   NEEDS_REWARD at 32, a passthrough, a dropped opcode, STOP): the loop
+   ends by itself once admission has ended and every row is free; its
+   completions, stats, per-step rows, tokens, logprobs and attention (bf16
+   and fp32 bits) and the final arena equal the launched run's, whose later
+   steps decoded nothing.
+2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
+   128,256 logits): max_steps 1, then a second loop that finds only STOP;
+   bit-equal to two launched steps.
+3. Exit paths: idle limit, bad rollout id, the host's stop flag (zero steps
+   run, status 1 / 2 / 4) and a full completion ring (status 3; the finished
+   descriptor stays in its row until a later loop pushes it).
+4. Arguments the loop does not take: max_steps 0 and a GQA group of 8 at
+   d128 (outside the fused kernel) return errors before any launch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+QH, KVH, D, TPB = 32, 8, 128, 16
+
+
+def _outputs(run, steps):
+    return [run.outputs(s) for s in range(steps)]
+
+
+def _same_outputs(a, b, what):
+    for k in ("rows", "tok", "out", "out32"):
+        assert np.array_equal(a[k], b[k]), (what, k)
+    assert np.array_equal(a["lp"].view(np.uint32), b["lp"].view(np.uint32)), (what, "lp")
+
+
+def _control_rule_case(rl, driver):
+    """The submissions of the ring-step control-rule test on a fresh arena,
+    run by driver(run); returns what the host sees."""
+    import ringstep
+
+    B, R, V, STEPS = 8, 13, 1024, 40
+    rng = np.random.default_rng(6160)
+    seq0 = rng.integers(20, 300, R).astype(np.int64)
+    seq0[1] = 30
+    w = synth.make_decode(6161, R, QH, KVH, D, 0, 0, ctx=seq0.astype(np.uint32), reserve_tokens=int(seq0.max()) + 16)
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    seeds = rng.integers(0, 2**63, R, dtype=np.uint64)
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(seq0.max()) + 16, B, V,
+                               input_slots=STEPS, output_slots=STEPS, temperature=1.0, top_k=20, top_p=0.8,
+                               seeds=seeds)
+    q = synth.f32_to_bf16(rng.standard_normal((STEPS, B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((STEPS, B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((STEPS, B, KVH, D), dtype=np.float32))
+    logits = rng.standard_normal((STEPS, B, V), dtype=np.float32)
+    for s in range(STEPS):
+        run.set_inputs(s, q[s], kn[s], vn[s], logits[s])
+    max_tok = seq0 + rng.integers(1, 9, R)
+    max_tok[0], max_tok[1], max_tok[2] = seq0[0] + 3, 40, seq0[2]
+    for r in [0, 1, 2, None] + list(range(3, R)):
+        if r is None:
+            run.push(rl.HwDesc(opcode=2, rollout_id=99))
+        else:
+            run.submit_decode(r, int(seq0[r]), int(max_tok[r]))
+    run.push(rl.HwDesc(opcode=255))
+    ran = driver(run, STEPS)
+    rl.sync()
+    res = {"ran": ran, "completions": run.completions(), "stats": run.stats(), "out": _outputs(run, STEPS),
+           "arena": arena.download(np.uint8, arena.nbytes)}
+    run.close()
+    arena.close()
+    return res
+
+
+def _enqueue(run, steps):
+    run.enqueue(steps)
+    return steps
+
+
+def test_ring_loop_equals_enqueue_control_rule(rl, gpu):
+    print("[loop] control rule: 40 launched steps", flush=True)
+    want = _control_rule_case(rl, _enqueue)
+    print("[loop] control rule: one loop of up to 40 steps", flush=True)
+    got = _control_rule_case(rl, lambda run, steps: run.loop(steps))
+    n = got["ran"]
+    assert 0 < n < 40, n
+    assert got["completions"] == want["completions"] and len(got["completions"]) == 13
+    assert got["stats"] == want["stats"] and got["stats"][3] == 4, (got["stats"], want["stats"])
+    for s in range(n):
+        _same_outputs(got["out"][s], want["out"][s], s)
+    # the launched run's later steps decoded nothing
+    assert any((want["out"][n - 1]["rows"] != 0xFFFFFFFF))
+    for s in range(n, 40):
+        assert (want["out"][s]["rows"] == 0xFFFFFFFF).all(), s
+    assert np.array_equal(got["arena"], want["arena"])
+
+
+def _batch64(rl, driver):
+    import ringstep
+
+    B, V = 64, 128256
+    rng = np.random.default_rng(5150)
+    w = synth.make_decode(5151, B, QH, KVH, D, 512, 4096, max_ctx=4096)
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    seeds = rng.integers(0, 2**63, B, dtype=np.uint64)
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, 4096, B, V, output_slots=2,
+                               temperature=0.8, top_k=50, top_p=0.9, seeds=seeds)
+    perm = rng.permutation(B)
+    q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    run.set_inputs(0, q, kn, vn, synth.make_logits(5152, B, V, spikes=5))
+    for r in perm:
+        run.submit_decode(int(r), int(w.ctx[r]), int(w.ctx[r]) + 1)
+    run.push(rl.HwDesc(opcode=255))
+    ran = driver(run)
+    rl.sync()
+    res = {"ran": ran, "completions": run.completions(), "stats": run.stats(), "out": run.outputs(0),
+           "arena": arena.download(np.uint8, arena.nbytes)}
+    run.close()
+    arena.close()
+    return res
+
+
+def test_ring_loop_batch64(rl, gpu):
+    print("[loop] batch 64: two launched steps", flush=True)
+    want = _batch64(rl, lambda run: _enqueue(run, 2))
+    print("[loop] batch 64: loop of 1 step, then a loop that finds STOP", flush=True)
+    got = _batch64(rl, lambda run: (run.loop(1), run.loop(4)))
+    assert got["ran"] == (1, 0)
+    assert got["completions"] == want["completions"] and len(got["completions"]) == 64
+    assert got["stats"] == want["stats"] == [64, 64, 1, 4]
+    _same_outputs(got["out"], want["out"], "step 0")
+    assert np.array_equal(got["arena"], want["arena"])
+
+
+def test_ring_loop_exit_paths(rl, gpu):
+    import ringstep
+
+    B, V = 4, 4096
+    rng = np.random.default_rng(7180)
+    w = synth.make_decode(7181, B, QH, KVH, D, 40, 300)
+    q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    logits = rng.standard_normal((B, V), dtype=np.float32)
+
+    def run_of(arena):
+        r = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
+                                 greedy=True, max_idle_polls=2000)
+        r.set_inputs(0, q, kn, vn, logits)
+        return r
+
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    for case in ("idle", "bad_id", "stop"):
+        run = run_of(arena)
+        if case == "bad_id":
+            run.submit_decode(B + 3, 10, 11)
+        if case == "stop":
+            run.stop()
+        print(f"[loop] exit path: {case}", flush=True)
+        assert run.loop(3) == 0
+        st = run.stats()
+        assert st == [0, 0, 0, {"idle": 1, "bad_id": 2, "stop": 4}[case]], (case, st)
+        assert run.completions() == []
+        run.close()
+
+    run = run_of(arena)
+    L = rl.lib()
+    filler = rl.HwDesc(opcode=7)
+    for _ in range(65536):
+        assert rl.hw_ring_push(run.dq, filler) == 0
+    r0 = 1
+    run.submit_decode(r0, int(w.ctx[r0]), int(w.ctx[r0]) + 1)
+    print("[loop] exit path: completion ring full", flush=True)
+    assert run.loop(1) == 1
+    assert run.stats() == [1, 0, 1, 3]
+    assert L.hw_ring_load_acquire(run.dq + 64) == 65536
+    got = run.completions()
+    assert len(got) == 65536 and all(g == bytes(filler) for g in got)
+    # the row stays held (a finished descriptor with no room), so the loop
+    # does not end early: its last turn pushes the row
+    assert run.loop(1) == 1
+    got = run.completions()
+    assert len(got) == 1
+    d = rl.HwDesc.from_buffer_copy(got[0])
+    assert (d.rollout_id, d.seq_len, d.max_tokens) == (r0, int(w.ctx[r0]) + 1, int(w.ctx[r0]) + 1)
+    assert d.flags & 2 and d.opcode == 1
+    st = run.stats()
+    assert st[0] == 1 and st[1] == 1 and st[3] == 3, st
+    assert run.loop(2) == 0                                # nothing held, admission closed
+    run.close()
+    arena.close()
+
+
+def test_ring_loop_rejects(rl, gpu):
+    import ringstep
+
+    B, V = 4, 1024
+    w = synth.make_decode(7191, B, 64, KVH, D, 40, 100)
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, 64, int(w.ctx.max()), B, V,
+                               greedy=True)
+    with pytest.raises(rl.RlrtError, match="fused kernel"):
+        run.loop(1)
+    run.close()
+    w = synth.make_decode(7192, B, QH, KVH, D, 40, 100)
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()), B, V,
+                               greedy=True)
+    with pytest.raises(rl.RlrtError, match="max_steps"):
+        run.loop(0)
+    run.close()
+    arena.close()
