@@ -869,9 +869,10 @@ def wl_ringstep(args):
     run.close()
     if stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
         raise rlrt.RlrtError(f"ring step stats {stats}, {n_comp} completions")
-    # the same pipeline as one persistent launch per call (rl_hip_ring_loop_launch)
+    # the same pipeline as one persistent launch per call (rl_hip_ring_loop_launch;
+    # consecutive steps write their own output slots)
     run = ringstep.RingStepRun(st.arena, st.layout, w.table, QH, MAX_CTX, B, VOCAB, input_slots=LOGIT_COPIES,
-                               output_slots=1, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
+                               output_slots=2, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
     for sl in range(LOGIT_COPIES):
         run.set_inputs(sl, w.q, kn, vn, logits)
     for _ in range(K + W):
@@ -914,7 +915,9 @@ def wl_ringstep(args):
             "note": "per step: the turn kernel (one wave: the previous step's 64 completions published and 64 "
                     "descriptors admitted over PCIe), the fused attention + sampling launch and its merge + append "
                     "kernel; loop_step_us: the same turns and steps in one persistent launch of K steps "
-                    "(rl_hip_ring_loop_launch: grid barriers between turn, step and merge); launched_fused_step_us: "
+                    "(rl_hip_ring_loop_launch: the turn on its own wave beside the steps, a step released once every "
+                    "workgroup has finished the one before, a step's split rows merged by the next step's sampling "
+                    "waves); launched_fused_step_us: "
                     "the same two kernels called directly; launched_step_us: rl_hip_decode_step + rl_hip_sample; "
                     "HIP events on the library stream"}
 

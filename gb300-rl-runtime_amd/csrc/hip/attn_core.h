@@ -139,23 +139,29 @@ struct StageMeta {
     bool bad;                   // ctx beyond max_ctx or a block outside the arena
 };
 
-// Context length of rollout b: from the ctx array (scalar load), or one
-// value fixed by the caller, or from a ctx array that the same launch
-// rewrites between steps (CtxLive; the row map is then read the same way).
+// Context length of rollout b and the block-table row it reads: from the
+// ctx array and p.row_map (scalar loads), or one context fixed by the
+// caller, or from copies in LDS (a persistent kernel's per-step arguments,
+// which the launch itself rewrites between steps).
+__device__ __forceinline__ uint32_t table_row_of(const AttnParams &p, uint32_t b)
+{
+    return p.row_map ? rl_sload(p.row_map + b) : b;
+}
 struct CtxFromArray {
-    static constexpr bool kLive = false;
     const uint32_t *ctx;
     __device__ __forceinline__ uint32_t operator()(uint32_t b) const { return rl_sload(ctx + b); }
+    __device__ __forceinline__ uint32_t table_row(const AttnParams &p, uint32_t b) const { return table_row_of(p, b); }
 };
 struct CtxFixed {
-    static constexpr bool kLive = false;
     uint32_t value;
     __device__ __forceinline__ uint32_t operator()(uint32_t) const { return value; }
+    __device__ __forceinline__ uint32_t table_row(const AttnParams &p, uint32_t b) const { return table_row_of(p, b); }
 };
-struct CtxLive {
-    static constexpr bool kLive = true;
-    const uint32_t *ctx;
-    __device__ __forceinline__ uint32_t operator()(uint32_t b) const { return rl_live_u32(ctx + b); }
+struct CtxLds {
+    RL_LDS const uint32_t *ctx;  // [batch]
+    RL_LDS const uint32_t *row;  // [batch]: the table row of each rollout
+    __device__ __forceinline__ uint32_t operator()(uint32_t b) const { return ctx[b]; }
+    __device__ __forceinline__ uint32_t table_row(const AttnParams &, uint32_t b) const { return row[b]; }
 };
 
 // Issue side of a wave: walks the wave's tile range and starts the copies.
@@ -189,7 +195,7 @@ struct Issuer {
     __device__ __forceinline__ void set_rollout(const AttnParams &p, uint32_t nb)
     {
         b = nb;
-        tb = !p.row_map ? nb : CtxFn::kLive ? rl_live_u32(p.row_map + nb) : rl_sload(p.row_map + nb);
+        tb = cf.table_row(p, nb);
         const uint32_t cin = cf(nb);
         ctx_bad = cin > p.max_ctx;
         ctx = ctx_bad ? p.max_ctx : cin;

@@ -233,17 +233,34 @@ __device__ __forceinline__ void merge_rows_waves(const AttnParams &pp, const App
     }
 }
 
-// One fused step by the calling workgroup (blockIdx.x), every thread of it;
-// lds is its LDS of FusedLayout::TOTAL bytes. LIVE: the contexts and the row
-// map were written by this launch (a persistent kernel's earlier steps), so
-// they are read past the scalar cache.
+// The sampling role of a fused step, for workgroups wg < f.si.sample_wgs:
+// rows wg, wg + sample_wgs, ... streamed by the whole workgroup.
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void fused_sample_part(const FusedParams &f, uint8_t *lds, uint32_t wg)
+{
+    if (wg < f.si.sample_wgs) {
+        StreamLds &L = *reinterpret_cast<StreamLds *>(lds);
+        for (uint32_t row = wg; row < f.sp.rows; row += f.si.sample_wgs) {
+            stream_sample_row<kFusedQuads>(f.sp, row, L);
+            __syncthreads();  // L is rewritten by the next row or by the attention below
+        }
+    }
+}
+
+// The attention role of a fused step by workgroup wg of the step's grid
+// (f.si.wgs workgroups, workgroup w on XCD w % 8), every thread of it: the
+// tile prefix, then each wave's piece. lds is its LDS of FusedLayout::TOTAL
+// bytes. LIVE: the contexts and the row map were written by this launch (a
+// persistent kernel's turn), so the prefix pass copies them into lctx / lrow
+// (LDS, batch entries each) and the attention reads them there, never
+// through the scalar cache.
 template <int D, int G, int DT, int TPB, bool LIVE = false>
-__device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *lds)
+__device__ __forceinline__ void fused_attn_part(const FusedParams &f, uint8_t *lds, uint32_t wg,
+                                                RL_LDS uint32_t *lctx = nullptr, RL_LDS uint32_t *lrow = nullptr)
 {
     using C = Cfg<D, G, DT, TPB>;
     using LY = FusedLayout<D, G, DT, TPB>;
     const AttnParams &p = f.p;
-    const uint32_t wg = blockIdx.x;
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
@@ -251,21 +268,6 @@ __device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *l
 
     if (wg == 0 && tid == 0)
         *f.si_out = f.si;  // read by the merge kernel, or by the next call of a pipeline
-
-    // ---- the previous step's rows: merge and append, one row per sampling wave ---
-    if (sampler && f.has_prev)
-        merge_rows_waves<D, G, DT>(f.pp, f.pap, *f.psi, wg * kFWaves + (uint32_t)wave, f.si.sample_wgs * kFWaves,
-                                   lane);
-
-    // ---- sampling role ----------------------------------------------------------
-    if (sampler) {
-        StreamLds &L = *reinterpret_cast<StreamLds *>(lds);
-        for (uint32_t row = wg; row < f.sp.rows; row += f.si.sample_wgs) {
-            stream_sample_row<kFusedQuads>(f.sp, row, L);
-            __syncthreads();  // L is rewritten by the next row or by the attention below
-        }
-    }
-
     // ---- tile prefix over the rollouts, in LDS -----------------------------------
     RL_LDS uint32_t *cum = (RL_LDS uint32_t *)(lds + LY::CUM_OFF);
     RL_LDS uint32_t *wtot = (RL_LDS uint32_t *)(lds + LY::Q_OFF);  // q slots as scratch until the copies start
@@ -273,8 +275,14 @@ __device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *l
         const uint32_t per = (p.batch + kFThreads - 1) / kFThreads;
         const uint32_t b0 = min(tid * per, p.batch), b1 = min(b0 + per, p.batch);
         uint32_t S = 0;
-        for (uint32_t bb = b0; bb < b1; bb++)
-            S += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+        for (uint32_t bb = b0; bb < b1; bb++) {
+            const uint32_t cb = p.ctx[bb];
+            if constexpr (LIVE) {
+                lctx[bb] = cb;
+                lrow[bb] = p.row_map ? p.row_map[bb] : bb;
+            }
+            S += tiles_of(p, cb) * p.kv_heads;
+        }
         const uint32_t inc = rl_wave_incl_scan_u32(S);
         if (lane == 63)
             wtot[wave] = inc;
@@ -291,7 +299,7 @@ __device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *l
             cum[bb] = c;
             if (wg == 0)
                 p.cum[bb] = c;
-            c += tiles_of(p, p.ctx[bb]) * p.kv_heads;
+            c += tiles_of(p, LIVE ? lctx[bb] : p.ctx[bb]) * p.kv_heads;
         }
         if (tid == 0) {
             cum[p.batch] = U;
@@ -319,11 +327,25 @@ __device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *l
     RL_LDS uint8_t *st = (RL_LDS uint8_t *)lds + wave * C::STAGE;
     RL_LDS uint8_t *qs = (RL_LDS uint8_t *)lds + LY::Q_OFF + wave * kFStages * C::QSLOT;
     if constexpr (LIVE)
-        attn_stream<D, G, DT, TPB, kFStages>(p, CtxLive{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b, cum[b],
-                                             st, kFWaves * C::STAGE, qs, lane);
+        attn_stream<D, G, DT, TPB, kFStages>(p, CtxLds{lctx, lrow}, xcd_base(x, U, f.si) + k, s_begin, s_end, b,
+                                             cum[b], st, kFWaves * C::STAGE, qs, lane);
     else
         attn_stream<D, G, DT, TPB, kFStages>(p, CtxFromArray{p.ctx}, xcd_base(x, U, f.si) + k, s_begin, s_end, b,
                                              cum[b], st, kFWaves * C::STAGE, qs, lane);
+}
+
+
+// One fused step by workgroup wg: the previous pipeline step's rows merged
+// (sampling waves, when f.has_prev), the sampling, the attention.
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void fused_step_body(const FusedParams &f, uint8_t *lds, uint32_t wg)
+{
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (wg < f.si.sample_wgs && f.has_prev)
+        merge_rows_waves<D, G, DT>(f.pp, f.pap, *f.psi, wg * kFWaves + (uint32_t)wave, f.si.sample_wgs * kFWaves,
+                                   (int)(threadIdx.x & 63));
+    fused_sample_part<D, G, DT, TPB>(f, lds, wg);
+    fused_attn_part<D, G, DT, TPB>(f, lds, wg);
 }
 
 template <int D, int G, int DT, int TPB>
@@ -332,7 +354,7 @@ __global__ __launch_bounds__(kFThreads) void decode_fused_kernel(FusedParams f)
     using LY = FusedLayout<D, G, DT, TPB>;
     static_assert(LY::FITS, "fused step LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
-    fused_step_body<D, G, DT, TPB>(f, lds);
+    fused_step_body<D, G, DT, TPB>(f, lds, blockIdx.x);
 }
 
 // Combines the partials of every row split across pieces (merge_span), writes
@@ -370,28 +392,47 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 // ---- the self-scheduled ring loop ----------------------------------------------
 // One cooperative launch of one workgroup per compute unit runs the
 // ring-driven batched step for as many steps as the rings call for, with no
-// launch between steps. Per step:
-//  turn    workgroup 0's first wave runs the ring turn (ring_core.h: publish
-//          the step just decoded, admit descriptors into free rows, write the
-//          rows' step arguments), then releases a flag; the other workgroups
-//          wait for it (bounded) and acquire. The turn also decides the end:
-//          admission has ended and no row decodes next step, or the step
-//          count reached max_steps.
-//  step    fused_step_body over the step's slots: attention tiles beside the
-//          sampling of the step's logits; rows read the rollout-ordered block
-//          table through the row map.
-//  merge   after a grid barrier, every wave merges split rows (one row per
-//          wave) and appends the step's K/V token; then a second barrier, so
-//          the next turn and step see every write.
-// Grid barriers: each workgroup releases its writes device-wide, adds one to
-// a counter and waits (bounded, acquire) until all workgroups of this epoch
-// have; a wait that runs out sets an error word that ends every workgroup's
-// loop at its next barrier. Cooperative launch keeps every workgroup
-// resident, so the waits are never for a workgroup that cannot run.
+// launch between steps. Two roles:
+//  turn   wave 0 of workgroup 0, beside the steps: turn t (ring_core.h)
+//         publishes step t - 1 (the hw_worker_sim rule does not depend on
+//         the token, so it runs while step t - 1 is still streaming) and
+//         admits descriptors for step t into argument set t % 2, once step
+//         t - 2's merges have released that set and step workspace t % 2.
+//         It releases step t (the go word) as soon as every step workgroup
+//         has finished step t - 1, then makes step t - 1's completions
+//         visible once its merges are done.
+//  steps  workgroups kLoopService.. (the same number on each XCD; the other
+//         workgroups of the first kLoopService, one per XCD, keep the turn
+//         off the steps' compute units): step t over argument set and step
+//         workspace t % 2 and step t's slots. The sampling workgroups first
+//         merge step t - 1's split rows (one row per wave; every workgroup
+//         has finished step t - 1 when step t is released) and sample the
+//         step's logits; the other workgroups' waves first append the
+//         step's K/V tokens (one (row, kv head) per wave; the attention
+//         masks positions past the context, the appended one among them);
+//         then every workgroup streams its attention pieces, split rows
+//         left as partials for the next step's merges. When the loop ends,
+//         the sampling workgroups merge the last step's rows.
+// Hand-offs are monotonic counters in the workspace: a release fence and an
+// atomic add by the producer, a bounded wait and an acquire fence by the
+// consumer; the counts of finished steps and of merges are kept per step
+// parity. A wait that runs out sets an error word that ends every role's
+// loop at its next wait. Cooperative launch keeps every workgroup resident,
+// so no wait is for a workgroup that cannot run. Step t's merges write
+// output slot t % output_slots while step t + 1 runs, so output_slots is at
+// least 2.
+constexpr uint32_t kLoopService = kXcds;  // workgroups kept off the steps: the turn's, one per XCD
+
 struct LoopParams {
-    RingParams rp;
-    FusedParams f;            // the step over input / output slot 0 (the slots are offsets from it)
-    AppendParams ap;          // the append over input slot 0
+    RingParams rp;            // the turn's arguments over argument set 0
+    FusedParams f;            // the step over input / output slot 0, argument set 0, step workspace 0
+    AppendParams ap;          // the append over input slot 0, argument set 0
+    // argument set 1 and step workspace 1
+    uint32_t *ctx1, *pos1, *rmap1;
+    uint64_t *rseed1, *rstep1;
+    uint32_t *cum1;
+    float *part1;
+    SplitIn *si_out1;
     size_t q_slot, out_slot;  // bytes per input slot of q, per output slot of the 16-bit outputs
     size_t out32_slot;        // floats per output slot of the fp32 outputs
     size_t logits_slot;       // floats per input slot of the logits
@@ -402,23 +443,37 @@ struct LoopParams {
     uint32_t input_slots, output_slots;
     uint64_t first_step;
     uint32_t max_steps;
-    uint32_t *sync;           // device [4], zeroed: go flag, barrier count, error, spare
-    uint64_t go_ticks;        // longest wait for the turn, in 100 MHz clock ticks
-    uint64_t bar_ticks;       // longest wait at a grid barrier
+    uint32_t *sync;           // device [8], zeroed: see kSync*
+    uint64_t go_ticks;        // longest wait for a turn, in 100 MHz clock ticks
+    uint64_t bar_ticks;       // longest wait for a step's workgroups or merges
 };
 
 enum : uint32_t { kLoopSyncTimeout = 5 };  // stats[3] when a wait of the loop ran out
+// The words at LoopParams::sync: the turn's go word; step workgroups done
+// with even / odd steps; sampling workgroups done with the merges of even /
+// odd steps; the error word.
+enum : uint32_t { kSyncGo = 0, kSyncSteps = 1, kSyncMerges = 3, kSyncError = 5 };
+
+// Counter of step u's parity in the pair at c, and its value once all n
+// producers are done with step u.
+__device__ __forceinline__ uint32_t par_ctr(uint32_t c, uint32_t u) { return c + (u & 1); }
+__device__ __forceinline__ uint32_t par_target(uint32_t u, uint32_t n) { return (u / 2 + 1) * n; }
 
 // The loop's arguments, read from the kernel-argument segment through a
 // pointer the optimizer cannot see through: each phase reloads (scalar loads
 // of memory that never changes) the fields it uses, instead of every phase's
 // fields being hoisted out of the loop and held in registers across all of
-// it, which spills.
-__device__ __forceinline__ const RL_CONST LoopParams &loop_args()
+// it, which spills. Only the kernel itself has the segment's address
+// (a called function gets it as an argument: loop_args_at).
+__device__ __forceinline__ const RL_CONST LoopParams &loop_args_at(uint64_t a)
 {
-    uint64_t a = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(a));
     return *(const RL_CONST LoopParams *)a;
+}
+
+__device__ __forceinline__ const RL_CONST LoopParams &loop_args()
+{
+    return loop_args_at((uint64_t)__builtin_amdgcn_kernarg_segment_ptr());
 }
 
 template <class T>
@@ -429,33 +484,264 @@ __device__ __forceinline__ T kcopy(const RL_CONST T &x)
     return v;
 }
 
-// Grid barrier number `epoch` (all gridDim.x workgroups): this workgroup's
-// writes released device-wide, the count raised, a bounded wait (acquire)
-// for every workgroup of the epoch. False when the wait ran out or another
-// workgroup's did (the error word), which ends the loop.
-__device__ bool loop_barrier(uint32_t *sync, uint64_t limit_ticks, uint32_t epoch, uint32_t *s_ok)
+__device__ __forceinline__ uint32_t sync_load(const uint32_t *w)
 {
+    return __hip_atomic_load(const_cast<uint32_t *>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait (acquire) until counter sync[c] reaches target. False when
+// the wait ran out or another wait did (the error word, then set).
+__device__ __forceinline__ bool loop_wait(uint32_t *sync, uint32_t c, uint32_t target, uint64_t limit_ticks)
+{
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (sync_load(&sync[c]) < target) {
+        if (sync_load(&sync[kSyncError]) != 0 || __builtin_amdgcn_s_memrealtime() - t0 > limit_ticks) {
+            __hip_atomic_store(&sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the producers' writes are visible here
+    return true;
+}
+
+// Bounded wait (acquire) for the turn's word on step t: true to run step t,
+// false when the loop ends before it (or a wait ran out). The word is the
+// number of steps released, with bit 31 set once no further step will be.
+__device__ __forceinline__ bool loop_go(uint32_t *sync, uint32_t t, uint64_t limit_ticks)
+{
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (;;) {
+        const uint32_t v = sync_load(&sync[kSyncGo]);
+        if ((v & 0x7FFFFFFFu) > t)
+            break;
+        if (v >> 31)
+            return false;
+        if (sync_load(&sync[kSyncError]) != 0 || __builtin_amdgcn_s_memrealtime() - t0 > limit_ticks) {
+            __hip_atomic_store(&sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return true;
+}
+
+// One count for the calling workgroup, after its writes are released
+// device-wide. Every thread of the workgroup calls it. Each wave waits for
+// its own stores to reach the L2 (the barrier does not wait for other
+// waves' stores); then one release - an L2 write-back, which every wave
+// doing its own would repeat while other workgroups still stream - covers
+// them all.
+__device__ __forceinline__ void loop_signal_wg(uint32_t *sync, uint32_t c)
+{
+    rl_wait_vmcnt<0>();
     __syncthreads();
     if (threadIdx.x == 0) {
-        __threadfence();  // this workgroup's writes, device-wide, before it counts in
-        atomicAdd(&sync[1], 1u);
-        const uint32_t target = epoch * gridDim.x;
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        uint32_t ok = 1;
-        while (__hip_atomic_load(&sync[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (__hip_atomic_load(&sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                __builtin_amdgcn_s_memrealtime() - t0 > limit_ticks) {
-                ok = 0;
-                __hip_atomic_store(&sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        __threadfence();  // the others' writes are visible to this workgroup
-        *s_ok = ok;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        rl_wait_vmcnt<0>();  // the write-back done before the count
+        atomicAdd(&sync[c], 1u);
     }
+}
+
+// Thread 0 waits (bounded) for counter c to reach target; the workgroup
+// follows. False when the wait ran out.
+__device__ __forceinline__ bool loop_wait_wg(uint32_t *sync, uint32_t c, uint32_t target, uint64_t limit,
+                                             uint32_t *s_flag)
+{
+    if (threadIdx.x == 0)
+        *s_flag = loop_wait(sync, c, target, limit) ? 1u : 0u;
     __syncthreads();
-    return *s_ok != 0;
+    return *s_flag != 0;
+}
+
+// The turn's admission may wait for the host only after step u's
+// completions are visible, which needs its merges done (n sampling
+// workgroups).
+struct MergedBy {
+    static constexpr bool kDefer = true;
+    uint32_t *sync;
+    uint32_t u, n;
+    uint64_t limit;
+    __device__ bool ready() const { return loop_wait(sync, par_ctr(kSyncMerges, u), par_target(u, n), limit); }
+};
+
+// Step t's kernel arguments: argument set and workspace t % 2, slots.
+__device__ __forceinline__ FusedParams loop_step_params(const RL_CONST LoopParams &L, uint32_t t)
+{
+    const uint64_t k = L.first_step + t;
+    const size_t si = k % L.input_slots, so = k % L.output_slots;
+    FusedParams f = kcopy(L.f);
+    if (t & 1) {
+        f.p.ctx = L.ctx1;
+        f.p.row_map = L.rmap1;
+        f.p.cum = L.cum1;
+        f.p.part = L.part1;
+        f.si_out = L.si_out1;
+        f.sp.seed = L.rseed1;
+        f.sp.steps = L.rstep1;
+        f.sp.draw_ids = L.rmap1;
+    }
+    f.p.q = (const uint16_t *)((const uint8_t *)f.p.q + si * L.q_slot);
+    f.p.out = (uint16_t *)((uint8_t *)f.p.out + so * L.out_slot);
+    f.p.out_f32 = f.p.out_f32 ? f.p.out_f32 + so * L.out32_slot : nullptr;
+    f.sp.logits = f.sp.logits + si * L.logits_slot;
+    f.sp.token_out = f.sp.token_out + so * L.tok_slot;
+    f.sp.logprob_out = f.sp.logprob_out + so * L.tok_slot;
+    return f;
+}
+
+// Step u's split rows merged by the sampling waves of workgroup wg (one row
+// per wave) - once every step workgroup has finished step u, which the
+// caller may already know (wait false) - then counted.
+template <int D, int G, int DT>
+__device__ __forceinline__ bool loop_merge_step(uint32_t u, uint32_t wg, uint32_t n_wgs, bool wait, uint32_t *s_flag)
+{
+    if (wait) {
+        const RL_CONST LoopParams &L = loop_args();
+        if (!loop_wait_wg(L.sync, par_ctr(kSyncSteps, u), par_target(u, n_wgs), L.bar_ticks, s_flag))
+            return false;
+    }
+    const RL_CONST LoopParams &L = loop_args();
+    const FusedParams f = loop_step_params(L, u);
+    AppendParams none = {};
+    none.arena = nullptr;
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    merge_rows_waves<D, G, DT, true>(f.p, none, f.si, wg * kFWaves + wave, f.si.sample_wgs * kFWaves,
+                                     (int)(threadIdx.x & 63));
+    loop_signal_wg(L.sync, par_ctr(kSyncMerges, u));
+    return true;
+}
+
+// The attention role of step t by step workgroup wg, compiled as a function
+// of its own (the sampling code beside it in one body made the compiler give
+// up the tight per-tile loop). Arguments arrive in vector registers; they are
+// wave-uniform, so they are read back from the first lane. args: the
+// kernel-argument segment's address, which a called function cannot obtain
+// itself.
+template <int D, int G, int DT, int TPB>
+__device__ __attribute__((noinline)) void loop_attn_fn(uint32_t args_lo, uint32_t args_hi, uint32_t t_in,
+                                                       uint32_t wg_in, uint32_t lds_in, uint32_t lctx_in,
+                                                       uint32_t lrow_in)
+{
+    const auto first = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
+    const uint64_t args = (uint64_t)first(args_lo) | ((uint64_t)first(args_hi) << 32);
+    const uint32_t t = first(t_in);
+    const uint32_t wg = first(wg_in);
+    RL_LDS uint8_t *lds = (RL_LDS uint8_t *)(uintptr_t)first(lds_in);
+    RL_LDS uint32_t *lctx = (RL_LDS uint32_t *)(uintptr_t)first(lctx_in);
+    RL_LDS uint32_t *lrow = (RL_LDS uint32_t *)(uintptr_t)first(lrow_in);
+    fused_attn_part<D, G, DT, TPB, true>(loop_step_params(loop_args_at(args), t), (uint8_t *)lds, wg, lctx, lrow);
+}
+
+template <int D, int G, int DT, int TPB>
+__device__ __forceinline__ void loop_steps(uint32_t wg, uint32_t n_wgs, uint8_t *lds, RL_LDS uint32_t *lctx,
+                                           RL_LDS uint32_t *lrow, uint32_t *s_go, uint32_t *s_flag)
+{
+    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const uint32_t n_samp = loop_args().f.si.sample_wgs;
+    const bool sampler = wg < n_samp;
+    for (uint32_t t = 0;; t++) {
+        // (s_go is rewritten only after the barriers of a whole step; s_flag,
+        // which the waits below write, may change while s_go is still read)
+        if (threadIdx.x == 0) {
+            const RL_CONST LoopParams &L = loop_args();
+            *s_go = loop_go(L.sync, t, L.go_ticks) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!*s_go) {
+            // the loop ends before step t: the last step's merges
+            if (sampler && t > 0)
+                (void)loop_merge_step<D, G, DT>(t - 1, wg, n_wgs, true, s_flag);
+            break;
+        }
+        if (sampler) {
+            // ---- step t - 1's split rows, then the sampling of step t's logits ----------
+            if (t > 0)
+                (void)loop_merge_step<D, G, DT>(t - 1, wg, n_wgs, false, s_flag);
+            fused_sample_part<D, G, DT, TPB>(loop_step_params(loop_args(), t), lds, wg);
+        } else {
+            // ---- step t's K/V token appends, one (row, kv head) per wave -----------------
+            const RL_CONST LoopParams &L = loop_args();
+            const uint64_t k = L.first_step + t;
+            AppendParams ap = kcopy(L.ap);
+            if (t & 1) {
+                ap.positions = L.pos1;
+                ap.row_map = L.rmap1;
+            }
+            ap.k_new = ap.k_new + (k % L.input_slots) * L.kv_slot;
+            ap.v_new = ap.v_new + (k % L.input_slots) * L.kv_slot;
+            const uint32_t pairs = L.f.p.batch * ap.kv_heads;
+            for (uint32_t pr = (wg - n_samp) * kFWaves + wave; pr < pairs; pr += (n_wgs - n_samp) * kFWaves)
+                append_row(ap, pr / ap.kv_heads, pr % ap.kv_heads, (uint32_t)lane, 64);
+        }
+        const uint64_t args = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+        loop_attn_fn<D, G, DT, TPB>((uint32_t)args, (uint32_t)(args >> 32), t, wg,
+                                    (uint32_t)(uintptr_t)(RL_LDS uint8_t *)lds, (uint32_t)(uintptr_t)lctx,
+                                    (uint32_t)(uintptr_t)lrow);
+        loop_signal_wg(loop_args().sync, par_ctr(kSyncSteps, t));
+    }
+}
+
+__device__ __forceinline__ void loop_turns(uint16_t *s_free, int lane)
+{
+    uint32_t t = 0;
+    bool ok = true;
+    for (;; t++) {
+        const RL_CONST LoopParams &L = loop_args();
+        uint32_t *sync = L.sync;
+        const uint32_t n_samp = L.f.si.sample_wgs;
+        const bool last = t >= L.max_steps;  // this turn only publishes
+        // argument set and workspace t % 2 are free once step t - 2's merges are done
+        if (t >= 2 &&
+            !(ok = loop_wait(sync, par_ctr(kSyncMerges, t - 2), par_target(t - 2, n_samp), L.bar_ticks)))
+            break;
+        RingParams rp = kcopy(L.rp);
+        if (t & 1) {
+            rp.ctx = L.ctx1;
+            rp.pos = L.pos1;
+            rp.rmap = L.rmap1;
+            rp.rseed = L.rseed1;
+            rp.rstep = L.rstep1;
+        }
+        const size_t so = (L.first_step + t) % L.output_slots;
+        rp.row_rollout = L.row_rollout && !last ? L.row_rollout + so * rp.batch : nullptr;
+        TurnOut to;
+        const MergedBy rel{sync, t - 1, n_samp, L.bar_ticks};  // used only by turns that publish (t >= 1)
+        const uint32_t held = ring_turn(rp, t > 0 ? 1u : 0u, last ? 0u : 1u, s_free, &to, rel);
+        // admission over and every row free: later steps would decode nothing
+        const bool end = last || (to.status != kRunning && held == 0);
+        // step t starts once every workgroup has finished step t - 1 (its K/V
+        // appends among it)
+        if (!end && t >= 1 &&
+            !(ok = loop_wait(sync, par_ctr(kSyncSteps, t - 1), par_target(t - 1, L.f.si.wgs), L.bar_ticks)))
+            break;
+        if (lane == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the rows' step arguments before the word
+            __hip_atomic_store(&sync[kSyncGo], end ? (t | 0x80000000u) : t + 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (to.pending) {
+            // step t - 1's completions: visible once its results are all written
+            if (!(ok = loop_wait(sync, par_ctr(kSyncMerges, t - 1), par_target(t - 1, n_samp), L.bar_ticks)))
+                break;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+            if (lane == 0)
+                sys_store(&rp.dq->tail, to.dtail);
+        }
+        if (end)
+            break;
+    }
+    if (lane == 0) {
+        const RL_CONST LoopParams &L = loop_args();
+        if (!ok)  // make sure every role stops
+            __hip_atomic_store(&L.sync[kSyncGo], t | 0x80000000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (L.steps_run)
+            *L.steps_run = t;
+        if (!ok || sync_load(&L.sync[kSyncError]) != 0)
+            L.rp.stats[3] = kLoopSyncTimeout;
+    }
 }
 
 template <int D, int G, int DT, int TPB>
@@ -465,107 +751,14 @@ __global__ __launch_bounds__(kFThreads) void ring_loop_kernel(LoopParams)
     static_assert(LY::FITS, "fused step LDS");
     static_assert(2 * kMaxBatch <= LY::TOTAL, "the turn's free-row list fits the stage buffers");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LY::TOTAL];
-    __shared__ uint32_t s_end;  // the turn's decision, read after it
-    __shared__ uint32_t s_ok;   // a barrier's outcome (its own word: s_end is rewritten while it is read)
-    const uint32_t wg = blockIdx.x, nwg = gridDim.x;
-    const uint32_t tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
-    uint32_t epoch = 0;
-    uint32_t n = 0;
-    for (;; n++) {
-        // ---- the turn, and the decision to go on -------------------------------
-        {
-            const RL_CONST LoopParams &L = loop_args();
-            const bool last = n >= L.max_steps;  // this turn only publishes
-            uint32_t *sync = L.sync;
-            if (wg == 0 && wave == 0) {
-                RingParams rp = kcopy(L.rp);
-                const size_t so = (L.first_step + n) % L.output_slots;
-                rp.row_rollout = L.row_rollout && !last ? L.row_rollout + so * rp.batch : nullptr;
-                uint32_t status = 0;
-                // the stage buffers hold the free-row list: no tile is in flight
-                const uint32_t held = ring_turn(rp, n > 0 ? 1u : 0u, last ? 0u : 1u,
-                                               reinterpret_cast<uint16_t *>(lds), &status);
-                // admission over and every row free: later steps would decode nothing
-                const bool end = last || (status != kRunning && held == 0);
-                if (lane == 0) {
-                    __threadfence();  // the rows' step arguments before the flag
-                    __hip_atomic_store(&sync[0], (n + 1) | (end ? 0x80000000u : 0u), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    s_end = end ? 1u : 0u;
-                }
-            } else if (wg != 0 && tid == 0) {
-                const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-                const uint64_t limit = L.go_ticks;
-                uint32_t v;
-                for (;;) {
-                    v = __hip_atomic_load(&sync[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if ((v & 0x7FFFFFFFu) >= n + 1)
-                        break;
-                    if (__hip_atomic_load(&sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0 ||
-                        __builtin_amdgcn_s_memrealtime() - t0 > limit) {
-                        __hip_atomic_store(&sync[2], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        v = 0x80000000u;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                __threadfence();  // the turn's writes are visible to this workgroup
-                s_end = v >> 31;
-            }
-            __syncthreads();
-            if (s_end)
-                break;
-        }
-
-        // ---- the step over this step's slots -------------------------------------
-        {
-            const RL_CONST LoopParams &L = loop_args();
-            const uint64_t k = L.first_step + n;
-            const size_t si = k % L.input_slots, so = k % L.output_slots;
-            FusedParams f = kcopy(L.f);
-            f.p.q = (const uint16_t *)((const uint8_t *)f.p.q + si * L.q_slot);
-            f.p.out = (uint16_t *)((uint8_t *)f.p.out + so * L.out_slot);
-            f.p.out_f32 = f.p.out_f32 ? f.p.out_f32 + so * L.out32_slot : nullptr;
-            f.sp.logits = f.sp.logits + si * L.logits_slot;
-            f.sp.token_out = f.sp.token_out + so * L.tok_slot;
-            f.sp.logprob_out = f.sp.logprob_out + so * L.tok_slot;
-            fused_step_body<D, G, DT, TPB, true>(f, lds);
-        }
-        {
-            const RL_CONST LoopParams &L = loop_args();
-            if (!loop_barrier(L.sync, L.bar_ticks, ++epoch, &s_ok))
-                break;
-        }
-
-        // ---- merge the split rows, append the step's token --------------------------
-        {
-            const RL_CONST LoopParams &L = loop_args();
-            const uint64_t k = L.first_step + n;
-            const size_t si = k % L.input_slots, so = k % L.output_slots;
-            AttnParams pp = kcopy(L.f.p);
-            pp.out = (uint16_t *)((uint8_t *)pp.out + so * L.out_slot);
-            pp.out_f32 = pp.out_f32 ? pp.out_f32 + so * L.out32_slot : nullptr;
-            AppendParams ap = kcopy(L.ap);
-            ap.k_new = ap.k_new + si * L.kv_slot;
-            ap.v_new = ap.v_new + si * L.kv_slot;
-            const SplitIn psi = kcopy(L.f.si);
-            merge_rows_waves<D, G, DT, true>(pp, ap, psi, wg * kFWaves + (uint32_t)wave, nwg * kFWaves, lane);
-        }
-        {
-            const RL_CONST LoopParams &L = loop_args();
-            if (!loop_barrier(L.sync, L.bar_ticks, ++epoch, &s_ok))
-                break;
-        }
-    }
-    if (wg == 0 && tid == 0) {
-        const RL_CONST LoopParams &L = loop_args();
-        if (L.steps_run)
-            *L.steps_run = n;
-        if (__hip_atomic_load(&L.sync[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
-            L.rp.stats[3] = kLoopSyncTimeout;
-    }
+    __shared__ uint32_t s_ctx[kFusedMaxBatch];  // the step's contexts and table rows (step workgroups)
+    __shared__ uint32_t s_row[kFusedMaxBatch];
+    __shared__ uint32_t s_go, s_flag;
+    if (blockIdx.x >= kLoopService)
+        loop_steps<D, G, DT, TPB>(blockIdx.x - kLoopService, gridDim.x - kLoopService, lds,
+                                  (RL_LDS uint32_t *)s_ctx, (RL_LDS uint32_t *)s_row, &s_go, &s_flag);
+    else if (blockIdx.x == 0 && threadIdx.x < 64)
+        loop_turns(reinterpret_cast<uint16_t *>(lds), (int)threadIdx.x);
 }
 
 struct FusedWs {
@@ -681,9 +874,9 @@ int launch_shape(int what, const rl_attn_decode_args_t *attn, const FusedParams 
 
 // Workgroups of the fused grid (one per compute unit, a multiple of 8) and
 // of them the sampling ones: one per row up to 64, never more than half.
-void grid_of(uint32_t rows, uint32_t &wgs, uint32_t &sample_wgs)
+void grid_of(uint32_t rows, uint32_t &wgs, uint32_t &sample_wgs, uint32_t avail = 0)
 {
-    wgs = rl_cu_count() / kXcds * kXcds;
+    wgs = avail ? avail : rl_cu_count() / kXcds * kXcds;
     if (wgs < 2 * kXcds)
         wgs = 2 * kXcds;
     uint32_t s = (rows + kXcds - 1) / kXcds * kXcds;
@@ -694,10 +887,12 @@ void grid_of(uint32_t rows, uint32_t &wgs, uint32_t &sample_wgs)
     sample_wgs = s;
 }
 
-SplitIn split_in_of(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp)
+// avail: workgroups the step may use (a multiple of 8; 0: one per compute
+// unit).
+SplitIn split_in_of(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp, uint32_t avail = 0)
 {
     SplitIn si;
-    grid_of(samp->rows, si.wgs, si.sample_wgs);
+    grid_of(samp->rows, si.wgs, si.sample_wgs, avail);
     si.tile_bytes = 2u * 16u * attn->layout.head_dim * 2u;
     const uint32_t rows_per_wg = (samp->rows + si.sample_wgs - 1) / si.sample_wgs;
     si.sample_bytes = (uint64_t)rows_per_wg * samp->vocab * 4u;
@@ -776,10 +971,10 @@ AttnParams attn_params_of(const rl_attn_decode_args_t *attn, uint8_t *ws, const 
 // The fused kernel's arguments for attention `attn` and sampling `samp` on
 // workspace ws; the previous pipeline step, if any, filled in by the caller.
 FusedParams fused_params_of(const rl_attn_decode_args_t *attn, const rl_sample_args_t *samp, void *workspace,
-                            uint32_t merge_rounds)
+                            uint32_t merge_rounds, uint32_t avail = 0)
 {
     FusedParams f;
-    f.si = split_in_of(attn, samp);
+    f.si = split_in_of(attn, samp, avail);
     f.si.merge_rounds = merge_rounds;
     const FusedWs w = fused_ws(attn, f.si);
     uint8_t *ws = (uint8_t *)workspace;
@@ -1070,22 +1265,41 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
         rl_set_error("%s: the shape does not fit the fused kernel (use rl_hip_ring_step_enqueue)", who);
         return -1;
     }
+    if (a->output_slots < 2) {
+        rl_set_error("%s: output_slots %u < 2 (a step's results are merged while the next step runs)", who,
+                     a->output_slots);
+        return -1;
+    }
     rl_sample_args_t s = samp_of(a);
     s.seed = L.rp.rseed;
     s.steps = L.rp.rstep;
     s.draw_ids = L.rp.rmap;  // the draw follows the rollout, not the row it was admitted into
     if (rl_attn_check(&t) || rl_sample_check(&s))
         return -1;
-    L.f = fused_params_of(&t, &s, ws + w.step, 0);
-    L.f.p.row_map = L.rp.rmap;
-    if (L.f.si.wgs > rl_cu_count()) {
-        rl_set_error("%s: %u workgroups for %u compute units", who, L.f.si.wgs, rl_cu_count());
+    const uint32_t grid = rl_cu_count() / kXcds * kXcds;
+    if (grid < kLoopService + 2 * kXcds) {
+        rl_set_error("%s: %u compute units are too few", who, rl_cu_count());
         return -1;
     }
-    // two barriers a step count to epoch * workgroups in 32 bits
-    if (max_steps == 0 || 2ull * (max_steps + 1ull) * L.f.si.wgs >= (1ull << 32)) {
+    {
+        // the sampling workgroups merge the previous step's rows, one per wave
+        uint32_t wgs, sample_wgs;
+        grid_of(s.rows, wgs, sample_wgs, grid - kLoopService);
+        const uint32_t rows = a->batch * a->kv_heads;
+        L.f = fused_params_of(&t, &s, ws + w.step, (rows + sample_wgs * kFWaves - 1) / (sample_wgs * kFWaves),
+                              grid - kLoopService);
+    }
+    L.f.p.row_map = L.rp.rmap;
+    const FusedWs fw = fused_ws(&t, L.f.si);
+    if (fw.total > w.step_bytes) {
+        rl_set_error("%s: step workspace %zu bytes < %zu", who, w.step_bytes, fw.total);
+        return -1;
+    }
+    // the counters (at most one per step workgroup and step) stay in 31 bits
+    const uint64_t per_step = L.f.si.wgs;
+    if (max_steps == 0 || (max_steps + 1ull) * per_step >= (1ull << 31)) {
         rl_set_error("%s: max_steps %u not in 1 .. %llu", who, max_steps,
-                     (unsigned long long)((1ull << 32) / (2ull * L.f.si.wgs) - 2));
+                     (unsigned long long)((1ull << 31) / per_step - 2));
         return -1;
     }
     rl_kv_append_args_t apa = {};
@@ -1102,6 +1316,14 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
     apa.v_new = a->v_new;
     L.ap = append_params(&apa);
     L.ap.row_map = L.rp.rmap;
+    L.ctx1 = (uint32_t *)(ws + w.ctx2);
+    L.pos1 = (uint32_t *)(ws + w.pos2);
+    L.rmap1 = (uint32_t *)(ws + w.rmap2);
+    L.rseed1 = (uint64_t *)(ws + w.rseed2);
+    L.rstep1 = (uint64_t *)(ws + w.rstep2);
+    L.cum1 = (uint32_t *)(ws + w.step2 + fw.cum_off);
+    L.part1 = (float *)(ws + w.step2 + fw.part_off);
+    L.si_out1 = (SplitIn *)(ws + w.step2 + fw.si_off);
     L.q_slot = B * qrow;
     L.out_slot = B * qrow;
     L.out32_slot = B * qrow / 2;
@@ -1117,14 +1339,15 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
     L.sync = (uint32_t *)(ws + w.ctl + kLoopSyncOff);
     // A turn waits at most max_idle polls for room on the completion ring and
     // as many for a descriptor, each poll one PCIe round trip and a short
-    // sleep (10 us is a generous bound); a step and its merge stream at most
-    // the device's memory once, far below 2 s.
-    L.go_ticks = 2000ull * L.rp.max_idle + 100000000ull;
+    // sleep (10 us is a generous bound), besides the merges of a step; a
+    // step and its merges stream at most the device's memory once, far
+    // below 2 s.
     L.bar_ticks = 200000000ull;
-    if (rl_check_hip(hipMemsetAsync(L.sync, 0, 4 * sizeof(uint32_t), rl_stream()), "hipMemsetAsync(loop sync)"))
+    L.go_ticks = 2000ull * L.rp.max_idle + 2 * L.bar_ticks;
+    if (rl_check_hip(hipMemsetAsync(L.sync, 0, 8 * sizeof(uint32_t), rl_stream()), "hipMemsetAsync(loop sync)"))
         return -1;
     const uint32_t G = a->q_heads / a->kv_heads;
     if (a->layout.head_dim == 128)
-        return loop_g<128>(L, L.f.si.wgs, G, a->dtype, a->layout.token_count);
-    return loop_g<64>(L, L.f.si.wgs, G, a->dtype, a->layout.token_count);
+        return loop_g<128>(L, grid, G, a->dtype, a->layout.token_count);
+    return loop_g<64>(L, grid, G, a->dtype, a->layout.token_count);
 }

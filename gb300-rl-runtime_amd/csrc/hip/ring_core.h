@@ -65,15 +65,35 @@ __device__ __forceinline__ uint32_t lanes_below(uint64_t m)
 }
 
 // Step arguments of a row that decodes seq_len next (rollout r), or of a row
-// that does not decode.
+// that does not decode: all five written every turn, so that a turn may
+// write a fresh set while the previous step still reads another.
 __device__ __forceinline__ void set_row_args(const RingParams &p, uint32_t i, bool dec, uint32_t r, uint32_t seq)
 {
     p.ctx[i] = dec ? seq : 0u;
     p.pos[i] = dec ? seq : 0xFFFFFFFFu;
     p.rstep[i] = dec ? (uint64_t)seq : 0ull;
+    p.rmap[i] = dec ? r : 0u;
+    p.rseed[i] = dec ? (p.seeds ? p.seeds[r] : (uint64_t)r) : 0ull;
     if (p.row_rollout)
         p.row_rollout[i] = dec ? r : 0xFFFFFFFFu;
 }
+
+// When the completions of a turn become visible. ReleaseNow: at the end of
+// the turn (and before an admission wait for the host). A deferring caller
+// (kDefer) releases them itself once the step they complete has all its
+// results written; ready() waits (bounded) for that, for the one case the
+// turn cannot defer: no row active and the host possibly waiting for those
+// completions before it submits more.
+struct ReleaseNow {
+    static constexpr bool kDefer = false;
+    __device__ bool ready() const { return true; }
+};
+
+struct TurnOut {
+    uint32_t status;   // admission status after the turn
+    uint32_t pending;  // completions written but not released (deferring callers)
+    uint32_t dtail;    // the completion ring tail that releases them
+};
 
 // One wave, between two decode steps: the publish of the step just decoded
 // (the hw_worker_sim rule for its token, completions in row order, finished
@@ -89,9 +109,11 @@ __device__ __forceinline__ void set_row_args(const RingParams &p, uint32_t i, bo
 // Run by one wave (lane = threadIdx.x % 64 of that wave); s_free is LDS of
 // kMaxBatch entries. Returns (in every lane) how many rows the turn leaves
 // held - decoding next step, or a finished descriptor still to be pushed -
-// and the admission status in *status_out when given.
+// and the admission status (and, for deferring callers, the completions left
+// to release) in *out when given.
+template <class Rel = ReleaseNow>
 __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t do_poll, uint16_t *s_free,
-                              uint32_t *status_out = nullptr)
+                              TurnOut *out = nullptr, const Rel &rel = Rel())
 {
     const uint32_t lane = threadIdx.x & 63;
     RingCtl *c = p.ctl;
@@ -192,6 +214,8 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
             }
         } else if (k == kDecode) {
             set_row_args(p, i, true, d.rollout_id, d.seq_len);  // the row decodes again
+        } else if (k == kPass) {
+            set_row_args(p, i, false, 0u, 0u);  // held for a publish (turns that do not publish)
         }
         n_done += (uint32_t)__builtin_popcountll(fm);
         n_dec += do_publish ? (uint32_t)__builtin_popcountll(__ballot(k == kDecode)) : 0u;
@@ -219,7 +243,7 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
             if (avail == 0) {
                 if (active > 0)
                     break;  // rows to decode: go with them
-                if (dq_pending) {
+                if (dq_pending && rel.ready()) {
                     // the host may wait for these completions before it submits more
                     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
                     if (lane == 0)
@@ -264,8 +288,6 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
                 const bool dec = d.seq_len < d.max_tokens;
                 p.rows[row] = d;
                 p.kind[row] = dec ? kDecode : kPass;
-                p.rmap[row] = dec ? d.rollout_id : 0u;
-                p.rseed[row] = dec ? (p.seeds ? p.seeds[d.rollout_id] : (uint64_t)d.rollout_id) : 0ull;
                 set_row_args(p, row, dec, d.rollout_id, d.seq_len);
             }
             const uint32_t n = (uint32_t)__builtin_popcountll(um);
@@ -286,10 +308,11 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
     }
 
     // ---- releases: the completions, then the consumed descriptors ------------
-    if (dq_pending || head != head0) {
+    const bool release_dq = dq_pending && !Rel::kDefer;
+    if (release_dq || head != head0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
         if (lane == 0) {
-            if (dq_pending)
+            if (release_dq)
                 sys_store(&p.dq->tail, dtail);
             if (head != head0)
                 sys_store(&p.cq->head, head);
@@ -297,11 +320,8 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
     }
 
     // ---- rows left free decode nothing next step --------------------------------
-    for (uint32_t j = taken + lane; j < nfree; j += 64) {
-        const uint32_t i = s_free[j];
-        p.rmap[i] = 0u;
-        set_row_args(p, i, false, 0u, 0u);
-    }
+    for (uint32_t j = taken + lane; j < nfree; j += 64)
+        set_row_args(p, s_free[j], false, 0u, 0u);
     if (lane == 0) {
         c->init = 1;
         c->status = status;
@@ -317,18 +337,24 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
         p.stats[2] = c->steps;
         p.stats[3] = status;
     }
-    if (status_out)
-        *status_out = status;
+    if (out) {
+        out->status = status;
+        out->pending = dq_pending && Rel::kDefer ? 1u : 0u;
+        out->dtail = dtail;
+    }
     return active;
 }
 
 // ---- host side -------------------------------------------------------------
 
 // The ring step's workspace: the control record at ctl (the self-scheduled
-// loop's four sync words at ctl + kLoopSyncOff), the row table and the rows'
-// step arguments, then the fused step's workspace at step.
+// loop's sync words at ctl + kLoopSyncOff), the row table and the rows' step
+// arguments, the fused step's workspace at step; then a second set of step
+// arguments and a second step workspace, which the self-scheduled loop
+// alternates with the first (the launched pipeline uses the first only).
 struct RingWs {
-    size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, step, total;
+    size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, step;
+    size_t rmap2, ctx2, pos2, rseed2, rstep2, step2, total;
     size_t step_bytes;
 };
 constexpr size_t kLoopSyncOff = 128;  // past the 40-byte RingCtl, before the rows at 256
@@ -418,7 +444,13 @@ inline int ring_layout(const rl_ring_step_args_t *a, RingWs &w)
     w.step_bytes = rl_hip_decode_sample_step_workspace(&t, &s);
     if (w.step_bytes == 0)
         return -1;
-    w.total = w.step + up256(w.step_bytes);
+    w.rmap2 = w.step + up256(w.step_bytes);
+    w.ctx2 = w.rmap2 + up256(B * 4);
+    w.pos2 = w.ctx2 + up256(B * 4);
+    w.rseed2 = w.pos2 + up256(B * 4);
+    w.rstep2 = w.rseed2 + up256(B * 8);
+    w.step2 = w.rstep2 + up256(B * 8);
+    w.total = w.step2 + up256(w.step_bytes);
     return 0;
 }
 

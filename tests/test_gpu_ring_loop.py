@@ -2,27 +2,34 @@
 batched decode step as one persistent launch, held to the launched pipeline
 (rl_hip_ring_step_enqueue), which the ring-step tests pin to the oracle and
 to hw_worker_sim_run. Each case runs the same submissions through both on
-copies of the same arena and compares everything the host can see:
+copies of the same arena and compares what the host can see: completions,
+stats, per-step rows, tokens and logprobs (bits) and the final arena are
+equal; the attention, which the loop splits over the compute units left
+beside its turn and merges (a different split from the launched step's, so
+other fp32 roundings), is checked against the oracle's fp64 as the
+ring-step tests check the launched step's.
 
 1. The control rule over many steps (8 rows, 13 descriptors of 1-8 tokens,
    NEEDS_REWARD at 32, a passthrough, a dropped opcode, STOP): the loop
-   ends by itself once admission has ended and every row is free; its
-   completions, stats, per-step rows, tokens, logprobs and attention (bf16
-   and fp32 bits) and the final arena equal the launched run's, whose later
-   steps decoded nothing.
+   ends by itself once admission has ended and every row is free, and the
+   launched run's later steps decoded nothing; every decoded row of every
+   step against the oracle with the rollout's context at that step.
 2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
-   128,256 logits): max_steps 1, then a second loop that finds only STOP;
-   bit-equal to two launched steps.
+   128,256 logits): max_steps 1, then a second loop that finds only STOP,
+   against two launched steps.
 3. Exit paths: idle limit, bad rollout id, the host's stop flag (zero steps
    run, status 1 / 2 / 4) and a full completion ring (status 3; the finished
    descriptor stays in its row until a later loop pushes it).
-4. Arguments the loop does not take: max_steps 0 and a GQA group of 8 at
-   d128 (outside the fused kernel) return errors before any launch."""
+4. Arguments the loop does not take: max_steps 0, one output slot (a step's
+   split rows are merged while the next step runs, so consecutive steps need
+   their own slots) and a GQA group of 8 at d128 (outside the fused kernel)
+   return errors before any launch."""
 import ctypes as C
 
 import numpy as np
 import pytest
 
+import gpu_helpers as gh
 import synth
 
 pytestmark = pytest.mark.gpu
@@ -35,7 +42,7 @@ def _outputs(run, steps):
 
 
 def _same_outputs(a, b, what):
-    for k in ("rows", "tok", "out", "out32"):
+    for k in ("rows", "tok"):
         assert np.array_equal(a[k], b[k]), (what, k)
     assert np.array_equal(a["lp"].view(np.uint32), b["lp"].view(np.uint32)), (what, "lp")
 
@@ -72,7 +79,7 @@ def _control_rule_case(rl, driver):
     ran = driver(run, STEPS)
     rl.sync()
     res = {"ran": ran, "completions": run.completions(), "stats": run.stats(), "out": _outputs(run, STEPS),
-           "arena": arena.download(np.uint8, arena.nbytes)}
+           "arena": arena.download(np.uint8, arena.nbytes), "w": w, "seq0": seq0, "q": q, "kn": kn, "vn": vn}
     run.close()
     arena.close()
     return res
@@ -83,7 +90,7 @@ def _enqueue(run, steps):
     return steps
 
 
-def test_ring_loop_equals_enqueue_control_rule(rl, gpu):
+def test_ring_loop_equals_enqueue_control_rule(rl, gpu, orc, olib):
     print("[loop] control rule: 40 launched steps", flush=True)
     want = _control_rule_case(rl, _enqueue)
     print("[loop] control rule: one loop of up to 40 steps", flush=True)
@@ -98,7 +105,49 @@ def test_ring_loop_equals_enqueue_control_rule(rl, gpu):
     assert any((want["out"][n - 1]["rows"] != 0xFFFFFFFF))
     for s in range(n, 40):
         assert (want["out"][s]["rows"] == 0xFFFFFFFF).all(), s
-    assert np.array_equal(got["arena"], want["arena"])
+    # the loop's attention, step by step, against the oracle (appends replayed)
+    w, q, kn, vn = got["w"], got["q"], got["kn"], got["vn"]
+    cur, host = got["seq0"].copy(), w.arena.copy()
+    for s in range(n):
+        o = got["out"][s]
+        rows = [i for i in range(8) if o["rows"][i] != 0xFFFFFFFF]
+        if not rows:
+            continue
+        rs = [int(o["rows"][i]) for i in rows]
+        ctx = cur[rs].astype(np.uint32)
+        wb = synth.DecodeWorkload(len(rows), QH, KVH, D, "bf16", TPB, ctx, np.ascontiguousarray(w.table[rs]), host,
+                                  np.ascontiguousarray(q[s][rows]), 0)
+        ref = orc.attn_f64(olib, wb, 0)
+        errs = [float(gh.rownorm_err(o["out32"][[i]], ref[[j]]).max()) for j, i in enumerate(rows)]
+        wl = want["out"][s]
+        werrs = [float(gh.rownorm_err(wl["out32"][[i]], ref[[j]]).max()) for j, i in enumerate(rows)]
+        if max(errs) >= 1e-4:
+            print(f"[loop] step {s}: rows {rows} rollouts {rs} ctx {ctx.tolist()} loop err "
+                  f"{[f'{e:.2e}' for e in errs]} launched err {[f'{e:.2e}' for e in werrs]}", flush=True)
+            o32 = o["out32"][rows]
+            print(f"[loop]   loop out32 zero rows {[(o32[j] == 0).all() for j in range(len(rows))]} "
+                  f"nan {[bool(np.isnan(o32[j]).any()) for j in range(len(rows))]}", flush=True)
+        k_rows, v_rows = np.ascontiguousarray(kn[s][rows]), np.ascontiguousarray(vn[s][rows])
+        olib.orc_kv_append(host.ctypes.data, w.block_bytes, TPB, D * 2, wb.table.ctypes.data, w.table_stride,
+                           len(rows), KVH, ctx.ctypes.data, None, k_rows.ctypes.data, v_rows.ctypes.data)
+        cur[rs] += 1
+    for s in range(n):
+        o = got["out"][s]
+        rows = [i for i in range(8) if o["rows"][i] != 0xFFFFFFFF]
+        for i in rows:
+            assert np.isfinite(o["out32"][i]).all(), (s, i)
+    for name, arena in (("launched", want["arena"]), ("loop", got["arena"])):
+        bad = np.nonzero(arena != host)[0]
+        if bad.size:
+            blk = bad // w.block_bytes
+            off = bad % w.block_bytes
+            print(f"[loop] {name} arena differs from the oracle replay at {bad.size} bytes; blocks "
+                  f"{np.unique(blk)[:10].tolist()}, offsets {off[:8].tolist()}", flush=True)
+            owners = [(int(r), int(h)) for r in range(w.table.shape[0]) for h in range(KVH)
+                      if np.isin(w.table[r, h], np.unique(blk)).any()]
+            print(f"[loop] owners (rollout, kv head): {owners[:10]}", flush=True)
+    assert np.array_equal(want["arena"], host)
+    assert np.array_equal(got["arena"], host)
 
 
 def _batch64(rl, driver):
@@ -122,13 +171,15 @@ def _batch64(rl, driver):
     ran = driver(run)
     rl.sync()
     res = {"ran": ran, "completions": run.completions(), "stats": run.stats(), "out": run.outputs(0),
-           "arena": arena.download(np.uint8, arena.nbytes)}
+           "arena": arena.download(np.uint8, arena.nbytes),
+           "wb": synth.DecodeWorkload(B, QH, KVH, D, "bf16", TPB, w.ctx[perm].copy(),
+                                      np.ascontiguousarray(w.table[perm]), w.arena, q, 0)}
     run.close()
     arena.close()
     return res
 
 
-def test_ring_loop_batch64(rl, gpu):
+def test_ring_loop_batch64(rl, gpu, orc, olib):
     print("[loop] batch 64: two launched steps", flush=True)
     want = _batch64(rl, lambda run: _enqueue(run, 2))
     print("[loop] batch 64: loop of 1 step, then a loop that finds STOP", flush=True)
@@ -138,6 +189,7 @@ def test_ring_loop_batch64(rl, gpu):
     assert got["stats"] == want["stats"] == [64, 64, 1, 4]
     _same_outputs(got["out"], want["out"], "step 0")
     assert np.array_equal(got["arena"], want["arena"])
+    gh.check_attn(got["out"]["out"], got["out"]["out32"], orc.attn_f64(olib, got["wb"], 0), "bf16")
 
 
 def test_ring_loop_exit_paths(rl, gpu):
@@ -153,7 +205,7 @@ def test_ring_loop_exit_paths(rl, gpu):
 
     def run_of(arena):
         r = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
-                                 greedy=True, max_idle_polls=2000)
+                                 output_slots=2, greedy=True, max_idle_polls=2000)
         r.set_inputs(0, q, kn, vn, logits)
         return r
 
@@ -213,6 +265,11 @@ def test_ring_loop_rejects(rl, gpu):
     w = synth.make_decode(7192, B, QH, KVH, D, 40, 100)
     run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()), B, V,
                                greedy=True)
+    with pytest.raises(rl.RlrtError, match="output_slots"):
+        run.loop(1)
+    run.close()
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()), B, V,
+                               output_slots=2, greedy=True)
     with pytest.raises(rl.RlrtError, match="max_steps"):
         run.loop(0)
     run.close()
