@@ -870,9 +870,9 @@ def wl_ringstep(args):
     if stats[:3] != [B * (K + W), B * (K + W), K + W] or n_comp != B * (K + W):
         raise rlrt.RlrtError(f"ring step stats {stats}, {n_comp} completions")
     # the same pipeline as one persistent launch per call (rl_hip_ring_loop_launch;
-    # consecutive steps write their own output slots)
+    # three consecutive steps write their own output slots)
     run = ringstep.RingStepRun(st.arena, st.layout, w.table, QH, MAX_CTX, B, VOCAB, input_slots=LOGIT_COPIES,
-                               output_slots=2, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
+                               output_slots=3, temperature=TEMP, top_k=TOPK, top_p=TOPP, seeds=seeds, f32_out=False)
     for sl in range(LOGIT_COPIES):
         run.set_inputs(sl, w.q, kn, vn, logits)
     for _ in range(K + W):

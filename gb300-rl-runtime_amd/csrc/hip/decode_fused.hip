@@ -396,43 +396,59 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 //  turn   wave 0 of workgroup 0, beside the steps: turn t (ring_core.h)
 //         publishes step t - 1 (the hw_worker_sim rule does not depend on
 //         the token, so it runs while step t - 1 is still streaming) and
-//         admits descriptors for step t into argument set t % 2, once step
-//         t - 2's merges have released that set and step workspace t % 2.
-//         It releases step t (the go word) as soon as every step workgroup
-//         has finished step t - 1, then makes step t - 1's completions
-//         visible once its merges are done.
+//         admits descriptors for step t into argument set t % 3, once step
+//         t - 3's merges have released that set and step workspace t % 3.
+//         It releases step t (the go word) as soon as step t - 1's K/V
+//         appends are done. Step t - 1's completions become visible once
+//         its merges are done: the turn keeps them pending and stores the
+//         completion ring's tail when it finds those merges finished (before
+//         a later turn, or waiting for them at the end).
 //  steps  workgroups kLoopService.. (the same number on each XCD; the other
 //         workgroups of the first kLoopService, one per XCD, keep the turn
 //         off the steps' compute units): step t over argument set and step
-//         workspace t % 2 and step t's slots. The sampling workgroups first
-//         merge step t - 1's split rows (one row per wave; every workgroup
-//         has finished step t - 1 when step t is released) and sample the
-//         step's logits; the other workgroups' waves first append the
-//         step's K/V tokens (one (row, kv head) per wave; the attention
-//         masks positions past the context, the appended one among them);
-//         then every workgroup streams its attention pieces, split rows
-//         left as partials for the next step's merges. When the loop ends,
-//         the sampling workgroups merge the last step's rows.
+//         workspace t % 3 and step t's slots. A workgroup starts step t as
+//         soon as it is released, while others may still finish step t - 1
+//         (or t - 2). The sampling workgroups merge step t - 1's split rows
+//         (one row per wave) once every workgroup has finished that step -
+//         before sampling the step's logits if it already has, else after;
+//         then every workgroup streams its attention pieces, split rows left
+//         as partials for the next step's merges. When the loop ends, the
+//         sampling workgroups merge the last step's rows.
+//  appends the other waves of the first kLoopService workgroups: once step
+//         t is released, its K/V tokens, four (row, kv head) pairs at a time
+//         per wave (the attention masks positions past the context, the
+//         appended one among them).
 // Hand-offs are monotonic counters in the workspace: a release fence and an
 // atomic add by the producer, a bounded wait and an acquire fence by the
-// consumer; the counts of finished steps and of merges are kept per step
-// parity. A wait that runs out sets an error word that ends every role's
-// loop at its next wait. Cooperative launch keeps every workgroup resident,
-// so no wait is for a workgroup that cannot run. Step t's merges write
-// output slot t % output_slots while step t + 1 runs, so output_slots is at
-// least 2.
+// consumer. Workgroups may run step t + 2 while others finish step t (never
+// t + 3: that needs step t's merges), so the counts of finished steps and of
+// merges are kept per step modulo 3. A wait that runs out sets an error word
+// that ends every role's loop at its next wait. Cooperative launch keeps
+// every workgroup resident, so no wait is for a workgroup that cannot run.
+// Step t's merges write output slot t % output_slots while steps t + 1 and
+// t + 2 run, so output_slots is at least 3.
 constexpr uint32_t kLoopService = kXcds;  // workgroups kept off the steps: the turn's, one per XCD
+constexpr uint32_t kLoopAppenders = kLoopService * kFWaves - 1;  // their waves less the turn's
+// A merge wave's cost in the loop's split, in the pipelined step's merge
+// rounds. The sampling workgroups set the loop's pace (every step they also
+// wait for the previous one to finish everywhere before merging it): at 4
+// they spent about 73 us sampling and merging and 78 us on attention a step
+// against 125 us for an attention workgroup; 9 gives them about a third less
+// attention.
+constexpr uint32_t kLoopMergeWeight = 9;
 
 struct LoopParams {
     RingParams rp;            // the turn's arguments over argument set 0
     FusedParams f;            // the step over input / output slot 0, argument set 0, step workspace 0
     AppendParams ap;          // the append over input slot 0, argument set 0
-    // argument set 1 and step workspace 1
-    uint32_t *ctx1, *pos1, *rmap1;
-    uint64_t *rseed1, *rstep1;
-    uint32_t *cum1;
-    float *part1;
-    SplitIn *si_out1;
+    // argument sets and step workspaces 1 and 2 (set 0 is in rp, f and ap)
+    struct Set {
+        uint32_t *ctx, *pos, *rmap;
+        uint64_t *rseed, *rstep;
+        uint32_t *cum;
+        float *part;
+        SplitIn *si_out;
+    } set[2];
     size_t q_slot, out_slot;  // bytes per input slot of q, per output slot of the 16-bit outputs
     size_t out32_slot;        // floats per output slot of the fp32 outputs
     size_t logits_slot;       // floats per input slot of the logits
@@ -450,14 +466,16 @@ struct LoopParams {
 
 enum : uint32_t { kLoopSyncTimeout = 5 };  // stats[3] when a wait of the loop ran out
 // The words at LoopParams::sync: the turn's go word; step workgroups done
-// with even / odd steps; sampling workgroups done with the merges of even /
-// odd steps; the error word.
-enum : uint32_t { kSyncGo = 0, kSyncSteps = 1, kSyncMerges = 3, kSyncError = 5 };
+// with steps 0, 1, 2 modulo 3; sampling workgroups done with the merges of
+// steps 0, 1, 2 modulo 3; append waves done with the appends of all steps;
+// the error word.
+enum : uint32_t { kSyncGo = 0, kSyncSteps = 1, kSyncMerges = 4, kSyncAppends = 7, kSyncError = 8 };
+constexpr uint32_t kLoopSyncWords = 16;
 
-// Counter of step u's parity in the pair at c, and its value once all n
+// Counter of step u modulo 3 among the three at c, and its value once all n
 // producers are done with step u.
-__device__ __forceinline__ uint32_t par_ctr(uint32_t c, uint32_t u) { return c + (u & 1); }
-__device__ __forceinline__ uint32_t par_target(uint32_t u, uint32_t n) { return (u / 2 + 1) * n; }
+__device__ __forceinline__ uint32_t par_ctr(uint32_t c, uint32_t u) { return c + u % 3u; }
+__device__ __forceinline__ uint32_t par_target(uint32_t u, uint32_t n) { return (u / 3u + 1) * n; }
 
 // The loop's arguments, read from the kernel-argument segment through a
 // pointer the optimizer cannot see through: each phase reloads (scalar loads
@@ -489,17 +507,30 @@ __device__ __forceinline__ uint32_t sync_load(const uint32_t *w)
     return __hip_atomic_load(const_cast<uint32_t *>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The pause between two polls of a sync word: short at first, then longer
+// (hundreds of waves may wait on one word while the steps stream, and each
+// poll is a load from the device-coherent copy of that line).
+__device__ __forceinline__ void loop_backoff(uint32_t polls)
+{
+    if (polls < 16)
+        __builtin_amdgcn_s_sleep(2);
+    else if (polls < 64)
+        __builtin_amdgcn_s_sleep(16);
+    else
+        __builtin_amdgcn_s_sleep(64);
+}
+
 // Bounded wait (acquire) until counter sync[c] reaches target. False when
 // the wait ran out or another wait did (the error word, then set).
 __device__ __forceinline__ bool loop_wait(uint32_t *sync, uint32_t c, uint32_t target, uint64_t limit_ticks)
 {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    while (sync_load(&sync[c]) < target) {
+    for (uint32_t polls = 0; sync_load(&sync[c]) < target; polls++) {
         if (sync_load(&sync[kSyncError]) != 0 || __builtin_amdgcn_s_memrealtime() - t0 > limit_ticks) {
             __hip_atomic_store(&sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
-        __builtin_amdgcn_s_sleep(2);
+        loop_backoff(polls);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // the producers' writes are visible here
     return true;
@@ -511,7 +542,7 @@ __device__ __forceinline__ bool loop_wait(uint32_t *sync, uint32_t c, uint32_t t
 __device__ __forceinline__ bool loop_go(uint32_t *sync, uint32_t t, uint64_t limit_ticks)
 {
     const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-    for (;;) {
+    for (uint32_t polls = 0;; polls++) {
         const uint32_t v = sync_load(&sync[kSyncGo]);
         if ((v & 0x7FFFFFFFu) > t)
             break;
@@ -521,7 +552,7 @@ __device__ __forceinline__ bool loop_go(uint32_t *sync, uint32_t t, uint64_t lim
             __hip_atomic_store(&sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
         }
-        __builtin_amdgcn_s_sleep(2);
+        loop_backoff(polls);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     return true;
@@ -566,21 +597,22 @@ struct MergedBy {
     __device__ bool ready() const { return loop_wait(sync, par_ctr(kSyncMerges, u), par_target(u, n), limit); }
 };
 
-// Step t's kernel arguments: argument set and workspace t % 2, slots.
+// Step t's kernel arguments: argument set and workspace t % 3, slots.
 __device__ __forceinline__ FusedParams loop_step_params(const RL_CONST LoopParams &L, uint32_t t)
 {
     const uint64_t k = L.first_step + t;
     const size_t si = k % L.input_slots, so = k % L.output_slots;
     FusedParams f = kcopy(L.f);
-    if (t & 1) {
-        f.p.ctx = L.ctx1;
-        f.p.row_map = L.rmap1;
-        f.p.cum = L.cum1;
-        f.p.part = L.part1;
-        f.si_out = L.si_out1;
-        f.sp.seed = L.rseed1;
-        f.sp.steps = L.rstep1;
-        f.sp.draw_ids = L.rmap1;
+    if (const uint32_t x = t % 3u) {
+        const LoopParams::Set z = kcopy(L.set[x - 1]);
+        f.p.ctx = z.ctx;
+        f.p.row_map = z.rmap;
+        f.p.cum = z.cum;
+        f.p.part = z.part;
+        f.si_out = z.si_out;
+        f.sp.seed = z.rseed;
+        f.sp.steps = z.rstep;
+        f.sp.draw_ids = z.rmap;
     }
     f.p.q = (const uint16_t *)((const uint8_t *)f.p.q + si * L.q_slot);
     f.p.out = (uint16_t *)((uint8_t *)f.p.out + so * L.out_slot);
@@ -613,33 +645,28 @@ __device__ __forceinline__ bool loop_merge_step(uint32_t u, uint32_t wg, uint32_
     return true;
 }
 
-// The attention role of step t by step workgroup wg, compiled as a function
-// of its own (the sampling code beside it in one body made the compiler give
-// up the tight per-tile loop). Arguments arrive in vector registers; they are
-// wave-uniform, so they are read back from the first lane. args: the
-// kernel-argument segment's address, which a called function cannot obtain
-// itself.
+// The sampling role of step t by sampling workgroup wg, compiled as a
+// function of its own: with the sampling code in the same body as the
+// attention, the compiler gives up the attention's tight per-tile loop.
+// Arguments arrive in vector registers; they are wave-uniform, so they are
+// read back from the first lane. args: the kernel-argument segment's address,
+// which a called function cannot obtain itself.
 template <int D, int G, int DT, int TPB>
-__device__ __attribute__((noinline)) void loop_attn_fn(uint32_t args_lo, uint32_t args_hi, uint32_t t_in,
-                                                       uint32_t wg_in, uint32_t lds_in, uint32_t lctx_in,
-                                                       uint32_t lrow_in)
+__device__ __attribute__((noinline)) void loop_sample_fn(uint32_t args_lo, uint32_t args_hi, uint32_t t_in,
+                                                         uint32_t wg_in, uint32_t lds_in)
 {
     const auto first = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); };
     const uint64_t args = (uint64_t)first(args_lo) | ((uint64_t)first(args_hi) << 32);
     const uint32_t t = first(t_in);
     const uint32_t wg = first(wg_in);
     RL_LDS uint8_t *lds = (RL_LDS uint8_t *)(uintptr_t)first(lds_in);
-    RL_LDS uint32_t *lctx = (RL_LDS uint32_t *)(uintptr_t)first(lctx_in);
-    RL_LDS uint32_t *lrow = (RL_LDS uint32_t *)(uintptr_t)first(lrow_in);
-    fused_attn_part<D, G, DT, TPB, true>(loop_step_params(loop_args_at(args), t), (uint8_t *)lds, wg, lctx, lrow);
+    fused_sample_part<D, G, DT, TPB>(loop_step_params(loop_args_at(args), t), (uint8_t *)lds, wg);
 }
 
 template <int D, int G, int DT, int TPB>
 __device__ __forceinline__ void loop_steps(uint32_t wg, uint32_t n_wgs, uint8_t *lds, RL_LDS uint32_t *lctx,
                                            RL_LDS uint32_t *lrow, uint32_t *s_go, uint32_t *s_flag)
 {
-    const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
     const uint32_t n_samp = loop_args().f.si.sample_wgs;
     const bool sampler = wg < n_samp;
     for (uint32_t t = 0;; t++) {
@@ -657,81 +684,156 @@ __device__ __forceinline__ void loop_steps(uint32_t wg, uint32_t n_wgs, uint8_t 
             break;
         }
         if (sampler) {
-            // ---- step t - 1's split rows, then the sampling of step t's logits ----------
-            if (t > 0)
-                (void)loop_merge_step<D, G, DT>(t - 1, wg, n_wgs, false, s_flag);
-            fused_sample_part<D, G, DT, TPB>(loop_step_params(loop_args(), t), lds, wg);
-        } else {
-            // ---- step t's K/V token appends, one (row, kv head) per wave -----------------
-            const RL_CONST LoopParams &L = loop_args();
-            const uint64_t k = L.first_step + t;
-            AppendParams ap = kcopy(L.ap);
-            if (t & 1) {
-                ap.positions = L.pos1;
-                ap.row_map = L.rmap1;
+            // ---- step t - 1's split rows (first when that step is already done
+            // everywhere, else after the sampling), the sampling of step t's logits
+            bool merged = t == 0;
+            if (!merged) {
+                if (threadIdx.x == 0) {
+                    const RL_CONST LoopParams &L = loop_args();
+                    *s_flag = sync_load(&L.sync[par_ctr(kSyncSteps, t - 1)]) >= par_target(t - 1, n_wgs) ? 1u : 0u;
+                }
+                __syncthreads();
+                if (*s_flag) {
+                    if (!loop_merge_step<D, G, DT>(t - 1, wg, n_wgs, true, s_flag))
+                        break;
+                    merged = true;
+                }
             }
-            ap.k_new = ap.k_new + (k % L.input_slots) * L.kv_slot;
-            ap.v_new = ap.v_new + (k % L.input_slots) * L.kv_slot;
-            const uint32_t pairs = L.f.p.batch * ap.kv_heads;
-            for (uint32_t pr = (wg - n_samp) * kFWaves + wave; pr < pairs; pr += (n_wgs - n_samp) * kFWaves)
-                append_row(ap, pr / ap.kv_heads, pr % ap.kv_heads, (uint32_t)lane, 64);
+            {
+                const uint64_t args = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
+                loop_sample_fn<D, G, DT, TPB>((uint32_t)args, (uint32_t)(args >> 32), t, wg,
+                                              (uint32_t)(uintptr_t)(RL_LDS uint8_t *)lds);
+            }
+            if (!merged && !loop_merge_step<D, G, DT>(t - 1, wg, n_wgs, true, s_flag))
+                break;
         }
-        const uint64_t args = (uint64_t)__builtin_amdgcn_kernarg_segment_ptr();
-        loop_attn_fn<D, G, DT, TPB>((uint32_t)args, (uint32_t)(args >> 32), t, wg,
-                                    (uint32_t)(uintptr_t)(RL_LDS uint8_t *)lds, (uint32_t)(uintptr_t)lctx,
-                                    (uint32_t)(uintptr_t)lrow);
+        fused_attn_part<D, G, DT, TPB, true>(loop_step_params(loop_args(), t), lds, wg, lctx, lrow);
         loop_signal_wg(loop_args().sync, par_ctr(kSyncSteps, t));
     }
+}
+
+// Append wave m (of kLoopAppenders): step t's K/V tokens, pairs m * 4 +
+// lane / 16 + 4 * kLoopAppenders * i, sixteen lanes a pair; then counted.
+__device__ __forceinline__ void loop_appends(uint32_t m, int lane)
+{
+    for (uint32_t t = 0;; t++) {
+        {
+            const RL_CONST LoopParams &L = loop_args();
+            if (!loop_go(L.sync, t, L.go_ticks))
+                break;
+        }
+        const RL_CONST LoopParams &L = loop_args();
+        const uint64_t k = L.first_step + t;
+        AppendParams ap = kcopy(L.ap);
+        if (const uint32_t x = t % 3u) {
+            ap.positions = L.set[x - 1].pos;
+            ap.row_map = L.set[x - 1].rmap;
+        }
+        ap.k_new = ap.k_new + (k % L.input_slots) * L.kv_slot;
+        ap.v_new = ap.v_new + (k % L.input_slots) * L.kv_slot;
+        const uint32_t pairs = L.f.p.batch * ap.kv_heads;
+        for (uint32_t pr = m * 4u + (uint32_t)lane / 16u; pr < pairs; pr += 4u * kLoopAppenders)
+            append_row(ap, pr / ap.kv_heads, pr % ap.kv_heads, (uint32_t)lane % 16u, 16);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        rl_wait_vmcnt<0>();
+        if (lane == 0)
+            atomicAdd(&L.sync[kSyncAppends], 1u);
+    }
+}
+
+// Completions written by turns but not yet visible, oldest first: the step
+// they complete and the completion ring tail that publishes them.
+struct PendingTails {
+    uint32_t n;
+    uint32_t step[3], tail[3];
+};
+
+// Stores the tail of every pending entry whose step's merges are done
+// (waiting for them when block), in order; false when a wait ran out.
+__device__ __forceinline__ bool loop_release(const RL_CONST LoopParams &L, PendingTails &q, bool block, int lane)
+{
+    uint32_t *sync = L.sync;
+    const uint32_t n_samp = L.f.si.sample_wgs;
+    uint32_t done = 0, tail = 0;
+    for (; done < q.n; done++) {
+        const uint32_t u = q.step[done];
+        if (block) {
+            if (!loop_wait(sync, par_ctr(kSyncMerges, u), par_target(u, n_samp), L.bar_ticks))
+                return false;
+        } else if (sync_load(&sync[par_ctr(kSyncMerges, u)]) < par_target(u, n_samp)) {
+            break;
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+        tail = q.tail[done];
+    }
+    if (done) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+        if (lane == 0)
+            sys_store(&L.rp.dq->tail, tail);
+        for (uint32_t i = done; i < q.n; i++) {
+            q.step[i - done] = q.step[i];
+            q.tail[i - done] = q.tail[i];
+        }
+        q.n -= done;
+    }
+    return true;
 }
 
 __device__ __forceinline__ void loop_turns(uint16_t *s_free, int lane)
 {
     uint32_t t = 0;
     bool ok = true;
+    PendingTails q;
+    q.n = 0;
     for (;; t++) {
         const RL_CONST LoopParams &L = loop_args();
         uint32_t *sync = L.sync;
         const uint32_t n_samp = L.f.si.sample_wgs;
         const bool last = t >= L.max_steps;  // this turn only publishes
-        // argument set and workspace t % 2 are free once step t - 2's merges are done
-        if (t >= 2 &&
-            !(ok = loop_wait(sync, par_ctr(kSyncMerges, t - 2), par_target(t - 2, n_samp), L.bar_ticks)))
+        // argument set and workspace t % 3 are free once step t - 3's merges are done
+        if (t >= 3 &&
+            !(ok = loop_wait(sync, par_ctr(kSyncMerges, t - 3), par_target(t - 3, n_samp), L.bar_ticks)))
+            break;
+        // completions whose steps are merged become visible; room for this turn's entry
+        if (!(ok = loop_release(L, q, q.n == 3, lane)))
             break;
         RingParams rp = kcopy(L.rp);
-        if (t & 1) {
-            rp.ctx = L.ctx1;
-            rp.pos = L.pos1;
-            rp.rmap = L.rmap1;
-            rp.rseed = L.rseed1;
-            rp.rstep = L.rstep1;
+        if (const uint32_t x = t % 3u) {
+            const LoopParams::Set z = kcopy(L.set[x - 1]);
+            rp.ctx = z.ctx;
+            rp.pos = z.pos;
+            rp.rmap = z.rmap;
+            rp.rseed = z.rseed;
+            rp.rstep = z.rstep;
         }
         const size_t so = (L.first_step + t) % L.output_slots;
         rp.row_rollout = L.row_rollout && !last ? L.row_rollout + so * rp.batch : nullptr;
         TurnOut to;
         const MergedBy rel{sync, t - 1, n_samp, L.bar_ticks};  // used only by turns that publish (t >= 1)
         const uint32_t held = ring_turn(rp, t > 0 ? 1u : 0u, last ? 0u : 1u, s_free, &to, rel);
+        if (to.released)
+            q.n = 0;  // the turn published every completion so far
+        if (to.pending) {
+            q.step[q.n] = t - 1;
+            q.tail[q.n] = to.dtail;
+            q.n++;
+        }
         // admission over and every row free: later steps would decode nothing
         const bool end = last || (to.status != kRunning && held == 0);
-        // step t starts once every workgroup has finished step t - 1 (its K/V
-        // appends among it)
-        if (!end && t >= 1 &&
-            !(ok = loop_wait(sync, par_ctr(kSyncSteps, t - 1), par_target(t - 1, L.f.si.wgs), L.bar_ticks)))
+        // step t reads the K/V tokens step t - 1 appended
+        if (!end && t >= 1 && !(ok = loop_wait(sync, kSyncAppends, t * kLoopAppenders, L.bar_ticks)))
             break;
         if (lane == 0) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the rows' step arguments before the word
             __hip_atomic_store(&sync[kSyncGo], end ? (t | 0x80000000u) : t + 1, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (to.pending) {
-            // step t - 1's completions: visible once its results are all written
-            if (!(ok = loop_wait(sync, par_ctr(kSyncMerges, t - 1), par_target(t - 1, n_samp), L.bar_ticks)))
-                break;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
-            if (lane == 0)
-                sys_store(&rp.dq->tail, to.dtail);
-        }
-        if (end)
+        if (end) {
+            // the last completions: visible once the sampling workgroups' final merges are done
+            ok = loop_release(L, q, true, lane);
             break;
+        }
     }
     if (lane == 0) {
         const RL_CONST LoopParams &L = loop_args();
@@ -759,6 +861,8 @@ __global__ __launch_bounds__(kFThreads) void ring_loop_kernel(LoopParams)
                                   (RL_LDS uint32_t *)s_ctx, (RL_LDS uint32_t *)s_row, &s_go, &s_flag);
     else if (blockIdx.x == 0 && threadIdx.x < 64)
         loop_turns(reinterpret_cast<uint16_t *>(lds), (int)threadIdx.x);
+    else
+        loop_appends(blockIdx.x * kFWaves + (threadIdx.x >> 6) - 1, (int)(threadIdx.x & 63));
 }
 
 struct FusedWs {
@@ -1265,8 +1369,8 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
         rl_set_error("%s: the shape does not fit the fused kernel (use rl_hip_ring_step_enqueue)", who);
         return -1;
     }
-    if (a->output_slots < 2) {
-        rl_set_error("%s: output_slots %u < 2 (a step's results are merged while the next step runs)", who,
+    if (a->output_slots < 3) {
+        rl_set_error("%s: output_slots %u < 3 (a step's results are merged while the next two steps run)", who,
                      a->output_slots);
         return -1;
     }
@@ -1282,12 +1386,15 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
         return -1;
     }
     {
-        // the sampling workgroups merge the previous step's rows, one per wave
+        // The sampling workgroups merge the previous step's rows, one per
+        // wave. In the loop a merge runs while every other workgroup streams
+        // (the pipelined step's estimate assumes a quieter device): it is
+        // weighted at kLoopMergeWeight of those rounds in the split.
         uint32_t wgs, sample_wgs;
         grid_of(s.rows, wgs, sample_wgs, grid - kLoopService);
         const uint32_t rows = a->batch * a->kv_heads;
-        L.f = fused_params_of(&t, &s, ws + w.step, (rows + sample_wgs * kFWaves - 1) / (sample_wgs * kFWaves),
-                              grid - kLoopService);
+        const uint32_t rounds = (rows + sample_wgs * kFWaves - 1) / (sample_wgs * kFWaves);
+        L.f = fused_params_of(&t, &s, ws + w.step, rounds * kLoopMergeWeight, grid - kLoopService);
     }
     L.f.p.row_map = L.rp.rmap;
     const FusedWs fw = fused_ws(&t, L.f.si);
@@ -1316,14 +1423,17 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
     apa.v_new = a->v_new;
     L.ap = append_params(&apa);
     L.ap.row_map = L.rp.rmap;
-    L.ctx1 = (uint32_t *)(ws + w.ctx2);
-    L.pos1 = (uint32_t *)(ws + w.pos2);
-    L.rmap1 = (uint32_t *)(ws + w.rmap2);
-    L.rseed1 = (uint64_t *)(ws + w.rseed2);
-    L.rstep1 = (uint64_t *)(ws + w.rstep2);
-    L.cum1 = (uint32_t *)(ws + w.step2 + fw.cum_off);
-    L.part1 = (float *)(ws + w.step2 + fw.part_off);
-    L.si_out1 = (SplitIn *)(ws + w.step2 + fw.si_off);
+    for (int i = 0; i < 2; i++) {
+        const RingWs::Set &x = w.set[i];
+        L.set[i].ctx = (uint32_t *)(ws + x.ctx);
+        L.set[i].pos = (uint32_t *)(ws + x.pos);
+        L.set[i].rmap = (uint32_t *)(ws + x.rmap);
+        L.set[i].rseed = (uint64_t *)(ws + x.rseed);
+        L.set[i].rstep = (uint64_t *)(ws + x.rstep);
+        L.set[i].cum = (uint32_t *)(ws + x.step + fw.cum_off);
+        L.set[i].part = (float *)(ws + x.step + fw.part_off);
+        L.set[i].si_out = (SplitIn *)(ws + x.step + fw.si_off);
+    }
     L.q_slot = B * qrow;
     L.out_slot = B * qrow;
     L.out32_slot = B * qrow / 2;
@@ -1344,7 +1454,9 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
     // below 2 s.
     L.bar_ticks = 200000000ull;
     L.go_ticks = 2000ull * L.rp.max_idle + 2 * L.bar_ticks;
-    if (rl_check_hip(hipMemsetAsync(L.sync, 0, 8 * sizeof(uint32_t), rl_stream()), "hipMemsetAsync(loop sync)"))
+    static_assert(kLoopSyncOff + kLoopSyncWords * 4 <= 256, "the sync words sit between the control record and the rows");
+    if (rl_check_hip(hipMemsetAsync(L.sync, 0, kLoopSyncWords * sizeof(uint32_t), rl_stream()),
+                     "hipMemsetAsync(loop sync)"))
         return -1;
     const uint32_t G = a->q_heads / a->kv_heads;
     if (a->layout.head_dim == 128)

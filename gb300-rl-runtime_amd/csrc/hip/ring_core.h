@@ -90,9 +90,10 @@ struct ReleaseNow {
 };
 
 struct TurnOut {
-    uint32_t status;   // admission status after the turn
-    uint32_t pending;  // completions written but not released (deferring callers)
-    uint32_t dtail;    // the completion ring tail that releases them
+    uint32_t status;    // admission status after the turn
+    uint32_t pending;   // completions written but not released (deferring callers)
+    uint32_t dtail;     // the completion ring tail that releases them
+    uint32_t released;  // the turn stored the completion ring tail (every completion so far is visible)
 };
 
 // One wave, between two decode steps: the publish of the step just decoded
@@ -179,6 +180,7 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
 
     // ---- publish: the rule, the completions, the free-row list ---------------
     uint32_t nfree = 0, n_done = 0, n_dec = 0;
+    bool released = false;
     for (uint32_t i0 = 0; i0 < p.batch; i0 += 64) {
         const uint32_t i = i0 + lane;
         const bool valid = i < p.batch;
@@ -249,6 +251,7 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
                     if (lane == 0)
                         sys_store(&p.dq->tail, dtail);
                     dq_pending = false;
+                    released = true;
                 }
                 const uint32_t stop = fresh ? stop0 : rl_wave_bcast_u32(lane == 0 ? sys_load(p.stop) : 0u, 0);
                 fresh = false;
@@ -309,6 +312,7 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
 
     // ---- releases: the completions, then the consumed descriptors ------------
     const bool release_dq = dq_pending && !Rel::kDefer;
+    released |= release_dq;
     if (release_dq || head != head0) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
         if (lane == 0) {
@@ -341,6 +345,7 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
         out->status = status;
         out->pending = dq_pending && Rel::kDefer ? 1u : 0u;
         out->dtail = dtail;
+        out->released = released ? 1u : 0u;
     }
     return active;
 }
@@ -349,12 +354,16 @@ __device__ uint32_t ring_turn(const RingParams &p, uint32_t do_publish, uint32_t
 
 // The ring step's workspace: the control record at ctl (the self-scheduled
 // loop's sync words at ctl + kLoopSyncOff), the row table and the rows' step
-// arguments, the fused step's workspace at step; then a second set of step
-// arguments and a second step workspace, which the self-scheduled loop
-// alternates with the first (the launched pipeline uses the first only).
+// arguments, the fused step's workspace at step; then two more sets of step
+// arguments and step workspaces (set[i]: rmap, ctx, pos, rseed, rstep and
+// step), which the self-scheduled loop rotates with the first (the launched
+// pipeline uses the first only).
 struct RingWs {
     size_t ctl, rows, kind, rmap, ctx, pos, rseed, rstep, step;
-    size_t rmap2, ctx2, pos2, rseed2, rstep2, step2, total;
+    struct Set {
+        size_t rmap, ctx, pos, rseed, rstep, step;
+    } set[2];
+    size_t total;
     size_t step_bytes;
 };
 constexpr size_t kLoopSyncOff = 128;  // past the 40-byte RingCtl, before the rows at 256
@@ -444,13 +453,17 @@ inline int ring_layout(const rl_ring_step_args_t *a, RingWs &w)
     w.step_bytes = rl_hip_decode_sample_step_workspace(&t, &s);
     if (w.step_bytes == 0)
         return -1;
-    w.rmap2 = w.step + up256(w.step_bytes);
-    w.ctx2 = w.rmap2 + up256(B * 4);
-    w.pos2 = w.ctx2 + up256(B * 4);
-    w.rseed2 = w.pos2 + up256(B * 4);
-    w.rstep2 = w.rseed2 + up256(B * 8);
-    w.step2 = w.rstep2 + up256(B * 8);
-    w.total = w.step2 + up256(w.step_bytes);
+    size_t o = w.step + up256(w.step_bytes);
+    for (RingWs::Set &x : w.set) {
+        x.rmap = o;
+        x.ctx = x.rmap + up256(B * 4);
+        x.pos = x.ctx + up256(B * 4);
+        x.rseed = x.pos + up256(B * 4);
+        x.rstep = x.rseed + up256(B * 8);
+        x.step = x.rstep + up256(B * 8);
+        o = x.step + up256(w.step_bytes);
+    }
+    w.total = o;
     return 0;
 }
 

@@ -20,10 +20,10 @@ ring-step tests check the launched step's.
 3. Exit paths: idle limit, bad rollout id, the host's stop flag (zero steps
    run, status 1 / 2 / 4) and a full completion ring (status 3; the finished
    descriptor stays in its row until a later loop pushes it).
-4. Arguments the loop does not take: max_steps 0, one output slot (a step's
-   split rows are merged while the next step runs, so consecutive steps need
-   their own slots) and a GQA group of 8 at d128 (outside the fused kernel)
-   return errors before any launch."""
+4. Arguments the loop does not take: max_steps 0, fewer than three output
+   slots (a step's split rows are merged while the next two steps run, so
+   three consecutive steps need their own slots) and a GQA group of 8 at d128
+   (outside the fused kernel) return errors before any launch."""
 import ctypes as C
 
 import numpy as np
@@ -158,7 +158,7 @@ def _batch64(rl, driver):
     w = synth.make_decode(5151, B, QH, KVH, D, 512, 4096, max_ctx=4096)
     arena = rl.DeviceBuffer.from_array(w.arena)
     seeds = rng.integers(0, 2**63, B, dtype=np.uint64)
-    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, 4096, B, V, output_slots=2,
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, 4096, B, V, output_slots=3,
                                temperature=0.8, top_k=50, top_p=0.9, seeds=seeds)
     perm = rng.permutation(B)
     q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
@@ -205,7 +205,7 @@ def test_ring_loop_exit_paths(rl, gpu):
 
     def run_of(arena):
         r = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
-                                 output_slots=2, greedy=True, max_idle_polls=2000)
+                                 output_slots=3, greedy=True, max_idle_polls=2000)
         r.set_inputs(0, q, kn, vn, logits)
         return r
 
@@ -270,6 +270,11 @@ def test_ring_loop_rejects(rl, gpu):
     run.close()
     run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()), B, V,
                                output_slots=2, greedy=True)
+    with pytest.raises(rl.RlrtError, match="output_slots"):
+        run.loop(1)
+    run.close()
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()), B, V,
+                               output_slots=3, greedy=True)
     with pytest.raises(rl.RlrtError, match="max_steps"):
         run.loop(0)
     run.close()
