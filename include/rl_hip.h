@@ -359,23 +359,30 @@ typedef struct {
 size_t rl_hip_ring_step_workspace(const rl_ring_step_args_t *args);
 int rl_hip_ring_step_enqueue(const rl_ring_step_args_t *args, uint32_t steps, uint64_t first_step);
 
-/* The same pipeline as one self-scheduled launch: a persistent grid of one
- * workgroup per compute unit (a cooperative launch) runs the turns and the
- * fused steps back to back, handing each step to the next through grid
- * barriers instead of kernel boundaries, like the reference's persistent
- * device worker (cu/worker.cu:66-131) but with every compute unit on each
- * step. It runs up to max_steps steps and ends earlier once admission has
- * ended and every row is free (later steps would decode nothing); the last
- * turn publishes the last step. Turns, steps, slots, stats, the row table
- * and the results are those of rl_hip_ring_step_enqueue(args, s, first_step)
- * for the s steps the loop ran, which it writes to *steps_run (device, may
- * be NULL) at its end: a following enqueue or loop continues at first_step
- * + s on the same workspace. Shapes must fit the fused kernel (as
- * rl_hip_decode_sample_step's fused path: batch <= 1024 and the GQA group,
- * head_dim and block size it takes); others return -1. The wait for a turn
- * and each barrier are bounded; a wait that runs out ends the loop with
- * stats status 5 (the run's ring state is then undefined). Queued on the
- * library stream; returns at once. */
+/* The same pipeline as one self-scheduled launch, like the reference's
+ * persistent device worker (cu/worker.cu:66-131) but with every compute unit
+ * on each step: a persistent grid of one workgroup per compute unit (a
+ * cooperative launch) in which one wave runs the turns beside the steps, a
+ * few service waves append the K/V tokens, and the other workgroups stream
+ * the fused steps back to back, a step released as soon as the previous
+ * step's tokens are appended (so consecutive steps overlap) and merged by
+ * the next step's sampling waves. It runs up to max_steps steps and ends
+ * earlier once admission has ended and every row is free (later steps would
+ * decode nothing); the last turn publishes the last step. Turns, stats, the
+ * row table, completions, rows, tokens, logprobs and the arena are those of
+ * rl_hip_ring_step_enqueue(args, s, first_step) for the s steps the loop
+ * ran, which it writes to *steps_run (device, may be NULL) at its end; the
+ * attention outputs agree to fp32 rounding (the steps' split differs). A
+ * step's completions become visible once its results are written, possibly a
+ * few steps later than the launched pipeline would show them; all of them
+ * before the launch ends. A following enqueue or loop continues at
+ * first_step + s on the same workspace. Requires output_slots >= 3 (a step's
+ * split rows are merged while the next two run) and a shape that fits the
+ * fused kernel (as rl_hip_decode_sample_step's fused path: batch <= 1024 and
+ * the GQA group, head_dim and block size it takes); others return -1. Every
+ * wait is bounded; one that runs out ends the loop with stats status 5 (the
+ * run's ring state is then undefined). Queued on the library stream; returns
+ * at once. */
 int rl_hip_ring_loop_launch(const rl_ring_step_args_t *args, uint32_t max_steps, uint64_t first_step,
                             uint32_t *steps_run);
 
