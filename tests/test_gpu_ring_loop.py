@@ -13,7 +13,9 @@ ring-step tests check the launched step's.
    NEEDS_REWARD at 32, a passthrough, a dropped opcode, STOP): the loop
    ends by itself once admission has ended and every row is free, and the
    launched run's later steps decoded nothing; every decoded row of every
-   step against the oracle with the rollout's context at that step.
+   step against the oracle with the rollout's context at that step. At the
+   headline shape and at four more (GQA 1, 2, 4; d64 and d128; fp16 and
+   bf16; 16- and 32-token blocks).
 2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
    128,256 logits): max_steps 1, then a second loop that finds only STOP,
    against two launched steps.
@@ -47,24 +49,27 @@ def _same_outputs(a, b, what):
     assert np.array_equal(a["lp"].view(np.uint32), b["lp"].view(np.uint32)), (what, "lp")
 
 
-def _control_rule_case(rl, driver):
-    """The submissions of the ring-step control-rule test on a fresh arena,
-    run by driver(run); returns what the host sees."""
+def _control_rule_case(rl, driver, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, V=1024, STEPS=40, seed=6160):
+    """The submissions of the ring-step control-rule test (at the given
+    q_heads, kv_heads, head_dim, dtype and block size) on a fresh arena, run
+    by driver(run, STEPS); returns what the host sees."""
     import ringstep
 
-    B, R, V, STEPS = 8, 13, 1024, 40
-    rng = np.random.default_rng(6160)
+    qh, kvh, d, dtype, tc = shape
+    code = rl.DTYPE_BF16 if dtype == "bf16" else rl.DTYPE_FP16
+    rng = np.random.default_rng(seed)
     seq0 = rng.integers(20, 300, R).astype(np.int64)
     seq0[1] = 30
-    w = synth.make_decode(6161, R, QH, KVH, D, 0, 0, ctx=seq0.astype(np.uint32), reserve_tokens=int(seq0.max()) + 16)
+    w = synth.make_decode(seed + 1, R, qh, kvh, d, 0, 0, dtype=dtype, token_count=tc, ctx=seq0.astype(np.uint32),
+                          reserve_tokens=int(seq0.max()) + 16)
     arena = rl.DeviceBuffer.from_array(w.arena)
     seeds = rng.integers(0, 2**63, R, dtype=np.uint64)
-    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(seq0.max()) + 16, B, V,
-                               input_slots=STEPS, output_slots=STEPS, temperature=1.0, top_k=20, top_p=0.8,
-                               seeds=seeds)
-    q = synth.f32_to_bf16(rng.standard_normal((STEPS, B, QH, D), dtype=np.float32))
-    kn = synth.f32_to_bf16(rng.standard_normal((STEPS, B, KVH, D), dtype=np.float32))
-    vn = synth.f32_to_bf16(rng.standard_normal((STEPS, B, KVH, D), dtype=np.float32))
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(tc, d), w.table, qh, int(seq0.max()) + 16, B, V,
+                               input_slots=STEPS, output_slots=STEPS, dtype=code, temperature=1.0, top_k=20,
+                               top_p=0.8, seeds=seeds)
+    q = synth.to_scalar16(rng.standard_normal((STEPS, B, qh, d), dtype=np.float32), dtype)
+    kn = synth.to_scalar16(rng.standard_normal((STEPS, B, kvh, d), dtype=np.float32), dtype)
+    vn = synth.to_scalar16(rng.standard_normal((STEPS, B, kvh, d), dtype=np.float32), dtype)
     logits = rng.standard_normal((STEPS, B, V), dtype=np.float32)
     for s in range(STEPS):
         run.set_inputs(s, q[s], kn[s], vn[s], logits[s])
@@ -90,64 +95,58 @@ def _enqueue(run, steps):
     return steps
 
 
-def test_ring_loop_equals_enqueue_control_rule(rl, gpu, orc, olib):
-    print("[loop] control rule: 40 launched steps", flush=True)
-    want = _control_rule_case(rl, _enqueue)
-    print("[loop] control rule: one loop of up to 40 steps", flush=True)
-    got = _control_rule_case(rl, lambda run, steps: run.loop(steps))
+def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, STEPS=40, seed=6160):
+    """The control-rule submissions through STEPS launched steps and through
+    one loop of up to STEPS steps: the loop ends by itself, and everything but
+    the attention's fp32 rounding is the launched run's; the loop's attention,
+    step by step, against the oracle's fp64 with the appends replayed."""
+    qh, kvh, d, dtype, tc = shape
+    print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: {STEPS} launched steps", flush=True)
+    want = _control_rule_case(rl, _enqueue, shape, B, R, STEPS=STEPS, seed=seed)
+    print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: one loop of up to {STEPS} steps", flush=True)
+    got = _control_rule_case(rl, lambda run, steps: run.loop(steps), shape, B, R, STEPS=STEPS, seed=seed)
     n = got["ran"]
-    assert 0 < n < 40, n
-    assert got["completions"] == want["completions"] and len(got["completions"]) == 13
+    assert 0 < n < STEPS, n
+    assert got["completions"] == want["completions"] and len(got["completions"]) == R
     assert got["stats"] == want["stats"] and got["stats"][3] == 4, (got["stats"], want["stats"])
     for s in range(n):
         _same_outputs(got["out"][s], want["out"][s], s)
     # the launched run's later steps decoded nothing
     assert any((want["out"][n - 1]["rows"] != 0xFFFFFFFF))
-    for s in range(n, 40):
+    for s in range(n, STEPS):
         assert (want["out"][s]["rows"] == 0xFFFFFFFF).all(), s
-    # the loop's attention, step by step, against the oracle (appends replayed)
+    assert np.array_equal(got["arena"], want["arena"])
     w, q, kn, vn = got["w"], got["q"], got["kn"], got["vn"]
     cur, host = got["seq0"].copy(), w.arena.copy()
     for s in range(n):
         o = got["out"][s]
-        rows = [i for i in range(8) if o["rows"][i] != 0xFFFFFFFF]
+        rows = [i for i in range(B) if o["rows"][i] != 0xFFFFFFFF]
         if not rows:
             continue
         rs = [int(o["rows"][i]) for i in rows]
         ctx = cur[rs].astype(np.uint32)
-        wb = synth.DecodeWorkload(len(rows), QH, KVH, D, "bf16", TPB, ctx, np.ascontiguousarray(w.table[rs]), host,
+        wb = synth.DecodeWorkload(len(rows), qh, kvh, d, dtype, tc, ctx, np.ascontiguousarray(w.table[rs]), host,
                                   np.ascontiguousarray(q[s][rows]), 0)
-        ref = orc.attn_f64(olib, wb, 0)
-        errs = [float(gh.rownorm_err(o["out32"][[i]], ref[[j]]).max()) for j, i in enumerate(rows)]
-        wl = want["out"][s]
-        werrs = [float(gh.rownorm_err(wl["out32"][[i]], ref[[j]]).max()) for j, i in enumerate(rows)]
-        if max(errs) >= 1e-4:
-            print(f"[loop] step {s}: rows {rows} rollouts {rs} ctx {ctx.tolist()} loop err "
-                  f"{[f'{e:.2e}' for e in errs]} launched err {[f'{e:.2e}' for e in werrs]}", flush=True)
-            o32 = o["out32"][rows]
-            print(f"[loop]   loop out32 zero rows {[(o32[j] == 0).all() for j in range(len(rows))]} "
-                  f"nan {[bool(np.isnan(o32[j]).any()) for j in range(len(rows))]}", flush=True)
+        gh.check_attn(o["out"][rows], o["out32"][rows], orc.attn_f64(olib, wb, 0 if dtype == "bf16" else 1), dtype)
         k_rows, v_rows = np.ascontiguousarray(kn[s][rows]), np.ascontiguousarray(vn[s][rows])
-        olib.orc_kv_append(host.ctypes.data, w.block_bytes, TPB, D * 2, wb.table.ctypes.data, w.table_stride,
-                           len(rows), KVH, ctx.ctypes.data, None, k_rows.ctypes.data, v_rows.ctypes.data)
+        olib.orc_kv_append(host.ctypes.data, w.block_bytes, tc, d * 2, wb.table.ctypes.data, w.table_stride,
+                           len(rows), kvh, ctx.ctypes.data, None, k_rows.ctypes.data, v_rows.ctypes.data)
         cur[rs] += 1
-    for s in range(n):
-        o = got["out"][s]
-        rows = [i for i in range(8) if o["rows"][i] != 0xFFFFFFFF]
-        for i in rows:
-            assert np.isfinite(o["out32"][i]).all(), (s, i)
-    for name, arena in (("launched", want["arena"]), ("loop", got["arena"])):
-        bad = np.nonzero(arena != host)[0]
-        if bad.size:
-            blk = bad // w.block_bytes
-            off = bad % w.block_bytes
-            print(f"[loop] {name} arena differs from the oracle replay at {bad.size} bytes; blocks "
-                  f"{np.unique(blk)[:10].tolist()}, offsets {off[:8].tolist()}", flush=True)
-            owners = [(int(r), int(h)) for r in range(w.table.shape[0]) for h in range(KVH)
-                      if np.isin(w.table[r, h], np.unique(blk)).any()]
-            print(f"[loop] owners (rollout, kv head): {owners[:10]}", flush=True)
-    assert np.array_equal(want["arena"], host)
     assert np.array_equal(got["arena"], host)
+
+
+def test_ring_loop_equals_enqueue_control_rule(rl, gpu, orc, olib):
+    _loop_against_launched(rl, orc, olib)
+
+
+@pytest.mark.parametrize("shape", [(16, 8, 64, "fp16", 32), (8, 8, 128, "fp16", 32), (16, 8, 128, "bf16", 16),
+                                   (8, 2, 64, "bf16", 16)],
+                         ids=["gqa2_d64_fp16_tc32", "mha_d128_fp16_tc32", "gqa2_d128_bf16", "gqa4_d64_bf16_kv2"])
+def test_ring_loop_shapes(rl, gpu, orc, olib, shape):
+    """The control rule through the loop on the other shapes the fused kernel
+    takes: GQA groups 1, 2 and 4, head_dim 64 and 128, fp16 and bf16, 16- and
+    32-token blocks (a loop kernel instantiation each)."""
+    _loop_against_launched(rl, orc, olib, shape, STEPS=32, seed=6170 + shape[0] + shape[1] + shape[2])
 
 
 def _batch64(rl, driver):
