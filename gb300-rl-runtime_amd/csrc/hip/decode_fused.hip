@@ -35,6 +35,9 @@
 //           last pieces leave idle: the end of a launch is uneven across the
 //           XCDs, and on one stream each launch waits for the previous one to
 //           finish.
+//  loop     ring_loop_kernel: the ring-driven batched step (ring_core.h's
+//           turn, then these steps over the rows the turn admitted) as one
+//           self-scheduled persistent launch; described where it is defined.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -1454,7 +1457,7 @@ extern "C" int rl_hip_ring_loop_launch(const rl_ring_step_args_t *a, uint32_t ma
     // below 2 s.
     L.bar_ticks = 200000000ull;
     L.go_ticks = 2000ull * L.rp.max_idle + 2 * L.bar_ticks;
-    static_assert(kLoopSyncOff + kLoopSyncWords * 4 <= 256, "the sync words sit between the control record and the rows");
+    static_assert(kLoopSyncOff + kLoopSyncWords * 4 <= 256, "the sync words fit before the rows");
     if (rl_check_hip(hipMemsetAsync(L.sync, 0, kLoopSyncWords * sizeof(uint32_t), rl_stream()),
                      "hipMemsetAsync(loop sync)"))
         return -1;
