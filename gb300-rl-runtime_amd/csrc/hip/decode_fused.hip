@@ -472,7 +472,10 @@ enum : uint32_t { kLoopSyncTimeout = 5 };  // stats[3] when a wait of the loop r
 // with steps 0, 1, 2 modulo 3; sampling workgroups done with the merges of
 // steps 0, 1, 2 modulo 3; append waves done with the appends of all steps;
 // the error word.
+// Then the turn's requests for an early merge (the count of requests, the
+// step of the last one) and the append waves' count of merges done for them.
 enum : uint32_t { kSyncGo = 0, kSyncSteps = 1, kSyncMerges = 4, kSyncAppends = 7, kSyncError = 8 };
+enum : uint32_t { kSyncFlushReq = 9, kSyncFlushStep = 10, kSyncFlushDone = 11 };
 constexpr uint32_t kLoopSyncWords = 16;
 
 // Counter of step u modulo 3 among the three at c, and its value once all n
@@ -589,15 +592,29 @@ __device__ __forceinline__ bool loop_wait_wg(uint32_t *sync, uint32_t c, uint32_
     return *s_flag != 0;
 }
 
-// The turn's admission may wait for the host only after step u's
-// completions are visible, which needs its merges done (n sampling
-// workgroups).
+// The turn's admission may wait for the host only after the completions
+// written so far are visible, step u's (the step just published) among them.
+// Earlier steps are merged by the sampling waves of steps already released
+// (n sampling workgroups); step u's merges would come with step u + 1, which
+// this turn has not released yet, so the append waves merge step u now (the
+// sampling waves merge it again later, to the same results).
 struct MergedBy {
     static constexpr bool kDefer = true;
     uint32_t *sync;
     uint32_t u, n;
     uint64_t limit;
-    __device__ bool ready() const { return loop_wait(sync, par_ctr(kSyncMerges, u), par_target(u, n), limit); }
+    __device__ bool ready() const
+    {
+        if (u >= 1 && !loop_wait(sync, par_ctr(kSyncMerges, u - 1), par_target(u - 1, n), limit))
+            return false;
+        const uint32_t req = sync_load(&sync[kSyncFlushReq]) + 1;  // the turn alone raises it
+        if ((threadIdx.x & 63) == 0) {
+            __hip_atomic_store(&sync[kSyncFlushStep], u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __hip_atomic_store(&sync[kSyncFlushReq], req, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return loop_wait(sync, kSyncFlushDone, req * kLoopAppenders, limit);
+    }
 };
 
 // Step t's kernel arguments: argument set and workspace t % 3, slots.
@@ -715,16 +732,66 @@ __device__ __forceinline__ void loop_steps(uint32_t wg, uint32_t n_wgs, uint8_t 
     }
 }
 
+// Step u's split rows merged by append wave m (one row per wave of the
+// kLoopAppenders), once every step workgroup has finished step u; counted in
+// kSyncFlushDone. False when a wait ran out.
+template <int D, int G, int DT>
+__device__ __forceinline__ bool loop_flush_merge(uint32_t u, uint32_t m, int lane)
+{
+    const RL_CONST LoopParams &L = loop_args();
+    if (!loop_wait(L.sync, par_ctr(kSyncSteps, u), par_target(u, L.f.si.wgs), L.bar_ticks))
+        return false;
+    const FusedParams f = loop_step_params(L, u);
+    AppendParams none = {};
+    none.arena = nullptr;
+    merge_rows_waves<D, G, DT, true>(f.p, none, f.si, m, kLoopAppenders, lane);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    rl_wait_vmcnt<0>();
+    if (lane == 0)
+        atomicAdd(&L.sync[kSyncFlushDone], 1u);
+    return true;
+}
+
 // Append wave m (of kLoopAppenders): step t's K/V tokens, pairs m * 4 +
 // lane / 16 + 4 * kLoopAppenders * i, sixteen lanes a pair; then counted.
+// While it waits for a step it serves the turn's early-merge requests.
+template <int D, int G, int DT>
 __device__ __forceinline__ void loop_appends(uint32_t m, int lane)
 {
+    uint32_t served = 0;
     for (uint32_t t = 0;; t++) {
+        bool go = false;
         {
             const RL_CONST LoopParams &L = loop_args();
-            if (!loop_go(L.sync, t, L.go_ticks))
-                break;
+            uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+            for (uint32_t polls = 0;; polls++) {
+                const uint32_t v = sync_load(&L.sync[kSyncGo]);
+                if ((v & 0x7FFFFFFFu) > t) {
+                    go = true;
+                    break;
+                }
+                if (v >> 31)
+                    break;
+                if (sync_load(&L.sync[kSyncFlushReq]) > served) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                    const uint32_t u = sync_load(&L.sync[kSyncFlushStep]);
+                    if (!loop_flush_merge<D, G, DT>(u, m, lane))
+                        break;
+                    served++;
+                    t0 = __builtin_amdgcn_s_memrealtime();
+                    polls = 0;
+                    continue;
+                }
+                if (sync_load(&L.sync[kSyncError]) != 0 || __builtin_amdgcn_s_memrealtime() - t0 > L.go_ticks) {
+                    __hip_atomic_store(&L.sync[kSyncError], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                loop_backoff(polls);
+            }
         }
+        if (!go)
+            break;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         const RL_CONST LoopParams &L = loop_args();
         const uint64_t k = L.first_step + t;
         AppendParams ap = kcopy(L.ap);
@@ -865,7 +932,7 @@ __global__ __launch_bounds__(kFThreads) void ring_loop_kernel(LoopParams)
     else if (blockIdx.x == 0 && threadIdx.x < 64)
         loop_turns(reinterpret_cast<uint16_t *>(lds), (int)threadIdx.x);
     else
-        loop_appends(blockIdx.x * kFWaves + (threadIdx.x >> 6) - 1, (int)(threadIdx.x & 63));
+        loop_appends<D, G, DT>(blockIdx.x * kFWaves + (threadIdx.x >> 6) - 1, (int)(threadIdx.x & 63));
 }
 
 struct FusedWs {

@@ -21,7 +21,9 @@ ring-step tests check the launched step's.
    against two launched steps.
 3. Exit paths: idle limit, bad rollout id, the host's stop flag (zero steps
    run, status 1 / 2 / 4) and a full completion ring (status 3; the finished
-   descriptor stays in its row until a later loop pushes it).
+   descriptor stays in its row until a later loop pushes it). A lock-step
+   host: it submits a batch only after it has seen the previous batch's
+   completions, which the loop makes visible before it waits for the host.
 4. Arguments the loop does not take: max_steps 0, fewer than three output
    slots (a step's split rows are merged while the next two steps run, so
    three consecutive steps need their own slots) and a GQA group of 8 at d128
@@ -246,6 +248,77 @@ def test_ring_loop_exit_paths(rl, gpu):
     st = run.stats()
     assert st[0] == 1 and st[1] == 1 and st[3] == 3, st
     assert run.loop(2) == 0                                # nothing held, admission closed
+    run.close()
+    arena.close()
+
+
+def test_ring_loop_lock_step_host(rl, gpu, orc, olib):
+    """A host that submits its next batch only after it has seen the previous
+    batch's completions, while the loop runs: 8 one-token descriptors, no
+    STOP; every row finishes and the ring is empty, so the turn waits for the
+    host - after making those completions visible (the step's merges are done
+    early for it). A host thread pops the 8 completions during that wait, then
+    submits 8 more and STOP, which the same launch decodes. Both batches'
+    completions follow the control rule and every decoded row matches the
+    oracle's tokens."""
+    import threading
+    import ringstep
+
+    B, V = 8, 4096
+    rng = np.random.default_rng(7290)
+    w = synth.make_decode(7291, 2 * B, QH, KVH, D, 40, 300)
+    arena = rl.DeviceBuffer.from_array(w.arena)
+    seeds = rng.integers(0, 2**63, 2 * B, dtype=np.uint64)
+    run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
+                               output_slots=4, temperature=1.0, top_k=50, top_p=0.9, seeds=seeds)
+    q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
+    kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
+    logits = rng.standard_normal((B, V), dtype=np.float32)
+    run.set_inputs(0, q, kn, vn, logits)
+    for r in range(B):
+        run.submit_decode(r, int(w.ctx[r]), int(w.ctx[r]) + 1)
+    seen, errs = [], []
+
+    def host():
+        try:
+            import time
+            t_end = time.monotonic() + 20
+            while len(seen) < B and time.monotonic() < t_end:
+                seen.extend(run.completions())
+            if len(seen) != B:
+                errs.append(f"first batch: {len(seen)} completions")
+                return
+            for r in range(B, 2 * B):
+                run.submit_decode(r, int(w.ctx[r]), int(w.ctx[r]) + 1)
+            run.push(rl.HwDesc(opcode=255))
+        except Exception as e:  # reported by the main thread
+            errs.append(repr(e))
+
+    th = threading.Thread(target=host)
+    print("[loop] lock-step host: 8 descriptors, then 8 more after their completions", flush=True)
+    run.loop_launch(8)
+    th.start()
+    ran = run.loop_done()
+    th.join(timeout=30)
+    assert not errs, errs
+    assert ran == 2, ran
+    got = seen + run.completions()
+    assert len(got) == 2 * B
+    by = {rl.HwDesc.from_buffer_copy(g).rollout_id: rl.HwDesc.from_buffer_copy(g) for g in got}
+    assert sorted(by) == list(range(2 * B))
+    for r, d in by.items():
+        assert (d.seq_len, d.max_tokens) == (int(w.ctx[r]) + 1, int(w.ctx[r]) + 1) and d.flags & 2, r
+    assert run.stats() == [2 * B, 2 * B, 2, 4]
+    lp = C.c_double()
+    for s in range(2):
+        o = run.outputs(s)
+        assert sorted(o["rows"].tolist()) == list(range(s * B, (s + 1) * B)), (s, o["rows"])
+        for i in range(B):
+            r = int(o["rows"][i])
+            want = olib.orc_sample_row(logits[i].ctypes.data, V, 0, 1.0, 50, 0.9, int(seeds[r]), int(w.ctx[r]), r,
+                                       C.byref(lp))
+            assert o["tok"][i] == want, (s, i)
     run.close()
     arena.close()
 
