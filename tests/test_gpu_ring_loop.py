@@ -270,7 +270,7 @@ def test_ring_loop_lock_step_host(rl, gpu, orc, olib):
     arena = rl.DeviceBuffer.from_array(w.arena)
     seeds = rng.integers(0, 2**63, 2 * B, dtype=np.uint64)
     run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(TPB, D), w.table, QH, int(w.ctx.max()) + 1, B, V,
-                               output_slots=4, temperature=1.0, top_k=50, top_p=0.9, seeds=seeds)
+                               output_slots=8, temperature=1.0, top_k=50, top_p=0.9, seeds=seeds)
     q = synth.f32_to_bf16(rng.standard_normal((B, QH, D), dtype=np.float32))
     kn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
     vn = synth.f32_to_bf16(rng.standard_normal((B, KVH, D), dtype=np.float32))
@@ -302,23 +302,30 @@ def test_ring_loop_lock_step_host(rl, gpu, orc, olib):
     ran = run.loop_done()
     th.join(timeout=30)
     assert not errs, errs
-    assert ran == 2, ran
+    # the second batch may be admitted over several turns, as the host's
+    # pushes arrive
+    assert 2 <= ran <= 8, ran
     got = seen + run.completions()
     assert len(got) == 2 * B
     by = {rl.HwDesc.from_buffer_copy(g).rollout_id: rl.HwDesc.from_buffer_copy(g) for g in got}
     assert sorted(by) == list(range(2 * B))
     for r, d in by.items():
         assert (d.seq_len, d.max_tokens) == (int(w.ctx[r]) + 1, int(w.ctx[r]) + 1) and d.flags & 2, r
-    assert run.stats() == [2 * B, 2 * B, 2, 4]
+    assert run.stats() == [2 * B, 2 * B, ran, 4]
     lp = C.c_double()
-    for s in range(2):
+    decoded = []
+    for s in range(ran):
         o = run.outputs(s)
-        assert sorted(o["rows"].tolist()) == list(range(s * B, (s + 1) * B)), (s, o["rows"])
         for i in range(B):
             r = int(o["rows"][i])
+            if r == 0xFFFFFFFF:
+                continue
+            decoded.append(r)
             want = olib.orc_sample_row(logits[i].ctypes.data, V, 0, 1.0, 50, 0.9, int(seeds[r]), int(w.ctx[r]), r,
                                        C.byref(lp))
             assert o["tok"][i] == want, (s, i)
+    assert sorted(decoded) == list(range(2 * B))
+    assert sorted(run.outputs(0)["rows"].tolist()) == list(range(B))
     run.close()
     arena.close()
 
