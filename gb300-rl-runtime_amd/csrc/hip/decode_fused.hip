@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 // ---- the self-scheduled ring loop ----------------------------------------------
 // One cooperative launch of one workgroup per compute unit runs the
 // ring-driven batched step for as many steps as the rings call for, with no
-// launch between steps. Two roles:
+// launch between steps. Three roles:
 //  turn   wave 0 of workgroup 0, beside the steps: turn t (ring_core.h)
 //         publishes step t - 1 (the hw_worker_sim rule does not depend on
 //         the token, so it runs while step t - 1 is still streaming) and
@@ -405,7 +405,10 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 //         appends are done. Step t - 1's completions become visible once
 //         its merges are done: the turn keeps them pending and stores the
 //         completion ring's tail when it finds those merges finished (before
-//         a later turn, or waiting for them at the end).
+//         a later turn, or waiting for them at the end). A turn that has to
+//         wait for the host with every row free has the append waves merge
+//         the step just published first, so that its completions are
+//         visible while it waits.
 //  steps  workgroups kLoopService.. (the same number on each XCD; the other
 //         workgroups of the first kLoopService, one per XCD, keep the turn
 //         off the steps' compute units): step t over argument set and step
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(256) void merge_pieces_kernel(AttnParams p, AppendP
 //  appends the other waves of the first kLoopService workgroups: once step
 //         t is released, its K/V tokens, four (row, kv head) pairs at a time
 //         per wave (the attention masks positions past the context, the
-//         appended one among them).
+//         appended one among them); between steps, the turn's early merges.
 // Hand-offs are monotonic counters in the workspace: a release fence and an
 // atomic add by the producer, a bounded wait and an acquire fence by the
 // consumer. Workgroups may run step t + 2 while others finish step t (never
@@ -462,7 +465,7 @@ struct LoopParams {
     uint32_t input_slots, output_slots;
     uint64_t first_step;
     uint32_t max_steps;
-    uint32_t *sync;           // device [8], zeroed: see kSync*
+    uint32_t *sync;           // device [kLoopSyncWords], zeroed: see kSync*
     uint64_t go_ticks;        // longest wait for a turn, in 100 MHz clock ticks
     uint64_t bar_ticks;       // longest wait for a step's workgroups or merges
 };
