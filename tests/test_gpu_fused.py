@@ -130,6 +130,26 @@ def test_fused_step_batch64(rl, gpu, orc, olib):
     _check(orc, olib, w, 4096, pos, None, kn, vn, logits, res, want, wlp)
 
 
+def test_fused_step_max_batch(rl, gpu, orc, olib):
+    """1,024 rollouts, the most the fused kernel takes (its tile prefix and
+    the loop's staged contexts are sized for it): GQA 16/4 d64 bf16, ctx
+    U[0, 600] (a few rows without context), every row appending; 1,024 rows
+    x 4,096 of sampling (T 0.9, top-k 40, top-p 0.9, per-row seeds), sixteen
+    rows per sampling workgroup."""
+    B, V = 1024, 4096
+    w = synth.make_decode(8106, B, 16, 4, 64, 0, 600)
+    rng = np.random.default_rng(8107)
+    pos = w.ctx.copy()
+    kn, vn = _kv_rows(rng, w)
+    logits = rng.standard_normal((B, V), dtype=np.float32) * np.float32(2.0)
+    seeds = rng.integers(0, 2**63, B, dtype=np.uint64)
+    res = _run(rl, w, int(w.ctx.max()), pos, None, kn, vn, logits, temperature=0.9, top_k=40, top_p=0.9,
+               seed=seeds.copy(), step=3)
+    want, wlp = orc.sample_rows_v(olib, logits, seeds=seeds, temperature_all=0.9, top_k_all=40, top_p_all=0.9,
+                                  step_all=3)
+    _check(orc, olib, w, int(w.ctx.max()), pos, None, kn, vn, logits, res, want, wlp)
+
+
 def test_fused_step_ragged_edges(rl, gpu, orc, olib):
     """Contexts 0, 1, 15, 16, 17 tokens, one beyond max_ctx (NaN rows), long
     ones; GQA 16/8 d64 fp16 in 32-token blocks; copy-on-write on a third of

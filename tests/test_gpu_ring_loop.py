@@ -18,7 +18,8 @@ ring-step tests check the launched step's.
    bf16; 16- and 32-token blocks).
 2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
    128,256 logits): max_steps 1, then a second loop that finds only STOP,
-   against two launched steps.
+   against two launched steps. The control rule at 1,024 rows, the most a
+   step takes, with more descriptors than rows.
 3. Exit paths: idle limit, bad rollout id, the host's stop flag (zero steps
    run, status 1 / 2 / 4) and a full completion ring (status 3; the finished
    descriptor stays in its row until a later loop pushes it). A lock-step
@@ -191,6 +192,14 @@ def test_ring_loop_batch64(rl, gpu, orc, olib):
     _same_outputs(got["out"], want["out"], "step 0")
     assert np.array_equal(got["arena"], want["arena"])
     gh.check_attn(got["out"]["out"], got["out"]["out32"], orc.attn_f64(olib, got["wb"], 0), "bf16")
+
+
+def test_ring_loop_max_batch(rl, gpu, orc, olib):
+    """The control rule at the most rows a step takes: 1,024 rows and 1,100
+    descriptors (GQA 16/4 d64 bf16), so the last 76 wait for rows that free
+    up; the launched pipeline and the loop against each other and the
+    loop's attention against fp64 at every step."""
+    _loop_against_launched(rl, orc, olib, (16, 4, 64, "bf16", 16), B=1024, R=1100, STEPS=24, seed=6190)
 
 
 def test_ring_loop_exit_paths(rl, gpu):
