@@ -6,8 +6,8 @@ copies of the same arena and compares what the host can see: completions,
 stats, per-step rows, tokens and logprobs (bits) and the final arena are
 equal; the attention, which the loop splits over the compute units left
 beside its turn and merges (a different split from the launched step's, so
-other fp32 roundings), is checked against the oracle's fp64 as the
-ring-step tests check the launched step's.
+other fp32 roundings), is checked against the oracle's fp64 in both runs,
+every decoded row of every step.
 
 1. The control rule over many steps (8 rows, 13 descriptors of 1-8 tokens,
    NEEDS_REWARD at 32, a passthrough, a dropped opcode, STOP): the loop
@@ -101,7 +101,7 @@ def _enqueue(run, steps):
 def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, STEPS=40, seed=6160):
     """The control-rule submissions through STEPS launched steps and through
     one loop of up to STEPS steps: the loop ends by itself, and everything but
-    the attention's fp32 rounding is the launched run's; the loop's attention,
+    the attention's fp32 rounding is the launched run's; both runs' attention,
     step by step, against the oracle's fp64 with the appends replayed."""
     qh, kvh, d, dtype, tc = shape
     print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: {STEPS} launched steps", flush=True)
@@ -119,10 +119,19 @@ def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, 
     for s in range(n, STEPS):
         assert (want["out"][s]["rows"] == 0xFFFFFFFF).all(), s
     assert np.array_equal(got["arena"], want["arena"])
-    w, q, kn, vn = got["w"], got["q"], got["kn"], got["vn"]
-    cur, host = got["seq0"].copy(), w.arena.copy()
+    for res in (got, want):
+        _attn_against_fp64(orc, olib, res, shape, B, n)
+
+
+def _attn_against_fp64(orc, olib, res, shape, B, n):
+    """Every decoded row of steps 0 .. n - 1 of a run against the oracle's fp64
+    attention over the arena as it stood at that step (the earlier steps'
+    appends replayed by the oracle), and the final arena against the replay."""
+    qh, kvh, d, dtype, tc = shape
+    w, q, kn, vn = res["w"], res["q"], res["kn"], res["vn"]
+    cur, host = res["seq0"].copy(), w.arena.copy()
     for s in range(n):
-        o = got["out"][s]
+        o = res["out"][s]
         rows = [i for i in range(B) if o["rows"][i] != 0xFFFFFFFF]
         if not rows:
             continue
@@ -135,7 +144,7 @@ def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, 
         olib.orc_kv_append(host.ctypes.data, w.block_bytes, tc, d * 2, wb.table.ctypes.data, w.table_stride,
                            len(rows), kvh, ctx.ctypes.data, None, k_rows.ctypes.data, v_rows.ctypes.data)
         cur[rs] += 1
-    assert np.array_equal(got["arena"], host)
+    assert np.array_equal(res["arena"], host)
 
 
 def test_ring_loop_equals_enqueue_control_rule(rl, gpu, orc, olib):
