@@ -15,7 +15,8 @@ every decoded row of every step.
    launched run's later steps decoded nothing; every decoded row of every
    step against the oracle with the rollout's context at that step. At the
    headline shape and at four more (GQA 1, 2, 4; d64 and d128; fp16 and
-   bf16; 16- and 32-token blocks).
+   bf16; 16- and 32-token blocks), and with greedy sampling (tokens the
+   first index of each row's maximum, logprobs the fp64 log-softmax).
 2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
    128,256 logits): max_steps 1, then a second loop that finds only STOP,
    against two launched steps. The control rule at 1,024 rows, the most a
@@ -52,7 +53,8 @@ def _same_outputs(a, b, what):
     assert np.array_equal(a["lp"].view(np.uint32), b["lp"].view(np.uint32)), (what, "lp")
 
 
-def _control_rule_case(rl, driver, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, V=1024, STEPS=40, seed=6160):
+def _control_rule_case(rl, driver, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, V=1024, STEPS=40, seed=6160,
+                       greedy=False):
     """The submissions of the ring-step control-rule test (at the given
     q_heads, kv_heads, head_dim, dtype and block size) on a fresh arena, run
     by driver(run, STEPS); returns what the host sees."""
@@ -68,8 +70,8 @@ def _control_rule_case(rl, driver, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, V
     arena = rl.DeviceBuffer.from_array(w.arena)
     seeds = rng.integers(0, 2**63, R, dtype=np.uint64)
     run = ringstep.RingStepRun(arena, rl.KvLayoutDesc.paged(tc, d), w.table, qh, int(seq0.max()) + 16, B, V,
-                               input_slots=STEPS, output_slots=STEPS, dtype=code, temperature=1.0, top_k=20,
-                               top_p=0.8, seeds=seeds)
+                               input_slots=STEPS, output_slots=STEPS, dtype=code, greedy=greedy, temperature=1.0,
+                               top_k=20, top_p=0.8, seeds=seeds)
     q = synth.to_scalar16(rng.standard_normal((STEPS, B, qh, d), dtype=np.float32), dtype)
     kn = synth.to_scalar16(rng.standard_normal((STEPS, B, kvh, d), dtype=np.float32), dtype)
     vn = synth.to_scalar16(rng.standard_normal((STEPS, B, kvh, d), dtype=np.float32), dtype)
@@ -87,7 +89,8 @@ def _control_rule_case(rl, driver, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, V
     ran = driver(run, STEPS)
     rl.sync()
     res = {"ran": ran, "completions": run.completions(), "stats": run.stats(), "out": _outputs(run, STEPS),
-           "arena": arena.download(np.uint8, arena.nbytes), "w": w, "seq0": seq0, "q": q, "kn": kn, "vn": vn}
+           "arena": arena.download(np.uint8, arena.nbytes), "w": w, "seq0": seq0, "q": q, "kn": kn, "vn": vn,
+           "logits": logits}
     run.close()
     arena.close()
     return res
@@ -98,16 +101,18 @@ def _enqueue(run, steps):
     return steps
 
 
-def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, STEPS=40, seed=6160):
+def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, STEPS=40, seed=6160,
+                           greedy=False):
     """The control-rule submissions through STEPS launched steps and through
     one loop of up to STEPS steps: the loop ends by itself, and everything but
     the attention's fp32 rounding is the launched run's; both runs' attention,
     step by step, against the oracle's fp64 with the appends replayed."""
     qh, kvh, d, dtype, tc = shape
     print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: {STEPS} launched steps", flush=True)
-    want = _control_rule_case(rl, _enqueue, shape, B, R, STEPS=STEPS, seed=seed)
+    want = _control_rule_case(rl, _enqueue, shape, B, R, STEPS=STEPS, seed=seed, greedy=greedy)
     print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: one loop of up to {STEPS} steps", flush=True)
-    got = _control_rule_case(rl, lambda run, steps: run.loop(steps), shape, B, R, STEPS=STEPS, seed=seed)
+    got = _control_rule_case(rl, lambda run, steps: run.loop(steps), shape, B, R, STEPS=STEPS, seed=seed,
+                             greedy=greedy)
     n = got["ran"]
     assert 0 < n < STEPS, n
     assert got["completions"] == want["completions"] and len(got["completions"]) == R
@@ -121,6 +126,7 @@ def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, 
     assert np.array_equal(got["arena"], want["arena"])
     for res in (got, want):
         _attn_against_fp64(orc, olib, res, shape, B, n)
+    return got
 
 
 def _attn_against_fp64(orc, olib, res, shape, B, n):
@@ -159,6 +165,25 @@ def test_ring_loop_shapes(rl, gpu, orc, olib, shape):
     takes: GQA groups 1, 2 and 4, head_dim 64 and 128, fp16 and bf16, 16- and
     32-token blocks (a loop kernel instantiation each)."""
     _loop_against_launched(rl, orc, olib, shape, STEPS=32, seed=6170 + shape[0] + shape[1] + shape[2])
+
+
+def test_ring_loop_greedy(rl, gpu, orc, olib):
+    """The control rule with greedy sampling (the sampling function's argmax
+    path): the loop against the launched run, and every decoded row's token
+    the lowest index of its row's maximum (numpy's argmax), its logprob the
+    fp64 log-softmax of that maximum within 1e-4."""
+    got = _loop_against_launched(rl, orc, olib, STEPS=32, seed=6180, greedy=True)
+    checked = 0
+    for s in range(got["ran"]):
+        o, x = got["out"][s], got["logits"][s].astype(np.float64)
+        for i in np.nonzero(o["rows"] != 0xFFFFFFFF)[0]:
+            row = x[i]
+            assert o["tok"][i] == np.argmax(row), (s, i)
+            m = row.max()
+            want_lp = -np.log(np.exp(row - m).sum())
+            assert abs(float(o["lp"][i]) - want_lp) < 1e-4, (s, i, o["lp"][i], want_lp)
+            checked += 1
+    assert checked > 0
 
 
 def _batch64(rl, driver):
