@@ -15,7 +15,8 @@ every decoded row of every step.
    launched run's later steps decoded nothing; every decoded row of every
    step against the oracle with the rollout's context at that step. At the
    headline shape and at four more (GQA 1, 2, 4; d64 and d128; fp16 and
-   bf16; 16- and 32-token blocks), and with greedy sampling (tokens the
+   bf16; 16- and 32-token blocks); loops and launched steps alternating
+   on one run; and with greedy sampling (tokens the
    first index of each row's maximum, logprobs the fp64 log-softmax).
 2. The benchmark's shape (64 rollouts, GQA 32/8, d128, ctx U[512, 4096],
    128,256 logits): max_steps 1, then a second loop that finds only STOP,
@@ -102,7 +103,7 @@ def _enqueue(run, steps):
 
 
 def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, R=13, STEPS=40, seed=6160,
-                           greedy=False):
+                           greedy=False, driver=None):
     """The control-rule submissions through STEPS launched steps and through
     one loop of up to STEPS steps: the loop ends by itself, and everything but
     the attention's fp32 rounding is the launched run's; both runs' attention,
@@ -111,8 +112,8 @@ def _loop_against_launched(rl, orc, olib, shape=(QH, KVH, D, "bf16", TPB), B=8, 
     print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: {STEPS} launched steps", flush=True)
     want = _control_rule_case(rl, _enqueue, shape, B, R, STEPS=STEPS, seed=seed, greedy=greedy)
     print(f"[loop] control rule {qh}/{kvh} d{d} {dtype} tc{tc}: one loop of up to {STEPS} steps", flush=True)
-    got = _control_rule_case(rl, lambda run, steps: run.loop(steps), shape, B, R, STEPS=STEPS, seed=seed,
-                             greedy=greedy)
+    got = _control_rule_case(rl, driver or (lambda run, steps: run.loop(steps)), shape, B, R, STEPS=STEPS,
+                             seed=seed, greedy=greedy)
     n = got["ran"]
     assert 0 < n < STEPS, n
     assert got["completions"] == want["completions"] and len(got["completions"]) == R
@@ -165,6 +166,20 @@ def test_ring_loop_shapes(rl, gpu, orc, olib, shape):
     takes: GQA groups 1, 2 and 4, head_dim 64 and 128, fp16 and bf16, 16- and
     32-token blocks (a loop kernel instantiation each)."""
     _loop_against_launched(rl, orc, olib, shape, STEPS=32, seed=6170 + shape[0] + shape[1] + shape[2])
+
+
+def test_ring_loop_continues_launched_steps(rl, gpu, orc, olib):
+    """Calls that share one run's workspace and rings: a loop of 4 steps,
+    3 launched steps, then a loop to the end. Each call starts at the step
+    after the last one run and publishes its own last step, so the whole
+    equals one launched run."""
+    def mixed(run, steps):
+        a = run.loop(4)
+        assert a == 4, a
+        run.enqueue(3)
+        return 7 + run.loop(steps - 7)
+
+    _loop_against_launched(rl, orc, olib, STEPS=40, seed=6200, driver=mixed)
 
 
 def test_ring_loop_greedy(rl, gpu, orc, olib):
