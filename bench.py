@@ -827,7 +827,7 @@ def wl_plumbing256(args):
 
 def wl_ringstep(args):
     """The headline step (64 rollouts, GQA 32/8, d128, bf16 K/V, ctx
-    U[512,4096], sampling of 64 x 128,256 logits with T 0.8 / top-k 50 /
+    U[512,4096] or the --ctx range, sampling of 64 x 128,256 logits with T 0.8 / top-k 50 /
     top-p 0.9, KV append) driven through the hw_desc rings
     (rl_hip_ring_step_enqueue): per step 64 one-token descriptors drained by
     the poll kernel, the batched step over every compute unit, 64 completions
@@ -904,7 +904,8 @@ def wl_ringstep(args):
     lms, _ = time_loop(st, K, "unfused")
     ring_us, launched_us, loop_us = ms / K * 1e3, lms / K * 1e3, loop_ms / K * 1e3
     step_bytes = st.attn_bytes() + st.sample_bytes() + st.append_bytes()
-    return {"workload": "ringstep_b64_q32kv8_d128_ctx512-4096_v128256_t0.8_k50_p0.9",
+    return {"workload": f"ringstep_b64_q32kv8_d128_ctx{CTX_LO}-{CTX_HI}_v128256_t0.8_k50_p0.9",
+            "ctx_sum": int(w.ctx.astype(np.int64).sum()), "step_alg_bytes": int(step_bytes),
             "steps": K, "ring_step_us": ring_us, "ring_steps_per_s": 1e6 / ring_us,
             "ring_tokens_per_s": B * 1e6 / ring_us, "ring_step_hbm_frac": step_bytes / (ring_us * 1e-6) / 1e9 / PEAK_HBM_GBPS,
             "loop_step_us": loop_us, "loop_tokens_per_s": B * 1e6 / loop_us,
@@ -1366,6 +1367,7 @@ WORKLOADS = {"sample256": wl_sample256, "sample32k": wl_sample32k, "longctx": wl
 
 
 def main():
+    global CTX_LO, CTX_HI
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -1379,6 +1381,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 counter passes")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--ctx", default=None, metavar="LO,HI",
+                    help=f"ringstep only: contexts uniform in [LO, HI] (1 <= LO <= HI <= {MAX_CTX}; default "
+                         f"{CTX_LO},{CTX_HI})")
     ap.add_argument("--grid-waves", type=int, default=0,
                     help="attention: persistent waves sharing the KV stream (0: library default, a full device)")
     args = ap.parse_args()
@@ -1386,6 +1391,14 @@ def main():
         print("bench.py: the decode hot path runs on one GPU here; multi-GPU runs are not part of it; "
               "the path shards by rollout, with no exchange inside a decode step.", file=sys.stderr)
         sys.exit(2)
+    if args.ctx is not None:
+        try:
+            lo, hi = (int(v) for v in args.ctx.split(","))
+        except ValueError:
+            raise SystemExit(f"bench.py: --ctx takes LO,HI, not {args.ctx!r}")
+        if args.workload != "ringstep" or not 1 <= lo <= hi <= MAX_CTX:
+            raise SystemExit(f"bench.py: --ctx LO,HI applies to --workload ringstep, with 1 <= LO <= HI <= {MAX_CTX}")
+        CTX_LO, CTX_HI = lo, hi
 
     traffic, traffic_note = None, "not measured (--no-traffic)"
     headline = args.workload == "step" and args.only == "step"
